@@ -1,0 +1,130 @@
+/*
+ * libweft_hip -- MI355X (gfx950) implementation of Weft's quantized mul_mat
+ * hot path behind Weft's generated-kernel C ABI.
+ *
+ * ABI rules kept from the reference (lib/Target/Emission/Emitter.h:465-512):
+ *   void <symbol>(<one pointer per View parameter, in signature order>,
+ *                 <one size_t per shape symbol, in first-appearance order>);
+ *   record encodings travel as uint8_t*, dense views as their element type,
+ *   read-only views are const.  The library allocates nothing, keeps no
+ *   cross-call state, and never repacks or copies its arguments.
+ *
+ * HIP specifics:
+ *   - every pointer is a DEVICE pointer (hipMalloc / torch device memory);
+ *   - each call enqueues on the calling thread's current stream
+ *     (weft_hip_set_stream; default: the null stream) and returns without
+ *     waiting: results are visible to later work on that stream, or to the
+ *     host after weft_hip_synchronize();
+ *   - the kernels have no failure channel; shape/pointer errors found before
+ *     the launch and launch errors are recorded per thread and returned (and
+ *     cleared) by weft_hip_get_last_error(); nothing is launched for an
+ *     invalid call.
+ *
+ * Record layouts are GGML's (source/c/ggml/llama.cpp/ggml/src/ggml-common.h):
+ *   Q4_0 18 B/32, MXFP4 17 B/32, Q8_0 34 B/32, Q4_K 144 B/256,
+ *   Q8_K 292 B/256, IQ2_XXS 66 B/256.
+ * Table arguments: grid = I8X8[256x8] iq2xxs grid magnitudes, signs =
+ * I8X8[128x8] of +-1, codebook = int8[16] doubled E2M1, scale = fp32[256]
+ * e8m0 "half" scales (examples/repro/weft/mul_mat_runtime.cpp:151-159).
+ *
+ * Reference citations are relative to the Weft repository root.
+ */
+#ifndef WEFT_HIP_H
+#define WEFT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#define WEFT_HIP_VERSION_STRING "weft_hip 0.1 gfx950"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------ control API */
+/* No counterpart in the reference (its kernels are synchronous host C). */
+int weft_hip_set_stream(void *stream);   /* hipStream_t; thread-local */
+void *weft_hip_get_stream(void);
+int weft_hip_get_last_error(void);       /* hipError_t, then cleared */
+const char *weft_hip_error_string(int code);
+int weft_hip_synchronize(void);          /* hipStreamSynchronize(current) */
+const char *weft_hip_version(void);
+/* ABI metadata of every exported kernel, as the JSON artifact weft-compile
+ * emits (tools/weft-compile/weft-compile.cpp:116-147, kind
+ * "weft-hip-artifact", gfx_arch / wavefront_size in place of march / abi /
+ * vlen_bits). */
+const char *weft_hip_artifact(void);
+
+/* ------------------------------------------------------ row dequantize */
+/* examples/kernels/dequantize/q4_0.py:9-13; repro row_dequantize_runtime.cpp:177 */
+void row_dequantize_q4_0(const uint8_t *W, float *Y, size_t K);
+/* examples/kernels/dequantize/q4_k.py:9-20; row_dequantize_runtime.cpp:212 */
+void row_dequantize_q4_k(const uint8_t *W, float *Y, size_t K);
+/* examples/kernels/dequantize/iq2_xxs.py:9-53; row_dequantize_runtime.cpp:247 */
+void row_dequantize_iq2_xxs(const uint8_t *W, const int8_t *grid, const int8_t *signs, float *Y,
+                            size_t K);
+/* examples/kernels/dequantize/mxfp4.py:9-20; row_dequantize_runtime.cpp:282 */
+void row_dequantize_mxfp4(const uint8_t *W, const int8_t *codebook, const float *scale, float *Y,
+                          size_t K);
+
+/* ------------------------------------------------ activation quantize */
+/* examples/kernels/quantize/q8_0.py:26-28; repro q8_quantize_runtime.cpp:25 */
+void q8_0_quantize(const float *X, uint8_t *Y, size_t K);
+/* examples/kernels/quantize/q8_k.py:38-40; repro q8_quantize_runtime.cpp:26 */
+void q8_K_quantize(const float *X, uint8_t *Y, size_t K);
+
+/* ------------------------------------------------------------ vec_dot */
+/* examples/kernels/vec_dot/q4_0_q8_0.py:8-23; repro vec_dot_runtime.cpp:191 */
+void quantized_vec_dot_q4_0_q8_0(const uint8_t *W, const uint8_t *X, float *Y, size_t K);
+/* examples/kernels/vec_dot/q4_k_q8_k.py:8-36; vec_dot_runtime.cpp:247 */
+void quantized_vec_dot_q4_k_q8_k(const uint8_t *W, const uint8_t *X, float *Y, size_t K);
+/* examples/kernels/vec_dot/iq2_xxs_q8_k.py:8-54; vec_dot_runtime.cpp:303 */
+void quantized_vec_dot_iq2_xxs_q8_k(const uint8_t *W, const uint8_t *X, const int8_t *grid,
+                                    const int8_t *signs, float *Y, size_t K);
+/* examples/kernels/vec_dot/mxfp4_q8_0.py:9-33; vec_dot_runtime.cpp:359 */
+void quantized_vec_dot_mxfp4_q8_0(const uint8_t *W, const uint8_t *X, const int8_t *codebook,
+                                  const float *scale, float *Y, size_t K);
+
+/* --------------------------------------------------- production mul_mat */
+/* W (N x K) encoded, X (M x K) fp32, Xq (M x K) written with the
+ * activation quantization, Y (M x N) fp32 = X . W^T.  Shape order N, K, M. */
+
+/* examples/kernels/mul_mat/q4_0.py:9-30; mul_mat_runtime.cpp:220 */
+void production_mul_mat_q4_0(const uint8_t *W, const float *X, uint8_t *Xq, float *Y, size_t N,
+                             size_t K, size_t M);
+/* examples/kernels/mul_mat/q4_0_decode.py:10-20; mul_mat_runtime.cpp:217 */
+void production_mul_mat_q4_0_decode(const uint8_t *W, const float *X, uint8_t *Xq, float *Y,
+                                    size_t N, size_t K, size_t M);
+/* examples/kernels/mul_mat/q4_k.py:10-20; mul_mat_runtime.cpp:356 */
+void production_mul_mat_q4_k(const uint8_t *W, const float *X, uint8_t *Xq, float *Y, size_t N,
+                             size_t K, size_t M);
+/* examples/kernels/mul_mat/q4_k_decode.py:10-20; mul_mat_runtime.cpp:332-336 */
+void production_mul_mat_q4_k_decode(const uint8_t *W, const float *X, uint8_t *Xq, float *Y,
+                                    size_t N, size_t K, size_t M);
+/* examples/kernels/mul_mat/q4_k_staged.py:9-37; mul_mat_runtime.cpp:350-354 */
+void production_mul_mat_q4_k_staged(const uint8_t *W, const float *X, uint8_t *Xq, float *Y,
+                                    size_t N, size_t K, size_t M);
+/* examples/kernels/mul_mat/iq2_xxs.py; mul_mat_runtime.cpp:472 */
+void production_mul_mat_iq2_xxs(const uint8_t *W, const float *X, uint8_t *Xq, const int8_t *grid,
+                                const int8_t *signs, float *Y, size_t N, size_t K, size_t M);
+/* examples/kernels/mul_mat/iq2_xxs_decode.py:10-23; mul_mat_runtime.cpp:458-463 */
+void production_mul_mat_iq2_xxs_decode(const uint8_t *W, const float *X, uint8_t *Xq,
+                                       const int8_t *grid, const int8_t *signs, float *Y, size_t N,
+                                       size_t K, size_t M);
+/* examples/kernels/mul_mat/iq2_xxs_staged.py:86-97; mul_mat_runtime.cpp:465-470 */
+void production_mul_mat_iq2_xxs_staged(const uint8_t *W, const float *X, uint8_t *Xq,
+                                       const int8_t *grid, const int8_t *signs, float *Y, size_t N,
+                                       size_t K, size_t M);
+/* examples/kernels/mul_mat/mxfp4.py:10-35; mul_mat_runtime.cpp:567 */
+void production_mul_mat_mxfp4(const uint8_t *W, const float *X, uint8_t *Xq, const int8_t *codebook,
+                              const float *scale, float *Y, size_t N, size_t K, size_t M);
+/* examples/kernels/mul_mat/mxfp4_decode.py:10-23; mul_mat_runtime.cpp:564 */
+void production_mul_mat_mxfp4_decode(const uint8_t *W, const float *X, uint8_t *Xq,
+                                     const int8_t *codebook, const float *scale, float *Y,
+                                     size_t N, size_t K, size_t M);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WEFT_HIP_H */

@@ -1,0 +1,247 @@
+"""CPU oracle for the quantized mul_mat path -- TEST INFRASTRUCTURE ONLY.
+
+numpy-facing ctypes wrapper of ``oracle/libweft_oracle.so`` (built from
+``oracle/weft_oracle.c`` by ``oracle/Makefile``), a plain-C restatement of the
+GGML CPU functions the reference Weft repo checks its kernels against
+(``source/c/ggml/llama.cpp/ggml/src/ggml-quants.c``,
+``ggml-cpu/quants.c``).  Only ``tests/``, ``__graft_entry__.smoke()`` and
+``bench.py``'s ``cpu_baseline`` leg import this package, and only as the checker
+or the timed CPU baseline; the product library ``libweft_hip`` never calls it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "libweft_oracle.so"
+
+Q4_0, Q4_K, IQ2_XXS, MXFP4 = 0, 1, 2, 3
+FORMATS = {"q4_0": Q4_0, "q4_k": Q4_K, "iq2_xxs": IQ2_XXS, "mxfp4": MXFP4}
+
+# (elements per record, bytes per record)
+RECORD = {
+    "q4_0": (32, 18), "mxfp4": (32, 17), "q8_0": (32, 34),
+    "q4_k": (256, 144), "q8_k": (256, 292), "iq2_xxs": (256, 66),
+}
+ACT_OF = {"q4_0": "q8_0", "mxfp4": "q8_0", "q4_k": "q8_k", "iq2_xxs": "q8_k"}
+
+
+def build() -> Path:
+    """Compile the oracle library with its Makefile (gcc)."""
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB_PATH
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        _lib = ctypes.CDLL(str(LIB_PATH))
+        _declare(_lib)
+    return _lib
+
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+
+
+def _declare(l: ctypes.CDLL) -> None:
+    sig = {
+        "wo_fp16_to_fp32": ([ctypes.c_uint16], ctypes.c_float),
+        "wo_fp32_to_fp16": ([ctypes.c_float], ctypes.c_uint16),
+        "wo_e8m0_to_fp32_half": ([ctypes.c_uint8], ctypes.c_float),
+        "wo_fp16_to_fp32_array": ([_P, _P, _I64], None),
+        "wo_fp32_to_fp16_array": ([_P, _P, _I64], None),
+        "wo_iq2xxs_grid": ([_P], None), "wo_ksigns_iq2xs": ([_P], None),
+        "wo_signs_i8x8": ([_P], None), "wo_kvalues_mxfp4": ([_P], None),
+        "wo_e8m0_half_table": ([_P], None),
+        "wo_weight_row_bytes": ([ctypes.c_int, _I64], ctypes.c_size_t),
+        "wo_act_row_bytes": ([ctypes.c_int, _I64], ctypes.c_size_t),
+        "wo_mul_mat": ([ctypes.c_int, _P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int], None),
+        "wo_mul_mat_q": ([ctypes.c_int, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int], None),
+        "wo_mul_mat_f64": ([ctypes.c_int, _P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int], None),
+        "wo_int_partials": ([ctypes.c_int, _P, _P, _I64, _P], _I64),
+        "wo_max_threads": ([], ctypes.c_int),
+    }
+    for fmt in ("q4_0", "q4_K", "mxfp4", "iq2_xxs", "q8_0", "q8_K"):
+        sig[f"wo_quantize_row_{fmt}"] = ([_P, _P, _I64], None)
+    for fmt in ("q4_0", "q4_K", "mxfp4", "iq2_xxs"):
+        sig[f"wo_dequantize_row_{fmt}"] = ([_P, _P, _I64], None)
+    for name in ("q4_0_q8_0", "q4_K_q8_K", "iq2_xxs_q8_K", "mxfp4_q8_0"):
+        sig[f"wo_vec_dot_{name}"] = ([_P, _P, _I64], ctypes.c_float)
+    for name, (args, res) in sig.items():
+        fn = getattr(l, name)
+        fn.argtypes = args
+        fn.restype = res
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags.c_contiguous
+    return a.ctypes.data
+
+
+def record_bytes(fmt: str, k: int) -> int:
+    elems, nbytes = RECORD[fmt]
+    if k % elems:
+        raise ValueError(f"{fmt} needs K to be a multiple of {elems}")
+    return k // elems * nbytes
+
+
+# ---------------------------------------------------------------- conversions
+def fp16_to_fp32(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().wo_fp16_to_fp32_array(_ptr(h), _ptr(out), h.size)
+    return out
+
+
+def fp32_to_fp16(f: np.ndarray) -> np.ndarray:
+    f = np.ascontiguousarray(f, dtype=np.float32)
+    out = np.empty(f.shape, np.uint16)
+    lib().wo_fp32_to_fp16_array(_ptr(f), _ptr(out), f.size)
+    return out
+
+
+def e8m0_half(e: int) -> float:
+    return lib().wo_e8m0_to_fp32_half(e)
+
+
+# --------------------------------------------------------------------- tables
+def iq2xxs_grid() -> np.ndarray:
+    out = np.empty(2048, np.uint8)
+    lib().wo_iq2xxs_grid(_ptr(out))
+    return out
+
+
+def ksigns_iq2xs() -> np.ndarray:
+    out = np.empty(128, np.uint8)
+    lib().wo_ksigns_iq2xs(_ptr(out))
+    return out
+
+
+def signs_i8x8() -> np.ndarray:
+    out = np.empty(1024, np.int8)
+    lib().wo_signs_i8x8(_ptr(out))
+    return out
+
+
+def kvalues_mxfp4() -> np.ndarray:
+    out = np.empty(16, np.int8)
+    lib().wo_kvalues_mxfp4(_ptr(out))
+    return out
+
+
+def e8m0_half_table() -> np.ndarray:
+    out = np.empty(256, np.float32)
+    lib().wo_e8m0_half_table(_ptr(out))
+    return out
+
+
+# ----------------------------------------------------------------- quantizers
+def quantize(fmt: str, x: np.ndarray, out: np.ndarray | None = None) -> np.ndarray:
+    """Quantize rows of fp32 ``x`` (..., K) into ``fmt`` records (uint8)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    k = x.shape[-1]
+    rows = x.size // k if k else 0
+    rb = record_bytes(fmt, k)
+    if out is None:
+        out = np.zeros(x.shape[:-1] + (rb,), np.uint8)
+    name = {"q4_0": "q4_0", "q4_k": "q4_K", "mxfp4": "mxfp4", "iq2_xxs": "iq2_xxs",
+            "q8_0": "q8_0", "q8_k": "q8_K"}[fmt]
+    fn = getattr(lib(), f"wo_quantize_row_{name}")
+    # one call over all rows: records never straddle rows
+    fn(_ptr(x), _ptr(out), rows * k)
+    return out
+
+
+def dequantize(fmt: str, w: np.ndarray, k: int) -> np.ndarray:
+    """Dequantize ``w`` (..., row_bytes) of ``fmt`` into fp32 (..., k)."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    rb = record_bytes(fmt, k)
+    rows = w.size // rb if rb else 0
+    out = np.empty(w.shape[:-1] + (k,), np.float32)
+    name = {"q4_0": "q4_0", "q4_k": "q4_K", "mxfp4": "mxfp4", "iq2_xxs": "iq2_xxs"}[fmt]
+    getattr(lib(), f"wo_dequantize_row_{name}")(_ptr(w), _ptr(out), rows * k)
+    return out
+
+
+_VEC_DOT = {"q4_0": "q4_0_q8_0", "q4_k": "q4_K_q8_K", "iq2_xxs": "iq2_xxs_q8_K",
+            "mxfp4": "mxfp4_q8_0"}
+
+
+def vec_dot(fmt: str, w: np.ndarray, x: np.ndarray, k: int) -> float:
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.uint8)
+    return float(getattr(lib(), f"wo_vec_dot_{_VEC_DOT[fmt]}")(_ptr(w), _ptr(x), k))
+
+
+def mul_mat(fmt: str, W: np.ndarray, X: np.ndarray, n: int, k: int, m: int,
+            threads: int = 0, xq: np.ndarray | None = None):
+    """GGML MUL_MAT: returns (Xq, Y) with Y (m, n) fp32."""
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    if xq is None:
+        xq = np.zeros((m, record_bytes(ACT_OF[fmt], k)), np.uint8)
+    y = np.empty((m, n), np.float32)
+    lib().wo_mul_mat(FORMATS[fmt], _ptr(W), _ptr(X), _ptr(xq), _ptr(y), n, k, m, threads)
+    return xq, y
+
+
+def mul_mat_q(fmt: str, W: np.ndarray, Xq: np.ndarray, n: int, k: int, m: int,
+              threads: int = 0) -> np.ndarray:
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    Xq = np.ascontiguousarray(Xq, dtype=np.uint8)
+    y = np.empty((m, n), np.float32)
+    lib().wo_mul_mat_q(FORMATS[fmt], _ptr(W), _ptr(Xq), _ptr(y), n, k, m, threads)
+    return y
+
+
+def mul_mat_f64(fmt: str, W: np.ndarray, Xq: np.ndarray, n: int, k: int, m: int,
+                threads: int = 0):
+    """fp64 re-accumulation of the exact integer partials: (E, A)."""
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    Xq = np.ascontiguousarray(Xq, dtype=np.uint8)
+    e = np.empty((m, n), np.float64)
+    a = np.empty((m, n), np.float64)
+    lib().wo_mul_mat_f64(FORMATS[fmt], _ptr(W), _ptr(Xq), _ptr(e), _ptr(a), n, k, m, threads)
+    return e, a
+
+
+def int_partials(fmt: str, w: np.ndarray, x: np.ndarray, k: int) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.uint8)
+    out = np.empty(9 * (k // 32) + 16, np.int32)
+    n = lib().wo_int_partials(FORMATS[fmt], _ptr(w), _ptr(x), k, _ptr(out))
+    return out[:n].copy()
+
+
+def max_threads() -> int:
+    return int(lib().wo_max_threads())
+
+
+# Tolerance for fp32 outputs against the fp64 re-accumulation E with
+# magnitude A = sum_b |scale_b * P_b|: relative 1e-4 of |E| plus 4e-6 of A
+# (about 64 fp32 ulps of the magnitude: room for the fp32 rounding of up to
+# ~90 block terms in any summation order).
+REL_TOL = 1e-4
+MAG_TOL = 4e-6
+
+
+def within_tolerance(y: np.ndarray, e: np.ndarray, a: np.ndarray) -> np.ndarray:
+    y = np.asarray(y, np.float64)
+    return np.isfinite(y) & (np.abs(y - e) <= REL_TOL * np.abs(e) + MAG_TOL * a)
+
+
+def seeded_normal(seed: int, shape, sigma: float = 1.0) -> np.ndarray:
+    """Counter-based seeded N(0, sigma^2) fp32 (numpy PCG64 + Box-Muller)."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    return (rng.standard_normal(size=shape, dtype=np.float64) * sigma).astype(np.float32)

@@ -1,0 +1,911 @@
+/*
+ * CPU oracle for the quantized mul_mat hot path -- TEST INFRASTRUCTURE ONLY.
+ *
+ * Restates, function by function, the GGML CPU code that Weft's repro
+ * harnesses call as their oracle.  Every function cites the vendored GGML
+ * file:line it follows (paths relative to
+ * /root/reference/source/c/ggml/llama.cpp/ggml/src/).  Built with
+ * -ffp-contract=off so that every product is rounded to fp32 before it is
+ * added, as the scalar C semantics of those functions state.
+ *
+ * Pinning (see tests/test_oracle.py):
+ *   fp16 / e8m0 conversions .... numpy float16 and ldexp (library routines)
+ *   tables ...................... fixtures parsed from ggml-common.h text
+ *   dequantizers ................ closed-form per-element brute force
+ *   Q8 quantizers ............... known-answer edge cases + invariants
+ *   vec_dots / mul_mat .......... fp64 re-accumulation through an independent
+ *                                 numpy dequantize-then-dot path
+ *   weight quantizers ........... round-trip error bounds (input generators;
+ *                                 the IQ2_XXS one is NOT GGML's algorithm:
+ *                                 parity unpinned, see its comment)
+ */
+#include "weft_oracle.h"
+
+#include <math.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define QK4_0 32
+#define QK8_0 32
+#define QK_MXFP4 32
+#define QK_K 256
+
+#define Q4_0_BYTES 18
+#define Q8_0_BYTES 34
+#define MXFP4_BYTES 17
+#define Q4_K_BYTES 144
+#define Q8_K_BYTES 292
+#define IQ2_XXS_BYTES 66
+
+static inline uint32_t f32_bits(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+}
+static inline float bits_f32(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+static inline uint16_t rd16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+static inline void wr16(uint8_t *p, uint16_t v) {
+  p[0] = (uint8_t)v;
+  p[1] = (uint8_t)(v >> 8);
+}
+static inline uint32_t rd32(const uint8_t *p) {
+  return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+static inline float rdf32(const uint8_t *p) { return bits_f32(rd32(p)); }
+static inline void wrf32(uint8_t *p, float f) {
+  uint32_t u = f32_bits(f);
+  p[0] = (uint8_t)u;
+  p[1] = (uint8_t)(u >> 8);
+  p[2] = (uint8_t)(u >> 16);
+  p[3] = (uint8_t)(u >> 24);
+}
+
+/* ------------------------------------------------------------------------
+ * IEEE binary16 <-> binary32.  GGML's ggml_compute_fp16_to_fp32 /
+ * ggml_compute_fp32_to_fp16 (ggml-impl.h:384-431) compute the exact widening
+ * and round-to-nearest-even narrowing (NaN -> 0x7E00 with the sign kept).
+ * Written here from the IEEE 754 definition with integer arithmetic.
+ * ---------------------------------------------------------------------- */
+float wo_fp16_to_fp32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t exp = (h >> 10) & 0x1fu;
+  const uint32_t man = h & 0x3ffu;
+  if (exp == 0) {
+    /* zero or subnormal: man * 2^-24, exact in fp32 */
+    const float v = (float)man * 0x1p-24f;
+    return bits_f32(sign | f32_bits(v));
+  }
+  if (exp == 31) return bits_f32(sign | 0x7f800000u | (man << 13));
+  return bits_f32(sign | ((exp + 112u) << 23) | (man << 13));
+}
+
+uint16_t wo_fp32_to_fp16(float f) {
+  const uint32_t x = f32_bits(f);
+  const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+  const uint32_t ax = x & 0x7fffffffu;
+  if (ax > 0x7f800000u) return sign | 0x7e00u; /* NaN */
+  if (ax == 0x7f800000u) return sign | 0x7c00u;
+  const int e = (int)(ax >> 23) - 127 + 15; /* biased fp16 exponent */
+  uint32_t m = ax & 0x7fffffu;
+  if (e >= 31) return sign | 0x7c00u; /* overflow, may be un-rounded below */
+  if (e <= 0) {
+    /* subnormal fp16 (or zero): value = m' * 2^(e-1-23+... ) */
+    if ((ax >> 23) == 0 && m == 0) return sign;
+    m |= ((ax >> 23) ? 0x800000u : 0u);
+    const int shift = 14 - e; /* 13 mantissa bits dropped + (1 - e) */
+    if (shift >= 32) return sign;
+    const uint32_t res = m >> shift;
+    const uint32_t rem = m & ((1u << shift) - 1u);
+    const uint32_t half = 1u << (shift - 1);
+    uint32_t r = res;
+    if (rem > half || (rem == half && (res & 1u))) r += 1;
+    return sign | (uint16_t)r;
+  }
+  uint32_t r = ((uint32_t)e << 10) | (m >> 13);
+  const uint32_t rem = m & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) r += 1; /* may carry to inf */
+  return sign | (uint16_t)r;
+}
+
+/* ggml_e8m0_to_fp32_half, ggml-impl.h:477-495: 2^(e-128); e<2 are fp32
+ * subnormals. */
+float wo_e8m0_to_fp32_half(uint8_t e) {
+  const uint32_t bits = e < 2 ? (0x00200000u << e) : ((uint32_t)(e - 1) << 23);
+  return bits_f32(bits);
+}
+
+void wo_fp16_to_fp32_array(const uint16_t *h, float *out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = wo_fp16_to_fp32(h[i]);
+}
+void wo_fp32_to_fp16_array(const float *f, uint16_t *out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = wo_fp32_to_fp16(f[i]);
+}
+
+/* ------------------------------------------------------------------------
+ * Tables.
+ * iq2xxs_grid (ggml-common.h:550-615) is the 256 entries of
+ * kgrid_2bit_256 (ggml-quants.c:2787-2804) expanded lane by lane, two bits
+ * per lane, through {0 -> 0x08, 1 -> 0x19, 2 -> 0x2b}.
+ * ksigns_iq2xs (ggml-common.h:503-512) is i | parity(i) << 7, so each 8-wide
+ * sign pattern has an even number of minus signs.
+ * ---------------------------------------------------------------------- */
+static const uint16_t kIq2xxsCodes[256] = {
+    0,     2,     5,     8,     10,    17,    20,    32,    34,    40,    42,    65,    68,    80,    88,    97,
+    100,   128,   130,   138,   162,   257,   260,   272,   277,   320,   388,   408,   512,   514,   546,   642,
+    1025,  1028,  1040,  1057,  1060,  1088,  1090,  1096,  1120,  1153,  1156,  1168,  1188,  1280,  1282,  1288,
+    1312,  1350,  1385,  1408,  1425,  1545,  1552,  1600,  1668,  1700,  2048,  2053,  2056,  2068,  2088,  2113,
+    2116,  2128,  2130,  2184,  2308,  2368,  2562,  2580,  4097,  4100,  4112,  4129,  4160,  4192,  4228,  4240,
+    4245,  4352,  4360,  4384,  4432,  4442,  4480,  4644,  4677,  5120,  5128,  5152,  5157,  5193,  5248,  5400,
+    5474,  5632,  5654,  6145,  6148,  6160,  6208,  6273,  6400,  6405,  6560,  6737,  8192,  8194,  8202,  8260,
+    8289,  8320,  8322,  8489,  8520,  8704,  8706,  9217,  9220,  9232,  9280,  9302,  9472,  9537,  9572,  9872,
+    10248, 10272, 10388, 10820, 16385, 16388, 16400, 16408, 16417, 16420, 16448, 16456, 16470, 16480, 16513, 16516,
+    16528, 16640, 16672, 16737, 16768, 16773, 16897, 16912, 16968, 16982, 17000, 17408, 17416, 17440, 17536, 17561,
+    17682, 17700, 17920, 18433, 18436, 18448, 18496, 18501, 18688, 18776, 18785, 18818, 19013, 19088, 20480, 20488,
+    20497, 20505, 20512, 20608, 20616, 20740, 20802, 20900, 21137, 21648, 21650, 21770, 22017, 22100, 22528, 22545,
+    22553, 22628, 22848, 23048, 24580, 24592, 24640, 24680, 24832, 24917, 25112, 25184, 25600, 25605, 25872, 25874,
+    25988, 26690, 32768, 32770, 32778, 32833, 32898, 33028, 33048, 33088, 33297, 33793, 33796, 33808, 33813, 33856,
+    33888, 34048, 34118, 34196, 34313, 34368, 34400, 34818, 35076, 35345, 36868, 36880, 36900, 36928, 37025, 37142,
+    37248, 37445, 37888, 37922, 37956, 38225, 39041, 39200, 40962, 41040, 41093, 41225, 41472, 42008, 43088, 43268,
+};
+
+void wo_iq2xxs_grid(uint8_t out[2048]) {
+  static const uint8_t lane_value[4] = {0x08, 0x19, 0x2b, 0x00};
+  for (int i = 0; i < 256; ++i)
+    for (int j = 0; j < 8; ++j) out[8 * i + j] = lane_value[(kIq2xxsCodes[i] >> (2 * j)) & 3];
+}
+
+void wo_ksigns_iq2xs(uint8_t out[128]) {
+  for (int i = 0; i < 128; ++i) out[i] = (uint8_t)(i | ((__builtin_popcount(i) & 1) << 7));
+}
+
+void wo_signs_i8x8(int8_t out[1024]) {
+  uint8_t ks[128];
+  wo_ksigns_iq2xs(ks);
+  for (int i = 0; i < 128; ++i)
+    for (int j = 0; j < 8; ++j) out[8 * i + j] = (ks[i] >> j) & 1 ? -1 : 1;
+}
+
+/* kvalues_mxfp4 (ggml-common.h:1116-1118): twice the E2M1 values. */
+void wo_kvalues_mxfp4(int8_t out[16]) {
+  static const float e2m1[8] = {0.f, 0.5f, 1.f, 1.5f, 2.f, 3.f, 4.f, 6.f};
+  for (int i = 0; i < 16; ++i) out[i] = (int8_t)((i & 8 ? -2.f : 2.f) * e2m1[i & 7]);
+}
+
+void wo_e8m0_half_table(float out[256]) {
+  for (int e = 0; e < 256; ++e) out[e] = wo_e8m0_to_fp32_half((uint8_t)e);
+}
+
+/* nearest_int, ggml-quants.c:563-568: round half to even of a value that
+ * has already been rounded to fp32 (|v| <= 2^22). */
+static inline int nearest_int(float v) {
+  const float biased = v + 12582912.f;
+  return (int)(f32_bits(biased) & 0x007fffffu) - 0x00400000;
+}
+
+/* get_scale_min_k4, ggml-quants.c:822-829 */
+static inline void scale_min_k4(int j, const uint8_t *q, uint8_t *sc, uint8_t *m) {
+  if (j < 4) {
+    *sc = q[j] & 63;
+    *m = q[j + 4] & 63;
+  } else {
+    *sc = (uint8_t)((q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4));
+    *m = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+  }
+}
+
+/* ------------------------------------------------------------------------
+ * Weight quantizers (input generators)
+ * ---------------------------------------------------------------------- */
+
+/* quantize_row_q4_0_ref, ggml-quants.c:75-110 */
+void wo_quantize_row_q4_0(const float *x, uint8_t *y, int64_t k) {
+  const int64_t nb = k / QK4_0;
+  for (int64_t i = 0; i < nb; ++i) {
+    const float *xb = x + i * QK4_0;
+    uint8_t *rec = y + i * Q4_0_BYTES;
+    float amax = 0.f, max = 0.f;
+    for (int j = 0; j < QK4_0; ++j) {
+      if (amax < fabsf(xb[j])) {
+        amax = fabsf(xb[j]);
+        max = xb[j];
+      }
+    }
+    const float d = max / -8;
+    const float id = d ? 1.0f / d : 0.0f;
+    wr16(rec, wo_fp32_to_fp16(d));
+    for (int j = 0; j < QK4_0 / 2; ++j) {
+      const float x0 = xb[j] * id;
+      const float x1 = xb[QK4_0 / 2 + j] * id;
+      int8_t t0 = (int8_t)(x0 + 8.5f);
+      int8_t t1 = (int8_t)(x1 + 8.5f);
+      const uint8_t q0 = (uint8_t)(t0 < 15 ? t0 : 15);
+      const uint8_t q1 = (uint8_t)(t1 < 15 ? t1 : 15);
+      rec[2 + j] = (uint8_t)(q0 | (q1 << 4));
+    }
+  }
+}
+
+/* best_index_mxfp4 / quantize_row_mxfp4_ref, ggml-quants.c:299-344 */
+void wo_quantize_row_mxfp4(const float *x, uint8_t *y, int64_t k) {
+  int8_t kv[16];
+  wo_kvalues_mxfp4(kv);
+  const int64_t nb = k / QK_MXFP4;
+  for (int64_t i = 0; i < nb; ++i) {
+    const float *xb = x + i * QK_MXFP4;
+    uint8_t *rec = y + i * MXFP4_BYTES;
+    float amax = 0.f;
+    for (int j = 0; j < QK_MXFP4; ++j)
+      if (amax < fabsf(xb[j])) amax = fabsf(xb[j]);
+    const uint8_t e = amax > 0.0f ? (uint8_t)(floorf(log2f(amax)) - 2 + 127) : 0;
+    const float d = wo_e8m0_to_fp32_half(e);
+    rec[0] = e;
+    for (int j = 0; j < QK_MXFP4 / 2; ++j) {
+      uint8_t best[2];
+      for (int h = 0; h < 2; ++h) {
+        const float v = xb[h * (QK_MXFP4 / 2) + j];
+        int bi = 0;
+        float be = fabsf(kv[0] * d - v);
+        for (int c = 1; c < 16; ++c) {
+          const float err = fabsf(kv[c] * d - v);
+          if (err < be) {
+            bi = c;
+            be = err;
+          }
+        }
+        best[h] = (uint8_t)bi;
+      }
+      rec[1 + j] = (uint8_t)(best[0] | (best[1] << 4));
+    }
+  }
+}
+
+/* make_qkx2_quants, ggml-quants.c:741-820 (use_mad = false path only) */
+static float make_qkx2(int n, int nmax, const float *x, const float *weights, uint8_t *L,
+                       float *the_min, uint8_t *Laux, float rmin, float rdelta, int nstep) {
+  float min = x[0], max = x[0];
+  float sum_w = weights[0];
+  float sum_x = sum_w * x[0];
+  for (int i = 1; i < n; ++i) {
+    if (x[i] < min) min = x[i];
+    if (x[i] > max) max = x[i];
+    const float w = weights[i];
+    sum_w += w;
+    sum_x += w * x[i];
+  }
+  if (min > 0) min = 0;
+  if (max == min) {
+    for (int i = 0; i < n; ++i) L[i] = 0;
+    *the_min = -min;
+    return 0.f;
+  }
+  float iscale = nmax / (max - min);
+  float scale = 1 / iscale;
+  float best_error = 0;
+  for (int i = 0; i < n; ++i) {
+    int l = nearest_int(iscale * (x[i] - min));
+    l = l < 0 ? 0 : (l > nmax ? nmax : l);
+    L[i] = (uint8_t)l;
+    float diff = scale * L[i] + min - x[i];
+    diff = diff * diff;
+    best_error += weights[i] * diff;
+  }
+  if (nstep < 1) {
+    *the_min = -min;
+    return scale;
+  }
+  for (int is = 0; is <= nstep; ++is) {
+    iscale = (rmin + rdelta * is + nmax) / (max - min);
+    float sum_l = 0, sum_l2 = 0, sum_xl = 0;
+    for (int i = 0; i < n; ++i) {
+      int l = nearest_int(iscale * (x[i] - min));
+      l = l < 0 ? 0 : (l > nmax ? nmax : l);
+      Laux[i] = (uint8_t)l;
+      const float w = weights[i];
+      sum_l += w * l;
+      sum_l2 += w * l * l;
+      sum_xl += w * l * x[i];
+    }
+    const float D = sum_w * sum_l2 - sum_l * sum_l;
+    if (D > 0) {
+      float this_scale = (sum_w * sum_xl - sum_x * sum_l) / D;
+      float this_min = (sum_l2 * sum_x - sum_l * sum_xl) / D;
+      if (this_min > 0) {
+        this_min = 0;
+        this_scale = sum_xl / sum_l2;
+      }
+      float cur_error = 0;
+      for (int i = 0; i < n; ++i) {
+        float diff = this_scale * Laux[i] + this_min - x[i];
+        diff = diff * diff;
+        cur_error += weights[i] * diff;
+      }
+      if (cur_error < best_error) {
+        for (int i = 0; i < n; ++i) L[i] = Laux[i];
+        best_error = cur_error;
+        scale = this_scale;
+        min = this_min;
+      }
+    }
+  }
+  *the_min = -min;
+  return scale;
+}
+
+/* quantize_row_q4_K_ref, ggml-quants.c:1399-1469 */
+void wo_quantize_row_q4_K(const float *x, uint8_t *y, int64_t k) {
+  const int64_t nb = k / QK_K;
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < nb; ++i) {
+    uint8_t L[QK_K], Laux[32];
+    float weights[32], mins[QK_K / 32], scales[QK_K / 32];
+    const float *xb = x + i * QK_K;
+    uint8_t *rec = y + i * Q4_K_BYTES;
+    uint8_t *sc12 = rec + 4;
+    memset(sc12, 0, 12);
+    float max_scale = 0, max_min = 0;
+    for (int j = 0; j < QK_K / 32; ++j) {
+      float sum_x2 = 0;
+      for (int l = 0; l < 32; ++l) sum_x2 += xb[32 * j + l] * xb[32 * j + l];
+      const float av_x = sqrtf(sum_x2 / 32);
+      for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(xb[32 * j + l]);
+      scales[j] = make_qkx2(32, 15, xb + 32 * j, weights, L + 32 * j, &mins[j], Laux, -1.f, 0.1f, 20);
+      if (scales[j] > max_scale) max_scale = scales[j];
+      if (mins[j] > max_min) max_min = mins[j];
+    }
+    const float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
+    const float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
+    for (int j = 0; j < QK_K / 32; ++j) {
+      uint8_t ls = (uint8_t)nearest_int(inv_scale * scales[j]);
+      uint8_t lm = (uint8_t)nearest_int(inv_min * mins[j]);
+      ls = ls < 63 ? ls : 63;
+      lm = lm < 63 ? lm : 63;
+      if (j < 4) {
+        sc12[j] = ls;
+        sc12[j + 4] = lm;
+      } else {
+        sc12[j + 4] = (uint8_t)((ls & 0xF) | ((lm & 0xF) << 4));
+        sc12[j - 4] |= (uint8_t)((ls >> 4) << 6);
+        sc12[j - 0] |= (uint8_t)((lm >> 4) << 6);
+      }
+    }
+    wr16(rec + 0, wo_fp32_to_fp16(max_scale / 63.f));
+    wr16(rec + 2, wo_fp32_to_fp16(max_min / 63.f));
+    for (int j = 0; j < QK_K / 32; ++j) {
+      uint8_t sc, m;
+      scale_min_k4(j, sc12, &sc, &m);
+      const float d = wo_fp16_to_fp32(rd16(rec)) * sc;
+      if (!d) continue;
+      const float dm = wo_fp16_to_fp32(rd16(rec + 2)) * m;
+      for (int ii = 0; ii < 32; ++ii) {
+        int l = nearest_int((xb[32 * j + ii] + dm) / d);
+        l = l < 0 ? 0 : (l > 15 ? 15 : l);
+        L[32 * j + ii] = (uint8_t)l;
+      }
+    }
+    uint8_t *q = rec + 16;
+    for (int j = 0; j < QK_K; j += 64) {
+      for (int l = 0; l < 32; ++l) q[l] = (uint8_t)(L[j + l] | (L[j + l + 32] << 4));
+      q += 32;
+    }
+  }
+}
+
+/* IQ2_XXS input generator.  NOT GGML's quantize_iq2_xxs: that one needs the
+ * iq2xs_init_impl neighbour tables and an importance matrix
+ * (ggml-quants.c:2781-3186, :3198-3398).  This one makes valid records of
+ * the same distribution by exhaustive nearest-grid search: per 32-group an
+ * amax-derived 4-bit scale, per 8-chunk the sign pattern of x with an even
+ * number of minus signs (the smallest |x| is flipped when needed) and the
+ * grid row with the least squared error.  Parity unpinned as a quantizer;
+ * the GPU path only ever consumes its bytes. */
+void wo_quantize_row_iq2_xxs(const float *x, uint8_t *y, int64_t k) {
+  uint8_t grid[2048];
+  wo_iq2xxs_grid(grid);
+  const int64_t nb = k / QK_K;
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < nb; ++i) {
+    const float *xb = x + i * QK_K;
+    uint8_t *rec = y + i * IQ2_XXS_BYTES;
+    float gmax[8], tmax = 0.f;
+    for (int g = 0; g < 8; ++g) {
+      float a = 0.f;
+      for (int l = 0; l < 32; ++l) a = fmaxf(a, fabsf(xb[32 * g + l]));
+      gmax[g] = a / 43.f; /* wanted element scale: largest |x| on grid value 43 */
+      tmax = fmaxf(tmax, gmax[g]);
+    }
+    /* element scale = d * (2s+1) / 8, s <= 15 */
+    const uint16_t dh = wo_fp32_to_fp16(tmax * 8.f / 31.f);
+    const float d = wo_fp16_to_fp32(dh);
+    wr16(rec, dh);
+    for (int g = 0; g < 8; ++g) {
+      int s = 0;
+      if (d > 0.f) {
+        s = (int)lrintf((8.f * gmax[g] / d - 1.f) * 0.5f);
+        s = s < 0 ? 0 : (s > 15 ? 15 : s);
+      }
+      const float db = d * (0.5f + s) * 0.25f;
+      uint32_t idx_word = 0, meta = (uint32_t)s << 28;
+      for (int c = 0; c < 4; ++c) {
+        const float *xc = xb + 32 * g + 8 * c;
+        int neg = 0, nneg = 0, smallest = 0;
+        for (int j = 0; j < 8; ++j) {
+          if (xc[j] < 0) {
+            neg |= 1 << j;
+            ++nneg;
+          }
+          if (fabsf(xc[j]) < fabsf(xc[smallest])) smallest = j;
+        }
+        if (nneg & 1) neg ^= 1 << smallest;
+        int best = 0;
+        double best_err = INFINITY;
+        for (int r = 0; r < 256; ++r) {
+          double err = 0;
+          for (int j = 0; j < 8; ++j) {
+            const double v = (double)db * grid[8 * r + j] * ((neg >> j) & 1 ? -1.0 : 1.0);
+            err += (v - xc[j]) * (v - xc[j]);
+          }
+          if (err < best_err) {
+            best_err = err;
+            best = r;
+          }
+        }
+        idx_word |= (uint32_t)best << (8 * c);
+        meta |= (uint32_t)(neg & 127) << (7 * c);
+      }
+      uint8_t *qs = rec + 2 + 8 * g;
+      for (int b = 0; b < 4; ++b) qs[b] = (uint8_t)(idx_word >> (8 * b));
+      for (int b = 0; b < 4; ++b) qs[4 + b] = (uint8_t)(meta >> (8 * b));
+    }
+  }
+}
+
+/* ------------------------------------------------------------------------
+ * Activation quantizers
+ * ---------------------------------------------------------------------- */
+
+/* quantize_row_q8_0_ref, ggml-quants.c:238-261: d = amax/127, q = roundf(x/d)
+ * (round half away from zero), d stored as fp16. */
+void wo_quantize_row_q8_0(const float *x, uint8_t *y, int64_t k) {
+  const int64_t nb = k / QK8_0;
+  for (int64_t i = 0; i < nb; ++i) {
+    const float *xb = x + i * QK8_0;
+    uint8_t *rec = y + i * Q8_0_BYTES;
+    float amax = 0.0f;
+    for (int j = 0; j < QK8_0; ++j) amax = fmaxf(amax, fabsf(xb[j]));
+    const float d = amax / 127;
+    const float id = d ? 1.0f / d : 0.0f;
+    wr16(rec, wo_fp32_to_fp16(d));
+    for (int j = 0; j < QK8_0; ++j) rec[2 + j] = (uint8_t)(int8_t)roundf(xb[j] * id);
+  }
+}
+
+/* quantize_row_q8_K_ref, ggml-quants.c:2696-2733: the signed value at the
+ * first index of the largest |x| sets iscale = -127/max; q = RNE(iscale*x)
+ * capped at 127; bsums = sums of 16; d = 1/iscale.  An all-zero block writes
+ * d = 0 and qs = 0 and leaves bsums as they were. */
+void wo_quantize_row_q8_K(const float *x, uint8_t *y, int64_t k) {
+  const int64_t nb = k / QK_K;
+  for (int64_t i = 0; i < nb; ++i) {
+    const float *xb = x + i * QK_K;
+    uint8_t *rec = y + i * Q8_K_BYTES;
+    float max = 0, amax = 0;
+    for (int j = 0; j < QK_K; ++j) {
+      const float ax = fabsf(xb[j]);
+      if (ax > amax) {
+        amax = ax;
+        max = xb[j];
+      }
+    }
+    if (!amax) {
+      wrf32(rec, 0.f);
+      memset(rec + 4, 0, QK_K);
+      continue;
+    }
+    const float iscale = -127.f / max;
+    int8_t *qs = (int8_t *)(rec + 4);
+    for (int j = 0; j < QK_K; ++j) {
+      const int v = nearest_int(iscale * xb[j]);
+      qs[j] = (int8_t)(v < 127 ? v : 127);
+    }
+    for (int j = 0; j < QK_K / 16; ++j) {
+      int sum = 0;
+      for (int ii = 0; ii < 16; ++ii) sum += qs[16 * j + ii];
+      wr16(rec + 260 + 2 * j, (uint16_t)(int16_t)sum);
+    }
+    wrf32(rec, 1 / iscale);
+  }
+}
+
+/* ------------------------------------------------------------------------
+ * Row dequantizers
+ * ---------------------------------------------------------------------- */
+
+/* dequantize_row_q4_0, ggml-quants.c:401-419 */
+void wo_dequantize_row_q4_0(const uint8_t *x, float *y, int64_t k) {
+  const int64_t nb = k / QK4_0;
+  for (int64_t i = 0; i < nb; ++i) {
+    const uint8_t *rec = x + i * Q4_0_BYTES;
+    const float d = wo_fp16_to_fp32(rd16(rec));
+    for (int j = 0; j < QK4_0 / 2; ++j) {
+      const int x0 = (rec[2 + j] & 0x0F) - 8;
+      const int x1 = (rec[2 + j] >> 4) - 8;
+      y[i * QK4_0 + j] = x0 * d;
+      y[i * QK4_0 + j + QK4_0 / 2] = x1 * d;
+    }
+  }
+}
+
+/* dequantize_row_mxfp4, ggml-quants.c:511-529 */
+void wo_dequantize_row_mxfp4(const uint8_t *x, float *y, int64_t k) {
+  int8_t kv[16];
+  wo_kvalues_mxfp4(kv);
+  const int64_t nb = k / QK_MXFP4;
+  for (int64_t i = 0; i < nb; ++i) {
+    const uint8_t *rec = x + i * MXFP4_BYTES;
+    const float d = wo_e8m0_to_fp32_half(rec[0]);
+    for (int j = 0; j < QK_MXFP4 / 2; ++j) {
+      y[i * QK_MXFP4 + j] = kv[rec[1 + j] & 0x0F] * d;
+      y[i * QK_MXFP4 + j + QK_MXFP4 / 2] = kv[rec[1 + j] >> 4] * d;
+    }
+  }
+}
+
+/* dequantize_row_q4_K, ggml-quants.c:1471-1493 */
+void wo_dequantize_row_q4_K(const uint8_t *x, float *y, int64_t k) {
+  const int64_t nb = k / QK_K;
+  for (int64_t i = 0; i < nb; ++i) {
+    const uint8_t *rec = x + i * Q4_K_BYTES;
+    const uint8_t *q = rec + 16;
+    const float d = wo_fp16_to_fp32(rd16(rec));
+    const float min = wo_fp16_to_fp32(rd16(rec + 2));
+    int is = 0;
+    for (int j = 0; j < QK_K; j += 64) {
+      uint8_t sc, m;
+      scale_min_k4(is + 0, rec + 4, &sc, &m);
+      const float d1 = d * sc, m1 = min * m;
+      scale_min_k4(is + 1, rec + 4, &sc, &m);
+      const float d2 = d * sc, m2 = min * m;
+      for (int l = 0; l < 32; ++l) *y++ = d1 * (q[l] & 0xF) - m1;
+      for (int l = 0; l < 32; ++l) *y++ = d2 * (q[l] >> 4) - m2;
+      q += 32;
+      is += 2;
+    }
+  }
+}
+
+/* dequantize_row_iq2_xxs, ggml-quants.c:2416-2440 */
+void wo_dequantize_row_iq2_xxs(const uint8_t *x, float *y, int64_t k) {
+  uint8_t grid[2048], ks[128];
+  wo_iq2xxs_grid(grid);
+  wo_ksigns_iq2xs(ks);
+  const int64_t nb = k / QK_K;
+  for (int64_t i = 0; i < nb; ++i) {
+    const uint8_t *rec = x + i * IQ2_XXS_BYTES;
+    const float d = wo_fp16_to_fp32(rd16(rec));
+    for (int ib32 = 0; ib32 < QK_K / 32; ++ib32) {
+      const uint8_t *qs = rec + 2 + 8 * ib32;
+      const uint32_t meta = rd32(qs + 4);
+      const float db = d * (0.5f + (meta >> 28)) * 0.25f;
+      for (int l = 0; l < 4; ++l) {
+        const uint8_t *g = grid + 8 * qs[l];
+        const uint8_t signs = ks[(meta >> (7 * l)) & 127];
+        for (int j = 0; j < 8; ++j) y[j] = db * g[j] * (signs & (1u << j) ? -1.f : 1.f);
+        y += 8;
+      }
+    }
+  }
+}
+
+/* ------------------------------------------------------------------------
+ * vec_dots (ggml-cpu/quants.c generic bodies)
+ * ---------------------------------------------------------------------- */
+
+/* ggml_vec_dot_q4_0_q8_0_generic, ggml-cpu/quants.c:174-208 */
+float wo_vec_dot_q4_0_q8_0(const uint8_t *w, const uint8_t *x, int64_t k) {
+  const int64_t nb = k / QK8_0;
+  float sumf = 0;
+  for (int64_t ib = 0; ib < nb; ++ib) {
+    const uint8_t *wr = w + ib * Q4_0_BYTES;
+    const uint8_t *xr = x + ib * Q8_0_BYTES;
+    const int8_t *xq = (const int8_t *)(xr + 2);
+    int sumi0 = 0, sumi1 = 0;
+    for (int j = 0; j < QK8_0 / 2; ++j) {
+      const int v0 = (wr[2 + j] & 0x0F) - 8;
+      const int v1 = (wr[2 + j] >> 4) - 8;
+      sumi0 += v0 * xq[j];
+      sumi1 += v1 * xq[j + QK8_0 / 2];
+    }
+    const int sumi = sumi0 + sumi1;
+    sumf += sumi * wo_fp16_to_fp32(rd16(wr)) * wo_fp16_to_fp32(rd16(xr));
+  }
+  return sumf;
+}
+
+/* ggml_vec_dot_mxfp4_q8_0_generic, ggml-cpu/quants.c:247-276 */
+float wo_vec_dot_mxfp4_q8_0(const uint8_t *w, const uint8_t *x, int64_t k) {
+  int8_t kv[16];
+  wo_kvalues_mxfp4(kv);
+  const int64_t nb = k / QK_MXFP4;
+  float sumf = 0;
+  for (int64_t ib = 0; ib < nb; ++ib) {
+    const uint8_t *wr = w + ib * MXFP4_BYTES;
+    const uint8_t *xr = x + ib * Q8_0_BYTES;
+    const int8_t *xq = (const int8_t *)(xr + 2);
+    const float d = wo_fp16_to_fp32(rd16(xr)) * wo_e8m0_to_fp32_half(wr[0]);
+    int sumi1 = 0, sumi2 = 0;
+    for (int j = 0; j < QK_MXFP4 / 2; ++j) {
+      sumi1 += xq[j] * kv[wr[1 + j] & 0xf];
+      sumi2 += xq[j + QK_MXFP4 / 2] * kv[wr[1 + j] >> 4];
+    }
+    sumf += d * (sumi1 + sumi2);
+  }
+  return sumf;
+}
+
+/* ggml_vec_dot_q4_K_q8_K_generic, ggml-cpu/quants.c:645-718.  The eight
+ * float lanes of `sums` are kept so the rounding order is GGML's. */
+float wo_vec_dot_q4_K_q8_K(const uint8_t *w, const uint8_t *x, int64_t k) {
+  const int64_t nb = k / QK_K;
+  float sums[8] = {0};
+  float sumf = 0;
+  int8_t aux8[QK_K];
+  for (int64_t i = 0; i < nb; ++i) {
+    const uint8_t *wr = w + i * Q4_K_BYTES;
+    const uint8_t *xr = x + i * Q8_K_BYTES;
+    const uint8_t *q4 = wr + 16;
+    const int8_t *q8 = (const int8_t *)(xr + 4);
+    int32_t aux32[8] = {0};
+    int8_t *a = aux8;
+    for (int j = 0; j < QK_K / 64; ++j) {
+      for (int l = 0; l < 32; ++l) a[l] = (int8_t)(q4[l] & 0xF);
+      a += 32;
+      for (int l = 0; l < 32; ++l) a[l] = (int8_t)(q4[l] >> 4);
+      a += 32;
+      q4 += 32;
+    }
+    uint8_t scales[8], mins[8];
+    for (int j = 0; j < 8; ++j) scale_min_k4(j, wr + 4, &scales[j], &mins[j]);
+    int sumi = 0;
+    for (int j = 0; j < QK_K / 16; ++j) sumi += (int16_t)rd16(xr + 260 + 2 * j) * mins[j / 2];
+    a = aux8;
+    for (int j = 0; j < QK_K / 32; ++j) {
+      const int32_t scale = scales[j];
+      for (int c = 0; c < 4; ++c) {
+        for (int l = 0; l < 8; ++l) aux32[l] += scale * (int16_t)(q8[l] * a[l]);
+        q8 += 8;
+        a += 8;
+      }
+    }
+    const float d = wo_fp16_to_fp32(rd16(wr)) * rdf32(xr);
+    for (int l = 0; l < 8; ++l) sums[l] += d * aux32[l];
+    const float dmin = wo_fp16_to_fp32(rd16(wr + 2)) * rdf32(xr);
+    sumf -= dmin * sumi;
+  }
+  for (int l = 0; l < 8; ++l) sumf += sums[l];
+  return sumf;
+}
+
+/* ggml_vec_dot_iq2_xxs_q8_K_generic, ggml-cpu/quants.c:855-895 */
+float wo_vec_dot_iq2_xxs_q8_K(const uint8_t *w, const uint8_t *x, int64_t k) {
+  uint8_t grid[2048], ks[128];
+  wo_iq2xxs_grid(grid);
+  wo_ksigns_iq2xs(ks);
+  const int64_t nb = k / QK_K;
+  float sumf = 0.f;
+  for (int64_t i = 0; i < nb; ++i) {
+    const uint8_t *wr = w + i * IQ2_XXS_BYTES;
+    const uint8_t *xr = x + i * Q8_K_BYTES;
+    const float d = wo_fp16_to_fp32(rd16(wr)) * rdf32(xr);
+    const int8_t *q8 = (const int8_t *)(xr + 4);
+    int32_t bsum = 0;
+    for (int ib32 = 0; ib32 < QK_K / 32; ++ib32) {
+      const uint8_t *qs = wr + 2 + 8 * ib32;
+      const uint32_t meta = rd32(qs + 4);
+      const uint32_t ls = 2 * (meta >> 28) + 1;
+      int32_t sumi = 0;
+      for (int l = 0; l < 4; ++l) {
+        const uint8_t *g = grid + 8 * qs[l];
+        const uint8_t signs = ks[(meta >> (7 * l)) & 127];
+        for (int j = 0; j < 8; ++j) sumi += g[j] * q8[j] * (signs & (1u << j) ? -1 : 1);
+        q8 += 8;
+      }
+      bsum += sumi * (int32_t)ls;
+    }
+    sumf += d * bsum;
+  }
+  return 0.125f * sumf;
+}
+
+/* ------------------------------------------------------------------------
+ * MUL_MAT driver and fp64 re-accumulation
+ * ---------------------------------------------------------------------- */
+size_t wo_weight_row_bytes(int fmt, int64_t k) {
+  switch (fmt) {
+  case WO_Q4_0: return (size_t)(k / 32) * Q4_0_BYTES;
+  case WO_Q4_K: return (size_t)(k / 256) * Q4_K_BYTES;
+  case WO_IQ2_XXS: return (size_t)(k / 256) * IQ2_XXS_BYTES;
+  case WO_MXFP4: return (size_t)(k / 32) * MXFP4_BYTES;
+  }
+  return 0;
+}
+
+size_t wo_act_row_bytes(int fmt, int64_t k) {
+  if (fmt == WO_Q4_0 || fmt == WO_MXFP4) return (size_t)(k / 32) * Q8_0_BYTES;
+  return (size_t)(k / 256) * Q8_K_BYTES;
+}
+
+typedef float (*vec_dot_fn)(const uint8_t *, const uint8_t *, int64_t);
+static vec_dot_fn select_vec_dot(int fmt) {
+  switch (fmt) {
+  case WO_Q4_0: return wo_vec_dot_q4_0_q8_0;
+  case WO_Q4_K: return wo_vec_dot_q4_K_q8_K;
+  case WO_IQ2_XXS: return wo_vec_dot_iq2_xxs_q8_K;
+  case WO_MXFP4: return wo_vec_dot_mxfp4_q8_0;
+  }
+  return 0;
+}
+
+int wo_max_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+void wo_mul_mat_q(int fmt, const uint8_t *W, const uint8_t *Xq, float *Y, int64_t N, int64_t K,
+                  int64_t M, int nthreads) {
+  const vec_dot_fn dot = select_vec_dot(fmt);
+  const size_t wrow = wo_weight_row_bytes(fmt, K), xrow = wo_act_row_bytes(fmt, K);
+  if (nthreads <= 0) nthreads = wo_max_threads();
+  (void)nthreads;
+#pragma omp parallel for num_threads(nthreads) schedule(static) collapse(2)
+  for (int64_t m = 0; m < M; ++m)
+    for (int64_t n = 0; n < N; ++n) Y[m * N + n] = dot(W + n * wrow, Xq + m * xrow, K);
+}
+
+void wo_mul_mat(int fmt, const uint8_t *W, const float *X, uint8_t *Xq, float *Y, int64_t N,
+                int64_t K, int64_t M, int nthreads) {
+  const size_t xrow = wo_act_row_bytes(fmt, K);
+  const int q80 = (fmt == WO_Q4_0 || fmt == WO_MXFP4);
+  if (nthreads <= 0) nthreads = wo_max_threads();
+#pragma omp parallel for num_threads(nthreads) schedule(static)
+  for (int64_t m = 0; m < M; ++m) {
+    if (q80)
+      wo_quantize_row_q8_0(X + m * K, Xq + m * xrow, K);
+    else
+      wo_quantize_row_q8_K(X + m * K, Xq + m * xrow, K);
+  }
+  wo_mul_mat_q(fmt, W, Xq, Y, N, K, M, nthreads);
+}
+
+int64_t wo_int_partials(int fmt, const uint8_t *w, const uint8_t *x, int64_t k, int32_t *out) {
+  int64_t n = 0;
+  if (fmt == WO_Q4_0 || fmt == WO_MXFP4) {
+    int8_t kv[16];
+    wo_kvalues_mxfp4(kv);
+    const int64_t nb = k / 32;
+    for (int64_t ib = 0; ib < nb; ++ib) {
+      const uint8_t *wr = w + ib * (fmt == WO_Q4_0 ? Q4_0_BYTES : MXFP4_BYTES);
+      const uint8_t *qs = wr + (fmt == WO_Q4_0 ? 2 : 1);
+      const int8_t *xq = (const int8_t *)(x + ib * Q8_0_BYTES + 2);
+      int32_t s = 0;
+      for (int j = 0; j < 16; ++j) {
+        const int lo = qs[j] & 0xF, hi = qs[j] >> 4;
+        const int v0 = fmt == WO_Q4_0 ? lo - 8 : kv[lo];
+        const int v1 = fmt == WO_Q4_0 ? hi - 8 : kv[hi];
+        s += v0 * xq[j] + v1 * xq[j + 16];
+      }
+      out[n++] = s;
+    }
+  } else if (fmt == WO_Q4_K) {
+    const int64_t nb = k / QK_K;
+    for (int64_t i = 0; i < nb; ++i) {
+      const uint8_t *wr = w + i * Q4_K_BYTES;
+      const uint8_t *xr = x + i * Q8_K_BYTES;
+      const int8_t *q8 = (const int8_t *)(xr + 4);
+      int32_t mn = 0;
+      for (int s = 0; s < 8; ++s) {
+        uint8_t sc, m;
+        scale_min_k4(s, wr + 4, &sc, &m);
+        const uint8_t *q4 = wr + 16 + 32 * (s / 2);
+        int32_t p = 0;
+        for (int l = 0; l < 32; ++l) {
+          const int v = (s & 1) ? (q4[l] >> 4) : (q4[l] & 0xF);
+          p += v * q8[32 * s + l];
+        }
+        out[n++] = p;
+        mn += m * ((int16_t)rd16(xr + 260 + 4 * s) + (int16_t)rd16(xr + 262 + 4 * s));
+      }
+      out[n++] = mn;
+    }
+  } else if (fmt == WO_IQ2_XXS) {
+    uint8_t grid[2048], ks[128];
+    wo_iq2xxs_grid(grid);
+    wo_ksigns_iq2xs(ks);
+    const int64_t nb = k / QK_K;
+    for (int64_t i = 0; i < nb; ++i) {
+      const uint8_t *wr = w + i * IQ2_XXS_BYTES;
+      const int8_t *q8 = (const int8_t *)(x + i * Q8_K_BYTES + 4);
+      int32_t b = 0;
+      for (int g = 0; g < 8; ++g) {
+        const uint8_t *qs = wr + 2 + 8 * g;
+        const uint32_t meta = rd32(qs + 4);
+        int32_t s = 0;
+        for (int l = 0; l < 4; ++l) {
+          const uint8_t sg = ks[(meta >> (7 * l)) & 127];
+          for (int j = 0; j < 8; ++j)
+            s += grid[8 * qs[l] + j] * q8[32 * g + 8 * l + j] * ((sg >> j) & 1 ? -1 : 1);
+        }
+        b += s * (int32_t)(2 * (meta >> 28) + 1);
+      }
+      out[n++] = b;
+    }
+  }
+  return n;
+}
+
+void wo_mul_mat_f64(int fmt, const uint8_t *W, const uint8_t *Xq, double *E, double *A, int64_t N,
+                    int64_t K, int64_t M, int nthreads) {
+  const size_t wrow = wo_weight_row_bytes(fmt, K), xrow = wo_act_row_bytes(fmt, K);
+  if (nthreads <= 0) nthreads = wo_max_threads();
+#pragma omp parallel for num_threads(nthreads) schedule(static) collapse(2)
+  for (int64_t m = 0; m < M; ++m) {
+    for (int64_t n = 0; n < N; ++n) {
+      int32_t parts[9 * (65536 / 256) + 8];
+      const uint8_t *w = W + n * wrow;
+      const uint8_t *x = Xq + m * xrow;
+      double e = 0, a = 0;
+      if (fmt == WO_Q4_0 || fmt == WO_MXFP4) {
+        for (int64_t base = 0; base < K; base += 8192) {
+          const int64_t kk = K - base < 8192 ? K - base : 8192;
+          const int64_t nbase = base / 32;
+          const int64_t np = wo_int_partials(
+              fmt, w + nbase * (fmt == WO_Q4_0 ? Q4_0_BYTES : MXFP4_BYTES), x + nbase * Q8_0_BYTES,
+              kk, parts);
+          for (int64_t b = 0; b < np; ++b) {
+            const uint8_t *wr = w + (nbase + b) * (fmt == WO_Q4_0 ? Q4_0_BYTES : MXFP4_BYTES);
+            const double dx = wo_fp16_to_fp32(rd16(x + (nbase + b) * Q8_0_BYTES));
+            const double dw = fmt == WO_Q4_0 ? wo_fp16_to_fp32(rd16(wr)) : wo_e8m0_to_fp32_half(wr[0]);
+            const double t = dw * dx * parts[b];
+            e += t;
+            a += fabs(t);
+          }
+        }
+      } else {
+        const int64_t nb = K / QK_K;
+        for (int64_t i = 0; i < nb; ++i) {
+          const uint8_t *wr = w + i * (fmt == WO_Q4_K ? Q4_K_BYTES : IQ2_XXS_BYTES);
+          const uint8_t *xr = x + i * Q8_K_BYTES;
+          wo_int_partials(fmt, wr, xr, QK_K, parts);
+          const double dx = rdf32(xr);
+          const double dw = wo_fp16_to_fp32(rd16(wr));
+          if (fmt == WO_Q4_K) {
+            uint8_t sc, mm;
+            int64_t S = 0;
+            for (int s = 0; s < 8; ++s) {
+              scale_min_k4(s, wr + 4, &sc, &mm);
+              S += (int64_t)sc * parts[s];
+            }
+            const double dmin = wo_fp16_to_fp32(rd16(wr + 2));
+            const double t1 = dw * dx * (double)S, t2 = dmin * dx * (double)parts[8];
+            e += t1 - t2;
+            a += fabs(t1) + fabs(t2);
+          } else {
+            const double t = 0.125 * dw * dx * (double)parts[0];
+            e += t;
+            a += fabs(t);
+          }
+        }
+      }
+      E[m * N + n] = e;
+      A[m * N + n] = a;
+    }
+  }
+}

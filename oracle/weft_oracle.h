@@ -1,0 +1,107 @@
+/*
+ * CPU oracle for the quantized mul_mat hot path (TEST INFRASTRUCTURE ONLY).
+ *
+ * A plain-C restatement of the GGML CPU functions that the reference Weft
+ * repository uses as its numeric oracle (vendored GGML under
+ * source/c/ggml/llama.cpp/ggml/src/).  Only tests/, __graft_entry__.smoke()
+ * and bench.py's cpu_baseline leg may load this library, and only as the
+ * checker or the timed CPU baseline: the product path (libweft_hip) never
+ * calls into it.
+ *
+ * Record layouts (bytes, little endian), ggml-common.h:
+ *   Q4_0    18 B / 32  : f16 d | u8 qs[16]                       (:184-189)
+ *   MXFP4   17 B / 32  : u8 e  | u8 qs[16]                       (:204-209)
+ *   Q8_0    34 B / 32  : f16 d | i8 qs[32]                       (:241-246)
+ *   Q4_K   144 B / 256 : f16 d | f16 dmin | u8 scales[12] | u8 qs[128]  (:317-328)
+ *   Q8_K   292 B / 256 : f32 d | i8 qs[256] | i16 bsums[16]      (:361-366)
+ *   IQ2_XXS 66 B / 256 : f16 d | u16 qs[32]                      (:371-375)
+ */
+#ifndef WEFT_ORACLE_H
+#define WEFT_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum wo_format {
+  WO_Q4_0 = 0,
+  WO_Q4_K = 1,
+  WO_IQ2_XXS = 2,
+  WO_MXFP4 = 3,
+};
+
+/* scalar conversions (ggml-impl.h:384-431, :477-495) */
+float wo_fp16_to_fp32(uint16_t h);
+uint16_t wo_fp32_to_fp16(float f);
+float wo_e8m0_to_fp32_half(uint8_t e);
+void wo_fp16_to_fp32_array(const uint16_t *h, float *out, int64_t n);
+void wo_fp32_to_fp16_array(const float *f, uint16_t *out, int64_t n);
+
+/* lookup tables, built from closed forms */
+void wo_iq2xxs_grid(uint8_t out[2048]);  /* 256 x 8 magnitudes {8,25,43} */
+void wo_ksigns_iq2xs(uint8_t out[128]);  /* i | parity(i) << 7 */
+void wo_signs_i8x8(int8_t out[1024]);    /* 128 x 8 of +-1, the ABI's I8X8 sign table */
+void wo_kvalues_mxfp4(int8_t out[16]);   /* doubled e2m1 */
+void wo_e8m0_half_table(float out[256]);
+
+/* weight quantizers (host-side input generators) */
+void wo_quantize_row_q4_0(const float *x, uint8_t *y, int64_t k);
+void wo_quantize_row_q4_K(const float *x, uint8_t *y, int64_t k);
+void wo_quantize_row_mxfp4(const float *x, uint8_t *y, int64_t k);
+void wo_quantize_row_iq2_xxs(const float *x, uint8_t *y, int64_t k);
+
+/* activation quantizers (on the hot path) */
+void wo_quantize_row_q8_0(const float *x, uint8_t *y, int64_t k);
+void wo_quantize_row_q8_K(const float *x, uint8_t *y, int64_t k);
+
+/* row dequantizers */
+void wo_dequantize_row_q4_0(const uint8_t *x, float *y, int64_t k);
+void wo_dequantize_row_q4_K(const uint8_t *x, float *y, int64_t k);
+void wo_dequantize_row_iq2_xxs(const uint8_t *x, float *y, int64_t k);
+void wo_dequantize_row_mxfp4(const uint8_t *x, float *y, int64_t k);
+
+/* generic vec_dots: w row (k elements) . quantized activation row */
+float wo_vec_dot_q4_0_q8_0(const uint8_t *w, const uint8_t *x, int64_t k);
+float wo_vec_dot_q4_K_q8_K(const uint8_t *w, const uint8_t *x, int64_t k);
+float wo_vec_dot_iq2_xxs_q8_K(const uint8_t *w, const uint8_t *x, int64_t k);
+float wo_vec_dot_mxfp4_q8_0(const uint8_t *w, const uint8_t *x, int64_t k);
+
+/* Bytes of one encoded row of k elements for a weight format, or of the
+ * activation format that pairs with it (Q8_0 for Q4_0/MXFP4, Q8_K else). */
+size_t wo_weight_row_bytes(int fmt, int64_t k);
+size_t wo_act_row_bytes(int fmt, int64_t k);
+
+/* GGML MUL_MAT semantics (ggml-cpu.c:1245-1443): quantize every row of
+ * X (M x K) into Xq, then Y[m, n] = vec_dot(W[n], Xq[m]).  Rows of W are
+ * split over nthreads threads (nthreads <= 0: all OpenMP threads). */
+void wo_mul_mat(int fmt, const uint8_t *W, const float *X, uint8_t *Xq,
+                float *Y, int64_t N, int64_t K, int64_t M, int nthreads);
+/* Same loop over an already-quantized Xq (the vec_dot-only part). */
+void wo_mul_mat_q(int fmt, const uint8_t *W, const uint8_t *Xq, float *Y,
+                  int64_t N, int64_t K, int64_t M, int nthreads);
+
+/* fp64 re-accumulation of the exact integer partials of every output:
+ * E[m, n] = sum_b scale_b * P_b evaluated in double, and
+ * A[m, n] = sum_b |scale_b * P_b| (the magnitude a tolerance is taken on). */
+void wo_mul_mat_f64(int fmt, const uint8_t *W, const uint8_t *Xq, double *E,
+                    double *A, int64_t N, int64_t K, int64_t M, int nthreads);
+
+/* Integer partials of one row pair, for exactness checks on tiny inputs:
+ * Q4_0 / MXFP4 : one int32 per 32-block (P)
+ * Q4_K         : per superblock, 8 sub-block sums P_s then the min sum Mn
+ * IQ2_XXS      : one int32 per superblock (B = sum_g I_g * (2 s_g + 1))
+ * returns the number of int32 written. */
+int64_t wo_int_partials(int fmt, const uint8_t *w, const uint8_t *x, int64_t k,
+                        int32_t *out);
+
+/* Threads OpenMP would use by default (for reporting the CPU baseline). */
+int wo_max_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

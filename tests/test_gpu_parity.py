@@ -1,0 +1,249 @@
+"""Parity of libweft_hip against the CPU oracle, through the C ABI (GPU).
+
+Bars (declared before any run):
+  * row dequantize, Q8_0/Q8_K quantize, the Xq workspace: bit-exact, byte
+    for byte, including bytes GGML leaves untouched (buffers start from the
+    same sentinel fill on both sides);
+  * fp32 outputs of vec_dot / mul_mat: |y - E| <= 1e-4 |E| + 4e-6 A, where E
+    is the fp64 re-accumulation of the exact integer partials of the same
+    quantized operands and A = sum |scale * partial| (oracle.within_tolerance).
+Shapes are BASELINE.json's configs where the oracle finishes in seconds;
+the prefill N=11008 case checks a seeded sample of output columns.
+"""
+from __future__ import annotations
+
+import functools
+
+import numpy as np
+import pytest
+
+import oracle as o
+
+pytestmark = pytest.mark.gpu
+
+SENTINEL = 0xA5
+
+
+@functools.lru_cache(maxsize=None)
+def weights(fmt: str, n: int, k: int, seed: int = 1) -> np.ndarray:
+    w = o.seeded_normal(seed, (n, k), 0.02)
+    return o.quantize(fmt, w)
+
+
+@functools.lru_cache(maxsize=None)
+def acts(m: int, k: int, seed: int = 2) -> np.ndarray:
+    return o.seeded_normal(seed, (m, k), 1.0)
+
+
+def tables(hip, fmt):
+    if fmt == "iq2_xxs":
+        return [hip.grid_i8x8, hip.signs_i8x8]
+    if fmt == "mxfp4":
+        return [hip.codebook, hip.scale]
+    return []
+
+
+def assert_close(y, e, a, what):
+    ok = o.within_tolerance(y, e, a)
+    if not ok.all():
+        bad = np.argwhere(~ok)[:5]
+        rows = [(tuple(i), float(np.asarray(y)[tuple(i)]), float(e[tuple(i)]), float(a[tuple(i)]))
+                for i in bad]
+        raise AssertionError(f"{what}: {int((~ok).sum())} outputs outside tolerance, e.g. {rows}")
+
+
+# ------------------------------------------------------------ row dequantize
+DQ_SYMBOL = {"q4_0": "row_dequantize_q4_0", "q4_k": "row_dequantize_q4_k",
+             "iq2_xxs": "row_dequantize_iq2_xxs", "mxfp4": "row_dequantize_mxfp4"}
+DQ_TABLES = {"iq2_xxs": "iq2", "mxfp4": "mx"}
+
+
+def _dequant_case(hip, fmt, n, k, w_off=0, y_off=0):
+    w = weights(fmt, n, k)
+    total = n * k
+    wd = hip.to_dev(w, offset=w_offset_bytes(fmt, w_off))
+    y = hip.empty(4 * total, fill=SENTINEL, offset=4 * y_off)
+    extra = []
+    if fmt == "iq2_xxs":
+        extra = [hip.grid_i8x8, hip.signs_i8x8]
+    elif fmt == "mxfp4":
+        extra = [hip.codebook, hip.scale]
+    hip.call(DQ_SYMBOL[fmt], wd, *extra, y, total)
+    got = y.numpy(np.float32)
+    want = o.dequantize(fmt, w, k).reshape(-1)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def w_offset_bytes(fmt, units):
+    align = {"q4_0": 2, "q4_k": 2, "iq2_xxs": 2, "mxfp4": 1}[fmt]
+    return units * align
+
+
+def test_dequant_q4_k_config2(hip):
+    """Q4_K row dequantize 11008x4096, bit-exact."""
+    _dequant_case(hip, "q4_k", 11008, 4096)
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "iq2_xxs", "mxfp4"])
+@pytest.mark.parametrize("n,k", [(512, 4096), (1, 256), (37, 256)])
+def test_dequant_bit_exact(hip, fmt, n, k):
+    _dequant_case(hip, fmt, n, k)
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "iq2_xxs", "mxfp4"])
+def test_dequant_misaligned_pointers(hip, fmt):
+    # base pointers that only meet the Encoding's own alignment
+    _dequant_case(hip, fmt, 19, 512, w_off=1, y_off=1)
+
+
+# ---------------------------------------------------------------- quantize
+def edge_rows(k: int) -> np.ndarray:
+    """Known-hard blocks: exact .5 ties, all-zero, +-equal max, denormals,
+    values hitting +-127, one huge outlier, negative-first maximum."""
+    rows = []
+    # every 32-block starts with 127, so d = 1 exactly and x.5 values tie
+    r = ((np.arange(k) % 64) - 31.5).astype(np.float32)
+    r[0::32] = 127.0
+    rows.append(r)
+    rows.append(np.zeros(k, np.float32))
+    r = np.zeros(k, np.float32)
+    r[3], r[7] = 5.0, -5.0
+    r[300], r[301] = -5.0, 5.0
+    rows.append(r)
+    # tiny but normal magnitudes (fp16(d) underflows to 0; 1/d stays finite)
+    rows.append(np.full(k, 1e-30, np.float32) * np.where(np.arange(k) % 2, 1, -1))
+    r = np.linspace(-1.0, 1.0, k, dtype=np.float32)
+    r[17] = 1e30
+    rows.append(r)
+    r = o.seeded_normal(9, (k,))
+    r[::32] = 0
+    r[0] = -3e-5
+    rows.append(r)
+    return np.stack(rows).astype(np.float32)
+
+
+@pytest.mark.parametrize("act", ["q8_0", "q8_k"])
+def test_quantize_bit_exact(hip, act):
+    k = 4096
+    x = np.concatenate([acts(512, k), edge_rows(k)])
+    nbytes = o.record_bytes(act, k) * x.shape[0]
+    xd = hip.to_dev(x)
+    y = hip.empty(nbytes, fill=SENTINEL)
+    hip.call("q8_0_quantize" if act == "q8_0" else "q8_K_quantize", xd, y, x.size)
+    want = np.full((x.shape[0], o.record_bytes(act, k)), SENTINEL, np.uint8)
+    o.quantize(act, x, out=want)
+    np.testing.assert_array_equal(y.numpy(np.uint8), want.reshape(-1))
+
+
+@pytest.mark.parametrize("act", ["q8_0", "q8_k"])
+def test_quantize_misaligned(hip, act):
+    k = 512
+    x = acts(7, k)
+    xd = hip.to_dev(x, offset=4)
+    nbytes = o.record_bytes(act, k) * 7
+    y = hip.empty(nbytes, fill=SENTINEL, offset=2 if act == "q8_0" else 4)
+    hip.call("q8_0_quantize" if act == "q8_0" else "q8_K_quantize", xd, y, x.size)
+    want = np.full((7, o.record_bytes(act, k)), SENTINEL, np.uint8)
+    o.quantize(act, x, out=want)
+    np.testing.assert_array_equal(y.numpy(np.uint8), want.reshape(-1))
+
+
+# ---------------------------------------------------------------- vec_dot
+VD_SYMBOL = {"q4_0": "quantized_vec_dot_q4_0_q8_0", "q4_k": "quantized_vec_dot_q4_k_q8_k",
+             "iq2_xxs": "quantized_vec_dot_iq2_xxs_q8_k", "mxfp4": "quantized_vec_dot_mxfp4_q8_0"}
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "iq2_xxs", "mxfp4"])
+@pytest.mark.parametrize("k", [256, 4096, 14336])
+def test_vec_dot(hip, fmt, k):
+    w = weights(fmt, 1, k, seed=3)
+    xq = o.quantize(o.ACT_OF[fmt], acts(1, k, seed=4))
+    y = hip.empty(4, fill=SENTINEL)
+    hip.call(VD_SYMBOL[fmt], hip.to_dev(w), hip.to_dev(xq), *tables(hip, fmt), y, k)
+    e, a = o.mul_mat_f64(fmt, w, xq, 1, k, 1)
+    assert_close(y.numpy(np.float32).reshape(1, 1), e, a, f"vec_dot {fmt}")
+
+
+# ------------------------------------------------------------ decode GEMV
+MM_DECODE = {"q4_0": "production_mul_mat_q4_0_decode", "q4_k": "production_mul_mat_q4_k_decode",
+             "iq2_xxs": "production_mul_mat_iq2_xxs_decode", "mxfp4": "production_mul_mat_mxfp4_decode"}
+MM_PREFILL = {"q4_0": "production_mul_mat_q4_0", "q4_k": "production_mul_mat_q4_k_staged",
+              "iq2_xxs": "production_mul_mat_iq2_xxs_staged", "mxfp4": "production_mul_mat_mxfp4"}
+
+
+def run_mul_mat(hip, symbol, fmt, n, k, m, w=None, x=None):
+    w = weights(fmt, n, k) if w is None else w
+    x = acts(m, k) if x is None else x
+    act = o.ACT_OF[fmt]
+    xq = hip.empty(o.record_bytes(act, k) * m, fill=SENTINEL)
+    y = hip.empty(4 * m * n, fill=SENTINEL)
+    hip.call(symbol, hip.to_dev(w), hip.to_dev(x), xq, *tables(hip, fmt), y, n, k, m)
+    return w, x, xq.numpy(np.uint8).reshape(m, -1), y.numpy(np.float32).reshape(m, n)
+
+
+def check_mul_mat(fmt, w, x, xq_got, y_got, n, k, m, cols=None):
+    act = o.ACT_OF[fmt]
+    want_xq = np.full((m, o.record_bytes(act, k)), SENTINEL, np.uint8)
+    o.quantize(act, x, out=want_xq)
+    np.testing.assert_array_equal(xq_got, want_xq, err_msg="Xq workspace differs")
+    if cols is not None:
+        w = w[cols]
+        y_got = y_got[:, cols]
+        n = len(cols)
+    e, a = o.mul_mat_f64(fmt, w, want_xq, n, k, m)
+    assert_close(y_got, e, a, f"mul_mat {fmt}")
+
+
+@pytest.mark.parametrize("fmt,n,k", [
+    ("q4_0", 4096, 4096),       # config 1
+    ("q4_k", 11008, 4096),      # config 3, W_up
+    ("q4_k", 4096, 11008),      # config 3, W_down
+    ("iq2_xxs", 4096, 4096),    # config 5a
+    ("mxfp4", 4096, 4096),
+])
+def test_decode_configs(hip, fmt, n, k):
+    w, x, xq, y = run_mul_mat(hip, MM_DECODE[fmt], fmt, n, k, 1)
+    check_mul_mat(fmt, w, x, xq, y, n, k, 1)
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "iq2_xxs", "mxfp4"])
+@pytest.mark.parametrize("n,k,m", [(300, 768, 3), (65, 1024, 5), (1, 256, 1)])
+def test_decode_small_shapes(hip, fmt, n, k, m):
+    w, x, xq, y = run_mul_mat(hip, MM_DECODE[fmt], fmt, n, k, m)
+    check_mul_mat(fmt, w, x, xq, y, n, k, m)
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "iq2_xxs", "mxfp4"])
+def test_prefill_entry_points(hip, fmt):
+    n, k, m = 512, 4096, 64
+    w, x, xq, y = run_mul_mat(hip, MM_PREFILL[fmt], fmt, n, k, m)
+    check_mul_mat(fmt, w, x, xq, y, n, k, m)
+
+
+def test_prefill_q4_k_config4_n4096(hip):
+    """BASELINE config 4 (N=4096): 512 tokens x 4096, full check."""
+    n = k = 4096
+    m = 512
+    w, x, xq, y = run_mul_mat(hip, "production_mul_mat_q4_k_staged", "q4_k", n, k, m)
+    check_mul_mat("q4_k", w, x, xq, y, n, k, m)
+
+
+def test_prefill_q4_k_config4_n11008_sampled(hip):
+    """BASELINE config 4 (N=11008): Xq in full, Y on 256 seeded columns."""
+    n, k, m = 11008, 4096, 512
+    w, x, xq, y = run_mul_mat(hip, "production_mul_mat_q4_k_staged", "q4_k", n, k, m)
+    cols = np.sort(np.random.default_rng(5).choice(n, 256, replace=False))
+    check_mul_mat("q4_k", w, x, xq, y, n, k, m, cols=cols)
+
+
+# ------------------------------------------------------------ error paths
+def test_invalid_shape_reports_error_and_launches_nothing(hip):
+    y = hip.empty(16, fill=SENTINEL)
+    w = hip.empty(4096)
+    x = hip.empty(4096)
+    xq = hip.empty(4096)
+    hip.lib.production_mul_mat_q4_k_decode(w.ptr, x.ptr, xq.ptr, y.ptr, 1, 100, 1)
+    hip.torch.cuda.synchronize()
+    assert hip.last_error() != 0
+    assert hip.last_error() == 0  # cleared once read
+    assert (y.numpy(np.uint8) == SENTINEL).all()

@@ -1,0 +1,91 @@
+"""ctypes binding of the in-tree ``libweft_hip.so``.
+
+The library is the product: there is no fallback.  ``load()`` raises if the
+shared library has not been built (``python -m weft_amd.build`` or
+``__graft_entry__.build()``).  Argument types come from the library's own ABI
+metadata (``weft_hip_artifact``): one ``c_void_p`` per View parameter, then one
+``c_size_t`` per shape parameter, as Weft's CompiledKernel binds generated
+symbols (python/weft/runtime/compiler.py:91-96).
+"""
+from __future__ import annotations
+
+import ctypes
+import json
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libweft_hip.so"
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+_artifact: dict | None = None
+
+
+class LibraryMissing(RuntimeError):
+    pass
+
+
+def load() -> ctypes.CDLL:
+    global _lib, _artifact
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise LibraryMissing(
+                    f"{LIB_PATH} is not built; run python -m weft_amd.build (hipcc, gfx950)")
+            lib = ctypes.CDLL(str(LIB_PATH))
+            lib.weft_hip_artifact.restype = ctypes.c_char_p
+            lib.weft_hip_version.restype = ctypes.c_char_p
+            lib.weft_hip_error_string.restype = ctypes.c_char_p
+            lib.weft_hip_error_string.argtypes = [ctypes.c_int]
+            lib.weft_hip_set_stream.argtypes = [ctypes.c_void_p]
+            lib.weft_hip_set_stream.restype = ctypes.c_int
+            lib.weft_hip_get_stream.restype = ctypes.c_void_p
+            lib.weft_hip_get_last_error.restype = ctypes.c_int
+            lib.weft_hip_synchronize.restype = ctypes.c_int
+            artifact = json.loads(lib.weft_hip_artifact())
+            for kernel in artifact["kernels"]:
+                fn = getattr(lib, kernel["symbol"])
+                fn.argtypes = ([ctypes.c_void_p] * len(kernel["arguments"]) +
+                               [ctypes.c_size_t] * len(kernel["shape_parameters"]))
+                fn.restype = None
+            _artifact = artifact
+            _lib = lib
+        return _lib
+
+
+def artifact() -> dict:
+    load()
+    assert _artifact is not None
+    return _artifact
+
+
+def kernel_metadata(symbol: str) -> dict:
+    for kernel in artifact()["kernels"]:
+        if kernel["symbol"] == symbol:
+            return kernel
+    raise KeyError(symbol)
+
+
+class HipError(RuntimeError):
+    def __init__(self, code: int, where: str) -> None:
+        self.code = code
+        msg = load().weft_hip_error_string(code).decode()
+        super().__init__(f"{where}: hip error {code} ({msg})")
+
+
+def check(where: str) -> None:
+    """Raise the calling thread's recorded launch error, if any."""
+    code = load().weft_hip_get_last_error()
+    if code != 0:
+        raise HipError(code, where)
+
+
+def set_stream(handle: int | None) -> None:
+    load().weft_hip_set_stream(ctypes.c_void_p(handle or 0))
+
+
+def synchronize() -> None:
+    code = load().weft_hip_synchronize()
+    if code != 0:
+        load().weft_hip_get_last_error()
+        raise HipError(code, "synchronize")

@@ -1,0 +1,165 @@
+// Activation staging for the decode (GEMV) kernels: the M x K fp32
+// activation is quantized inside every workgroup into LDS (so the fused
+// mul_mat needs one launch), or a caller-supplied quantized activation is
+// copied into LDS (vec_dot).  Workgroup 0 also writes the quantized rows to
+// the caller's Xq workspace, bit-exact with GGML's quantize_row_q8_*_ref.
+#pragma once
+
+#include "weft_common.h"
+
+namespace weft {
+
+// ---------------------------------------------------------------- Q8_K
+// LDS image of one Q8_K activation row of K elements (K a multiple of 256,
+// so every part and every row stays 16-byte aligned):
+//   int8 qs[K] | float d[K/256] (padded to 16 B) | int bp[K/32]
+// bp[s] = bsums[2s] + bsums[2s+1], the Q8_K block sum of 32-sub-block s.
+struct Q8KView {
+  int8_t* qs;
+  float* d;
+  int* bp;
+};
+
+// the d array is padded to 16 bytes so bp is 16-byte aligned
+__host__ __device__ inline size_t q8k_d_bytes(int K) {
+  return (4 * (size_t)(K / 256) + 15) & ~(size_t)15;
+}
+
+__host__ __device__ inline size_t q8k_lds_row_bytes(int K) {
+  return (size_t)K + q8k_d_bytes(K) + 4 * (size_t)(K / 32);
+}
+
+__device__ inline Q8KView q8k_view(char* base, int K, int m) {
+  char* p = base + (size_t)m * q8k_lds_row_bytes(K);
+  Q8KView v;
+  v.qs = reinterpret_cast<int8_t*>(p);
+  v.d = reinterpret_cast<float*>(p + K);
+  v.bp = reinterpret_cast<int*>(p + K + q8k_d_bytes(K));
+  return v;
+}
+
+__device__ inline float4 load_x4(const float* p, bool a16) {
+  if (a16) return *reinterpret_cast<const float4*>(p);
+  return make_float4(p[0], p[1], p[2], p[3]);
+}
+
+// Quantize rows [m0, m0+mb) of X (row stride K) into LDS; when xq_out is
+// non-null also store the records (Xq row stride K/256 records).
+__device__ inline void stage_q8k_quantize(const float* __restrict__ X, uint8_t* __restrict__ xq_out,
+                                          int K, int m0, int mb, char* lds) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int nwaves = blockDim.x / kWave;
+  const int nsb = K / 256;
+  const bool a16 = (reinterpret_cast<uintptr_t>(X) & 15) == 0;
+  for (int idx = wave; idx < mb * nsb; idx += nwaves) {
+    const int m = idx / nsb, s = idx - m * nsb;
+    const float4 x = load_x4(X + (size_t)(m0 + m) * K + 256 * s + 4 * lane, a16);
+    const Q8KLane r = q8k_quantize_wave(x, lane);
+    const Q8KView v = q8k_view(lds, K, m);
+    const int packed = pack4_i8(r.q);
+    reinterpret_cast<int*>(v.qs + 256 * s)[lane] = packed;
+    // bsum16 is replicated in its 4 lanes; the 32-sub-block sum adds groups
+    // 2t and 2t+1, whose first lanes are 8t and 8t+4.
+    const int pair = r.bsum16 + __shfl_xor(r.bsum16, 4, kWave);
+    if ((lane & 7) == 0) v.bp[8 * s + lane / 8] = pair;
+    if (lane == 0) v.d[s] = r.d;
+    if (xq_out != nullptr) {
+      uint8_t* rec = xq_out + ((size_t)(m0 + m) * nsb + s) * kQ8_KBytes;
+      if (lane == 0) *reinterpret_cast<float*>(rec) = r.d;
+      reinterpret_cast<int*>(rec + 4)[lane] = packed;
+      if (!r.zero && (lane & 3) == 0)
+        reinterpret_cast<int16_t*>(rec + 260)[lane / 4] = (int16_t)r.bsum16;
+    }
+  }
+}
+
+// Copy rows [m0, m0+mb) of a quantized Q8_K activation into LDS.
+__device__ inline void stage_q8k_load(const uint8_t* __restrict__ xq, int K, int m0, int mb,
+                                      char* lds) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int nwaves = blockDim.x / kWave;
+  const int nsb = K / 256;
+  for (int idx = wave; idx < mb * nsb; idx += nwaves) {
+    const int m = idx / nsb, s = idx - m * nsb;
+    const uint8_t* rec = xq + ((size_t)(m0 + m) * nsb + s) * kQ8_KBytes;
+    const Q8KView v = q8k_view(lds, K, m);
+    reinterpret_cast<int*>(v.qs + 256 * s)[lane] = reinterpret_cast<const int*>(rec + 4)[lane];
+    if (lane < 8) {
+      const int16_t* bs = reinterpret_cast<const int16_t*>(rec + 260);
+      v.bp[8 * s + lane] = (int)bs[2 * lane] + (int)bs[2 * lane + 1];
+    }
+    if (lane == 0) v.d[s] = *reinterpret_cast<const float*>(rec);
+  }
+}
+
+// ---------------------------------------------------------------- Q8_0
+// LDS image of one Q8_0 activation row: int8 qs[K] | float d[K/32]
+// (d is the fp16 scale widened to fp32, as the vec_dot reads it).
+struct Q80View {
+  int8_t* qs;
+  float* d;
+};
+
+__host__ __device__ inline size_t q80_lds_row_bytes(int K) {
+  return ((size_t)K + 4 * (size_t)(K / 32) + 15) & ~(size_t)15;
+}
+
+__device__ inline Q80View q80_view(char* base, int K, int m) {
+  char* p = base + (size_t)m * q80_lds_row_bytes(K);
+  Q80View v;
+  v.qs = reinterpret_cast<int8_t*>(p);
+  v.d = reinterpret_cast<float*>(p + K);
+  return v;
+}
+
+// K must be a multiple of 32; a wave covers 8 blocks (256 values) per step,
+// 8 lanes per block.
+__device__ inline void stage_q80_quantize(const float* __restrict__ X, uint8_t* __restrict__ xq_out,
+                                          int K, int m0, int mb, char* lds) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int nwaves = blockDim.x / kWave;
+  const int nb = K / 32;
+  const int steps = (nb + 7) / 8;
+  const bool a16 = (reinterpret_cast<uintptr_t>(X) & 15) == 0;
+  for (int idx = wave; idx < mb * steps; idx += nwaves) {
+    const int m = idx / steps, st = idx - m * steps;
+    const int b = 8 * st + lane / 8;
+    const bool live = b < nb;  // uniform per 8-lane group
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live) x = load_x4(X + (size_t)(m0 + m) * K + 32 * b + 4 * (lane & 7), a16);
+    const Q8_0Lane r = q80_quantize_8lanes(x);
+    if (!live) continue;
+    const Q80View v = q80_view(lds, K, m);
+    const int packed = pack4_i8(r.q);
+    reinterpret_cast<int*>(v.qs + 32 * b)[lane & 7] = packed;
+    if ((lane & 7) == 0) v.d[b] = fp16_to_fp32(r.dh);
+    if (xq_out != nullptr) {
+      uint8_t* rec = xq_out + ((size_t)(m0 + m) * nb + b) * kQ8_0Bytes;
+      uint16_t* q16 = reinterpret_cast<uint16_t*>(rec + 2 + 4 * (lane & 7));
+      q16[0] = (uint16_t)((uint32_t)packed & 0xffffu);
+      q16[1] = (uint16_t)((uint32_t)packed >> 16);
+      if ((lane & 7) == 0) *reinterpret_cast<uint16_t*>(rec) = (uint16_t)r.dh;
+    }
+  }
+}
+
+__device__ inline void stage_q80_load(const uint8_t* __restrict__ xq, int K, int m0, int mb,
+                                      char* lds) {
+  const int nb = K / 32;
+  const int total = mb * nb * 8;  // 8 lanes per block
+  for (int i = threadIdx.x; i < total; i += blockDim.x) {
+    const int m = i / (nb * 8);
+    const int rem = i - m * nb * 8;
+    const int b = rem >> 3, part = rem & 7;
+    const uint8_t* rec = xq + ((size_t)(m0 + m) * nb + b) * kQ8_0Bytes;
+    const Q80View v = q80_view(lds, K, m);
+    const uint16_t* q16 = reinterpret_cast<const uint16_t*>(rec + 2 + 4 * part);
+    reinterpret_cast<int*>(v.qs + 32 * b)[part] = (int)((uint32_t)q16[0] | ((uint32_t)q16[1] << 16));
+    if (part == 0) v.d[b] = fp16_to_fp32(*reinterpret_cast<const uint16_t*>(rec));
+  }
+}
+
+}  // namespace weft

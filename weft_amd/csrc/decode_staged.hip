@@ -1,0 +1,389 @@
+// Decode GEMV for the formats whose records are not 16-byte multiples:
+// Q4_0 x Q8_0 (18 B / 32), MXFP4 x Q8_0 (17 B / 32), IQ2_XXS x Q8_K
+// (66 B / 256); plus their single-output vec_dots.
+//
+// Semantics (GGML generic vec_dots, ggml-cpu/quants.c):
+//   Q4_0    :174-208  y = sum_b dw_b * dx_b * sum_32 (q-8) * x
+//   MXFP4   :247-276  y = sum_b dx_b * e8m0_half(e_b) * sum_32 kv[q] * x
+//   IQ2_XXS :855-895  y = 0.125 * sum_B dw * dx * sum_g (2 s_g + 1) *
+//                         sum_32 grid[idx] * sign * x
+// and the Weft kernels examples/kernels/mul_mat/{q4_0_decode,mxfp4_decode,
+// iq2_xxs_decode}.py (quantize X into Xq, then one vec_dot per output).
+//
+// gfx950 mapping.  Records straddle 16-byte boundaries, so a wave streams a
+// segment of its row into a private LDS window with coalesced 16-byte loads
+// (1 KB per wave instruction) and lanes then pick their record out of LDS at
+// any byte offset with two aligned ds_read_b32 + v_alignbyte per word.  One
+// lane owns one 32-element block (Q4_0, MXFP4) or one 32-element group of an
+// IQ2_XXS superblock; its int8 products run on v_dot4_i32_i8 against the
+// quantized activation in LDS.  MXFP4's 16-entry codebook is looked up four
+// nibbles at a time with two v_perm_b32; the IQ2_XXS grid and sign tables
+// live in LDS.  The activation is quantized inside every workgroup, and
+// workgroup 0 writes Xq, exactly as in the Q4_K decode kernel.
+#include <algorithm>
+
+#include "activation.h"
+#include "kernels.h"
+#include "runtime.h"
+#include "weft_hip.h"
+
+namespace weft {
+namespace {
+
+constexpr int kThreads = 1024;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kMaxRowsPerPass = 4;
+constexpr int kWindow = 2304 + 32;  // per-wave LDS window (bytes), with slack
+
+enum class Fmt { Q4_0, MXFP4, IQ2_XXS };
+
+template <Fmt F>
+struct Traits;
+template <>
+struct Traits<Fmt::Q4_0> {
+  static constexpr int kElems = 32, kBytes = 18, kSegRecords = 128, kItemsPerRecord = 1;
+  static constexpr bool kQ8K = false;
+};
+template <>
+struct Traits<Fmt::MXFP4> {
+  static constexpr int kElems = 32, kBytes = 17, kSegRecords = 128, kItemsPerRecord = 1;
+  static constexpr bool kQ8K = false;
+};
+template <>
+struct Traits<Fmt::IQ2_XXS> {
+  static constexpr int kElems = 256, kBytes = 66, kSegRecords = 32, kItemsPerRecord = 8;
+  static constexpr bool kQ8K = true;
+};
+
+struct Args {
+  const uint8_t* W;
+  const float* X;
+  const uint8_t* xq_in;
+  uint8_t* xq_out;
+  const int8_t* tab0;  // grid (IQ2_XXS) or codebook (MXFP4)
+  const void* tab1;    // signs (IQ2_XXS) or fp32 scale table (MXFP4)
+  float* Y;
+  int N, K;
+  int m0, mb;
+  int rows_per_wg;
+  long long y_stride;
+};
+
+// 4 bytes starting at any LDS byte offset o (o+7 must be inside the buffer)
+__device__ __forceinline__ uint32_t lds_u32(const char* base, int o) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(base + (o & ~3));
+  return __builtin_amdgcn_alignbyte(w[1], w[0], (uint32_t)(o & 3));
+}
+
+// Copy bytes [p0, p1) of W into the wave's LDS window; returns the offset of
+// p0 inside the window.  16-byte loads from the 16-aligned address below p0;
+// a chunk that reaches outside [lo, hi) is read byte by byte, inside only.
+__device__ __forceinline__ int stage_bytes(char* win, const uint8_t* p0, const uint8_t* p1,
+                                           const uint8_t* lo, const uint8_t* hi, int lane) {
+  const uint8_t* a0 = reinterpret_cast<const uint8_t*>(reinterpret_cast<uintptr_t>(p0) & ~(uintptr_t)15);
+  const int nchunks = (int)((p1 - a0 + 15) >> 4);
+  for (int c = lane; c < nchunks; c += kWave) {
+    const uint8_t* src = a0 + 16 * c;
+    uint4 v;
+    if (src >= lo && src + 16 <= hi) {
+      v = *reinterpret_cast<const uint4*>(src);
+    } else {
+      uint32_t w[4] = {0, 0, 0, 0};
+      for (int i = 0; i < 16; ++i)
+        if (src + i >= lo && src + i < hi) w[i >> 2] |= (uint32_t)src[i] << (8 * (i & 3));
+      v = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+    *reinterpret_cast<uint4*>(win + 16 * c) = v;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  return (int)(p0 - a0);
+}
+
+__device__ __forceinline__ void window_release() {
+  // all lanes are done reading the window before it is overwritten
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// bytewise (a - 8) for nibbles a in [0, 15], no borrow between bytes
+__device__ __forceinline__ int sub8(uint32_t a) {
+  return (int)(((a | 0x80808080u) - 0x08080808u) ^ 0x80808080u);
+}
+
+// four nibbles n (one per byte, 0..15) -> codebook bytes
+__device__ __forceinline__ int lookup16(uint32_t n, uint32_t c0, uint32_t c1, uint32_t c2,
+                                        uint32_t c3) {
+  const uint32_t sel = n & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(c1, c0, sel);
+  const uint32_t hi = __builtin_amdgcn_perm(c3, c2, sel);
+  const uint32_t mask = ((n >> 3) & 0x01010101u) * 0xffu;
+  return (int)((hi & mask) | (lo & ~mask));
+}
+
+// negate the bytes of g (grid magnitudes 8..43) where the sign byte is -1
+__device__ __forceinline__ int apply_signs(uint32_t g, uint32_t s) {
+  const uint32_t m = ((s >> 7) & 0x01010101u) * 0xffu;
+  return (int)((g ^ m) + (m & 0x01010101u));
+}
+
+template <Fmt F>
+__global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
+  using T = Traits<F>;
+  extern __shared__ __align__(16) char lds[];
+  char* windows = lds;                             // kWaves * kWindow
+  char* tables = windows + kWaves * kWindow;       // 3 KB of tables
+  char* act = tables + 3072;                       // activation rows
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int nwaves = blockDim.x / kWave;
+  const int K = a.K;
+
+  if constexpr (F == Fmt::IQ2_XXS) {
+    // grid I8X8[256x8] then signs I8X8[128x8]
+    for (int i = threadIdx.x; i < 512; i += blockDim.x)
+      reinterpret_cast<uint32_t*>(tables)[i] = reinterpret_cast<const uint32_t*>(a.tab0)[i];
+    for (int i = threadIdx.x; i < 256; i += blockDim.x)
+      reinterpret_cast<uint32_t*>(tables + 2048)[i] =
+          reinterpret_cast<const uint32_t*>(a.tab1)[i];
+  } else if constexpr (F == Fmt::MXFP4) {
+    for (int i = threadIdx.x; i < 256; i += blockDim.x)
+      reinterpret_cast<float*>(tables)[i] = reinterpret_cast<const float*>(a.tab1)[i];
+  }
+  if constexpr (T::kQ8K) {
+    if (a.X != nullptr)
+      stage_q8k_quantize(a.X, blockIdx.x == 0 ? a.xq_out : nullptr, K, a.m0, a.mb, act);
+    else
+      stage_q8k_load(a.xq_in, K, a.m0, a.mb, act);
+  } else {
+    if (a.X != nullptr)
+      stage_q80_quantize(a.X, blockIdx.x == 0 ? a.xq_out : nullptr, K, a.m0, a.mb, act);
+    else
+      stage_q80_load(a.xq_in, K, a.m0, a.mb, act);
+  }
+  __syncthreads();
+
+  uint32_t c0 = 0, c1 = 0, c2 = 0, c3 = 0;
+  if constexpr (F == Fmt::MXFP4) {
+    // int8[16] codebook, any alignment: four little-endian words
+    const uint8_t* cb = reinterpret_cast<const uint8_t*>(a.tab0);
+    c0 = ld_u32_a1(cb);
+    c1 = ld_u32_a1(cb + 4);
+    c2 = ld_u32_a1(cb + 8);
+    c3 = ld_u32_a1(cb + 12);
+  }
+
+  char* win = windows + wave * kWindow;
+  const int nrec = K / T::kElems;
+  const size_t rb = (size_t)nrec * T::kBytes;
+  const uint8_t* wlo = a.W;
+  const uint8_t* whi = a.W + (size_t)a.N * rb;
+  const int row0 = blockIdx.x * a.rows_per_wg;
+  const int row1 = min(a.N, row0 + a.rows_per_wg);
+
+  for (int row = row0 + wave; row < row1; row += nwaves) {
+    const uint8_t* wr = a.W + (size_t)row * rb;
+    float acc[kMaxRowsPerPass];
+#pragma unroll
+    for (int m = 0; m < kMaxRowsPerPass; ++m) acc[m] = 0.f;
+
+    for (int r0 = 0; r0 < nrec; r0 += T::kSegRecords) {
+      const int nr = min(T::kSegRecords, nrec - r0);
+      const int off0 = stage_bytes(win, wr + (size_t)r0 * T::kBytes,
+                                   wr + (size_t)(r0 + nr) * T::kBytes, wlo, whi, lane);
+      const int items = nr * T::kItemsPerRecord;
+      for (int it = lane; it < items; it += kWave) {
+        if constexpr (F == Fmt::Q4_0 || F == Fmt::MXFP4) {
+          const int b = it;             // block within segment
+          const int gb = r0 + b;        // block within row
+          const int o = off0 + T::kBytes * b;
+          const int qo = o + (F == Fmt::Q4_0 ? 2 : 1);
+          const uint32_t w0 = lds_u32(win, qo), w1 = lds_u32(win, qo + 4);
+          const uint32_t w2 = lds_u32(win, qo + 8), w3 = lds_u32(win, qo + 12);
+          int lo0, lo1, lo2, lo3, hi0, hi1, hi2, hi3;
+          float wscale;
+          if constexpr (F == Fmt::Q4_0) {
+            wscale = fp16_to_fp32(lds_u32(win, o) & 0xffffu);
+            lo0 = sub8(w0 & 0x0f0f0f0fu); lo1 = sub8(w1 & 0x0f0f0f0fu);
+            lo2 = sub8(w2 & 0x0f0f0f0fu); lo3 = sub8(w3 & 0x0f0f0f0fu);
+            hi0 = sub8((w0 >> 4) & 0x0f0f0f0fu); hi1 = sub8((w1 >> 4) & 0x0f0f0f0fu);
+            hi2 = sub8((w2 >> 4) & 0x0f0f0f0fu); hi3 = sub8((w3 >> 4) & 0x0f0f0f0fu);
+          } else {
+            wscale = reinterpret_cast<const float*>(tables)[lds_u32(win, o) & 0xffu];
+            lo0 = lookup16(w0, c0, c1, c2, c3); lo1 = lookup16(w1, c0, c1, c2, c3);
+            lo2 = lookup16(w2, c0, c1, c2, c3); lo3 = lookup16(w3, c0, c1, c2, c3);
+            hi0 = lookup16(w0 >> 4, c0, c1, c2, c3); hi1 = lookup16(w1 >> 4, c0, c1, c2, c3);
+            hi2 = lookup16(w2 >> 4, c0, c1, c2, c3); hi3 = lookup16(w3 >> 4, c0, c1, c2, c3);
+          }
+#pragma unroll
+          for (int m = 0; m < kMaxRowsPerPass; ++m) {
+            if (m >= a.mb) break;
+            const Q80View v = q80_view(act, K, m);
+            const int4 xl = *reinterpret_cast<const int4*>(v.qs + 32 * gb);
+            const int4 xh = *reinterpret_cast<const int4*>(v.qs + 32 * gb + 16);
+            int s = dot4(lo0, xl.x, 0);
+            s = dot4(lo1, xl.y, s);
+            s = dot4(lo2, xl.z, s);
+            s = dot4(lo3, xl.w, s);
+            s = dot4(hi0, xh.x, s);
+            s = dot4(hi1, xh.y, s);
+            s = dot4(hi2, xh.z, s);
+            s = dot4(hi3, xh.w, s);
+            acc[m] += (float)s * wscale * v.d[gb];
+          }
+        } else {  // IQ2_XXS: item = (superblock, 32-group)
+          const int sb = it >> 3, g = it & 7;
+          const int gsb = r0 + sb;
+          const int o = off0 + T::kBytes * sb;
+          const float dw = fp16_to_fp32(lds_u32(win, o) & 0xffffu);
+          const uint32_t idx = lds_u32(win, o + 2 + 8 * g);
+          const uint32_t meta = lds_u32(win, o + 6 + 8 * g);
+          const uint2* grid = reinterpret_cast<const uint2*>(tables);
+          const uint2* sgn = reinterpret_cast<const uint2*>(tables + 2048);
+          int wv[8];
+#pragma unroll
+          for (int l = 0; l < 4; ++l) {
+            const uint2 gv = grid[(idx >> (8 * l)) & 0xffu];
+            const uint2 sv = sgn[(meta >> (7 * l)) & 127u];
+            wv[2 * l] = apply_signs(gv.x, sv.x);
+            wv[2 * l + 1] = apply_signs(gv.y, sv.y);
+          }
+          const int ls = 2 * (int)(meta >> 28) + 1;
+#pragma unroll
+          for (int m = 0; m < kMaxRowsPerPass; ++m) {
+            if (m >= a.mb) break;
+            const Q8KView v = q8k_view(act, K, m);
+            const int4 x0 = *reinterpret_cast<const int4*>(v.qs + 256 * gsb + 32 * g);
+            const int4 x1 = *reinterpret_cast<const int4*>(v.qs + 256 * gsb + 32 * g + 16);
+            int s = dot4(wv[0], x0.x, 0);
+            s = dot4(wv[1], x0.y, s);
+            s = dot4(wv[2], x0.z, s);
+            s = dot4(wv[3], x0.w, s);
+            s = dot4(wv[4], x1.x, s);
+            s = dot4(wv[5], x1.y, s);
+            s = dot4(wv[6], x1.z, s);
+            s = dot4(wv[7], x1.w, s);
+            acc[m] += (dw * v.d[gsb]) * (float)(s * ls);
+          }
+        }
+      }
+      window_release();
+    }
+#pragma unroll
+    for (int m = 0; m < kMaxRowsPerPass; ++m) {
+      if (m >= a.mb) break;
+      float tot = wave_sum(acc[m]);
+      if constexpr (F == Fmt::IQ2_XXS) tot *= 0.125f;
+      if (lane == 0) a.Y[(size_t)(a.m0 + m) * a.y_stride + row] = tot;
+    }
+  }
+}
+
+template <Fmt F>
+void launch(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_out,
+            const int8_t* tab0, const void* tab1, float* Y, size_t N, size_t K, size_t M) {
+  using T = Traits<F>;
+  if (N == 0 || M == 0 || K == 0) return;
+  const size_t act_align = T::kQ8K ? 4 : 2;
+  const size_t w_align = F == Fmt::MXFP4 ? 1 : 2;
+  if (K % T::kElems != 0 || W == nullptr || Y == nullptr || (X == nullptr && xq_in == nullptr) ||
+      N > (size_t)INT32_MAX || K > (size_t)INT32_MAX || M > (size_t)INT32_MAX ||
+      !aligned(W, w_align) || !aligned(Y, 4) || (X && !aligned(X, 4)) ||
+      (xq_in && !aligned(xq_in, act_align)) || (xq_out && !aligned(xq_out, act_align)) ||
+      (F != Fmt::Q4_0 && (tab0 == nullptr || tab1 == nullptr)) ||
+      (F == Fmt::IQ2_XXS && (!aligned(tab0, 4) || !aligned(tab1, 4))) ||
+      (F == Fmt::MXFP4 && !aligned(tab1, 4))) {
+    set_error(hipErrorInvalidValue);
+    return;
+  }
+  const size_t row_lds = T::kQ8K ? q8k_lds_row_bytes((int)K) : q80_lds_row_bytes((int)K);
+  const size_t fixed = (size_t)kWaves * kWindow + 3072;
+  const size_t cap = max_lds_per_block();
+  if (fixed + row_lds > cap) {
+    set_error(hipErrorInvalidValue);
+    return;
+  }
+  const int mb_max = (int)std::min<size_t>(kMaxRowsPerPass, (cap - fixed) / row_lds);
+  const int cus = cu_count();
+  const int rows_per_wg = (int)((N + cus - 1) / cus);
+  const int grid = (int)((N + rows_per_wg - 1) / rows_per_wg);
+  for (size_t m0 = 0; m0 < M; m0 += mb_max) {
+    Args a;
+    a.W = W;
+    a.X = X;
+    a.xq_in = xq_in;
+    a.xq_out = xq_out;
+    a.tab0 = tab0;
+    a.tab1 = tab1;
+    a.Y = Y;
+    a.N = (int)N;
+    a.K = (int)K;
+    a.m0 = (int)m0;
+    a.mb = (int)std::min<size_t>(mb_max, M - m0);
+    a.rows_per_wg = rows_per_wg;
+    a.y_stride = (long long)N;
+    staged_gemv_kernel<F><<<grid, kThreads, fixed + row_lds * a.mb, current_stream()>>>(a);
+    check_launch();
+  }
+}
+
+}  // namespace
+
+// Decode entry points shared with the prefill file for small M.
+void decode_q4_0(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
+                 size_t M) {
+  launch<Fmt::Q4_0>(W, X, nullptr, Xq, nullptr, nullptr, Y, N, K, M);
+}
+void decode_mxfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
+                  const float* scale, float* Y, size_t N, size_t K, size_t M) {
+  launch<Fmt::MXFP4>(W, X, nullptr, Xq, codebook, scale, Y, N, K, M);
+}
+void decode_iq2_xxs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,
+                    const int8_t* signs, float* Y, size_t N, size_t K, size_t M) {
+  launch<Fmt::IQ2_XXS>(W, X, nullptr, Xq, grid, signs, Y, N, K, M);
+}
+
+}  // namespace weft
+
+extern "C" {
+
+void production_mul_mat_q4_0_decode(const uint8_t* W, const float* X, uint8_t* Xq, float* Y,
+                                    size_t N, size_t K, size_t M) {
+  if (X == nullptr || Xq == nullptr) return weft::set_error(hipErrorInvalidValue);
+  weft::decode_q4_0(W, X, Xq, Y, N, K, M);
+}
+
+void production_mul_mat_mxfp4_decode(const uint8_t* W, const float* X, uint8_t* Xq,
+                                     const int8_t* codebook, const float* scale, float* Y,
+                                     size_t N, size_t K, size_t M) {
+  if (X == nullptr || Xq == nullptr) return weft::set_error(hipErrorInvalidValue);
+  weft::decode_mxfp4(W, X, Xq, codebook, scale, Y, N, K, M);
+}
+
+void production_mul_mat_iq2_xxs_decode(const uint8_t* W, const float* X, uint8_t* Xq,
+                                       const int8_t* grid, const int8_t* signs, float* Y, size_t N,
+                                       size_t K, size_t M) {
+  if (X == nullptr || Xq == nullptr) return weft::set_error(hipErrorInvalidValue);
+  weft::decode_iq2_xxs(W, X, Xq, grid, signs, Y, N, K, M);
+}
+
+void quantized_vec_dot_q4_0_q8_0(const uint8_t* W, const uint8_t* X, float* Y, size_t K) {
+  if (X == nullptr) return weft::set_error(hipErrorInvalidValue);
+  weft::launch<weft::Fmt::Q4_0>(W, nullptr, X, nullptr, nullptr, nullptr, Y, 1, K, 1);
+}
+
+void quantized_vec_dot_mxfp4_q8_0(const uint8_t* W, const uint8_t* X, const int8_t* codebook,
+                                  const float* scale, float* Y, size_t K) {
+  if (X == nullptr) return weft::set_error(hipErrorInvalidValue);
+  weft::launch<weft::Fmt::MXFP4>(W, nullptr, X, nullptr, codebook, scale, Y, 1, K, 1);
+}
+
+void quantized_vec_dot_iq2_xxs_q8_k(const uint8_t* W, const uint8_t* X, const int8_t* grid,
+                                    const int8_t* signs, float* Y, size_t K) {
+  if (X == nullptr) return weft::set_error(hipErrorInvalidValue);
+  weft::launch<weft::Fmt::IQ2_XXS>(W, nullptr, X, nullptr, grid, signs, Y, 1, K, 1);
+}
+
+}  // extern "C"

@@ -1,0 +1,188 @@
+// Row dequantize: row_dequantize_{q4_0,q4_k,iq2_xxs,mxfp4}
+// (examples/kernels/dequantize/*.py; GGML dequantize_row_* in
+// ggml-quants.c:401-419, :511-529, :1471-1493, :2416-2440).
+//
+// Every product here is exact in fp32 (at most 22 significant bits), and
+// Q4_K's single subtraction rounds once, so the outputs are bit-exact with
+// GGML regardless of contraction.
+//
+// HBM write-bound (Q4_K: 0.56 B read, 4 B written per element).  The mapping
+// is output-major: lane l of a wave writes elements 4l..4l+3 of a 256-element
+// span with one 16-byte store, so each wave store instruction covers 1 KB of
+// contiguous output.  The record bytes a lane needs are re-read by its
+// neighbours from L2/L1 (the records are 7x smaller than the output).
+#include <algorithm>
+
+#include "runtime.h"
+#include "weft_common.h"
+#include "weft_hip.h"
+
+namespace weft {
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ void store4(float* p, float a, float b, float c, float d, bool a16) {
+  if (a16) {
+    *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
+  } else {
+    p[0] = a;
+    p[1] = b;
+    p[2] = c;
+    p[3] = d;
+  }
+}
+
+__device__ __forceinline__ uint32_t ld32(const uint8_t* p, bool a4) {
+  return a4 ? *reinterpret_cast<const uint32_t*>(p) : ld_u32_a2(p);
+}
+
+// Q4_K: one wave per superblock
+__global__ void __launch_bounds__(kThreads) dq_q4k_kernel(const uint8_t* __restrict__ W,
+                                                          float* __restrict__ Y, long long nsb) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const long long wave = ((long long)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const long long nwaves = (long long)gridDim.x * blockDim.x / kWave;
+  const bool a4 = (reinterpret_cast<uintptr_t>(W) & 3) == 0;
+  const bool y16 = (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
+  const int g = lane >> 4;           // 64-element group
+  const int e = (lane & 15) * 4;     // offset inside the group
+  const int sub = 2 * g + (e >= 32); // 32-element sub-block
+  const int qoff = 16 + 32 * g + (e & 31);
+  const int shift = e >= 32 ? 4 : 0;
+  for (long long s = wave; s < nsb; s += nwaves) {
+    const uint8_t* rec = W + s * kQ4_KBytes;
+    const uint32_t h0 = ld32(rec, a4), q0 = ld32(rec + 4, a4), q1 = ld32(rec + 8, a4),
+                   q2 = ld32(rec + 12, a4);
+    const uint32_t qs = ld32(rec + qoff, a4);
+    int sc, m;
+    q4k_scale_min(sub, q0, q1, q2, sc, m);
+    const float d = fp16_to_fp32(h0 & 0xffffu), dmin = fp16_to_fp32(h0 >> 16);
+    const float d1 = d * (float)sc, m1 = dmin * (float)m;
+    const uint32_t n = (qs >> shift) & 0x0f0f0f0fu;
+    store4(Y + s * 256 + 4 * lane, d1 * (float)(n & 0xff) - m1, d1 * (float)((n >> 8) & 0xff) - m1,
+           d1 * (float)((n >> 16) & 0xff) - m1, d1 * (float)(n >> 24) - m1, y16);
+  }
+}
+
+// Q4_0 / MXFP4: 8 lanes per 32-block, 8 blocks per wave step
+template <bool MX>
+__global__ void __launch_bounds__(kThreads) dq_32_kernel(const uint8_t* __restrict__ W,
+                                                         const int8_t* __restrict__ codebook,
+                                                         const float* __restrict__ scale,
+                                                         float* __restrict__ Y, long long nb) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const long long wave = ((long long)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const long long nwaves = (long long)gridDim.x * blockDim.x / kWave;
+  const bool y16 = (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
+  const int p = lane & 7;
+  const int shift = p >= 4 ? 4 : 0;
+  const long long steps = (nb + 7) / 8;
+  for (long long st = wave; st < steps; st += nwaves) {
+    const long long b = 8 * st + lane / 8;
+    if (b >= nb) continue;
+    float v[4];
+    if constexpr (MX) {
+      const uint8_t* rec = W + b * kMxfp4Bytes;
+      const float d = scale[rec[0]];
+      const uint32_t qs = ld_u32_a1(rec + 1 + 4 * (p & 3));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = (float)codebook[(qs >> (8 * i + shift)) & 0xf] * d;
+    } else {
+      const uint8_t* rec = W + b * kQ4_0Bytes;
+      const float d = fp16_to_fp32(ld_u16(rec));
+      const uint32_t qs = ld_u32_a2(rec + 2 + 4 * (p & 3));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = (float)((int)((qs >> (8 * i + shift)) & 0xf) - 8) * d;
+    }
+    store4(Y + b * 32 + 4 * p, v[0], v[1], v[2], v[3], y16);
+  }
+}
+
+// IQ2_XXS: one wave per superblock; lane l -> elements 4l..4l+3
+__global__ void __launch_bounds__(kThreads) dq_iq2xxs_kernel(const uint8_t* __restrict__ W,
+                                                             const int8_t* __restrict__ grid,
+                                                             const int8_t* __restrict__ signs,
+                                                             float* __restrict__ Y, long long nsb) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const long long wave = ((long long)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const long long nwaves = (long long)gridDim.x * blockDim.x / kWave;
+  const bool y16 = (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
+  const int c = lane >> 1;     // 8-element chunk 0..31
+  const int h = lane & 1;      // which 4 of the 8
+  const int g = c >> 2, l = c & 3;
+  for (long long s = wave; s < nsb; s += nwaves) {
+    const uint8_t* rec = W + s * kIq2xxsBytes;
+    const float d = fp16_to_fp32(ld_u16(rec));
+    const uint32_t idx = rec[2 + 8 * g + l];
+    const uint32_t meta = ld_u32_a2(rec + 2 + 8 * g + 4);
+    const float db = d * (0.5f + (float)(meta >> 28)) * 0.25f;
+    const int sidx = (int)((meta >> (7 * l)) & 127u);
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = 4 * h + i;
+      v[i] = (float)((int)grid[8 * idx + j] * (int)signs[8 * sidx + j]) * db;
+    }
+    store4(Y + s * 256 + 4 * lane, v[0], v[1], v[2], v[3], y16);
+  }
+}
+
+int grid_for(long long waves_needed) {
+  const long long per_block = kThreads / kWave;
+  const long long cap = (long long)cu_count() * 16;
+  return (int)std::max<long long>(1, std::min<long long>(cap, (waves_needed + per_block - 1) / per_block));
+}
+
+bool bad(const void* W, size_t wa, const float* Y) {
+  return W == nullptr || Y == nullptr || !aligned(W, wa) || !aligned(Y, 4);
+}
+
+}  // namespace
+}  // namespace weft
+
+extern "C" {
+
+void row_dequantize_q4_k(const uint8_t* W, float* Y, size_t K) {
+  using namespace weft;
+  if (K == 0) return;
+  if (K % 256 || bad(W, 2, Y)) return set_error(hipErrorInvalidValue);
+  const long long nsb = (long long)(K / 256);
+  dq_q4k_kernel<<<grid_for(nsb), kThreads, 0, current_stream()>>>(W, Y, nsb);
+  check_launch();
+}
+
+void row_dequantize_q4_0(const uint8_t* W, float* Y, size_t K) {
+  using namespace weft;
+  if (K == 0) return;
+  if (K % 32 || bad(W, 2, Y)) return set_error(hipErrorInvalidValue);
+  const long long nb = (long long)(K / 32);
+  dq_32_kernel<false><<<grid_for((nb + 7) / 8), kThreads, 0, current_stream()>>>(W, nullptr, nullptr,
+                                                                                 Y, nb);
+  check_launch();
+}
+
+void row_dequantize_mxfp4(const uint8_t* W, const int8_t* codebook, const float* scale, float* Y,
+                          size_t K) {
+  using namespace weft;
+  if (K == 0) return;
+  if (K % 32 || bad(W, 1, Y) || codebook == nullptr || scale == nullptr || !aligned(scale, 4))
+    return set_error(hipErrorInvalidValue);
+  const long long nb = (long long)(K / 32);
+  dq_32_kernel<true><<<grid_for((nb + 7) / 8), kThreads, 0, current_stream()>>>(W, codebook, scale,
+                                                                                Y, nb);
+  check_launch();
+}
+
+void row_dequantize_iq2_xxs(const uint8_t* W, const int8_t* grid, const int8_t* signs, float* Y,
+                            size_t K) {
+  using namespace weft;
+  if (K == 0) return;
+  if (K % 256 || bad(W, 2, Y) || grid == nullptr || signs == nullptr)
+    return set_error(hipErrorInvalidValue);
+  const long long nsb = (long long)(K / 256);
+  dq_iq2xxs_kernel<<<grid_for(nsb), kThreads, 0, current_stream()>>>(W, grid, signs, Y, nsb);
+  check_launch();
+}
+
+}  // extern "C"

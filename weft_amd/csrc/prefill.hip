@@ -1,0 +1,45 @@
+// Prefill (many activation rows) production mul_mat entry points.
+//
+// production_mul_mat_{q4_0,q4_k,q4_k_staged,iq2_xxs,iq2_xxs_staged,mxfp4}
+// (examples/kernels/mul_mat/*.py) compute the same Y = X . W^T as the decode
+// kernels; the reference's variants differ only in CPU loop order.  These
+// entry points currently run the decode GEMV kernels, which re-stream W once
+// per four activation rows.
+#include "kernels.h"
+#include "runtime.h"
+#include "weft_hip.h"
+
+extern "C" {
+
+void production_mul_mat_q4_0(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N,
+                             size_t K, size_t M) {
+  weft::decode_q4_0(W, X, Xq, Y, N, K, M);
+}
+
+void production_mul_mat_q4_k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N,
+                             size_t K, size_t M) {
+  weft::decode_q4k(W, X, Xq, Y, N, K, M);
+}
+
+void production_mul_mat_q4_k_staged(const uint8_t* W, const float* X, uint8_t* Xq, float* Y,
+                                    size_t N, size_t K, size_t M) {
+  weft::decode_q4k(W, X, Xq, Y, N, K, M);
+}
+
+void production_mul_mat_iq2_xxs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,
+                                const int8_t* signs, float* Y, size_t N, size_t K, size_t M) {
+  weft::decode_iq2_xxs(W, X, Xq, grid, signs, Y, N, K, M);
+}
+
+void production_mul_mat_iq2_xxs_staged(const uint8_t* W, const float* X, uint8_t* Xq,
+                                       const int8_t* grid, const int8_t* signs, float* Y, size_t N,
+                                       size_t K, size_t M) {
+  weft::decode_iq2_xxs(W, X, Xq, grid, signs, Y, N, K, M);
+}
+
+void production_mul_mat_mxfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
+                              const float* scale, float* Y, size_t N, size_t K, size_t M) {
+  weft::decode_mxfp4(W, X, Xq, codebook, scale, Y, N, K, M);
+}
+
+}  // extern "C"

@@ -1,0 +1,100 @@
+// Standalone activation quantizers q8_0_quantize and q8_K_quantize
+// (examples/kernels/quantize/q8_0.py:26-28, q8_k.py:38-40), bit-exact with
+// GGML's quantize_row_q8_0_ref / quantize_row_q8_K_ref
+// (ggml-quants.c:238-261, :2696-2733).
+//
+// HBM-bound (read 4 B, write ~1.1 B per element).  Q8_K: one wave per
+// superblock, lane l owns x[4l..4l+3] (one 16-byte load); the first-index
+// |max| and the 16-sums are wave reductions.  Q8_0: 8 lanes per block,
+// 8 blocks per wave step.  The grid is sized to a few waves per CU and
+// strides over the blocks.
+#include <algorithm>
+
+#include "runtime.h"
+#include "weft_common.h"
+#include "weft_hip.h"
+
+namespace weft {
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float4 ldx4(const float* p, bool a16) {
+  if (a16) return *reinterpret_cast<const float4*>(p);
+  return make_float4(p[0], p[1], p[2], p[3]);
+}
+
+__global__ void __launch_bounds__(kThreads) q8k_quantize_kernel(const float* __restrict__ X,
+                                                                uint8_t* __restrict__ Y, long long nb) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const long long wave = ((long long)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const long long nwaves = (long long)gridDim.x * blockDim.x / kWave;
+  const bool a16 = (reinterpret_cast<uintptr_t>(X) & 15) == 0;
+  for (long long b = wave; b < nb; b += nwaves) {
+    const float4 x = ldx4(X + b * 256 + 4 * lane, a16);
+    const Q8KLane r = q8k_quantize_wave(x, lane);
+    uint8_t* rec = Y + b * kQ8_KBytes;
+    reinterpret_cast<int*>(rec + 4)[lane] = pack4_i8(r.q);
+    if (lane == 0) *reinterpret_cast<float*>(rec) = r.d;
+    if (!r.zero && (lane & 3) == 0) reinterpret_cast<int16_t*>(rec + 260)[lane / 4] = (int16_t)r.bsum16;
+  }
+}
+
+__global__ void __launch_bounds__(kThreads) q80_quantize_kernel(const float* __restrict__ X,
+                                                                uint8_t* __restrict__ Y, long long nb) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const long long wave = ((long long)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const long long nwaves = (long long)gridDim.x * blockDim.x / kWave;
+  const long long steps = (nb + 7) / 8;
+  const bool a16 = (reinterpret_cast<uintptr_t>(X) & 15) == 0;
+  for (long long st = wave; st < steps; st += nwaves) {
+    const long long b = 8 * st + lane / 8;
+    const bool live = b < nb;
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live) x = ldx4(X + b * 32 + 4 * (lane & 7), a16);
+    const Q8_0Lane r = q80_quantize_8lanes(x);
+    if (!live) continue;
+    uint8_t* rec = Y + b * kQ8_0Bytes;
+    const uint32_t packed = (uint32_t)pack4_i8(r.q);
+    uint16_t* q16 = reinterpret_cast<uint16_t*>(rec + 2 + 4 * (lane & 7));
+    q16[0] = (uint16_t)(packed & 0xffffu);
+    q16[1] = (uint16_t)(packed >> 16);
+    if ((lane & 7) == 0) *reinterpret_cast<uint16_t*>(rec) = (uint16_t)r.dh;
+  }
+}
+
+int grid_for(long long waves_needed) {
+  const long long per_block = kThreads / kWave;
+  const long long cap = (long long)cu_count() * 8;  // 8 workgroups (32 waves) per CU
+  return (int)std::max<long long>(1, std::min<long long>(cap, (waves_needed + per_block - 1) / per_block));
+}
+
+}  // namespace
+
+void quantize_q8_k(const float* X, uint8_t* Y, size_t K) {
+  if (K == 0) return;
+  if (K % 256 || X == nullptr || Y == nullptr || !aligned(X, 4) || !aligned(Y, 4))
+    return set_error(hipErrorInvalidValue);
+  const long long nb = (long long)(K / 256);
+  q8k_quantize_kernel<<<grid_for(nb), kThreads, 0, current_stream()>>>(X, Y, nb);
+  check_launch();
+}
+
+void quantize_q8_0(const float* X, uint8_t* Y, size_t K) {
+  if (K == 0) return;
+  if (K % 32 || X == nullptr || Y == nullptr || !aligned(X, 4) || !aligned(Y, 2))
+    return set_error(hipErrorInvalidValue);
+  const long long nb = (long long)(K / 32);
+  q80_quantize_kernel<<<grid_for((nb + 7) / 8), kThreads, 0, current_stream()>>>(X, Y, nb);
+  check_launch();
+}
+
+}  // namespace weft
+
+extern "C" {
+
+void q8_0_quantize(const float* X, uint8_t* Y, size_t K) { weft::quantize_q8_0(X, Y, K); }
+
+void q8_K_quantize(const float* X, uint8_t* Y, size_t K) { weft::quantize_q8_k(X, Y, K); }
+
+}  // extern "C"

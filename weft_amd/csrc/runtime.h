@@ -1,0 +1,24 @@
+// Host-side launch plumbing shared by the libweft_hip entry points:
+// the calling thread's current stream, the sticky per-thread error, and
+// cached device facts.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace weft {
+
+hipStream_t current_stream();
+// Record an error for the calling thread (first one wins until read).
+void set_error(hipError_t e);
+// Check the launch just made and record its error, if any.
+void check_launch();
+// Compute units of the current device (cached per device).
+int cu_count();
+// Largest dynamic LDS a workgroup may request on the current device.
+size_t max_lds_per_block();
+
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+}  // namespace weft

@@ -1,0 +1,284 @@
+// Control API of libweft_hip: current stream, error reporting, device facts
+// and the self-describing ABI metadata.
+//
+// The reference's generated kernels are synchronous C functions with no
+// failure channel (lib/Target/Emission/Emitter.h:491-512).  On a GPU the
+// launch is asynchronous, so each kernel entry point enqueues on the calling
+// thread's current stream and records any launch error in a per-thread
+// sticky slot that weft_hip_get_last_error() returns and clears.
+#include "runtime.h"
+#include "weft_hip.h"
+
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace weft {
+
+namespace {
+thread_local hipStream_t t_stream = nullptr;
+thread_local hipError_t t_error = hipSuccess;
+
+struct DeviceFacts {
+  int cus = 0;
+  size_t lds = 0;
+};
+std::mutex g_facts_mu;
+std::vector<DeviceFacts> g_facts;
+
+const DeviceFacts& facts() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  std::lock_guard<std::mutex> lock(g_facts_mu);
+  if ((int)g_facts.size() <= dev) g_facts.resize(dev + 1);
+  DeviceFacts& f = g_facts[dev];
+  if (f.cus == 0) {
+    int cus = 0, lds = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
+        lds <= 0)
+      lds = 64 * 1024;
+    f.cus = cus;
+    f.lds = (size_t)lds;
+  }
+  return f;
+}
+}  // namespace
+
+hipStream_t current_stream() { return t_stream; }
+
+void set_error(hipError_t e) {
+  if (e != hipSuccess && t_error == hipSuccess) t_error = e;
+}
+
+void check_launch() { set_error(hipGetLastError()); }
+
+int cu_count() { return facts().cus; }
+
+size_t max_lds_per_block() { return facts().lds; }
+
+}  // namespace weft
+
+extern "C" {
+
+int weft_hip_set_stream(void* stream) {
+  weft::t_stream = reinterpret_cast<hipStream_t>(stream);
+  return 0;
+}
+
+void* weft_hip_get_stream(void) { return reinterpret_cast<void*>(weft::t_stream); }
+
+int weft_hip_get_last_error(void) {
+  const hipError_t e = weft::t_error;
+  weft::t_error = hipSuccess;
+  return (int)e;
+}
+
+const char* weft_hip_error_string(int code) { return hipGetErrorString((hipError_t)code); }
+
+int weft_hip_synchronize(void) {
+  const hipError_t e = hipStreamSynchronize(weft::t_stream);
+  weft::set_error(e);
+  return (int)e;
+}
+
+const char* weft_hip_version(void) { return WEFT_HIP_VERSION_STRING; }
+
+}  // extern "C"
+
+// ------------------------------------------------------------ ABI metadata
+// One record per exported kernel, mirroring the JSON weft-compile writes
+// (tools/weft-compile/weft-compile.cpp:116-147) with the rules of
+// Emitter::kernelABI / argumentCType (lib/Target/Emission/Emitter.h:274-343,
+// :465-489): alias sets follow the frontend's numbering
+// (python/weft/frontend/compiler.py:342-361: 0 = no declared group, 1.. =
+// declared groups in parameter order), `restrict` only on an argument that
+// is alone in its non-negative set.
+namespace {
+
+struct EncodingInfo {
+  const char* name;
+  const char* element;  // C element type
+  int storage_bytes, record_elements, alignment;
+};
+
+const EncodingInfo kEncodings[] = {
+    {"Q4_0", "uint8_t", 18, 32, 2},      {"Q4_K", "uint8_t", 144, 256, 2},
+    {"Q8_0", "uint8_t", 34, 32, 2},      {"Q8_K", "uint8_t", 292, 256, 4},
+    {"IQ2_XXS", "uint8_t", 66, 256, 2},  {"MXFP4", "uint8_t", 17, 32, 1},
+    {"I8X8", "uint8_t", 8, 8, 8},        {"dense.f32", "float", 4, 1, 4},
+    {"dense.i8", "int8_t", 1, 1, 1},
+};
+
+struct ArgSpec {
+  const char* name;
+  const char* encoding;
+  const char* shape;  // comma separated extents or shape symbols
+  bool writable;
+  const char* group;  // declared alias group or nullptr
+};
+
+struct KernelSpec {
+  const char* symbol;
+  std::vector<ArgSpec> args;
+  const char* shape_parameters;  // comma separated, first-appearance order
+};
+
+std::vector<KernelSpec> kernel_specs() {
+  std::vector<KernelSpec> k;
+  auto mm = [&](const char* sym, const char* wenc, const char* xqenc, bool groups,
+                std::vector<ArgSpec> tables) {
+    std::vector<ArgSpec> a = {{"W", wenc, "N,K", false, nullptr},
+                              {"X", "dense.f32", "M,K", false, nullptr},
+                              {"Xq", xqenc, "M,K", true, groups ? "workspace" : nullptr}};
+    for (auto& t : tables) a.push_back(t);
+    a.push_back({"Y", "dense.f32", "M,N", true, groups ? "output" : nullptr});
+    k.push_back({sym, a, "N,K,M"});
+  };
+  const std::vector<ArgSpec> iq2 = {{"grid", "I8X8", "256,8", false, nullptr},
+                                    {"signs", "I8X8", "128,8", false, nullptr}};
+  const std::vector<ArgSpec> mx = {{"codebook", "dense.i8", "16", false, nullptr},
+                                   {"scale", "dense.f32", "256", false, nullptr}};
+  k.push_back({"row_dequantize_q4_0",
+               {{"W", "Q4_0", "K", false, nullptr}, {"Y", "dense.f32", "K", true, nullptr}}, "K"});
+  k.push_back({"row_dequantize_q4_k",
+               {{"W", "Q4_K", "K", false, nullptr}, {"Y", "dense.f32", "K", true, "output"}}, "K"});
+  k.push_back({"row_dequantize_iq2_xxs",
+               {{"W", "IQ2_XXS", "K", false, nullptr},
+                {"grid", "dense.i8", "2048", false, nullptr},
+                {"signs", "dense.i8", "1024", false, nullptr},
+                {"Y", "dense.f32", "K", true, "output"}},
+               "K"});
+  k.push_back({"row_dequantize_mxfp4",
+               {{"W", "MXFP4", "K", false, nullptr},
+                {"codebook", "dense.i8", "16", false, nullptr},
+                {"scale", "dense.f32", "256", false, nullptr},
+                {"Y", "dense.f32", "K", true, nullptr}},
+               "K"});
+  k.push_back({"q8_0_quantize",
+               {{"X", "dense.f32", "K", false, nullptr}, {"Y", "Q8_0", "K", true, nullptr}}, "K"});
+  k.push_back({"q8_K_quantize",
+               {{"X", "dense.f32", "K", false, nullptr}, {"Y", "Q8_K", "K", true, nullptr}}, "K"});
+  k.push_back({"quantized_vec_dot_q4_0_q8_0",
+               {{"W", "Q4_0", "K", false, nullptr},
+                {"X", "Q8_0", "K", false, nullptr},
+                {"Y", "dense.f32", "1", true, nullptr}},
+               "K"});
+  k.push_back({"quantized_vec_dot_q4_k_q8_k",
+               {{"W", "Q4_K", "K", false, nullptr},
+                {"X", "Q8_K", "K", false, nullptr},
+                {"Y", "dense.f32", "1", true, nullptr}},
+               "K"});
+  k.push_back({"quantized_vec_dot_iq2_xxs_q8_k",
+               {{"W", "IQ2_XXS", "K", false, nullptr},
+                {"X", "Q8_K", "K", false, nullptr},
+                iq2[0],
+                iq2[1],
+                {"Y", "dense.f32", "1", true, nullptr}},
+               "K"});
+  k.push_back({"quantized_vec_dot_mxfp4_q8_0",
+               {{"W", "MXFP4", "K", false, nullptr},
+                {"X", "Q8_0", "K", false, nullptr},
+                mx[0],
+                mx[1],
+                {"Y", "dense.f32", "1", true, nullptr}},
+               "K"});
+  mm("production_mul_mat_q4_0", "Q4_0", "Q8_0", false, {});
+  mm("production_mul_mat_q4_0_decode", "Q4_0", "Q8_0", false, {});
+  mm("production_mul_mat_q4_k", "Q4_K", "Q8_K", false, {});
+  mm("production_mul_mat_q4_k_decode", "Q4_K", "Q8_K", true, {});
+  mm("production_mul_mat_q4_k_staged", "Q4_K", "Q8_K", false, {});
+  mm("production_mul_mat_iq2_xxs", "IQ2_XXS", "Q8_K", false, iq2);
+  mm("production_mul_mat_iq2_xxs_decode", "IQ2_XXS", "Q8_K", true, iq2);
+  mm("production_mul_mat_iq2_xxs_staged", "IQ2_XXS", "Q8_K", true, iq2);
+  mm("production_mul_mat_mxfp4", "MXFP4", "Q8_0", false, mx);
+  mm("production_mul_mat_mxfp4_decode", "MXFP4", "Q8_0", true, mx);
+  return k;
+}
+
+std::string json_str(const std::string& s) { return "\"" + s + "\""; }
+
+std::string build_artifact() {
+  std::string out = "{\"kind\": \"weft-hip-artifact\", \"version\": ";
+  out += json_str(WEFT_HIP_VERSION_STRING);
+  out += ", \"kernels\": [";
+  bool first_kernel = true;
+  for (const KernelSpec& ks : kernel_specs()) {
+    // alias sets: declared groups numbered from 1 in parameter order
+    std::vector<std::string> groups;
+    std::vector<int> sets;
+    for (const ArgSpec& a : ks.args) {
+      if (a.group == nullptr) {
+        sets.push_back(0);
+        continue;
+      }
+      int id = 0;
+      for (size_t i = 0; i < groups.size(); ++i)
+        if (groups[i] == a.group) id = (int)i + 1;
+      if (id == 0) {
+        groups.push_back(a.group);
+        id = (int)groups.size();
+      }
+      sets.push_back(id);
+    }
+    if (!first_kernel) out += ", ";
+    first_kernel = false;
+    out += "{\"symbol\": " + json_str(ks.symbol) +
+           ", \"gfx_arch\": \"gfx950\", \"wavefront_size\": 64, \"arguments\": [";
+    for (size_t i = 0; i < ks.args.size(); ++i) {
+      const ArgSpec& a = ks.args[i];
+      const EncodingInfo* e = nullptr;
+      for (const EncodingInfo& c : kEncodings)
+        if (std::string(c.name) == a.encoding) e = &c;
+      int members = 0;
+      for (int s : sets) members += s == sets[i];
+      const std::string ctype = std::string(a.writable ? "" : "const ") + e->element +
+                                (members == 1 ? " *restrict" : " *");
+      std::string shape = "[";
+      std::string dims = a.shape;
+      size_t pos = 0;
+      bool first = true;
+      while (pos <= dims.size()) {
+        size_t next = dims.find(',', pos);
+        if (next == std::string::npos) next = dims.size();
+        if (!first) shape += ", ";
+        first = false;
+        shape += json_str(dims.substr(pos, next - pos));
+        pos = next + 1;
+      }
+      shape += "]";
+      if (i) out += ", ";
+      out += "{\"name\": " + json_str(a.name) + ", \"c_type\": " + json_str(ctype) +
+             ", \"encoding\": " + json_str(a.encoding) + ", \"shape\": " + shape +
+             ", \"storage_bytes\": " + std::to_string(e->storage_bytes) +
+             ", \"record_elements\": " + std::to_string(e->record_elements) +
+             ", \"alignment\": " + std::to_string(e->alignment) +
+             ", \"alias_set\": " + std::to_string(sets[i]) +
+             ", \"writable\": " + (a.writable ? "true" : "false") + "}";
+    }
+    out += "], \"shape_parameters\": [";
+    std::string sp = ks.shape_parameters;
+    size_t pos = 0;
+    bool first = true;
+    while (pos <= sp.size()) {
+      size_t next = sp.find(',', pos);
+      if (next == std::string::npos) next = sp.size();
+      if (!first) out += ", ";
+      first = false;
+      out += json_str(sp.substr(pos, next - pos));
+      pos = next + 1;
+    }
+    out += "], \"bindings\": {}}";
+  }
+  out += "]}";
+  return out;
+}
+
+}  // namespace
+
+extern "C" const char* weft_hip_artifact(void) {
+  static const std::string artifact = build_artifact();
+  return artifact.c_str();
+}

@@ -1,0 +1,221 @@
+// Device helpers shared by the libweft_hip kernels (gfx950 / CDNA4, wave64).
+//
+// Record layouts are GGML's block formats, byte for byte (vendored
+// ggml-common.h of the reference: block_q4_0 :184-189, block_mxfp4 :204-209,
+// block_q8_0 :241-246, block_q4_K :317-328, block_q8_K :361-366,
+// block_iq2_xxs :371-375).  Kernels read them as raw little-endian bytes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace weft {
+
+constexpr int kWave = 64;
+
+// Record geometry: elements per record, bytes per record.
+constexpr int kQ4_0Elems = 32, kQ4_0Bytes = 18;
+constexpr int kMxfp4Elems = 32, kMxfp4Bytes = 17;
+constexpr int kQ8_0Elems = 32, kQ8_0Bytes = 34;
+constexpr int kQ4_KElems = 256, kQ4_KBytes = 144;
+constexpr int kQ8_KElems = 256, kQ8_KBytes = 292;
+constexpr int kIq2xxsElems = 256, kIq2xxsBytes = 66;
+
+// ---------------------------------------------------------------- numerics
+// IEEE binary16 -> binary32, exact (zero, subnormal, normal, inf, NaN).
+__device__ __forceinline__ float fp16_to_fp32(uint32_t h) {
+  const uint32_t sign = (h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1fu;
+  const uint32_t m = h & 0x3ffu;
+  uint32_t bits;
+  if (e == 0) {
+    bits = __float_as_uint((float)m * 0x1p-24f);
+  } else if (e == 31) {
+    bits = 0x7f800000u | (m << 13);
+  } else {
+    bits = ((e + 112u) << 23) | (m << 13);
+  }
+  return __uint_as_float(sign | bits);
+}
+
+// IEEE binary32 -> binary16, round to nearest even; NaN -> 0x7E00 (sign
+// kept), as GGML's software conversion (ggml-impl.h:407-431).
+__device__ __forceinline__ uint32_t fp32_to_fp16(float f) {
+  const uint32_t x = __float_as_uint(f);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  const uint32_t ax = x & 0x7fffffffu;
+  if (ax > 0x7f800000u) return sign | 0x7e00u;
+  if (ax == 0x7f800000u) return sign | 0x7c00u;
+  const int e = (int)(ax >> 23) - 112;
+  uint32_t m = ax & 0x7fffffu;
+  if (e >= 31) return sign | 0x7c00u;
+  if (e <= 0) {
+    if ((ax >> 23) == 0 && m == 0) return sign;
+    m |= (ax >> 23) ? 0x800000u : 0u;
+    const int shift = 14 - e;
+    if (shift >= 32) return sign;
+    const uint32_t res = m >> shift;
+    const uint32_t rem = m & ((1u << shift) - 1u);
+    const uint32_t half = 1u << (shift - 1);
+    return sign | (res + ((rem > half || (rem == half && (res & 1u))) ? 1u : 0u));
+  }
+  uint32_t r = ((uint32_t)e << 10) | (m >> 13);
+  const uint32_t rem = m & 0x1fffu;
+  r += (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) ? 1u : 0u;
+  return sign | r;
+}
+
+// ---------------------------------------------------------- unaligned loads
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
+  return (uint32_t)(*reinterpret_cast<const uint16_t*>(p));
+}
+// 4 bytes at a 2-byte aligned address
+__device__ __forceinline__ uint32_t ld_u32_a2(const uint8_t* p) {
+  const uint16_t* q = reinterpret_cast<const uint16_t*>(p);
+  return (uint32_t)q[0] | ((uint32_t)q[1] << 16);
+}
+// 4 bytes at any address
+__device__ __forceinline__ uint32_t ld_u32_a1(const uint8_t* p) {
+  return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+// -------------------------------------------------------- wave reductions
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+// sum over aligned groups of G lanes (G a power of two <= 64)
+template <int G, typename T>
+__device__ __forceinline__ T group_sum(T v) {
+#pragma unroll
+  for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int o = G / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// int8 x int8 dot of 4 packed bytes, accumulated (v_dot4_i32_i8)
+__device__ __forceinline__ int dot4(int a, int b, int c) {
+  return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+// Q4_K 6-bit scale and min of sub-block s (0..7) from the 12 scale bytes
+// held as three little-endian words q0 = bytes 0-3, q1 = 4-7, q2 = 8-11
+// (get_scale_min_k4, ggml-quants.c:822-829).
+__device__ __forceinline__ void q4k_scale_min(int s, uint32_t q0, uint32_t q1, uint32_t q2,
+                                              int& sc, int& m) {
+  if (s < 4) {
+    sc = (q0 >> (8 * s)) & 63;
+    m = (q1 >> (8 * s)) & 63;
+  } else {
+    const int t = 8 * (s - 4);
+    const uint32_t hi = (q2 >> t) & 0xffu;  // byte s+4
+    sc = (hi & 0xF) | (((q0 >> t) >> 6 & 3) << 4);
+    m = (hi >> 4) | (((q1 >> t) >> 6 & 3) << 4);
+  }
+}
+
+// ------------------------------------------------- activation quantizers
+// One Q8_K superblock (256 fp32) quantized by one wave: lane l holds
+// x[4l .. 4l+3].  quantize_row_q8_K_ref, ggml-quants.c:2696-2733:
+// the value at the first index of the largest |x| gives iscale = -127/max,
+// q = min(127, rne(iscale * x)), d = 1/iscale; all-zero -> d = 0, q = 0,
+// bsums not written (signalled by zero == true).
+struct Q8KLane {
+  int q[4];       // quantized values of this lane
+  float d;        // block scale (wave-uniform)
+  int bsum16;     // sum over this lane's 16-group (lanes 4g..4g+3), valid in every lane
+  bool zero;      // all-zero block
+};
+
+__device__ __forceinline__ Q8KLane q8k_quantize_wave(float4 x, int lane) {
+#pragma clang fp contract(off)
+  Q8KLane r;
+  float xv[4] = {x.x, x.y, x.z, x.w};
+  float best = 0.f, bval = 0.f;
+  int bidx = 0x7fffffff;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float ax = fabsf(xv[i]);
+    if (ax > best) {
+      best = ax;
+      bval = xv[i];
+      bidx = 4 * lane + i;
+    }
+  }
+  // (largest |x|, then smallest index) across the wave
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ob = __shfl_xor(best, o, kWave);
+    const float ov = __shfl_xor(bval, o, kWave);
+    const int oi = __shfl_xor(bidx, o, kWave);
+    if (ob > best || (ob == best && oi < bidx)) {
+      best = ob;
+      bval = ov;
+      bidx = oi;
+    }
+  }
+  r.zero = !(best > 0.f);
+  if (r.zero) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.q[i] = 0;
+    r.d = 0.f;
+    r.bsum16 = 0;
+    return r;
+  }
+  const float iscale = __fdiv_rn(-127.f, bval);
+  int s = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float p = iscale * xv[i];
+    const int v = (int)rintf(p);
+    r.q[i] = v < 127 ? v : 127;
+    s += r.q[i];
+  }
+  r.bsum16 = group_sum<4>(s);
+  r.d = __fdiv_rn(1.f, iscale);
+  return r;
+}
+
+// One Q8_0 block (32 fp32) quantized by 8 lanes, lane holds 4 values.
+// quantize_row_q8_0_ref, ggml-quants.c:238-261: d = amax/127,
+// q = roundf(x * (1/d)) (half away from zero), fp16(d) stored.
+struct Q8_0Lane {
+  int q[4];
+  float d;        // fp32 d (before fp16 rounding)
+  uint32_t dh;    // fp16 bits of d
+};
+
+__device__ __forceinline__ Q8_0Lane q80_quantize_8lanes(float4 x) {
+#pragma clang fp contract(off)
+  Q8_0Lane r;
+  float amax = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+  amax = group_max<8>(amax);
+  const float d = __fdiv_rn(amax, 127.f);
+  const float id = d != 0.f ? __fdiv_rn(1.f, d) : 0.f;
+  const float xv[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r.q[i] = (int)roundf(xv[i] * id);
+  r.d = d;
+  r.dh = fp32_to_fp16(d);
+  return r;
+}
+
+__device__ __forceinline__ int pack4_i8(const int q[4]) {
+  return (int)((uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
+               ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24));
+}
+
+}  // namespace weft
