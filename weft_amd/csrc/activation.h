@@ -43,34 +43,86 @@ __device__ inline float4 load_x4(const float* p, bool a16) {
   return make_float4(p[0], p[1], p[2], p[3]);
 }
 
+// Quantize one Q8_K superblock (index idx = m * nsb + s of this launch's
+// activation rows) held as this lane's float4 into LDS, and into xq_out
+// when non-null.
+__device__ inline void q8k_quantize_store(float4 x, int idx, int nsb, int K, int m0,
+                                          uint8_t* __restrict__ xq_out, char* lds, int lane) {
+  const int m = idx / nsb, s = idx - m * nsb;
+  const Q8KLane r = q8k_quantize_wave(x, lane);
+  const Q8KView v = q8k_view(lds, K, m);
+  const int packed = pack4_i8(r.q);
+  reinterpret_cast<int*>(v.qs + 256 * s)[lane] = packed;
+  // bsum16 is replicated in its 4 lanes; the 32-sub-block sum adds groups
+  // 2t and 2t+1, whose first lanes are 8t and 8t+4.
+  const int pair = sum8_of_sum4(r.bsum16);
+  if ((lane & 7) == 0) v.bp[8 * s + lane / 8] = pair;
+  if (lane == 0) v.d[s] = r.d;
+  if (xq_out != nullptr) {
+    uint8_t* rec = xq_out + ((size_t)(m0 + m) * nsb + s) * kQ8_KBytes;
+    if (lane == 0) *reinterpret_cast<float*>(rec) = r.d;
+    reinterpret_cast<int*>(rec + 4)[lane] = packed;
+    if (!r.zero && (lane & 3) == 0)
+      reinterpret_cast<int16_t*>(rec + 260)[lane / 4] = (int16_t)r.bsum16;
+  }
+}
+
+// Two-phase Q8_K staging so a kernel can put the activation's loads in front
+// of its weight stream: prefetch() issues the loads of this wave's first
+// kPrefetch superblocks (vector loads complete in issue order, so waiting for
+// these does not wait for weight loads issued after them); finish()
+// quantizes them into LDS and handles any remaining superblocks.
+struct Q8KStager {
+  static constexpr int kPrefetch = 4;
+  float4 x[kPrefetch];
+
+  __device__ inline void prefetch(const float* __restrict__ X, int K, int m0, int mb) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int nwaves = blockDim.x / kWave;
+    const int nsb = K / 256, total = mb * nsb;
+    const bool a16 = (reinterpret_cast<uintptr_t>(X) & 15) == 0;
+#pragma unroll
+    for (int i = 0; i < kPrefetch; ++i) {
+      const int idx = min(wave + i * nwaves, total - 1);  // clamped: always a valid load
+      const int m = idx / nsb, s = idx - m * nsb;
+      x[i] = load_x4(X + (size_t)(m0 + m) * K + 256 * s + 4 * lane, a16);
+    }
+  }
+
+  __device__ inline void finish(const float* __restrict__ X, uint8_t* __restrict__ xq_out, int K,
+                                int m0, int mb, char* lds) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int nwaves = blockDim.x / kWave;
+    const int nsb = K / 256, total = mb * nsb;
+#pragma unroll
+    for (int i = 0; i < kPrefetch; ++i) {
+      const int idx = wave + i * nwaves;
+      if (idx < total) q8k_quantize_store(x[i], idx, nsb, K, m0, xq_out, lds, lane);
+    }
+    const bool a16 = (reinterpret_cast<uintptr_t>(X) & 15) == 0;
+    for (int idx = wave + kPrefetch * nwaves; idx < total; idx += nwaves) {
+      const int m = idx / nsb, s = idx - m * nsb;
+      const float4 v = load_x4(X + (size_t)(m0 + m) * K + 256 * s + 4 * lane, a16);
+      q8k_quantize_store(v, idx, nsb, K, m0, xq_out, lds, lane);
+    }
+  }
+};
+
 // Quantize rows [m0, m0+mb) of X (row stride K) into LDS; when xq_out is
 // non-null also store the records (Xq row stride K/256 records).
 __device__ inline void stage_q8k_quantize(const float* __restrict__ X, uint8_t* __restrict__ xq_out,
                                           int K, int m0, int mb, char* lds) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int nwaves = blockDim.x / kWave;
   const int nsb = K / 256;
   const bool a16 = (reinterpret_cast<uintptr_t>(X) & 15) == 0;
   for (int idx = wave; idx < mb * nsb; idx += nwaves) {
     const int m = idx / nsb, s = idx - m * nsb;
     const float4 x = load_x4(X + (size_t)(m0 + m) * K + 256 * s + 4 * lane, a16);
-    const Q8KLane r = q8k_quantize_wave(x, lane);
-    const Q8KView v = q8k_view(lds, K, m);
-    const int packed = pack4_i8(r.q);
-    reinterpret_cast<int*>(v.qs + 256 * s)[lane] = packed;
-    // bsum16 is replicated in its 4 lanes; the 32-sub-block sum adds groups
-    // 2t and 2t+1, whose first lanes are 8t and 8t+4.
-    const int pair = r.bsum16 + __shfl_xor(r.bsum16, 4, kWave);
-    if ((lane & 7) == 0) v.bp[8 * s + lane / 8] = pair;
-    if (lane == 0) v.d[s] = r.d;
-    if (xq_out != nullptr) {
-      uint8_t* rec = xq_out + ((size_t)(m0 + m) * nsb + s) * kQ8_KBytes;
-      if (lane == 0) *reinterpret_cast<float*>(rec) = r.d;
-      reinterpret_cast<int*>(rec + 4)[lane] = packed;
-      if (!r.zero && (lane & 3) == 0)
-        reinterpret_cast<int16_t*>(rec + 260)[lane / 4] = (int16_t)r.bsum16;
-    }
+    q8k_quantize_store(x, idx, nsb, K, m0, xq_out, lds, lane);
   }
 }
 
@@ -78,7 +130,7 @@ __device__ inline void stage_q8k_quantize(const float* __restrict__ X, uint8_t* 
 __device__ inline void stage_q8k_load(const uint8_t* __restrict__ xq, int K, int m0, int mb,
                                       char* lds) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int nwaves = blockDim.x / kWave;
   const int nsb = K / 256;
   for (int idx = wave; idx < mb * nsb; idx += nwaves) {
@@ -119,7 +171,7 @@ __device__ inline Q80View q80_view(char* base, int K, int m) {
 __device__ inline void stage_q80_quantize(const float* __restrict__ X, uint8_t* __restrict__ xq_out,
                                           int K, int m0, int mb, char* lds) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int nwaves = blockDim.x / kWave;
   const int nb = K / 32;
   const int steps = (nb + 7) / 8;

@@ -9,21 +9,22 @@
 //   Mn_b = sum_s m_s * (bsum_{2s} + bsum_{2s+1})                 (exact int32)
 //
 // gfx950 mapping.  The kernel is HBM-bound: every weight byte is read once.
-// A wave walks one weight row at a time.  Lane t of a 64-item step owns
-// (superblock s = t/8, 16-byte qs chunk j = t%8): it issues one 16-byte load
-// of its qs chunk and one 16-byte load of the superblock's header (d, dmin,
-// 12 scale bytes; the 8 lanes of a superblock hit the same line), so each
-// step reads 8 whole consecutive superblocks (1152 B) with 16-byte loads.
-// The 32 nibbles of a chunk are two 16-element halves of sub-blocks 2g and
-// 2g+1 (g = j/2); each half is dotted against the Q8_K activation held in
-// LDS with four v_dot4_i32_i8, scaled by its 6-bit sub-block scale (unpacked
-// in VGPRs), and converted to fp32 once per lane.  A row's lanes are summed
-// with a wave reduction.
+// Lane t of a 64-item step owns (superblock s = t/8, 16-byte qs chunk
+// j = t%8): one 16-byte load of its qs chunk and one of the superblock's
+// 16-byte header (the 8 lanes of a superblock share its cache line), so a
+// step reads 8 consecutive superblocks (1152 B).  The 32 nibbles of a chunk
+// are 16-element halves of sub-blocks 2g and 2g+1 (g = j/2); each half is
+// dotted with the Q8_K activation in LDS by four v_dot4_i32_i8, scaled by its
+// 6-bit sub-block scale (unpacked in VGPRs with GGML's 32-bit mask trick) and
+// folded into one fp32 FMA chain per lane.  Rows are summed with DPP.
 //
-// The activation is quantized inside every workgroup (one wave per Q8_K
-// superblock, bit-exact with quantize_row_q8_K_ref) so the whole mul_mat is
-// one launch; workgroup 0 also stores the records into Xq.  The grid has
-// about one workgroup per CU so that quantization is paid once per CU.
+// Chunk c of a wave's work is step (c % iters) of its row (c / iters).  A
+// wave works in rounds of kDepth chunks whose loads are all issued before any
+// is consumed.  The activation's loads go out first, then the first round of
+// weight loads, then the activation is quantized into LDS (one wave per Q8_K
+// superblock, bit-exact with quantize_row_q8_K_ref) while the weights stream
+// in.  Workgroup 0 also stores the quantized records into Xq, so the whole
+// mul_mat is a single launch.
 #include <algorithm>
 
 #include "activation.h"
@@ -32,11 +33,8 @@
 #include "weft_hip.h"
 
 namespace weft {
-namespace {
 
-constexpr int kThreads = 1024;
-constexpr int kMaxRowsPerPass = 4;  // activation rows staged per launch
-constexpr int kChunk = 4;           // 64-item steps loaded before computing
+constexpr int kQ4KDepth = 6;  // 64-item steps in flight per wave
 
 struct Q4KArgs {
   const uint8_t* W;
@@ -65,91 +63,273 @@ __device__ __forceinline__ uint4 load16(const uint8_t* p) {
   }
 }
 
-template <bool A16>
-__global__ void __launch_bounds__(kThreads) q4k_gemv_kernel(Q4KArgs a) {
+// MB: compile-time bound on the activation rows of one launch (a.mb <= MB).
+template <bool A16, int MB, int NT>
+__global__ void __launch_bounds__(NT) q4k_gemv_kernel(Q4KArgs a) {
   extern __shared__ __align__(16) char lds[];
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const int nwaves = blockDim.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  constexpr int nwaves = NT / kWave;
   const int K = a.K;
+  const int nsb = K >> 8;
+  const int items = nsb * 8;
+  const int iters = (items + kWave - 1) / kWave;
+  const size_t rb = (size_t)nsb * kQ4_KBytes;
+  const int row0 = blockIdx.x * a.rows_per_wg + wave;
+  const int row_end = min(a.N, blockIdx.x * a.rows_per_wg + a.rows_per_wg);
+  const int my_rows = row0 < row_end ? (row_end - row0 + nwaves - 1) / nwaves : 0;
+  const int nchunks = my_rows * iters;
+
+  uint4 hb[kQ4KDepth], qb[kQ4KDepth];
+  // lanes past the row's last item re-read its last item (same cache lines)
+  auto issue = [&](int c, uint4& h, uint4& q) {
+    const int r = c / iters, it = c - r * iters;
+    const int t = min(it * kWave + lane, items - 1);
+    const int row = min(row0 + r * nwaves, a.N - 1);  // a wave without rows re-reads a valid row
+    const uint8_t* sb = a.W + (size_t)row * rb + (size_t)(t >> 3) * kQ4_KBytes;
+    h = load16<A16>(sb);
+    q = load16<A16>(sb + 16 + 16 * (t & 7));
+  };
+
+  Q8KStager stager;
+  if (a.X != nullptr) stager.prefetch(a.X, K, a.m0, a.mb);
+  __builtin_amdgcn_sched_barrier(0);
+  // The first round's loads are unconditional (straight-line code keeps the
+  // in-order wait counts exact): past its last chunk a lane re-requests a
+  // chunk it already holds (an L1/L2 hit, never extra HBM traffic).
+#pragma unroll
+  for (int d = 0; d < kQ4KDepth; ++d) issue(min(d, max(nchunks, 1) - 1), hb[d], qb[d]);
+  __builtin_amdgcn_sched_barrier(0);
 
   if (a.X != nullptr)
-    stage_q8k_quantize(a.X, blockIdx.x == 0 ? a.xq_out : nullptr, K, a.m0, a.mb, lds);
+    stager.finish(a.X, blockIdx.x == 0 ? a.xq_out : nullptr, K, a.m0, a.mb, lds);
   else
     stage_q8k_load(a.xq_in, K, a.m0, a.mb, lds);
   __syncthreads();
 
-  const int nsb = K >> 8;
-  const int items = nsb * 8;
-  const size_t rb = (size_t)nsb * kQ4_KBytes;
-  const int row0 = blockIdx.x * a.rows_per_wg;
-  const int row1 = min(a.N, row0 + a.rows_per_wg);
+  float acc[MB];
+#pragma unroll
+  for (int m = 0; m < MB; ++m) acc[m] = 0.f;
 
-  for (int row = row0 + wave; row < row1; row += nwaves) {
-    const uint8_t* wr = a.W + (size_t)row * rb;
-    float acc[kMaxRowsPerPass];
+  for (int base = 0; base < nchunks; base += kQ4KDepth) {
 #pragma unroll
-    for (int m = 0; m < kMaxRowsPerPass; ++m) acc[m] = 0.f;
-
-    for (int t0 = 0; t0 < items; t0 += kWave * kChunk) {
-      uint4 hdr[kChunk], qs[kChunk];
+    for (int d = 0; d < kQ4KDepth; ++d) {
+      const int c = base + d;
+      if (c < nchunks) {
+        const int r = c / iters, it = c - r * iters;
+        const int t = it * kWave + lane;
+        const bool live = t < items;
+        const int tt = live ? t : items - 1;
+        const int s = tt >> 3, j = tt & 7, g = j >> 1, half = j & 1;
+        // 6-bit scales and mins of the 8 sub-blocks as bytes of four words
+        // (the utmp unpack of ggml-cpu/quants.c:676-681)
+        const uint32_t u0 = hb[d].y, u1 = hb[d].z, u2 = hb[d].w;
+        const uint32_t sc03 = u0 & 0x3f3f3f3fu;
+        const uint32_t sc47 = (u2 & 0x0f0f0f0fu) | (((u0 >> 6) & 0x03030303u) << 4);
+        const uint32_t mn03 = u1 & 0x3f3f3f3fu;
+        const uint32_t mn47 = ((u2 >> 4) & 0x0f0f0f0fu) | (((u1 >> 6) & 0x03030303u) << 4);
+        const uint32_t scw = g < 2 ? sc03 : sc47;
+        const uint32_t mnw = g < 2 ? mn03 : mn47;
+        const int sh = 16 * (g & 1);
+        const int sc_lo = (scw >> sh) & 0xff, sc_hi = (scw >> (sh + 8)) & 0xff;
+        const int m_lo = (mnw >> sh) & 0xff, m_hi = (mnw >> (sh + 8)) & 0xff;
+        const float dw = fp16_to_fp32(hb[d].x & 0xffffu);
+        const float dmin = fp16_to_fp32(hb[d].x >> 16);
+        const uint32_t q0 = qb[d].x, q1 = qb[d].y, q2 = qb[d].z, q3 = qb[d].w;
+        const int l0 = (int)(q0 & 0x0f0f0f0fu), l1 = (int)(q1 & 0x0f0f0f0fu);
+        const int l2 = (int)(q2 & 0x0f0f0f0fu), l3 = (int)(q3 & 0x0f0f0f0fu);
+        const int h0 = (int)((q0 >> 4) & 0x0f0f0f0fu), h1 = (int)((q1 >> 4) & 0x0f0f0f0fu);
+        const int h2 = (int)((q2 >> 4) & 0x0f0f0f0fu), h3 = (int)((q3 >> 4) & 0x0f0f0f0fu);
 #pragma unroll
-      for (int c = 0; c < kChunk; ++c) {
-        const int t = t0 + kWave * c + lane;
-        if (t < items) {
-          const uint8_t* sb = wr + (size_t)(t >> 3) * kQ4_KBytes;
-          hdr[c] = load16<A16>(sb);
-          qs[c] = load16<A16>(sb + 16 + 16 * (t & 7));
-        }
-      }
-#pragma unroll
-      for (int c = 0; c < kChunk; ++c) {
-        const int t = t0 + kWave * c + lane;
-        if (t >= items) continue;
-        const int s = t >> 3, j = t & 7, g = j >> 1, half = j & 1;
-        int sc_lo, m_lo, sc_hi, m_hi;
-        q4k_scale_min(2 * g, hdr[c].y, hdr[c].z, hdr[c].w, sc_lo, m_lo);
-        q4k_scale_min(2 * g + 1, hdr[c].y, hdr[c].z, hdr[c].w, sc_hi, m_hi);
-        const float dw = fp16_to_fp32(hdr[c].x & 0xffffu);
-        const float dmin = fp16_to_fp32(hdr[c].x >> 16);
-        const uint32_t q0 = qs[c].x, q1 = qs[c].y, q2 = qs[c].z, q3 = qs[c].w;
-        const uint32_t l0 = q0 & 0x0f0f0f0fu, l1 = q1 & 0x0f0f0f0fu;
-        const uint32_t l2 = q2 & 0x0f0f0f0fu, l3 = q3 & 0x0f0f0f0fu;
-        const uint32_t h0 = (q0 >> 4) & 0x0f0f0f0fu, h1 = (q1 >> 4) & 0x0f0f0f0fu;
-        const uint32_t h2 = (q2 >> 4) & 0x0f0f0f0fu, h3 = (q3 >> 4) & 0x0f0f0f0fu;
-#pragma unroll
-        for (int m = 0; m < kMaxRowsPerPass; ++m) {
+        for (int m = 0; m < MB; ++m) {
           if (m >= a.mb) break;
           const Q8KView v = q8k_view(lds, K, m);
           const int8_t* xb = v.qs + 256 * s + 64 * g + 16 * half;
           const int4 xl = *reinterpret_cast<const int4*>(xb);
           const int4 xh = *reinterpret_cast<const int4*>(xb + 32);
-          int pl = dot4((int)l0, xl.x, 0);
-          pl = dot4((int)l1, xl.y, pl);
-          pl = dot4((int)l2, xl.z, pl);
-          pl = dot4((int)l3, xl.w, pl);
-          int ph = dot4((int)h0, xh.x, 0);
-          ph = dot4((int)h1, xh.y, ph);
-          ph = dot4((int)h2, xh.z, ph);
-          ph = dot4((int)h3, xh.w, ph);
-          const int S = sc_lo * pl + sc_hi * ph;
+          int pl = dot4(l0, xl.x, 0);
+          pl = dot4(l1, xl.y, pl);
+          pl = dot4(l2, xl.z, pl);
+          pl = dot4(l3, xl.w, pl);
+          int ph = dot4(h0, xh.x, 0);
+          ph = dot4(h1, xh.y, ph);
+          ph = dot4(h2, xh.z, ph);
+          ph = dot4(h3, xh.w, ph);
+          // |pl|, |ph| <= 16*15*127 and scales <= 63: 24-bit multiplies are exact
+          const int S = __mul24(sc_lo, pl) + __mul24(sc_hi, ph);
           const int2 bp = *reinterpret_cast<const int2*>(v.bp + 8 * s + 2 * g);
-          const int Mn = half ? 0 : m_lo * bp.x + m_hi * bp.y;
+          const int Mn = half ? 0 : __mul24(m_lo, bp.x) + __mul24(m_hi, bp.y);
           const float dx = v.d[s];
-          acc[m] += (dw * dx) * (float)S - (dmin * dx) * (float)Mn;
+          const float val = dx * (dw * (float)S - dmin * (float)Mn);
+          acc[m] += live ? val : 0.f;
+        }
+        if (it == iters - 1) {
+          const int row = row0 + r * nwaves;
+#pragma unroll
+          for (int m = 0; m < MB; ++m) {
+            if (m >= a.mb) break;
+            const float tot = wave_sum_f(acc[m]);
+            if (lane == 0) a.Y[(size_t)(a.m0 + m) * a.y_stride + row] = tot;
+            acc[m] = 0.f;
+          }
         }
       }
     }
+    if (base + kQ4KDepth < nchunks) {
 #pragma unroll
-    for (int m = 0; m < kMaxRowsPerPass; ++m) {
-      if (m >= a.mb) break;
-      const float tot = wave_sum(acc[m]);
-      if (lane == 0) a.Y[(size_t)(a.m0 + m) * a.y_stride + row] = tot;
+      for (int d = 0; d < kQ4KDepth; ++d)
+        issue(min(base + kQ4KDepth + d, nchunks - 1), hb[d], qb[d]);
     }
   }
 }
 
-// Shared launcher: X != null -> quantize (and write Xq), else read xq_in.
+// ---------------------------------------------------------------------------
+// Batch-1 kernel.  The arithmetic per weight byte decides this kernel on
+// CDNA4: a wave64 VALU op occupies a SIMD16 for 4 cycles, so a CU retires
+// about one wave-instruction per cycle, and the decode of 1 KB of Q4_K costs
+// tens of them.  This variant cuts VALU work per byte:
+//   * lane l of a step owns superblock l/4 of the step and its 64-element
+//     group g = l%4: 32 B of qs (two 16-byte loads) and the 16-byte header,
+//     so one header decode serves 64 weights and a step is 16 consecutive
+//     superblocks (2304 B);
+//   * that lane meets the same 64 activation values in every row, so they
+//     are read from LDS into VGPRs once, after quantization;
+//   * load addresses are a wave-uniform row base (SGPRs) plus a lane-constant
+//     offset, so the weight stream needs no per-load VALU address math.
+// STEPS = steps per row (K <= 4096 * STEPS); RPW = rows per wave per round.
+template <int STEPS, int RPW, int NT>
+__global__ void __launch_bounds__(NT) q4k_gemv_m1_kernel(Q4KArgs a) {
+  extern __shared__ __align__(16) char lds[];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  constexpr int nwaves = NT / kWave;
+  const int K = a.K;
+  const int nsb = K >> 8;
+  const size_t rb = (size_t)nsb * kQ4_KBytes;
+  const int lsb = lane >> 2, g = lane & 3;
+  // lane-constant byte offsets of step st (clamped to the row's last superblock)
+  int off[STEPS];
+  bool live[STEPS];
+#pragma unroll
+  for (int st = 0; st < STEPS; ++st) {
+    const int sb = 16 * st + lsb;
+    live[st] = sb < nsb;
+    off[st] = min(sb, nsb - 1) * kQ4_KBytes;
+  }
+  const int row_first = blockIdx.x * a.rows_per_wg + wave;
+  const int row_end = min(a.N, blockIdx.x * a.rows_per_wg + a.rows_per_wg);
+
+  Q8KStager stager;
+  stager.prefetch(a.X, K, a.m0, 1);
+  // keep the activation loads ahead of the weight loads: waits are in issue
+  // order, so the quantization then waits for X only
+  __builtin_amdgcn_sched_barrier(0);
+
+  uint4 hb[RPW][STEPS], qa[RPW][STEPS], qc[RPW][STEPS];
+  auto issue_round = [&](int rr0) {
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      const int row = min(rr0 + i * nwaves, a.N - 1);  // clamped: always a valid row
+      const uint8_t* wr = a.W + (size_t)row * rb;
+#pragma unroll
+      for (int st = 0; st < STEPS; ++st) {
+        const uint8_t* sb = wr + off[st];
+        hb[i][st] = *reinterpret_cast<const uint4*>(sb);
+        qa[i][st] = *reinterpret_cast<const uint4*>(sb + 16 + 32 * g);
+        qc[i][st] = *reinterpret_cast<const uint4*>(sb + 32 + 32 * g);
+      }
+    }
+  };
+  issue_round(row_first);
+  __builtin_amdgcn_sched_barrier(0);
+
+  stager.finish(a.X, blockIdx.x == 0 ? a.xq_out : nullptr, K, a.m0, 1, lds);
+  __syncthreads();
+
+  // this lane's activation slice of every step
+  int4 xl0[STEPS], xl1[STEPS], xh0[STEPS], xh1[STEPS];
+  float dx[STEPS];
+  int bp0[STEPS], bp1[STEPS];
+  {
+    const Q8KView v = q8k_view(lds, K, 0);
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st) {
+      const int sb = min(16 * st + lsb, nsb - 1);
+      const int8_t* xb = v.qs + 256 * sb + 64 * g;
+      xl0[st] = *reinterpret_cast<const int4*>(xb);
+      xl1[st] = *reinterpret_cast<const int4*>(xb + 16);
+      xh0[st] = *reinterpret_cast<const int4*>(xb + 32);
+      xh1[st] = *reinterpret_cast<const int4*>(xb + 48);
+      dx[st] = live[st] ? v.d[sb] : 0.f;  // dead lanes contribute exactly 0
+      const int2 bp = *reinterpret_cast<const int2*>(v.bp + 8 * sb + 2 * g);
+      bp0[st] = bp.x;
+      bp1[st] = bp.y;
+    }
+  }
+
+  for (int rr0 = row_first; rr0 < row_end; rr0 += RPW * nwaves) {
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      const int row = rr0 + i * nwaves;
+      if (row < row_end) {  // wave-uniform
+        float acc = 0.f;
+#pragma unroll
+        for (int st = 0; st < STEPS; ++st) {
+          const uint4 h = hb[i][st];
+          // 6-bit scale / min of sub-blocks 2g and 2g+1 (the utmp unpack of
+          // ggml-cpu/quants.c:676-681, one word picked per lane)
+          const uint32_t scw = g < 2 ? (h.y & 0x3f3f3f3fu)
+                                     : ((h.w & 0x0f0f0f0fu) | (((h.y >> 6) & 0x03030303u) << 4));
+          const uint32_t mnw = g < 2 ? (h.z & 0x3f3f3f3fu)
+                                     : (((h.w >> 4) & 0x0f0f0f0fu) | (((h.z >> 6) & 0x03030303u) << 4));
+          const int sh = 16 * (g & 1);
+          const int sc_lo = (scw >> sh) & 0xff, sc_hi = (scw >> (sh + 8)) & 0xff;
+          const int m_lo = (mnw >> sh) & 0xff, m_hi = (mnw >> (sh + 8)) & 0xff;
+          const uint4 qa4 = qa[i][st], qc4 = qc[i][st];
+          int pl = dot4((int)(qa4.x & 0x0f0f0f0fu), xl0[st].x, 0);
+          pl = dot4((int)(qa4.y & 0x0f0f0f0fu), xl0[st].y, pl);
+          pl = dot4((int)(qa4.z & 0x0f0f0f0fu), xl0[st].z, pl);
+          pl = dot4((int)(qa4.w & 0x0f0f0f0fu), xl0[st].w, pl);
+          pl = dot4((int)(qc4.x & 0x0f0f0f0fu), xl1[st].x, pl);
+          pl = dot4((int)(qc4.y & 0x0f0f0f0fu), xl1[st].y, pl);
+          pl = dot4((int)(qc4.z & 0x0f0f0f0fu), xl1[st].z, pl);
+          pl = dot4((int)(qc4.w & 0x0f0f0f0fu), xl1[st].w, pl);
+          int ph = dot4((int)((qa4.x >> 4) & 0x0f0f0f0fu), xh0[st].x, 0);
+          ph = dot4((int)((qa4.y >> 4) & 0x0f0f0f0fu), xh0[st].y, ph);
+          ph = dot4((int)((qa4.z >> 4) & 0x0f0f0f0fu), xh0[st].z, ph);
+          ph = dot4((int)((qa4.w >> 4) & 0x0f0f0f0fu), xh0[st].w, ph);
+          ph = dot4((int)((qc4.x >> 4) & 0x0f0f0f0fu), xh1[st].x, ph);
+          ph = dot4((int)((qc4.y >> 4) & 0x0f0f0f0fu), xh1[st].y, ph);
+          ph = dot4((int)((qc4.z >> 4) & 0x0f0f0f0fu), xh1[st].z, ph);
+          ph = dot4((int)((qc4.w >> 4) & 0x0f0f0f0fu), xh1[st].w, ph);
+          // |pl|, |ph| <= 32*15*127 and scales <= 63: 24-bit multiplies are exact
+          const int S = __mul24(sc_lo, pl) + __mul24(sc_hi, ph);
+          const int Mn = __mul24(m_lo, bp0[st]) + __mul24(m_hi, bp1[st]);
+          const float dw = fp16_to_fp32(h.x & 0xffffu);
+          const float dmin = fp16_to_fp32(h.x >> 16);
+          acc += dx[st] * (dw * (float)S - dmin * (float)Mn);
+        }
+        const float tot = wave_sum_f(acc);
+        if (lane == 0) a.Y[row] = tot;
+      }
+    }
+    if (rr0 + RPW * nwaves < row_end) issue_round(rr0 + RPW * nwaves);
+  }
+}
+
+namespace {
+
+constexpr int kMaxRowsPerPass = 4;
+
+template <int MB, int NT>
+void launch_one(bool a16, int grid, size_t lds, const Q4KArgs& a) {
+  if (a16)
+    q4k_gemv_kernel<true, MB, NT><<<grid, NT, lds, current_stream()>>>(a);
+  else
+    q4k_gemv_kernel<false, MB, NT><<<grid, NT, lds, current_stream()>>>(a);
+}
+
+// X != null -> quantize (and write Xq), else read xq_in.
 void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_out, float* Y,
                 size_t N, size_t K, size_t M) {
   if (N == 0 || M == 0 || K == 0) return;
@@ -166,11 +346,40 @@ void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t*
     set_error(hipErrorInvalidValue);  // activation row does not fit in LDS
     return;
   }
+  constexpr int NT = 1024;
   const int mb_max = (int)std::min<size_t>(kMaxRowsPerPass, lds_cap / row_lds);
   const int cus = cu_count();
   const int rows_per_wg = (int)((N + cus - 1) / cus);
   const int grid = (int)((N + rows_per_wg - 1) / rows_per_wg);
   const bool a16 = aligned(W, 16);
+  if (M == 1 && X != nullptr && a16 && aligned(X, 16) && K <= 3 * 4096) {
+    Q4KArgs a;
+    a.W = W;
+    a.X = X;
+    a.xq_in = nullptr;
+    a.xq_out = xq_out;
+    a.Y = Y;
+    a.N = (int)N;
+    a.K = (int)K;
+    a.m0 = 0;
+    a.mb = 1;
+    a.rows_per_wg = rows_per_wg;
+    a.y_stride = (long long)N;
+    const int steps = (int)((K + 4095) / 4096);
+    const int rpw = (rows_per_wg + NT / kWave - 1) / (NT / kWave);
+    auto go = [&](auto kern) {
+      kern<<<grid, NT, row_lds, current_stream()>>>(a);
+      check_launch();
+    };
+    if (steps == 1)
+      rpw <= 1 ? go(q4k_gemv_m1_kernel<1, 1, NT>) : rpw <= 2 ? go(q4k_gemv_m1_kernel<1, 2, NT>)
+               : go(q4k_gemv_m1_kernel<1, 3, NT>);
+    else if (steps == 2)
+      rpw <= 1 ? go(q4k_gemv_m1_kernel<2, 1, NT>) : go(q4k_gemv_m1_kernel<2, 2, NT>);
+    else
+      go(q4k_gemv_m1_kernel<3, 1, NT>);
+    return;
+  }
   for (size_t m0 = 0; m0 < M; m0 += mb_max) {
     Q4KArgs a;
     a.W = W;
@@ -185,10 +394,10 @@ void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t*
     a.rows_per_wg = rows_per_wg;
     a.y_stride = (long long)N;
     const size_t lds = row_lds * a.mb;
-    if (a16)
-      q4k_gemv_kernel<true><<<grid, kThreads, lds, current_stream()>>>(a);
+    if (a.mb == 1)
+      launch_one<1, NT>(a16, grid, lds, a);
     else
-      q4k_gemv_kernel<false><<<grid, kThreads, lds, current_stream()>>>(a);
+      launch_one<kMaxRowsPerPass, NT>(a16, grid, lds, a);
     check_launch();
   }
 }
@@ -210,7 +419,7 @@ void production_mul_mat_q4_k_decode(const uint8_t* W, const float* X, uint8_t* X
     weft::set_error(hipErrorInvalidValue);
     return;
   }
-  weft::launch_q4k(W, X, nullptr, Xq, Y, N, K, M);
+  weft::decode_q4k(W, X, Xq, Y, N, K, M);
 }
 
 void quantized_vec_dot_q4_k_q8_k(const uint8_t* W, const uint8_t* X, float* Y, size_t K) {

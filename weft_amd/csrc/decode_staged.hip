@@ -137,7 +137,7 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
   char* tables = windows + kWaves * kWindow;       // 3 KB of tables
   char* act = tables + 3072;                       // activation rows
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int nwaves = blockDim.x / kWave;
   const int K = a.K;
 
@@ -274,7 +274,7 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
 #pragma unroll
     for (int m = 0; m < kMaxRowsPerPass; ++m) {
       if (m >= a.mb) break;
-      float tot = wave_sum(acc[m]);
+      float tot = wave_sum_f(acc[m]);
       if constexpr (F == Fmt::IQ2_XXS) tot *= 0.125f;
       if (lane == 0) a.Y[(size_t)(a.m0 + m) * a.y_stride + row] = tot;
     }

@@ -23,20 +23,11 @@ constexpr int kQ8_KElems = 256, kQ8_KBytes = 292;
 constexpr int kIq2xxsElems = 256, kIq2xxsBytes = 66;
 
 // ---------------------------------------------------------------- numerics
-// IEEE binary16 -> binary32, exact (zero, subnormal, normal, inf, NaN).
+// IEEE binary16 -> binary32 with v_cvt_f32_f16.  Exact for every input
+// (zero, subnormal, normal, inf; NaN stays NaN): the kernels run with fp16
+// denormals preserved (amdhsa_float_denorm_mode_16_64 = 3).
 __device__ __forceinline__ float fp16_to_fp32(uint32_t h) {
-  const uint32_t sign = (h & 0x8000u) << 16;
-  const uint32_t e = (h >> 10) & 0x1fu;
-  const uint32_t m = h & 0x3ffu;
-  uint32_t bits;
-  if (e == 0) {
-    bits = __float_as_uint((float)m * 0x1p-24f);
-  } else if (e == 31) {
-    bits = 0x7f800000u | (m << 13);
-  } else {
-    bits = ((e + 112u) << 23) | (m << 13);
-  }
-  return __uint_as_float(sign | bits);
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
 // IEEE binary32 -> binary16, round to nearest even; NaN -> 0x7E00 (sign
@@ -64,6 +55,51 @@ __device__ __forceinline__ uint32_t fp32_to_fp16(float f) {
   const uint32_t rem = m & 0x1fffu;
   r += (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) ? 1u : 0u;
   return sign | r;
+}
+
+// ------------------------------------------------------ DPP lane exchange
+// gfx9 DPP controls used by the reductions below.
+constexpr int kDppXor1 = 0xB1;          // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;          // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;   // lane i <-> 7-i inside 8
+constexpr int kDppMirror = 0x140;       // lane i <-> 15-i inside 16
+constexpr int kDppBcast15 = 0x142;      // lane 15 of a row -> next row
+constexpr int kDppBcast31 = 0x143;      // lane 31 -> rows 2 and 3
+
+template <int Ctrl, int RowMask = 0xF>
+__device__ __forceinline__ int dpp(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, Ctrl, RowMask, 0xF, false);
+}
+template <int Ctrl, int RowMask = 0xF>
+__device__ __forceinline__ float dppf(float v) {
+  return __int_as_float(dpp<Ctrl, RowMask>(__float_as_int(v)));
+}
+
+// Sum over aligned groups of 4 / 8 lanes, result in every lane of the group.
+__device__ __forceinline__ int sum4(int v) {
+  v += dpp<kDppXor1>(v);
+  return v + dpp<kDppXor2>(v);
+}
+__device__ __forceinline__ int sum8_of_sum4(int v4) { return v4 + dpp<kDppHalfMirror>(v4); }
+
+// Whole-wave sum / max (max of non-negative values), returned to all lanes.
+__device__ __forceinline__ float wave_sum_f(float v) {
+  v += dppf<kDppXor1>(v);
+  v += dppf<kDppXor2>(v);
+  v += dppf<kDppHalfMirror>(v);
+  v += dppf<kDppMirror>(v);
+  v += dppf<kDppBcast15, 0xA>(v);
+  v += dppf<kDppBcast31, 0xC>(v);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+  v = fmaxf(v, dppf<kDppXor1>(v));
+  v = fmaxf(v, dppf<kDppXor2>(v));
+  v = fmaxf(v, dppf<kDppHalfMirror>(v));
+  v = fmaxf(v, dppf<kDppMirror>(v));
+  v = fmaxf(v, dppf<kDppBcast15, 0xA>(v));
+  v = fmaxf(v, dppf<kDppBcast31, 0xC>(v));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 // ---------------------------------------------------------- unaligned loads
@@ -143,31 +179,9 @@ struct Q8KLane {
 __device__ __forceinline__ Q8KLane q8k_quantize_wave(float4 x, int lane) {
 #pragma clang fp contract(off)
   Q8KLane r;
-  float xv[4] = {x.x, x.y, x.z, x.w};
-  float best = 0.f, bval = 0.f;
-  int bidx = 0x7fffffff;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float ax = fabsf(xv[i]);
-    if (ax > best) {
-      best = ax;
-      bval = xv[i];
-      bidx = 4 * lane + i;
-    }
-  }
-  // (largest |x|, then smallest index) across the wave
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ob = __shfl_xor(best, o, kWave);
-    const float ov = __shfl_xor(bval, o, kWave);
-    const int oi = __shfl_xor(bidx, o, kWave);
-    if (ob > best || (ob == best && oi < bidx)) {
-      best = ob;
-      bval = ov;
-      bidx = oi;
-    }
-  }
-  r.zero = !(best > 0.f);
+  const float xv[4] = {x.x, x.y, x.z, x.w};
+  const float amax = wave_max_nonneg(fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w))));
+  r.zero = !(amax > 0.f);
   if (r.zero) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) r.q[i] = 0;
@@ -175,6 +189,20 @@ __device__ __forceinline__ Q8KLane q8k_quantize_wave(float4 x, int lane) {
     r.bsum16 = 0;
     return r;
   }
+  // the signed value at the first index whose |x| is amax: first lane with
+  // a match (ballot), then that lane's first match
+  float first = 0.f;
+  bool hit = false;
+#pragma unroll
+  for (int i = 3; i >= 0; --i) {
+    if (fabsf(xv[i]) == amax) {
+      first = xv[i];
+      hit = true;
+    }
+  }
+  const unsigned long long hits = __ballot(hit);
+  const int src = __ffsll(hits) - 1;
+  const float bval = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(first), src));
   const float iscale = __fdiv_rn(-127.f, bval);
   int s = 0;
 #pragma unroll
@@ -184,7 +212,7 @@ __device__ __forceinline__ Q8KLane q8k_quantize_wave(float4 x, int lane) {
     r.q[i] = v < 127 ? v : 127;
     s += r.q[i];
   }
-  r.bsum16 = group_sum<4>(s);
+  r.bsum16 = sum4(s);
   r.d = __fdiv_rn(1.f, iscale);
   return r;
 }
