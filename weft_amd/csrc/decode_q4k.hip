@@ -196,8 +196,13 @@ __global__ void __launch_bounds__(NT) q4k_gemv_kernel(Q4KArgs a) {
 //     are read from LDS into VGPRs once, after quantization;
 //   * load addresses are a wave-uniform row base (SGPRs) plus a lane-constant
 //     offset, so the weight stream needs no per-load VALU address math.
-// STEPS = steps per row (K <= 4096 * STEPS); RPW = rows per wave per round.
-template <int STEPS, int RPW, int NT>
+// STEPS = steps per row (K <= 4096 * STEPS).  A wave walks its rows
+// row_first + k * nwaves with one row of lookahead (ping-pong register
+// buffers): the next row's loads are in flight while the current row is
+// computed, so every CU keeps ~16 rows in flight and computes as its data
+// streams in, instead of bursting all its requests up front and computing
+// after the last one lands.
+template <int STEPS, int NT>
 __global__ void __launch_bounds__(NT) q4k_gemv_m1_kernel(Q4KArgs a) {
   extern __shared__ __align__(16) char lds[];
   const int lane = threadIdx.x & (kWave - 1);
@@ -218,6 +223,7 @@ __global__ void __launch_bounds__(NT) q4k_gemv_m1_kernel(Q4KArgs a) {
   }
   const int row_first = blockIdx.x * a.rows_per_wg + wave;
   const int row_end = min(a.N, blockIdx.x * a.rows_per_wg + a.rows_per_wg);
+  const int nrows = row_first < row_end ? (row_end - row_first + nwaves - 1) / nwaves : 0;
 
   Q8KStager stager;
   stager.prefetch(a.X, K, a.m0, 1);
@@ -225,22 +231,22 @@ __global__ void __launch_bounds__(NT) q4k_gemv_m1_kernel(Q4KArgs a) {
   // order, so the quantization then waits for X only
   __builtin_amdgcn_sched_barrier(0);
 
-  uint4 hb[RPW][STEPS], qa[RPW][STEPS], qc[RPW][STEPS];
-  auto issue_round = [&](int rr0) {
+  struct RowBuf {
+    uint4 h[STEPS], qa[STEPS], qc[STEPS];
+  };
+  auto issue = [&](RowBuf& buf, int k) {
+    const int row = min(row_first + k * nwaves, a.N - 1);  // clamped: always a valid row
+    const uint8_t* wr = a.W + (size_t)row * rb;
 #pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-      const int row = min(rr0 + i * nwaves, a.N - 1);  // clamped: always a valid row
-      const uint8_t* wr = a.W + (size_t)row * rb;
-#pragma unroll
-      for (int st = 0; st < STEPS; ++st) {
-        const uint8_t* sb = wr + off[st];
-        hb[i][st] = *reinterpret_cast<const uint4*>(sb);
-        qa[i][st] = *reinterpret_cast<const uint4*>(sb + 16 + 32 * g);
-        qc[i][st] = *reinterpret_cast<const uint4*>(sb + 32 + 32 * g);
-      }
+    for (int st = 0; st < STEPS; ++st) {
+      const uint8_t* sb = wr + off[st];
+      buf.h[st] = *reinterpret_cast<const uint4*>(sb);
+      buf.qa[st] = *reinterpret_cast<const uint4*>(sb + 16 + 32 * g);
+      buf.qc[st] = *reinterpret_cast<const uint4*>(sb + 32 + 32 * g);
     }
   };
-  issue_round(row_first);
+  RowBuf bufA, bufB;
+  issue(bufA, 0);
   __builtin_amdgcn_sched_barrier(0);
 
   stager.finish(a.X, blockIdx.x == 0 ? a.xq_out : nullptr, K, a.m0, 1, lds);
@@ -267,53 +273,63 @@ __global__ void __launch_bounds__(NT) q4k_gemv_m1_kernel(Q4KArgs a) {
     }
   }
 
-  for (int rr0 = row_first; rr0 < row_end; rr0 += RPW * nwaves) {
+  auto compute = [&](const RowBuf& buf, int k) {
+    float acc = 0.f;
 #pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-      const int row = rr0 + i * nwaves;
-      if (row < row_end) {  // wave-uniform
-        float acc = 0.f;
-#pragma unroll
-        for (int st = 0; st < STEPS; ++st) {
-          const uint4 h = hb[i][st];
-          // 6-bit scale / min of sub-blocks 2g and 2g+1 (the utmp unpack of
-          // ggml-cpu/quants.c:676-681, one word picked per lane)
-          const uint32_t scw = g < 2 ? (h.y & 0x3f3f3f3fu)
-                                     : ((h.w & 0x0f0f0f0fu) | (((h.y >> 6) & 0x03030303u) << 4));
-          const uint32_t mnw = g < 2 ? (h.z & 0x3f3f3f3fu)
-                                     : (((h.w >> 4) & 0x0f0f0f0fu) | (((h.z >> 6) & 0x03030303u) << 4));
-          const int sh = 16 * (g & 1);
-          const int sc_lo = (scw >> sh) & 0xff, sc_hi = (scw >> (sh + 8)) & 0xff;
-          const int m_lo = (mnw >> sh) & 0xff, m_hi = (mnw >> (sh + 8)) & 0xff;
-          const uint4 qa4 = qa[i][st], qc4 = qc[i][st];
-          int pl = dot4((int)(qa4.x & 0x0f0f0f0fu), xl0[st].x, 0);
-          pl = dot4((int)(qa4.y & 0x0f0f0f0fu), xl0[st].y, pl);
-          pl = dot4((int)(qa4.z & 0x0f0f0f0fu), xl0[st].z, pl);
-          pl = dot4((int)(qa4.w & 0x0f0f0f0fu), xl0[st].w, pl);
-          pl = dot4((int)(qc4.x & 0x0f0f0f0fu), xl1[st].x, pl);
-          pl = dot4((int)(qc4.y & 0x0f0f0f0fu), xl1[st].y, pl);
-          pl = dot4((int)(qc4.z & 0x0f0f0f0fu), xl1[st].z, pl);
-          pl = dot4((int)(qc4.w & 0x0f0f0f0fu), xl1[st].w, pl);
-          int ph = dot4((int)((qa4.x >> 4) & 0x0f0f0f0fu), xh0[st].x, 0);
-          ph = dot4((int)((qa4.y >> 4) & 0x0f0f0f0fu), xh0[st].y, ph);
-          ph = dot4((int)((qa4.z >> 4) & 0x0f0f0f0fu), xh0[st].z, ph);
-          ph = dot4((int)((qa4.w >> 4) & 0x0f0f0f0fu), xh0[st].w, ph);
-          ph = dot4((int)((qc4.x >> 4) & 0x0f0f0f0fu), xh1[st].x, ph);
-          ph = dot4((int)((qc4.y >> 4) & 0x0f0f0f0fu), xh1[st].y, ph);
-          ph = dot4((int)((qc4.z >> 4) & 0x0f0f0f0fu), xh1[st].z, ph);
-          ph = dot4((int)((qc4.w >> 4) & 0x0f0f0f0fu), xh1[st].w, ph);
-          // |pl|, |ph| <= 32*15*127 and scales <= 63: 24-bit multiplies are exact
-          const int S = __mul24(sc_lo, pl) + __mul24(sc_hi, ph);
-          const int Mn = __mul24(m_lo, bp0[st]) + __mul24(m_hi, bp1[st]);
-          const float dw = fp16_to_fp32(h.x & 0xffffu);
-          const float dmin = fp16_to_fp32(h.x >> 16);
-          acc += dx[st] * (dw * (float)S - dmin * (float)Mn);
-        }
-        const float tot = wave_sum_f(acc);
-        if (lane == 0) a.Y[row] = tot;
-      }
+    for (int st = 0; st < STEPS; ++st) {
+      const uint4 h = buf.h[st];
+      // 6-bit scale / min of sub-blocks 2g and 2g+1 (the utmp unpack of
+      // ggml-cpu/quants.c:676-681, one word picked per lane)
+      const uint32_t scw = g < 2 ? (h.y & 0x3f3f3f3fu)
+                                 : ((h.w & 0x0f0f0f0fu) | (((h.y >> 6) & 0x03030303u) << 4));
+      const uint32_t mnw = g < 2 ? (h.z & 0x3f3f3f3fu)
+                                 : (((h.w >> 4) & 0x0f0f0f0fu) | (((h.z >> 6) & 0x03030303u) << 4));
+      const int sh = 16 * (g & 1);
+      const int sc_lo = (scw >> sh) & 0xff, sc_hi = (scw >> (sh + 8)) & 0xff;
+      const int m_lo = (mnw >> sh) & 0xff, m_hi = (mnw >> (sh + 8)) & 0xff;
+      const uint4 qa4 = buf.qa[st], qc4 = buf.qc[st];
+      int pl = dot4((int)(qa4.x & 0x0f0f0f0fu), xl0[st].x, 0);
+      pl = dot4((int)(qa4.y & 0x0f0f0f0fu), xl0[st].y, pl);
+      pl = dot4((int)(qa4.z & 0x0f0f0f0fu), xl0[st].z, pl);
+      pl = dot4((int)(qa4.w & 0x0f0f0f0fu), xl0[st].w, pl);
+      pl = dot4((int)(qc4.x & 0x0f0f0f0fu), xl1[st].x, pl);
+      pl = dot4((int)(qc4.y & 0x0f0f0f0fu), xl1[st].y, pl);
+      pl = dot4((int)(qc4.z & 0x0f0f0f0fu), xl1[st].z, pl);
+      pl = dot4((int)(qc4.w & 0x0f0f0f0fu), xl1[st].w, pl);
+      int ph = dot4((int)((qa4.x >> 4) & 0x0f0f0f0fu), xh0[st].x, 0);
+      ph = dot4((int)((qa4.y >> 4) & 0x0f0f0f0fu), xh0[st].y, ph);
+      ph = dot4((int)((qa4.z >> 4) & 0x0f0f0f0fu), xh0[st].z, ph);
+      ph = dot4((int)((qa4.w >> 4) & 0x0f0f0f0fu), xh0[st].w, ph);
+      ph = dot4((int)((qc4.x >> 4) & 0x0f0f0f0fu), xh1[st].x, ph);
+      ph = dot4((int)((qc4.y >> 4) & 0x0f0f0f0fu), xh1[st].y, ph);
+      ph = dot4((int)((qc4.z >> 4) & 0x0f0f0f0fu), xh1[st].z, ph);
+      ph = dot4((int)((qc4.w >> 4) & 0x0f0f0f0fu), xh1[st].w, ph);
+      // |pl|, |ph| <= 32*15*127 and scales <= 63: 24-bit multiplies are exact
+      const int S = __mul24(sc_lo, pl) + __mul24(sc_hi, ph);
+      const int Mn = __mul24(m_lo, bp0[st]) + __mul24(m_hi, bp1[st]);
+      const float dw = fp16_to_fp32(h.x & 0xffffu);
+      const float dmin = fp16_to_fp32(h.x >> 16);
+      acc += dx[st] * (dw * (float)S - dmin * (float)Mn);
     }
-    if (rr0 + RPW * nwaves < row_end) issue_round(rr0 + RPW * nwaves);
+    const float tot = wave_sum_f(acc);
+    if (lane == 0) a.Y[row_first + k * nwaves] = tot;
+  };
+
+  // Issues inside the loop are unconditional so the in-order wait counts stay
+  // exact (a conditional issue forces a full wait on the other path).
+  int k = 0;
+  for (; k + 2 < nrows; k += 2) {
+    issue(bufB, k + 1);
+    compute(bufA, k);
+    issue(bufA, k + 2);
+    compute(bufB, k + 1);
+  }
+  if (nrows - k == 2) {
+    issue(bufB, k + 1);
+    compute(bufA, k);
+    compute(bufB, k + 1);
+  } else if (nrows - k == 1) {
+    compute(bufA, k);
   }
 }
 
@@ -353,6 +369,12 @@ void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t*
   const int grid = (int)((N + rows_per_wg - 1) / rows_per_wg);
   const bool a16 = aligned(W, 16);
   if (M == 1 && X != nullptr && a16 && aligned(X, 16) && K <= 3 * 4096) {
+    // batch 1: the register-resident kernel.  One step per row (K <= 4096)
+    // runs 1024-thread workgroups, two per CU (62 VGPRs); longer rows keep
+    // three activation slices in VGPRs and run 512 threads, one per CU.
+    const int steps = (int)((K + 4095) / 4096);
+    const int wgs = steps == 1 ? 2 * cus : cus;
+    const int rpw = (int)((N + wgs - 1) / wgs);
     Q4KArgs a;
     a.W = W;
     a.X = X;
@@ -363,21 +385,16 @@ void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t*
     a.K = (int)K;
     a.m0 = 0;
     a.mb = 1;
-    a.rows_per_wg = rows_per_wg;
+    a.rows_per_wg = rpw;
     a.y_stride = (long long)N;
-    const int steps = (int)((K + 4095) / 4096);
-    const int rpw = (rows_per_wg + NT / kWave - 1) / (NT / kWave);
-    auto go = [&](auto kern) {
-      kern<<<grid, NT, row_lds, current_stream()>>>(a);
-      check_launch();
-    };
+    const int g1 = (int)((N + rpw - 1) / rpw);
     if (steps == 1)
-      rpw <= 1 ? go(q4k_gemv_m1_kernel<1, 1, NT>) : rpw <= 2 ? go(q4k_gemv_m1_kernel<1, 2, NT>)
-               : go(q4k_gemv_m1_kernel<1, 3, NT>);
+      q4k_gemv_m1_kernel<1, 1024><<<g1, 1024, row_lds, current_stream()>>>(a);
     else if (steps == 2)
-      rpw <= 1 ? go(q4k_gemv_m1_kernel<2, 1, NT>) : go(q4k_gemv_m1_kernel<2, 2, NT>);
+      q4k_gemv_m1_kernel<2, 512><<<g1, 512, row_lds, current_stream()>>>(a);
     else
-      go(q4k_gemv_m1_kernel<3, 1, NT>);
+      q4k_gemv_m1_kernel<3, 512><<<g1, 512, row_lds, current_stream()>>>(a);
+    check_launch();
     return;
   }
   for (size_t m0 = 0; m0 < M; m0 += mb_max) {
