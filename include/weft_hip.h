@@ -49,6 +49,11 @@ int weft_hip_get_last_error(void);       /* hipError_t, then cleared */
 const char *weft_hip_error_string(int code);
 int weft_hip_synchronize(void);          /* hipStreamSynchronize(current) */
 const char *weft_hip_version(void);
+/* Target discovery (stands in for weft-compile --query-native-target,
+ * python/weft/runtime/driver.py:62-69): number of visible HIP devices, or a
+ * negative hipError_t; the gcnArchName of device `dev` copied into `buf`. */
+int weft_hip_device_count(void);
+int weft_hip_device_arch(int dev, char *buf, size_t len);
 /* ABI metadata of every exported kernel, as the JSON artifact weft-compile
  * emits (tools/weft-compile/weft-compile.cpp:116-147, kind
  * "weft-hip-artifact", gfx_arch / wavefront_size in place of march / abi /

@@ -1,0 +1,80 @@
+"""The C ABI of libweft_hip, checked without a GPU: the library loads, exports
+every function include/weft_hip.h declares, and its self-describing metadata
+agrees with the header (pointer count, const-ness, size_t shape count) and
+with the reference's ABI rules (lib/Target/Emission/Emitter.h:465-512)."""
+from __future__ import annotations
+
+import re
+from pathlib import Path
+
+import pytest
+
+from weft_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "weft_hip.h"
+
+
+def header_functions() -> dict[str, list[str]]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"^\s*(?:const\s+)?[\w]+\s*\*?\s*(\w+)\(([^)]*)\);", text, re.M):
+        params = [p.strip() for p in m.group(2).replace("\n", " ").split(",") if p.strip() not in ("", "void")]
+        out[m.group(1)] = params
+    return out
+
+
+def test_library_loads_and_reports_version():
+    lib = _lib.load()
+    assert lib.weft_hip_version().decode().startswith("weft_hip")
+    assert lib.weft_hip_get_last_error() == 0
+
+
+def test_every_header_function_is_exported():
+    lib = _lib.load()
+    funcs = header_functions()
+    assert len(funcs) >= 27
+    missing = [name for name in funcs if not hasattr(lib, name)]
+    assert not missing
+
+
+def test_artifact_covers_every_kernel_in_the_header():
+    funcs = {k for k in header_functions() if not k.startswith("weft_hip_")}
+    kernels = {k["symbol"] for k in _lib.artifact()["kernels"]}
+    assert funcs == kernels
+
+
+@pytest.mark.parametrize("kernel", _lib.artifact()["kernels"], ids=lambda k: k["symbol"])
+def test_artifact_matches_header_prototype(kernel):
+    params = header_functions()[kernel["symbol"]]
+    ptrs = [p for p in params if "*" in p]
+    sizes = [p for p in params if p.startswith("size_t")]
+    assert len(ptrs) + len(sizes) == len(params)
+    assert len(ptrs) == len(kernel["arguments"])
+    assert [p.split()[-1] for p in sizes] == kernel["shape_parameters"]
+    for decl, arg in zip(ptrs, kernel["arguments"]):
+        name = decl.replace("*", " ").split()[-1]
+        assert name == arg["name"]
+        assert decl.startswith("const") == (not arg["writable"])
+        assert arg["c_type"].startswith("const ") == (not arg["writable"])
+        # restrict only on an argument alone in its non-negative alias set
+        members = sum(1 for a in kernel["arguments"] if a["alias_set"] == arg["alias_set"])
+        assert arg["c_type"].endswith("*restrict") == (members == 1 and arg["alias_set"] >= 0)
+        assert arg["storage_bytes"] > 0 and arg["record_elements"] > 0 and arg["alignment"] > 0
+
+
+def test_decode_kernels_declare_workspace_and_output_groups():
+    # alias_groups={"Xq": "workspace", "Y": "output"} in the Weft sources
+    for sym in ("production_mul_mat_q4_k_decode", "production_mul_mat_iq2_xxs_decode",
+                "production_mul_mat_mxfp4_decode", "production_mul_mat_iq2_xxs_staged"):
+        args = {a["name"]: a for a in _lib.kernel_metadata(sym)["arguments"]}
+        assert (args["W"]["alias_set"], args["Xq"]["alias_set"], args["Y"]["alias_set"]) == (0, 1, 2)
+    args = {a["name"]: a for a in _lib.kernel_metadata("production_mul_mat_q4_0_decode")["arguments"]}
+    assert {a["alias_set"] for a in args.values()} == {0}
+
+
+def test_invalid_call_records_an_error_without_a_device():
+    lib = _lib.load()
+    # K not a multiple of the record: rejected before any HIP call
+    lib.row_dequantize_q4_k(None, None, 100)
+    assert lib.weft_hip_get_last_error() != 0
+    assert lib.weft_hip_get_last_error() == 0

@@ -1,0 +1,63 @@
+"""End-to-end through weft_amd.runtime (the weft.runtime mirror) on the GPU:
+device Buffers from torch tensors, shape inference, JIT reuse, and the
+reference's native_jit repro case (examples/repro/weft/native_jit.py:52-79:
+one Q4_0 / Q8_0 block replicated x8, K = 256, against the vec_dot oracle)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as o
+from weft_amd import kernels as K
+from weft_amd.runtime import Buffer, compile, jit
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    return torch, torch.device("cuda:0")
+
+
+def test_jit_q4_k_decode_with_device_buffers(torch_dev):
+    torch, dev = torch_dev
+    n, k, m = 1024, 4096, 1
+    w = o.quantize("q4_k", o.seeded_normal(61, (n, k), 0.02))
+    x = o.seeded_normal(62, (m, k))
+    W = Buffer(torch.from_numpy(w).to(dev), shape=(n, k), encoding="Q4_K")
+    xq_t = torch.zeros(m * (k // 256) * 292, dtype=torch.uint8, device=dev)
+    Xq = Buffer(xq_t, shape=(m, k), encoding="Q8_K")
+    y_t = torch.zeros((m, n), dtype=torch.float32, device=dev)
+    fn = jit(K.production_mul_mat_q4_k_decode)
+    fn(W, torch.from_numpy(x).to(dev), Xq, y_t)
+    want_xq = o.quantize("q8_k", x)
+    assert np.array_equal(xq_t.cpu().numpy().reshape(m, -1), want_xq)
+    e, a = o.mul_mat_f64("q4_k", w, want_xq, n, k, m)
+    assert o.within_tolerance(y_t.cpu().numpy(), e, a).all()
+    assert compile(K.production_mul_mat_q4_k_decode) is compile(K.production_mul_mat_q4_k_decode)
+
+
+def test_native_jit_q4_0_replicated_block(torch_dev):
+    torch, dev = torch_dev
+    k = 256
+    rng = np.random.default_rng(0x57454654)
+    wb = o.quantize("q4_0", rng.standard_normal(32).astype(np.float32))
+    xb = o.quantize("q8_0", rng.standard_normal(32).astype(np.float32))
+    w, x = np.tile(wb, 8), np.tile(xb, 8)
+    y_t = torch.zeros(1, dtype=torch.float32, device=dev)
+    fn = compile(K.quantized_vec_dot_q4_0_q8_0)
+    fn(Buffer(torch.from_numpy(w).to(dev), shape=(k,), encoding="Q4_0"),
+       Buffer(torch.from_numpy(x).to(dev), shape=(k,), encoding="Q8_0"), y_t)
+    want = o.vec_dot("q4_0", w, x, k)
+    assert abs(float(y_t.item()) - want) <= 1e-4 + 2e-3 * abs(want)  # native_jit.py tolerance
+
+
+def test_host_buffer_rejected_on_device(torch_dev):
+    torch, dev = torch_dev
+    fn = compile(K.row_dequantize_q4_k)
+    w = torch.zeros(144, dtype=torch.uint8, device=dev)
+    with pytest.raises(TypeError, match="host memory"):
+        fn(Buffer(w, shape=(256,), encoding="Q4_K"), np.zeros(256, np.float32))

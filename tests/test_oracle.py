@@ -1,0 +1,361 @@
+"""Pins the CPU oracle (oracle/weft_oracle.c) before any GPU result is
+compared with it.  Each check is independent of the oracle's own formula:
+
+  * fp16 / e8m0 conversions against numpy's IEEE float16 and math.ldexp;
+  * lookup tables against tests/golden/ggml_tables.json, parsed from the
+    reference's ggml-common.h text by tests/golden/make_tables.py;
+  * dequantizers by brute force over every code at every position, with the
+    expected value built in float64 from the record layout as Weft's own
+    encodings declare it (examples/formats/ggml.py) and its dequantize
+    kernels compute it (examples/kernels/dequantize/*.py) -- a different
+    description from the GGML C the oracle restates;
+  * Q8 quantizers by hand-computed known answers (rounding ties, first-index
+    maximum, all-zero block) and invariants;
+  * vec_dot / mul_mat and the fp64 re-accumulation against an independent
+    numpy path: dequantize both operands to float64 and take the dot.
+GGML itself is not built here: ggml-impl.h includes gguf.h, which the
+reference does not vendor.
+"""
+from __future__ import annotations
+
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle as o
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "ggml_tables.json").read_text())
+
+
+# ------------------------------------------------------------ conversions
+def test_fp16_to_fp32_exhaustive_vs_numpy():
+    h = np.arange(65536, dtype=np.uint16)
+    got = o.fp16_to_fp32(h)
+    want = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_fp32_to_fp16_round_to_nearest_even_vs_numpy():
+    # every fp16 value, every midpoint between neighbours (ties), their
+    # fp32 neighbours, and 2M random bit patterns
+    h = np.arange(0, 0x7c00, dtype=np.uint16)
+    v = h.view(np.float16).astype(np.float64)
+    mids = ((v[:-1] + v[1:]) / 2).astype(np.float32)
+    probes = [v.astype(np.float32), mids, np.nextafter(mids, np.float32(np.inf)),
+              np.nextafter(mids, np.float32(0)), np.float32([65504, 65519.99, 65520, 1e9, 6e-8, 3e-8])]
+    rng = np.random.default_rng(0)
+    probes.append(rng.integers(0, 2**32, 2_000_000, dtype=np.uint64).astype(np.uint32).view(np.float32))
+    x = np.concatenate([np.concatenate([p, -p]) for p in probes]).astype(np.float32)
+    finite = ~np.isnan(x)
+    with np.errstate(over="ignore"):
+        want = x[finite].astype(np.float16).view(np.uint16)
+    got = o.fp32_to_fp16(x)
+    assert np.array_equal(got[finite], want)
+    # NaN keeps its sign and becomes the quiet NaN 0x7E00 (ggml-impl.h:431)
+    assert set(np.unique(got[~finite] & 0x7fff)) <= {0x7e00}
+
+
+def test_e8m0_half_is_two_to_the_e_minus_128():
+    for e in range(256):
+        assert o.e8m0_half(e) == np.float32(math.ldexp(1.0, e - 128)) or (
+            math.ldexp(1.0, e - 128) > 3.4e38)
+    assert np.array_equal(o.e8m0_half_table(),
+                          np.array([np.float32(math.ldexp(1.0, e - 128)) if e < 255 else np.float32(2.0**127)
+                                    for e in range(256)], np.float32))
+
+
+# ----------------------------------------------------------------- tables
+def test_iq2xxs_grid_matches_ggml_table():
+    want = np.array([int(x, 16) for x in GOLDEN["iq2xxs_grid"]], np.uint64)
+    got = o.iq2xxs_grid().view(np.uint64)
+    assert np.array_equal(got, want)
+    assert set(np.unique(o.iq2xxs_grid())) == {0x08, 0x19, 0x2b}
+
+
+def test_sign_tables_match_ggml():
+    assert list(o.ksigns_iq2xs()) == GOLDEN["ksigns_iq2xs"]
+    kmask = GOLDEN["kmask_iq2xs"]
+    s = o.signs_i8x8().reshape(128, 8)
+    for i, ks in enumerate(GOLDEN["ksigns_iq2xs"]):
+        assert list(s[i]) == [-1 if ks & kmask[j] else 1 for j in range(8)]
+        assert (s[i] < 0).sum() % 2 == 0  # even number of minus signs
+
+
+def test_kvalues_mxfp4_matches_ggml():
+    assert list(o.kvalues_mxfp4()) == GOLDEN["kvalues_mxfp4"]
+
+
+def test_record_sizes_match_ggml_static_asserts():
+    # sizeof expressions of ggml-common.h evaluated with QK4_0 = QK8_0 =
+    # QK_MXFP4 = 32, QK_K = 256, K_SCALE_SIZE = 12, ggml_half = 2 bytes
+    env = {"ggml_half": 2, "uint8_t": 1, "int16_t": 2, "uint16_t": 2, "float": 4,
+           "QK4_0": 32, "QK8_0": 32, "QK_MXFP4": 32, "QK_K": 256, "K_SCALE_SIZE": 12}
+    sizes = {}
+    for k, expr in GOLDEN["record_size_asserts"].items():
+        e = expr.replace("sizeof", "")
+        for name in sorted(env, key=len, reverse=True):
+            e = e.replace(name, str(env[name]))
+        sizes[k] = eval(e, {"__builtins__": {}})  # arithmetic on literals only
+    assert sizes == {"block_q4_0": 18, "block_mxfp4": 17, "block_q8_0": 34, "block_q4_K": 144,
+                     "block_q8_K": 292, "block_iq2_xxs": 66}
+    assert {k: o.RECORD[k][1] for k in o.RECORD} == {
+        "q4_0": 18, "mxfp4": 17, "q8_0": 34, "q4_k": 144, "q8_k": 292, "iq2_xxs": 66}
+
+
+# ------------------------------------------------------------ dequantizers
+def _f16(x: float) -> int:
+    return int(np.float16(x).view(np.uint16))
+
+
+D16 = [_f16(v) for v in (0.5, -0.0373, 1.0, 6.0e-8, -3.0e-5, 1234.0)]
+
+
+def test_dequant_q4_0_brute_force():
+    # Weft Q4_0: f16 d, then q: u4[32] grouped(32) bit_layers(16, lo_first):
+    # element j < 16 is the low nibble of byte j, j >= 16 the high nibble of
+    # byte j-16; value (q - 8) * d (examples/kernels/dequantize/q4_0.py).
+    recs, want = [], []
+    for dh in D16:
+        d = float(np.uint16(dh).view(np.float16))
+        for pos in range(32):
+            for q in range(16):
+                codes = [(pos * 7 + j * 3 + q) % 16 for j in range(32)]
+                codes[pos] = q
+                b = bytearray(18)
+                b[0:2] = dh.to_bytes(2, "little")
+                for j in range(16):
+                    b[2 + j] = codes[j] | (codes[j + 16] << 4)
+                recs.append(bytes(b))
+                want.append([np.float32((c - 8) * d) for c in codes])
+    w = np.frombuffer(b"".join(recs), np.uint8).reshape(len(recs), 18)
+    got = o.dequantize("q4_0", w, 32)
+    assert np.array_equal(got, np.array(want, np.float32))
+
+
+def _pack_q4k_scales(sc, m):
+    """6-bit scale/min packing as quantize_row_q4_K_ref writes it."""
+    out = [0] * 12
+    for j in range(8):
+        if j < 4:
+            out[j] = sc[j]
+            out[j + 4] = m[j]
+        else:
+            out[j + 4] = (sc[j] & 0xF) | ((m[j] & 0xF) << 4)
+            out[j - 4] |= (sc[j] >> 4) << 6
+            out[j] |= (m[j] >> 4) << 6
+    return bytes(out)
+
+
+def test_dequant_q4_k_brute_force():
+    # Weft Q4_K: d, dmin, (sc, m) 6-bit x 8, q: u4[256] grouped(64)
+    # bit_layers(32, lo_first): element e is byte 32*(e//64) + e%32, low
+    # nibble when e%64 < 32; value d*sc*q - dmin*m of sub-block e//32
+    # (examples/kernels/dequantize/q4_k.py, functions/quantization.py:14-17).
+    rng = np.random.default_rng(7)
+    recs, want = [], []
+    for trial in range(600):
+        sc = [int(v) for v in rng.integers(0, 64, 8)]
+        m = [int(v) for v in rng.integers(0, 64, 8)]
+        if trial < 64:  # every scale and min value in every sub-block
+            sc = [(trial + 7 * s) % 64 for s in range(8)]
+            m = [(63 - trial + 5 * s) % 64 for s in range(8)]
+        codes = [int(v) for v in rng.integers(0, 16, 256)]
+        dh, mh = D16[trial % 6], D16[(trial + 3) % 6]
+        d = float(np.uint16(dh).view(np.float16))
+        dm = float(np.uint16(mh).view(np.float16))
+        qs = bytearray(128)
+        for e, c in enumerate(codes):
+            byte = 32 * (e // 64) + e % 32
+            qs[byte] |= c if e % 64 < 32 else c << 4
+        recs.append(dh.to_bytes(2, "little") + mh.to_bytes(2, "little") + _pack_q4k_scales(sc, m) + bytes(qs))
+        want.append([np.float32(d * sc[e // 32] * c - dm * m[e // 32]) for e, c in enumerate(codes)])
+    w = np.frombuffer(b"".join(recs), np.uint8).reshape(len(recs), 144)
+    got = o.dequantize("q4_k", w, 256)
+    assert np.array_equal(got.view(np.uint32), np.array(want, np.float32).view(np.uint32))
+
+
+def test_dequant_mxfp4_brute_force():
+    kv = GOLDEN["kvalues_mxfp4"]
+    recs, want = [], []
+    for e in list(range(0, 256, 5)) + [1, 2, 127, 254]:
+        for q in range(16):
+            codes = [(q + 5 * j) % 16 for j in range(32)]
+            b = bytearray(17)
+            b[0] = e
+            for j in range(16):
+                b[1 + j] = codes[j] | (codes[j + 16] << 4)
+            recs.append(bytes(b))
+            with np.errstate(over="ignore"):  # 12 * 2^126 is +-inf in fp32, as in GGML
+                want.append([np.float32(kv[c] * math.ldexp(1.0, e - 128)) for c in codes])
+    w = np.frombuffer(b"".join(recs), np.uint8).reshape(len(recs), 17)
+    assert np.array_equal(o.dequantize("mxfp4", w, 32), np.array(want, np.float32))
+
+
+def test_dequant_iq2_xxs_brute_force():
+    # examples/kernels/dequantize/iq2_xxs.py: per 32-group g, word pair
+    # q[4g..4g+3]: metadata = q[4g+2] | q[4g+3] << 16; scale = d*(0.5 +
+    # meta>>28)*0.25; entry l: grid row = byte l%2 of q[4g + l//2], sign row
+    # = (meta >> 7l) & 127.
+    grid = np.array([int(x, 16) for x in GOLDEN["iq2xxs_grid"]], np.uint64).view(np.uint8).reshape(256, 8)
+    ks = GOLDEN["ksigns_iq2xs"]
+    rng = np.random.default_rng(3)
+    raw = rng.integers(0, 256, (300, 66), dtype=np.uint8)
+    raw[:, 0:2] = np.array([np.uint16(D16[i % 6]) for i in range(300)], np.uint16).view(np.uint8).reshape(300, 2)
+    want = np.zeros((300, 256), np.float32)
+    for r in range(300):
+        d = float(raw[r, 0:2].view(np.float16)[0])
+        q = raw[r, 2:].view(np.uint16)
+        for gi in range(8):
+            meta = int(q[4 * gi + 2]) | (int(q[4 * gi + 3]) << 16)
+            scale = d * (0.5 + (meta >> 28)) * 0.25
+            for l in range(4):
+                idx = (int(q[4 * gi + l // 2]) >> (8 * (l % 2))) & 0xFF
+                sgn = ks[(meta >> (7 * l)) & 127]
+                for j in range(8):
+                    s = -1 if sgn & (1 << j) else 1
+                    want[r, 32 * gi + 8 * l + j] = np.float32(int(grid[idx, j]) * s * scale)
+    assert np.array_equal(o.dequantize("iq2_xxs", raw, 256).view(np.uint32), want.view(np.uint32))
+
+
+# ---------------------------------------------------------- Q8 quantizers
+def test_q8_0_known_answers():
+    x = np.zeros(64, np.float32)
+    x[0] = 127.0
+    x[1:8] = [0.5, 1.5, 2.5, -0.5, -2.5, 3.5, 126.5]  # d = 1: ties round away from zero
+    x[32:64] = np.linspace(-3.0, 1.0, 32, dtype=np.float32)
+    y = o.quantize("q8_0", x)
+    assert y[0:2].view(np.uint16)[0] == 0x3C00  # fp16(1.0)
+    assert list(y[2:10].view(np.int8)) == [127, 1, 2, 3, -1, -3, 4, 127]
+    d2 = np.float32(3.0) / np.float32(127)
+    assert y[34:36].view(np.uint16)[0] == np.float16(d2).view(np.uint16)
+    assert y[36:68].view(np.int8)[0] == -127  # -3.0 is the block maximum
+    z = o.quantize("q8_0", np.zeros(32, np.float32))
+    assert not z.any()
+
+
+def test_q8_k_known_answers():
+    x = np.zeros(512, np.float32)
+    x[0] = 127.0          # iscale = -1: q = rne(-x)
+    x[1:7] = [0.5, 1.5, 2.5, -0.5, -1.5, 126.5]
+    x[256 + 3] = 5.0      # first index of the largest |x| wins: +5 -> -127
+    x[256 + 7] = -5.0
+    sentinel = 0x5A
+    y = np.full(2 * 292, sentinel, np.uint8)
+    o.quantize("q8_k", x, out=y.reshape(2, 292))
+    b0, b1 = y[:292], y[292:]
+    assert b0[0:4].view(np.float32)[0] == -1.0
+    assert list(b0[4:11].view(np.int8)) == [-127, 0, -2, -2, 0, 2, -126]
+    bs = b0[260:292].view(np.int16)
+    assert bs[0] == int(b0[4:20].view(np.int8).astype(int).sum())
+    assert b1[4 + 3].astype(np.int8) == -127 and np.int8(b1[4 + 7]) == 127
+    assert b1[0:4].view(np.float32)[0] == np.float32(1.0) / (np.float32(-127.0) / np.float32(5.0))
+    # all-zero block: d = 0, qs = 0, bsums left as they were
+    z = np.full(292, sentinel, np.uint8)
+    o.quantize("q8_k", np.zeros(256, np.float32), out=z.reshape(1, 292))
+    assert not z[:260].any() and (z[260:] == sentinel).all()
+
+
+@pytest.mark.parametrize("act", ["q8_0", "q8_k"])
+def test_q8_invariants(act):
+    x = o.seeded_normal(21, (64, 1024))
+    y = o.quantize(act, x)
+    elems, nbytes = o.RECORD[act]
+    recs = y.reshape(-1, nbytes)
+    xb = x.reshape(-1, elems).astype(np.float64)
+    if act == "q8_0":
+        d = recs[:, 0:2].copy().view(np.float16).astype(np.float64)[:, 0]
+        q = recs[:, 2:].view(np.int8).astype(np.float64)
+        assert (np.abs(q).max(axis=1) == 127).all()
+        # q is rounded against the fp32 d, the record holds fp16(d): up to
+        # 127 * 2^-11 * d more
+        assert (np.abs(xb - q * d[:, None]) <= (0.5 + 127 * 2.0**-11 + 1e-3) * d[:, None]).all()
+    else:
+        d = recs[:, 0:4].copy().view(np.float32).astype(np.float64)[:, 0]
+        q = recs[:, 4:260].view(np.int8).astype(np.int64)
+        bs = recs[:, 260:292].copy().view(np.int16).astype(np.int64)
+        assert np.array_equal(bs, q.reshape(-1, 16, 16).sum(axis=2))
+        assert (np.abs(q).max(axis=1) == 127).all()
+        assert (np.abs(xb - q * d[:, None]) <= 0.5 * np.abs(d)[:, None] * (1 + 1e-5)).all()
+
+
+# ----------------------------------------------- vec_dot / mul_mat / fp64
+def _dequant_act(act, xq, k):
+    elems, nbytes = o.RECORD[act]
+    recs = xq.reshape(-1, nbytes)
+    if act == "q8_0":
+        d = recs[:, 0:2].copy().view(np.float16).astype(np.float64)
+        q = recs[:, 2:].view(np.int8).astype(np.float64)
+    else:
+        d = recs[:, 0:4].copy().view(np.float32).astype(np.float64)
+        q = recs[:, 4:260].view(np.int8).astype(np.float64)
+    return (q * d).reshape(xq.shape[0], k)
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "iq2_xxs", "mxfp4"])
+def test_mul_mat_against_independent_float64_path(fmt):
+    n, k, m = 48, 2048, 3
+    w = o.quantize(fmt, o.seeded_normal(31, (n, k), 0.02))
+    x = o.seeded_normal(32, (m, k))
+    xq, y = o.mul_mat(fmt, w, x, n, k, m)
+    e, a = o.mul_mat_f64(fmt, w, xq, n, k, m)
+    # independent: dequantize both operands (pinned above) and multiply
+    ref = _dequant_act(o.ACT_OF[fmt], xq, k) @ o.dequantize(fmt, w, k).astype(np.float64).T
+    assert np.allclose(e, ref, rtol=1e-12, atol=1e-12 * np.abs(ref).max())
+    assert o.within_tolerance(y, e, a).all()
+    # a wrong sign or a dropped min term would not be near: check the bound bites
+    assert not o.within_tolerance(y * 1.001 + 1e-3, e, a).all()
+    # vec_dot of one row pair is the same function
+    assert o.vec_dot(fmt, w[5], xq[1], k) == y[1, 5]
+
+
+def test_int_partials_q4_0_are_the_block_dots():
+    k = 512
+    w = o.quantize("q4_0", o.seeded_normal(41, (1, k), 0.02))
+    xq = o.quantize("q8_0", o.seeded_normal(42, (1, k)))
+    p = o.int_partials("q4_0", w, xq, k)
+    rec = w.reshape(-1, 18)
+    qs = rec[:, 2:]
+    codes = np.concatenate([qs & 0xF, qs >> 4], axis=1).astype(np.int64) - 8
+    xv = xq.reshape(-1, 34)[:, 2:].view(np.int8).astype(np.int64)
+    assert np.array_equal(p, (codes * xv).sum(axis=1))
+
+
+def test_int_partials_q4_k_match_dequantized_integers():
+    k = 512
+    w = o.quantize("q4_k", o.seeded_normal(43, (1, k), 0.02))
+    xq = o.quantize("q8_k", o.seeded_normal(44, (1, k)))
+    p = o.int_partials("q4_k", w, xq, k).reshape(-1, 9)
+    for b in range(k // 256):
+        rec = w[0, 144 * b:144 * (b + 1)]
+        qs = rec[16:]
+        codes = np.zeros(256, np.int64)
+        for e in range(256):
+            byte = qs[32 * (e // 64) + e % 32]
+            codes[e] = byte & 0xF if e % 64 < 32 else byte >> 4
+        xr = xq[0, 292 * b:292 * (b + 1)]
+        xv = xr[4:260].view(np.int8).astype(np.int64)
+        assert list(p[b, :8]) == [int((codes[32 * s:32 * s + 32] * xv[32 * s:32 * s + 32]).sum())
+                                  for s in range(8)]
+
+
+# ------------------------------------------------ weight quantizers (inputs)
+@pytest.mark.parametrize("fmt,bound", [("q4_0", 0.10), ("q4_k", 0.09), ("mxfp4", 0.13), ("iq2_xxs", 0.45)])
+def test_weight_quantizer_round_trip(fmt, bound):
+    w = o.seeded_normal(51, (32, 4096), 0.02)
+    d = o.dequantize(fmt, o.quantize(fmt, w), 4096)
+    rel = np.sqrt(((d - w) ** 2).mean()) / np.sqrt((w ** 2).mean())
+    assert rel < bound
+
+
+def test_q4_0_quantizer_error_is_half_a_step():
+    w = o.seeded_normal(52, (16, 1024), 0.02)
+    q = o.quantize("q4_0", w).reshape(-1, 18)
+    d = np.abs(q[:, 0:2].copy().view(np.float16).astype(np.float64)[:, 0])
+    err = np.abs(o.dequantize("q4_0", q, 32).astype(np.float64) - w.reshape(-1, 32))
+    # the block maximum maps to -8 exactly; the +7 clamp side may lose up to a full step
+    assert (err <= d[:, None] * 1.001 + 1e-7).all()

@@ -25,10 +25,25 @@ class LibraryMissing(RuntimeError):
     pass
 
 
+def _share_torch_hip_runtime() -> None:
+    """Import torch (when installed) before dlopen-ing libweft_hip.
+
+    PyTorch-ROCm ships its own libamdhip64 with the same SONAME
+    (libamdhip64.so.7) as /opt/rocm's.  Loaded after torch, libweft_hip binds
+    to torch's copy and the process has one HIP runtime; loaded first, torch
+    would bring in a second HIP/HSA runtime and device discovery fails.
+    """
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def load() -> ctypes.CDLL:
     global _lib, _artifact
     with _lock:
         if _lib is None:
+            _share_torch_hip_runtime()
             if not LIB_PATH.exists():
                 raise LibraryMissing(
                     f"{LIB_PATH} is not built; run python -m weft_amd.build (hipcc, gfx950)")
@@ -42,6 +57,9 @@ def load() -> ctypes.CDLL:
             lib.weft_hip_get_stream.restype = ctypes.c_void_p
             lib.weft_hip_get_last_error.restype = ctypes.c_int
             lib.weft_hip_synchronize.restype = ctypes.c_int
+            lib.weft_hip_device_count.restype = ctypes.c_int
+            lib.weft_hip_device_arch.argtypes = [ctypes.c_int, ctypes.c_char_p, ctypes.c_size_t]
+            lib.weft_hip_device_arch.restype = ctypes.c_int
             artifact = json.loads(lib.weft_hip_artifact())
             for kernel in artifact["kernels"]:
                 fn = getattr(lib, kernel["symbol"])

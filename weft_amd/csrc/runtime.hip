@@ -86,6 +86,24 @@ int weft_hip_synchronize(void) {
 
 const char* weft_hip_version(void) { return WEFT_HIP_VERSION_STRING; }
 
+int weft_hip_device_count(void) {
+  int n = 0;
+  const hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) return -(int)e;
+  return n;
+}
+
+int weft_hip_device_arch(int dev, char* buf, size_t len) {
+  if (buf == nullptr || len == 0) return (int)hipErrorInvalidValue;
+  hipDeviceProp_t prop;
+  const hipError_t e = hipGetDeviceProperties(&prop, dev);
+  if (e != hipSuccess) return (int)e;
+  size_t i = 0;
+  for (; i + 1 < len && prop.gcnArchName[i] != 0; ++i) buf[i] = prop.gcnArchName[i];
+  buf[i] = 0;
+  return 0;
+}
+
 }  // extern "C"
 
 // ------------------------------------------------------------ ABI metadata
