@@ -47,7 +47,26 @@ def parse():
                    help="wall-clock budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-prefill", action="store_true")
+    p.add_argument("--no-wdown", action="store_true")
+    p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                   help="also run one plain device-to-device copy of MIB MiB, the known-size "
+                        "kernel that HBM byte counters are scaled against")
     return p.parse_args()
+
+
+def profiled_traffic(name: str):
+    """HBM bytes per launch measured by the FETCH_SIZE / WRITE_SIZE counter
+    runs recorded in profiles/<name>.md (scaled against a known-size copy),
+    or None when no such profile is committed."""
+    path = os.path.join(ROOT, "profiles", name + ".md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def algorithmic_bytes(n, k, m, w_bytes):
@@ -160,7 +179,16 @@ def main():
 
     sec, nbytes, copies = decode_case(b, 11008, 4096, steps, warmup)
     gbs = nbytes / sec / 1e9
-    sec_dn, nbytes_dn, _ = decode_case(b, 4096, 11008, steps, warmup)
+    sec_dn = nbytes_dn = None
+    if not args.no_wdown:
+        sec_dn, nbytes_dn, _ = decode_case(b, 4096, 11008, steps, warmup)
+    if args.calibrate_copy:
+        n = args.calibrate_copy << 20
+        src = b.torch.empty(n, dtype=b.torch.uint8, device=b.dev)
+        dst = b.torch.empty_like(src)
+        b.torch.cuda.synchronize()
+        dst.copy_(src)
+        b.torch.cuda.synchronize()
     prefill = {}
     if not args.no_prefill:
         for n in (4096, 11008):
@@ -188,10 +216,13 @@ def main():
                                "M=1, Q8_K activation quantize inside the timed call",
                    "N": 11008, "K": 4096, "M": 1, "weight_copies_rotated": copies},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": profiled_traffic("q4k_decode_w_up"),
+                     "algorithmic_bytes": nbytes},
         "cpu_baseline": cpu,
-        "w_down": {"N": 4096, "K": 11008, "us": round(sec_dn * 1e6, 3),
-                   "GBs": round(nbytes_dn / sec_dn / 1e9, 2)},
+        "w_down": None if sec_dn is None else {
+            "N": 4096, "K": 11008, "us": round(sec_dn * 1e6, 3),
+            "GBs": round(nbytes_dn / sec_dn / 1e9, 2)},
         "prefill_q4_k_M512_K4096": prefill,
     }
     print(json.dumps(line))
