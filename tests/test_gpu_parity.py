@@ -220,6 +220,13 @@ def test_prefill_entry_points(hip, fmt):
     check_mul_mat(fmt, w, x, xq, y, n, k, m)
 
 
+@pytest.mark.parametrize("n,k,m", [(300, 512, 37), (129, 768, 16), (128, 256, 65)])
+def test_prefill_q4_k_ragged_tiles(hip, n, k, m):
+    # shapes that leave partial 64 x 128 MFMA tiles on both axes
+    w, x, xq, y = run_mul_mat(hip, "production_mul_mat_q4_k_staged", "q4_k", n, k, m)
+    check_mul_mat("q4_k", w, x, xq, y, n, k, m)
+
+
 def test_prefill_q4_k_config4_n4096(hip):
     """BASELINE config 4 (N=4096): 512 tokens x 4096, full check."""
     n = k = 4096

@@ -2,9 +2,9 @@
 //
 // production_mul_mat_{q4_0,q4_k,q4_k_staged,iq2_xxs,iq2_xxs_staged,mxfp4}
 // (examples/kernels/mul_mat/*.py) compute the same Y = X . W^T as the decode
-// kernels; the reference's variants differ only in CPU loop order.  These
-// entry points currently run the decode GEMV kernels, which re-stream W once
-// per four activation rows.
+// kernels; the reference's variants differ only in CPU loop order.  Q4_K
+// runs the int8-MFMA GEMM (prefill_q4k.hip); the other formats currently run
+// the decode GEMV kernels, which re-stream W once per four activation rows.
 #include "kernels.h"
 #include "runtime.h"
 #include "weft_hip.h"
@@ -18,12 +18,12 @@ void production_mul_mat_q4_0(const uint8_t* W, const float* X, uint8_t* Xq, floa
 
 void production_mul_mat_q4_k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N,
                              size_t K, size_t M) {
-  weft::decode_q4k(W, X, Xq, Y, N, K, M);
+  weft::mul_mat_q4k(W, X, Xq, Y, N, K, M);
 }
 
 void production_mul_mat_q4_k_staged(const uint8_t* W, const float* X, uint8_t* Xq, float* Y,
                                     size_t N, size_t K, size_t M) {
-  weft::decode_q4k(W, X, Xq, Y, N, K, M);
+  weft::mul_mat_q4k(W, X, Xq, Y, N, K, M);
 }
 
 void production_mul_mat_iq2_xxs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,
