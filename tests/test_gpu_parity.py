@@ -220,11 +220,26 @@ def test_prefill_entry_points(hip, fmt):
     check_mul_mat(fmt, w, x, xq, y, n, k, m)
 
 
+@pytest.mark.parametrize("fmt", ["q4_k", "q4_0", "mxfp4"])
 @pytest.mark.parametrize("n,k,m", [(300, 512, 37), (129, 768, 16), (128, 256, 65)])
-def test_prefill_q4_k_ragged_tiles(hip, n, k, m):
-    # shapes that leave partial 64 x 128 MFMA tiles on both axes
-    w, x, xq, y = run_mul_mat(hip, "production_mul_mat_q4_k_staged", "q4_k", n, k, m)
-    check_mul_mat("q4_k", w, x, xq, y, n, k, m)
+def test_prefill_ragged_tiles(hip, fmt, n, k, m):
+    # shapes that leave partial 64 x 128 MFMA tiles on both axes, and an odd
+    # number of 256-value stages (K = 768) for the stage-parity waves
+    w, x, xq, y = run_mul_mat(hip, MM_PREFILL[fmt], fmt, n, k, m)
+    check_mul_mat(fmt, w, x, xq, y, n, k, m)
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "mxfp4"])
+def test_prefill_misaligned_weights_fall_back(hip, fmt):
+    # W at a 2-byte offset is valid for these records but not for the MFMA
+    # path's 4-byte direct loads: the call must take the GEMV path and agree
+    n, k, m = 96, 512, 20
+    w, x = weights(fmt, n, k), acts(m, k)
+    act = o.ACT_OF[fmt]
+    xq = hip.empty(o.record_bytes(act, k) * m, fill=SENTINEL)
+    y = hip.empty(4 * m * n, fill=SENTINEL)
+    hip.call(MM_PREFILL[fmt], hip.to_dev(w, offset=2), hip.to_dev(x), xq, *tables(hip, fmt), y, n, k, m)
+    check_mul_mat(fmt, w, x, xq.numpy(np.uint8).reshape(m, -1), y.numpy(np.float32).reshape(m, n), n, k, m)
 
 
 def test_prefill_q4_k_config4_n4096(hip):
@@ -241,6 +256,17 @@ def test_prefill_q4_k_config4_n11008_sampled(hip):
     w, x, xq, y = run_mul_mat(hip, "production_mul_mat_q4_k_staged", "q4_k", n, k, m)
     cols = np.sort(np.random.default_rng(5).choice(n, 256, replace=False))
     check_mul_mat("q4_k", w, x, xq, y, n, k, m, cols=cols)
+
+
+@pytest.mark.parametrize("fmt", ["mxfp4", "q4_0"])
+def test_prefill_config5b_sampled(hip, fmt):
+    """BASELINE config 5b (MXFP4, 512 x 4096 x 4096; Q4_0 at the same shape):
+    Xq in full, Y on 256 seeded columns."""
+    n = k = 4096
+    m = 512
+    w, x, xq, y = run_mul_mat(hip, MM_PREFILL[fmt], fmt, n, k, m)
+    cols = np.sort(np.random.default_rng(6).choice(n, 256, replace=False))
+    check_mul_mat(fmt, w, x, xq, y, n, k, m, cols=cols)
 
 
 # ------------------------------------------------------------ error paths

@@ -13,7 +13,7 @@ extern "C" {
 
 void production_mul_mat_q4_0(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N,
                              size_t K, size_t M) {
-  weft::decode_q4_0(W, X, Xq, Y, N, K, M);
+  weft::mul_mat_q4_0(W, X, Xq, Y, N, K, M);
 }
 
 void production_mul_mat_q4_k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N,
@@ -39,7 +39,7 @@ void production_mul_mat_iq2_xxs_staged(const uint8_t* W, const float* X, uint8_t
 
 void production_mul_mat_mxfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
                               const float* scale, float* Y, size_t N, size_t K, size_t M) {
-  weft::decode_mxfp4(W, X, Xq, codebook, scale, Y, N, K, M);
+  weft::mul_mat_mxfp4(W, X, Xq, codebook, scale, Y, N, K, M);
 }
 
 }  // extern "C"

@@ -40,7 +40,6 @@
 #include <algorithm>
 
 #include "kernels.h"
-#pragma clang diagnostic ignored "-Winline-asm"
 #include "runtime.h"
 #include "weft_common.h"
 #include "weft_hip.h"

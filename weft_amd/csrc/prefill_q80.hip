@@ -1,0 +1,380 @@
+// Q4_0 / MXFP4 x Q8_0 prefill GEMM on int8 MFMA (production_mul_mat_q4_0,
+// examples/kernels/mul_mat/q4_0.py:9-30; production_mul_mat_mxfp4,
+// examples/kernels/mul_mat/mxfp4.py:10-35).
+//
+//   Y[m, n] = sum_b dx[m,b] * ws[n,b] * I[m,n,b],   I = sum_{k in b} q8[m,k] * w[n,k]
+//   Q4_0:  w = q - 8,            ws = fp16 d        (ggml-cpu/quants.c:174-208)
+//   MXFP4: w = codebook[q],      ws = scale[e]      (ggml-cpu/quants.c:247-276)
+// One v_mfma_i32_32x32x32_i8 per 32x32 tile and 32-block gives I exactly; the
+// two per-block scales are applied in fp32 on VALU (3 instructions per
+// output and block), which is what bounds these kernels.
+//
+// Activation layout.  A Q8_0 record is 34 bytes at 2-byte alignment, which
+// cannot feed 16-byte operand reads.  The activation is therefore quantized
+// first into Xq in a planar layout of the same size -- row m holds its K int8
+// values followed by its K/32 fp16 scales (row stride 17K/16) -- and, after
+// the GEMM, quantized again in GGML's record layout, so Xq ends exactly as
+// q8_0_quantize writes it.  Quantization is deterministic, so both passes
+// produce the same int8 values and scales.
+//
+// Tiling as in the Q4_K prefill: 64 tokens x 128 weight rows per workgroup,
+// 8 waves (superblock parity x 4 column groups), each wave two 32x32 tiles.
+// A stage is 8 blocks (256 K values).  The activation int8 tile (swizzled
+// 16-byte chunks) and the raw weight rows (8 records per row) are copied to
+// LDS by direct loads a stage ahead; weight operands are unpacked from the
+// raw records with aligned dword reads and byte alignment.  The per-block
+// token scales are loaded by one wave per parity and transposed to fp32
+// [block][token] so the combine reads four tokens with one instruction.
+#include <algorithm>
+
+#include "kernels.h"
+#include "runtime.h"
+#include "weft_common.h"
+#include "weft_hip.h"
+
+namespace weft {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+enum class WFmt { Q4_0, MXFP4 };
+
+template <WFmt F>
+struct WTraits;
+template <>
+struct WTraits<WFmt::Q4_0> {
+  static constexpr int kRec = kQ4_0Bytes;  // 18
+  static constexpr int kHdr = 2;           // fp16 d, then 16 nibble bytes
+};
+template <>
+struct WTraits<WFmt::MXFP4> {
+  static constexpr int kRec = kMxfp4Bytes;  // 17
+  static constexpr int kHdr = 1;            // e8m0 e, then 16 nibble bytes
+};
+
+constexpr int kMT = 64;        // tokens per workgroup tile
+constexpr int kNT = 128;       // weight rows per workgroup tile
+constexpr int kThreads = 512;  // 8 waves: 4 column groups x 2 stage parities
+constexpr int kAQ = kMT * 256;  // activation int8 per stage
+
+struct GemmArgs {
+  const uint8_t* W;
+  const uint8_t* Xp;  // planar activation (rows of K int8 + K/32 fp16)
+  const int8_t* codebook;
+  const float* scale;
+  float* Y;
+  int N, K, M;
+};
+
+// 16 bytes per lane from global straight into LDS: lane l writes
+// [lds + 16 l, +16).  Inline asm keeps the compiler from making unrelated LDS
+// reads wait for it; the kernel waits (s_waitcnt) itself.  Nothing else in
+// this file's kernels uses M0.
+__device__ __forceinline__ void lds_dma16(const uint8_t* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds), "v"(g)
+               : "memory", "m0");
+}
+// 4 bytes per lane: lane l writes [lds + 4 l, +4)
+__device__ __forceinline__ void lds_dma4(const uint8_t* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
+               :
+               : "s"(lds), "v"(g)
+               : "memory", "m0");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_ptr)p;
+}
+__device__ __forceinline__ uint32_t ld32(const uint8_t* p) {
+  return *reinterpret_cast<const uint32_t*>(p);
+}
+
+// four nibbles (one per byte) -> the 16-entry int8 codebook c0..c3
+__device__ __forceinline__ uint32_t lookup16(uint32_t n, uint32_t c0, uint32_t c1, uint32_t c2,
+                                             uint32_t c3) {
+  const uint32_t sel = n & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(c1, c0, sel);
+  const uint32_t hi = __builtin_amdgcn_perm(c3, c2, sel);
+  const uint32_t mask = ((n >> 3) & 0x01010101u) * 0xffu;
+  return (hi & mask) | (lo & ~mask);
+}
+
+template <WFmt F>
+__global__ void __launch_bounds__(kThreads, 1) q80_mfma_gemm(GemmArgs a) {
+  using T = WTraits<F>;
+  constexpr int kRB = 8 * T::kRec;           // raw weight bytes per row and stage
+  constexpr int kWT = kNT * kRB;             // 18432 (Q4_0) / 17408 (MXFP4)
+  constexpr int kStage = kAQ + kWT;
+  constexpr int kWD = kRB / 4;               // dwords per weight row and stage
+  constexpr int kWSlots = kNT * kWD / 64;    // 72 / 68 wave-wide dword loads
+  constexpr int kWPerWave = kWSlots / 4;     // 18 / 17
+  static_assert(kNT * kWD % 256 == 0, "weight slots split evenly over four waves");
+  static_assert(4 * 32 * 64 * 4 <= 2 * kStage, "reduction buffer fits one ring slot");
+
+  __shared__ __align__(16) uint8_t ring0[2 * kStage];
+  __shared__ __align__(16) uint8_t ring1[2 * kStage];
+  __shared__ __align__(16) float adt[2][2][8 * kMT];  // [slot][parity][block][token]
+  __shared__ float scl[F == WFmt::MXFP4 ? 256 : 1];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+  const int par = wave >> 2, wcol = wave & 3;
+  const int col = lane & 31, kg = lane >> 5;
+  const int nst = a.K >> 8;                         // stages (8 blocks each)
+  const size_t xs = (size_t)a.K + (size_t)a.K / 16;  // planar activation row stride
+  const size_t ws_row = (size_t)(a.K / 32) * T::kRec;
+
+  // XCD-aware tile order (workgroups are dealt round-robin to 8 XCDs)
+  int m0, n0;
+  {
+    const int ntm = (a.M + kMT - 1) / kMT;
+    const int Tn = ntm * ((a.N + kNT - 1) / kNT);
+    const int L = blockIdx.x, x = L & 7, j = L >> 3;
+    const int t = x * (Tn >> 3) + min(x, Tn & 7) + j;
+    m0 = (t % ntm) * kMT;
+    n0 = (t / ntm) * kNT;
+  }
+
+  uint32_t c0 = 0, c1 = 0, c2 = 0, c3 = 0;
+  if constexpr (F == WFmt::MXFP4) {
+    // int8[16] codebook at any alignment: four little-endian words
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = (uint32_t)(uint8_t)a.codebook[4 * i] | (uint32_t)(uint8_t)a.codebook[4 * i + 1] << 8 |
+             (uint32_t)(uint8_t)a.codebook[4 * i + 2] << 16 |
+             (uint32_t)(uint8_t)a.codebook[4 * i + 3] << 24;
+    c0 = w[0], c1 = w[1], c2 = w[2], c3 = w[3];
+    if (tid < 256) scl[tid] = a.scale[tid];
+  }
+
+  // activation int8 tile: 16 wave-wide 16-byte loads per stage, 4 per wave
+  const uint8_t* asrc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int k = wcol + 4 * i;
+    const int q = 64 * k + lane, r = q >> 4, c = (q & 15) ^ (r & 15);
+    asrc[i] = a.Xp + (size_t)min(m0 + r, a.M - 1) * xs + 16 * c;
+  }
+  // per-block token scales of this parity's stage: wave wcol == 0, token = lane
+  const uint8_t* dsrc = a.Xp + (size_t)min(m0 + lane, a.M - 1) * xs + a.K;
+
+  auto issue = [&](int pair, uint8_t* ring) {
+    const int st = min(2 * pair + par, nst - 1);
+    uint8_t* stage = ring + par * kStage;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      lds_dma16(asrc[i] + 256 * (size_t)st,
+                __builtin_amdgcn_readfirstlane(lds_addr(stage + 1024 * (wcol + 4 * i))));
+#pragma unroll
+    for (int i = 0; i < kWPerWave; ++i) {
+      const int k = wcol + 4 * i;
+      const int q = 64 * k + lane, row = q / kWD, part = q - kWD * row;
+      const uint8_t* g = a.W + (size_t)min(n0 + row, a.N - 1) * ws_row + (size_t)st * kRB + 4 * part;
+      lds_dma4(g, __builtin_amdgcn_readfirstlane(lds_addr(stage + kAQ + 256 * k)));
+    }
+  };
+  uint4 dxraw = make_uint4(0, 0, 0, 0);
+  auto load_dx = [&](int pair) {
+    const int st = min(2 * pair + par, nst - 1);
+    dxraw = *reinterpret_cast<const uint4*>(dsrc + 16 * (size_t)st);
+  };
+  auto store_dx = [&](int slot) {
+    float* d = &adt[slot][par][0];
+    const uint32_t w[4] = {dxraw.x, dxraw.y, dxraw.z, dxraw.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) d[j * kMT + lane] = fp16_to_fp32((w[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+  };
+
+  v16i I[2];
+  v16f y[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) y[t][r] = 0.f;
+  const v16i zero = {};
+  const int npair = (nst + 1) >> 1;
+  const int sw = col & 15;
+
+  auto step = [&](int pair, const uint8_t* cur, uint8_t* nxt) {
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of this pair have landed
+    __syncthreads();                // everyone's; the previous pair is consumed
+    const bool refill = pair + 1 < npair;
+    if (refill) {
+      issue(pair + 1, nxt);
+      if (wcol == 0) load_dx(pair + 1);
+    }
+    if (2 * pair + par < nst) {
+      const uint8_t* stage = cur + par * kStage;
+      const uint8_t* AQ = stage;
+      const uint8_t* wrow = stage + kAQ + (32 * wcol + col) * kRB;
+      const float* dxs = &adt[pair & 1][par][0];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        // raw record j of this lane's weight row: header, then 16 nibble bytes
+        const int off = T::kRec * j + T::kHdr;  // first nibble byte
+        const int sh = off & 3, b4 = off - sh;
+        uint32_t w0 = ld32(wrow + b4), w1 = ld32(wrow + b4 + 4), w2 = ld32(wrow + b4 + 8),
+                 w3 = ld32(wrow + b4 + 12);
+        uint32_t q0 = w0, q1 = w1, q2 = w2, q3 = w3;
+        if (sh) {
+          const uint32_t w4 = ld32(wrow + b4 + 16);
+          q0 = __builtin_amdgcn_alignbyte(w1, w0, sh);
+          q1 = __builtin_amdgcn_alignbyte(w2, w1, sh);
+          q2 = __builtin_amdgcn_alignbyte(w3, w2, sh);
+          q3 = __builtin_amdgcn_alignbyte(w4, w3, sh);
+        }
+        // header byte(s) just before the nibbles
+        float wsc;
+        if constexpr (F == WFmt::Q4_0) {
+          const uint32_t dbits = sh >= 2 ? (w0 & 0xffffu) : (ld32(wrow + b4 - 4) >> 16);
+          wsc = fp16_to_fp32(dbits);
+        } else {
+          const uint32_t e = sh >= 1 ? ((w0 >> (8 * (sh - 1))) & 0xffu) : (ld32(wrow + b4 - 4) >> 24);
+          wsc = scl[e];
+        }
+        const uint32_t shn = 4 * kg;  // kg 0: elements 0..15 (low nibbles), 1: 16..31 (high)
+        uint32_t n[4] = {(q0 >> shn) & 0x0f0f0f0fu, (q1 >> shn) & 0x0f0f0f0fu,
+                         (q2 >> shn) & 0x0f0f0f0fu, (q3 >> shn) & 0x0f0f0f0fu};
+        v4i bv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if constexpr (F == WFmt::Q4_0)
+            bv[i] = (int)(((n[i] | 0x80808080u) - 0x08080808u) ^ 0x80808080u);  // q - 8 per byte
+          else
+            bv[i] = (int)lookup16(n[i], c0, c1, c2, c3);
+        }
+        const int chunk = (2 * j + kg) ^ sw;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const v4i av = *reinterpret_cast<const v4i*>(AQ + (32 * t + col) * 256 + 16 * chunk);
+          I[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, zero, 0, 0, 0);
+        }
+        // y += (dx * ws) * I; register r of a tile holds token 8*(r/4) + 4*kg + r%4
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const float4 d4 = *reinterpret_cast<const float4*>(dxs + j * kMT + 32 * t + 8 * r4 + 4 * kg);
+            const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int r = 4 * r4 + q;
+              y[t][r] += (dv[q] * wsc) * (float)I[t][r];
+            }
+          }
+      }
+    }
+    if (refill && wcol == 0) store_dx((pair + 1) & 1);  // slot last read a pair ago
+  };
+
+  issue(0, ring0);
+  if (wcol == 0) {
+    load_dx(0);
+    store_dx(0);
+  }
+  for (int pair = 0; pair < npair; pair += 2) {
+    step(pair, ring0, ring1);
+    if (pair + 1 < npair) step(pair + 1, ring1, ring0);
+  }
+
+  // odd-parity partial sums -> LDS -> even waves, one ordered add per output
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(ring0) + wcol * (32 * 64) + lane;
+  if (par == 1) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[(16 * t + r) * 64] = y[t][r];
+  }
+  __syncthreads();
+  if (par == 1) return;
+  const int gn = n0 + 32 * wcol + col;
+  if (gn < a.N) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int gm = m0 + 32 * t + 8 * (r >> 2) + 4 * kg + (r & 3);
+        if (gm < a.M) a.Y[(size_t)gm * a.N + gn] = y[t][r] + red[(16 * t + r) * 64];
+      }
+  }
+}
+
+__device__ __forceinline__ float4 ldx4(const float* p, bool a16) {
+  if (a16) return *reinterpret_cast<const float4*>(p);
+  return make_float4(p[0], p[1], p[2], p[3]);
+}
+
+// Q8_0 quantization of X (M x K) into the planar layout: row m at m * 17K/16,
+// K int8 values then K/32 fp16 scales.  Same arithmetic as q8_0_quantize
+// (ggml-quants.c:238-261), so the values equal the record layout's.
+__global__ void __launch_bounds__(256) q80_planar_kernel(const float* __restrict__ X,
+                                                         uint8_t* __restrict__ Xp, long long nb,
+                                                         int bpr, long long xs) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const long long wave = ((long long)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const long long nwaves = (long long)gridDim.x * blockDim.x / kWave;
+  const long long steps = (nb + 7) / 8;
+  const bool a16 = (reinterpret_cast<uintptr_t>(X) & 15) == 0;
+  for (long long s = wave; s < steps; s += nwaves) {
+    const long long b = 8 * s + lane / 8;
+    const bool live = b < nb;
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live) x = ldx4(X + b * 32 + 4 * (lane & 7), a16);
+    const Q8_0Lane r = q80_quantize_8lanes(x);
+    if (!live) continue;
+    const long long row = b / bpr, blk = b - row * bpr;
+    uint8_t* rp = Xp + row * xs;
+    *reinterpret_cast<uint32_t*>(rp + 32 * blk + 4 * (lane & 7)) = (uint32_t)pack4_i8(r.q);
+    if ((lane & 7) == 0) *reinterpret_cast<uint16_t*>(rp + (long long)bpr * 32 + 2 * blk) = (uint16_t)r.dh;
+  }
+}
+
+template <WFmt F>
+bool prefill_q80(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
+                 const float* scale, float* Y, size_t N, size_t K, size_t M) {
+  // MFMA path preconditions; otherwise the caller runs the GEMV kernels
+  if (M < 16 || K % 256 || !aligned(W, 4) || !aligned(Xq, 16) || !aligned(Y, 4) ||
+      !aligned(X, 4) || N > (size_t)INT32_MAX || K > (size_t)INT32_MAX || M > (size_t)INT32_MAX ||
+      ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT) > (size_t)INT32_MAX)
+    return false;
+  if (F == WFmt::MXFP4 && (codebook == nullptr || scale == nullptr)) return false;
+  const long long nb = (long long)(M * K / 32);
+  const long long xs = (long long)(K + K / 16);
+  const long long waves = (nb + 7) / 8;
+  const int grid = (int)std::max<long long>(1, std::min<long long>((long long)cu_count() * 8, (waves + 3) / 4));
+  q80_planar_kernel<<<grid, 256, 0, current_stream()>>>(X, Xq, nb, (int)(K / 32), xs);
+  check_launch();
+  GemmArgs ga{W, Xq, codebook, scale, Y, (int)N, (int)K, (int)M};
+  const size_t tiles = ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT);
+  q80_mfma_gemm<F><<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(ga);
+  check_launch();
+  quantize_q8_0(X, Xq, M * K);  // Xq ends in GGML's record layout
+  return true;
+}
+
+}  // namespace
+
+void mul_mat_q4_0(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
+                  size_t M) {
+  if (N == 0 || M == 0 || K == 0) return decode_q4_0(W, X, Xq, Y, N, K, M);
+  if (W == nullptr || X == nullptr || Xq == nullptr || Y == nullptr ||
+      !prefill_q80<WFmt::Q4_0>(W, X, Xq, nullptr, nullptr, Y, N, K, M))
+    decode_q4_0(W, X, Xq, Y, N, K, M);
+}
+
+void mul_mat_mxfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
+                   const float* scale, float* Y, size_t N, size_t K, size_t M) {
+  if (N == 0 || M == 0 || K == 0) return decode_mxfp4(W, X, Xq, codebook, scale, Y, N, K, M);
+  if (W == nullptr || X == nullptr || Xq == nullptr || Y == nullptr ||
+      !prefill_q80<WFmt::MXFP4>(W, X, Xq, codebook, scale, Y, N, K, M))
+    decode_mxfp4(W, X, Xq, codebook, scale, Y, N, K, M);
+}
+
+}  // namespace weft
