@@ -220,16 +220,18 @@ def test_prefill_entry_points(hip, fmt):
     check_mul_mat(fmt, w, x, xq, y, n, k, m)
 
 
-@pytest.mark.parametrize("fmt", ["q4_k", "q4_0", "mxfp4"])
-@pytest.mark.parametrize("n,k,m", [(300, 512, 37), (129, 768, 16), (128, 256, 65)])
+@pytest.mark.parametrize("fmt", ["q4_k", "q4_0", "mxfp4", "iq2_xxs"])
+@pytest.mark.parametrize("n,k,m", [(300, 512, 37), (129, 768, 16), (128, 256, 65), (200, 1536, 70)])
 def test_prefill_ragged_tiles(hip, fmt, n, k, m):
-    # shapes that leave partial 64 x 128 MFMA tiles on both axes, and an odd
-    # number of 256-value stages (K = 768) for the stage-parity waves
+    # shapes that leave partial 64 x 128 MFMA tiles on both axes, an odd
+    # number of 256-value stages (K = 768) for the stage-parity waves, and an
+    # odd number of stage pairs (K = 1536) for the two LDS ring slots; IQ2_XXS
+    # at K = 768 / 256 takes the GEMV path (its GEMM stages superblock pairs)
     w, x, xq, y = run_mul_mat(hip, MM_PREFILL[fmt], fmt, n, k, m)
     check_mul_mat(fmt, w, x, xq, y, n, k, m)
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "mxfp4"])
+@pytest.mark.parametrize("fmt", ["q4_0", "mxfp4", "iq2_xxs"])
 def test_prefill_misaligned_weights_fall_back(hip, fmt):
     # W at a 2-byte offset is valid for these records but not for the MFMA
     # path's 4-byte direct loads: the call must take the GEMV path and agree
@@ -258,10 +260,10 @@ def test_prefill_q4_k_config4_n11008_sampled(hip):
     check_mul_mat("q4_k", w, x, xq, y, n, k, m, cols=cols)
 
 
-@pytest.mark.parametrize("fmt", ["mxfp4", "q4_0"])
+@pytest.mark.parametrize("fmt", ["mxfp4", "q4_0", "iq2_xxs"])
 def test_prefill_config5b_sampled(hip, fmt):
-    """BASELINE config 5b (MXFP4, 512 x 4096 x 4096; Q4_0 at the same shape):
-    Xq in full, Y on 256 seeded columns."""
+    """BASELINE config 5b (MXFP4, 512 x 4096 x 4096; Q4_0 and IQ2_XXS at the
+    same shape): Xq in full, Y on 256 seeded columns."""
     n = k = 4096
     m = 512
     w, x, xq, y = run_mul_mat(hip, MM_PREFILL[fmt], fmt, n, k, m)

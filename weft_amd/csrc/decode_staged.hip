@@ -194,8 +194,12 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
       const int off0 = stage_bytes(win, wr + (size_t)r0 * T::kBytes,
                                    wr + (size_t)(r0 + nr) * T::kBytes, wlo, whi, lane);
       const int items = nr * T::kItemsPerRecord;
-      for (int it = lane; it < items; it += kWave) {
+      // wave-uniform trip count: the IQ2_XXS branch reduces across lanes
+      for (int it0 = 0; it0 < items; it0 += kWave) {
+        const int it = it0 + lane;
+        const bool valid = it < items;
         if constexpr (F == Fmt::Q4_0 || F == Fmt::MXFP4) {
+          if (!valid) continue;
           const int b = it;             // block within segment
           const int gb = r0 + b;        // block within row
           const int o = off0 + T::kBytes * b;
@@ -233,8 +237,8 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
             s = dot4(hi3, xh.w, s);
             acc[m] += (float)s * wscale * v.d[gb];
           }
-        } else {  // IQ2_XXS: item = (superblock, 32-group)
-          const int sb = it >> 3, g = it & 7;
+        } else {  // IQ2_XXS: item = (superblock, 32-group); 8 lanes per superblock
+          const int sb = valid ? it >> 3 : 0, g = it & 7;
           const int gsb = r0 + sb;
           const int o = off0 + T::kBytes * sb;
           const float dw = fp16_to_fp32(lds_u32(win, o) & 0xffffu);
@@ -265,7 +269,10 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
             s = dot4(wv[5], x1.y, s);
             s = dot4(wv[6], x1.z, s);
             s = dot4(wv[7], x1.w, s);
-            acc[m] += (dw * v.d[gsb]) * (float)(s * ls);
+            // the superblock's integer sum over its 8 groups (8 aligned lanes),
+            // then one fp32 term, as ggml_vec_dot_iq2_xxs_q8_K_generic
+            const int bsum = sum8_of_sum4(sum4(valid ? s * ls : 0));
+            if (valid && g == 0) acc[m] += (dw * v.d[gsb]) * (float)bsum;
           }
         }
       }

@@ -26,6 +26,10 @@ void mul_mat_q4_0(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_
 void mul_mat_mxfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
                    const float* scale, float* Y, size_t N, size_t K, size_t M);
 
+// IQ2_XXS mul_mat for any M: int8-MFMA GEMM for prefill shapes, GEMV otherwise.
+void mul_mat_iq2_xxs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,
+                     const int8_t* signs, float* Y, size_t N, size_t K, size_t M);
+
 // Activation quantizers over K contiguous values.
 void quantize_q8_k(const float* X, uint8_t* Y, size_t K);
 void quantize_q8_0(const float* X, uint8_t* Y, size_t K);

@@ -2,9 +2,10 @@
 //
 // production_mul_mat_{q4_0,q4_k,q4_k_staged,iq2_xxs,iq2_xxs_staged,mxfp4}
 // (examples/kernels/mul_mat/*.py) compute the same Y = X . W^T as the decode
-// kernels; the reference's variants differ only in CPU loop order.  Q4_K
-// runs the int8-MFMA GEMM (prefill_q4k.hip); the other formats currently run
-// the decode GEMV kernels, which re-stream W once per four activation rows.
+// kernels; the reference's variants differ only in CPU loop order.  All four
+// formats run int8-MFMA GEMMs for prefill shapes (prefill_q4k.hip,
+// prefill_q80.hip, prefill_iq2.hip) and the decode GEMV kernels otherwise
+// (small M, unaligned weights, K that does not fill the GEMM's staging unit).
 #include "kernels.h"
 #include "runtime.h"
 #include "weft_hip.h"
@@ -28,13 +29,13 @@ void production_mul_mat_q4_k_staged(const uint8_t* W, const float* X, uint8_t* X
 
 void production_mul_mat_iq2_xxs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,
                                 const int8_t* signs, float* Y, size_t N, size_t K, size_t M) {
-  weft::decode_iq2_xxs(W, X, Xq, grid, signs, Y, N, K, M);
+  weft::mul_mat_iq2_xxs(W, X, Xq, grid, signs, Y, N, K, M);
 }
 
 void production_mul_mat_iq2_xxs_staged(const uint8_t* W, const float* X, uint8_t* Xq,
                                        const int8_t* grid, const int8_t* signs, float* Y, size_t N,
                                        size_t K, size_t M) {
-  weft::decode_iq2_xxs(W, X, Xq, grid, signs, Y, N, K, M);
+  weft::mul_mat_iq2_xxs(W, X, Xq, grid, signs, Y, N, K, M);
 }
 
 void production_mul_mat_mxfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,

@@ -1,0 +1,277 @@
+// IQ2_XXS x Q8_K prefill GEMM on int8 MFMA (production_mul_mat_iq2_xxs,
+// production_mul_mat_iq2_xxs_staged; examples/kernels/mul_mat/iq2_xxs_staged.py:9-97).
+//
+//   Y[m, n] = 1/8 * sum_b dw[n,b] * dx[m,b] * sum_g ls[n,b,g] * I[m,n,b,g]
+//   I = sum_{k in group g} q8[m,k] * grid[idx][j] * sign      (exact int32)
+//   ls = 2 s + 1 (4-bit s)              (ggml-cpu/quants.c:855-895)
+// One v_mfma_i32_32x32x32_i8 per 32x32 tile and 32-group gives I (weight
+// operand bytes are +-{8, 25, 43}); the small integer group scale folds in
+// with one v_mad_i32_i24 per output, exact in int32 (|I| < 2^18, ls <= 31,
+// eight groups < 2^26), and the fp32 combine runs once per superblock on the
+// same integer GGML converts.
+//
+// Tiling as in the Q4_K prefill: 64 tokens x 128 weight rows per workgroup,
+// 8 waves (superblock parity x 4 column groups), each wave two 32x32 tiles.
+// A 66-byte record is only 2-byte aligned, so the weight rows of a superblock
+// PAIR (132 bytes, 4-byte aligned when K/256 is even) are staged together;
+// each parity reads its half with aligned dword reads and byte alignment.
+// Grid and sign tables live in LDS.
+#include <algorithm>
+
+#include "kernels.h"
+#include "runtime.h"
+#include "weft_common.h"
+#include "weft_hip.h"
+
+namespace weft {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+constexpr int kMT = 64;        // tokens per workgroup tile
+constexpr int kNT = 128;       // weight rows per workgroup tile
+constexpr int kThreads = 512;  // 8 waves: 4 column groups x 2 superblock parities
+constexpr int kAQ = kMT * 256;                    // activation int8 of one superblock
+constexpr int kPairB = 2 * kIq2xxsBytes;          // 132 weight bytes per row and pair
+constexpr int kWT = kNT * kPairB;                 // 16896
+constexpr int kSlot = 2 * kAQ + kWT;              // one ring slot: both parities + weights
+constexpr int kSlotAlloc = kSlot + 16;            // slack: a group read may run 4 bytes past row 127
+constexpr int kWD = kPairB / 4;                   // 33 dwords per row and pair
+constexpr int kWSlots = kNT * kWD / 64;           // 66 wave-wide dword loads per pair
+static_assert(kNT * kWD % 64 == 0, "weight pair tile is whole wave loads");
+static_assert(4 * 32 * 64 * 4 <= kSlot, "reduction buffer fits one ring slot");
+
+struct GemmArgs {
+  const uint8_t* W;
+  const uint8_t* Xq;
+  const int8_t* grid;   // 256 x 8
+  const int8_t* signs;  // 128 x 8 (+-1)
+  float* Y;
+  int N, K, M;
+};
+
+// Direct global->LDS loads; lane l writes [lds + size*l, +size).  Inline asm
+// keeps the compiler from making unrelated LDS reads wait for them; the
+// kernel waits (s_waitcnt) itself.  Nothing else in this kernel uses M0.
+__device__ __forceinline__ void lds_dma16(const uint8_t* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds), "v"(g)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma4(const uint8_t* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
+               :
+               : "s"(lds), "v"(g)
+               : "memory", "m0");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_ptr)p;
+}
+__device__ __forceinline__ uint32_t ld32(const uint8_t* p) {
+  return *reinterpret_cast<const uint32_t*>(p);
+}
+// An empty asm that claims to modify v: the optimizer cannot re-associate a
+// running sum through it.  Used on the eight-group sum, which it would
+// otherwise turn into a tree holding every group's 16-register product tile
+// live.  (It emits nothing, so the compiler still places the wait states a
+// VALU read of an MFMA result needs.)
+__device__ __forceinline__ void pin(int& v) { asm volatile("" : "+v"(v)); }
+// negate the bytes of g whose sign byte in s is -1 (bit 7 set): bytes of g
+// are in [0, 43], so (b ^ 0xff) + 1 never carries into the next byte
+__device__ __forceinline__ uint32_t apply_signs(uint32_t g, uint32_t s) {
+  const uint32_t m = ((s >> 7) & 0x01010101u) * 0xffu;
+  return (g ^ m) + (m & 0x01010101u);
+}
+
+__global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
+  __shared__ __align__(16) uint8_t ring0[kSlotAlloc];
+  __shared__ __align__(16) uint8_t ring1[kSlotAlloc];
+  __shared__ __align__(16) float dxs[2][2][kMT];  // [slot][parity][token]
+  __shared__ __align__(16) uint8_t tgrid[256 * 8];
+  __shared__ __align__(16) uint8_t tsign[128 * 8];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+  const int par = wave >> 2, wcol = wave & 3;
+  const int col = lane & 31, kg = lane >> 5;
+  const int nsb = a.K >> 8;
+  const int npair = nsb >> 1;  // nsb is even on this path
+  const size_t wrb = (size_t)nsb * kIq2xxsBytes;
+  const size_t xrb = (size_t)nsb * kQ8_KBytes;
+
+  int m0, n0;  // XCD-aware tile order (workgroups are dealt round-robin to 8 XCDs)
+  {
+    const int ntm = (a.M + kMT - 1) / kMT;
+    const int Tn = ntm * ((a.N + kNT - 1) / kNT);
+    const int L = blockIdx.x, x = L & 7, j = L >> 3;
+    const int t = x * (Tn >> 3) + min(x, Tn & 7) + j;
+    m0 = (t % ntm) * kMT;
+    n0 = (t / ntm) * kNT;
+  }
+
+  for (int i = tid; i < 256 * 8; i += kThreads) tgrid[i] = (uint8_t)a.grid[i];
+  for (int i = tid; i < 128 * 8; i += kThreads) tsign[i] = (uint8_t)a.signs[i];
+
+  // activation int8 of superblock 2*pair + par: 16 wave-wide 16-byte loads, 4 per wave
+  const uint8_t* asrc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int k = wcol + 4 * i;
+    const int q = 64 * k + lane, r = q >> 4, c = (q & 15) ^ (r & 15);
+    asrc[i] = a.Xq + (size_t)min(m0 + r, a.M - 1) * xrb + 4 + 16 * c;
+  }
+  const uint8_t* dsrc = a.Xq + (size_t)min(m0 + lane, a.M - 1) * xrb;  // Q8_K d of token lane
+
+  auto issue = [&](int pair, uint8_t* ring) {
+    const int b = 2 * pair + par;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      lds_dma16(asrc[i] + (size_t)b * kQ8_KBytes,
+                __builtin_amdgcn_readfirstlane(lds_addr(ring + par * kAQ + 1024 * (wcol + 4 * i))));
+    // weight pair: 66 dword loads over the 8 waves
+#pragma unroll
+    for (int i = 0; i < (kWSlots + 7) / 8; ++i) {
+      const int k = wave + 8 * i;
+      if (k < kWSlots) {
+        const int q = 64 * k + lane, row = q / kWD, part = q - kWD * row;
+        const uint8_t* g = a.W + (size_t)min(n0 + row, a.N - 1) * wrb + (size_t)pair * kPairB + 4 * part;
+        lds_dma4(g, __builtin_amdgcn_readfirstlane(lds_addr(ring + 2 * kAQ + 256 * k)));
+      }
+    }
+  };
+  float dxr = 0.f;
+  auto load_dx = [&](int pair) {
+    dxr = *reinterpret_cast<const float*>(dsrc + (size_t)(2 * pair + par) * kQ8_KBytes);
+  };
+
+  v16i I[2], acc[2];
+  v16f y[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) y[t][r] = 0.f;
+  const v16i zero = {};
+  const int sw = col & 15;
+  const int sb0 = par * kIq2xxsBytes;  // this parity's record within the pair: 0 or 66
+
+  auto step = [&](int pair, const uint8_t* cur, uint8_t* nxt) {
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of this pair have landed
+    __syncthreads();                // everyone's; the previous pair is consumed
+    const bool refill = pair + 1 < npair;
+    if (refill) {
+      issue(pair + 1, nxt);
+      if (wcol == 0) load_dx(pair + 1);
+    }
+    const uint8_t* AQ = cur + par * kAQ;
+    const uint8_t* rec = cur + 2 * kAQ + (32 * wcol + col) * kPairB + sb0;
+    const float* dx = &dxs[pair & 1][par][0];
+    // fp16 d: bytes 0-1 of the record (rec is 4-byte aligned for parity 0,
+    // 2 past an aligned dword for parity 1)
+    const uint32_t dword0 = ld32(rec - 2 * par);
+    const float dw = fp16_to_fp32(par ? dword0 >> 16 : dword0 & 0xffffu);
+    const int sh = 2 - 2 * par;  // byte offset of group data (rec + 2 + 8g) in its dword
+    const uint8_t* gbase = rec + 2 - sh;  // 4-byte aligned
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      const uint32_t w0 = ld32(gbase + 8 * g), w1 = ld32(gbase + 8 * g + 4), w2 = ld32(gbase + 8 * g + 8);
+      const uint32_t idx = __builtin_amdgcn_alignbyte(w1, w0, sh);   // 4 grid indices
+      const uint32_t meta = __builtin_amdgcn_alignbyte(w2, w1, sh);  // 4 x 7-bit signs, 4-bit s
+      // this lane's 16 elements: grid entries l = 2kg, 2kg+1 (8 elements each)
+      const uint32_t i0 = (idx >> (16 * kg)) & 0xffu, i1 = (idx >> (16 * kg + 8)) & 0xffu;
+      const uint32_t s0 = (meta >> (14 * kg)) & 127u, s1 = (meta >> (14 * kg + 7)) & 127u;
+      const uint2 g0 = *reinterpret_cast<const uint2*>(tgrid + 8 * i0);
+      const uint2 g1 = *reinterpret_cast<const uint2*>(tgrid + 8 * i1);
+      const uint2 z0 = *reinterpret_cast<const uint2*>(tsign + 8 * s0);
+      const uint2 z1 = *reinterpret_cast<const uint2*>(tsign + 8 * s1);
+      const v4i bv = {(int)apply_signs(g0.x, z0.x), (int)apply_signs(g0.y, z0.y),
+                      (int)apply_signs(g1.x, z1.x), (int)apply_signs(g1.y, z1.y)};
+      const int ls = 2 * (int)(meta >> 28) + 1;
+      const int chunk = (2 * g + kg) ^ sw;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const v4i av = *reinterpret_cast<const v4i*>(AQ + (32 * t + col) * 256 + 16 * chunk);
+        I[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, zero, 0, 0, 0);
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          int v = __mul24(I[t][r], ls) + (g == 0 ? 0 : acc[t][r]);
+          pin(v);
+          acc[t][r] = v;
+        }
+    }
+    // y += (dw * dx) * acc; register r of a tile holds token 8*(r/4) + 4*kg + r%4
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const float4 d4 = *reinterpret_cast<const float4*>(dx + 32 * t + 8 * r4 + 4 * kg);
+        const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int r = 4 * r4 + q;
+          y[t][r] += (dw * dv[q]) * (float)acc[t][r];
+        }
+      }
+    if (refill && wcol == 0) dxs[(pair + 1) & 1][par][lane] = dxr;  // slot last read a pair ago
+  };
+
+  issue(0, ring0);
+  if (wcol == 0) {
+    load_dx(0);
+    dxs[0][par][lane] = dxr;
+  }
+  for (int pair = 0; pair < npair; pair += 2) {
+    step(pair, ring0, ring1);
+    if (pair + 1 < npair) step(pair + 1, ring1, ring0);
+  }
+
+  // odd-parity partial sums -> LDS -> even waves, one ordered add per output
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(ring0) + wcol * (32 * 64) + lane;
+  if (par == 1) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[(16 * t + r) * 64] = y[t][r];
+  }
+  __syncthreads();
+  if (par == 1) return;
+  const int gn = n0 + 32 * wcol + col;
+  if (gn < a.N) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int gm = m0 + 32 * t + 8 * (r >> 2) + 4 * kg + (r & 3);
+        if (gm < a.M) a.Y[(size_t)gm * a.N + gn] = 0.125f * (y[t][r] + red[(16 * t + r) * 64]);
+      }
+  }
+}
+
+}  // namespace
+
+void mul_mat_iq2_xxs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,
+                     const int8_t* signs, float* Y, size_t N, size_t K, size_t M) {
+  // MFMA path: prefill shapes with an even number of superblocks per row and
+  // 4-byte aligned weights; the GEMV kernels take everything else
+  const bool mfma = M >= 16 && N > 0 && K > 0 && K % 512 == 0 && W != nullptr && X != nullptr &&
+                    Xq != nullptr && Y != nullptr && grid != nullptr && signs != nullptr &&
+                    aligned(W, 4) && aligned(Xq, 4) && aligned(Y, 4) && aligned(X, 4) &&
+                    N <= (size_t)INT32_MAX && K <= (size_t)INT32_MAX && M <= (size_t)INT32_MAX &&
+                    ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT) <= (size_t)INT32_MAX;
+  if (!mfma) return decode_iq2_xxs(W, X, Xq, grid, signs, Y, N, K, M);
+  quantize_q8_k(X, Xq, M * K);
+  GemmArgs ga{W, Xq, grid, signs, Y, (int)N, (int)K, (int)M};
+  const size_t tiles = ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT);
+  iq2_mfma_gemm<<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(ga);
+  check_launch();
+}
+
+}  // namespace weft
