@@ -206,6 +206,14 @@ def test_decode_configs(hip, fmt, n, k):
     check_mul_mat(fmt, w, x, xq, y, n, k, 1)
 
 
+@pytest.mark.parametrize("n,k", [(300, 8192), (5000, 8192), (4100, 12288), (17, 11008)])
+def test_decode_q4_k_long_rows(hip, n, k):
+    # batch-1 Q4_K launch shapes: two and three 4096-column steps per row,
+    # with one row per wave (N <= 16 per CU) and with two row buffers
+    w, x, xq, y = run_mul_mat(hip, MM_DECODE["q4_k"], "q4_k", n, k, 1)
+    check_mul_mat("q4_k", w, x, xq, y, n, k, 1)
+
+
 @pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "iq2_xxs", "mxfp4"])
 @pytest.mark.parametrize("n,k,m", [(300, 768, 3), (65, 1024, 5), (1, 256, 1)])
 def test_decode_small_shapes(hip, fmt, n, k, m):

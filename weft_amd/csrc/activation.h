@@ -43,13 +43,11 @@ __device__ inline float4 load_x4(const float* p, bool a16) {
   return make_float4(p[0], p[1], p[2], p[3]);
 }
 
-// Quantize one Q8_K superblock (index idx = m * nsb + s of this launch's
-// activation rows) held as this lane's float4 into LDS, and into xq_out
-// when non-null.
-__device__ inline void q8k_quantize_store(float4 x, int idx, int nsb, int K, int m0,
-                                          uint8_t* __restrict__ xq_out, char* lds, int lane) {
+// Store one quantized Q8_K superblock (index idx = m * nsb + s of this
+// launch's activation rows) into LDS, and into xq_out when non-null.
+__device__ inline void q8k_store(const Q8KLane& r, int idx, int nsb, int K, int m0,
+                                 uint8_t* __restrict__ xq_out, char* lds, int lane) {
   const int m = idx / nsb, s = idx - m * nsb;
-  const Q8KLane r = q8k_quantize_wave(x, lane);
   const Q8KView v = q8k_view(lds, K, m);
   const int packed = pack4_i8(r.q);
   reinterpret_cast<int*>(v.qs + 256 * s)[lane] = packed;
@@ -67,13 +65,22 @@ __device__ inline void q8k_quantize_store(float4 x, int idx, int nsb, int K, int
   }
 }
 
+// Quantize one Q8_K superblock held as this lane's float4 and store it.
+__device__ inline void q8k_quantize_store(float4 x, int idx, int nsb, int K, int m0,
+                                          uint8_t* __restrict__ xq_out, char* lds, int lane) {
+  q8k_store(q8k_quantize_wave(x, lane), idx, nsb, K, m0, xq_out, lds, lane);
+}
+
 // Two-phase Q8_K staging so a kernel can put the activation's loads in front
 // of its weight stream: prefetch() issues the loads of this wave's first
-// kPrefetch superblocks (vector loads complete in issue order, so waiting for
+// P superblocks (vector loads complete in issue order, so waiting for
 // these does not wait for weight loads issued after them); finish()
-// quantizes them into LDS and handles any remaining superblocks.
-struct Q8KStager {
-  static constexpr int kPrefetch = 4;
+// quantizes them into LDS and handles any remaining superblocks.  A kernel
+// that knows its row length picks P = superblocks per wave, so no load is
+// issued twice.
+template <int P>
+struct Q8KStagerT {
+  static constexpr int kPrefetch = P;
   float4 x[kPrefetch];
 
   __device__ inline void prefetch(const float* __restrict__ X, int K, int m0, int mb) {
@@ -96,16 +103,113 @@ struct Q8KStager {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int nwaves = blockDim.x / kWave;
     const int nsb = K / 256, total = mb * nsb;
+    // quantize every prefetched superblock first (independent straight-line
+    // chains the scheduler interleaves), then store the live ones
+    Q8KLane r[kPrefetch];
+#pragma unroll
+    for (int i = 0; i < kPrefetch; ++i) r[i] = q8k_quantize_wave(x[i], lane);
 #pragma unroll
     for (int i = 0; i < kPrefetch; ++i) {
       const int idx = wave + i * nwaves;
-      if (idx < total) q8k_quantize_store(x[i], idx, nsb, K, m0, xq_out, lds, lane);
+      if (idx < total) q8k_store(r[i], idx, nsb, K, m0, xq_out, lds, lane);
     }
     const bool a16 = (reinterpret_cast<uintptr_t>(X) & 15) == 0;
     for (int idx = wave + kPrefetch * nwaves; idx < total; idx += nwaves) {
       const int m = idx / nsb, s = idx - m * nsb;
       const float4 v = load_x4(X + (size_t)(m0 + m) * K + 256 * s + 4 * lane, a16);
       q8k_quantize_store(v, idx, nsb, K, m0, xq_out, lds, lane);
+    }
+  }
+};
+using Q8KStager = Q8KStagerT<4>;
+
+// Q8_K staging with 16 lanes per superblock (q8k_quantize_16lanes): pass i
+// of wave w quantizes superblock 4 (w + i * nwaves) + lane / 16 of the
+// launch's rows; P passes are prefetched (a kernel picks P so that they
+// cover every superblock), further superblocks are loaded in finish().
+template <int P>
+struct Q8KStager16 {
+  float4 x[P][4];
+
+  __device__ inline void prefetch(const float* __restrict__ X, int K, int m0, int mb) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int nwaves = blockDim.x / kWave;
+    const int nsb = K / 256, total = mb * nsb;
+    const bool a16 = (reinterpret_cast<uintptr_t>(X) & 15) == 0;
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      // a wave whose pass i is past the end loads nothing (uniform branch)
+      if (4 * (wave + i * nwaves) >= total) break;
+      const int idx = min(4 * (wave + i * nwaves) + lane / 16, total - 1);  // clamped: a valid load
+      const int m = idx / nsb, s = idx - m * nsb;
+      const float* src = X + (size_t)(m0 + m) * K + 256 * s + 16 * (lane & 15);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[i][j] = load_x4(src + 4 * j, a16);
+    }
+  }
+
+  __device__ static inline void store(const Q8K16& r, int idx, int nsb, int K, int m0,
+                                      uint8_t* __restrict__ xq_out, char* lds, int part) {
+    const int m = idx / nsb, s = idx - m * nsb;
+    const Q8KView v = q8k_view(lds, K, m);
+    *reinterpret_cast<uint4*>(v.qs + 256 * s + 16 * part) = make_uint4(r.qs[0], r.qs[1], r.qs[2], r.qs[3]);
+    // 32-sub-block sum = groups 2t and 2t+1, held by parts 2t and 2t+1
+    const int pair = r.bsum + dpp_row_i<kDppXor1>(r.bsum);
+    if ((part & 1) == 0) v.bp[8 * s + part / 2] = pair;
+    if (part == 0) v.d[s] = r.d;
+    if (xq_out != nullptr) {
+      uint8_t* rec = xq_out + ((size_t)(m0 + m) * nsb + s) * kQ8_KBytes;
+      if (part == 0) *reinterpret_cast<float*>(rec) = r.d;
+      uint32_t* q = reinterpret_cast<uint32_t*>(rec + 4 + 16 * part);
+      q[0] = r.qs[0];
+      q[1] = r.qs[1];
+      q[2] = r.qs[2];
+      q[3] = r.qs[3];
+      if (!r.zero) reinterpret_cast<int16_t*>(rec + 260)[part] = (int16_t)r.bsum;
+    }
+  }
+
+  __device__ inline void finish(const float* __restrict__ X, uint8_t* __restrict__ xq_out, int K,
+                                int m0, int mb, char* lds) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int nwaves = blockDim.x / kWave;
+    const int nsb = K / 256, total = mb * nsb;
+    const int part = lane & 15;
+    // passes are all-or-nothing per wave except the last superblocks of the
+    // final pass; waves without work skip straight to the caller's barrier
+    int live = 0;
+#pragma unroll
+    for (int i = 0; i < P; ++i) live += 4 * (wave + i * nwaves) < total ? 1 : 0;
+    if (live == P) {
+      Q8K16 r[P];
+#pragma unroll
+      for (int i = 0; i < P; ++i) r[i] = q8k_quantize_16lanes(x[i], part);
+#pragma unroll
+      for (int i = 0; i < P; ++i) {
+        const int idx = 4 * (wave + i * nwaves) + lane / 16;
+        if (idx < total) store(r[i], idx, nsb, K, m0, xq_out, lds, part);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < P; ++i) {
+        if (i >= live) break;
+        const int idx = 4 * (wave + i * nwaves) + lane / 16;
+        const Q8K16 r = q8k_quantize_16lanes(x[i], part);
+        if (idx < total) store(r, idx, nsb, K, m0, xq_out, lds, part);
+      }
+    }
+    const bool a16 = (reinterpret_cast<uintptr_t>(X) & 15) == 0;
+    for (int w = wave + P * nwaves; 4 * w < total; w += nwaves) {
+      const int idx = min(4 * w + lane / 16, total - 1);
+      const int m = idx / nsb, s = idx - m * nsb;
+      const float* src = X + (size_t)(m0 + m) * K + 256 * s + 16 * part;
+      float4 v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = load_x4(src + 4 * j, a16);
+      const Q8K16 q = q8k_quantize_16lanes(v, part);
+      if (4 * w + lane / 16 < total) store(q, idx, nsb, K, m0, xq_out, lds, part);
     }
   }
 };

@@ -202,8 +202,12 @@ __global__ void __launch_bounds__(NT) q4k_gemv_kernel(Q4KArgs a) {
 // computed, so every CU keeps ~16 rows in flight and computes as its data
 // streams in, instead of bursting all its requests up front and computing
 // after the last one lands.
-template <int STEPS, int NT>
+// RB = row buffers: 2 for the ping-pong walk above, 1 when the launch gives
+// every wave at most one row (long rows at NT = 1024, where a second buffer
+// would not fit the register budget).
+template <int STEPS, int NT, int RB>
 __global__ void __launch_bounds__(NT) q4k_gemv_m1_kernel(Q4KArgs a) {
+  static_assert(RB == 1 || RB == 2, "one or two row buffers");
   extern __shared__ __align__(16) char lds[];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -225,7 +229,9 @@ __global__ void __launch_bounds__(NT) q4k_gemv_m1_kernel(Q4KArgs a) {
   const int row_end = min(a.N, blockIdx.x * a.rows_per_wg + a.rows_per_wg);
   const int nrows = row_first < row_end ? (row_end - row_first + nwaves - 1) / nwaves : 0;
 
-  Q8KStager stager;
+  // 16 lanes per superblock, four superblocks per wave pass: P passes cover
+  // the 16 STEPS superblocks of the longest row
+  Q8KStager16<(4 * STEPS + nwaves - 1) / nwaves> stager;
   stager.prefetch(a.X, K, a.m0, 1);
   // keep the activation loads ahead of the weight loads: waits are in issue
   // order, so the quantization then waits for X only
@@ -246,7 +252,7 @@ __global__ void __launch_bounds__(NT) q4k_gemv_m1_kernel(Q4KArgs a) {
     }
   };
   RowBuf bufA, bufB;
-  issue(bufA, 0);
+  issue(bufA, 0);  // bufB is only used (and allocated) when RB == 2
   __builtin_amdgcn_sched_barrier(0);
 
   stager.finish(a.X, blockIdx.x == 0 ? a.xq_out : nullptr, K, a.m0, 1, lds);
@@ -315,6 +321,10 @@ __global__ void __launch_bounds__(NT) q4k_gemv_m1_kernel(Q4KArgs a) {
     if (lane == 0) a.Y[row_first + k * nwaves] = tot;
   };
 
+  if constexpr (RB == 1) {
+    if (nrows > 0) compute(bufA, 0);
+    return;
+  }
   // Issues inside the loop are unconditional so the in-order wait counts stay
   // exact (a conditional issue forces a full wait on the other path).
   int k = 0;
@@ -373,8 +383,11 @@ void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t*
     // runs 1024-thread workgroups, two per CU (62 VGPRs); longer rows keep
     // three activation slices in VGPRs and run 512 threads, one per CU.
     const int steps = (int)((K + 4095) / 4096);
+    // one row per wave at NT = 1024 (one workgroup per CU) when the rows are
+    // long and few enough: 16 waves share the activation quantization
+    const bool one_row = steps > 1 && N <= (size_t)cus * 16;
     const int wgs = steps == 1 ? 2 * cus : cus;
-    const int rpw = (int)((N + wgs - 1) / wgs);
+    const int rpw = one_row ? 16 : (int)((N + wgs - 1) / wgs);
     Q4KArgs a;
     a.W = W;
     a.X = X;
@@ -389,11 +402,15 @@ void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t*
     a.y_stride = (long long)N;
     const int g1 = (int)((N + rpw - 1) / rpw);
     if (steps == 1)
-      q4k_gemv_m1_kernel<1, 1024><<<g1, 1024, row_lds, current_stream()>>>(a);
+      q4k_gemv_m1_kernel<1, 1024, 2><<<g1, 1024, row_lds, current_stream()>>>(a);
+    else if (one_row && steps == 2)
+      q4k_gemv_m1_kernel<2, 1024, 1><<<g1, 1024, row_lds, current_stream()>>>(a);
+    else if (one_row)
+      q4k_gemv_m1_kernel<3, 1024, 1><<<g1, 1024, row_lds, current_stream()>>>(a);
     else if (steps == 2)
-      q4k_gemv_m1_kernel<2, 512><<<g1, 512, row_lds, current_stream()>>>(a);
+      q4k_gemv_m1_kernel<2, 512, 2><<<g1, 512, row_lds, current_stream()>>>(a);
     else
-      q4k_gemv_m1_kernel<3, 512><<<g1, 512, row_lds, current_stream()>>>(a);
+      q4k_gemv_m1_kernel<3, 512, 2><<<g1, 512, row_lds, current_stream()>>>(a);
     check_launch();
     return;
   }

@@ -178,17 +178,12 @@ struct Q8KLane {
 
 __device__ __forceinline__ Q8KLane q8k_quantize_wave(float4 x, int lane) {
 #pragma clang fp contract(off)
+  // Straight-line code (no early exit for the all-zero block): a wave that
+  // quantizes several superblocks runs their dependency chains interleaved.
   Q8KLane r;
   const float xv[4] = {x.x, x.y, x.z, x.w};
   const float amax = wave_max_nonneg(fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w))));
   r.zero = !(amax > 0.f);
-  if (r.zero) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r.q[i] = 0;
-    r.d = 0.f;
-    r.bsum16 = 0;
-    return r;
-  }
   // the signed value at the first index whose |x| is amax: first lane with
   // a match (ballot), then that lane's first match
   float first = 0.f;
@@ -201,19 +196,124 @@ __device__ __forceinline__ Q8KLane q8k_quantize_wave(float4 x, int lane) {
     }
   }
   const unsigned long long hits = __ballot(hit);
-  const int src = __ffsll(hits) - 1;
+  const int src = hits ? __ffsll(hits) - 1 : 0;
   const float bval = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(first), src));
-  const float iscale = __fdiv_rn(-127.f, bval);
+  // an all-zero block divides by a stand-in 1 and selects zeros below
+  const float iscale = __fdiv_rn(-127.f, r.zero ? 1.f : bval);
   int s = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const float p = iscale * xv[i];
     const int v = (int)rintf(p);
-    r.q[i] = v < 127 ? v : 127;
+    r.q[i] = r.zero ? 0 : (v < 127 ? v : 127);
     s += r.q[i];
   }
   r.bsum16 = sum4(s);
-  r.d = __fdiv_rn(1.f, iscale);
+  const float d = __fdiv_rn(1.f, iscale);
+  r.d = r.zero ? 0.f : d;
+  return r;
+}
+
+// One Q8_K superblock quantized by 16 lanes (four superblocks per wave):
+// lane part p = lane % 16 holds x[16p .. 16p+15], which is exactly bsum
+// group p, so the block sums need no cross-lane step.  Same arithmetic as
+// q8k_quantize_wave / quantize_row_q8_K_ref:
+//   * amax over the superblock: 4-step DPP max inside the 16-lane row;
+//   * the signed value at the first index with |x| == amax: each lane's
+//     first match, then the lowest matching lane (DPP min of its part
+//     index) and that lane's value (DPP sum of a one-hot value);
+//   * q = nearest_int(iscale * x) with GGML's 1.5 * 2^23 bias, whose float
+//     bits carry q in their low byte; GGML's MIN(127, q) never binds since
+//     |iscale * x| <= 127 (1 + 2^-24)^2 < 127.5.
+struct Q8K16 {
+  uint32_t qs[4];  // this lane's 16 quantized values, packed little-endian
+  float d;         // block scale (uniform in the 16 lanes)
+  int bsum;        // sum of this lane's 16 values (GGML bsums[p])
+  bool zero;       // all-zero block: d = 0, q = 0, bsums left untouched
+};
+
+template <int Ctrl>
+__device__ __forceinline__ float dpp_row(float v) {  // DPP inside 16-lane rows
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), Ctrl, 0xF, 0xF, false));
+}
+template <int Ctrl>
+__device__ __forceinline__ int dpp_row_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, Ctrl, 0xF, 0xF, false);
+}
+
+__device__ __forceinline__ Q8K16 q8k_quantize_16lanes(const float4 (&x4)[4], int part) {
+#pragma clang fp contract(off)
+  float x[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[4 * i] = x4[i].x;
+    x[4 * i + 1] = x4[i].y;
+    x[4 * i + 2] = x4[i].z;
+    x[4 * i + 3] = x4[i].w;
+  }
+  // reductions are written as trees: the dependent chain is what the
+  // workgroup waits for
+  float m8[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) m8[i] = fmaxf(fabsf(x[2 * i]), fabsf(x[2 * i + 1]));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) m8[i] = fmaxf(m8[2 * i], m8[2 * i + 1]);
+  float am = fmaxf(fmaxf(m8[0], m8[1]), fmaxf(m8[2], m8[3]));
+  am = fmaxf(am, dpp_row<kDppXor1>(am));
+  am = fmaxf(am, dpp_row<kDppXor2>(am));
+  am = fmaxf(am, dpp_row<kDppHalfMirror>(am));
+  am = fmaxf(am, dpp_row<kDppMirror>(am));
+  Q8K16 r;
+  r.zero = !(am > 0.f);
+  // this lane's first match: a tree over pairs, the lower index winning
+  float fv[16];
+  bool fh[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    fv[i] = x[i];
+    fh[i] = fabsf(x[i]) == am;
+  }
+#pragma unroll
+  for (int w = 1; w < 16; w *= 2) {
+#pragma unroll
+    for (int i = 0; i < 16; i += 2 * w) {
+      fv[i] = fh[i] ? fv[i] : fv[i + w];
+      fh[i] = fh[i] || fh[i + w];
+    }
+  }
+  const float first = fv[0];
+  const bool hit = fh[0];
+  int key = hit ? part : 16;
+  key = min(key, dpp_row_i<kDppXor1>(key));
+  key = min(key, dpp_row_i<kDppXor2>(key));
+  key = min(key, dpp_row_i<kDppHalfMirror>(key));
+  key = min(key, dpp_row_i<kDppMirror>(key));
+  float bv = part == key ? first : 0.f;  // one lane holds the value, the rest +0
+  bv += dpp_row<kDppXor1>(bv);
+  bv += dpp_row<kDppXor2>(bv);
+  bv += dpp_row<kDppHalfMirror>(bv);
+  bv += dpp_row<kDppMirror>(bv);
+  const float iscale = __fdiv_rn(-127.f, r.zero ? 1.f : bv);
+  uint32_t b[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float p = iscale * x[i];
+    b[i] = __float_as_uint(p + 12582912.f);  // 0x4B400000 + q
+  }
+  // modulo 2^32 the sixteen biases cancel exactly
+  uint32_t t4[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) t4[i] = (b[4 * i] + b[4 * i + 1]) + (b[4 * i + 2] + b[4 * i + 3]);
+  const uint32_t sum = (t4[0] + t4[1]) + (t4[2] + t4[3]) - 16u * 0x4B400000u;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // low bytes of four biased floats -> one packed word
+    const uint32_t lo = __builtin_amdgcn_perm(b[4 * i + 1], b[4 * i], 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(b[4 * i + 3], b[4 * i + 2], 0x04000c0cu);
+    r.qs[i] = r.zero ? 0u : (lo | hi);
+  }
+  r.bsum = r.zero ? 0 : (int)sum;
+  r.d = r.zero ? 0.f : __fdiv_rn(1.f, iscale);
   return r;
 }
 
