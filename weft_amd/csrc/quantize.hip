@@ -3,11 +3,11 @@
 // GGML's quantize_row_q8_0_ref / quantize_row_q8_K_ref
 // (ggml-quants.c:238-261, :2696-2733).
 //
-// HBM-bound (read 4 B, write ~1.1 B per element).  Q8_K: one wave per
-// superblock, lane l owns x[4l..4l+3] (one 16-byte load); the first-index
-// |max| and the 16-sums are wave reductions.  Q8_0: 8 lanes per block,
-// 8 blocks per wave step.  The grid is sized to a few waves per CU and
-// strides over the blocks.
+// HBM-bound (read 4 B, write ~1.1 B per element).  Q8_K: 16 lanes per
+// superblock, lane p owns x[16p..16p+15] (four 16-byte loads), so the
+// 16-sums are in-lane and the first-index |max| is a 16-lane reduction.
+// Q8_0: 8 lanes per block, 8 blocks per wave step.  The grid is sized to a
+// few waves per CU and strides over the blocks.
 #include <algorithm>
 
 #include "runtime.h"
@@ -24,19 +24,41 @@ __device__ __forceinline__ float4 ldx4(const float* p, bool a16) {
   return make_float4(p[0], p[1], p[2], p[3]);
 }
 
+// 16 lanes per superblock (q8k_quantize_16lanes): lane part p holds bsum
+// group p, a wave quantizes four superblocks per pass; both passes' loads are
+// issued before the first is quantized.
 __global__ void __launch_bounds__(kThreads) q8k_quantize_kernel(const float* __restrict__ X,
                                                                 uint8_t* __restrict__ Y, long long nb) {
+  constexpr int U = 2;  // passes in flight per wave
   const int lane = threadIdx.x & (kWave - 1);
+  const int part = lane & 15;
   const long long wave = ((long long)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
   const long long nwaves = (long long)gridDim.x * blockDim.x / kWave;
   const bool a16 = (reinterpret_cast<uintptr_t>(X) & 15) == 0;
-  for (long long b = wave; b < nb; b += nwaves) {
-    const float4 x = ldx4(X + b * 256 + 4 * lane, a16);
-    const Q8KLane r = q8k_quantize_wave(x, lane);
-    uint8_t* rec = Y + b * kQ8_KBytes;
-    reinterpret_cast<int*>(rec + 4)[lane] = pack4_i8(r.q);
-    if (lane == 0) *reinterpret_cast<float*>(rec) = r.d;
-    if (!r.zero && (lane & 3) == 0) reinterpret_cast<int16_t*>(rec + 260)[lane / 4] = (int16_t)r.bsum16;
+  for (long long p0 = wave * U; 4 * p0 < nb; p0 += nwaves * U) {
+    float4 x[U][4];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long long b = min(4 * (p0 + u) + lane / 16, nb - 1);  // clamped: a valid load
+      const float* src = X + b * 256 + 16 * part;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[u][j] = ldx4(src + 4 * j, a16);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long long b = 4 * (p0 + u) + lane / 16;
+      const Q8K16 r = q8k_quantize_16lanes(x[u], part);
+      if (b < nb) {
+        uint8_t* rec = Y + b * kQ8_KBytes;
+        if (part == 0) *reinterpret_cast<float*>(rec) = r.d;
+        uint32_t* q = reinterpret_cast<uint32_t*>(rec + 4 + 16 * part);
+        q[0] = r.qs[0];
+        q[1] = r.qs[1];
+        q[2] = r.qs[2];
+        q[3] = r.qs[3];
+        if (!r.zero) reinterpret_cast<int16_t*>(rec + 260)[part] = (int16_t)r.bsum;
+      }
+    }
   }
 }
 
@@ -76,7 +98,7 @@ void quantize_q8_k(const float* X, uint8_t* Y, size_t K) {
   if (K % 256 || X == nullptr || Y == nullptr || !aligned(X, 4) || !aligned(Y, 4))
     return set_error(hipErrorInvalidValue);
   const long long nb = (long long)(K / 256);
-  q8k_quantize_kernel<<<grid_for(nb), kThreads, 0, current_stream()>>>(X, Y, nb);
+  q8k_quantize_kernel<<<grid_for((nb + 7) / 8), kThreads, 0, current_stream()>>>(X, Y, nb);
   check_launch();
 }
 
