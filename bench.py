@@ -8,13 +8,18 @@ included, exactly as the reference's timed mul_mat (weft-kernel-performance.csv:
 ``value`` is the algorithmic HBM bytes of the call (encoded W + fp32 X + Xq
 write + fp32 Y = 25,427,520 B) divided by the measured time per call, in GB/s.
 
-Inputs are seeded synthetic data (W ~ N(0, 0.02^2) quantized with the GGML
-Q4_K reference quantizer restated in oracle/, X ~ N(0, 1)) resident in HBM
-before timing.  W is rotated over enough copies (> 2 x the 256 MB Infinity
-Cache) that every call streams its weights from HBM.  The timed region is K
-back-to-back calls on one stream between two HIP events, bracketed by device
-synchronisation.  Secondary lines time W_down (4096 x 11008) and the Q4_K
-prefill entry point (config 4, M=512).
+Inputs are seeded synthetic data (weights ~ N(0, 0.02^2) quantized with the
+GGML reference quantizers restated in oracle/, activations ~ N(0, 1)) resident
+in HBM before timing.  For the HBM-bound decode cases the weights are rotated
+over enough copies (> 2 x the 256 MB Infinity Cache) that every call streams
+them from HBM.  A timed region is K back-to-back calls on the library's stream
+between two HIP events, bracketed by device synchronisation.
+
+Secondary figures (the other BASELINE.json configs) ride in the same JSON
+line under ``configs``: W_down decode, the Q4_0 / IQ2_XXS / MXFP4 decode GEMVs,
+the Q4_K row dequantize, and the prefill mul_mats (Q4_K config 4 at N=4096 and
+N=11008, MXFP4 config 5b, Q4_0 and IQ2_XXS at the same shape), the latter
+against the int8 MFMA peak.
 
 The CPU baseline is oracle/'s restatement of GGML's generic MUL_MAT path
 (quantize_row_q8_K_ref + ggml_vec_dot_q4_K_q8_K_generic, rows over OpenMP
@@ -37,6 +42,22 @@ HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
 MALL_BYTES = 256 << 20
 
+# name: (symbol, format, N, K, M, bound)
+CASES = {
+    "q4_k_decode_w_up": ("production_mul_mat_q4_k_decode", "q4_k", 11008, 4096, 1, "hbm"),
+    "q4_k_decode_w_down": ("production_mul_mat_q4_k_decode", "q4_k", 4096, 11008, 1, "hbm"),
+    "q4_0_decode": ("production_mul_mat_q4_0_decode", "q4_0", 4096, 4096, 1, "hbm"),
+    "iq2_xxs_decode": ("production_mul_mat_iq2_xxs_decode", "iq2_xxs", 4096, 4096, 1, "hbm"),
+    "mxfp4_decode": ("production_mul_mat_mxfp4_decode", "mxfp4", 4096, 4096, 1, "hbm"),
+    "q4_k_dequant": ("row_dequantize_q4_k", "q4_k", 11008, 4096, 0, "hbm"),
+    "q4_k_prefill_n4096": ("production_mul_mat_q4_k_staged", "q4_k", 4096, 4096, 512, "mfma"),
+    "q4_k_prefill_n11008": ("production_mul_mat_q4_k_staged", "q4_k", 11008, 4096, 512, "mfma"),
+    "mxfp4_prefill": ("production_mul_mat_mxfp4", "mxfp4", 4096, 4096, 512, "mfma"),
+    "q4_0_prefill": ("production_mul_mat_q4_0", "q4_0", 4096, 4096, 512, "mfma"),
+    "iq2_xxs_prefill": ("production_mul_mat_iq2_xxs_staged", "iq2_xxs", 4096, 4096, 512, "mfma"),
+}
+HEADLINE = "q4_k_decode_w_up"
+
 
 def parse():
     p = argparse.ArgumentParser()
@@ -46,8 +67,9 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="wall-clock budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--no-prefill", action="store_true")
-    p.add_argument("--no-wdown", action="store_true")
+    p.add_argument("--cases", default="all",
+                   help="comma-separated secondary cases to run (default all; 'none' for "
+                        "the headline only): " + ",".join(c for c in CASES if c != HEADLINE))
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                    help="also run one plain device-to-device copy of MIB MiB, the known-size "
                         "kernel that HBM byte counters are scaled against")
@@ -69,15 +91,11 @@ def profiled_traffic(name: str):
     return None
 
 
-def algorithmic_bytes(n, k, m, w_bytes):
-    xq = m * (k // 256) * 292
-    return w_bytes + 4 * m * k + xq + 4 * m * n
-
-
 class Bench:
     def __init__(self):
         import torch
 
+        import oracle as o
         from weft_amd import _lib
         self.torch = torch
         self.lib = _lib.load()
@@ -85,12 +103,17 @@ class Bench:
         self.dev = torch.device("cuda:0")
         self.stream = torch.cuda.current_stream()
         _lib.set_stream(self.stream.cuda_stream)
+        self.tables = {
+            "iq2_xxs": [self.dev_copy(o.iq2xxs_grid().view(np.int8)), self.dev_copy(o.signs_i8x8())],
+            "mxfp4": [self.dev_copy(o.kvalues_mxfp4()), self.dev_copy(o.e8m0_half_table())],
+        }
 
     def dev_copy(self, a: np.ndarray):
         return self.torch.from_numpy(np.ascontiguousarray(a)).to(self.dev)
 
     def time_calls(self, launch, steps, warmup):
-        """launch(i) enqueues call i; returns seconds per call over `steps`."""
+        """launch(i) enqueues call i; returns seconds per call over `steps`,
+        from two HIP events on the stream the library launches on."""
         torch = self.torch
         for i in range(warmup):
             launch(i)
@@ -108,49 +131,55 @@ class Bench:
         return start.elapsed_time(end) / 1e3 / steps
 
 
-def q4k_weights(n, k, seed):
+def run_case(b: Bench, name: str, steps: int, warmup: int) -> dict:
+    """Time one case; returns its figures (algorithmic bytes / ops, rate, roofline fraction)."""
     import oracle as o
-    return o.quantize("q4_k", o.seeded_normal(seed, (n, k), 0.02))
-
-
-def decode_case(b, n, k, steps, warmup):
-    import oracle as o
-    w = q4k_weights(n, k, 1)
-    copies = max(2, int(np.ceil(2 * MALL_BYTES / w.nbytes)) + 1)
+    sym, fmt, n, k, m, bound = CASES[name]
+    w = o.quantize(fmt, o.seeded_normal(1, (n, k), 0.02))
+    torch = b.torch
+    copies = 1
+    if bound == "hbm":  # stream the weights from HBM on every call
+        copies = max(2, int(np.ceil(2 * MALL_BYTES / w.nbytes)) + 1)
     wd = [b.dev_copy(w) for _ in range(copies)]
-    x = b.dev_copy(o.seeded_normal(2, (1, k)))
-    xq = b.torch.empty((k // 256) * 292, dtype=b.torch.uint8, device=b.dev)
-    y = b.torch.empty(n, dtype=b.torch.float32, device=b.dev)
-    fn = b.lib.production_mul_mat_q4_k_decode
+    fn = getattr(b.lib, sym)
+    if m == 0:  # row dequantize of the whole matrix
+        y = torch.empty(n * k, dtype=torch.float32, device=b.dev)
 
-    def launch(i):
-        fn(wd[i % copies].data_ptr(), x.data_ptr(), xq.data_ptr(), y.data_ptr(), n, k, 1)
+        def launch(i):
+            fn(wd[i % copies].data_ptr(), y.data_ptr(), n * k)
 
+        nbytes = w.nbytes + 4 * n * k
+    else:
+        act = o.ACT_OF[fmt]
+        x = b.dev_copy(o.seeded_normal(2, (m, k)))
+        xq = torch.empty(o.record_bytes(act, k) * m, dtype=torch.uint8, device=b.dev)
+        y = torch.empty(m * n, dtype=torch.float32, device=b.dev)
+        tabs = [t.data_ptr() for t in b.tables.get(fmt, [])]
+
+        def launch(i):
+            fn(wd[i % copies].data_ptr(), x.data_ptr(), xq.data_ptr(), *tabs, y.data_ptr(), n, k, m)
+
+        nbytes = w.nbytes + 4 * m * k + xq.numel() + 4 * m * n
+    if bound == "mfma":
+        steps, warmup = max(3, steps // 20), 3
     sec = b.time_calls(launch, steps, warmup)
-    nbytes = algorithmic_bytes(n, k, 1, w.nbytes)
     del wd
-    b.torch.cuda.empty_cache()
-    return sec, nbytes, copies
-
-
-def prefill_case(b, n, k, m, steps, warmup):
-    import oracle as o
-    w = b.dev_copy(q4k_weights(n, k, 1))
-    x = b.dev_copy(o.seeded_normal(2, (m, k)))
-    xq = b.torch.empty(m * (k // 256) * 292, dtype=b.torch.uint8, device=b.dev)
-    y = b.torch.empty(m * n, dtype=b.torch.float32, device=b.dev)
-    fn = b.lib.production_mul_mat_q4_k_staged
-
-    def launch(i):
-        fn(w.data_ptr(), x.data_ptr(), xq.data_ptr(), y.data_ptr(), n, k, m)
-
-    sec = b.time_calls(launch, steps, warmup)
-    return sec, 2.0 * m * n * k
+    torch.cuda.empty_cache()
+    out = {"symbol": sym, "N": n, "K": k, "M": m, "us": round(sec * 1e6, 3),
+           "algorithmic_bytes": int(nbytes), "GBs": round(nbytes / sec / 1e9, 2),
+           "weight_copies_rotated": copies, "steps": steps}
+    if bound == "hbm":
+        out["frac_hbm_peak"] = round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4)
+    else:
+        tops = 2.0 * m * n * k / sec / 1e12
+        out.update({"ops": 2 * m * n * k, "TOPS": round(tops, 2),
+                    "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)})
+    return out
 
 
 def cpu_baseline(n, k, budget_s):
     import oracle as o
-    w = q4k_weights(n, k, 1)
+    w = o.quantize("q4_k", o.seeded_normal(1, (n, k), 0.02))
     x = o.seeded_normal(2, (1, k))
     threads = o.max_threads()
     o.mul_mat("q4_k", w, x, n, k, 1, threads=threads)  # warmup
@@ -162,8 +191,8 @@ def cpu_baseline(n, k, budget_s):
         if el >= budget_s or reps >= 100000:
             break
     per = el / reps
-    gbs = algorithmic_bytes(n, k, 1, w.nbytes) / per / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+    nbytes = w.nbytes + 4 * k + (k // 256) * 292 + 4 * n
+    return {"value": round(nbytes / per / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"{reps} full decode calls (N={n}, K={k}, M=1) in {el:.1f} s, "
                       f"{per * 1e3:.3f} ms/call, OpenMP over {threads} host threads"}
 
@@ -177,11 +206,16 @@ def main():
     b = Bench()
     steps, warmup = args.steps, args.warmup
 
-    sec, nbytes, copies = decode_case(b, 11008, 4096, steps, warmup)
-    gbs = nbytes / sec / 1e9
-    sec_dn = nbytes_dn = None
-    if not args.no_wdown:
-        sec_dn, nbytes_dn, _ = decode_case(b, 4096, 11008, steps, warmup)
+    head = run_case(b, HEADLINE, steps, warmup)
+    sec = head["us"] / 1e6
+    gbs = head["GBs"]
+    if args.cases == "all":
+        names = [c for c in CASES if c != HEADLINE]
+    elif args.cases == "none":
+        names = []
+    else:
+        names = [c for c in args.cases.split(",") if c]
+    secondary = {name: run_case(b, name, steps, warmup) for name in names}
     if args.calibrate_copy:
         n = args.calibrate_copy << 20
         src = b.torch.empty(n, dtype=b.torch.uint8, device=b.dev)
@@ -189,18 +223,11 @@ def main():
         b.torch.cuda.synchronize()
         dst.copy_(src)
         b.torch.cuda.synchronize()
-    prefill = {}
-    if not args.no_prefill:
-        for n in (4096, 11008):
-            psec, ops = prefill_case(b, n, 4096, 512, max(3, steps // 20), 2)
-            tops = ops / psec / 1e12
-            prefill[f"N{n}"] = {"us": round(psec * 1e6, 2), "TOPS": round(tops, 3),
-                                "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 5)}
     cpu = None if args.no_cpu else cpu_baseline(11008, 4096, args.cpu_seconds)
 
     line = {
         "metric": "Q4_K mul_mat: decode GB/s (% of 8 TB/s) + prefill TOPS (% int8 MFMA peak)",
-        "value": round(gbs, 2),
+        "value": gbs,
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
@@ -210,20 +237,19 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic (seeded N(0,0.02) weights quantized by the oracle's GGML Q4_K "
-                "quantizer, N(0,1) activations)",
+        "data": "synthetic (seeded N(0,0.02) weights quantized by the oracle's GGML reference "
+                "quantizers, N(0,1) activations)",
         "config": {"workload": "production_mul_mat_q4_k_decode, config 3 W_up: N=11008 K=4096 "
                                "M=1, Q8_K activation quantize inside the timed call",
-                   "N": 11008, "K": 4096, "M": 1, "weight_copies_rotated": copies},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                   "N": 11008, "K": 4096, "M": 1,
+                   "weight_copies_rotated": head["weight_copies_rotated"]},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": profiled_traffic("q4k_decode_w_up"),
-                     "algorithmic_bytes": nbytes},
+                     "algorithmic_bytes": head["algorithmic_bytes"],
+                     "kernel": "q4k_gemv_m1_kernel<1,1024,2>"},
         "cpu_baseline": cpu,
-        "w_down": None if sec_dn is None else {
-            "N": 4096, "K": 11008, "us": round(sec_dn * 1e6, 3),
-            "GBs": round(nbytes_dn / sec_dn / 1e9, 2)},
-        "prefill_q4_k_M512_K4096": prefill,
+        "configs": secondary,
     }
     print(json.dumps(line))
 
