@@ -22,8 +22,13 @@ namespace {
 
 constexpr int kThreads = 256;
 
-__device__ __forceinline__ void store4(float* p, float a, float b, float c, float d, bool a16) {
-  if (a16) {
+// Y16 (16-byte aligned output) is a template parameter, not a runtime flag:
+// with a runtime choice the compiler merges both paths into four strided
+// dword stores per lane, which halves the write bandwidth of these
+// store-bound kernels.
+template <bool Y16>
+__device__ __forceinline__ void store4(float* p, float a, float b, float c, float d) {
+  if constexpr (Y16) {
     *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
   } else {
     p[0] = a;
@@ -37,36 +42,53 @@ __device__ __forceinline__ uint32_t ld32(const uint8_t* p, bool a4) {
   return a4 ? *reinterpret_cast<const uint32_t*>(p) : ld_u32_a2(p);
 }
 
-// Q4_K: one wave per superblock
+// Q4_K: a wave dequantizes U superblocks per pass, lane l writing elements
+// 4l..4l+3 of each; all U passes' loads (the 16-byte header and the lane's
+// nibble word) are issued before the first is used, so a wave keeps U
+// records in flight instead of one.
+template <int U, bool A16, bool Y16>
 __global__ void __launch_bounds__(kThreads) dq_q4k_kernel(const uint8_t* __restrict__ W,
                                                           float* __restrict__ Y, long long nsb) {
   const int lane = threadIdx.x & (kWave - 1);
   const long long wave = ((long long)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
   const long long nwaves = (long long)gridDim.x * blockDim.x / kWave;
   const bool a4 = (reinterpret_cast<uintptr_t>(W) & 3) == 0;
-  const bool y16 = (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
   const int g = lane >> 4;           // 64-element group
   const int e = (lane & 15) * 4;     // offset inside the group
   const int sub = 2 * g + (e >= 32); // 32-element sub-block
   const int qoff = 16 + 32 * g + (e & 31);
   const int shift = e >= 32 ? 4 : 0;
-  for (long long s = wave; s < nsb; s += nwaves) {
-    const uint8_t* rec = W + s * kQ4_KBytes;
-    const uint32_t h0 = ld32(rec, a4), q0 = ld32(rec + 4, a4), q1 = ld32(rec + 8, a4),
-                   q2 = ld32(rec + 12, a4);
-    const uint32_t qs = ld32(rec + qoff, a4);
-    int sc, m;
-    q4k_scale_min(sub, q0, q1, q2, sc, m);
-    const float d = fp16_to_fp32(h0 & 0xffffu), dmin = fp16_to_fp32(h0 >> 16);
-    const float d1 = d * (float)sc, m1 = dmin * (float)m;
-    const uint32_t n = (qs >> shift) & 0x0f0f0f0fu;
-    store4(Y + s * 256 + 4 * lane, d1 * (float)(n & 0xff) - m1, d1 * (float)((n >> 8) & 0xff) - m1,
-           d1 * (float)((n >> 16) & 0xff) - m1, d1 * (float)(n >> 24) - m1, y16);
+  for (long long s0 = wave * U; s0 < nsb; s0 += nwaves * U) {
+    uint4 h[U];
+    uint32_t qs[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint8_t* rec = W + min(s0 + u, nsb - 1) * kQ4_KBytes;  // clamped: a valid record
+      if constexpr (A16) {
+        h[u] = *reinterpret_cast<const uint4*>(rec);
+        qs[u] = *reinterpret_cast<const uint32_t*>(rec + qoff);
+      } else {
+        h[u] = make_uint4(ld32(rec, a4), ld32(rec + 4, a4), ld32(rec + 8, a4), ld32(rec + 12, a4));
+        qs[u] = ld32(rec + qoff, a4);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (s0 + u >= nsb) break;
+      int sc, m;
+      q4k_scale_min(sub, h[u].y, h[u].z, h[u].w, sc, m);
+      const float d = fp16_to_fp32(h[u].x & 0xffffu), dmin = fp16_to_fp32(h[u].x >> 16);
+      const float d1 = d * (float)sc, m1 = dmin * (float)m;
+      const uint32_t n = (qs[u] >> shift) & 0x0f0f0f0fu;
+      store4<Y16>(Y + (s0 + u) * 256 + 4 * lane, d1 * (float)(n & 0xff) - m1,
+                  d1 * (float)((n >> 8) & 0xff) - m1, d1 * (float)((n >> 16) & 0xff) - m1,
+                  d1 * (float)(n >> 24) - m1);
+    }
   }
 }
 
 // Q4_0 / MXFP4: 8 lanes per 32-block, 8 blocks per wave step
-template <bool MX>
+template <bool MX, bool Y16>
 __global__ void __launch_bounds__(kThreads) dq_32_kernel(const uint8_t* __restrict__ W,
                                                          const int8_t* __restrict__ codebook,
                                                          const float* __restrict__ scale,
@@ -74,7 +96,6 @@ __global__ void __launch_bounds__(kThreads) dq_32_kernel(const uint8_t* __restri
   const int lane = threadIdx.x & (kWave - 1);
   const long long wave = ((long long)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
   const long long nwaves = (long long)gridDim.x * blockDim.x / kWave;
-  const bool y16 = (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
   const int p = lane & 7;
   const int shift = p >= 4 ? 4 : 0;
   const long long steps = (nb + 7) / 8;
@@ -95,11 +116,12 @@ __global__ void __launch_bounds__(kThreads) dq_32_kernel(const uint8_t* __restri
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[i] = (float)((int)((qs >> (8 * i + shift)) & 0xf) - 8) * d;
     }
-    store4(Y + b * 32 + 4 * p, v[0], v[1], v[2], v[3], y16);
+    store4<Y16>(Y + b * 32 + 4 * p, v[0], v[1], v[2], v[3]);
   }
 }
 
 // IQ2_XXS: one wave per superblock; lane l -> elements 4l..4l+3
+template <bool Y16>
 __global__ void __launch_bounds__(kThreads) dq_iq2xxs_kernel(const uint8_t* __restrict__ W,
                                                              const int8_t* __restrict__ grid,
                                                              const int8_t* __restrict__ signs,
@@ -107,7 +129,6 @@ __global__ void __launch_bounds__(kThreads) dq_iq2xxs_kernel(const uint8_t* __re
   const int lane = threadIdx.x & (kWave - 1);
   const long long wave = ((long long)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
   const long long nwaves = (long long)gridDim.x * blockDim.x / kWave;
-  const bool y16 = (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
   const int c = lane >> 1;     // 8-element chunk 0..31
   const int h = lane & 1;      // which 4 of the 8
   const int g = c >> 2, l = c & 3;
@@ -124,7 +145,7 @@ __global__ void __launch_bounds__(kThreads) dq_iq2xxs_kernel(const uint8_t* __re
       const int j = 4 * h + i;
       v[i] = (float)((int)grid[8 * idx + j] * (int)signs[8 * sidx + j]) * db;
     }
-    store4(Y + s * 256 + 4 * lane, v[0], v[1], v[2], v[3], y16);
+    store4<Y16>(Y + s * 256 + 4 * lane, v[0], v[1], v[2], v[3]);
   }
 }
 
@@ -148,7 +169,15 @@ void row_dequantize_q4_k(const uint8_t* W, float* Y, size_t K) {
   if (K == 0) return;
   if (K % 256 || bad(W, 2, Y)) return set_error(hipErrorInvalidValue);
   const long long nsb = (long long)(K / 256);
-  dq_q4k_kernel<<<grid_for(nsb), kThreads, 0, current_stream()>>>(W, Y, nsb);
+  constexpr int U = 4;
+  const int g = grid_for((nsb + U - 1) / U);
+  const bool w16 = aligned(W, 16), y16 = aligned(Y, 16);
+  if (w16 && y16)
+    dq_q4k_kernel<U, true, true><<<g, kThreads, 0, current_stream()>>>(W, Y, nsb);
+  else if (y16)
+    dq_q4k_kernel<U, false, true><<<g, kThreads, 0, current_stream()>>>(W, Y, nsb);
+  else
+    dq_q4k_kernel<U, false, false><<<g, kThreads, 0, current_stream()>>>(W, Y, nsb);
   check_launch();
 }
 
@@ -157,8 +186,11 @@ void row_dequantize_q4_0(const uint8_t* W, float* Y, size_t K) {
   if (K == 0) return;
   if (K % 32 || bad(W, 2, Y)) return set_error(hipErrorInvalidValue);
   const long long nb = (long long)(K / 32);
-  dq_32_kernel<false><<<grid_for((nb + 7) / 8), kThreads, 0, current_stream()>>>(W, nullptr, nullptr,
-                                                                                 Y, nb);
+  const int g = grid_for((nb + 7) / 8);
+  if (aligned(Y, 16))
+    dq_32_kernel<false, true><<<g, kThreads, 0, current_stream()>>>(W, nullptr, nullptr, Y, nb);
+  else
+    dq_32_kernel<false, false><<<g, kThreads, 0, current_stream()>>>(W, nullptr, nullptr, Y, nb);
   check_launch();
 }
 
@@ -169,8 +201,11 @@ void row_dequantize_mxfp4(const uint8_t* W, const int8_t* codebook, const float*
   if (K % 32 || bad(W, 1, Y) || codebook == nullptr || scale == nullptr || !aligned(scale, 4))
     return set_error(hipErrorInvalidValue);
   const long long nb = (long long)(K / 32);
-  dq_32_kernel<true><<<grid_for((nb + 7) / 8), kThreads, 0, current_stream()>>>(W, codebook, scale,
-                                                                                Y, nb);
+  const int g = grid_for((nb + 7) / 8);
+  if (aligned(Y, 16))
+    dq_32_kernel<true, true><<<g, kThreads, 0, current_stream()>>>(W, codebook, scale, Y, nb);
+  else
+    dq_32_kernel<true, false><<<g, kThreads, 0, current_stream()>>>(W, codebook, scale, Y, nb);
   check_launch();
 }
 
@@ -181,7 +216,10 @@ void row_dequantize_iq2_xxs(const uint8_t* W, const int8_t* grid, const int8_t* 
   if (K % 256 || bad(W, 2, Y) || grid == nullptr || signs == nullptr)
     return set_error(hipErrorInvalidValue);
   const long long nsb = (long long)(K / 256);
-  dq_iq2xxs_kernel<<<grid_for(nsb), kThreads, 0, current_stream()>>>(W, grid, signs, Y, nsb);
+  if (aligned(Y, 16))
+    dq_iq2xxs_kernel<true><<<grid_for(nsb), kThreads, 0, current_stream()>>>(W, grid, signs, Y, nsb);
+  else
+    dq_iq2xxs_kernel<false><<<grid_for(nsb), kThreads, 0, current_stream()>>>(W, grid, signs, Y, nsb);
   check_launch();
 }
 
