@@ -3,36 +3,45 @@
 //
 //   Y[m, n] = sum_b dx[m,b] * (dw[n,b] * S[m,n,b] - dmin[n,b] * Mn[m,n,b])
 //   S  = sum_s sc[n,b,s] * sum_{k in s} q8[m,k] * q4[n,k]     (exact int32)
-//   Mn = sum_s m[n,b,s]  * BS[m,b,s],  BS = Q8_K bsums[2s] + bsums[2s+1]
+//   Mn = sum_j m[n,b,j/2] * bsum[m,b,j], j = 0..15            (exact)
 //
 // S on int8 MFMA.  The 6-bit sub-block scale sc does not fit an int8 operand
 // once multiplied by a nibble (sc*q <= 945), and applying it per sub-block on
 // VALU costs one instruction per output per 32 products.  So the scale is
 // split, sc = 8a + b with a, b in [0, 7], and every product stays an exact
 // int8 x int8 term: two accumulators per output over each superblock,
-//   lo = sum_k q8 * (q * b_s),   hi = sum_k q8 * (q * a_s),   S = lo + 8 hi,
-// combined in fp32 once per superblock.  v_mfma_i32_32x32x32_i8 has K = 32 =
-// one sub-block, so a sub-block's weight operand is its nibbles times a
-// per-column constant (v_pk_mul_lo_u16 on packed bytes: 105*256+105 < 2^16).
+//   lo = sum_k q8 * (q * b_s),   hi = sum_k q8 * (q * a_s),   S = lo + 8 hi.
+// v_mfma_i32_32x32x32_i8 has K = 32 = one sub-block, so a sub-block's weight
+// operand is its nibbles times a per-column constant (v_pk_mul_lo_u16 on
+// packed bytes: 105*256+105 < 2^16).
 //
-// Mn on fp32 MFMA.  The min term is a GEMM over (superblock, sub-block) with
-// operands A' = dx * BS (per token) and B' = -dmin * m (per weight row), so
-// v_mfma_f32_32x32x2_f32 accumulates it straight into the fp32 outputs:
-// 4 instructions per superblock and tile, no per-output combine.
+// Mn on one f16 MFMA per superblock and 32x32 tile.  Q8_K's 16 bsums are
+// sums of 16 int8 (|bsum| <= 2032 < 2^11) and the mins are 6-bit, so both
+// are exact f16 operands and v_mfma_f32_32x32x16_f16 (K = 16 = the bsums)
+// returns Mn exactly in fp32 (|Mn| <= 2.05e6 < 2^24).  Once per superblock
+// every output then takes
+//   D = (lo + 8 hi) - r * Mn,   y += (dx * f) * D
+// with f = dw, r = dmin / dw; a superblock with dw == 0 zeroes its sc
+// operands (S = 0) and uses f = dmin, r = 1.  The rounding of D and of r
+// stays within 2^-22 of |dw S| + |dmin Mn|, far inside the tolerance.
 //
-// Tiling: a workgroup computes 64 (tokens) x 128 (weight rows) with 8 waves.
-// Waves 0-3 take the even superblocks and waves 4-7 the odd ones; wave w owns
-// weight rows 32*(w%4)..+31 for all 64 tokens (two 32x32 tiles sharing one
-// weight operand).  Each superblock pair is staged by direct global->LDS
-// loads (global_load_lds_dwordx4) into one of two ring slots, issued a pair
-// ahead; one barrier per pair.  The odd waves run their fp32 combine one
-// superblock late, so on every SIMD one wave's combine overlaps the other's
-// MFMAs.  Odd partial sums are added to the even waves' through LDS at the
-// end: every output is written once, in a fixed order.
+// Tiling: a workgroup computes 64 (tokens) x 128 (weight rows) with 8 MFMA
+// waves and 2 loader waves.  MFMA waves 0-3 take the even superblocks and
+// 4-7 the odd ones; wave w owns weight rows 32*(w%4)..+31 for all 64 tokens
+// (two 32x32 tiles sharing one weight operand).  The loader waves stage the
+// next superblock pair into LDS by direct global->LDS loads
+// (global_load_lds_dwordx4, SGPR base + per-lane constant offset) while the
+// MFMA waves compute the current one, so no MFMA wave ever issues or waits on
+// a global memory instruction; one barrier per pair hands a filled ring slot
+// over.  The odd waves run their fp32 combine one superblock late, so on
+// every SIMD one wave's combine overlaps the other's MFMAs.  Odd partial sums
+// are added to the even waves' through LDS at the end: every output is
+// written once, in a fixed order.
 //
-// LDS per superblock stage (37,888 B; 4 stages):
-//   AQ  64 rows x 256 qs bytes; row r keeps 16-byte chunk c at position
-//       c ^ (r & 15), so the 8 lanes of an A-operand read hit distinct banks
+// LDS per superblock stage (38,912 B; 2 pairs = 4 stages):
+//   AQ  64 rows x 17 16-byte chunks: the 16 chunks of qs, then one pad chunk,
+//       so row r starts at 272 r and the 8 lanes of an A-operand read (8
+//       consecutive rows, one chunk) hit distinct banks with immediate offsets
 //   AX  64 rows x 3 chunks: record bytes [0,16) (d), [260,276), [276,292) (bsums)
 //   WT  128 rows x the 144-byte Q4_K record
 // The activation is quantized first, into the caller's Xq, by q8_K_quantize's
@@ -50,20 +59,26 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
-typedef short v2i16 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
 constexpr int kMT = 64;          // tokens per workgroup tile
 constexpr int kNT = 128;         // weight rows per workgroup tile
-constexpr int kThreads = 512;    // 8 waves: 4 column groups x 2 superblock parities
-constexpr int kAQ = kMT * 256;                 // 16384
+constexpr int kMfmaWaves = 8;    // 4 column groups x 2 superblock parities
+constexpr int kLoaders = 2;      // loader waves, one per parity
+constexpr int kThreads = 64 * (kMfmaWaves + kLoaders);
+constexpr int kAQRow = 272;                    // 16 qs chunks + 1 pad chunk
+constexpr int kAQ = kMT * kAQRow;              // 17408
 constexpr int kAX = kMT * 48;                  // 3072
 constexpr int kWT = kNT * kQ4_KBytes;          // 18432
-constexpr int kStage = kAQ + kAX + kWT;        // 37888
-constexpr int kSlots = (kAQ + kAX + kWT) / 1024;  // 37 wave-wide 1 KB loads per superblock
-constexpr int kSlotsPerWave = (kSlots + 3) / 4;   // 10
-static_assert(kStage % 1024 == 0, "a stage is a whole number of wave loads");
+constexpr int kStage = kAQ + kAX + kWT;        // 38912
+constexpr int kAQSlots = kAQ / 1024;           // 17
+constexpr int kAXSlots = kAX / 1024;           // 3
+constexpr int kSlots = kStage / 1024;          // 38 wave-wide 1 KB loads per superblock
+static_assert(kAQ % 1024 == 0 && kAX % 1024 == 0 && kStage % 1024 == 0,
+              "every region is a whole number of wave loads");
 static_assert(4 * 32 * 64 * 4 <= 2 * kStage, "reduction buffer fits one ring slot");
 
 struct GemmArgs {
@@ -80,17 +95,15 @@ __device__ __forceinline__ uint32_t mul_bytes(uint32_t packed, uint32_t c) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
-// Direct global->LDS load of 16 bytes per lane: lane l writes LDS bytes
-// [lds + 16 l, lds + 16 l + 16) (lds wave-uniform).  Issued as inline asm so
-// that the compiler does not make the following LDS reads, which never touch
-// a slot being filled, wait for it; the kernel waits (s_waitcnt) itself.  One
-// wait state separates the M0 write from the load that reads it.
-// Nothing else in this file's kernel uses M0, so clobbering it is safe (the
-// backend's note that a reserved register "may not be preserved" is moot).
-__device__ __forceinline__ void lds_dma16(const uint8_t* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+// Direct global->LDS load of 16 bytes per lane: lane l reads sbase + voff
+// and writes LDS bytes [lds + 16 l, lds + 16 l + 16) (lds wave-uniform).
+// Inline asm: the loader waves wait for these loads themselves (s_waitcnt
+// vmcnt(0) before the step barrier).  One wait state separates the M0 write
+// from the load that reads it; nothing else in this kernel uses M0.
+__device__ __forceinline__ void lds_dma16(const uint8_t* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                :
-               : "s"(lds), "v"(g)
+               : "s"(lds), "v"(voff), "s"(sbase)
                : "memory", "m0");
 }
 
@@ -98,23 +111,28 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(lds_ptr)p;
 }
 
-__device__ __forceinline__ int bsum_pair(uint32_t w) {
-  // bsums[2s] + bsums[2s+1], two int16 in one dword
-  return __builtin_amdgcn_sdot2(__builtin_bit_cast(v2i16, w), (v2i16){1, 1}, 0, false);
+// two int16 (one dword) -> two f16, exact for |v| <= 2048
+__device__ __forceinline__ uint32_t i16x2_to_f16x2(uint32_t w) {
+  const v2h h = {(_Float16)(short)(w & 0xffffu), (_Float16)(short)(w >> 16)};
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+// byte i of w (a 6-bit min) twice, as two f16
+__device__ __forceinline__ uint32_t dup_byte_f16x2(uint32_t w, int i) {
+  // v_perm: bytes [w.i, 0x64, w.i, 0x64] -> halves 0x6400 + m = 1024 + m
+  const uint32_t sel = (uint32_t)i | (4u << 8) | ((uint32_t)i << 16) | (4u << 24);
+  const uint32_t biased = __builtin_amdgcn_perm(0x64646464u, w, sel);
+  const v2h h = __builtin_bit_cast(v2h, biased) - (v2h){(_Float16)1024.f, (_Float16)1024.f};
+  return __builtin_bit_cast(uint32_t, h);
 }
 
 __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
-  // two ring slots as separate objects: a slot being filled by direct loads
-  // never aliases the slot being read
-  __shared__ __align__(16) uint8_t ring0[2 * kStage];
-  __shared__ __align__(16) uint8_t ring1[2 * kStage];
-  __shared__ __align__(16) float dxr[8 * 2 * 64];  // per wave, 2 slots, 64 token scales
+  __shared__ __align__(16) uint8_t ring[4 * kStage];  // [pair slot][parity]
+  __shared__ __align__(16) float dxr[8 * 2 * 64];     // per wave, 2 slots, 64 token scales
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
-  const int par = wave >> 2, wcol = wave & 3;  // superblock parity, column group
-  const int col = lane & 31, kg = lane >> 5;
   // Workgroups are dealt round-robin to the 8 XCDs (linear id % 8), each with
   // its own L2.  Give XCD x a contiguous run of tiles, ordered token-tile
   // fastest, so the workgroups resident on one XCD share weight rows and
@@ -128,55 +146,73 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
     m0 = (t % ntm) * kMT;
     n0 = (t / ntm) * kNT;
   }
+  m0 = __builtin_amdgcn_readfirstlane(m0);
+  n0 = __builtin_amdgcn_readfirstlane(n0);
   const int nsb = a.K >> 8;
-  const size_t wrb = (size_t)nsb * kQ4_KBytes;  // bytes per weight row
-  const size_t xrb = (size_t)nsb * kQ8_KBytes;  // bytes per activation row
+  const int npair = (nsb + 1) >> 1;
 
-  // Direct loads: the waves of parity P stage superblock 2*pair + P.  Wave
-  // wcol issues slots k = wcol + 4i; slot k writes LDS bytes [1024k, 1024k +
-  // 1024) of the stage, lane l the 16 bytes at 1024k + 16l.  src[i] is this
-  // lane's source for superblock 0; superblock b adds b * record size.
-  const uint8_t* src[kSlotsPerWave];
+  if (wave >= kMfmaWaves) {
+    // ---------------------------------------------------------- loader wave
+    // Loader P stages superblock 2*pair + P: slot k of the stage is LDS bytes
+    // [1024k, 1024k + 1024), lane l the 16 bytes at 1024k + 16l.  voff[k] is
+    // this lane's source offset from the tile base of superblock 0.
+    const int par = wave - kMfmaWaves;
+    const uint32_t wrb = (uint32_t)nsb * kQ4_KBytes;
+    const uint32_t xrb = (uint32_t)nsb * kQ8_KBytes;
+    const uint8_t* xbase = a.Xq + (size_t)m0 * xrb;
+    const uint8_t* wbase = a.W + (size_t)n0 * wrb;
+    uint32_t voff[kSlots];
 #pragma unroll
-  for (int i = 0; i < kSlotsPerWave; ++i) {
-    const int k = min(wcol + 4 * i, kSlots - 1);
-    const uint8_t* p;
-    if (k < 16) {
-      const int q = 64 * k + lane, r = q >> 4, c = (q & 15) ^ (r & 15);
-      p = a.Xq + (size_t)min(m0 + r, a.M - 1) * xrb + 4 + 16 * c;
-    } else if (k < 19) {
-      const int q = 64 * (k - 16) + lane, r = q / 3, e = q - 3 * r;
-      p = a.Xq + (size_t)min(m0 + r, a.M - 1) * xrb + (e == 0 ? 0 : 244 + 16 * e);
-    } else {
-      const int q = 64 * (k - 19) + lane, row = q / 9, part = q - 9 * row;
-      p = a.W + (size_t)min(n0 + row, a.N - 1) * wrb + 16 * part;
-    }
-    src[i] = p;
-  }
-  // issue this wave's slots i in [i0, i1) of `pair` into `ring`
-  auto issue = [&](int pair, uint8_t* ring, int i0, int i1) {
-    const int b = min(2 * pair + par, nsb - 1);
-    uint8_t* stage = ring + par * kStage;
-#pragma unroll
-    for (int i = i0; i < i1; ++i) {
-      const int k = wcol + 4 * i;
-      if (k < kSlots) {
-        const size_t off = (size_t)b * (k < 19 ? kQ8_KBytes : kQ4_KBytes);
-        lds_dma16(src[i] + off, __builtin_amdgcn_readfirstlane(lds_addr(stage + 1024 * k)));
+    for (int k = 0; k < kSlots; ++k) {
+      uint32_t o;
+      if (k < kAQSlots) {
+        const int q = 64 * k + lane, r = q / 17, c = min(q - 17 * r, 15);
+        o = (uint32_t)(min(m0 + r, a.M - 1) - m0) * xrb + 4 + 16 * c;
+      } else if (k < kAQSlots + kAXSlots) {
+        const int q = 64 * (k - kAQSlots) + lane, r = q / 3, e = q - 3 * r;
+        o = (uint32_t)(min(m0 + r, a.M - 1) - m0) * xrb + (e == 0 ? 0 : 244 + 16 * e);
+      } else {
+        const int q = 64 * (k - kAQSlots - kAXSlots) + lane, row = q / 9, part = q - 9 * row;
+        o = (uint32_t)(min(n0 + row, a.N - 1) - n0) * wrb + 16 * part;
       }
+      voff[k] = o;
     }
-  };
+    auto issue = [&](int pair) {
+      const int b = min(2 * pair + par, nsb - 1);
+      uint8_t* stage = ring + (2 * (pair & 1) + par) * kStage;
+      const uint8_t* xb = xbase + (size_t)b * kQ8_KBytes;
+      const uint8_t* wb = wbase + (size_t)b * kQ4_KBytes;
+#pragma unroll
+      for (int k = 0; k < kSlots; ++k)
+        lds_dma16(k < kAQSlots + kAXSlots ? xb : wb, voff[k],
+                  __builtin_amdgcn_readfirstlane(lds_addr(stage + 1024 * k)));
+    };
+    issue(0);
+    for (int pair = 0; pair < npair; ++pair) {
+      __builtin_amdgcn_s_waitcnt(0);  // this pair's stage has landed
+      __syncthreads();                // hand it over; the slot of pair - 1 is free
+      if (pair + 1 < npair) issue(pair + 1);
+    }
+    __syncthreads();  // the epilogue's barriers
+    __syncthreads();
+    return;
+  }
+
+  // ------------------------------------------------------------ MFMA wave
+  const int par = wave >> 2, wcol = wave & 3;  // superblock parity, column group
+  const int col = lane & 31, kg = lane >> 5;
 
   v16i lo[2], hi[2];
-  v16f y[2];
+  v16f y[2], mn[2];
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int r = 0; r < 16; ++r) y[t][r] = 0.f;
 
-  // y[t] += dx[row] * dw * (lo + 8 hi); D[i][j] of a 32x32 tile lives in lane
-  // j (+32 for the odd 4-row groups), register r holds row 8*(r/4) + 4*kg + r%4
-  auto combine = [&](float dwv, const float* dxs) {
+  // y[t] += dx[row] * f * (lo + 8 hi - r Mn); D[i][j] of a 32x32 tile lives
+  // in lane j (+32 for the odd 4-row groups), register r holds row
+  // 8*(r/4) + 4*kg + r%4
+  auto combine = [&](float f, float nr, const float* dxs) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
@@ -186,74 +222,60 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int r = 4 * r4 + q;
-          y[t][r] += (dv[q] * dwv) * (float)(lo[t][r] + 8 * hi[t][r]);
+          const float d = fmaf(mn[t][r], nr, (float)(lo[t][r] + 8 * hi[t][r]));
+          y[t][r] = fmaf(d, dv[q] * f, y[t][r]);
         }
       }
     }
   };
 
   const v16i zero = {};
-  const int npair = (nsb + 1) >> 1;
-  const int sw = col & 15;  // A-operand chunk swizzle of this lane's rows
+  const v16f fzero = {};
   bool pending = false;     // odd waves: a combine is owed from the previous pair
-  float dw_prev = 0.f;
-  // one superblock pair: compute from ring slot `cur` while slot `nxt` fills
-  auto step = [&](int pair, const uint8_t* cur, uint8_t* nxt) {
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of this pair have landed
-    __syncthreads();                // everyone's have; the previous pair is consumed
-    // the next pair's loads are spread over this pair's compute, a few per
-    // weight-byte group, so no wave stalls on a burst of ten
-    const bool refill = pair + 1 < npair;
+  float f_prev = 0.f, nr_prev = 0.f;
+  for (int pair = 0; pair < npair; ++pair) {
+    __syncthreads();  // the loaders have staged this pair; the previous pair is consumed
     float* dxs = dxr + (2 * wave + (pair & 1)) * 64;
     if (pending) {  // odd waves: combine of the previous superblock
-      combine(dw_prev, dxr + (2 * wave + ((pair - 1) & 1)) * 64);
+      combine(f_prev, nr_prev, dxr + (2 * wave + ((pair - 1) & 1)) * 64);
       pending = false;
     }
-    if (2 * pair + par >= nsb) {  // odd nsb: the last pair has one superblock
-      if (refill) issue(pair + 1, nxt, 0, kSlotsPerWave);
-      return;
-    }
-
-    const uint8_t* stage = cur + par * kStage;
-    const uint8_t* AQ = stage;
-    const uint8_t* AX = stage + kAQ;
+    if (2 * pair + par >= nsb) continue;  // odd nsb: the last pair has one superblock
+    const uint8_t* stage = ring + (2 * (pair & 1) + par) * kStage;
+    const uint8_t* AQ = stage + kAQRow * col + 16 * kg;          // + 8704 t + 32 s
+    const uint8_t* AX = stage + kAQ + 48 * col;                   // + 1536 t
     const uint8_t* wrow = stage + kAQ + kAX + (32 * wcol + col) * kQ4_KBytes;
 
     const uint4 h = *reinterpret_cast<const uint4*>(wrow);
-    const uint32_t sc03 = h.y & 0x3f3f3f3fu;
-    const uint32_t sc47 = (h.w & 0x0f0f0f0fu) | (((h.y >> 6) & 0x03030303u) << 4);
-    const uint32_t mn03 = h.z & 0x3f3f3f3fu;
-    const uint32_t mn47 = ((h.w >> 4) & 0x0f0f0f0fu) | (((h.z >> 6) & 0x03030303u) << 4);
     const float dw = fp16_to_fp32(h.x & 0xffffu);
     const float dmin = fp16_to_fp32(h.x >> 16);
+    const bool dz = dw == 0.f;
+    const uint32_t sc03 = dz ? 0u : h.y & 0x3f3f3f3fu;
+    const uint32_t sc47 = dz ? 0u : (h.w & 0x0f0f0f0fu) | (((h.y >> 6) & 0x03030303u) << 4);
+    const float f = dz ? dmin : dw;
+    const float nr = dz ? -1.f : -(dmin * __builtin_amdgcn_rcpf(dw));
 
-    // min term: k index of v_mfma_f32_32x32x2f32 = lane / 32, so instruction j
-    // covers sub-blocks s = 2j + kg
-    float dxa[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) dxa[t] = *reinterpret_cast<const float*>(AX + (32 * t + col) * 48);
-    dxs[32 * kg + col] = dxa[kg];  // token scales for the combine (this wave only)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t mw = j < 2 ? mn03 : mn47;
-      const float bm = -dmin * (float)((mw >> (8 * (2 * (j & 1) + kg))) & 0xffu);
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const uint32_t bw = *reinterpret_cast<const uint32_t*>(AX + (32 * t + col) * 48 + 16 + 4 * (2 * j + kg));
-        const float am = dxa[t] * (float)bsum_pair(bw);
-        y[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(am, bm, y[t], 0, 0, 0);
-      }
-    }
+    // token scales for the combine (this wave only)
+    dxs[32 * kg + col] = *reinterpret_cast<const float*>(AX + 1536 * kg);
 
+    // A operands (activation rows, 16 bytes per lane) run one sub-block ahead
+    // of their MFMAs, so no MFMA waits on an LDS read issued just before it
+    v4i acur[2], anxt[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) acur[t] = *reinterpret_cast<const v4i*>(AQ + 32 * kAQRow * t);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      if (refill) issue(pair + 1, nxt, (kSlotsPerWave * g) / 4, (kSlotsPerWave * (g + 1)) / 4);
       // 16 qs bytes: elements 64g + 16kg + i (low nibble) and 64g + 32 + 16kg + i (high)
       const uint4 q = *reinterpret_cast<const uint4*>(wrow + 16 + 32 * g + 16 * kg);
       const uint32_t scw = g < 2 ? sc03 : sc47;
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
         const int s = 2 * g + hf;
+        if (s < 7) {
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+            anxt[t] = *reinterpret_cast<const v4i*>(AQ + 32 * kAQRow * t + 32 * (s + 1));
+        }
         const uint32_t sc = (scw >> (8 * (s & 3))) & 0xffu;
         const uint32_t n0w = hf ? (q.x >> 4) & 0x0f0f0f0fu : q.x & 0x0f0f0f0fu;
         const uint32_t n1w = hf ? (q.y >> 4) & 0x0f0f0f0fu : q.y & 0x0f0f0f0fu;
@@ -264,35 +286,45 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
                           (int)mul_bytes(n3w, cb)};
         const v4i b_hi = {(int)mul_bytes(n0w, ca), (int)mul_bytes(n1w, ca), (int)mul_bytes(n2w, ca),
                           (int)mul_bytes(n3w, ca)};
-        const int chunk = (2 * s + kg) ^ sw;
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-          const v4i av = *reinterpret_cast<const v4i*>(AQ + (32 * t + col) * 256 + 16 * chunk);
-          lo[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b_lo, s == 0 ? zero : lo[t], 0, 0, 0);
-          hi[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b_hi, s == 0 ? zero : hi[t], 0, 0, 0);
+          lo[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(acur[t], b_lo, s == 0 ? zero : lo[t], 0, 0, 0);
+          hi[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(acur[t], b_hi, s == 0 ? zero : hi[t], 0, 0, 0);
         }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) acur[t] = anxt[t];
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // min term: bsums j = 8 kg .. 8 kg + 7 of each token against m[j / 2]
+    {
+      const uint32_t mn03 = h.z & 0x3f3f3f3fu;
+      const uint32_t mn47 = ((h.w >> 4) & 0x0f0f0f0fu) | (((h.z >> 6) & 0x03030303u) << 4);
+      const uint32_t mw = kg ? mn47 : mn03;
+      const v4i bm = {(int)dup_byte_f16x2(mw, 0), (int)dup_byte_f16x2(mw, 1),
+                      (int)dup_byte_f16x2(mw, 2), (int)dup_byte_f16x2(mw, 3)};
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint4 bs = *reinterpret_cast<const uint4*>(AX + 1536 * t + 16 + 16 * kg);
+        const v4i am = {(int)i16x2_to_f16x2(bs.x), (int)i16x2_to_f16x2(bs.y),
+                        (int)i16x2_to_f16x2(bs.z), (int)i16x2_to_f16x2(bs.w)};
+        mn[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, am),
+                                                      __builtin_bit_cast(v8h, bm), fzero, 0, 0, 0);
+      }
+    }
     if (par == 0) {
-      combine(dw, dxs);
+      combine(f, nr, dxs);
     } else {
       pending = true;
-      dw_prev = dw;
+      f_prev = f;
+      nr_prev = nr;
     }
-  };
-  issue(0, ring0, 0, kSlotsPerWave);
-  for (int pair = 0; pair < npair; pair += 2) {
-    step(pair, ring0, ring1);
-    if (pair + 1 < npair) step(pair + 1, ring1, ring0);
   }
-  if (pending) combine(dw_prev, dxr + (2 * wave + ((npair - 1) & 1)) * 64);
+  if (pending) combine(f_prev, nr_prev, dxr + (2 * wave + ((npair - 1) & 1)) * 64);
 
   // odd-parity partial sums -> LDS (reusing the stages) -> even waves
   __syncthreads();
-  float* red = reinterpret_cast<float*>(ring0) + wcol * (32 * 64) + lane;
+  float* red = reinterpret_cast<float*>(ring) + wcol * (32 * 64) + lane;
   if (par == 1) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
