@@ -279,6 +279,45 @@ def test_prefill_config5b_sampled(hip, fmt):
     check_mul_mat(fmt, w, x, xq, y, n, k, m, cols=cols)
 
 
+def test_prefill_mxfp4_crafted_scales(hip):
+    """MXFP4 prefill on the block-scaled MFMA with every nibble and a wide
+    spread of E8M0 exponents (2..200, whole rows at both ends), not just the
+    few a quantizer emits; products stay inside fp32's range."""
+    n, k, m = 256, 1024, 64
+    rng = np.random.default_rng(21)
+    rec = rng.integers(0, 256, size=(n, k // 32, 17), dtype=np.uint8)
+    rec[:, :, 0] = rng.integers(2, 201, size=(n, k // 32), dtype=np.uint8)
+    rec[0, :, 0] = 200
+    rec[1, :, 0] = 2  # 2^-126: the smallest normal block scale
+    w = rec.reshape(n, -1)
+    x = acts(m, k)
+    xq = hip.empty(o.record_bytes("q8_0", k) * m, fill=SENTINEL)
+    y = hip.empty(4 * m * n, fill=SENTINEL)
+    hip.call("production_mul_mat_mxfp4", hip.to_dev(w), hip.to_dev(x), xq, hip.codebook, hip.scale, y,
+             n, k, m)
+    check_mul_mat("mxfp4", w, x, xq.numpy(np.uint8).reshape(m, -1), y.numpy(np.float32).reshape(m, n),
+                  n, k, m)
+
+
+@pytest.mark.parametrize("symbol,m", [("production_mul_mat_mxfp4", 64), ("production_mul_mat_mxfp4_decode", 1)])
+def test_mxfp4_caller_tables_are_used(hip, symbol, m):
+    """A scale table that is not GGML's (every entry doubled) is honoured:
+    the prefill takes the table-driven int8-MFMA GEMM and the result is
+    exactly twice GGML's."""
+    n, k = 256, 1024
+    w, x = weights("mxfp4", n, k), acts(m, k)
+    with np.errstate(over="ignore"):  # entry 255 (2^127) doubles to inf
+        scale2 = hip.to_dev(2.0 * o.e8m0_half_table())
+    xq = hip.empty(o.record_bytes("q8_0", k) * m, fill=SENTINEL)
+    y = hip.empty(4 * m * n, fill=SENTINEL)
+    hip.call(symbol, hip.to_dev(w), hip.to_dev(x), xq, hip.codebook, scale2, y, n, k, m)
+    want_xq = np.full((m, o.record_bytes("q8_0", k)), SENTINEL, np.uint8)
+    o.quantize("q8_0", x, out=want_xq)
+    np.testing.assert_array_equal(xq.numpy(np.uint8).reshape(m, -1), want_xq)
+    e, a = o.mul_mat_f64("mxfp4", w, want_xq, n, k, m)
+    assert_close(y.numpy(np.float32).reshape(m, n), 2.0 * e, 2.0 * a, "mxfp4 with doubled scale table")
+
+
 # ------------------------------------------------------------ error paths
 def test_invalid_shape_reports_error_and_launches_nothing(hip):
     y = hip.empty(16, fill=SENTINEL)

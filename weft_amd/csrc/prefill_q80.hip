@@ -86,6 +86,13 @@ __device__ __forceinline__ void lds_dma4(const uint8_t* g, uint32_t lds) {
                : "s"(lds), "v"(g)
                : "memory", "m0");
 }
+// 4 bytes per lane from sbase + voff (SGPR base, 32-bit lane offset)
+__device__ __forceinline__ void lds_dma4_s(const uint8_t* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
+               :
+               : "s"(lds), "v"(voff), "s"(sbase)
+               : "memory", "m0");
+}
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(lds_ptr)p;
 }
@@ -103,8 +110,15 @@ __device__ __forceinline__ uint32_t lookup16(uint32_t n, uint32_t c0, uint32_t c
   return (hi & mask) | (lo & ~mask);
 }
 
+// LDS bytes of the int8 GEMM body: two ring slots of two stages, the token
+// scales, the MXFP4 scale table
 template <WFmt F>
-__global__ void __launch_bounds__(kThreads, 1) q80_mfma_gemm(GemmArgs a) {
+constexpr int q80_lds_bytes() {
+  return 4 * (kAQ + kNT * 8 * WTraits<F>::kRec) + 2 * 2 * 8 * kMT * 4 + 256 * 4;
+}
+
+template <WFmt F>
+__device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
   using T = WTraits<F>;
   constexpr int kRB = 8 * T::kRec;           // raw weight bytes per row and stage
   constexpr int kWT = kNT * kRB;             // 18432 (Q4_0) / 17408 (MXFP4)
@@ -115,10 +129,13 @@ __global__ void __launch_bounds__(kThreads, 1) q80_mfma_gemm(GemmArgs a) {
   static_assert(kNT * kWD % 256 == 0, "weight slots split evenly over four waves");
   static_assert(4 * 32 * 64 * 4 <= 2 * kStage, "reduction buffer fits one ring slot");
 
-  __shared__ __align__(16) uint8_t ring0[2 * kStage];
-  __shared__ __align__(16) uint8_t ring1[2 * kStage];
-  __shared__ __align__(16) float adt[2][2][8 * kMT];  // [slot][parity][block][token]
-  __shared__ float scl[F == WFmt::MXFP4 ? 256 : 1];
+  // two ring slots; a slot being filled by direct loads never aliases the
+  // slot being read
+  uint8_t* ring0 = lds;
+  uint8_t* ring1 = lds + 2 * kStage;
+  float(*adt)[2][8 * kMT] = reinterpret_cast<float(*)[2][8 * kMT]>(lds + 4 * kStage);  // [slot][parity][block][token]
+  float* scl = reinterpret_cast<float*>(lds + 4 * kStage) + 2 * 2 * 8 * kMT;
+  static_assert(q80_lds_bytes<F>() == 4 * kStage + 2 * 2 * 8 * kMT * 4 + 256 * 4, "LDS carve");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -306,17 +323,48 @@ __global__ void __launch_bounds__(kThreads, 1) q80_mfma_gemm(GemmArgs a) {
   }
 }
 
+template <WFmt F>
+__global__ void __launch_bounds__(kThreads, 1) q80_mfma_gemm(GemmArgs a) {
+  __shared__ __align__(16) uint8_t lds[q80_lds_bytes<F>()];
+  q80_gemm_body<F>(a, lds);
+}
+
 __device__ __forceinline__ float4 ldx4(const float* p, bool a16) {
   if (a16) return *reinterpret_cast<const float4*>(p);
   return make_float4(p[0], p[1], p[2], p[3]);
 }
 
+// GGML's MXFP4 tables: kvalues_mxfp4 (ggml-common.h:1116-1118) and
+// ggml_e8m0_to_fp32_half (ggml-impl.h:477-495): 2^(e-128), e < 2 as fp32
+// subnormals.  Thread i checks entry i; a workgroup of at least 256 threads
+// covers both tables.
+__device__ __forceinline__ bool ggml_mxfp4_entry(const int8_t* codebook, const float* scale, int i) {
+  bool ok = true;
+  if (i < 256) {
+    const uint32_t bits = i < 2 ? 0x00200000u << i : (uint32_t)(i - 1) << 23;
+    ok = __float_as_uint(scale[i]) == bits;
+  }
+  if (i < 16) {
+    const int u = i & 7, kv = u < 5 ? u : u == 5 ? 6 : u == 6 ? 8 : 12;
+    ok = ok && codebook[i] == ((i & 8) ? -kv : kv);
+  }
+  return ok;
+}
+
 // Q8_0 quantization of X (M x K) into the planar layout: row m at m * 17K/16,
 // K int8 values then K/32 fp16 scales.  Same arithmetic as q8_0_quantize
 // (ggml-quants.c:238-261), so the values equal the record layout's.
+//
+// For the MXFP4 block-scaled GEMM (kMx, and the caller passed GGML's tables)
+// the int8 values are stored as sign and magnitude and in that GEMM's K
+// order: byte 2i of a block holds element i, byte 2i + 1 element i + 16.
+template <bool kMx>
 __global__ void __launch_bounds__(256) q80_planar_kernel(const float* __restrict__ X,
                                                          uint8_t* __restrict__ Xp, long long nb,
-                                                         int bpr, long long xs) {
+                                                         int bpr, long long xs, const int8_t* codebook,
+                                                         const float* scale) {
+  bool kord = false;
+  if constexpr (kMx) kord = __syncthreads_and(ggml_mxfp4_entry(codebook, scale, threadIdx.x)) != 0;
   const int lane = threadIdx.x & (kWave - 1);
   const long long wave = ((long long)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
   const long long nwaves = (long long)gridDim.x * blockDim.x / kWave;
@@ -328,12 +376,286 @@ __global__ void __launch_bounds__(256) q80_planar_kernel(const float* __restrict
     float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
     if (live) x = ldx4(X + b * 32 + 4 * (lane & 7), a16);
     const Q8_0Lane r = q80_quantize_8lanes(x);
+    uint32_t word = (uint32_t)pack4_i8(r.q);
+    int at = 4 * (lane & 7);
+    if (kord) {
+      // lane g holds elements 4g..4g+3; lanes g and g ^ 4 (elements 16
+      // apart) interleave into bytes 8(g % 4) .. 8(g % 4) + 7
+      uint32_t sm = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) sm |= (uint32_t)(r.q[k] < 0 ? 0x80 | -r.q[k] : r.q[k]) << (8 * k);
+      const uint32_t other = (uint32_t)__shfl_xor((int)sm, 4);
+      const bool upper = (lane & 4) != 0;
+      word = upper ? __builtin_amdgcn_perm(sm, other, 0x07030602u) : __builtin_amdgcn_perm(other, sm, 0x05010400u);
+      at = 8 * (lane & 3) + (upper ? 4 : 0);
+    }
     if (!live) continue;
     const long long row = b / bpr, blk = b - row * bpr;
     uint8_t* rp = Xp + row * xs;
-    *reinterpret_cast<uint32_t*>(rp + 32 * blk + 4 * (lane & 7)) = (uint32_t)pack4_i8(r.q);
+    *reinterpret_cast<uint32_t*>(rp + 32 * blk + at) = word;
     if ((lane & 7) == 0) *reinterpret_cast<uint16_t*>(rp + (long long)bpr * 32 + 2 * blk) = (uint16_t)r.dh;
   }
+}
+
+// ---------------------------------------------------------------------------
+// MXFP4 x Q8_0 prefill on the gfx950 block-scaled f8f6f4 MFMA.
+//
+// GGML's MXFP4 record is OCP MXFP4: 16 bytes of E2M1 nibbles (kvalues_mxfp4
+// is twice E2M1) and an E8M0 exponent whose GGML scale is 2^(e-128).  So
+// v_mfma_scale_f32_32x32x64_f8f6f4 takes the weight bytes unchanged as its
+// fp4 A operand and e as the A block scale: a block contributes
+// 2^(e-127) * sum E2M1(q) * x = ws * I exactly.  The activation side must be
+// an 8-bit float, and a Q8_0 value (int8, |x| <= 127) is not exact in E4M3,
+// so each value is split by magnitude: |x| = 16 mh + ml with mh in 0..7 and
+// ml in 0..15, both planes carrying the sign of x.  With a block scale of
+// 2^9 the E4M3 codes 0x00..0x0f are exactly the integers 0..15 (subnormals,
+// then the first binade), so a plane's code is its magnitude with x's sign
+// bit; the hi plane's block scale is 2^13 (x16).  The planar pre-pass stores
+// x as a sign-and-magnitude byte (s | mh << 4 | ml), so the codes are
+// lo = b & 0x8f and hi = b & 0x80 | (b >> 4) & 7: four VALU operations per
+// four values.  One MFMA (K = 64) takes a 32-value weight block, twice,
+// against the hi and lo planes of the matching activation block and returns
+// ws * I for a 32x32 tile; the fp16 token scale is applied by one FMA per
+// output and block.
+//
+// Operand layout (measured on the device): the weights are the fp4 A
+// operand and the activation the fp8 B operand, so a lane owns one token and
+// its scale is one value per block.  The fp4 operand of lane (row i, half h)
+// holds K values [32h, 32h + 32) as 32 nibbles, low nibble first: both
+// halves carry the same weight record.  The fp8 operand of lane (col j,
+// half h) holds K values [16h, 16h + 16) of each 32-value half in dwords 0-3
+// (hi plane) and 4-7 (lo plane).  Block b's scales come from lanes i + 32b /
+// j + 32b.  The MFMA's K order within a block therefore pairs nibble k with
+// GGML element k/2 + 16 (k%2), the order the pre-pass writes.
+//
+// Tiling: 64 tokens x 128 weight rows per workgroup, 8 waves = 2 column
+// halves x 4 K phases.  A stage is 8 blocks (256 K values); a wave takes
+// blocks 2p and 2p + 1 of each stage and computes all four 32x32 tiles of its
+// 64 x 64 quarter, so each weight operand and each split activation operand
+// feeds two MFMAs.  The four phases' partial sums are added through LDS at
+// the end, in phase order.  Every global byte arrives by direct
+// global->LDS loads into a ring of four stages, a pair of stages ahead:
+// activation rows with their 16 chunks of 16 bytes XOR-swizzled by token
+// (conflict-free operand reads), the token scales block-major, and the raw
+// weight rows at an odd dword stride (140 bytes).  One barrier per two stages.
+namespace mx {
+
+constexpr int kMT = 64;
+constexpr int kNT = 128;
+constexpr int kRowW = 140;                 // LDS bytes per weight row and stage: 136 + pad
+constexpr int kSD = kMT * 256;             // 16384: token scales, fp16 [block pair][token][2]
+constexpr int kSW = kSD + kMT * 16;        // 17408: weight rows
+constexpr int kSlot = kSW + kNT * kRowW;   // 35328
+constexpr int kLds = 4 * kSlot;            // 141312
+constexpr int kWLoads = kNT * kRowW / 256; // 70 wave-wide dword loads of weights
+static_assert(kNT * kRowW % 256 == 0, "whole wave-wide weight loads");
+static_assert(8 * 4 * 16 * 64 * 4 <= kLds, "partial sums fit the ring");
+
+// 16 bytes per lane from sbase + voff into [lds + 16 lane, +16)
+__device__ __forceinline__ void dma16_s(const uint8_t* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(lds), "v"(voff), "s"(sbase)
+               : "memory", "m0");
+}
+
+// LDS-only barrier: outstanding direct loads stay in flight
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+
+__device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+  const int cp = wave & 1, ph = wave >> 1;  // column half, K phase
+  const int col = lane & 31, h = lane >> 5;
+  const int nst = a.K >> 8;
+  const uint32_t xs = (uint32_t)a.K + (uint32_t)a.K / 16;  // planar activation row stride
+  const uint32_t ws_row = (uint32_t)(a.K / 32) * kMxfp4Bytes;
+
+  int m0, n0;
+  {
+    const int ntm = (a.M + kMT - 1) / kMT;
+    const int Tn = ntm * ((a.N + kNT - 1) / kNT);
+    const int L = blockIdx.x, x = L & 7, j = L >> 3;
+    const int t = x * (Tn >> 3) + min(x, Tn & 7) + j;
+    m0 = __builtin_amdgcn_readfirstlane((t % ntm) * kMT);
+    n0 = __builtin_amdgcn_readfirstlane((t / ntm) * kNT);
+  }
+  const uint8_t* xbase = a.Xp + (size_t)m0 * xs;
+  const uint8_t* wbase = a.W + (size_t)n0 * ws_row;
+  const int mlast = a.M - 1 - m0, nlast = a.N - 1 - n0;
+
+  // Load plan per stage: 16 activation loads (1 KB = 4 tokens each), 4 dword
+  // loads of the token scales (block pair kp of 64 tokens each), 70 weight
+  // dword loads.  Wave w issues loads g = w + 8i: g < 16 activation,
+  // 16 <= g < 20 scales, then weights g - 20.  Rows past M / N repeat the
+  // last row.
+  auto act_off = [&](int c) {
+    const int q = 64 * c + lane, t = q >> 4, s = q & 15;
+    return (uint32_t)min(t, mlast) * xs + 16 * (uint32_t)(s ^ (t & 15));
+  };
+  auto w_off = [&](int k) {
+    const int q = 64 * k + lane, row = q / (kRowW / 4), part = q - (kRowW / 4) * row;
+    return (uint32_t)min(row, nlast) * ws_row + 4 * (uint32_t)min(part, 33);
+  };
+  const uint32_t va0 = act_off(wave), va1 = act_off(wave + 8);
+  const uint32_t v2 = wave < 4 ? (uint32_t)min(lane, mlast) * xs + (uint32_t)a.K + 4 * wave : w_off(wave - 4);
+  uint32_t vw[9];
+#pragma unroll
+  for (int i = 0; i < 9; ++i) vw[i] = w_off(min(wave + 8 * i + 4, kWLoads - 1));
+
+  auto issue = [&](int st) {
+    uint8_t* slot = lds + (st & 3) * kSlot;
+    const uint8_t* xb = xbase + 256 * (size_t)st;
+    const uint8_t* wb = wbase + 136 * (size_t)st;
+    dma16_s(xb, va0, __builtin_amdgcn_readfirstlane(lds_addr(slot + 1024 * wave)));
+    dma16_s(xb, va1, __builtin_amdgcn_readfirstlane(lds_addr(slot + 1024 * (wave + 8))));
+    if (wave < 4)
+      lds_dma4_s(xbase + 16 * (size_t)st, v2, __builtin_amdgcn_readfirstlane(lds_addr(slot + kSD + 256 * wave)));
+    else
+      lds_dma4_s(wb, v2, __builtin_amdgcn_readfirstlane(lds_addr(slot + kSW + 256 * (wave - 4))));
+#pragma unroll
+    for (int i = 0; i < 9; ++i)
+      if (i < 8 || wave < 2)
+        lds_dma4_s(wb, vw[i], __builtin_amdgcn_readfirstlane(lds_addr(slot + kSW + 256 * (wave + 8 * i + 4))));
+  };
+
+  float y[4][16];  // tile 2 * token half + column tile
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) y[q][r] = 0.f;
+  const v16f fzero = {};
+  const int x_scale = h ? 127 + 9 : 127 + 13;  // B block 0: hi plane (x16), block 1: lo plane
+
+  // blocks 2 ph and 2 ph + 1 of stage st
+  auto stage = [&](int st) {
+    const uint8_t* slot = lds + (st & 3) * kSlot;
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi) {
+      const int b = 2 * ph + bi;
+      // weight records b of rows 64 cp + 32 ct + col: e at byte 17b, then
+      // 16 nibble bytes, read as aligned dwords and shifted into place
+      const int off = kMxfp4Bytes * b;
+      const int b4 = (off + 1) & ~3, sh = (off + 1) & 3;
+      v8i wv[2];
+      int wsc[2];
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const uint8_t* wr = slot + kSW + kRowW * (64 * cp + 32 * ct + col);
+        const uint32_t w0 = ld32(wr + b4), w1 = ld32(wr + b4 + 4), w2 = ld32(wr + b4 + 8),
+                       w3 = ld32(wr + b4 + 12), w4 = ld32(wr + b4 + 16);
+        const uint32_t e = __builtin_amdgcn_ubfe(ld32(wr + (off & ~3)), 8 * (off & 3), 8);
+        // e = 255 (2^127 in GGML's table) has no E8M0 block-scale encoding;
+        // GGML's quantizer never produces it from finite weights
+        wsc[ct] = (int)min(e, 254u);
+        wv[ct] = v8i{(int)__builtin_amdgcn_alignbyte(w1, w0, sh), (int)__builtin_amdgcn_alignbyte(w2, w1, sh),
+                     (int)__builtin_amdgcn_alignbyte(w3, w2, sh), (int)__builtin_amdgcn_alignbyte(w4, w3, sh),
+                     0, 0, 0, 0};
+      }
+      v8i xv[2];
+      float dx[2];
+#pragma unroll
+      for (int th = 0; th < 2; ++th) {
+        const int t = 32 * th + col;
+        const uint4 raw = *reinterpret_cast<const uint4*>(slot + 256 * t + 16 * ((2 * b + h) ^ (col & 15)));
+        const uint32_t rw[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          xv[th][k] = (int)(((rw[k] >> 4) & 0x07070707u) | (rw[k] & 0x80808080u));
+          xv[th][4 + k] = (int)(rw[k] & 0x8f8f8f8fu);
+        }
+        dx[th] = (float)*reinterpret_cast<const _Float16*>(slot + kSD + 4 * (64 * (b >> 1) + t) + 2 * (b & 1));
+      }
+      // four independent MFMAs in flight, then y += dx * (ws * I)
+      v16f d[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        d[q] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wv[q & 1], xv[q >> 1], fzero, 4, 0, 0, wsc[q & 1], 0,
+                                                               x_scale);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) y[q][r] = fmaf(d[q][r], dx[q >> 1], y[q][r]);
+    }
+  };
+
+  // Two stages per barrier: the direct loads of the next pair go out right
+  // after the barrier, into the slots the previous pair used, so each wave
+  // waits for all of its own loads (vmcnt 0) at the top of a pair.
+  issue(0);
+  if (nst > 1) issue(1);
+  int st = 0;
+  for (; st + 1 < nst; st += 2) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();  // the pair is in for every wave; the previous pair's slots are free
+    if (st + 2 < nst) issue(st + 2);
+    if (st + 3 < nst) issue(st + 3);
+    stage(st);
+    stage(st + 1);
+  }
+  if (st < nst) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();
+    stage(st);
+  }
+
+  // partial sums of the four K phases -> LDS; wave (cp, p) finishes tile p
+  __syncthreads();
+  float4* red = reinterpret_cast<float4*>(lds);
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4)
+      red[((wave * 4 + q) * 4 + r4) * 64 + lane] =
+          make_float4(y[q][4 * r4], y[q][4 * r4 + 1], y[q][4 * r4 + 2], y[q][4 * r4 + 3]);
+  __syncthreads();
+  const int q = ph, th = q >> 1, ct = q & 1;
+  const int gm = m0 + 32 * th + col;
+  const bool v4 = (a.N & 3) == 0 && (reinterpret_cast<uintptr_t>(a.Y) & 15) == 0;
+#pragma unroll
+  for (int r4 = 0; r4 < 4; ++r4) {
+    float4 v = red[(((cp + 0) * 4 + q) * 4 + r4) * 64 + lane];
+#pragma unroll
+    for (int p2 = 1; p2 < 4; ++p2) {
+      const float4 u = red[(((cp + 2 * p2) * 4 + q) * 4 + r4) * 64 + lane];
+      v.x += u.x;
+      v.y += u.y;
+      v.z += u.z;
+      v.w += u.w;
+    }
+    // register r holds weight row 8*(r/4) + 4*h + r%4 of the tile
+    const int gn = n0 + 64 * cp + 32 * ct + 8 * r4 + 4 * h;
+    if (gm < a.M) {
+      float* yr = a.Y + (size_t)gm * a.N;
+      if (v4 && gn + 3 < a.N) {
+        *reinterpret_cast<float4*>(yr + gn) = v;
+      } else {
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (gn + k < a.N) yr[gn + k] = vv[k];
+      }
+    }
+  }
+}
+
+}  // namespace mx
+
+constexpr int kMxLds = mx::kLds > q80_lds_bytes<WFmt::MXFP4>() ? mx::kLds : q80_lds_bytes<WFmt::MXFP4>();
+
+// The block-scaled MFMA computes with GGML's tables; with any other tables
+// the workgroup runs the int8 body, which looks every value up.
+__global__ void __launch_bounds__(kThreads, 1) mxfp4_gemm(GemmArgs a) {
+  __shared__ __align__(16) uint8_t lds[kMxLds];
+  if (__syncthreads_and(ggml_mxfp4_entry(a.codebook, a.scale, threadIdx.x)))
+    mx::scaled_body(a, lds);
+  else
+    q80_gemm_body<WFmt::MXFP4>(a, lds);
 }
 
 template <WFmt F>
@@ -349,11 +671,16 @@ bool prefill_q80(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* co
   const long long xs = (long long)(K + K / 16);
   const long long waves = (nb + 7) / 8;
   const int grid = (int)std::max<long long>(1, std::min<long long>((long long)cu_count() * 8, (waves + 3) / 4));
-  q80_planar_kernel<<<grid, 256, 0, current_stream()>>>(X, Xq, nb, (int)(K / 32), xs);
+  q80_planar_kernel<F == WFmt::MXFP4>
+      <<<grid, 256, 0, current_stream()>>>(X, Xq, nb, (int)(K / 32), xs, codebook, scale);
   check_launch();
-  GemmArgs ga{W, Xq, codebook, scale, Y, (int)N, (int)K, (int)M};
   const size_t tiles = ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT);
-  q80_mfma_gemm<F><<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(ga);
+  GemmArgs ga{W, Xq, codebook, scale, Y, (int)N, (int)K, (int)M};
+  if constexpr (F == WFmt::MXFP4) {
+    mxfp4_gemm<<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(ga);
+  } else {
+    q80_mfma_gemm<F><<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(ga);
+  }
   check_launch();
   quantize_q8_0(X, Xq, M * K);  // Xq ends in GGML's record layout
   return true;
