@@ -18,12 +18,15 @@
 // Mn on one f16 MFMA per superblock and 32x32 tile.  Q8_K's 16 bsums are
 // sums of 16 int8 (|bsum| <= 2032 < 2^11) and the mins are 6-bit, so both
 // are exact f16 operands and v_mfma_f32_32x32x16_f16 (K = 16 = the bsums)
-// returns Mn exactly in fp32 (|Mn| <= 2.05e6 < 2^24).  Once per superblock
-// every output then takes
-//   D = (lo + 8 hi) - r * Mn,   y += (dx * f) * D
+// returns Mn exactly in fp32 (|Mn| <= 2.05e6 < 2^24).  The token scale times
+// the column scale, Q = dx * f, comes from one bf16 MFMA per tile as an outer
+// product: dx = h + m + l (three bf16, to 2^-24) against f = f_h + f_l (an
+// fp16 value is exactly two bf16), six exact products summed in fp32.  Once
+// per superblock every output then takes
+//   D = (lo + 8 hi) - r * Mn,   y += Q * D
 // with f = dw, r = dmin / dw; a superblock with dw == 0 zeroes its sc
-// operands (S = 0) and uses f = dmin, r = 1.  The rounding of D and of r
-// stays within 2^-22 of |dw S| + |dmin Mn|, far inside the tolerance.
+// operands (S = 0) and uses f = dmin, r = 1.  The rounding of D, r and Q
+// stays within 2^-21 of |dw S| + |dmin Mn|, far inside the tolerance.
 //
 // Tiling: a workgroup computes 64 (tokens) x 128 (weight rows) with 8 MFMA
 // waves and 2 loader waves.  MFMA waves 0-3 take the even superblocks and
@@ -32,17 +35,19 @@
 // next superblock pair into LDS by direct global->LDS loads
 // (global_load_lds_dwordx4, SGPR base + per-lane constant offset) while the
 // MFMA waves compute the current one, so no MFMA wave ever issues or waits on
-// a global memory instruction; one barrier per pair hands a filled ring slot
-// over.  The odd waves run their fp32 combine one superblock late, so on
-// every SIMD one wave's combine overlaps the other's MFMAs.  Odd partial sums
-// are added to the even waves' through LDS at the end: every output is
-// written once, in a fixed order.
+// a global memory instruction.  Once a pair has landed, each loader rewrites
+// its stage's per-token data in place, once for all four column groups: the
+// bsums become f16 and the token scale becomes the outer product's bf16
+// operand.  One barrier per pair hands the filled ring slots over.  Odd
+// partial sums are added to the even waves' through LDS at the end: every
+// output is written once, in a fixed order.
 //
 // LDS per superblock stage (38,912 B; 2 pairs = 4 stages):
 //   AQ  64 rows x 17 16-byte chunks: the 16 chunks of qs, then one pad chunk,
 //       so row r starts at 272 r and the 8 lanes of an A-operand read (8
 //       consecutive rows, one chunk) hit distinct banks with immediate offsets
-//   AX  64 rows x 3 chunks: record bytes [0,16) (d), [260,276), [276,292) (bsums)
+//   AX  64 rows x 3 chunks: record bytes [0,16) (d), [260,276), [276,292)
+//       (bsums), rewritten in place as described above
 //   WT  128 rows x the 144-byte Q4_K record
 // The activation is quantized first, into the caller's Xq, by q8_K_quantize's
 // kernel (Xq is part of the ABI), then read back from L2.
@@ -88,13 +93,6 @@ struct GemmArgs {
   int N, K, M;
 };
 
-__device__ __forceinline__ uint32_t mul_bytes(uint32_t packed, uint32_t c) {
-  // four bytes (each <= 15) times c (<= 7): no byte overflows into the next
-  v2u16 v = __builtin_bit_cast(v2u16, packed);
-  v2u16 r = v * (v2u16){(unsigned short)c, (unsigned short)c};
-  return __builtin_bit_cast(uint32_t, r);
-}
-
 // Direct global->LDS load of 16 bytes per lane: lane l reads sbase + voff
 // and writes LDS bytes [lds + 16 l, lds + 16 l + 16) (lds wave-uniform).
 // Inline asm: the loader waves wait for these loads themselves (s_waitcnt
@@ -126,17 +124,24 @@ __device__ __forceinline__ uint32_t dup_byte_f16x2(uint32_t w, int i) {
   return __builtin_bit_cast(uint32_t, h);
 }
 
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+// fp32 -> two bf16 (round to nearest even) packed low | high << 16
+__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
+  typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+  const v2bf v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ float bf16_lo_to_f32(uint32_t p) { return __uint_as_float(p << 16); }
+
 __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
   __shared__ __align__(16) uint8_t ring[4 * kStage];  // [pair slot][parity]
-  __shared__ __align__(16) float dxr[8 * 2 * 64];     // per wave, 2 slots, 64 token scales
+  __shared__ __align__(16) uint32_t zero16[4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
-  // Workgroups are dealt round-robin to the 8 XCDs (linear id % 8), each with
-  // its own L2.  Give XCD x a contiguous run of tiles, ordered token-tile
-  // fastest, so the workgroups resident on one XCD share weight rows and
-  // the whole activation block while they sweep K together.
+  if (tid < 4) zero16[tid] = 0u;
   int m0, n0;
   {
     const int ntm = (a.M + kMT - 1) / kMT;
@@ -153,9 +158,6 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
 
   if (wave >= kMfmaWaves) {
     // ---------------------------------------------------------- loader wave
-    // Loader P stages superblock 2*pair + P: slot k of the stage is LDS bytes
-    // [1024k, 1024k + 1024), lane l the 16 bytes at 1024k + 16l.  voff[k] is
-    // this lane's source offset from the tile base of superblock 0.
     const int par = wave - kMfmaWaves;
     const uint32_t wrb = (uint32_t)nsb * kQ4_KBytes;
     const uint32_t xrb = (uint32_t)nsb * kQ8_KBytes;
@@ -187,9 +189,31 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
         lds_dma16(k < kAQSlots + kAXSlots ? xb : wb, voff[k],
                   __builtin_amdgcn_readfirstlane(lds_addr(stage + 1024 * k)));
     };
+    // In place in the landed stage, token t = lane: the 16 bsums become f16
+    // (min-term A operand) and the 16-byte d chunk becomes the token-scale
+    // operand of the dx (x) dw outer product: bf16 pairs (h,h), (m,m), (l,l),
+    // 0 with d = h + m + l to 2^-24.
+    auto convert = [&](int pair) {
+      uint8_t* ax = ring + (2 * (pair & 1) + par) * kStage + kAQ + 48 * lane;
+      const uint4 dch = *reinterpret_cast<const uint4*>(ax);
+      const uint4 b0 = *reinterpret_cast<const uint4*>(ax + 16);
+      const uint4 b1 = *reinterpret_cast<const uint4*>(ax + 32);
+      const float d = __uint_as_float(dch.x);
+      const uint32_t ph = pk_bf16(d, d);
+      const float r1 = d - bf16_lo_to_f32(ph);
+      const uint32_t pm = pk_bf16(r1, r1);
+      const float r2 = r1 - bf16_lo_to_f32(pm);
+      const uint32_t pl = pk_bf16(r2, r2);
+      *reinterpret_cast<uint4*>(ax) = make_uint4(ph, pm, pl, 0u);
+      *reinterpret_cast<uint4*>(ax + 16) =
+          make_uint4(i16x2_to_f16x2(b0.x), i16x2_to_f16x2(b0.y), i16x2_to_f16x2(b0.z), i16x2_to_f16x2(b0.w));
+      *reinterpret_cast<uint4*>(ax + 32) =
+          make_uint4(i16x2_to_f16x2(b1.x), i16x2_to_f16x2(b1.y), i16x2_to_f16x2(b1.z), i16x2_to_f16x2(b1.w));
+    };
     issue(0);
     for (int pair = 0; pair < npair; ++pair) {
       __builtin_amdgcn_s_waitcnt(0);  // this pair's stage has landed
+      convert(pair);
       __syncthreads();                // hand it over; the slot of pair - 1 is free
       if (pair + 1 < npair) issue(pair + 1);
     }
@@ -201,45 +225,19 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
   // ------------------------------------------------------------ MFMA wave
   const int par = wave >> 2, wcol = wave & 3;  // superblock parity, column group
   const int col = lane & 31, kg = lane >> 5;
+  const uint32_t zaddr = lds_addr(zero16);
 
   v16i lo[2], hi[2];
-  v16f y[2], mn[2];
+  v16f y[2];
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int r = 0; r < 16; ++r) y[t][r] = 0.f;
 
-  // y[t] += dx[row] * f * (lo + 8 hi - r Mn); D[i][j] of a 32x32 tile lives
-  // in lane j (+32 for the odd 4-row groups), register r holds row
-  // 8*(r/4) + 4*kg + r%4
-  auto combine = [&](float f, float nr, const float* dxs) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const float4 d4 = *reinterpret_cast<const float4*>(dxs + 32 * t + 8 * r4 + 4 * kg);
-        const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int r = 4 * r4 + q;
-          const float d = fmaf(mn[t][r], nr, (float)(lo[t][r] + 8 * hi[t][r]));
-          y[t][r] = fmaf(d, dv[q] * f, y[t][r]);
-        }
-      }
-    }
-  };
-
   const v16i zero = {};
   const v16f fzero = {};
-  bool pending = false;     // odd waves: a combine is owed from the previous pair
-  float f_prev = 0.f, nr_prev = 0.f;
   for (int pair = 0; pair < npair; ++pair) {
-    __syncthreads();  // the loaders have staged this pair; the previous pair is consumed
-    float* dxs = dxr + (2 * wave + (pair & 1)) * 64;
-    if (pending) {  // odd waves: combine of the previous superblock
-      combine(f_prev, nr_prev, dxr + (2 * wave + ((pair - 1) & 1)) * 64);
-      pending = false;
-    }
+    __syncthreads();  // the loaders have staged and converted this pair
     if (2 * pair + par >= nsb) continue;  // odd nsb: the last pair has one superblock
     const uint8_t* stage = ring + (2 * (pair & 1) + par) * kStage;
     const uint8_t* AQ = stage + kAQRow * col + 16 * kg;          // + 8704 t + 32 s
@@ -254,20 +252,28 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
     const uint32_t sc47 = dz ? 0u : (h.w & 0x0f0f0f0fu) | (((h.y >> 6) & 0x03030303u) << 4);
     const float f = dz ? dmin : dw;
     const float nr = dz ? -1.f : -(dmin * __builtin_amdgcn_rcpf(dw));
+    // per sub-block pair, the b (= sc & 7) and a (= sc >> 3) multipliers in
+    // the two 16-bit halves of one register
+    uint32_t cb[4], ca[4];
+    {
+      const uint32_t b03 = sc03 & 0x07070707u, a03 = (sc03 >> 3) & 0x07070707u;
+      const uint32_t b47 = sc47 & 0x07070707u, a47 = (sc47 >> 3) & 0x07070707u;
+      cb[0] = __builtin_amdgcn_perm(0u, b03, 0x0c010c00u);
+      cb[1] = __builtin_amdgcn_perm(0u, b03, 0x0c030c02u);
+      cb[2] = __builtin_amdgcn_perm(0u, b47, 0x0c010c00u);
+      cb[3] = __builtin_amdgcn_perm(0u, b47, 0x0c030c02u);
+      ca[0] = __builtin_amdgcn_perm(0u, a03, 0x0c010c00u);
+      ca[1] = __builtin_amdgcn_perm(0u, a03, 0x0c030c02u);
+      ca[2] = __builtin_amdgcn_perm(0u, a47, 0x0c010c00u);
+      ca[3] = __builtin_amdgcn_perm(0u, a47, 0x0c030c02u);
+    }
 
-    // token scales for the combine (this wave only)
-    dxs[32 * kg + col] = *reinterpret_cast<const float*>(AX + 1536 * kg);
-
-    // A operands (activation rows, 16 bytes per lane) run one sub-block ahead
-    // of their MFMAs, so no MFMA waits on an LDS read issued just before it
     v4i acur[2], anxt[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) acur[t] = *reinterpret_cast<const v4i*>(AQ + 32 * kAQRow * t);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      // 16 qs bytes: elements 64g + 16kg + i (low nibble) and 64g + 32 + 16kg + i (high)
       const uint4 q = *reinterpret_cast<const uint4*>(wrow + 16 + 32 * g + 16 * kg);
-      const uint32_t scw = g < 2 ? sc03 : sc47;
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
         const int s = 2 * g + hf;
@@ -276,16 +282,19 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
           for (int t = 0; t < 2; ++t)
             anxt[t] = *reinterpret_cast<const v4i*>(AQ + 32 * kAQRow * t + 32 * (s + 1));
         }
-        const uint32_t sc = (scw >> (8 * (s & 3))) & 0xffu;
         const uint32_t n0w = hf ? (q.x >> 4) & 0x0f0f0f0fu : q.x & 0x0f0f0f0fu;
         const uint32_t n1w = hf ? (q.y >> 4) & 0x0f0f0f0fu : q.y & 0x0f0f0f0fu;
         const uint32_t n2w = hf ? (q.z >> 4) & 0x0f0f0f0fu : q.z & 0x0f0f0f0fu;
         const uint32_t n3w = hf ? (q.w >> 4) & 0x0f0f0f0fu : q.w & 0x0f0f0f0fu;
-        const uint32_t cb = sc & 7u, ca = sc >> 3;
-        const v4i b_lo = {(int)mul_bytes(n0w, cb), (int)mul_bytes(n1w, cb), (int)mul_bytes(n2w, cb),
-                          (int)mul_bytes(n3w, cb)};
-        const v4i b_hi = {(int)mul_bytes(n0w, ca), (int)mul_bytes(n1w, ca), (int)mul_bytes(n2w, ca),
-                          (int)mul_bytes(n3w, ca)};
+        const v2u16 pb = __builtin_bit_cast(v2u16, cb[s >> 1]);
+        const v2u16 pa = __builtin_bit_cast(v2u16, ca[s >> 1]);
+        const v2u16 mb = (s & 1) ? __builtin_shufflevector(pb, pb, 1, 1) : __builtin_shufflevector(pb, pb, 0, 0);
+        const v2u16 ma = (s & 1) ? __builtin_shufflevector(pa, pa, 1, 1) : __builtin_shufflevector(pa, pa, 0, 0);
+        auto mul = [](uint32_t n, v2u16 m) {
+          return (int)__builtin_bit_cast(uint32_t, __builtin_bit_cast(v2u16, n) * m);
+        };
+        const v4i b_lo = {mul(n0w, mb), mul(n1w, mb), mul(n2w, mb), mul(n3w, mb)};
+        const v4i b_hi = {mul(n0w, ma), mul(n1w, ma), mul(n2w, ma), mul(n3w, ma)};
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           lo[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(acur[t], b_lo, s == 0 ? zero : lo[t], 0, 0, 0);
@@ -296,31 +305,38 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
       }
     }
 
-    // min term: bsums j = 8 kg .. 8 kg + 7 of each token against m[j / 2]
+    // min term (f16: converted bsums x duplicated mins) and the dx (x) f
+    // outer product (bf16: token-scale splits x f = f_h + f_l, exact)
+    v16f mn[2], qd[2];
     {
       const uint32_t mn03 = h.z & 0x3f3f3f3fu;
       const uint32_t mn47 = ((h.w >> 4) & 0x0f0f0f0fu) | (((h.z >> 6) & 0x03030303u) << 4);
       const uint32_t mw = kg ? mn47 : mn03;
       const v4i bm = {(int)dup_byte_f16x2(mw, 0), (int)dup_byte_f16x2(mw, 1),
                       (int)dup_byte_f16x2(mw, 2), (int)dup_byte_f16x2(mw, 3)};
+      const uint32_t pfh = pk_bf16(f, f);
+      const uint32_t pf = kg ? 0u : pk_bf16(f, f - bf16_lo_to_f32(pfh));
+      const v4i bq = {(int)pf, (int)pf, (int)pf, 0};
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const uint4 bs = *reinterpret_cast<const uint4*>(AX + 1536 * t + 16 + 16 * kg);
-        const v4i am = {(int)i16x2_to_f16x2(bs.x), (int)i16x2_to_f16x2(bs.y),
-                        (int)i16x2_to_f16x2(bs.z), (int)i16x2_to_f16x2(bs.w)};
+        const v4i am = *reinterpret_cast<const v4i*>(AX + 1536 * t + 16 + 16 * kg);
         mn[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, am),
                                                       __builtin_bit_cast(v8h, bm), fzero, 0, 0, 0);
+        const uint32_t qaddr = kg ? zaddr : lds_addr(AX + 1536 * t);
+        const v4i aq = *(const __attribute__((address_space(3))) v4i*)(size_t)qaddr;
+        qd[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aq),
+                                                       __builtin_bit_cast(v8bf, bq), fzero, 0, 0, 0);
       }
     }
-    if (par == 0) {
-      combine(f, nr, dxs);
-    } else {
-      pending = true;
-      f_prev = f;
-      nr_prev = nr;
-    }
+    // y += (dx f) (lo + 8 hi - r Mn)
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float d = fmaf(mn[t][r], nr, (float)(lo[t][r] + 8 * hi[t][r]));
+        y[t][r] = fmaf(d, qd[t][r], y[t][r]);
+      }
   }
-  if (pending) combine(f_prev, nr_prev, dxr + (2 * wave + ((npair - 1) & 1)) * 64);
 
   // odd-parity partial sums -> LDS (reusing the stages) -> even waves
   __syncthreads();

@@ -25,11 +25,12 @@ __device__ __forceinline__ float4 ldx4(const float* p, bool a16) {
 }
 
 // 16 lanes per superblock (q8k_quantize_16lanes): lane part p holds bsum
-// group p, a wave quantizes four superblocks per pass; both passes' loads are
-// issued before the first is quantized.
+// group p, a wave quantizes four superblocks per pass.  The grid gives each
+// wave one pass (two waves per SIMD for a prefill-sized activation): with a
+// single wave per SIMD the quantization arithmetic issues at half the rate.
 __global__ void __launch_bounds__(kThreads) q8k_quantize_kernel(const float* __restrict__ X,
                                                                 uint8_t* __restrict__ Y, long long nb) {
-  constexpr int U = 2;  // passes in flight per wave
+  constexpr int U = 1;  // passes in flight per wave
   const int lane = threadIdx.x & (kWave - 1);
   const int part = lane & 15;
   const long long wave = ((long long)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
@@ -98,7 +99,9 @@ void quantize_q8_k(const float* X, uint8_t* Y, size_t K) {
   if (K % 256 || X == nullptr || Y == nullptr || !aligned(X, 4) || !aligned(Y, 4))
     return set_error(hipErrorInvalidValue);
   const long long nb = (long long)(K / 256);
-  q8k_quantize_kernel<<<grid_for((nb + 7) / 8), kThreads, 0, current_stream()>>>(X, Y, nb);
+  // one pass (four superblocks) per wave, four waves per workgroup
+  const long long blocks = std::max<long long>(1, (nb + 15) / 16);
+  q8k_quantize_kernel<<<(int)std::min<long long>(blocks, INT32_MAX), kThreads, 0, current_stream()>>>(X, Y, nb);
   check_launch();
 }
 
