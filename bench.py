@@ -50,6 +50,9 @@ CASES = {
     "iq2_xxs_decode": ("production_mul_mat_iq2_xxs_decode", "iq2_xxs", 4096, 4096, 1, "hbm"),
     "mxfp4_decode": ("production_mul_mat_mxfp4_decode", "mxfp4", 4096, 4096, 1, "hbm"),
     "q4_k_dequant": ("row_dequantize_q4_k", "q4_k", 11008, 4096, 0, "hbm"),
+    # Q4K_I[16] GEMV at the reference harness's shape (q4_k_gemv_runtime.cpp:77-78);
+    # N is the row count M of that ABI, the activation is pre-quantized Q8_K
+    "q4_k_gemv_interleaved": ("q4_k_q8_k_gemv", "q4_k", 14336, 4096, -1, "hbm"),
     "q4_k_prefill_n4096": ("production_mul_mat_q4_k_staged", "q4_k", 4096, 4096, 512, "mfma"),
     "q4_k_prefill_n11008": ("production_mul_mat_q4_k_staged", "q4_k", 11008, 4096, 512, "mfma"),
     "mxfp4_prefill": ("production_mul_mat_mxfp4", "mxfp4", 4096, 4096, 512, "mfma"),
@@ -149,6 +152,21 @@ def run_case(b: Bench, name: str, steps: int, warmup: int) -> dict:
             fn(wd[i % copies].data_ptr(), y.data_ptr(), n * k)
 
         nbytes = w.nbytes + 4 * n * k
+    elif m < 0:  # GEMV over the Q4K_I[16] layout: pack every copy once, outside the timing
+        packed = [torch.empty_like(t) for t in wd]
+        pack = getattr(b.lib, sym + "_W_pack")
+        for src, dst in zip(wd, packed):
+            pack(src.data_ptr(), dst.data_ptr(), n, k)
+        torch.cuda.synchronize()
+        b._lib.check(sym + "_W_pack")
+        wd = packed
+        xq = b.dev_copy(o.quantize("q8_k", o.seeded_normal(2, (1, k))))
+        y = torch.empty(n, dtype=torch.float32, device=b.dev)
+
+        def launch(i):
+            fn(wd[i % copies].data_ptr(), xq.data_ptr(), y.data_ptr(), n, k)
+
+        nbytes = w.nbytes + xq.numel() + 4 * n
     else:
         act = o.ACT_OF[fmt]
         x = b.dev_copy(o.seeded_normal(2, (m, k)))
@@ -165,7 +183,7 @@ def run_case(b: Bench, name: str, steps: int, warmup: int) -> dict:
     sec = b.time_calls(launch, steps, warmup)
     del wd
     torch.cuda.empty_cache()
-    out = {"symbol": sym, "N": n, "K": k, "M": m, "us": round(sec * 1e6, 3),
+    out = {"symbol": sym, "N": n, "K": k, "M": max(m, 1) if m < 0 else m, "us": round(sec * 1e6, 3),
            "algorithmic_bytes": int(nbytes), "GBs": round(nbytes / sec / 1e9, 2),
            "weight_copies_rotated": copies, "steps": steps}
     if bound == "hbm":

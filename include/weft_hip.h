@@ -128,6 +128,31 @@ void production_mul_mat_mxfp4_decode(const uint8_t *W, const float *X, uint8_t *
                                      const int8_t *codebook, const float *scale, float *Y,
                                      size_t N, size_t K, size_t M);
 
+/* ------------------------------- Q4_K GEMV over the Q4K_I[16] layout */
+/* W is the persisted 16-row interleave of an M x K Q4_K matrix (M a multiple
+ * of 16; examples/formats/ggml.py:286-290): superblock j of rows 16c..16c+15
+ * is the 2304-byte block ((c * K/256) + j) * 2304 whose byte 16 b + r is byte
+ * b of row 16 c + r's record (lib/Target/Emission/Memory.cpp:984-991).  X is
+ * K/256 Q8_K records, Y gets M fp32.  _W_packed_size / _W_pack are the
+ * artifact-phase functions Emitter::emitArtifact generates for the derived W
+ * (lib/Target/Emission/Emitter.h:231-272): sizes in bytes, and a device-side
+ * repack from a row-major Q4_K matrix (source and target are device pointers,
+ * target 16-byte aligned).  The _groups4 and _contract variants are the same
+ * function (the reference's RVV loop orders of one DSL computation). */
+
+/* examples/kernels/gemv/q4_k.py:8-26; repro q4_k_gemv_runtime.cpp:28-32 */
+size_t q4_k_q8_k_gemv_W_packed_size(size_t M, size_t K);
+void q4_k_q8_k_gemv_W_pack(const uint8_t *source, uint8_t *target, size_t M, size_t K);
+void q4_k_q8_k_gemv(const uint8_t *W, const uint8_t *X, float *Y, size_t M, size_t K);
+/* examples/kernels/gemv/q4_k_groups4.py; repro q4_k_gemv_runtime.cpp:20-26 */
+size_t q4_k_q8_k_gemv_groups4_W_packed_size(size_t M, size_t K);
+void q4_k_q8_k_gemv_groups4_W_pack(const uint8_t *source, uint8_t *target, size_t M, size_t K);
+void q4_k_q8_k_gemv_groups4(const uint8_t *W, const uint8_t *X, float *Y, size_t M, size_t K);
+/* examples/kernels/gemv/q4_k_contract.py; repro q4_k_gemv_runtime.cpp:13-18 */
+size_t q4_k_q8_k_gemv_contract_W_packed_size(size_t M, size_t K);
+void q4_k_q8_k_gemv_contract_W_pack(const uint8_t *source, uint8_t *target, size_t M, size_t K);
+void q4_k_q8_k_gemv_contract(const uint8_t *W, const uint8_t *X, float *Y, size_t M, size_t K);
+
 #ifdef __cplusplus
 }
 #endif

@@ -224,6 +224,19 @@ def int_partials(fmt: str, w: np.ndarray, x: np.ndarray, k: int) -> np.ndarray:
     return out[:n].copy()
 
 
+def interleave_rows(w: np.ndarray, n: int, k: int, rows: int = 16) -> np.ndarray:
+    """The derived layout Q4K_I[rows] of an n x k Q4_K matrix
+    (examples/formats/ggml.py:286-290): each ``rows``-row cohort is written
+    byte-major per record (doc/dsl/encoding-and-artifacts.md:209), cohort
+    superblock j at ((c * nsb) + j) * 144 * rows, byte b of row r at
+    16 b + r (lib/Target/Emission/Memory.cpp:984-991)."""
+    nsb = k // 256
+    if n % rows or k % 256:
+        raise ValueError("Q4K_I needs whole row cohorts and whole superblocks")
+    src = np.ascontiguousarray(w, dtype=np.uint8).reshape(n // rows, rows, nsb, 144)
+    return np.ascontiguousarray(src.transpose(0, 2, 3, 1)).reshape(-1)
+
+
 def max_threads() -> int:
     return int(lib().wo_max_threads())
 

@@ -37,8 +37,14 @@ def test_every_header_function_is_exported():
     assert not missing
 
 
+def artifact_phase(name: str) -> bool:
+    # <symbol>_W_packed_size / <symbol>_W_pack: the artifact functions of a
+    # derived weight layout (lib/Target/Emission/Emitter.h:231-272), not kernels
+    return name.endswith("_W_packed_size") or name.endswith("_W_pack")
+
+
 def test_artifact_covers_every_kernel_in_the_header():
-    funcs = {k for k in header_functions() if not k.startswith("weft_hip_")}
+    funcs = {k for k in header_functions() if not k.startswith("weft_hip_") and not artifact_phase(k)}
     kernels = {k["symbol"] for k in _lib.artifact()["kernels"]}
     assert funcs == kernels
 
@@ -70,6 +76,31 @@ def test_decode_kernels_declare_workspace_and_output_groups():
         assert (args["W"]["alias_set"], args["Xq"]["alias_set"], args["Y"]["alias_set"]) == (0, 1, 2)
     args = {a["name"]: a for a in _lib.kernel_metadata("production_mul_mat_q4_0_decode")["arguments"]}
     assert {a["alias_set"] for a in args.values()} == {0}
+
+
+def test_artifact_phase_functions_pair_with_their_kernels():
+    funcs = header_functions()
+    for name, params in funcs.items():
+        if name.endswith("_W_packed_size"):
+            kernel = name[:-len("_W_packed_size")]
+            assert kernel in funcs and kernel + "_W_pack" in funcs
+            assert [p.split()[-1] for p in params] == ["M", "K"]
+            assert [p.split()[-1] for p in funcs[kernel + "_W_pack"]] == ["*source", "*target", "M", "K"]
+
+
+def test_packed_size_is_computed_on_the_host():
+    import ctypes
+    lib = _lib.load()
+    fn = lib.q4_k_q8_k_gemv_W_packed_size
+    fn.restype = ctypes.c_size_t
+    fn.argtypes = [ctypes.c_size_t, ctypes.c_size_t]
+    assert fn(14336, 4096) == 14336 * 16 * 144
+    assert lib.weft_hip_get_last_error() == 0
+    # rows must form whole 16-row cohorts, K whole superblocks
+    assert fn(14330, 4096) == 0
+    assert lib.weft_hip_get_last_error() != 0
+    assert fn(32, 300) == 0
+    assert lib.weft_hip_get_last_error() != 0
 
 
 def test_invalid_call_records_an_error_without_a_device():

@@ -359,3 +359,39 @@ def test_q4_0_quantizer_error_is_half_a_step():
     err = np.abs(o.dequantize("q4_0", q, 32).astype(np.float64) - w.reshape(-1, 32))
     # the block maximum maps to -8 exactly; the +7 clamp side may lose up to a full step
     assert (err <= d[:, None] * 1.001 + 1e-7).all()
+
+
+# ------------------------------------------------ Q4K_I[16] interleave layout
+def test_interleave_matches_the_reference_record_address():
+    """oracle.interleave_rows against the record pointer the reference's
+    emitter generates for a derived interleave (lib/Target/Emission/
+    Memory.cpp:984-991: ((row / R) * blocks + block) * (144 * R) + row % R,
+    bytes at stride R), evaluated element by element."""
+    rows, n, k = 16, 48, 768
+    nsb = k // 256
+    rng = np.random.default_rng(5)
+    w = rng.integers(0, 256, size=n * nsb * 144, dtype=np.uint8)
+    packed = o.interleave_rows(w, n, k, rows)
+    assert packed.shape == w.shape
+    src = w.reshape(n, nsb, 144)
+    for row in range(n):
+        for block in range(nsb):
+            record = ((row // rows) * nsb + block) * (144 * rows) + row % rows
+            got = packed[record + rows * np.arange(144)]
+            np.testing.assert_array_equal(got, src[row, block])
+
+
+def test_interleave_known_answer_and_inverse():
+    # byte b of row r of superblock j holds (r + 7 j + 13 b) % 256: spot
+    # positions, then the permutation is a bijection with a known inverse
+    n, k = 32, 512
+    r, j, b = np.meshgrid(np.arange(n), np.arange(k // 256), np.arange(144), indexing="ij")
+    w = ((r + 7 * j + 13 * b) % 256).astype(np.uint8).reshape(-1)
+    p = o.interleave_rows(w, n, k)
+    assert p[0] == 0 and p[1] == 1 and p[16] == 13           # rows 0, 1 byte 0; row 0 byte 1
+    assert p[2304] == 7                                       # cohort 0, superblock 1, row 0, byte 0
+    assert p[2 * 2304 + 16 * 143 + 15] == (16 + 15 + 13 * 143) % 256  # cohort 1, superblock 0
+    back = p.reshape(n // 16, k // 256, 144, 16).transpose(0, 3, 1, 2).reshape(-1)
+    np.testing.assert_array_equal(back, w)
+    with pytest.raises(ValueError):
+        o.interleave_rows(w[: 30 * 2 * 144], 30, k)

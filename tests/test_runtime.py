@@ -160,3 +160,17 @@ def test_buffer_inference_and_contiguity():
         Buffer(FakeDev(1 << 20, (8,), "|V8"))
     with pytest.raises(ValueError):
         Buffer(np.zeros(4, np.uint8), shape=(-1,), encoding="Q4_0")
+
+
+def test_interleaved_weights_need_whole_row_cohorts():
+    fn = compiled("q4_k_q8_k_gemv")
+    k = 512
+    X = Buffer(FakeDev(2 << 20, (2 * 292,)), shape=(k,), encoding="Q8_K")
+    Y = Buffer(FakeDev(3 << 20, (24,), "<f4"))
+    W = Buffer(FakeDev(1 << 20, (24 * 288,)), shape=(24, k), encoding="Q4K_I[16]")
+    with pytest.raises(ValueError, match="16-row cohorts"):
+        fn(W, X, Y)
+    # the layout identity is checked like any Encoding
+    W = Buffer(FakeDev(1 << 20, (32 * 288,)), shape=(32, k), encoding="Q4_K")
+    with pytest.raises(TypeError, match="requires Q4K_I"):
+        fn(W, X, Buffer(FakeDev(3 << 20, (32,), "<f4")))

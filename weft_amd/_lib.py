@@ -66,6 +66,15 @@ def load() -> ctypes.CDLL:
                 fn.argtypes = ([ctypes.c_void_p] * len(kernel["arguments"]) +
                                [ctypes.c_size_t] * len(kernel["shape_parameters"]))
                 fn.restype = None
+                # artifact-phase functions of a derived weight layout
+                # (lib/Target/Emission/Emitter.h:231-272)
+                if hasattr(lib, kernel["symbol"] + "_W_pack"):
+                    size = getattr(lib, kernel["symbol"] + "_W_packed_size")
+                    size.argtypes = [ctypes.c_size_t, ctypes.c_size_t]
+                    size.restype = ctypes.c_size_t
+                    pack = getattr(lib, kernel["symbol"] + "_W_pack")
+                    pack.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t]
+                    pack.restype = None
             _artifact = artifact
             _lib = lib
         return _lib

@@ -126,7 +126,8 @@ const EncodingInfo kEncodings[] = {
     {"Q4_0", "uint8_t", 18, 32, 2},      {"Q4_K", "uint8_t", 144, 256, 2},
     {"Q8_0", "uint8_t", 34, 32, 2},      {"Q8_K", "uint8_t", 292, 256, 4},
     {"IQ2_XXS", "uint8_t", 66, 256, 2},  {"MXFP4", "uint8_t", 17, 32, 1},
-    {"I8X8", "uint8_t", 8, 8, 8},        {"dense.f32", "float", 4, 1, 4},
+    {"I8X8", "uint8_t", 8, 8, 8},        {"Q4K_I[16]", "uint8_t", 144, 256, 16},
+    {"dense.f32", "float", 4, 1, 4},
     {"dense.i8", "int8_t", 1, 1, 1},
 };
 
@@ -213,6 +214,12 @@ std::vector<KernelSpec> kernel_specs() {
   mm("production_mul_mat_iq2_xxs_staged", "IQ2_XXS", "Q8_K", true, iq2);
   mm("production_mul_mat_mxfp4", "MXFP4", "Q8_0", false, mx);
   mm("production_mul_mat_mxfp4_decode", "MXFP4", "Q8_0", true, mx);
+  for (const char* sym : {"q4_k_q8_k_gemv", "q4_k_q8_k_gemv_groups4", "q4_k_q8_k_gemv_contract"})
+    k.push_back({sym,
+                 {{"W", "Q4K_I[16]", "M,K", false, nullptr},
+                  {"X", "Q8_K", "K", false, nullptr},
+                  {"Y", "dense.f32", "M", true, nullptr}},
+                 "M,K"});
   return k;
 }
 

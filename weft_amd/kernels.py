@@ -78,6 +78,9 @@ _DEFS = [
     ("production_mul_mat_mxfp4", _MM_MX, "examples/kernels/mul_mat/mxfp4.py:10-35", None),
     ("production_mul_mat_mxfp4_decode", _MM_MX, "examples/kernels/mul_mat/mxfp4_decode.py:10-23",
      _DECODE_GROUPS),
+    ("q4_k_q8_k_gemv", ("W", "X", "Y"), "examples/kernels/gemv/q4_k.py:8-26", None),
+    ("q4_k_q8_k_gemv_groups4", ("W", "X", "Y"), "examples/kernels/gemv/q4_k_groups4.py:8-26", None),
+    ("q4_k_q8_k_gemv_contract", ("W", "X", "Y"), "examples/kernels/gemv/q4_k_contract.py:8-26", None),
 ]
 
 DEFINITIONS: dict[str, KernelDefinition] = {}

@@ -25,6 +25,15 @@ from .buffer import Buffer
 from .driver import CompilationError, HipTarget, Toolchain
 
 
+def _interleave_rows(encoding: str) -> int:
+    """Cohort size of a derived row-interleave encoding such as ``Q4K_I[16]``
+    (examples/formats/ggml.py:286-290), 0 for any other encoding."""
+    head, sep, tail = encoding.partition("_I[")
+    if not sep or not head or not tail.endswith("]") or not tail[:-1].isdecimal():
+        return 0
+    return int(tail[:-1])
+
+
 def _freeze(value):
     if isinstance(value, dict):
         return MappingProxyType({key: _freeze(item) for key, item in value.items()})
@@ -126,6 +135,11 @@ class CompiledKernel:
                 elements = parameter["record_elements"]
                 if buffer.shape and buffer.shape[-1] % elements:
                     raise ValueError(f"{parameter['name']} does not contain complete Encoding records")
+                cohort = _interleave_rows(parameter["encoding"])
+                if cohort and buffer.shape and buffer.shape[0] % cohort:
+                    # the interleave builder needs whole row cohorts
+                    # (doc/dsl/encoding-and-artifacts.md:209)
+                    raise ValueError(f"{parameter['name']} rows are not whole {cohort}-row cohorts")
                 required = math.prod(buffer.shape) // elements * parameter["storage_bytes"]
                 if required > buffer.nbytes:
                     raise ValueError(f"{parameter['name']} storage is shorter than its logical View")
