@@ -45,10 +45,10 @@ typedef __attribute__((address_space(3))) v2i lds_v2i;
 
 constexpr int kCohort = 16;                          // rows per interleaved cohort
 constexpr int kBlock = kCohort * kQ4_KBytes;          // 2304 bytes per cohort superblock
-constexpr int kWaves = 4;                             // waves per workgroup (K split)
-constexpr int kThreads = 64 * kWaves;
-constexpr int kRing = 4;                              // blocks per wave in LDS
-constexpr int kRingBytes = kWaves * kRing * kBlock;   // 36864
+// Blocks per wave in LDS: one being computed, one in flight.  Deeper rings
+// measured slower on this chip (more requests in flight per wave queue in
+// front of the ones needed next); parallelism comes from waves instead.
+constexpr int kRing = 2;
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(lds_ptr)p;
@@ -77,6 +77,19 @@ __device__ __forceinline__ v2i tr8(const uint8_t* base, uint32_t offset) {
   return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)((lds_u8*)base + offset));
 }
 
+// s_waitcnt for "at most n younger blocks (3 loads each) still in flight"
+__device__ __forceinline__ void wait_blocks_younger(int n) {
+  switch (n) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+    case 3: asm volatile("s_waitcnt vmcnt(9)" ::: "memory"); break;
+    case 4: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
+    case 5: asm volatile("s_waitcnt vmcnt(15)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(18)" ::: "memory"); break;
+  }
+}
+
 struct GemvArgs {
   const uint8_t* W;   // packed Q4K_I[16]
   const uint8_t* X;   // Q8_K records
@@ -84,7 +97,11 @@ struct GemvArgs {
   int M, K;
 };
 
-__global__ void __launch_bounds__(kThreads) q4k_i16_gemv_kernel(GemvArgs a) {
+// kWaves waves per workgroup split the cohort's superblocks round-robin.
+template <int kWaves>
+__global__ void __launch_bounds__(64 * kWaves) q4k_i16_gemv_kernel(GemvArgs a) {
+  constexpr int kThreads = 64 * kWaves;
+  constexpr int kRingBytes = kWaves * kRing * kBlock;
   extern __shared__ __align__(16) uint8_t lds[];
   const int nsb = a.K >> 8;
   uint8_t* ring = lds;                                                // [wave][kRing][2304]
@@ -138,14 +155,9 @@ __global__ void __launch_bounds__(kThreads) q4k_i16_gemv_kernel(GemvArgs a) {
 
   float acc = 0.f;
   for (int i = 0; i < my; ++i) {
-    // block i has landed once only the (at most two) younger blocks' loads
-    // are outstanding: three loads per block, in order
-    if (my - i >= kRing - 1)
-      asm volatile("s_waitcnt vmcnt(6)" ::: "memory");  // 3 loads per block, 2 blocks younger
-    else if (my - i == 2)
-      asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // block i has landed once only the younger blocks' loads (three per
+    // block, completing in order) are outstanding
+    wait_blocks_younger(min(kRing - 2, my - 1 - i));
     const uint8_t* blk = wring + (i % kRing) * kBlock;
     // header: bytes 0..7 (d, dmin, scales 0..3) and 8..15 (scales 4..11) of row r
     const v2i h0 = tr8(blk, lofs);
@@ -268,14 +280,30 @@ void q4k_i16_gemv(const uint8_t* W, const uint8_t* X, float* Y, size_t M, size_t
     set_error(hipErrorInvalidValue);
     return;
   }
-  const size_t nsb = K / 256;
-  const size_t lds = kRingBytes + nsb * (256 + 4 + 32) + kWaves * kCohort * 4;
+  // waves per cohort: the power of two (up to 16, and at most one per
+  // superblock) nearest to 4096 waves in all, which measured best from
+  // 14 to 22 waves per CU at the reference's shapes
+  const size_t nsb = K / 256, cohorts = M / kCohort;
+  int waves = 1;
+  while (waves < 16 && (size_t)waves * 2 <= nsb && (double)cohorts * waves * 1.41421356 < 4096.0) waves *= 2;
+  const size_t lds = (size_t)waves * kRing * kBlock + nsb * (256 + 32 + 4) + (size_t)waves * kCohort * 4;
   if (lds > max_lds_per_block()) {
     set_error(hipErrorInvalidValue);  // the activation does not fit in LDS
     return;
   }
+  if (cohorts > (size_t)INT32_MAX) {
+    set_error(hipErrorInvalidValue);
+    return;
+  }
   GemvArgs a{W, X, Y, (int)M, (int)K};
-  q4k_i16_gemv_kernel<<<(unsigned)(M / kCohort), kThreads, lds, current_stream()>>>(a);
+  const dim3 grid((unsigned)cohorts);
+  switch (waves) {
+    case 1: q4k_i16_gemv_kernel<1><<<grid, 64, lds, current_stream()>>>(a); break;
+    case 2: q4k_i16_gemv_kernel<2><<<grid, 128, lds, current_stream()>>>(a); break;
+    case 4: q4k_i16_gemv_kernel<4><<<grid, 256, lds, current_stream()>>>(a); break;
+    case 8: q4k_i16_gemv_kernel<8><<<grid, 512, lds, current_stream()>>>(a); break;
+    default: q4k_i16_gemv_kernel<16><<<grid, 1024, lds, current_stream()>>>(a); break;
+  }
   check_launch();
 }
 
