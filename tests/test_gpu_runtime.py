@@ -9,7 +9,7 @@ import pytest
 
 import oracle as o
 from weft_amd import kernels as K
-from weft_amd.runtime import Buffer, compile, jit
+from weft_amd.runtime import Buffer, CompileOptions, compile, jit
 
 pytestmark = pytest.mark.gpu
 
@@ -61,3 +61,26 @@ def test_host_buffer_rejected_on_device(torch_dev):
     w = torch.zeros(144, dtype=torch.uint8, device=dev)
     with pytest.raises(TypeError, match="host memory"):
         fn(Buffer(w, shape=(256,), encoding="Q4_K"), np.zeros(256, np.float32))
+
+
+def test_jit_staged_prefill_with_the_reference_tuning_bindings(torch_dev):
+    """production_mul_mat_q4_k_staged as weft-mul-mat.sh runs it: jit with the
+    bindings of examples/kernels/mul_mat/tuning.json ("mul-mat:k1 q4_k
+    prefill"), a second call reusing the artifact."""
+    torch, dev = torch_dev
+    n, k, m = 256, 1024, 80
+    w = o.quantize("q4_k", o.seeded_normal(63, (n, k), 0.02))
+    x = o.seeded_normal(64, (m, k))
+    xq_t = torch.zeros(m * (k // 256) * 292, dtype=torch.uint8, device=dev)
+    y_t = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+    options = CompileOptions(meta={"NC": 64, "KC": 512, "MC": 8, "MR": 2})
+    fn = jit(K.production_mul_mat_q4_k_staged, options=options)
+    args = (Buffer(torch.from_numpy(w).to(dev), shape=(n, k), encoding="Q4_K"),
+            torch.from_numpy(x).to(dev), Buffer(xq_t, shape=(m, k), encoding="Q8_K"), y_t)
+    fn(*args)
+    fn(*args)
+    assert compile(K.production_mul_mat_q4_k_staged, options=options) is fn.compiled
+    want_xq = o.quantize("q8_k", x)
+    assert np.array_equal(xq_t.cpu().numpy().reshape(m, -1), want_xq)
+    e, a = o.mul_mat_f64("q4_k", w, want_xq, n, k, m)
+    assert o.within_tolerance(y_t.cpu().numpy(), e, a).all()

@@ -18,7 +18,8 @@ from .diagnostics import DefinitionError, LanguageUseError
 
 class KernelDefinition:
     def __init__(self, name: str, parameters: tuple[str, ...], source: str,
-                 alias_groups: Mapping[str, str] | None = None) -> None:
+                 alias_groups: Mapping[str, str] | None = None,
+                 source_bindings: tuple[str, ...] = ()) -> None:
         groups = dict(alias_groups or {})
         if any(not isinstance(k, str) or not k or not isinstance(v, str) or not v
                for k, v in groups.items()):
@@ -31,6 +32,9 @@ class KernelDefinition:
         self.parameters = tuple(parameters)
         self.alias_groups = groups
         self.source = source
+        # names of the reference kernel's ``wl.auto`` extents: each needs one
+        # concrete ``CompileOptions.meta`` binding at compile time
+        self.source_bindings = tuple(sorted(source_bindings))
 
     @property
     def signature(self) -> inspect.Signature:
@@ -49,6 +53,15 @@ _MM = ("W", "X", "Xq", "Y")
 _MM_IQ2 = ("W", "X", "Xq", "grid", "signs", "Y")
 _MM_MX = ("W", "X", "Xq", "codebook", "scale", "Y")
 _DECODE_GROUPS = {"Xq": "workspace", "Y": "output"}
+
+# wl.auto extents of the tiled prefill kernels (mul_mat/q4_0.py:17-22,
+# q4_k_staged.py:20-24, iq2_xxs_staged.py:43-48 and :80-83, mxfp4.py:21-25)
+_AUTO = {
+    "production_mul_mat_q4_0": ("MC", "MR", "NC", "NR"),
+    "production_mul_mat_q4_k_staged": ("KC", "MC", "MR", "NC"),
+    "production_mul_mat_iq2_xxs_staged": ("KC", "MC", "MR", "NC", "NR"),
+    "production_mul_mat_mxfp4": ("MC", "MR", "NC", "NR"),
+}
 
 # (symbol, parameters, reference source, alias groups)
 _DEFS = [
@@ -85,7 +98,7 @@ _DEFS = [
 
 DEFINITIONS: dict[str, KernelDefinition] = {}
 for _name, _params, _src, _groups in _DEFS:
-    DEFINITIONS[_name] = KernelDefinition(_name, _params, _src, _groups)
+    DEFINITIONS[_name] = KernelDefinition(_name, _params, _src, _groups, _AUTO.get(_name, ()))
     globals()[_name] = DEFINITIONS[_name]
 
 __all__ = ["KernelDefinition", "DEFINITIONS", *DEFINITIONS]

@@ -42,10 +42,6 @@ def _freeze(value):
     return value
 
 
-# gfx950 bindings a kernel accepts through CompileOptions.meta: none of the
-# hand-written kernels exposes a tile binding yet.
-_TARGET_BINDINGS: dict[str, frozenset[str]] = {}
-
 _RVV_DEFAULTS = {"lmul_eighths": 8, "unroll": 1, "pipeline_depth": 1, "scalar_load_prime": 0,
                  "partial_combine_policy": "independent-multilevel",
                  "record_axis_policy": "within-record", "max_widening_combine_groups": 2}
@@ -85,6 +81,9 @@ class CompiledKernel:
 
         if metadata["gfx_arch"] != target.gfx_arch:
             raise CompilationError("compiled artifact disagrees with its discovered target")
+        # the artifact records the source bindings it was compiled with, sorted
+        # by name (lib/Target/ConvertWeftToRISCV.cpp:944-954)
+        metadata = dict(metadata, bindings=dict(sorted(options.meta.items())))
         self.metadata = _freeze(metadata)
         self.target = target
         self.options = options
@@ -191,11 +190,14 @@ class _Compiler:
         for name, default in _RVV_DEFAULTS.items():
             if getattr(options, name) != default:
                 raise CompilationError(f"RISC-V physical binding {name} has no gfx950 meaning")
-        allowed = _TARGET_BINDINGS.get(definition.__name__, frozenset())
-        unknown = set(options.meta).difference(allowed)
-        if unknown:
-            raise CompilationError(
-                f"{definition.__name__} has no gfx950 binding named {', '.join(sorted(unknown))}")
+        # every wl.auto extent needs one concrete binding; other names are
+        # accepted and recorded (lib/Target/ConvertWeftToRISCV.cpp:730-745).
+        # The gfx950 kernels' tiles are fixed by their hand-written code, so
+        # a binding selects an artifact identity, not a different tiling.
+        for name in definition.source_bindings:
+            if name not in options.meta:
+                raise CompilationError(
+                    f"source auto parameter '{name}' requires one concrete --meta binding")
         key = (definition, tuple(options.arguments()))
         with self._lock:
             self.target.check_execution()
