@@ -153,6 +153,52 @@ size_t q4_k_q8_k_gemv_contract_W_packed_size(size_t M, size_t K);
 void q4_k_q8_k_gemv_contract_W_pack(const uint8_t *source, uint8_t *target, size_t M, size_t K);
 void q4_k_q8_k_gemv_contract(const uint8_t *W, const uint8_t *X, float *Y, size_t M, size_t K);
 
+/* ----------------------------------------------- GGML MUL_MAT boundary */
+/* The quantized mul_mat behind GGML's MUL_MAT op, for a ggml-style graph
+ * executor: ggml_compute_forward_mul_mat's contract
+ * (source/c/ggml/llama.cpp/ggml/src/ggml-cpu/ggml-cpu.c:1245-1443) with
+ * src0 of type Q4_0, Q4_K, IQ2_XXS or MXFP4, src1 F32 (quantized into wdata
+ * as GGML does) or already of src0's vec_dot type, dst F32; GGML's byte
+ * strides and broadcast of src0 over src1's planes (ne12 / ne02, ne13 / ne03).
+ * All data pointers are device pointers; the call is stream-ordered.
+ * Returns 0, or the error it also records for weft_hip_get_last_error():
+ * hipErrorInvalidValue where GGML asserts (nothing is launched),
+ * hipErrorNotSupported for types outside this path. */
+
+/* enum ggml_type values (ggml/include/ggml.h:389-431) of this path */
+enum {
+  WEFT_GGML_TYPE_F32 = 0,
+  WEFT_GGML_TYPE_Q4_0 = 2,
+  WEFT_GGML_TYPE_Q8_0 = 8,
+  WEFT_GGML_TYPE_Q4_K = 12,
+  WEFT_GGML_TYPE_Q8_K = 15,
+  WEFT_GGML_TYPE_IQ2_XXS = 16,
+  WEFT_GGML_TYPE_MXFP4 = 39
+};
+
+/* the fields of struct ggml_tensor (ggml/include/ggml.h:667-692) MUL_MAT reads */
+typedef struct weft_ggml_tensor {
+  int32_t type;   /* enum ggml_type */
+  int64_t ne[4];  /* elements per dimension */
+  size_t nb[4];   /* bytes per step of each dimension */
+  void *data;     /* device pointer */
+} weft_ggml_tensor;
+
+/* ggml_type_size / ggml_blck_size / ggml_row_size (ggml/src/ggml.c:1303-1320)
+ * and type_traits_cpu[type].vec_dot_type (ggml-cpu.c:230-331) for this path's
+ * types; 0 (-1 for the vec_dot type) for any other type */
+size_t weft_ggml_type_size(int32_t type);
+int64_t weft_ggml_blck_size(int32_t type);
+size_t weft_ggml_row_size(int32_t type, int64_t ne);
+int32_t weft_ggml_vec_dot_type(int32_t type);
+/* MUL_MAT's work size in ggml_graph_plan (ggml-cpu.c:2819-2826):
+ * ggml_row_size(vec_dot_type, nelements(src1)), 0 when src1 needs no quantization */
+size_t weft_ggml_mul_mat_work_size(const weft_ggml_tensor *src0, const weft_ggml_tensor *src1);
+/* GGML_OP_MUL_MAT (ggml-cpu.c:1245-1443); wdata: work buffer of wsize bytes,
+ * 4-byte aligned, ends holding src1 quantized as GGML's wdata would */
+int weft_ggml_mul_mat(const weft_ggml_tensor *src0, const weft_ggml_tensor *src1,
+                      const weft_ggml_tensor *dst, void *wdata, size_t wsize);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,119 @@
+"""GGML MUL_MAT through libweft_hip's weft_ggml_mul_mat on the GPU, against the
+oracle's GGML MUL_MAT (ggml-cpu/ggml-cpu.c:1245-1443) applied plane by plane.
+
+Bars: the work buffer holds each src1 row quantized bit-exactly as GGML's
+wdata would; dst within |y - E| <= 1e-4 |E| + 4e-6 A (oracle.within_tolerance)
+of the fp64 re-accumulation for the src0 plane that broadcast selects
+(i02 = i12 / r2, i03 = i13 / r3); bytes between strided dst rows untouched.
+Cases: contiguous 2D at decode and prefill batch sizes, padded rows on every
+operand (aligned, and 2-byte pads that take the unaligned kernels), src0
+broadcast over src1 planes, batched planes that collapse into one GEMM, and a
+src1 already quantized to the vec_dot type."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as o
+from weft_amd import ggml as G
+
+pytestmark = pytest.mark.gpu
+
+TYPE = {"q4_0": G.Q4_0, "q4_k": G.Q4_K, "iq2_xxs": G.IQ2_XXS, "mxfp4": G.MXFP4}
+VDT = {"q4_0": G.Q8_0, "mxfp4": G.Q8_0, "q4_k": G.Q8_K, "iq2_xxs": G.Q8_K}
+FMTS = list(TYPE)
+NAN = 0x7FC00001  # a quiet NaN the kernels never produce
+
+
+def run(hip, fmt, k, n, m, planes0=(1, 1), planes1=(1, 1), pad_w=0, pad_x=0, pad_y=0,
+        prequant=False, seed=7):
+    hip.torch.cuda.synchronize()
+    ne02, ne03 = planes0
+    ne12, ne13 = planes1
+    rb = o.record_bytes(fmt, k)
+    act = o.ACT_OF[fmt]
+    rq = o.record_bytes(act, k)
+    # src0: ne03 x ne02 planes of n rows, each row followed by pad_w bytes
+    w = np.stack([o.quantize(fmt, o.seeded_normal(seed + p, (n, k), 0.02))
+                  for p in range(ne02 * ne03)]).reshape(ne03, ne02, n, rb)
+    w_host = np.full((ne03, ne02, n, rb + pad_w), 0x5A, np.uint8)
+    w_host[..., :rb] = w
+    x = o.seeded_normal(seed + 100, (ne13, ne12, m, k))
+    if prequant:
+        src1_host = np.stack([o.quantize(act, x[i3, i2]) for i3 in range(ne13)
+                              for i2 in range(ne12)]).reshape(ne13, ne12, m, rq)
+        nb1 = [G.type_size(VDT[fmt]), rq, rq * m, rq * m * ne12]
+        t1 = VDT[fmt]
+    else:
+        src1_host = np.zeros((ne13, ne12, m, k + pad_x), np.float32)
+        src1_host[..., :k] = x
+        row = 4 * (k + pad_x)
+        nb1 = [4, row, row * m, row * m * ne12]
+        t1 = G.F32
+    y_row = 4 * (n + pad_y)
+    wd = hip.to_dev(w_host)
+    xd = hip.to_dev(src1_host)
+    yd = hip.empty(y_row * m * ne12 * ne13)
+    yd.t[:yd.nbytes].view(hip.torch.int32).fill_(NAN)
+    nb0 = [G.type_size(TYPE[fmt]), rb + pad_w, (rb + pad_w) * n, (rb + pad_w) * n * ne02]
+    s0 = G.tensor(TYPE[fmt], (k, n, ne02, ne03), wd.ptr, nb0)
+    s1 = G.tensor(t1, (k, m, ne12, ne13), xd.ptr, nb1)
+    d = G.tensor(G.F32, (n, m, ne12, ne13), yd.ptr, [4, y_row, y_row * m, y_row * m * ne12])
+    wsize = G.mul_mat_work_size(s0, s1)
+    assert wsize == (0 if prequant else rq * m * ne12 * ne13)
+    wdata = hip.empty(max(wsize, 4), fill=0xA5)
+    print(f"ggml mul_mat {fmt} k={k} n={n} m={m} planes0={planes0} planes1={planes1} "
+          f"pads={pad_w},{pad_x},{pad_y} prequant={prequant}", flush=True)
+    G.mul_mat(s0, s1, d, wdata.ptr, wsize)
+    hip.torch.cuda.synchronize()
+    assert hip.last_error() == 0
+    y = yd.numpy(np.float32).reshape(ne13, ne12, m, n + pad_y)
+    wq = wdata.numpy(np.uint8)[:wsize].reshape(ne13, ne12, m, rq) if wsize else None
+    r2, r3 = ne12 // ne02, ne13 // ne03
+    for i3 in range(ne13):
+        for i2 in range(ne12):
+            xq = o.quantize(act, x[i3, i2])
+            if wq is not None:
+                np.testing.assert_array_equal(wq[i3, i2], xq, err_msg=f"wdata plane {i2},{i3}")
+            e, a = o.mul_mat_f64(fmt, w[i3 // r3, i2 // r2], xq, n, k, m)
+            ok = o.within_tolerance(y[i3, i2, :, :n], e, a)
+            assert ok.all(), f"plane {i2},{i3}: {int((~ok).sum())} outputs outside tolerance"
+    if pad_y:
+        assert (y[..., n:].view(np.int32) == NAN).all(), "dst padding written"
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("m", [1, 3, 40])
+def test_contiguous(hip, fmt, m):
+    run(hip, fmt, 1024, 256, m)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("m", [1, 40])
+def test_padded_rows(hip, fmt, m):
+    # 16-byte pads keep the aligned kernels (GEMM / 16-byte GEMV paths)
+    run(hip, fmt, 512, 200, m, pad_w=16, pad_x=12, pad_y=8)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("m", [1, 24])
+def test_unaligned_row_pads(hip, fmt, m):
+    # a 2-byte (1-byte for MXFP4) weight-row pad: rows keep only the Encoding
+    # alignment, so the GEMV kernels take every size
+    run(hip, fmt, 512, 96, m, pad_w=1 if fmt == "mxfp4" else 2, pad_x=1, pad_y=3)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_broadcast_over_planes(hip, fmt):
+    run(hip, fmt, 512, 64, 3, planes0=(2, 1), planes1=(4, 2))
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_batched_planes_collapse(hip, fmt):
+    run(hip, fmt, 512, 160, 20, planes1=(3, 1))
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("m", [1, 33])
+def test_prequantized_src1(hip, fmt, m):
+    run(hip, fmt, 512, 128, m, planes1=(2, 1), prequant=True)

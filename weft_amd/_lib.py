@@ -60,6 +60,7 @@ def load() -> ctypes.CDLL:
             lib.weft_hip_device_count.restype = ctypes.c_int
             lib.weft_hip_device_arch.argtypes = [ctypes.c_int, ctypes.c_char_p, ctypes.c_size_t]
             lib.weft_hip_device_arch.restype = ctypes.c_int
+            _bind_ggml(lib)
             artifact = json.loads(lib.weft_hip_artifact())
             for kernel in artifact["kernels"]:
                 fn = getattr(lib, kernel["symbol"])
@@ -78,6 +79,18 @@ def load() -> ctypes.CDLL:
             _artifact = artifact
             _lib = lib
         return _lib
+
+
+def _bind_ggml(lib: ctypes.CDLL) -> None:
+    """Types of the GGML MUL_MAT boundary (weft_ggml_*)."""
+    i32, i64, sz, vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p
+    for name, args, res in (("weft_ggml_type_size", [i32], sz), ("weft_ggml_blck_size", [i32], i64),
+                            ("weft_ggml_row_size", [i32, i64], sz),
+                            ("weft_ggml_vec_dot_type", [i32], i32),
+                            ("weft_ggml_mul_mat_work_size", [vp, vp], sz),
+                            ("weft_ggml_mul_mat", [vp, vp, vp, vp, sz], ctypes.c_int)):
+        fn = getattr(lib, name)
+        fn.argtypes, fn.restype = args, res
 
 
 def artifact() -> dict:

@@ -43,6 +43,11 @@ __device__ inline float4 load_x4(const float* p, bool a16) {
   return make_float4(p[0], p[1], p[2], p[3]);
 }
 
+// X rows start ldx floats apart; 16-byte loads need every row start aligned
+__host__ __device__ inline bool x_rows_a16(const float* X, size_t ldx) {
+  return (reinterpret_cast<uintptr_t>(X) & 15) == 0 && ldx % 4 == 0;
+}
+
 // Store one quantized Q8_K superblock (index idx = m * nsb + s of this
 // launch's activation rows) into LDS, and into xq_out when non-null.
 __device__ inline void q8k_store(const Q8KLane& r, int idx, int nsb, int K, int m0,
@@ -83,22 +88,22 @@ struct Q8KStagerT {
   static constexpr int kPrefetch = P;
   float4 x[kPrefetch];
 
-  __device__ inline void prefetch(const float* __restrict__ X, int K, int m0, int mb) {
+  __device__ inline void prefetch(const float* __restrict__ X, size_t ldx, int K, int m0, int mb) {
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int nwaves = blockDim.x / kWave;
     const int nsb = K / 256, total = mb * nsb;
-    const bool a16 = (reinterpret_cast<uintptr_t>(X) & 15) == 0;
+    const bool a16 = x_rows_a16(X, ldx);
 #pragma unroll
     for (int i = 0; i < kPrefetch; ++i) {
       const int idx = min(wave + i * nwaves, total - 1);  // clamped: always a valid load
       const int m = idx / nsb, s = idx - m * nsb;
-      x[i] = load_x4(X + (size_t)(m0 + m) * K + 256 * s + 4 * lane, a16);
+      x[i] = load_x4(X + (size_t)(m0 + m) * ldx + 256 * s + 4 * lane, a16);
     }
   }
 
-  __device__ inline void finish(const float* __restrict__ X, uint8_t* __restrict__ xq_out, int K,
-                                int m0, int mb, char* lds) {
+  __device__ inline void finish(const float* __restrict__ X, size_t ldx, uint8_t* __restrict__ xq_out,
+                                int K, int m0, int mb, char* lds) {
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int nwaves = blockDim.x / kWave;
@@ -113,10 +118,10 @@ struct Q8KStagerT {
       const int idx = wave + i * nwaves;
       if (idx < total) q8k_store(r[i], idx, nsb, K, m0, xq_out, lds, lane);
     }
-    const bool a16 = (reinterpret_cast<uintptr_t>(X) & 15) == 0;
+    const bool a16 = x_rows_a16(X, ldx);
     for (int idx = wave + kPrefetch * nwaves; idx < total; idx += nwaves) {
       const int m = idx / nsb, s = idx - m * nsb;
-      const float4 v = load_x4(X + (size_t)(m0 + m) * K + 256 * s + 4 * lane, a16);
+      const float4 v = load_x4(X + (size_t)(m0 + m) * ldx + 256 * s + 4 * lane, a16);
       q8k_quantize_store(v, idx, nsb, K, m0, xq_out, lds, lane);
     }
   }
@@ -131,19 +136,19 @@ template <int P>
 struct Q8KStager16 {
   float4 x[P][4];
 
-  __device__ inline void prefetch(const float* __restrict__ X, int K, int m0, int mb) {
+  __device__ inline void prefetch(const float* __restrict__ X, size_t ldx, int K, int m0, int mb) {
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int nwaves = blockDim.x / kWave;
     const int nsb = K / 256, total = mb * nsb;
-    const bool a16 = (reinterpret_cast<uintptr_t>(X) & 15) == 0;
+    const bool a16 = x_rows_a16(X, ldx);
 #pragma unroll
     for (int i = 0; i < P; ++i) {
       // a wave whose pass i is past the end loads nothing (uniform branch)
       if (4 * (wave + i * nwaves) >= total) break;
       const int idx = min(4 * (wave + i * nwaves) + lane / 16, total - 1);  // clamped: a valid load
       const int m = idx / nsb, s = idx - m * nsb;
-      const float* src = X + (size_t)(m0 + m) * K + 256 * s + 16 * (lane & 15);
+      const float* src = X + (size_t)(m0 + m) * ldx + 256 * s + 16 * (lane & 15);
 #pragma unroll
       for (int j = 0; j < 4; ++j) x[i][j] = load_x4(src + 4 * j, a16);
     }
@@ -170,8 +175,8 @@ struct Q8KStager16 {
     }
   }
 
-  __device__ inline void finish(const float* __restrict__ X, uint8_t* __restrict__ xq_out, int K,
-                                int m0, int mb, char* lds) {
+  __device__ inline void finish(const float* __restrict__ X, size_t ldx, uint8_t* __restrict__ xq_out,
+                                int K, int m0, int mb, char* lds) {
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int nwaves = blockDim.x / kWave;
@@ -200,11 +205,11 @@ struct Q8KStager16 {
         if (idx < total) store(r, idx, nsb, K, m0, xq_out, lds, part);
       }
     }
-    const bool a16 = (reinterpret_cast<uintptr_t>(X) & 15) == 0;
+    const bool a16 = x_rows_a16(X, ldx);
     for (int w = wave + P * nwaves; 4 * w < total; w += nwaves) {
       const int idx = min(4 * w + lane / 16, total - 1);
       const int m = idx / nsb, s = idx - m * nsb;
-      const float* src = X + (size_t)(m0 + m) * K + 256 * s + 16 * part;
+      const float* src = X + (size_t)(m0 + m) * ldx + 256 * s + 16 * part;
       float4 v[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) v[j] = load_x4(src + 4 * j, a16);
@@ -214,18 +219,19 @@ struct Q8KStager16 {
   }
 };
 
-// Quantize rows [m0, m0+mb) of X (row stride K) into LDS; when xq_out is
-// non-null also store the records (Xq row stride K/256 records).
-__device__ inline void stage_q8k_quantize(const float* __restrict__ X, uint8_t* __restrict__ xq_out,
-                                          int K, int m0, int mb, char* lds) {
+// Quantize rows [m0, m0+mb) of X (row stride ldx floats) into LDS; when
+// xq_out is non-null also store the records (Xq row stride K/256 records).
+__device__ inline void stage_q8k_quantize(const float* __restrict__ X, size_t ldx,
+                                          uint8_t* __restrict__ xq_out, int K, int m0, int mb,
+                                          char* lds) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int nwaves = blockDim.x / kWave;
   const int nsb = K / 256;
-  const bool a16 = (reinterpret_cast<uintptr_t>(X) & 15) == 0;
+  const bool a16 = x_rows_a16(X, ldx);
   for (int idx = wave; idx < mb * nsb; idx += nwaves) {
     const int m = idx / nsb, s = idx - m * nsb;
-    const float4 x = load_x4(X + (size_t)(m0 + m) * K + 256 * s + 4 * lane, a16);
+    const float4 x = load_x4(X + (size_t)(m0 + m) * ldx + 256 * s + 4 * lane, a16);
     q8k_quantize_store(x, idx, nsb, K, m0, xq_out, lds, lane);
   }
 }
@@ -272,20 +278,21 @@ __device__ inline Q80View q80_view(char* base, int K, int m) {
 
 // K must be a multiple of 32; a wave covers 8 blocks (256 values) per step,
 // 8 lanes per block.
-__device__ inline void stage_q80_quantize(const float* __restrict__ X, uint8_t* __restrict__ xq_out,
-                                          int K, int m0, int mb, char* lds) {
+__device__ inline void stage_q80_quantize(const float* __restrict__ X, size_t ldx,
+                                          uint8_t* __restrict__ xq_out, int K, int m0, int mb,
+                                          char* lds) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int nwaves = blockDim.x / kWave;
   const int nb = K / 32;
   const int steps = (nb + 7) / 8;
-  const bool a16 = (reinterpret_cast<uintptr_t>(X) & 15) == 0;
+  const bool a16 = x_rows_a16(X, ldx);
   for (int idx = wave; idx < mb * steps; idx += nwaves) {
     const int m = idx / steps, st = idx - m * steps;
     const int b = 8 * st + lane / 8;
     const bool live = b < nb;  // uniform per 8-lane group
     float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (live) x = load_x4(X + (size_t)(m0 + m) * K + 32 * b + 4 * (lane & 7), a16);
+    if (live) x = load_x4(X + (size_t)(m0 + m) * ldx + 32 * b + 4 * (lane & 7), a16);
     const Q8_0Lane r = q80_quantize_8lanes(x);
     if (!live) continue;
     const Q80View v = q80_view(lds, K, m);

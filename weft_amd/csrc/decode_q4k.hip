@@ -46,6 +46,8 @@ struct Q4KArgs {
   int m0, mb;            // activation rows of this launch
   int rows_per_wg;
   long long y_stride;    // elements between output rows
+  size_t ldw;            // bytes between weight rows
+  size_t ldx;            // elements between activation rows
 };
 
 template <bool A16>
@@ -74,7 +76,7 @@ __global__ void __launch_bounds__(NT) q4k_gemv_kernel(Q4KArgs a) {
   const int nsb = K >> 8;
   const int items = nsb * 8;
   const int iters = (items + kWave - 1) / kWave;
-  const size_t rb = (size_t)nsb * kQ4_KBytes;
+  const size_t rb = a.ldw;
   const int row0 = blockIdx.x * a.rows_per_wg + wave;
   const int row_end = min(a.N, blockIdx.x * a.rows_per_wg + a.rows_per_wg);
   const int my_rows = row0 < row_end ? (row_end - row0 + nwaves - 1) / nwaves : 0;
@@ -92,7 +94,7 @@ __global__ void __launch_bounds__(NT) q4k_gemv_kernel(Q4KArgs a) {
   };
 
   Q8KStager stager;
-  if (a.X != nullptr) stager.prefetch(a.X, K, a.m0, a.mb);
+  if (a.X != nullptr) stager.prefetch(a.X, a.ldx, K, a.m0, a.mb);
   __builtin_amdgcn_sched_barrier(0);
   // The first round's loads are unconditional (straight-line code keeps the
   // in-order wait counts exact): past its last chunk a lane re-requests a
@@ -102,7 +104,7 @@ __global__ void __launch_bounds__(NT) q4k_gemv_kernel(Q4KArgs a) {
   __builtin_amdgcn_sched_barrier(0);
 
   if (a.X != nullptr)
-    stager.finish(a.X, blockIdx.x == 0 ? a.xq_out : nullptr, K, a.m0, a.mb, lds);
+    stager.finish(a.X, a.ldx, blockIdx.x == 0 ? a.xq_out : nullptr, K, a.m0, a.mb, lds);
   else
     stage_q8k_load(a.xq_in, K, a.m0, a.mb, lds);
   __syncthreads();
@@ -214,7 +216,7 @@ __global__ void __launch_bounds__(NT) q4k_gemv_m1_kernel(Q4KArgs a) {
   constexpr int nwaves = NT / kWave;
   const int K = a.K;
   const int nsb = K >> 8;
-  const size_t rb = (size_t)nsb * kQ4_KBytes;
+  const size_t rb = a.ldw;
   const int lsb = lane >> 2, g = lane & 3;
   // lane-constant byte offsets of step st (clamped to the row's last superblock)
   int off[STEPS];
@@ -232,7 +234,7 @@ __global__ void __launch_bounds__(NT) q4k_gemv_m1_kernel(Q4KArgs a) {
   // 16 lanes per superblock, four superblocks per wave pass: P passes cover
   // the 16 STEPS superblocks of the longest row
   Q8KStager16<(4 * STEPS + nwaves - 1) / nwaves> stager;
-  stager.prefetch(a.X, K, a.m0, 1);
+  stager.prefetch(a.X, a.ldx, K, a.m0, 1);
   // keep the activation loads ahead of the weight loads: waits are in issue
   // order, so the quantization then waits for X only
   __builtin_amdgcn_sched_barrier(0);
@@ -255,7 +257,7 @@ __global__ void __launch_bounds__(NT) q4k_gemv_m1_kernel(Q4KArgs a) {
   issue(bufA, 0);  // bufB is only used (and allocated) when RB == 2
   __builtin_amdgcn_sched_barrier(0);
 
-  stager.finish(a.X, blockIdx.x == 0 ? a.xq_out : nullptr, K, a.m0, 1, lds);
+  stager.finish(a.X, a.ldx, blockIdx.x == 0 ? a.xq_out : nullptr, K, a.m0, 1, lds);
   __syncthreads();
 
   // this lane's activation slice of every step
@@ -357,12 +359,13 @@ void launch_one(bool a16, int grid, size_t lds, const Q4KArgs& a) {
 
 // X != null -> quantize (and write Xq), else read xq_in.
 void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_out, float* Y,
-                size_t N, size_t K, size_t M) {
+                size_t N, size_t K, size_t M, const RowStrides& st) {
   if (N == 0 || M == 0 || K == 0) return;
   if (K % 256 != 0 || W == nullptr || Y == nullptr || (X == nullptr && xq_in == nullptr) ||
       N > (size_t)INT32_MAX || K > (size_t)INT32_MAX || M > (size_t)INT32_MAX ||
       !aligned(W, 2) || !aligned(Y, 4) || (xq_in && !aligned(xq_in, 4)) ||
-      (xq_out && !aligned(xq_out, 4)) || (X && !aligned(X, 4))) {
+      (xq_out && !aligned(xq_out, 4)) || (X && !aligned(X, 4)) ||
+      !strides_ok(st, K / 256 * kQ4_KBytes, 2, K, N, N, M)) {
     set_error(hipErrorInvalidValue);
     return;
   }
@@ -377,7 +380,7 @@ void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t*
   const int cus = cu_count();
   const int rows_per_wg = (int)((N + cus - 1) / cus);
   const int grid = (int)((N + rows_per_wg - 1) / rows_per_wg);
-  const bool a16 = aligned(W, 16);
+  const bool a16 = aligned(W, 16) && (N == 1 || st.ldw % 16 == 0);
   if (M == 1 && X != nullptr && a16 && aligned(X, 16) && K <= 3 * 4096) {
     // batch 1: the register-resident kernel.  One step per row (K <= 4096)
     // runs 1024-thread workgroups, two per CU (62 VGPRs); longer rows keep
@@ -399,7 +402,9 @@ void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t*
     a.m0 = 0;
     a.mb = 1;
     a.rows_per_wg = rpw;
-    a.y_stride = (long long)N;
+    a.y_stride = (long long)st.ldy;
+    a.ldw = st.ldw;
+    a.ldx = st.ldx;
     const int g1 = (int)((N + rpw - 1) / rpw);
     if (steps == 1)
       q4k_gemv_m1_kernel<1, 1024, 2><<<g1, 1024, row_lds, current_stream()>>>(a);
@@ -426,7 +431,9 @@ void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t*
     a.m0 = (int)m0;
     a.mb = (int)std::min<size_t>(mb_max, M - m0);
     a.rows_per_wg = rows_per_wg;
-    a.y_stride = (long long)N;
+    a.y_stride = (long long)st.ldy;
+    a.ldw = st.ldw;
+    a.ldx = st.ldx;
     const size_t lds = row_lds * a.mb;
     if (a.mb == 1)
       launch_one<1, NT>(a16, grid, lds, a);
@@ -439,8 +446,13 @@ void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t*
 }  // namespace
 
 void decode_q4k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
-                size_t M) {
-  launch_q4k(W, X, nullptr, Xq, Y, N, K, M);
+                size_t M, const RowStrides& st) {
+  launch_q4k(W, X, nullptr, Xq, Y, N, K, M, st);
+}
+
+void decode_q4k_quantized(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K,
+                          size_t M, const RowStrides& st) {
+  launch_q4k(W, nullptr, Xq, nullptr, Y, N, K, M, st);
 }
 
 }  // namespace weft
@@ -453,7 +465,7 @@ void production_mul_mat_q4_k_decode(const uint8_t* W, const float* X, uint8_t* X
     weft::set_error(hipErrorInvalidValue);
     return;
   }
-  weft::decode_q4k(W, X, Xq, Y, N, K, M);
+  weft::decode_q4k(W, X, Xq, Y, N, K, M, weft::packed(K / 256 * weft::kQ4_KBytes, K, N));
 }
 
 void quantized_vec_dot_q4_k_q8_k(const uint8_t* W, const uint8_t* X, float* Y, size_t K) {
@@ -461,7 +473,7 @@ void quantized_vec_dot_q4_k_q8_k(const uint8_t* W, const uint8_t* X, float* Y, s
     weft::set_error(hipErrorInvalidValue);
     return;
   }
-  weft::launch_q4k(W, nullptr, X, nullptr, Y, 1, K, 1);
+  weft::launch_q4k(W, nullptr, X, nullptr, Y, 1, K, 1, weft::packed(K / 256 * weft::kQ4_KBytes, K, 1));
 }
 
 }  // extern "C"

@@ -67,6 +67,8 @@ struct Args {
   int m0, mb;
   int rows_per_wg;
   long long y_stride;
+  size_t ldw;  // bytes between weight rows
+  size_t ldx;  // elements between activation rows
 };
 
 // 4 bytes starting at any LDS byte offset o (o+7 must be inside the buffer)
@@ -154,12 +156,12 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
   }
   if constexpr (T::kQ8K) {
     if (a.X != nullptr)
-      stage_q8k_quantize(a.X, blockIdx.x == 0 ? a.xq_out : nullptr, K, a.m0, a.mb, act);
+      stage_q8k_quantize(a.X, a.ldx, blockIdx.x == 0 ? a.xq_out : nullptr, K, a.m0, a.mb, act);
     else
       stage_q8k_load(a.xq_in, K, a.m0, a.mb, act);
   } else {
     if (a.X != nullptr)
-      stage_q80_quantize(a.X, blockIdx.x == 0 ? a.xq_out : nullptr, K, a.m0, a.mb, act);
+      stage_q80_quantize(a.X, a.ldx, blockIdx.x == 0 ? a.xq_out : nullptr, K, a.m0, a.mb, act);
     else
       stage_q80_load(a.xq_in, K, a.m0, a.mb, act);
   }
@@ -177,9 +179,10 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
 
   char* win = windows + wave * kWindow;
   const int nrec = K / T::kElems;
-  const size_t rb = (size_t)nrec * T::kBytes;
+  const size_t rb = a.ldw;
   const uint8_t* wlo = a.W;
-  const uint8_t* whi = a.W + (size_t)a.N * rb;
+  // end of the last row: staging windows are clamped to [wlo, whi)
+  const uint8_t* whi = a.W + (size_t)(a.N - 1) * rb + (size_t)nrec * T::kBytes;
   const int row0 = blockIdx.x * a.rows_per_wg;
   const int row1 = min(a.N, row0 + a.rows_per_wg);
 
@@ -290,7 +293,8 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
 
 template <Fmt F>
 void launch(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_out,
-            const int8_t* tab0, const void* tab1, float* Y, size_t N, size_t K, size_t M) {
+            const int8_t* tab0, const void* tab1, float* Y, size_t N, size_t K, size_t M,
+            const RowStrides& st) {
   using T = Traits<F>;
   if (N == 0 || M == 0 || K == 0) return;
   const size_t act_align = T::kQ8K ? 4 : 2;
@@ -301,7 +305,8 @@ void launch(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_
       (xq_in && !aligned(xq_in, act_align)) || (xq_out && !aligned(xq_out, act_align)) ||
       (F != Fmt::Q4_0 && (tab0 == nullptr || tab1 == nullptr)) ||
       (F == Fmt::IQ2_XXS && (!aligned(tab0, 4) || !aligned(tab1, 4))) ||
-      (F == Fmt::MXFP4 && !aligned(tab1, 4))) {
+      (F == Fmt::MXFP4 && !aligned(tab1, 4)) ||
+      !strides_ok(st, K / T::kElems * T::kBytes, w_align, K, N, N, M)) {
     set_error(hipErrorInvalidValue);
     return;
   }
@@ -330,7 +335,9 @@ void launch(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_
     a.m0 = (int)m0;
     a.mb = (int)std::min<size_t>(mb_max, M - m0);
     a.rows_per_wg = rows_per_wg;
-    a.y_stride = (long long)N;
+    a.y_stride = (long long)st.ldy;
+    a.ldw = st.ldw;
+    a.ldx = st.ldx;
     staged_gemv_kernel<F><<<grid, kThreads, fixed + row_lds * a.mb, current_stream()>>>(a);
     check_launch();
   }
@@ -340,16 +347,27 @@ void launch(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_
 
 // Decode entry points shared with the prefill file for small M.
 void decode_q4_0(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
-                 size_t M) {
-  launch<Fmt::Q4_0>(W, X, nullptr, Xq, nullptr, nullptr, Y, N, K, M);
+                 size_t M, const RowStrides& st) {
+  launch<Fmt::Q4_0>(W, X, nullptr, Xq, nullptr, nullptr, Y, N, K, M, st);
 }
 void decode_mxfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
-                  const float* scale, float* Y, size_t N, size_t K, size_t M) {
-  launch<Fmt::MXFP4>(W, X, nullptr, Xq, codebook, scale, Y, N, K, M);
+                  const float* scale, float* Y, size_t N, size_t K, size_t M, const RowStrides& st) {
+  launch<Fmt::MXFP4>(W, X, nullptr, Xq, codebook, scale, Y, N, K, M, st);
 }
 void decode_iq2_xxs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,
-                    const int8_t* signs, float* Y, size_t N, size_t K, size_t M) {
-  launch<Fmt::IQ2_XXS>(W, X, nullptr, Xq, grid, signs, Y, N, K, M);
+                    const int8_t* signs, float* Y, size_t N, size_t K, size_t M,
+                    const RowStrides& st) {
+  launch<Fmt::IQ2_XXS>(W, X, nullptr, Xq, grid, signs, Y, N, K, M, st);
+}
+
+void decode_quantized(int fmt, const uint8_t* W, const uint8_t* Xq, const int8_t* tab0,
+                      const void* tab1, float* Y, size_t N, size_t K, size_t M,
+                      const RowStrides& st) {
+  switch (fmt) {
+    case 0: return launch<Fmt::Q4_0>(W, nullptr, Xq, nullptr, nullptr, nullptr, Y, N, K, M, st);
+    case 1: return launch<Fmt::MXFP4>(W, nullptr, Xq, nullptr, tab0, tab1, Y, N, K, M, st);
+    default: return launch<Fmt::IQ2_XXS>(W, nullptr, Xq, nullptr, tab0, tab1, Y, N, K, M, st);
+  }
 }
 
 }  // namespace weft
@@ -359,38 +377,39 @@ extern "C" {
 void production_mul_mat_q4_0_decode(const uint8_t* W, const float* X, uint8_t* Xq, float* Y,
                                     size_t N, size_t K, size_t M) {
   if (X == nullptr || Xq == nullptr) return weft::set_error(hipErrorInvalidValue);
-  weft::decode_q4_0(W, X, Xq, Y, N, K, M);
+  weft::decode_q4_0(W, X, Xq, Y, N, K, M, weft::packed(K / 32 * weft::kQ4_0Bytes, K, N));
 }
 
 void production_mul_mat_mxfp4_decode(const uint8_t* W, const float* X, uint8_t* Xq,
                                      const int8_t* codebook, const float* scale, float* Y,
                                      size_t N, size_t K, size_t M) {
   if (X == nullptr || Xq == nullptr) return weft::set_error(hipErrorInvalidValue);
-  weft::decode_mxfp4(W, X, Xq, codebook, scale, Y, N, K, M);
+  weft::decode_mxfp4(W, X, Xq, codebook, scale, Y, N, K, M, weft::packed(K / 32 * weft::kMxfp4Bytes, K, N));
 }
 
 void production_mul_mat_iq2_xxs_decode(const uint8_t* W, const float* X, uint8_t* Xq,
                                        const int8_t* grid, const int8_t* signs, float* Y, size_t N,
                                        size_t K, size_t M) {
   if (X == nullptr || Xq == nullptr) return weft::set_error(hipErrorInvalidValue);
-  weft::decode_iq2_xxs(W, X, Xq, grid, signs, Y, N, K, M);
+  weft::decode_iq2_xxs(W, X, Xq, grid, signs, Y, N, K, M,
+                       weft::packed(K / 256 * weft::kIq2xxsBytes, K, N));
 }
 
 void quantized_vec_dot_q4_0_q8_0(const uint8_t* W, const uint8_t* X, float* Y, size_t K) {
   if (X == nullptr) return weft::set_error(hipErrorInvalidValue);
-  weft::launch<weft::Fmt::Q4_0>(W, nullptr, X, nullptr, nullptr, nullptr, Y, 1, K, 1);
+  weft::launch<weft::Fmt::Q4_0>(W, nullptr, X, nullptr, nullptr, nullptr, Y, 1, K, 1, weft::packed(0, K, 1));
 }
 
 void quantized_vec_dot_mxfp4_q8_0(const uint8_t* W, const uint8_t* X, const int8_t* codebook,
                                   const float* scale, float* Y, size_t K) {
   if (X == nullptr) return weft::set_error(hipErrorInvalidValue);
-  weft::launch<weft::Fmt::MXFP4>(W, nullptr, X, nullptr, codebook, scale, Y, 1, K, 1);
+  weft::launch<weft::Fmt::MXFP4>(W, nullptr, X, nullptr, codebook, scale, Y, 1, K, 1, weft::packed(0, K, 1));
 }
 
 void quantized_vec_dot_iq2_xxs_q8_k(const uint8_t* W, const uint8_t* X, const int8_t* grid,
                                     const int8_t* signs, float* Y, size_t K) {
   if (X == nullptr) return weft::set_error(hipErrorInvalidValue);
-  weft::launch<weft::Fmt::IQ2_XXS>(W, nullptr, X, nullptr, grid, signs, Y, 1, K, 1);
+  weft::launch<weft::Fmt::IQ2_XXS>(W, nullptr, X, nullptr, grid, signs, Y, 1, K, 1, weft::packed(0, K, 1));
 }
 
 }  // extern "C"

@@ -1,0 +1,273 @@
+// GGML's MUL_MAT op on the quantized mul_mat kernels: the contract of
+// ggml_compute_forward_mul_mat (ggml-cpu/ggml-cpu.c:1245-1443) for src0 of
+// type Q4_0, Q4_K, IQ2_XXS or MXFP4, so the kernels can sit under a
+// ggml-style graph executor.
+//
+//   dst[i3, i2, i1, i0] = vec_dot(src0 row i0 of plane (i2 / r2, i3 / r3),
+//                                 src1 row (i1, i2, i3) quantized to the
+//                                 type's vec_dot_type),
+//   r2 = ne12 / ne02, r3 = ne13 / ne03 (src0 broadcast over src1's planes).
+//
+// Strides are GGML's byte strides: src0 rows nb01 apart (nb00 the block
+// size: not transposed), src1 rows nb11 apart (nb10 = 4), dst rows nb1
+// apart (nb0 = 4).  An F32 src1 is quantized into the caller's work buffer
+// as GGML does (rows contiguous, planes nbw2 = ne11 rows and nbw3 = ne12
+// planes apart, :1309-1340), so wdata ends holding what GGML's would; a
+// src1 already of the vec_dot_type is read in place.  GGML_ASSERT
+// conditions become error returns: nothing is launched.
+//
+// IQ2_XXS and MXFP4 need GGML's tables, which GGML compiles in rather than
+// passing; this file holds device copies built at compile time from the
+// format definitions (iq2xxs_grid as its kgrid_2bit_256 codes,
+// ggml-quants.c:2787-2804, expanded through {0x08, 0x19, 0x2b};
+// ksigns_iq2xs = i | parity(i) << 7 as +-1 bytes; kvalues_mxfp4 and
+// ggml_e8m0_to_fp32_half, ggml-common.h:1116-1118, ggml-impl.h:477-495).
+#include <mutex>
+#include <vector>
+
+#include "kernels.h"
+#include "runtime.h"
+#include "weft_common.h"
+#include "weft_hip.h"
+
+namespace weft {
+namespace {
+
+// ---------------------------------------------------------------- types
+struct TypeInfo {
+  int32_t type;
+  int64_t blck;
+  size_t size;
+  int32_t vec_dot;  // -1: not a MUL_MAT src0 type here
+};
+
+// ggml.c type_traits (blck_size, type_size) and ggml-cpu.c type_traits_cpu
+// (vec_dot_type, :230-239, :277-281, :301-309, :327-331) of this path's types
+constexpr TypeInfo kTypes[] = {
+    {WEFT_GGML_TYPE_F32, 1, 4, -1},
+    {WEFT_GGML_TYPE_Q4_0, 32, kQ4_0Bytes, WEFT_GGML_TYPE_Q8_0},
+    {WEFT_GGML_TYPE_Q8_0, 32, kQ8_0Bytes, -1},
+    {WEFT_GGML_TYPE_Q4_K, 256, kQ4_KBytes, WEFT_GGML_TYPE_Q8_K},
+    {WEFT_GGML_TYPE_Q8_K, 256, kQ8_KBytes, -1},
+    {WEFT_GGML_TYPE_IQ2_XXS, 256, kIq2xxsBytes, WEFT_GGML_TYPE_Q8_K},
+    {WEFT_GGML_TYPE_MXFP4, 32, kMxfp4Bytes, WEFT_GGML_TYPE_Q8_0},
+};
+
+const TypeInfo* info(int32_t type) {
+  for (const TypeInfo& t : kTypes)
+    if (t.type == type) return &t;
+  return nullptr;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- tables
+struct GgmlTables {
+  int8_t grid[256 * 8];
+  int8_t signs[128 * 8];
+  int8_t codebook[16];
+  float scale[256];
+};
+
+constexpr uint16_t kGridCodes[256] = {
+    0,     2,     5,     8,     10,    17,    20,    32,    34,    40,    42,    65,    68,    80,    88,    97,
+    100,   128,   130,   138,   162,   257,   260,   272,   277,   320,   388,   408,   512,   514,   546,   642,
+    1025,  1028,  1040,  1057,  1060,  1088,  1090,  1096,  1120,  1153,  1156,  1168,  1188,  1280,  1282,  1288,
+    1312,  1350,  1385,  1408,  1425,  1545,  1552,  1600,  1668,  1700,  2048,  2053,  2056,  2068,  2088,  2113,
+    2116,  2128,  2130,  2184,  2308,  2368,  2562,  2580,  4097,  4100,  4112,  4129,  4160,  4192,  4228,  4240,
+    4245,  4352,  4360,  4384,  4432,  4442,  4480,  4644,  4677,  5120,  5128,  5152,  5157,  5193,  5248,  5400,
+    5474,  5632,  5654,  6145,  6148,  6160,  6208,  6273,  6400,  6405,  6560,  6737,  8192,  8194,  8202,  8260,
+    8289,  8320,  8322,  8489,  8520,  8704,  8706,  9217,  9220,  9232,  9280,  9302,  9472,  9537,  9572,  9872,
+    10248, 10272, 10388, 10820, 16385, 16388, 16400, 16408, 16417, 16420, 16448, 16456, 16470, 16480, 16513, 16516,
+    16528, 16640, 16672, 16737, 16768, 16773, 16897, 16912, 16968, 16982, 17000, 17408, 17416, 17440, 17536, 17561,
+    17682, 17700, 17920, 18433, 18436, 18448, 18496, 18501, 18688, 18776, 18785, 18818, 19013, 19088, 20480, 20488,
+    20497, 20505, 20512, 20608, 20616, 20740, 20802, 20900, 21137, 21648, 21650, 21770, 22017, 22100, 22528, 22545,
+    22553, 22628, 22848, 23048, 24580, 24592, 24640, 24680, 24832, 24917, 25112, 25184, 25600, 25605, 25872, 25874,
+    25988, 26690, 32768, 32770, 32778, 32833, 32898, 33028, 33048, 33088, 33297, 33793, 33796, 33808, 33813, 33856,
+    33888, 34048, 34118, 34196, 34313, 34368, 34400, 34818, 35076, 35345, 36868, 36880, 36900, 36928, 37025, 37142,
+    37248, 37445, 37888, 37922, 37956, 38225, 39041, 39200, 40962, 41040, 41093, 41225, 41472, 42008, 43088, 43268,
+};
+
+constexpr GgmlTables make_tables() {
+  GgmlTables t{};
+  constexpr int8_t lane_value[4] = {0x08, 0x19, 0x2b, 0x00};
+  for (int i = 0; i < 256; ++i)
+    for (int j = 0; j < 8; ++j) t.grid[8 * i + j] = lane_value[(kGridCodes[i] >> (2 * j)) & 3];
+  for (int i = 0; i < 128; ++i) {
+    int parity = 0;
+    for (int b = 0; b < 7; ++b) parity ^= (i >> b) & 1;
+    const int ks = i | parity << 7;
+    for (int j = 0; j < 8; ++j) t.signs[8 * i + j] = (ks >> j) & 1 ? -1 : 1;
+  }
+  constexpr int8_t kv[8] = {0, 1, 2, 3, 4, 6, 8, 12};  // twice E2M1
+  for (int i = 0; i < 16; ++i) t.codebook[i] = (int8_t)(i & 8 ? -kv[i & 7] : kv[i & 7]);
+  for (int e = 0; e < 256; ++e)
+    t.scale[e] = __builtin_bit_cast(float, e < 2 ? 0x00200000u << e : (uint32_t)(e - 1) << 23);
+  return t;
+}
+
+
+// External linkage and not const: the device code object must keep the
+// symbol the host side registers (an internal const object that no kernel
+// reads is dropped from the device code, and its address cannot be looked up).
+__device__ GgmlTables g_weft_ggml_tables = make_tables();
+
+namespace {
+
+// Device address of the tables on the current device (one copy per device).
+const GgmlTables* device_tables() {
+  static std::mutex mu;
+  static std::vector<const GgmlTables*> addr;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if ((int)addr.size() <= dev) addr.resize(dev + 1, nullptr);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_weft_ggml_tables)) != hipSuccess) return nullptr;
+    addr[dev] = static_cast<const GgmlTables*>(p);
+  }
+  return addr[dev];
+}
+
+// ---------------------------------------------------------------- the op
+size_t row_size(const TypeInfo* t, int64_t ne) { return t->size * (size_t)(ne / t->blck); }
+
+hipError_t fail(hipError_t e) {
+  set_error(e);
+  return e;
+}
+
+bool nonneg(const weft_ggml_tensor* t) {
+  for (int i = 0; i < 4; ++i)
+    if (t->ne[i] < 0) return false;
+  return true;
+}
+
+hipError_t mul_mat(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1, const weft_ggml_tensor* d,
+                   void* wdata, size_t wsize) {
+  if (s0 == nullptr || s1 == nullptr || d == nullptr) return fail(hipErrorInvalidValue);
+  const TypeInfo* t0 = info(s0->type);
+  const TypeInfo* t1 = info(s1->type);
+  if (t0 == nullptr || t0->vec_dot < 0 || t1 == nullptr || d->type != WEFT_GGML_TYPE_F32)
+    return fail(hipErrorNotSupported);
+  const TypeInfo* vd = info(t0->vec_dot);
+  if (s1->type != WEFT_GGML_TYPE_F32 && s1->type != t0->vec_dot) return fail(hipErrorNotSupported);
+  if (!nonneg(s0) || !nonneg(s1) || !nonneg(d)) return fail(hipErrorInvalidValue);
+  // an empty dst is skipped before the op runs (ggml_compute_forward,
+  // ggml-cpu.c:1705)
+  if (d->ne[0] == 0 || d->ne[1] == 0 || d->ne[2] == 0 || d->ne[3] == 0) return hipSuccess;
+  // ggml_can_mul_mat (ggml.c:3234-3240) and the op's asserts (ggml-cpu.c:1266-1282)
+  const int64_t K = s0->ne[0], N = s0->ne[1];
+  if (s1->ne[0] != K || s0->ne[2] == 0 || s0->ne[3] == 0 || s1->ne[2] % s0->ne[2] != 0 ||
+      s1->ne[3] % s0->ne[3] != 0 || d->ne[0] != N || d->ne[1] != s1->ne[1] ||
+      d->ne[2] != s1->ne[2] || d->ne[3] != s1->ne[3] || K % t0->blck != 0 ||
+      s0->nb[0] != t0->size || s1->nb[0] != t1->size || d->nb[0] != sizeof(float) ||
+      d->nb[0] > d->nb[1] || d->nb[1] > d->nb[2] || d->nb[2] > d->nb[3])
+    return fail(hipErrorInvalidValue);
+  const int64_t M = s1->ne[1], ne12 = s1->ne[2], ne13 = s1->ne[3];
+  if (K == 0 || N == 0 || M == 0 || ne12 == 0 || ne13 == 0) return hipSuccess;
+  if (d->nb[1] % 4 != 0 || (s1->type == WEFT_GGML_TYPE_F32 && s1->nb[1] % 4 != 0))
+    return fail(hipErrorInvalidValue);
+  const bool quantize = s1->type == WEFT_GGML_TYPE_F32;
+  const size_t nbw1 = row_size(vd, K);
+  if (quantize) {
+    if (wdata == nullptr || !aligned(wdata, 4) || wsize < nbw1 * (size_t)(M * ne12 * ne13))
+      return fail(hipErrorInvalidValue);
+  } else if (M > 1 && s1->nb[1] != nbw1) {
+    return fail(hipErrorNotSupported);  // quantized src1 rows must be packed
+  }
+  const GgmlTables* tab = nullptr;
+  if (s0->type == WEFT_GGML_TYPE_IQ2_XXS || s0->type == WEFT_GGML_TYPE_MXFP4) {
+    tab = device_tables();
+    if (tab == nullptr) return fail(hipErrorInvalidDevice);
+  }
+  const int64_t r2 = ne12 / s0->ne[2], r3 = ne13 / s0->ne[3];
+  const RowStrides st{s0->nb[1], quantize ? s1->nb[1] / 4 : (size_t)K, d->nb[1] / 4};
+
+  // one call over all planes when src0 is one matrix and src1 / dst planes
+  // continue their rows (the usual batched activation)
+  int64_t mm = M, p2 = ne12, p3 = ne13;
+  if (s0->ne[2] == 1 && s0->ne[3] == 1 && (!quantize || (s1->nb[2] == (size_t)M * s1->nb[1] &&
+                                                         s1->nb[3] == (size_t)ne12 * s1->nb[2])) &&
+      (quantize || (s1->nb[2] == (size_t)M * nbw1 && s1->nb[3] == (size_t)ne12 * s1->nb[2])) &&
+      d->nb[2] == (size_t)M * d->nb[1] && d->nb[3] == (size_t)ne12 * d->nb[2]) {
+    mm = M * ne12 * ne13;
+    p2 = p3 = 1;
+  }
+  const size_t nbw2 = nbw1 * (size_t)M, nbw3 = nbw2 * (size_t)ne12;
+  for (int64_t i13 = 0; i13 < p3; ++i13)
+    for (int64_t i12 = 0; i12 < p2; ++i12) {
+      const uint8_t* W = static_cast<const uint8_t*>(s0->data) + (size_t)(i12 / r2) * s0->nb[2] +
+                         (size_t)(i13 / r3) * s0->nb[3];
+      const uint8_t* src1 =
+          static_cast<const uint8_t*>(s1->data) + (size_t)i12 * s1->nb[2] + (size_t)i13 * s1->nb[3];
+      float* Y = reinterpret_cast<float*>(static_cast<uint8_t*>(d->data) + (size_t)i12 * d->nb[2] +
+                                          (size_t)i13 * d->nb[3]);
+      const size_t n = (size_t)N, k = (size_t)K, m = (size_t)mm;
+      if (quantize) {
+        const float* X = reinterpret_cast<const float*>(src1);
+        uint8_t* Xq = static_cast<uint8_t*>(wdata) + (size_t)i12 * nbw2 + (size_t)i13 * nbw3;
+        switch (s0->type) {
+          case WEFT_GGML_TYPE_Q4_0: mul_mat_q4_0(W, X, Xq, Y, n, k, m, st); break;
+          case WEFT_GGML_TYPE_Q4_K: mul_mat_q4k(W, X, Xq, Y, n, k, m, st); break;
+          case WEFT_GGML_TYPE_IQ2_XXS:
+            mul_mat_iq2_xxs(W, X, Xq, tab->grid, tab->signs, Y, n, k, m, st);
+            break;
+          default: mul_mat_mxfp4(W, X, Xq, tab->codebook, tab->scale, Y, n, k, m, st); break;
+        }
+      } else {
+        switch (s0->type) {
+          case WEFT_GGML_TYPE_Q4_0: decode_quantized(0, W, src1, nullptr, nullptr, Y, n, k, m, st); break;
+          case WEFT_GGML_TYPE_Q4_K: mul_mat_q4k_quantized(W, src1, Y, n, k, m, st); break;
+          case WEFT_GGML_TYPE_IQ2_XXS:
+            mul_mat_iq2_xxs_quantized(W, src1, tab->grid, tab->signs, Y, n, k, m, st);
+            break;
+          default: decode_quantized(1, W, src1, tab->codebook, tab->scale, Y, n, k, m, st); break;
+        }
+      }
+      if (pending_error() != hipSuccess) return pending_error();
+    }
+  return pending_error();
+}
+
+}  // namespace
+}  // namespace weft
+
+extern "C" {
+
+size_t weft_ggml_type_size(int32_t type) {
+  const weft::TypeInfo* t = weft::info(type);
+  return t ? t->size : 0;
+}
+
+int64_t weft_ggml_blck_size(int32_t type) {
+  const weft::TypeInfo* t = weft::info(type);
+  return t ? t->blck : 0;
+}
+
+size_t weft_ggml_row_size(int32_t type, int64_t ne) {
+  const weft::TypeInfo* t = weft::info(type);
+  return t && ne >= 0 && ne % t->blck == 0 ? weft::row_size(t, ne) : 0;
+}
+
+int32_t weft_ggml_vec_dot_type(int32_t type) {
+  const weft::TypeInfo* t = weft::info(type);
+  return t ? t->vec_dot : -1;
+}
+
+size_t weft_ggml_mul_mat_work_size(const weft_ggml_tensor* src0, const weft_ggml_tensor* src1) {
+  if (src0 == nullptr || src1 == nullptr) return 0;
+  const weft::TypeInfo* t0 = weft::info(src0->type);
+  if (t0 == nullptr || t0->vec_dot < 0 || src1->type == t0->vec_dot) return 0;
+  int64_t n = 1;
+  for (int i = 0; i < 4; ++i) n *= src1->ne[i];
+  return weft_ggml_row_size(t0->vec_dot, n);
+}
+
+int weft_ggml_mul_mat(const weft_ggml_tensor* src0, const weft_ggml_tensor* src1,
+                      const weft_ggml_tensor* dst, void* wdata, size_t wsize) {
+  return (int)weft::mul_mat(src0, src1, dst, wdata, wsize);
+}
+
+}  // extern "C"

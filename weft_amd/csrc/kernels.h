@@ -6,32 +6,71 @@
 
 namespace weft {
 
+// Row strides of one mul_mat: bytes between weight rows (ldw), floats between
+// activation rows (ldx) and floats between output rows (ldy).  The reference
+// ABI's matrices are packed: {row bytes, K, N}.  GGML's MUL_MAT passes its
+// tensors' nb01, nb11 / 4 and nb1 / 4 (ggml-cpu/ggml-cpu.c:1245-1443).
+struct RowStrides {
+  size_t ldw, ldx, ldy;
+};
+
+inline RowStrides packed(size_t row_bytes, size_t K, size_t N) { return RowStrides{row_bytes, K, N}; }
+
+// Strides a launcher can take: rows at least as long as the packed ones
+// (only checked when there is a second row), weight rows at the Encoding's
+// alignment, and every byte offset representable.
+inline bool strides_ok(const RowStrides& st, size_t row_bytes, size_t w_align, size_t K, size_t N,
+                       size_t ny, size_t M) {
+  if (N > 1 && (st.ldw < row_bytes || st.ldw % w_align != 0)) return false;
+  if (M > 1 && (st.ldx < K || st.ldy < ny)) return false;
+  return st.ldw < ((size_t)1 << 40) && st.ldx < ((size_t)1 << 38) && st.ldy < ((size_t)1 << 38);
+}
+
 // Decode GEMV launchers (quantize X in-kernel, write Xq, any M).
 void decode_q4k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
-                size_t M);
+                size_t M, const RowStrides& st);
+// the same GEMV over an already quantized Q8_K activation (Xq read, not written)
+void decode_q4k_quantized(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K,
+                          size_t M, const RowStrides& st);
 void decode_q4_0(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
-                 size_t M);
+                 size_t M, const RowStrides& st);
 void decode_mxfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
-                  const float* scale, float* Y, size_t N, size_t K, size_t M);
+                  const float* scale, float* Y, size_t N, size_t K, size_t M, const RowStrides& st);
 void decode_iq2_xxs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,
-                    const int8_t* signs, float* Y, size_t N, size_t K, size_t M);
+                    const int8_t* signs, float* Y, size_t N, size_t K, size_t M,
+                    const RowStrides& st);
+// Q4_0 (fmt 0), MXFP4 (1) or IQ2_XXS (2) GEMV over an already quantized
+// activation (Q8_0 / Q8_0 / Q8_K records, read only)
+void decode_quantized(int fmt, const uint8_t* W, const uint8_t* Xq, const int8_t* tab0,
+                      const void* tab1, float* Y, size_t N, size_t K, size_t M,
+                      const RowStrides& st);
 
 // Q4_K mul_mat for any M: int8-MFMA GEMM for prefill shapes, GEMV otherwise.
 void mul_mat_q4k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
-                 size_t M);
+                 size_t M, const RowStrides& st);
+// the same over an already quantized Q8_K activation
+void mul_mat_q4k_quantized(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K,
+                           size_t M, const RowStrides& st);
 
 // Q4_0 / MXFP4 mul_mat for any M: int8-MFMA GEMM for prefill shapes, GEMV otherwise.
 void mul_mat_q4_0(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
-                  size_t M);
+                  size_t M, const RowStrides& st);
 void mul_mat_mxfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
-                   const float* scale, float* Y, size_t N, size_t K, size_t M);
+                   const float* scale, float* Y, size_t N, size_t K, size_t M, const RowStrides& st);
 
 // IQ2_XXS mul_mat for any M: int8-MFMA GEMM for prefill shapes, GEMV otherwise.
 void mul_mat_iq2_xxs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,
-                     const int8_t* signs, float* Y, size_t N, size_t K, size_t M);
+                     const int8_t* signs, float* Y, size_t N, size_t K, size_t M,
+                     const RowStrides& st);
+void mul_mat_iq2_xxs_quantized(const uint8_t* W, const uint8_t* Xq, const int8_t* grid,
+                               const int8_t* signs, float* Y, size_t N, size_t K, size_t M,
+                               const RowStrides& st);
 
-// Activation quantizers over K contiguous values.
+// Activation quantizers over K contiguous values, and over M rows of K
+// values ldx floats apart (records written contiguously).
 void quantize_q8_k(const float* X, uint8_t* Y, size_t K);
 void quantize_q8_0(const float* X, uint8_t* Y, size_t K);
+void quantize_q8_k_rows(const float* X, size_t ldx, uint8_t* Y, size_t M, size_t K);
+void quantize_q8_0_rows(const float* X, size_t ldx, uint8_t* Y, size_t M, size_t K);
 
 }  // namespace weft

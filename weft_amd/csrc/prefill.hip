@@ -8,39 +8,43 @@
 // (small M, unaligned weights, K that does not fill the GEMM's staging unit).
 #include "kernels.h"
 #include "runtime.h"
+#include "weft_common.h"
 #include "weft_hip.h"
 
 extern "C" {
 
 void production_mul_mat_q4_0(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N,
                              size_t K, size_t M) {
-  weft::mul_mat_q4_0(W, X, Xq, Y, N, K, M);
+  weft::mul_mat_q4_0(W, X, Xq, Y, N, K, M, weft::packed(K / 32 * weft::kQ4_0Bytes, K, N));
 }
 
 void production_mul_mat_q4_k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N,
                              size_t K, size_t M) {
-  weft::mul_mat_q4k(W, X, Xq, Y, N, K, M);
+  weft::mul_mat_q4k(W, X, Xq, Y, N, K, M, weft::packed(K / 256 * weft::kQ4_KBytes, K, N));
 }
 
 void production_mul_mat_q4_k_staged(const uint8_t* W, const float* X, uint8_t* Xq, float* Y,
                                     size_t N, size_t K, size_t M) {
-  weft::mul_mat_q4k(W, X, Xq, Y, N, K, M);
+  weft::mul_mat_q4k(W, X, Xq, Y, N, K, M, weft::packed(K / 256 * weft::kQ4_KBytes, K, N));
 }
 
 void production_mul_mat_iq2_xxs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,
                                 const int8_t* signs, float* Y, size_t N, size_t K, size_t M) {
-  weft::mul_mat_iq2_xxs(W, X, Xq, grid, signs, Y, N, K, M);
+  weft::mul_mat_iq2_xxs(W, X, Xq, grid, signs, Y, N, K, M,
+                        weft::packed(K / 256 * weft::kIq2xxsBytes, K, N));
 }
 
 void production_mul_mat_iq2_xxs_staged(const uint8_t* W, const float* X, uint8_t* Xq,
                                        const int8_t* grid, const int8_t* signs, float* Y, size_t N,
                                        size_t K, size_t M) {
-  weft::mul_mat_iq2_xxs(W, X, Xq, grid, signs, Y, N, K, M);
+  weft::mul_mat_iq2_xxs(W, X, Xq, grid, signs, Y, N, K, M,
+                        weft::packed(K / 256 * weft::kIq2xxsBytes, K, N));
 }
 
 void production_mul_mat_mxfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
                               const float* scale, float* Y, size_t N, size_t K, size_t M) {
-  weft::mul_mat_mxfp4(W, X, Xq, codebook, scale, Y, N, K, M);
+  weft::mul_mat_mxfp4(W, X, Xq, codebook, scale, Y, N, K, M,
+                      weft::packed(K / 32 * weft::kMxfp4Bytes, K, N));
 }
 
 }  // extern "C"

@@ -51,6 +51,8 @@ struct GemmArgs {
   const int8_t* signs;  // 128 x 8 (+-1)
   float* Y;
   int N, K, M;
+  size_t ldw;     // bytes between weight rows
+  long long ldy;  // floats between output rows
 };
 
 // Direct global->LDS loads; lane l writes [lds + size*l, +size).  Inline asm
@@ -101,7 +103,7 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
   const int col = lane & 31, kg = lane >> 5;
   const int nsb = a.K >> 8;
   const int npair = nsb >> 1;  // nsb is even on this path
-  const size_t wrb = (size_t)nsb * kIq2xxsBytes;
+  const size_t wrb = a.ldw;
   const size_t xrb = (size_t)nsb * kQ8_KBytes;
 
   int m0, n0;  // XCD-aware tile order (workgroups are dealt round-robin to 8 XCDs)
@@ -250,28 +252,50 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int gm = m0 + 32 * t + 8 * (r >> 2) + 4 * kg + (r & 3);
-        if (gm < a.M) a.Y[(size_t)gm * a.N + gn] = 0.125f * (y[t][r] + red[(16 * t + r) * 64]);
+        if (gm < a.M) a.Y[(size_t)gm * a.ldy + gn] = 0.125f * (y[t][r] + red[(16 * t + r) * 64]);
       }
   }
+}
+
+
+bool gemm_iq2_ok(const uint8_t* W, const void* Xq, const float* Y, const int8_t* grid,
+                 const int8_t* signs, size_t N, size_t K, size_t M, const RowStrides& st) {
+  // MFMA path: prefill shapes with an even number of superblocks per row and
+  // 4-byte aligned weight rows; the GEMV kernels take everything else
+  const size_t ldw = N > 1 ? st.ldw : K / 256 * kIq2xxsBytes;
+  return M >= 16 && N > 0 && K > 0 && K % 512 == 0 && W != nullptr && Xq != nullptr &&
+         Y != nullptr && grid != nullptr && signs != nullptr && aligned(W, 4) && ldw % 4 == 0 &&
+         aligned(Xq, 4) && aligned(Y, 4) && N <= (size_t)INT32_MAX && K <= (size_t)INT32_MAX &&
+         M <= (size_t)INT32_MAX && strides_ok(st, K / 256 * kIq2xxsBytes, 2, K, N, N, M) &&
+         ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT) <= (size_t)INT32_MAX;
+}
+
+void gemm_iq2(const uint8_t* W, const uint8_t* Xq, const int8_t* grid, const int8_t* signs, float* Y,
+              size_t N, size_t K, size_t M, const RowStrides& st) {
+  const size_t ldw = N > 1 ? st.ldw : K / 256 * kIq2xxsBytes;
+  GemmArgs ga{W, Xq, grid, signs, Y, (int)N, (int)K, (int)M, ldw, (long long)st.ldy};
+  const size_t tiles = ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT);
+  iq2_mfma_gemm<<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(ga);
+  check_launch();
 }
 
 }  // namespace
 
 void mul_mat_iq2_xxs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,
-                     const int8_t* signs, float* Y, size_t N, size_t K, size_t M) {
-  // MFMA path: prefill shapes with an even number of superblocks per row and
-  // 4-byte aligned weights; the GEMV kernels take everything else
-  const bool mfma = M >= 16 && N > 0 && K > 0 && K % 512 == 0 && W != nullptr && X != nullptr &&
-                    Xq != nullptr && Y != nullptr && grid != nullptr && signs != nullptr &&
-                    aligned(W, 4) && aligned(Xq, 4) && aligned(Y, 4) && aligned(X, 4) &&
-                    N <= (size_t)INT32_MAX && K <= (size_t)INT32_MAX && M <= (size_t)INT32_MAX &&
-                    ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT) <= (size_t)INT32_MAX;
-  if (!mfma) return decode_iq2_xxs(W, X, Xq, grid, signs, Y, N, K, M);
-  quantize_q8_k(X, Xq, M * K);
-  GemmArgs ga{W, Xq, grid, signs, Y, (int)N, (int)K, (int)M};
-  const size_t tiles = ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT);
-  iq2_mfma_gemm<<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(ga);
-  check_launch();
+                     const int8_t* signs, float* Y, size_t N, size_t K, size_t M,
+                     const RowStrides& st) {
+  if (X == nullptr || !aligned(X, 4) || !gemm_iq2_ok(W, Xq, Y, grid, signs, N, K, M, st))
+    return decode_iq2_xxs(W, X, Xq, grid, signs, Y, N, K, M, st);
+  quantize_q8_k_rows(X, st.ldx, Xq, M, K);
+  gemm_iq2(W, Xq, grid, signs, Y, N, K, M, st);
+}
+
+void mul_mat_iq2_xxs_quantized(const uint8_t* W, const uint8_t* Xq, const int8_t* grid,
+                               const int8_t* signs, float* Y, size_t N, size_t K, size_t M,
+                               const RowStrides& st) {
+  if (!gemm_iq2_ok(W, Xq, Y, grid, signs, N, K, M, st))
+    return decode_quantized(2, W, Xq, grid, signs, Y, N, K, M, st);
+  gemm_iq2(W, Xq, grid, signs, Y, N, K, M, st);
 }
 
 }  // namespace weft

@@ -91,6 +91,8 @@ struct GemmArgs {
   const uint8_t* Xq;
   float* Y;
   int N, K, M;
+  uint32_t ldw;   // bytes between weight rows (a tile's 128 rows stay in 32-bit offsets)
+  long long ldy;  // floats between output rows
 };
 
 // Direct global->LDS load of 16 bytes per lane: lane l reads sbase + voff
@@ -159,7 +161,7 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
   if (wave >= kMfmaWaves) {
     // ---------------------------------------------------------- loader wave
     const int par = wave - kMfmaWaves;
-    const uint32_t wrb = (uint32_t)nsb * kQ4_KBytes;
+    const uint32_t wrb = a.ldw;
     const uint32_t xrb = (uint32_t)nsb * kQ8_KBytes;
     const uint8_t* xbase = a.Xq + (size_t)m0 * xrb;
     const uint8_t* wbase = a.W + (size_t)n0 * wrb;
@@ -357,36 +359,58 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int gm = m0 + 32 * t + 8 * (r >> 2) + 4 * kg + (r & 3);
-        if (gm < a.M) a.Y[(size_t)gm * a.N + gn] = y[t][r] + red[(16 * t + r) * 64];
+        if (gm < a.M) a.Y[(size_t)gm * a.ldy + gn] = y[t][r] + red[(16 * t + r) * 64];
       }
   }
 }
 
-void prefill_q4k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
-                 size_t M) {
-  if (N == 0 || M == 0 || K == 0) return;
-  if (K % 256 || W == nullptr || X == nullptr || Xq == nullptr || Y == nullptr || !aligned(W, 4) ||
-      !aligned(Xq, 4) || !aligned(Y, 4) || N > (size_t)INT32_MAX || K > (size_t)INT32_MAX ||
-      M > (size_t)INT32_MAX || ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT) > (size_t)INT32_MAX) {
-    set_error(hipErrorInvalidValue);
-    return;
-  }
-  quantize_q8_k(X, Xq, M * K);
-  GemmArgs a{W, Xq, Y, (int)N, (int)K, (int)M};
+// The GEMM over an already quantized activation.  Weight rows must be
+// 4-byte aligned (dword direct-to-LDS loads) and a tile's 128 rows must stay
+// within 32-bit offsets.
+bool gemm_q4k_ok(const uint8_t* W, size_t N, size_t K, size_t M, const RowStrides& st) {
+  const size_t rb = K / 256 * kQ4_KBytes;
+  const size_t ldw = N > 1 ? st.ldw : rb;
+  return aligned(W, 4) && ldw % 4 == 0 && (kNT - 1) * ldw + rb < ((size_t)1 << 32) &&
+         N <= (size_t)INT32_MAX && K <= (size_t)INT32_MAX && M <= (size_t)INT32_MAX &&
+         ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT) <= (size_t)INT32_MAX;
+}
+
+void gemm_q4k(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K, size_t M,
+              const RowStrides& st) {
+  const size_t rb = K / 256 * kQ4_KBytes;
+  GemmArgs a{W, Xq, Y, (int)N, (int)K, (int)M, (uint32_t)(N > 1 ? st.ldw : rb), (long long)st.ldy};
   const size_t tiles = ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT);
   q4k_mfma_gemm<<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(a);
   check_launch();
+}
+
+bool args_ok(const uint8_t* W, const void* Xq, const float* Y, size_t N, size_t K, size_t M,
+             const RowStrides& st) {
+  return K % 256 == 0 && W != nullptr && Xq != nullptr && Y != nullptr && aligned(Xq, 4) &&
+         aligned(Y, 4) && strides_ok(st, K / 256 * kQ4_KBytes, 2, K, N, N, M);
 }
 
 }  // namespace
 
 // Prefill entry: MFMA GEMM when the shape suits it, the decode GEMV otherwise.
 void mul_mat_q4k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
-                 size_t M) {
-  if (M >= 16 && aligned(W, 4))
-    prefill_q4k(W, X, Xq, Y, N, K, M);
+                 size_t M, const RowStrides& st) {
+  if (N == 0 || M == 0 || K == 0) return;
+  if (M >= 16 && X != nullptr && args_ok(W, Xq, Y, N, K, M, st) && gemm_q4k_ok(W, N, K, M, st)) {
+    quantize_q8_k_rows(X, st.ldx, Xq, M, K);
+    gemm_q4k(W, Xq, Y, N, K, M, st);
+  } else {
+    decode_q4k(W, X, Xq, Y, N, K, M, st);
+  }
+}
+
+void mul_mat_q4k_quantized(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K,
+                           size_t M, const RowStrides& st) {
+  if (N == 0 || M == 0 || K == 0) return;
+  if (M >= 16 && args_ok(W, Xq, Y, N, K, M, st) && gemm_q4k_ok(W, N, K, M, st))
+    gemm_q4k(W, Xq, Y, N, K, M, st);
   else
-    decode_q4k(W, X, Xq, Y, N, K, M);
+    decode_q4k_quantized(W, Xq, Y, N, K, M, st);
 }
 
 }  // namespace weft

@@ -67,6 +67,8 @@ struct GemmArgs {
   const float* scale;
   float* Y;
   int N, K, M;
+  size_t ldw;     // bytes between weight rows
+  long long ldy;  // floats between output rows
 };
 
 // 16 bytes per lane from global straight into LDS: lane l writes
@@ -144,7 +146,7 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
   const int col = lane & 31, kg = lane >> 5;
   const int nst = a.K >> 8;                         // stages (8 blocks each)
   const size_t xs = (size_t)a.K + (size_t)a.K / 16;  // planar activation row stride
-  const size_t ws_row = (size_t)(a.K / 32) * T::kRec;
+  const size_t ws_row = a.ldw;
 
   // XCD-aware tile order (workgroups are dealt round-robin to 8 XCDs)
   int m0, n0;
@@ -318,7 +320,7 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int gm = m0 + 32 * t + 8 * (r >> 2) + 4 * kg + (r & 3);
-        if (gm < a.M) a.Y[(size_t)gm * a.N + gn] = y[t][r] + red[(16 * t + r) * 64];
+        if (gm < a.M) a.Y[(size_t)gm * a.ldy + gn] = y[t][r] + red[(16 * t + r) * 64];
       }
   }
 }
@@ -359,22 +361,22 @@ __device__ __forceinline__ bool ggml_mxfp4_entry(const int8_t* codebook, const f
 // the int8 values are stored as sign and magnitude and in that GEMM's K
 // order: byte 2i of a block holds element i, byte 2i + 1 element i + 16.
 template <bool kMx>
-__global__ void __launch_bounds__(256) q80_planar_kernel(const float* __restrict__ X,
-                                                         uint8_t* __restrict__ Xp, long long nb,
-                                                         int bpr, long long xs, const int8_t* codebook,
-                                                         const float* scale) {
+__global__ void __launch_bounds__(256) q80_planar_kernel(const float* __restrict__ X, long long ldx,
+                                                         bool a16, uint8_t* __restrict__ Xp,
+                                                         long long nb, int bpr, long long xs,
+                                                         const int8_t* codebook, const float* scale) {
   bool kord = false;
   if constexpr (kMx) kord = __syncthreads_and(ggml_mxfp4_entry(codebook, scale, threadIdx.x)) != 0;
   const int lane = threadIdx.x & (kWave - 1);
   const long long wave = ((long long)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
   const long long nwaves = (long long)gridDim.x * blockDim.x / kWave;
   const long long steps = (nb + 7) / 8;
-  const bool a16 = (reinterpret_cast<uintptr_t>(X) & 15) == 0;
   for (long long s = wave; s < steps; s += nwaves) {
     const long long b = 8 * s + lane / 8;
     const bool live = b < nb;
+    const long long row = b / bpr, blk = b - row * bpr;
     float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (live) x = ldx4(X + b * 32 + 4 * (lane & 7), a16);
+    if (live) x = ldx4(X + row * ldx + 32 * blk + 4 * (lane & 7), a16);
     const Q8_0Lane r = q80_quantize_8lanes(x);
     uint32_t word = (uint32_t)pack4_i8(r.q);
     int at = 4 * (lane & 7);
@@ -390,7 +392,6 @@ __global__ void __launch_bounds__(256) q80_planar_kernel(const float* __restrict
       at = 8 * (lane & 3) + (upper ? 4 : 0);
     }
     if (!live) continue;
-    const long long row = b / bpr, blk = b - row * bpr;
     uint8_t* rp = Xp + row * xs;
     *reinterpret_cast<uint32_t*>(rp + 32 * blk + at) = word;
     if ((lane & 7) == 0) *reinterpret_cast<uint16_t*>(rp + (long long)bpr * 32 + 2 * blk) = (uint16_t)r.dh;
@@ -474,7 +475,7 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
   const int col = lane & 31, h = lane >> 5;
   const int nst = a.K >> 8;
   const uint32_t xs = (uint32_t)a.K + (uint32_t)a.K / 16;  // planar activation row stride
-  const uint32_t ws_row = (uint32_t)(a.K / 32) * kMxfp4Bytes;
+  const uint32_t ws_row = (uint32_t)a.ldw;  // the host keeps a tile's rows in 32-bit offsets
 
   int m0, n0;
   {
@@ -616,7 +617,7 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
   __syncthreads();
   const int q = ph, th = q >> 1, ct = q & 1;
   const int gm = m0 + 32 * th + col;
-  const bool v4 = (a.N & 3) == 0 && (reinterpret_cast<uintptr_t>(a.Y) & 15) == 0;
+  const bool v4 = (a.ldy & 3) == 0 && (reinterpret_cast<uintptr_t>(a.Y) & 15) == 0;
 #pragma unroll
   for (int r4 = 0; r4 < 4; ++r4) {
     float4 v = red[(((cp + 0) * 4 + q) * 4 + r4) * 64 + lane];
@@ -631,7 +632,7 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
     // register r holds weight row 8*(r/4) + 4*h + r%4 of the tile
     const int gn = n0 + 64 * cp + 32 * ct + 8 * r4 + 4 * h;
     if (gm < a.M) {
-      float* yr = a.Y + (size_t)gm * a.N;
+      float* yr = a.Y + (size_t)gm * a.ldy;
       if (v4 && gn + 3 < a.N) {
         *reinterpret_cast<float4*>(yr + gn) = v;
       } else {
@@ -660,10 +661,17 @@ __global__ void __launch_bounds__(kThreads, 1) mxfp4_gemm(GemmArgs a) {
 
 template <WFmt F>
 bool prefill_q80(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
-                 const float* scale, float* Y, size_t N, size_t K, size_t M) {
-  // MFMA path preconditions; otherwise the caller runs the GEMV kernels
-  if (M < 16 || K % 256 || !aligned(W, 4) || !aligned(Xq, 16) || !aligned(Y, 4) ||
-      !aligned(X, 4) || N > (size_t)INT32_MAX || K > (size_t)INT32_MAX || M > (size_t)INT32_MAX ||
+                 const float* scale, float* Y, size_t N, size_t K, size_t M, const RowStrides& st) {
+  using T = WTraits<F>;
+  const size_t rb = K / 32 * T::kRec;
+  const size_t ldw = N > 1 ? st.ldw : rb;
+  // MFMA path preconditions; otherwise the caller runs the GEMV kernels.
+  // Weight rows feed dword direct-to-LDS loads (4-byte aligned) and a tile's
+  // rows must stay within 32-bit offsets.
+  if (M < 16 || K % 256 || !aligned(W, 4) || ldw % 4 != 0 || (kNT - 1) * ldw + rb >= ((size_t)1 << 32) ||
+      !aligned(Xq, 16) || !aligned(Y, 4) || !aligned(X, 4) || N > (size_t)INT32_MAX ||
+      K > (size_t)INT32_MAX || M > (size_t)INT32_MAX ||
+      !strides_ok(st, rb, 1, K, N, N, M) ||
       ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT) > (size_t)INT32_MAX)
     return false;
   if (F == WFmt::MXFP4 && (codebook == nullptr || scale == nullptr)) return false;
@@ -671,37 +679,39 @@ bool prefill_q80(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* co
   const long long xs = (long long)(K + K / 16);
   const long long waves = (nb + 7) / 8;
   const int grid = (int)std::max<long long>(1, std::min<long long>((long long)cu_count() * 8, (waves + 3) / 4));
-  q80_planar_kernel<F == WFmt::MXFP4>
-      <<<grid, 256, 0, current_stream()>>>(X, Xq, nb, (int)(K / 32), xs, codebook, scale);
+  const size_t ldx = M > 1 ? st.ldx : K;
+  const bool a16 = aligned(X, 16) && ldx % 4 == 0;
+  q80_planar_kernel<F == WFmt::MXFP4><<<grid, 256, 0, current_stream()>>>(
+      X, (long long)ldx, a16, Xq, nb, (int)(K / 32), xs, codebook, scale);
   check_launch();
   const size_t tiles = ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT);
-  GemmArgs ga{W, Xq, codebook, scale, Y, (int)N, (int)K, (int)M};
+  GemmArgs ga{W, Xq, codebook, scale, Y, (int)N, (int)K, (int)M, ldw, (long long)st.ldy};
   if constexpr (F == WFmt::MXFP4) {
     mxfp4_gemm<<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(ga);
   } else {
     q80_mfma_gemm<F><<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(ga);
   }
   check_launch();
-  quantize_q8_0(X, Xq, M * K);  // Xq ends in GGML's record layout
+  quantize_q8_0_rows(X, ldx, Xq, M, K);  // Xq ends in GGML's record layout
   return true;
 }
 
 }  // namespace
 
 void mul_mat_q4_0(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
-                  size_t M) {
-  if (N == 0 || M == 0 || K == 0) return decode_q4_0(W, X, Xq, Y, N, K, M);
+                  size_t M, const RowStrides& st) {
+  if (N == 0 || M == 0 || K == 0) return decode_q4_0(W, X, Xq, Y, N, K, M, st);
   if (W == nullptr || X == nullptr || Xq == nullptr || Y == nullptr ||
-      !prefill_q80<WFmt::Q4_0>(W, X, Xq, nullptr, nullptr, Y, N, K, M))
-    decode_q4_0(W, X, Xq, Y, N, K, M);
+      !prefill_q80<WFmt::Q4_0>(W, X, Xq, nullptr, nullptr, Y, N, K, M, st))
+    decode_q4_0(W, X, Xq, Y, N, K, M, st);
 }
 
 void mul_mat_mxfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
-                   const float* scale, float* Y, size_t N, size_t K, size_t M) {
-  if (N == 0 || M == 0 || K == 0) return decode_mxfp4(W, X, Xq, codebook, scale, Y, N, K, M);
+                   const float* scale, float* Y, size_t N, size_t K, size_t M, const RowStrides& st) {
+  if (N == 0 || M == 0 || K == 0) return decode_mxfp4(W, X, Xq, codebook, scale, Y, N, K, M, st);
   if (W == nullptr || X == nullptr || Xq == nullptr || Y == nullptr ||
-      !prefill_q80<WFmt::MXFP4>(W, X, Xq, codebook, scale, Y, N, K, M))
-    decode_mxfp4(W, X, Xq, codebook, scale, Y, N, K, M);
+      !prefill_q80<WFmt::MXFP4>(W, X, Xq, codebook, scale, Y, N, K, M, st))
+    decode_mxfp4(W, X, Xq, codebook, scale, Y, N, K, M, st);
 }
 
 }  // namespace weft

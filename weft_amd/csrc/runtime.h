@@ -14,6 +14,8 @@ hipStream_t current_stream();
 void set_error(hipError_t e);
 // Check the launch just made and record its error, if any.
 void check_launch();
+// The calling thread's recorded error, left in place.
+hipError_t pending_error();
 // Compute units of the current device (cached per device).
 int cu_count();
 // Largest dynamic LDS a workgroup may request on the current device.

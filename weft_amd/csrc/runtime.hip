@@ -55,6 +55,8 @@ void set_error(hipError_t e) {
 
 void check_launch() { set_error(hipGetLastError()); }
 
+hipError_t pending_error() { return t_error; }
+
 int cu_count() { return facts().cus; }
 
 size_t max_lds_per_block() { return facts().lds; }
