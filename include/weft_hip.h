@@ -198,6 +198,17 @@ size_t weft_ggml_mul_mat_work_size(const weft_ggml_tensor *src0, const weft_ggml
  * 4-byte aligned, ends holding src1 quantized as GGML's wdata would */
 int weft_ggml_mul_mat(const weft_ggml_tensor *src0, const weft_ggml_tensor *src1,
                       const weft_ggml_tensor *dst, void *wdata, size_t wsize);
+/* MUL_MAT_ID's work size in ggml_graph_plan (ggml-cpu.c:2827-2845, cache line 64) */
+size_t weft_ggml_mul_mat_id_work_size(const weft_ggml_tensor *src0, const weft_ggml_tensor *src1,
+                                      const weft_ggml_tensor *ids);
+/* GGML_OP_MUL_MAT_ID (ggml-cpu.c:1454-1698; shapes of ggml_mul_mat_id,
+ * ggml/src/ggml.c:3293-3317): src0 = n_as expert matrices (ne02), ids = I32
+ * expert choices (n_ids x n_tokens), dst (ne01, n_ids, n_tokens).  Every
+ * (slot, token) pair runs in one launch, its expert read from ids on the
+ * device; an id outside [0, n_as) (a GGML assert) leaves its dst row untouched. */
+int weft_ggml_mul_mat_id(const weft_ggml_tensor *src0, const weft_ggml_tensor *src1,
+                         const weft_ggml_tensor *ids, const weft_ggml_tensor *dst, void *wdata,
+                         size_t wsize);
 
 #ifdef __cplusplus
 }

@@ -91,3 +91,41 @@ def test_empty_product_launches_nothing():
     s0, _, _ = ok_args()
     G.mul_mat(s0, G.tensor(G.F32, (512, 0), data=2 << 20), G.tensor(G.F32, (64, 0), data=3 << 20))
     assert _lib.load().weft_hip_get_last_error() == 0
+
+
+# ---------------------------------------------------------------- MUL_MAT_ID
+def moe_args(t=G.Q4_K, k=512, n=64, n_as=8, n_ids=4, ne11=1, n_tok=3):
+    return (G.tensor(t, (k, n, n_as), data=1 << 20),
+            G.tensor(G.F32, (k, ne11, n_tok), data=2 << 20),
+            G.tensor(G.I32, (n_ids, n_tok), data=4 << 20),
+            G.tensor(G.F32, (n, n_ids, n_tok), data=3 << 20))
+
+
+def test_mul_mat_id_work_size_is_the_graph_plan_size():
+    # ggml-cpu.c:2827-2845 with CACHE_LINE_SIZE 64 and 8-byte row mappings
+    s0, s1, ids, _ = moe_args(n_as=8, n_ids=4, ne11=1, n_tok=3)
+    want = G.row_size(G.Q8_K, 512 * 3) + 8 + 8 * 8 + 8 + 8 * 4 * 3 * 8 + 8 + 64 * 8 + 64
+    assert G.mul_mat_id_work_size(s0, s1, ids) == want
+    q = G.tensor(G.Q8_K, (512, 1, 3))
+    assert G.mul_mat_id_work_size(s0, q, ids) == want - G.row_size(G.Q8_K, 512 * 3) - 8
+
+
+def call_id(s0, s1, ids, d, wdata=1 << 30, wsize=1 << 30):
+    with pytest.raises(_lib.HipError) as e:
+        G.mul_mat_id(s0, s1, ids, d, wdata, wsize)
+    assert _lib.load().weft_hip_get_last_error() == 0
+    return e.value.code
+
+
+def test_mul_mat_id_asserts_become_invalid_value():
+    s0, s1, ids, d = moe_args()
+    f32_ids = G.tensor(G.F32, (4, 3), data=4 << 20)
+    assert call_id(s0, s1, f32_ids, d) == INVALID                                  # ids not I32
+    assert call_id(s0, s1, G.tensor(G.I32, (4, 2), data=4 << 20), d) == INVALID   # ids ne1 != tokens
+    assert call_id(s0, G.tensor(G.F32, (512, 3, 3), data=2 << 20), ids,
+                   G.tensor(G.F32, (64, 4, 3), data=3 << 20)) == INVALID          # n_ids % ne11
+    assert call_id(s0, s1, ids, G.tensor(G.F32, (64, 3, 3), data=3 << 20)) == INVALID  # dst ne1
+    assert call_id(G.tensor(G.Q4_K, (512, 64, 8, 2), data=1 << 20), s1, ids, d) == INVALID  # 4-d src0
+    assert call_id(s0, s1, ids, d, wsize=G.row_size(G.Q8_K, 512 * 3) - 1) == INVALID
+    assert call_id(G.tensor(3, (512, 64, 8), data=1 << 20, nb=[20, 320, 320 * 64, 0]), s1, ids,
+                   d) == NOT_SUPPORTED

@@ -117,3 +117,75 @@ def test_batched_planes_collapse(hip, fmt):
 @pytest.mark.parametrize("m", [1, 33])
 def test_prequantized_src1(hip, fmt, m):
     run(hip, fmt, 512, 128, m, planes1=(2, 1), prequant=True)
+
+
+# ---------------------------------------------------------------- MUL_MAT_ID
+def run_id(hip, fmt, k, n, n_as, n_ids, ne11, n_tok, ids, pad_w=0, prequant=False, seed=11):
+    """ids: (n_tok, n_ids) int32 expert choices; entries outside [0, n_as)
+    must leave their dst rows untouched."""
+    hip.torch.cuda.synchronize()
+    rb = o.record_bytes(fmt, k)
+    act = o.ACT_OF[fmt]
+    rq = o.record_bytes(act, k)
+    w = np.stack([o.quantize(fmt, o.seeded_normal(seed + e, (n, k), 0.02)) for e in range(n_as)])
+    w_host = np.full((n_as, n, rb + pad_w), 0x5A, np.uint8)
+    w_host[..., :rb] = w
+    x = o.seeded_normal(seed + 500, (n_tok, ne11, k))
+    xq = np.stack([o.quantize(act, x[t]) for t in range(n_tok)])  # (n_tok, ne11, rq)
+    if prequant:
+        xd = hip.to_dev(xq)
+        s1 = G.tensor(VDT[fmt], (k, ne11, n_tok), xd.ptr)
+    else:
+        xd = hip.to_dev(x)
+        s1 = G.tensor(G.F32, (k, ne11, n_tok), xd.ptr)
+    wd = hip.to_dev(w_host)
+    idd = hip.to_dev(np.ascontiguousarray(ids, dtype=np.int32))
+    yd = hip.empty(4 * n * n_ids * n_tok)
+    yd.t[:yd.nbytes].view(hip.torch.int32).fill_(NAN)
+    s0 = G.tensor(TYPE[fmt], (k, n, n_as), wd.ptr,
+                  [G.type_size(TYPE[fmt]), rb + pad_w, (rb + pad_w) * n, (rb + pad_w) * n * n_as])
+    it = G.tensor(G.I32, (n_ids, n_tok), idd.ptr)
+    d = G.tensor(G.F32, (n, n_ids, n_tok), yd.ptr)
+    wsize = G.mul_mat_id_work_size(s0, s1, it)
+    wdata = hip.empty(wsize, fill=0xA5)
+    print(f"ggml mul_mat_id {fmt} k={k} n={n} n_as={n_as} n_ids={n_ids} ne11={ne11} "
+          f"n_tok={n_tok} pad_w={pad_w} prequant={prequant}", flush=True)
+    G.mul_mat_id(s0, s1, it, d, wdata.ptr, wsize)
+    hip.torch.cuda.synchronize()
+    assert hip.last_error() == 0
+    y = yd.numpy(np.float32).reshape(n_tok, n_ids, n)
+    wq = None if prequant else wdata.numpy(np.uint8)[:n_tok * ne11 * rq].reshape(n_tok, ne11, rq)
+    for t in range(n_tok):
+        for s in range(n_ids):
+            e = int(ids[t, s])
+            if not 0 <= e < n_as:
+                assert (y[t, s].view(np.int32) == NAN).all(), f"pair {t},{s} with id {e} written"
+                continue
+            want_e, want_a = o.mul_mat_f64(fmt, w[e], xq[t, s % ne11][None], n, k, 1)
+            ok = o.within_tolerance(y[t, s][None], want_e, want_a)
+            assert ok.all(), f"pair {t},{s} expert {e}: {int((~ok).sum())} outside tolerance"
+        if wq is not None:
+            for r in range(ne11):
+                if 0 <= int(ids[t, r]) < n_as:  # the row's writer pair ran
+                    np.testing.assert_array_equal(wq[t, r], xq[t, r], err_msg=f"wdata row {t},{r}")
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_mul_mat_id_decode(hip, fmt):
+    # one token, 4 of 8 experts, the activation broadcast to every slot
+    run_id(hip, fmt, 1024, 256, 8, 4, 1, 1, np.array([[5, 0, 7, 2]]))
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_mul_mat_id_tokens_and_invalid_ids(hip, fmt):
+    rng = np.random.default_rng(3)
+    ids = rng.integers(0, 6, size=(7, 2))
+    ids[2, 1] = -1
+    ids[5, 0] = 6
+    run_id(hip, fmt, 512, 96, 6, 2, 2, 7, ids)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_mul_mat_id_prequantized_and_strided(hip, fmt):
+    ids = np.array([[1, 3, 0], [2, 2, 1]])
+    run_id(hip, fmt, 512, 64, 4, 3, 1, 2, ids, pad_w=1 if fmt == "mxfp4" else 2, prequant=True)

@@ -88,7 +88,9 @@ def _bind_ggml(lib: ctypes.CDLL) -> None:
                             ("weft_ggml_row_size", [i32, i64], sz),
                             ("weft_ggml_vec_dot_type", [i32], i32),
                             ("weft_ggml_mul_mat_work_size", [vp, vp], sz),
-                            ("weft_ggml_mul_mat", [vp, vp, vp, vp, sz], ctypes.c_int)):
+                            ("weft_ggml_mul_mat", [vp, vp, vp, vp, sz], ctypes.c_int),
+                            ("weft_ggml_mul_mat_id_work_size", [vp, vp, vp], sz),
+                            ("weft_ggml_mul_mat_id", [vp, vp, vp, vp, vp, sz], ctypes.c_int)):
         fn = getattr(lib, name)
         fn.argtypes, fn.restype = args, res
 

@@ -29,6 +29,7 @@
 
 #include "activation.h"
 #include "kernels.h"
+#include "pairs.h"
 #include "runtime.h"
 #include "weft_hip.h"
 
@@ -48,6 +49,7 @@ struct Q4KArgs {
   long long y_stride;    // elements between output rows
   size_t ldw;            // bytes between weight rows
   size_t ldx;            // elements between activation rows
+  PairArgs pair;         // MUL_MAT_ID pairs (pair.ids null: none)
 };
 
 template <bool A16>
@@ -68,6 +70,7 @@ __device__ __forceinline__ uint4 load16(const uint8_t* p) {
 // MB: compile-time bound on the activation rows of one launch (a.mb <= MB).
 template <bool A16, int MB, int NT>
 __global__ void __launch_bounds__(NT) q4k_gemv_kernel(Q4KArgs a) {
+  if (a.pair.ids != nullptr && !resolve_pair(a)) return;
   extern __shared__ __align__(16) char lds[];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -210,6 +213,7 @@ __global__ void __launch_bounds__(NT) q4k_gemv_kernel(Q4KArgs a) {
 template <int STEPS, int NT, int RB>
 __global__ void __launch_bounds__(NT) q4k_gemv_m1_kernel(Q4KArgs a) {
   static_assert(RB == 1 || RB == 2, "one or two row buffers");
+  if (a.pair.ids != nullptr && !resolve_pair(a)) return;
   extern __shared__ __align__(16) char lds[];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -350,22 +354,25 @@ namespace {
 constexpr int kMaxRowsPerPass = 4;
 
 template <int MB, int NT>
-void launch_one(bool a16, int grid, size_t lds, const Q4KArgs& a) {
+void launch_one(bool a16, dim3 grid, size_t lds, const Q4KArgs& a) {
   if (a16)
     q4k_gemv_kernel<true, MB, NT><<<grid, NT, lds, current_stream()>>>(a);
   else
     q4k_gemv_kernel<false, MB, NT><<<grid, NT, lds, current_stream()>>>(a);
 }
 
-// X != null -> quantize (and write Xq), else read xq_in.
+// X != null -> quantize (and write Xq), else read xq_in.  pr: MUL_MAT_ID
+// pairs (one activation row each, blockIdx.y = pair).
 void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_out, float* Y,
-                size_t N, size_t K, size_t M, const RowStrides& st) {
-  if (N == 0 || M == 0 || K == 0) return;
+                size_t N, size_t K, size_t M, const RowStrides& st, const PairArgs* pr = nullptr,
+                int n_pairs = 0) {
+  if (pr != nullptr) M = 1;
+  if (N == 0 || M == 0 || K == 0 || (pr != nullptr && n_pairs <= 0)) return;
   if (K % 256 != 0 || W == nullptr || Y == nullptr || (X == nullptr && xq_in == nullptr) ||
       N > (size_t)INT32_MAX || K > (size_t)INT32_MAX || M > (size_t)INT32_MAX ||
       !aligned(W, 2) || !aligned(Y, 4) || (xq_in && !aligned(xq_in, 4)) ||
       (xq_out && !aligned(xq_out, 4)) || (X && !aligned(X, 4)) ||
-      !strides_ok(st, K / 256 * kQ4_KBytes, 2, K, N, N, M)) {
+      !strides_ok(st, K / 256 * kQ4_KBytes, 2, K, N, N, M) || (pr != nullptr && pr->w_es % 2 != 0)) {
     set_error(hipErrorInvalidValue);
     return;
   }
@@ -380,8 +387,22 @@ void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t*
   const int cus = cu_count();
   const int rows_per_wg = (int)((N + cus - 1) / cus);
   const int grid = (int)((N + rows_per_wg - 1) / rows_per_wg);
-  const bool a16 = aligned(W, 16) && (N == 1 || st.ldw % 16 == 0);
-  if (M == 1 && X != nullptr && a16 && aligned(X, 16) && K <= 3 * 4096) {
+  const bool a16 = aligned(W, 16) && (N == 1 || st.ldw % 16 == 0) && (pr == nullptr || pr->w_es % 16 == 0);
+  const bool x16 = aligned(X, 16) && (pr == nullptr || (pr->x_s1 % 4 == 0 && pr->x_s2 % 4 == 0));
+  // launch over the pairs (or once), gridDim.y pairs at a time
+  auto each = [&](Q4KArgs a, int g, auto&& go) {
+    if (pr == nullptr) {
+      a.pair = PairArgs{};
+      go(a, dim3((unsigned)g));
+      return;
+    }
+    for (int p0 = 0; p0 < n_pairs; p0 += kMaxGridY) {
+      a.pair = *pr;
+      a.pair.pair0 = p0;
+      go(a, dim3((unsigned)g, (unsigned)std::min(kMaxGridY, n_pairs - p0)));
+    }
+  };
+  if (M == 1 && X != nullptr && a16 && x16 && K <= 3 * 4096) {
     // batch 1: the register-resident kernel.  One step per row (K <= 4096)
     // runs 1024-thread workgroups, two per CU (62 VGPRs); longer rows keep
     // three activation slices in VGPRs and run 512 threads, one per CU.
@@ -406,17 +427,19 @@ void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t*
     a.ldw = st.ldw;
     a.ldx = st.ldx;
     const int g1 = (int)((N + rpw - 1) / rpw);
-    if (steps == 1)
-      q4k_gemv_m1_kernel<1, 1024, 2><<<g1, 1024, row_lds, current_stream()>>>(a);
-    else if (one_row && steps == 2)
-      q4k_gemv_m1_kernel<2, 1024, 1><<<g1, 1024, row_lds, current_stream()>>>(a);
-    else if (one_row)
-      q4k_gemv_m1_kernel<3, 1024, 1><<<g1, 1024, row_lds, current_stream()>>>(a);
-    else if (steps == 2)
-      q4k_gemv_m1_kernel<2, 512, 2><<<g1, 512, row_lds, current_stream()>>>(a);
-    else
-      q4k_gemv_m1_kernel<3, 512, 2><<<g1, 512, row_lds, current_stream()>>>(a);
-    check_launch();
+    each(a, g1, [&](const Q4KArgs& b, dim3 g) {
+      if (steps == 1)
+        q4k_gemv_m1_kernel<1, 1024, 2><<<g, 1024, row_lds, current_stream()>>>(b);
+      else if (one_row && steps == 2)
+        q4k_gemv_m1_kernel<2, 1024, 1><<<g, 1024, row_lds, current_stream()>>>(b);
+      else if (one_row)
+        q4k_gemv_m1_kernel<3, 1024, 1><<<g, 1024, row_lds, current_stream()>>>(b);
+      else if (steps == 2)
+        q4k_gemv_m1_kernel<2, 512, 2><<<g, 512, row_lds, current_stream()>>>(b);
+      else
+        q4k_gemv_m1_kernel<3, 512, 2><<<g, 512, row_lds, current_stream()>>>(b);
+      check_launch();
+    });
     return;
   }
   for (size_t m0 = 0; m0 < M; m0 += mb_max) {
@@ -435,11 +458,13 @@ void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t*
     a.ldw = st.ldw;
     a.ldx = st.ldx;
     const size_t lds = row_lds * a.mb;
-    if (a.mb == 1)
-      launch_one<1, NT>(a16, grid, lds, a);
-    else
-      launch_one<kMaxRowsPerPass, NT>(a16, grid, lds, a);
-    check_launch();
+    each(a, grid, [&](const Q4KArgs& b, dim3 g) {
+      if (b.mb == 1)
+        launch_one<1, NT>(a16, g, lds, b);
+      else
+        launch_one<kMaxRowsPerPass, NT>(a16, g, lds, b);
+      check_launch();
+    });
   }
 }
 
@@ -453,6 +478,12 @@ void decode_q4k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t 
 void decode_q4k_quantized(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K,
                           size_t M, const RowStrides& st) {
   launch_q4k(W, nullptr, Xq, nullptr, Y, N, K, M, st);
+}
+
+void decode_q4k_pairs(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_out,
+                      float* Y, size_t N, size_t K, const RowStrides& st, const PairArgs& pr,
+                      int n_pairs) {
+  launch_q4k(W, X, xq_in, xq_out, Y, N, K, 1, st, &pr, n_pairs);
 }
 
 }  // namespace weft

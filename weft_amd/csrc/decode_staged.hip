@@ -24,6 +24,7 @@
 
 #include "activation.h"
 #include "kernels.h"
+#include "pairs.h"
 #include "runtime.h"
 #include "weft_hip.h"
 
@@ -69,6 +70,7 @@ struct Args {
   long long y_stride;
   size_t ldw;  // bytes between weight rows
   size_t ldx;  // elements between activation rows
+  PairArgs pair;  // MUL_MAT_ID pairs (pair.ids null: none)
 };
 
 // 4 bytes starting at any LDS byte offset o (o+7 must be inside the buffer)
@@ -134,6 +136,7 @@ __device__ __forceinline__ int apply_signs(uint32_t g, uint32_t s) {
 template <Fmt F>
 __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
   using T = Traits<F>;
+  if (a.pair.ids != nullptr && !resolve_pair(a)) return;
   extern __shared__ __align__(16) char lds[];
   char* windows = lds;                             // kWaves * kWindow
   char* tables = windows + kWaves * kWindow;       // 3 KB of tables
@@ -294,9 +297,10 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
 template <Fmt F>
 void launch(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_out,
             const int8_t* tab0, const void* tab1, float* Y, size_t N, size_t K, size_t M,
-            const RowStrides& st) {
+            const RowStrides& st, const PairArgs* pr = nullptr, int n_pairs = 0) {
   using T = Traits<F>;
-  if (N == 0 || M == 0 || K == 0) return;
+  if (pr != nullptr) M = 1;  // one activation row per pair
+  if (N == 0 || M == 0 || K == 0 || (pr != nullptr && n_pairs <= 0)) return;
   const size_t act_align = T::kQ8K ? 4 : 2;
   const size_t w_align = F == Fmt::MXFP4 ? 1 : 2;
   if (K % T::kElems != 0 || W == nullptr || Y == nullptr || (X == nullptr && xq_in == nullptr) ||
@@ -306,7 +310,8 @@ void launch(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_
       (F != Fmt::Q4_0 && (tab0 == nullptr || tab1 == nullptr)) ||
       (F == Fmt::IQ2_XXS && (!aligned(tab0, 4) || !aligned(tab1, 4))) ||
       (F == Fmt::MXFP4 && !aligned(tab1, 4)) ||
-      !strides_ok(st, K / T::kElems * T::kBytes, w_align, K, N, N, M)) {
+      !strides_ok(st, K / T::kElems * T::kBytes, w_align, K, N, N, M) ||
+      (pr != nullptr && pr->w_es % (long long)w_align != 0)) {
     set_error(hipErrorInvalidValue);
     return;
   }
@@ -338,8 +343,19 @@ void launch(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_
     a.y_stride = (long long)st.ldy;
     a.ldw = st.ldw;
     a.ldx = st.ldx;
-    staged_gemv_kernel<F><<<grid, kThreads, fixed + row_lds * a.mb, current_stream()>>>(a);
-    check_launch();
+    a.pair = PairArgs{};
+    if (pr == nullptr) {
+      staged_gemv_kernel<F><<<grid, kThreads, fixed + row_lds * a.mb, current_stream()>>>(a);
+      check_launch();
+      continue;
+    }
+    for (int p0 = 0; p0 < n_pairs; p0 += kMaxGridY) {
+      a.pair = *pr;
+      a.pair.pair0 = p0;
+      const dim3 g((unsigned)grid, (unsigned)std::min(kMaxGridY, n_pairs - p0));
+      staged_gemv_kernel<F><<<g, kThreads, fixed + row_lds, current_stream()>>>(a);
+      check_launch();
+    }
   }
 }
 
@@ -358,6 +374,16 @@ void decode_iq2_xxs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t*
                     const int8_t* signs, float* Y, size_t N, size_t K, size_t M,
                     const RowStrides& st) {
   launch<Fmt::IQ2_XXS>(W, X, nullptr, Xq, grid, signs, Y, N, K, M, st);
+}
+
+void decode_pairs(int fmt, const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_out,
+                  const int8_t* tab0, const void* tab1, float* Y, size_t N, size_t K,
+                  const RowStrides& st, const PairArgs& pr, int n_pairs) {
+  switch (fmt) {
+    case 0: return launch<Fmt::Q4_0>(W, X, xq_in, xq_out, nullptr, nullptr, Y, N, K, 1, st, &pr, n_pairs);
+    case 1: return launch<Fmt::MXFP4>(W, X, xq_in, xq_out, tab0, tab1, Y, N, K, 1, st, &pr, n_pairs);
+    default: return launch<Fmt::IQ2_XXS>(W, X, xq_in, xq_out, tab0, tab1, Y, N, K, 1, st, &pr, n_pairs);
+  }
 }
 
 void decode_quantized(int fmt, const uint8_t* W, const uint8_t* Xq, const int8_t* tab0,

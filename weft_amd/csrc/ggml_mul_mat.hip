@@ -53,6 +53,8 @@ constexpr TypeInfo kTypes[] = {
     {WEFT_GGML_TYPE_MXFP4, 32, kMxfp4Bytes, WEFT_GGML_TYPE_Q8_0},
 };
 
+constexpr int32_t kGgmlTypeI32 = 26;  // GGML_TYPE_I32
+
 const TypeInfo* info(int32_t type) {
   for (const TypeInfo& t : kTypes)
     if (t.type == type) return &t;
@@ -231,6 +233,87 @@ hipError_t mul_mat(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1, const
   return pending_error();
 }
 
+// GGML_OP_MUL_MAT_ID (ggml-cpu.c:1454-1698; shape rules of ggml_mul_mat_id,
+// ggml.c:3293-3317): src0 holds n_as = ne02 expert matrices, ids (I32,
+// n_ids x n_tokens) picks an expert per (slot, token), src1 row
+// (s % ne11, t) meets it, dst row (s, t) receives the product.
+hipError_t mul_mat_id(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1,
+                      const weft_ggml_tensor* ids, const weft_ggml_tensor* d, void* wdata,
+                      size_t wsize) {
+  if (s0 == nullptr || s1 == nullptr || ids == nullptr || d == nullptr) return fail(hipErrorInvalidValue);
+  const TypeInfo* t0 = info(s0->type);
+  if (t0 == nullptr || t0->vec_dot < 0 || d->type != WEFT_GGML_TYPE_F32 ||
+      (s1->type != WEFT_GGML_TYPE_F32 && s1->type != t0->vec_dot))
+    return fail(hipErrorNotSupported);
+  if (ids->type != kGgmlTypeI32) return fail(hipErrorInvalidValue);
+  const TypeInfo* t1 = info(s1->type);
+  const TypeInfo* vd = info(t0->vec_dot);
+  if (!nonneg(s0) || !nonneg(s1) || !nonneg(ids) || !nonneg(d)) return fail(hipErrorInvalidValue);
+  const int64_t K = s0->ne[0], N = s0->ne[1], n_as = s0->ne[2];
+  const int64_t ne11 = s1->ne[1], n_tok = s1->ne[2], n_ids = ids->ne[0];
+  if (d->ne[0] == 0 || d->ne[1] == 0 || d->ne[2] == 0 || d->ne[3] == 0) return hipSuccess;
+  if (s0->ne[3] != 1 || s1->ne[3] != 1 || ids->ne[2] != 1 || ids->ne[3] != 1 || ids->ne[1] != n_tok ||
+      s1->ne[0] != K || ne11 == 0 || n_ids % ne11 != 0 || d->ne[0] != N || d->ne[1] != n_ids ||
+      d->ne[2] != n_tok || d->ne[3] != 1 || K % t0->blck != 0 || s0->nb[0] != t0->size ||
+      s1->nb[0] != t1->size || d->nb[0] != sizeof(float) || d->nb[0] > d->nb[1] ||
+      d->nb[1] > d->nb[2] || d->nb[2] > d->nb[3] || d->nb[1] % 4 != 0 || d->nb[2] % 4 != 0 ||
+      ids->nb[0] % 4 != 0 || ids->nb[1] % 4 != 0 || ids->data == nullptr ||
+      !aligned(ids->data, 4) || n_as > INT32_MAX || n_ids > INT32_MAX ||
+      n_ids * n_tok > INT32_MAX)
+    return fail(hipErrorInvalidValue);
+  if (K == 0 || N == 0) return hipSuccess;
+  const bool quantize = s1->type == WEFT_GGML_TYPE_F32;
+  const size_t nbw1 = row_size(vd, K);
+  if (quantize) {
+    if (s1->nb[1] % 4 != 0 || s1->nb[2] % 4 != 0 || wdata == nullptr || !aligned(wdata, 4) ||
+        wsize < nbw1 * (size_t)(ne11 * n_tok))
+      return fail(hipErrorInvalidValue);
+  } else if ((ne11 > 1 && s1->nb[1] != nbw1) || (n_tok > 1 && s1->nb[2] != nbw1 * (size_t)ne11)) {
+    return fail(hipErrorNotSupported);  // quantized src1 rows must be packed
+  }
+  const GgmlTables* tab = nullptr;
+  if (s0->type == WEFT_GGML_TYPE_IQ2_XXS || s0->type == WEFT_GGML_TYPE_MXFP4) {
+    tab = device_tables();
+    if (tab == nullptr) return fail(hipErrorInvalidDevice);
+  }
+  PairArgs pr{};
+  pr.ids = static_cast<const int32_t*>(ids->data);
+  pr.ids_s0 = (long long)(ids->nb[0] / 4);
+  pr.ids_s1 = (long long)(ids->nb[1] / 4);
+  pr.n_ids = (int)n_ids;
+  pr.ne11 = (int)ne11;
+  pr.n_as = (int)n_as;
+  pr.w_es = (long long)s0->nb[2];
+  pr.x_s1 = quantize ? (long long)(s1->nb[1] / 4) : 0;
+  pr.x_s2 = quantize ? (long long)(s1->nb[2] / 4) : 0;
+  pr.xq_row = (long long)nbw1;
+  pr.y_s1 = (long long)(d->nb[1] / 4);
+  pr.y_s2 = (long long)(d->nb[2] / 4);
+  const int n_pairs = (int)(n_ids * n_tok);
+  const RowStrides st{s0->nb[1], (size_t)K, (size_t)N};
+  const uint8_t* W = static_cast<const uint8_t*>(s0->data);
+  const float* X = quantize ? static_cast<const float*>(s1->data) : nullptr;
+  const uint8_t* xq_in = quantize ? nullptr : static_cast<const uint8_t*>(s1->data);
+  uint8_t* xq_out = quantize ? static_cast<uint8_t*>(wdata) : nullptr;
+  float* Y = static_cast<float*>(d->data);
+  switch (s0->type) {
+    case WEFT_GGML_TYPE_Q4_K:
+      decode_q4k_pairs(W, X, xq_in, xq_out, Y, (size_t)N, (size_t)K, st, pr, n_pairs);
+      break;
+    case WEFT_GGML_TYPE_Q4_0:
+      decode_pairs(0, W, X, xq_in, xq_out, nullptr, nullptr, Y, (size_t)N, (size_t)K, st, pr, n_pairs);
+      break;
+    case WEFT_GGML_TYPE_MXFP4:
+      decode_pairs(1, W, X, xq_in, xq_out, tab->codebook, tab->scale, Y, (size_t)N, (size_t)K, st, pr,
+                   n_pairs);
+      break;
+    default:
+      decode_pairs(2, W, X, xq_in, xq_out, tab->grid, tab->signs, Y, (size_t)N, (size_t)K, st, pr, n_pairs);
+      break;
+  }
+  return pending_error();
+}
+
 }  // namespace
 }  // namespace weft
 
@@ -254,6 +337,31 @@ size_t weft_ggml_row_size(int32_t type, int64_t ne) {
 int32_t weft_ggml_vec_dot_type(int32_t type) {
   const weft::TypeInfo* t = weft::info(type);
   return t ? t->vec_dot : -1;
+}
+
+size_t weft_ggml_mul_mat_id_work_size(const weft_ggml_tensor* src0, const weft_ggml_tensor* src1,
+                                      const weft_ggml_tensor* ids) {
+  // ggml_graph_plan's MUL_MAT_ID size (ggml-cpu.c:2827-2845, CACHE_LINE_SIZE 64)
+  if (src0 == nullptr || src1 == nullptr || ids == nullptr) return 0;
+  const weft::TypeInfo* t0 = weft::info(src0->type);
+  if (t0 == nullptr || t0->vec_dot < 0) return 0;
+  size_t cur = 0;
+  if (src1->type != t0->vec_dot) {
+    int64_t n = 1;
+    for (int i = 0; i < 4; ++i) n *= src1->ne[i];
+    cur += weft_ggml_row_size(t0->vec_dot, n) + sizeof(int64_t);
+  }
+  const size_t n_as = (size_t)src0->ne[2];
+  cur += n_as * sizeof(int64_t) + sizeof(int64_t);
+  cur += n_as * (size_t)ids->ne[0] * (size_t)ids->ne[1] * 2 * sizeof(int32_t) + sizeof(int64_t);
+  cur += 64 * n_as + 64;
+  return cur;
+}
+
+int weft_ggml_mul_mat_id(const weft_ggml_tensor* src0, const weft_ggml_tensor* src1,
+                         const weft_ggml_tensor* ids, const weft_ggml_tensor* dst, void* wdata,
+                         size_t wsize) {
+  return (int)weft::mul_mat_id(src0, src1, ids, dst, wdata, wsize);
 }
 
 size_t weft_ggml_mul_mat_work_size(const weft_ggml_tensor* src0, const weft_ggml_tensor* src1) {

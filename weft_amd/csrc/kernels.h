@@ -4,6 +4,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "pairs.h"
+
 namespace weft {
 
 // Row strides of one mul_mat: bytes between weight rows (ldw), floats between
@@ -39,6 +41,16 @@ void decode_mxfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* c
 void decode_iq2_xxs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,
                     const int8_t* signs, float* Y, size_t N, size_t K, size_t M,
                     const RowStrides& st);
+// MUL_MAT_ID: the GEMV over every (token, slot) pair of pr, each with the
+// expert ids[t, s] selects (one activation row per pair; X quantized into
+// xq_out, or the quantized xq_in read).  Q4_K, and Q4_0 (fmt 0), MXFP4 (1),
+// IQ2_XXS (2).
+void decode_q4k_pairs(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_out,
+                      float* Y, size_t N, size_t K, const RowStrides& st, const PairArgs& pr,
+                      int n_pairs);
+void decode_pairs(int fmt, const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_out,
+                  const int8_t* tab0, const void* tab1, float* Y, size_t N, size_t K,
+                  const RowStrides& st, const PairArgs& pr, int n_pairs);
 // Q4_0 (fmt 0), MXFP4 (1) or IQ2_XXS (2) GEMV over an already quantized
 // activation (Q8_0 / Q8_0 / Q8_K records, read only)
 void decode_quantized(int fmt, const uint8_t* W, const uint8_t* Xq, const int8_t* tab0,

@@ -1,4 +1,4 @@
-"""GGML MUL_MAT boundary of libweft_hip from Python.
+"""GGML MUL_MAT / MUL_MAT_ID boundary of libweft_hip from Python.
 
 ``Tensor`` is the part of ``struct ggml_tensor`` (ggml/include/ggml.h:667-692)
 that MUL_MAT reads: type id, ``ne``, byte strides ``nb`` and a device data
@@ -15,7 +15,7 @@ from collections.abc import Sequence
 from . import _lib
 
 # enum ggml_type (ggml/include/ggml.h:389-431), the types of this path
-F32, Q4_0, Q8_0, Q4_K, Q8_K, IQ2_XXS, MXFP4 = 0, 2, 8, 12, 15, 16, 39
+F32, Q4_0, Q8_0, Q4_K, Q8_K, IQ2_XXS, I32, MXFP4 = 0, 2, 8, 12, 15, 16, 26, 39
 
 
 class Tensor(ctypes.Structure):
@@ -45,7 +45,8 @@ def tensor(t: int, ne: Sequence[int], data: int = 0, nb: Sequence[int] | None = 
     unless ``nb`` is given."""
     ne = list(ne) + [1] * (4 - len(ne))
     if nb is None:
-        nb = [type_size(t), row_size(t, ne[0])]
+        size = 4 if t == I32 else type_size(t)
+        nb = [size, size * ne[0] if t == I32 else row_size(t, ne[0])]
         nb += [nb[1] * ne[1], nb[1] * ne[1] * ne[2]]
     return Tensor(t, (ctypes.c_int64 * 4)(*ne), (ctypes.c_size_t * 4)(*nb), data)
 
@@ -62,3 +63,19 @@ def mul_mat(src0: Tensor, src1: Tensor, dst: Tensor, wdata: int = 0, wsize: int 
     if code != 0:
         lib.weft_hip_get_last_error()  # the same error, recorded: clear it
         raise _lib.HipError(code, "weft_ggml_mul_mat")
+
+
+def mul_mat_id_work_size(src0: Tensor, src1: Tensor, ids: Tensor) -> int:
+    return _lib.load().weft_ggml_mul_mat_id_work_size(ctypes.byref(src0), ctypes.byref(src1),
+                                                      ctypes.byref(ids))
+
+
+def mul_mat_id(src0: Tensor, src1: Tensor, ids: Tensor, dst: Tensor, wdata: int = 0,
+               wsize: int = 0) -> None:
+    """Enqueue dst = MUL_MAT_ID(src0 experts, src1, ids) on the current stream."""
+    lib = _lib.load()
+    code = lib.weft_ggml_mul_mat_id(ctypes.byref(src0), ctypes.byref(src1), ctypes.byref(ids),
+                                    ctypes.byref(dst), ctypes.c_void_p(wdata), wsize)
+    if code != 0:
+        lib.weft_hip_get_last_error()
+        raise _lib.HipError(code, "weft_ggml_mul_mat_id")
