@@ -19,7 +19,9 @@ Secondary figures (the other BASELINE.json configs) ride in the same JSON
 line under ``configs``: W_down decode, the Q4_0 / IQ2_XXS / MXFP4 decode GEMVs,
 the Q4_K row dequantize, and the prefill mul_mats (Q4_K config 4 at N=4096 and
 N=11008, MXFP4 config 5b, Q4_0 and IQ2_XXS at the same shape), the latter
-against the int8 MFMA peak.
+against the int8 MFMA peak, plus the derived Q4K_I[16] GEMV and GGML's
+MUL_MAT_ID at a Mixtral-8x7B expert shape (ops counted per (token, expert)
+pair).
 
 The CPU baseline is oracle/'s restatement of GGML's generic MUL_MAT path
 (quantize_row_q8_K_ref + ggml_vec_dot_q4_K_q8_K_generic, rows over OpenMP
@@ -58,7 +60,11 @@ CASES = {
     "mxfp4_prefill": ("production_mul_mat_mxfp4", "mxfp4", 4096, 4096, 512, "mfma"),
     "q4_0_prefill": ("production_mul_mat_q4_0", "q4_0", 4096, 4096, 512, "mfma"),
     "iq2_xxs_prefill": ("production_mul_mat_iq2_xxs_staged", "iq2_xxs", 4096, 4096, 512, "mfma"),
+    # GGML MUL_MAT_ID (MoE) prefill at a Mixtral-8x7B FFN shape: 8 experts of
+    # 14336 x 4096 Q4_K, 2 experts per token, 512 tokens (the grouped GEMM)
+    "q4_k_moe_prefill": ("weft_ggml_mul_mat_id", "q4_k", 14336, 4096, 512, "mfma"),
 }
+MOE_EXPERTS, MOE_USED = 8, 2
 HEADLINE = "q4_k_decode_w_up"
 
 
@@ -167,6 +173,30 @@ def run_case(b: Bench, name: str, steps: int, warmup: int) -> dict:
             fn(wd[i % copies].data_ptr(), xq.data_ptr(), y.data_ptr(), n, k)
 
         nbytes = w.nbytes + xq.numel() + 4 * n
+    elif sym == "weft_ggml_mul_mat_id":
+        # one quantized expert matrix copied MOE_EXPERTS times (the timing
+        # does not depend on the values); seeded top-MOE_USED choices per token
+        from weft_amd import ggml as G
+        experts = b.dev_copy(np.concatenate([w] * MOE_EXPERTS))
+        del wd
+        wd = [experts]
+        rng = np.random.default_rng(3)
+        ids_h = np.stack([rng.choice(MOE_EXPERTS, MOE_USED, replace=False) for _ in range(m)]).astype(np.int32)
+        ids = b.dev_copy(ids_h)
+        x = b.dev_copy(o.seeded_normal(2, (m, k)))
+        y = torch.empty(m * MOE_USED * n, dtype=torch.float32, device=b.dev)
+        s0 = G.tensor(G.Q4_K, (k, n, MOE_EXPERTS), experts.data_ptr())
+        s1 = G.tensor(G.F32, (k, 1, m), x.data_ptr())
+        it = G.tensor(G.I32, (MOE_USED, m), ids.data_ptr())
+        d = G.tensor(G.F32, (n, MOE_USED, m), y.data_ptr())
+        wsize = G.mul_mat_id_work_size(s0, s1, it)
+        work = torch.empty(wsize, dtype=torch.uint8, device=b.dev)
+
+        def launch(i):
+            G.mul_mat_id(s0, s1, it, d, work.data_ptr(), wsize)
+
+        nbytes = MOE_EXPERTS * w.nbytes + 4 * m * k + o.record_bytes("q8_k", k) * m + 4 * m * MOE_USED * n
+        m *= MOE_USED  # products: one per (token, expert) pair
     else:
         act = o.ACT_OF[fmt]
         x = b.dev_copy(o.seeded_normal(2, (m, k)))

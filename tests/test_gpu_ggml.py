@@ -120,7 +120,7 @@ def test_prequantized_src1(hip, fmt, m):
 
 
 # ---------------------------------------------------------------- MUL_MAT_ID
-def run_id(hip, fmt, k, n, n_as, n_ids, ne11, n_tok, ids, pad_w=0, prequant=False, seed=11):
+def run_id(hip, fmt, k, n, n_as, n_ids, ne11, n_tok, ids, pad_w=0, pad_x=0, prequant=False, seed=11):
     """ids: (n_tok, n_ids) int32 expert choices; entries outside [0, n_as)
     must leave their dst rows untouched."""
     hip.torch.cuda.synchronize()
@@ -136,8 +136,11 @@ def run_id(hip, fmt, k, n, n_as, n_ids, ne11, n_tok, ids, pad_w=0, prequant=Fals
         xd = hip.to_dev(xq)
         s1 = G.tensor(VDT[fmt], (k, ne11, n_tok), xd.ptr)
     else:
-        xd = hip.to_dev(x)
-        s1 = G.tensor(G.F32, (k, ne11, n_tok), xd.ptr)
+        xp = np.zeros((n_tok, ne11, k + pad_x), np.float32)
+        xp[..., :k] = x
+        xd = hip.to_dev(xp)
+        row = 4 * (k + pad_x)
+        s1 = G.tensor(G.F32, (k, ne11, n_tok), xd.ptr, [4, row, row * ne11, row * ne11 * n_tok])
     wd = hip.to_dev(w_host)
     idd = hip.to_dev(np.ascontiguousarray(ids, dtype=np.int32))
     yd = hip.empty(4 * n * n_ids * n_tok)
@@ -149,7 +152,7 @@ def run_id(hip, fmt, k, n, n_as, n_ids, ne11, n_tok, ids, pad_w=0, prequant=Fals
     wsize = G.mul_mat_id_work_size(s0, s1, it)
     wdata = hip.empty(wsize, fill=0xA5)
     print(f"ggml mul_mat_id {fmt} k={k} n={n} n_as={n_as} n_ids={n_ids} ne11={ne11} "
-          f"n_tok={n_tok} pad_w={pad_w} prequant={prequant}", flush=True)
+          f"n_tok={n_tok} pad_w={pad_w} pad_x={pad_x} prequant={prequant}", flush=True)
     G.mul_mat_id(s0, s1, it, d, wdata.ptr, wsize)
     hip.torch.cuda.synchronize()
     assert hip.last_error() == 0
@@ -189,3 +192,18 @@ def test_mul_mat_id_tokens_and_invalid_ids(hip, fmt):
 def test_mul_mat_id_prequantized_and_strided(hip, fmt):
     ids = np.array([[1, 3, 0], [2, 2, 1]])
     run_id(hip, fmt, 512, 64, 4, 3, 1, 2, ids, pad_w=1 if fmt == "mxfp4" else 2, prequant=True)
+
+
+@pytest.mark.parametrize("ne11", [1, 4])
+@pytest.mark.parametrize("prequant", [False, True])
+def test_mul_mat_id_q4_k_grouped_gemm(hip, ne11, prequant):
+    """Q4_K with many pairs per expert: the device groups the pairs by expert
+    and the grouped MFMA GEMM runs them (ragged tiles, one expert unused,
+    invalid ids skipped)."""
+    rng = np.random.default_rng(5)
+    n_tok, n_ids, n_as = 70, 4, 8
+    ids = rng.integers(0, n_as - 1, size=(n_tok, n_ids))  # expert 7 never chosen
+    ids[3, 2] = -1
+    ids[40, 0] = n_as
+    run_id(hip, "q4_k", 1024, 300, n_as, n_ids, ne11, n_tok, ids, pad_w=16,
+           pad_x=0 if prequant else 4, prequant=prequant)

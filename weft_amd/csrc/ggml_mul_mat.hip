@@ -296,6 +296,30 @@ hipError_t mul_mat_id(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1,
   const uint8_t* xq_in = quantize ? nullptr : static_cast<const uint8_t*>(s1->data);
   uint8_t* xq_out = quantize ? static_cast<uint8_t*>(wdata) : nullptr;
   float* Y = static_cast<float*>(d->data);
+  // Q4_K with several pairs per expert on average: group the pairs by
+  // expert on the device and run the grouped MFMA GEMM over the quantized
+  // activation (GGML's own order: quantize src1, group, multiply)
+  if (s0->type == WEFT_GGML_TYPE_Q4_K && n_pairs >= 64 && n_pairs >= 4 * n_as) {
+    const size_t xq_bytes = nbw1 * (size_t)(ne11 * n_tok);
+    const size_t used = quantize ? (xq_bytes + 15) & ~(size_t)15 : 0;
+    uint8_t* ws = static_cast<uint8_t*>(wdata) + used;
+    if (wdata != nullptr && wsize >= used &&
+        mul_mat_id_q4k_grouped_ok(W, xq_bytes, Y, (size_t)N, (size_t)K, st, pr, n_pairs, ws,
+                                  wsize - used)) {
+      if (quantize) {
+        const size_t ldx = s1->nb[1] / 4;
+        if (n_tok == 1 || s1->nb[2] == (size_t)ne11 * s1->nb[1]) {
+          quantize_q8_k_rows(X, ldx, xq_out, (size_t)(ne11 * n_tok), (size_t)K);
+        } else {
+          for (int64_t t = 0; t < n_tok; ++t)
+            quantize_q8_k_rows(X + (size_t)t * (s1->nb[2] / 4), ldx, xq_out + (size_t)t * ne11 * nbw1,
+                               (size_t)ne11, (size_t)K);
+        }
+      }
+      mul_mat_id_q4k_grouped(W, quantize ? xq_out : xq_in, Y, (size_t)N, (size_t)K, st, pr, n_pairs, ws);
+      return pending_error();
+    }
+  }
   switch (s0->type) {
     case WEFT_GGML_TYPE_Q4_K:
       decode_q4k_pairs(W, X, xq_in, xq_out, Y, (size_t)N, (size_t)K, st, pr, n_pairs);

@@ -51,6 +51,29 @@ void decode_q4k_pairs(const uint8_t* W, const float* X, const uint8_t* xq_in, ui
 void decode_pairs(int fmt, const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_out,
                   const int8_t* tab0, const void* tab1, float* Y, size_t N, size_t K,
                   const RowStrides& st, const PairArgs& pr, int n_pairs);
+// MUL_MAT_ID grouping on the device (moe.hip): pairs grouped by expert and
+// a table of tiles of at most kMoeTileRows pairs of one expert, written into
+// ws (moe_group_bytes of it, 16-byte aligned).  The tile count stays on the
+// device; tmax bounds it.
+constexpr int kMaxExperts = 4096;
+constexpr int kMoeTileRows = 64;
+struct MoeGroups {
+  int32_t* ntiles;
+  int32_t* tiles;  // [tmax][3]: expert, first pair index, pairs
+  int32_t* pairs;
+  int tmax;
+};
+int moe_tile_bound(int n_pairs, int n_as);
+size_t moe_group_bytes(int n_pairs, int n_as);
+MoeGroups moe_group(const PairArgs& pr, int n_pairs, void* ws);
+// Q4_K MUL_MAT_ID on the grouped MFMA GEMM: Xq holds the quantized src1 rows
+// (token * ne11 + row, xq_bytes in all), ws the grouping (moe_group_bytes).
+// _ok: whether the shape suits the GEMM.
+bool mul_mat_id_q4k_grouped_ok(const uint8_t* W, size_t xq_bytes, const float* Y, size_t N, size_t K,
+                               const RowStrides& st, const PairArgs& pr, int n_pairs, const void* ws,
+                               size_t ws_bytes);
+void mul_mat_id_q4k_grouped(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K,
+                            const RowStrides& st, const PairArgs& pr, int n_pairs, void* ws);
 // Q4_0 (fmt 0), MXFP4 (1) or IQ2_XXS (2) GEMV over an already quantized
 // activation (Q8_0 / Q8_0 / Q8_K records, read only)
 void decode_quantized(int fmt, const uint8_t* W, const uint8_t* Xq, const int8_t* tab0,

@@ -51,6 +51,14 @@
 //   WT  128 rows x the 144-byte Q4_K record
 // The activation is quantized first, into the caller's Xq, by q8_K_quantize's
 // kernel (Xq is part of the ABI), then read back from L2.
+//
+// Grouped mode (kGroup, GGML's MUL_MAT_ID, ggml-cpu/ggml-cpu.c:1454-1698):
+// the (token, slot) pairs are grouped by expert on the device
+// (moe_group_kernel: a pair list per expert and a table of 64-row tiles), and
+// workgroup (tile, column block) runs the same GEMM on its tile's pairs: the
+// loader gathers their activation rows through the pair list, W is the
+// tile's expert matrix, and each output goes to the pair's dst row.  Tiles
+// past the device's tile count exit at once.
 #include <algorithm>
 
 #include "kernels.h"
@@ -93,6 +101,14 @@ struct GemmArgs {
   int N, K, M;
   uint32_t ldw;   // bytes between weight rows (a tile's 128 rows stay in 32-bit offsets)
   long long ldy;  // floats between output rows
+  // grouped mode: tile g = {expert, first pair index, pairs}; pairs are
+  // p = token * n_ids + slot, activation row token * ne11 + slot % ne11
+  const int32_t* tiles;
+  const int32_t* ntiles;
+  const int32_t* pairs;
+  int n_ids, ne11, tmax;
+  long long w_es;        // bytes between expert matrices
+  long long y_s1, y_s2;  // floats between dst rows (slots) / planes (tokens)
 };
 
 // Direct global->LDS load of 16 bytes per lane: lane l reads sbase + voff
@@ -136,6 +152,7 @@ __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
 }
 __device__ __forceinline__ float bf16_lo_to_f32(uint32_t p) { return __uint_as_float(p << 16); }
 
+template <bool kGroup>
 __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
   __shared__ __align__(16) uint8_t ring[4 * kStage];  // [pair slot][parity]
   __shared__ __align__(16) uint32_t zero16[4];
@@ -145,16 +162,42 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
   if (tid < 4) zero16[tid] = 0u;
   int m0, n0;
-  {
+  int mrows;  // activation rows of this tile (the last row repeats past them)
+  const uint8_t* W = a.W;
+  if constexpr (kGroup) {
+    // m0 indexes the pair list.  XCD-aware order as below: an expert's
+    // consecutive tiles on one column block meet in one XCD's L2.
+    const int T = a.tmax * ((a.N + kNT - 1) / kNT);
+    const int L = blockIdx.x, x = L & 7, j = L >> 3;
+    const int t = x * (T >> 3) + min(x, T & 7) + j;
+    const int g = t % a.tmax;
+    if (g >= __builtin_amdgcn_readfirstlane(*a.ntiles)) return;  // whole workgroup, no barrier yet
+    W += (long long)__builtin_amdgcn_readfirstlane(a.tiles[3 * g]) * a.w_es;
+    m0 = a.tiles[3 * g + 1];
+    mrows = a.tiles[3 * g + 2];
+    n0 = (t / a.tmax) * kNT;
+  } else {
     const int ntm = (a.M + kMT - 1) / kMT;
     const int T = ntm * ((a.N + kNT - 1) / kNT);
     const int L = blockIdx.x, x = L & 7, j = L >> 3;
     const int t = x * (T >> 3) + min(x, T & 7) + j;
     m0 = (t % ntm) * kMT;
     n0 = (t / ntm) * kNT;
+    mrows = min(kMT, a.M - m0);
   }
   m0 = __builtin_amdgcn_readfirstlane(m0);
   n0 = __builtin_amdgcn_readfirstlane(n0);
+  mrows = __builtin_amdgcn_readfirstlane(mrows);
+  // activation row of tile row r (r < mrows)
+  auto act_row = [&](int r) -> int {
+    if constexpr (kGroup) {
+      const int p = a.pairs[m0 + r];
+      const int t = p / a.n_ids, s = p - t * a.n_ids;
+      return t * a.ne11 + s % a.ne11;
+    } else {
+      return m0 + r;
+    }
+  };
   const int nsb = a.K >> 8;
   const int npair = (nsb + 1) >> 1;
 
@@ -163,18 +206,21 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
     const int par = wave - kMfmaWaves;
     const uint32_t wrb = a.ldw;
     const uint32_t xrb = (uint32_t)nsb * kQ8_KBytes;
-    const uint8_t* xbase = a.Xq + (size_t)m0 * xrb;
-    const uint8_t* wbase = a.W + (size_t)n0 * wrb;
+    // grouped: rows are gathered, offsets from Xq itself (the host keeps
+    // the quantized activation within 32-bit offsets)
+    const uint8_t* xbase = kGroup ? a.Xq : a.Xq + (size_t)m0 * xrb;
+    const uint8_t* wbase = W + (size_t)n0 * wrb;
     uint32_t voff[kSlots];
 #pragma unroll
     for (int k = 0; k < kSlots; ++k) {
       uint32_t o;
       if (k < kAQSlots) {
         const int q = 64 * k + lane, r = q / 17, c = min(q - 17 * r, 15);
-        o = (uint32_t)(min(m0 + r, a.M - 1) - m0) * xrb + 4 + 16 * c;
+        o = (uint32_t)(kGroup ? act_row(min(r, mrows - 1)) : min(r, mrows - 1)) * xrb + 4 + 16 * c;
       } else if (k < kAQSlots + kAXSlots) {
         const int q = 64 * (k - kAQSlots) + lane, r = q / 3, e = q - 3 * r;
-        o = (uint32_t)(min(m0 + r, a.M - 1) - m0) * xrb + (e == 0 ? 0 : 244 + 16 * e);
+        o = (uint32_t)(kGroup ? act_row(min(r, mrows - 1)) : min(r, mrows - 1)) * xrb +
+            (e == 0 ? 0 : 244 + 16 * e);
       } else {
         const int q = 64 * (k - kAQSlots - kAXSlots) + lane, row = q / 9, part = q - 9 * row;
         o = (uint32_t)(min(n0 + row, a.N - 1) - n0) * wrb + 16 * part;
@@ -358,8 +404,17 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int gm = m0 + 32 * t + 8 * (r >> 2) + 4 * kg + (r & 3);
-        if (gm < a.M) a.Y[(size_t)gm * a.ldy + gn] = y[t][r] + red[(16 * t + r) * 64];
+        const int rr = 32 * t + 8 * (r >> 2) + 4 * kg + (r & 3);
+        if (rr < mrows) {
+          const float v = y[t][r] + red[(16 * t + r) * 64];
+          if constexpr (kGroup) {
+            const int p = a.pairs[m0 + rr];
+            const int tk = p / a.n_ids, sl = p - tk * a.n_ids;
+            a.Y[tk * a.y_s2 + sl * a.y_s1 + gn] = v;
+          } else {
+            a.Y[(size_t)(m0 + rr) * a.ldy + gn] = v;
+          }
+        }
       }
   }
 }
@@ -378,9 +433,17 @@ bool gemm_q4k_ok(const uint8_t* W, size_t N, size_t K, size_t M, const RowStride
 void gemm_q4k(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K, size_t M,
               const RowStrides& st) {
   const size_t rb = K / 256 * kQ4_KBytes;
-  GemmArgs a{W, Xq, Y, (int)N, (int)K, (int)M, (uint32_t)(N > 1 ? st.ldw : rb), (long long)st.ldy};
+  GemmArgs a{};
+  a.W = W;
+  a.Xq = Xq;
+  a.Y = Y;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.M = (int)M;
+  a.ldw = (uint32_t)(N > 1 ? st.ldw : rb);
+  a.ldy = (long long)st.ldy;
   const size_t tiles = ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT);
-  q4k_mfma_gemm<<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(a);
+  q4k_mfma_gemm<false><<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(a);
   check_launch();
 }
 
@@ -402,6 +465,43 @@ void mul_mat_q4k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t
   } else {
     decode_q4k(W, X, Xq, Y, N, K, M, st);
   }
+}
+
+bool mul_mat_id_q4k_grouped_ok(const uint8_t* W, size_t xq_bytes, const float* Y, size_t N, size_t K,
+                               const RowStrides& st, const PairArgs& pr, int n_pairs, const void* ws,
+                               size_t ws_bytes) {
+  const size_t rb = K / 256 * kQ4_KBytes;
+  return N > 0 && K > 0 && n_pairs > 0 && K % 256 == 0 && pr.n_as <= kMaxExperts &&
+         xq_bytes < ((size_t)1 << 32) && aligned(Y, 4) && aligned(ws, 16) &&
+         ws_bytes >= moe_group_bytes(n_pairs, pr.n_as) && pr.w_es % 4 == 0 &&
+         gemm_q4k_ok(W, N, K, kMT, st) && strides_ok(st, rb, 2, K, N, N, 1) &&
+         (size_t)moe_tile_bound(n_pairs, pr.n_as) * ((N + kNT - 1) / kNT) <= (size_t)INT32_MAX;
+}
+
+void mul_mat_id_q4k_grouped(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K,
+                            const RowStrides& st, const PairArgs& pr, int n_pairs, void* ws) {
+  const size_t rb = K / 256 * kQ4_KBytes;
+  const MoeGroups g = moe_group(pr, n_pairs, ws);
+  GemmArgs a{};
+  a.W = W;
+  a.Xq = Xq;
+  a.Y = Y;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.M = kMT;
+  a.ldw = (uint32_t)(N > 1 ? st.ldw : rb);
+  a.tiles = g.tiles;
+  a.ntiles = g.ntiles;
+  a.pairs = g.pairs;
+  a.n_ids = pr.n_ids;
+  a.ne11 = pr.ne11;
+  a.tmax = g.tmax;
+  a.w_es = pr.w_es;
+  a.y_s1 = pr.y_s1;
+  a.y_s2 = pr.y_s2;
+  const size_t wgs = (size_t)g.tmax * ((N + kNT - 1) / kNT);
+  q4k_mfma_gemm<true><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(a);
+  check_launch();
 }
 
 void mul_mat_q4k_quantized(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K,
