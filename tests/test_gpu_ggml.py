@@ -194,16 +194,18 @@ def test_mul_mat_id_prequantized_and_strided(hip, fmt):
     run_id(hip, fmt, 512, 64, 4, 3, 1, 2, ids, pad_w=1 if fmt == "mxfp4" else 2, prequant=True)
 
 
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("ne11", [1, 4])
 @pytest.mark.parametrize("prequant", [False, True])
-def test_mul_mat_id_q4_k_grouped_gemm(hip, ne11, prequant):
-    """Q4_K with many pairs per expert: the device groups the pairs by expert
-    and the grouped MFMA GEMM runs them (ragged tiles, one expert unused,
-    invalid ids skipped)."""
+def test_mul_mat_id_grouped_gemm(hip, fmt, ne11, prequant):
+    """Many pairs per expert: the device groups the pairs by expert and the
+    grouped MFMA GEMMs run them (ragged tiles, one expert unused, invalid ids
+    skipped).  A pre-quantized Q8_0 src1 takes the pair GEMV (the Q4_0 / MXFP4
+    GEMMs read a planar activation quantized from F32)."""
     rng = np.random.default_rng(5)
     n_tok, n_ids, n_as = 70, 4, 8
     ids = rng.integers(0, n_as - 1, size=(n_tok, n_ids))  # expert 7 never chosen
     ids[3, 2] = -1
     ids[40, 0] = n_as
-    run_id(hip, "q4_k", 1024, 300, n_as, n_ids, ne11, n_tok, ids, pad_w=16,
+    run_id(hip, fmt, 1024, 300, n_as, n_ids, ne11, n_tok, ids, pad_w=16,
            pad_x=0 if prequant else 4, prequant=prequant)

@@ -296,28 +296,57 @@ hipError_t mul_mat_id(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1,
   const uint8_t* xq_in = quantize ? nullptr : static_cast<const uint8_t*>(s1->data);
   uint8_t* xq_out = quantize ? static_cast<uint8_t*>(wdata) : nullptr;
   float* Y = static_cast<float*>(d->data);
-  // Q4_K with several pairs per expert on average: group the pairs by
-  // expert on the device and run the grouped MFMA GEMM over the quantized
-  // activation (GGML's own order: quantize src1, group, multiply)
-  if (s0->type == WEFT_GGML_TYPE_Q4_K && n_pairs >= 64 && n_pairs >= 4 * n_as) {
+  // several pairs per expert on average: group the pairs by expert on the
+  // device and run the grouped MFMA GEMM (GGML's own order: quantize src1,
+  // group, multiply); the grouping lives in the part of wdata GGML's plan
+  // reserves for its row mapping
+  if (n_pairs >= 64 && n_pairs >= 4 * n_as && wdata != nullptr) {
     const size_t xq_bytes = nbw1 * (size_t)(ne11 * n_tok);
     const size_t used = quantize ? (xq_bytes + 15) & ~(size_t)15 : 0;
     uint8_t* ws = static_cast<uint8_t*>(wdata) + used;
-    if (wdata != nullptr && wsize >= used &&
-        mul_mat_id_q4k_grouped_ok(W, xq_bytes, Y, (size_t)N, (size_t)K, st, pr, n_pairs, ws,
-                                  wsize - used)) {
-      if (quantize) {
-        const size_t ldx = s1->nb[1] / 4;
-        if (n_tok == 1 || s1->nb[2] == (size_t)ne11 * s1->nb[1]) {
-          quantize_q8_k_rows(X, ldx, xq_out, (size_t)(ne11 * n_tok), (size_t)K);
-        } else {
-          for (int64_t t = 0; t < n_tok; ++t)
-            quantize_q8_k_rows(X + (size_t)t * (s1->nb[2] / 4), ldx, xq_out + (size_t)t * ne11 * nbw1,
-                               (size_t)ne11, (size_t)K);
-        }
+    const size_t ws_bytes = wsize >= used ? wsize - used : 0;
+    const size_t n = (size_t)N, k = (size_t)K;
+    // src1 rows (t, j) -> Q8_K records at (t * ne11 + j) * nbw1 of wdata
+    auto quantize_q8k = [&]() {
+      if (!quantize) return;
+      if (ne11 == 1) {
+        quantize_q8_k_rows(X, n_tok > 1 ? (size_t)pr.x_s2 : k, xq_out, (size_t)n_tok, k);
+      } else if (n_tok == 1 || pr.x_s2 == (long long)ne11 * pr.x_s1) {
+        quantize_q8_k_rows(X, (size_t)pr.x_s1, xq_out, (size_t)(ne11 * n_tok), k);
+      } else {
+        for (int64_t t = 0; t < n_tok; ++t)
+          quantize_q8_k_rows(X + (size_t)t * pr.x_s2, (size_t)pr.x_s1, xq_out + (size_t)t * ne11 * nbw1,
+                             (size_t)ne11, k);
       }
-      mul_mat_id_q4k_grouped(W, quantize ? xq_out : xq_in, Y, (size_t)N, (size_t)K, st, pr, n_pairs, ws);
-      return pending_error();
+    };
+    const uint8_t* xq = quantize ? xq_out : xq_in;
+    switch (s0->type) {
+      case WEFT_GGML_TYPE_Q4_K:
+        if (mul_mat_id_q4k_grouped_ok(W, xq_bytes, Y, n, k, st, pr, n_pairs, ws, ws_bytes)) {
+          quantize_q8k();
+          mul_mat_id_q4k_grouped(W, xq, Y, n, k, st, pr, n_pairs, ws);
+          return pending_error();
+        }
+        break;
+      case WEFT_GGML_TYPE_IQ2_XXS:
+        if (mul_mat_id_iq2_grouped_ok(W, xq_bytes, Y, tab->grid, tab->signs, n, k, st, pr, n_pairs, ws,
+                                      ws_bytes)) {
+          quantize_q8k();
+          mul_mat_id_iq2_grouped(W, xq, tab->grid, tab->signs, Y, n, k, st, pr, n_pairs, ws);
+          return pending_error();
+        }
+        break;
+      default: {  // Q4_0 / MXFP4: the GEMMs read a planar activation quantized from X
+        const int fmt = s0->type == WEFT_GGML_TYPE_Q4_0 ? 0 : 1;
+        const int8_t* cb = fmt ? tab->codebook : nullptr;
+        const float* sc = fmt ? tab->scale : nullptr;
+        if (quantize && mul_mat_id_q80_grouped_ok(fmt, W, X, xq_out, Y, n, k, st, pr, n_pairs,
+                                                  (int)n_tok, ws, ws_bytes, cb, sc)) {
+          mul_mat_id_q80_grouped(fmt, W, X, xq_out, Y, n, k, st, pr, n_pairs, (int)n_tok, ws, cb, sc);
+          return pending_error();
+        }
+        break;
+      }
     }
   }
   switch (s0->type) {

@@ -63,6 +63,9 @@ struct MoeGroups {
   int32_t* pairs;
   int tmax;
 };
+inline GroupTiles group_tiles(const MoeGroups& g, const PairArgs& pr) {
+  return GroupTiles{g.tiles, g.ntiles, g.pairs, pr.n_ids, pr.ne11, g.tmax, pr.w_es, pr.y_s1, pr.y_s2};
+}
 int moe_tile_bound(int n_pairs, int n_as);
 size_t moe_group_bytes(int n_pairs, int n_as);
 MoeGroups moe_group(const PairArgs& pr, int n_pairs, void* ws);
@@ -74,6 +77,23 @@ bool mul_mat_id_q4k_grouped_ok(const uint8_t* W, size_t xq_bytes, const float* Y
                                size_t ws_bytes);
 void mul_mat_id_q4k_grouped(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K,
                             const RowStrides& st, const PairArgs& pr, int n_pairs, void* ws);
+// Q4_0 (fmt 0) / MXFP4 (fmt 1) MUL_MAT_ID on the grouped MFMA GEMMs: src1
+// rows (token t, row j) at t * pr.x_s2 + j * pr.x_s1 floats, quantized into
+// Xq (planar for the GEMM, GGML's records at the end).
+bool mul_mat_id_q80_grouped_ok(int fmt, const uint8_t* W, const float* X, const uint8_t* Xq, const float* Y,
+                               size_t N, size_t K, const RowStrides& st, const PairArgs& pr, int n_pairs,
+                               int n_tok, const void* ws, size_t ws_bytes, const int8_t* codebook,
+                               const float* scale);
+void mul_mat_id_q80_grouped(int fmt, const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N,
+                            size_t K, const RowStrides& st, const PairArgs& pr, int n_pairs, int n_tok,
+                            void* ws, const int8_t* codebook, const float* scale);
+// IQ2_XXS MUL_MAT_ID on the grouped MFMA GEMM over quantized Q8_K rows
+bool mul_mat_id_iq2_grouped_ok(const uint8_t* W, size_t xq_bytes, const float* Y, const int8_t* grid,
+                               const int8_t* signs, size_t N, size_t K, const RowStrides& st,
+                               const PairArgs& pr, int n_pairs, const void* ws, size_t ws_bytes);
+void mul_mat_id_iq2_grouped(const uint8_t* W, const uint8_t* Xq, const int8_t* grid, const int8_t* signs,
+                            float* Y, size_t N, size_t K, const RowStrides& st, const PairArgs& pr,
+                            int n_pairs, void* ws);
 // Q4_0 (fmt 0), MXFP4 (1) or IQ2_XXS (2) GEMV over an already quantized
 // activation (Q8_0 / Q8_0 / Q8_K records, read only)
 void decode_quantized(int fmt, const uint8_t* W, const uint8_t* Xq, const int8_t* tab0,

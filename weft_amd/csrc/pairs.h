@@ -47,4 +47,41 @@ __device__ inline bool resolve_pair(A& a) {
   return true;
 }
 
+// Grouped (MUL_MAT_ID) mode of the MFMA GEMMs: the pairs grouped by expert
+// into tiles of at most 64 (moe_group in moe.hip); a workgroup takes tile g
+// (tiles past the device's count exit before any barrier), gathers its
+// activation rows through the pair list and scatters its outputs.
+struct GroupTiles {
+  const int32_t* tiles;   // [tmax][3]: expert, first index into pairs, count
+  const int32_t* ntiles;  // the tile count (device)
+  const int32_t* pairs;   // p = token * n_ids + slot, grouped by expert
+  int n_ids, ne11, tmax;
+  long long w_es;         // bytes between expert matrices
+  long long y_s1, y_s2;   // floats between dst rows (slots) / planes (tokens)
+};
+
+// Tile g of the table: false past the tile count; else its first pair index,
+// its pair count and the byte offset of its expert's matrix.
+__device__ inline bool group_tile(const GroupTiles& g, int tile, int& m0, int& mrows, long long& w_off) {
+  if (tile >= __builtin_amdgcn_readfirstlane(*g.ntiles)) return false;
+  w_off = (long long)__builtin_amdgcn_readfirstlane(g.tiles[3 * tile]) * g.w_es;
+  m0 = __builtin_amdgcn_readfirstlane(g.tiles[3 * tile + 1]);
+  mrows = __builtin_amdgcn_readfirstlane(g.tiles[3 * tile + 2]);
+  return true;
+}
+
+// activation row (token * ne11 + slot % ne11) of the tile's row r
+__device__ inline int group_act_row(const GroupTiles& g, int m0, int r) {
+  const int p = g.pairs[m0 + r];
+  const int t = p / g.n_ids, s = p - t * g.n_ids;
+  return t * g.ne11 + s % g.ne11;
+}
+
+// float offset of the dst row of the tile's row r
+__device__ inline long long group_dst_row(const GroupTiles& g, int m0, int r) {
+  const int p = g.pairs[m0 + r];
+  const int t = p / g.n_ids, s = p - t * g.n_ids;
+  return t * g.y_s2 + s * g.y_s1;
+}
+
 }  // namespace weft

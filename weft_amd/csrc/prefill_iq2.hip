@@ -53,6 +53,7 @@ struct GemmArgs {
   int N, K, M;
   size_t ldw;     // bytes between weight rows
   long long ldy;  // floats between output rows
+  GroupTiles grp;  // grouped (MUL_MAT_ID) mode
 };
 
 // Direct global->LDS loads; lane l writes [lds + size*l, +size).  Inline asm
@@ -89,6 +90,7 @@ __device__ __forceinline__ uint32_t apply_signs(uint32_t g, uint32_t s) {
   return (g ^ m) + (m & 0x01010101u);
 }
 
+template <bool kGroup>
 __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
   __shared__ __align__(16) uint8_t ring0[kSlotAlloc];
   __shared__ __align__(16) uint8_t ring1[kSlotAlloc];
@@ -106,15 +108,31 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
   const size_t wrb = a.ldw;
   const size_t xrb = (size_t)nsb * kQ8_KBytes;
 
-  int m0, n0;  // XCD-aware tile order (workgroups are dealt round-robin to 8 XCDs)
+  // XCD-aware tile order (workgroups are dealt round-robin to 8 XCDs);
+  // grouped: m0 indexes the pair list, mrows pairs, W the tile's expert
+  int m0, n0, mrows;
+  const uint8_t* W = a.W;
   {
-    const int ntm = (a.M + kMT - 1) / kMT;
+    const int ntm = kGroup ? a.grp.tmax : (a.M + kMT - 1) / kMT;
     const int Tn = ntm * ((a.N + kNT - 1) / kNT);
     const int L = blockIdx.x, x = L & 7, j = L >> 3;
     const int t = x * (Tn >> 3) + min(x, Tn & 7) + j;
-    m0 = (t % ntm) * kMT;
     n0 = (t / ntm) * kNT;
+    if constexpr (kGroup) {
+      long long w_off;
+      if (!group_tile(a.grp, t % ntm, m0, mrows, w_off)) return;  // no barrier yet
+      W += w_off;
+    } else {
+      m0 = (t % ntm) * kMT;
+      mrows = min(kMT, a.M - m0);
+    }
   }
+  auto act_row = [&](int r) -> int {
+    if constexpr (kGroup)
+      return group_act_row(a.grp, m0, r);
+    else
+      return m0 + r;
+  };
 
   for (int i = tid; i < 256 * 8; i += kThreads) tgrid[i] = (uint8_t)a.grid[i];
   for (int i = tid; i < 128 * 8; i += kThreads) tsign[i] = (uint8_t)a.signs[i];
@@ -125,9 +143,9 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
   for (int i = 0; i < 4; ++i) {
     const int k = wcol + 4 * i;
     const int q = 64 * k + lane, r = q >> 4, c = (q & 15) ^ (r & 15);
-    asrc[i] = a.Xq + (size_t)min(m0 + r, a.M - 1) * xrb + 4 + 16 * c;
+    asrc[i] = a.Xq + (size_t)act_row(min(r, mrows - 1)) * xrb + 4 + 16 * c;
   }
-  const uint8_t* dsrc = a.Xq + (size_t)min(m0 + lane, a.M - 1) * xrb;  // Q8_K d of token lane
+  const uint8_t* dsrc = a.Xq + (size_t)act_row(min(lane, mrows - 1)) * xrb;  // Q8_K d of token lane
 
   auto issue = [&](int pair, uint8_t* ring) {
     const int b = 2 * pair + par;
@@ -141,7 +159,7 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
       const int k = wave + 8 * i;
       if (k < kWSlots) {
         const int q = 64 * k + lane, row = q / kWD, part = q - kWD * row;
-        const uint8_t* g = a.W + (size_t)min(n0 + row, a.N - 1) * wrb + (size_t)pair * kPairB + 4 * part;
+        const uint8_t* g = W + (size_t)min(n0 + row, a.N - 1) * wrb + (size_t)pair * kPairB + 4 * part;
         lds_dma4(g, __builtin_amdgcn_readfirstlane(lds_addr(ring + 2 * kAQ + 256 * k)));
       }
     }
@@ -251,8 +269,11 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int gm = m0 + 32 * t + 8 * (r >> 2) + 4 * kg + (r & 3);
-        if (gm < a.M) a.Y[(size_t)gm * a.ldy + gn] = 0.125f * (y[t][r] + red[(16 * t + r) * 64]);
+        const int rr = 32 * t + 8 * (r >> 2) + 4 * kg + (r & 3);
+        if (rr < mrows) {
+          const long long yrow = kGroup ? group_dst_row(a.grp, m0, rr) : (long long)(m0 + rr) * a.ldy;
+          a.Y[yrow + gn] = 0.125f * (y[t][r] + red[(16 * t + r) * 64]);
+        }
       }
   }
 }
@@ -273,13 +294,37 @@ bool gemm_iq2_ok(const uint8_t* W, const void* Xq, const float* Y, const int8_t*
 void gemm_iq2(const uint8_t* W, const uint8_t* Xq, const int8_t* grid, const int8_t* signs, float* Y,
               size_t N, size_t K, size_t M, const RowStrides& st) {
   const size_t ldw = N > 1 ? st.ldw : K / 256 * kIq2xxsBytes;
-  GemmArgs ga{W, Xq, grid, signs, Y, (int)N, (int)K, (int)M, ldw, (long long)st.ldy};
+  GemmArgs ga{W, Xq, grid, signs, Y, (int)N, (int)K, (int)M, ldw, (long long)st.ldy, GroupTiles{}};
   const size_t tiles = ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT);
-  iq2_mfma_gemm<<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(ga);
+  iq2_mfma_gemm<false><<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(ga);
   check_launch();
 }
 
 }  // namespace
+
+bool mul_mat_id_iq2_grouped_ok(const uint8_t* W, size_t xq_bytes, const float* Y, const int8_t* grid,
+                               const int8_t* signs, size_t N, size_t K, const RowStrides& st,
+                               const PairArgs& pr, int n_pairs, const void* ws, size_t ws_bytes) {
+  const size_t rb = K / 256 * kIq2xxsBytes;
+  const size_t ldw = N > 1 ? st.ldw : rb;
+  return N > 0 && n_pairs > 0 && K > 0 && K % 512 == 0 && W != nullptr && Y != nullptr &&
+         grid != nullptr && signs != nullptr && aligned(W, 4) && ldw % 4 == 0 && aligned(Y, 4) &&
+         xq_bytes < ((size_t)1 << 32) && aligned(ws, 16) && ws_bytes >= moe_group_bytes(n_pairs, pr.n_as) &&
+         pr.w_es % 4 == 0 && pr.n_as <= kMaxExperts && N <= (size_t)INT32_MAX && K <= (size_t)INT32_MAX &&
+         strides_ok(st, rb, 2, K, N, N, 1) &&
+         (size_t)moe_tile_bound(n_pairs, pr.n_as) * ((N + kNT - 1) / kNT) <= (size_t)INT32_MAX;
+}
+
+void mul_mat_id_iq2_grouped(const uint8_t* W, const uint8_t* Xq, const int8_t* grid, const int8_t* signs,
+                            float* Y, size_t N, size_t K, const RowStrides& st, const PairArgs& pr,
+                            int n_pairs, void* ws) {
+  const MoeGroups g = moe_group(pr, n_pairs, ws);
+  const size_t ldw = N > 1 ? st.ldw : K / 256 * kIq2xxsBytes;
+  GemmArgs ga{W, Xq, grid, signs, Y, (int)N, (int)K, kMT, ldw, 0, group_tiles(g, pr)};
+  const size_t wgs = (size_t)g.tmax * ((N + kNT - 1) / kNT);
+  iq2_mfma_gemm<true><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(ga);
+  check_launch();
+}
 
 void mul_mat_iq2_xxs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,
                      const int8_t* signs, float* Y, size_t N, size_t K, size_t M,

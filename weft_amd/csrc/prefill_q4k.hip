@@ -101,14 +101,7 @@ struct GemmArgs {
   int N, K, M;
   uint32_t ldw;   // bytes between weight rows (a tile's 128 rows stay in 32-bit offsets)
   long long ldy;  // floats between output rows
-  // grouped mode: tile g = {expert, first pair index, pairs}; pairs are
-  // p = token * n_ids + slot, activation row token * ne11 + slot % ne11
-  const int32_t* tiles;
-  const int32_t* ntiles;
-  const int32_t* pairs;
-  int n_ids, ne11, tmax;
-  long long w_es;        // bytes between expert matrices
-  long long y_s1, y_s2;  // floats between dst rows (slots) / planes (tokens)
+  GroupTiles grp;  // grouped (MUL_MAT_ID) mode
 };
 
 // Direct global->LDS load of 16 bytes per lane: lane l reads sbase + voff
@@ -167,15 +160,13 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
   if constexpr (kGroup) {
     // m0 indexes the pair list.  XCD-aware order as below: an expert's
     // consecutive tiles on one column block meet in one XCD's L2.
-    const int T = a.tmax * ((a.N + kNT - 1) / kNT);
+    const int T = a.grp.tmax * ((a.N + kNT - 1) / kNT);
     const int L = blockIdx.x, x = L & 7, j = L >> 3;
     const int t = x * (T >> 3) + min(x, T & 7) + j;
-    const int g = t % a.tmax;
-    if (g >= __builtin_amdgcn_readfirstlane(*a.ntiles)) return;  // whole workgroup, no barrier yet
-    W += (long long)__builtin_amdgcn_readfirstlane(a.tiles[3 * g]) * a.w_es;
-    m0 = a.tiles[3 * g + 1];
-    mrows = a.tiles[3 * g + 2];
-    n0 = (t / a.tmax) * kNT;
+    long long w_off;
+    if (!group_tile(a.grp, t % a.grp.tmax, m0, mrows, w_off)) return;  // no barrier yet
+    W += w_off;
+    n0 = (t / a.grp.tmax) * kNT;
   } else {
     const int ntm = (a.M + kMT - 1) / kMT;
     const int T = ntm * ((a.N + kNT - 1) / kNT);
@@ -190,13 +181,10 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
   mrows = __builtin_amdgcn_readfirstlane(mrows);
   // activation row of tile row r (r < mrows)
   auto act_row = [&](int r) -> int {
-    if constexpr (kGroup) {
-      const int p = a.pairs[m0 + r];
-      const int t = p / a.n_ids, s = p - t * a.n_ids;
-      return t * a.ne11 + s % a.ne11;
-    } else {
+    if constexpr (kGroup)
+      return group_act_row(a.grp, m0, r);
+    else
       return m0 + r;
-    }
   };
   const int nsb = a.K >> 8;
   const int npair = (nsb + 1) >> 1;
@@ -408,9 +396,7 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
         if (rr < mrows) {
           const float v = y[t][r] + red[(16 * t + r) * 64];
           if constexpr (kGroup) {
-            const int p = a.pairs[m0 + rr];
-            const int tk = p / a.n_ids, sl = p - tk * a.n_ids;
-            a.Y[tk * a.y_s2 + sl * a.y_s1 + gn] = v;
+            a.Y[group_dst_row(a.grp, m0, rr) + gn] = v;
           } else {
             a.Y[(size_t)(m0 + rr) * a.ldy + gn] = v;
           }
@@ -490,15 +476,7 @@ void mul_mat_id_q4k_grouped(const uint8_t* W, const uint8_t* Xq, float* Y, size_
   a.K = (int)K;
   a.M = kMT;
   a.ldw = (uint32_t)(N > 1 ? st.ldw : rb);
-  a.tiles = g.tiles;
-  a.ntiles = g.ntiles;
-  a.pairs = g.pairs;
-  a.n_ids = pr.n_ids;
-  a.ne11 = pr.ne11;
-  a.tmax = g.tmax;
-  a.w_es = pr.w_es;
-  a.y_s1 = pr.y_s1;
-  a.y_s2 = pr.y_s2;
+  a.grp = group_tiles(g, pr);
   const size_t wgs = (size_t)g.tmax * ((N + kNT - 1) / kNT);
   q4k_mfma_gemm<true><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(a);
   check_launch();

@@ -69,6 +69,7 @@ struct GemmArgs {
   int N, K, M;
   size_t ldw;     // bytes between weight rows
   long long ldy;  // floats between output rows
+  GroupTiles grp;  // grouped (MUL_MAT_ID) mode
 };
 
 // 16 bytes per lane from global straight into LDS: lane l writes
@@ -119,7 +120,7 @@ constexpr int q80_lds_bytes() {
   return 4 * (kAQ + kNT * 8 * WTraits<F>::kRec) + 2 * 2 * 8 * kMT * 4 + 256 * 4;
 }
 
-template <WFmt F>
+template <WFmt F, bool kGroup>
 __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
   using T = WTraits<F>;
   constexpr int kRB = 8 * T::kRec;           // raw weight bytes per row and stage
@@ -148,16 +149,31 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
   const size_t xs = (size_t)a.K + (size_t)a.K / 16;  // planar activation row stride
   const size_t ws_row = a.ldw;
 
-  // XCD-aware tile order (workgroups are dealt round-robin to 8 XCDs)
-  int m0, n0;
+  // XCD-aware tile order (workgroups are dealt round-robin to 8 XCDs);
+  // grouped: m0 indexes the pair list, mrows pairs, W the tile's expert
+  int m0, n0, mrows;
+  const uint8_t* W = a.W;
   {
-    const int ntm = (a.M + kMT - 1) / kMT;
+    const int ntm = kGroup ? a.grp.tmax : (a.M + kMT - 1) / kMT;
     const int Tn = ntm * ((a.N + kNT - 1) / kNT);
     const int L = blockIdx.x, x = L & 7, j = L >> 3;
     const int t = x * (Tn >> 3) + min(x, Tn & 7) + j;
-    m0 = (t % ntm) * kMT;
     n0 = (t / ntm) * kNT;
+    if constexpr (kGroup) {
+      long long w_off;
+      if (!group_tile(a.grp, t % ntm, m0, mrows, w_off)) return;  // no barrier yet
+      W += w_off;
+    } else {
+      m0 = (t % ntm) * kMT;
+      mrows = min(kMT, a.M - m0);
+    }
   }
+  auto act_row = [&](int r) -> int {
+    if constexpr (kGroup)
+      return group_act_row(a.grp, m0, r);
+    else
+      return m0 + r;
+  };
 
   uint32_t c0 = 0, c1 = 0, c2 = 0, c3 = 0;
   if constexpr (F == WFmt::MXFP4) {
@@ -178,10 +194,10 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
   for (int i = 0; i < 4; ++i) {
     const int k = wcol + 4 * i;
     const int q = 64 * k + lane, r = q >> 4, c = (q & 15) ^ (r & 15);
-    asrc[i] = a.Xp + (size_t)min(m0 + r, a.M - 1) * xs + 16 * c;
+    asrc[i] = a.Xp + (size_t)act_row(min(r, mrows - 1)) * xs + 16 * c;
   }
   // per-block token scales of this parity's stage: wave wcol == 0, token = lane
-  const uint8_t* dsrc = a.Xp + (size_t)min(m0 + lane, a.M - 1) * xs + a.K;
+  const uint8_t* dsrc = a.Xp + (size_t)act_row(min(lane, mrows - 1)) * xs + a.K;
 
   auto issue = [&](int pair, uint8_t* ring) {
     const int st = min(2 * pair + par, nst - 1);
@@ -194,7 +210,7 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
     for (int i = 0; i < kWPerWave; ++i) {
       const int k = wcol + 4 * i;
       const int q = 64 * k + lane, row = q / kWD, part = q - kWD * row;
-      const uint8_t* g = a.W + (size_t)min(n0 + row, a.N - 1) * ws_row + (size_t)st * kRB + 4 * part;
+      const uint8_t* g = W + (size_t)min(n0 + row, a.N - 1) * ws_row + (size_t)st * kRB + 4 * part;
       lds_dma4(g, __builtin_amdgcn_readfirstlane(lds_addr(stage + kAQ + 256 * k)));
     }
   };
@@ -319,16 +335,19 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int gm = m0 + 32 * t + 8 * (r >> 2) + 4 * kg + (r & 3);
-        if (gm < a.M) a.Y[(size_t)gm * a.ldy + gn] = y[t][r] + red[(16 * t + r) * 64];
+        const int rr = 32 * t + 8 * (r >> 2) + 4 * kg + (r & 3);
+        if (rr < mrows) {
+          const long long yrow = kGroup ? group_dst_row(a.grp, m0, rr) : (long long)(m0 + rr) * a.ldy;
+          a.Y[yrow + gn] = y[t][r] + red[(16 * t + r) * 64];
+        }
       }
   }
 }
 
-template <WFmt F>
+template <WFmt F, bool kGroup>
 __global__ void __launch_bounds__(kThreads, 1) q80_mfma_gemm(GemmArgs a) {
   __shared__ __align__(16) uint8_t lds[q80_lds_bytes<F>()];
-  q80_gemm_body<F>(a, lds);
+  q80_gemm_body<F, kGroup>(a, lds);
 }
 
 __device__ __forceinline__ float4 ldx4(const float* p, bool a16) {
@@ -467,6 +486,7 @@ __device__ __forceinline__ void lds_barrier() {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 
+template <bool kGroup>
 __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -477,18 +497,34 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
   const uint32_t xs = (uint32_t)a.K + (uint32_t)a.K / 16;  // planar activation row stride
   const uint32_t ws_row = (uint32_t)a.ldw;  // the host keeps a tile's rows in 32-bit offsets
 
-  int m0, n0;
+  int m0, n0, mrows;
+  const uint8_t* W = a.W;
   {
-    const int ntm = (a.M + kMT - 1) / kMT;
+    const int ntm = kGroup ? a.grp.tmax : (a.M + kMT - 1) / kMT;
     const int Tn = ntm * ((a.N + kNT - 1) / kNT);
     const int L = blockIdx.x, x = L & 7, j = L >> 3;
     const int t = x * (Tn >> 3) + min(x, Tn & 7) + j;
-    m0 = __builtin_amdgcn_readfirstlane((t % ntm) * kMT);
     n0 = __builtin_amdgcn_readfirstlane((t / ntm) * kNT);
+    if constexpr (kGroup) {
+      long long w_off;
+      if (!group_tile(a.grp, t % ntm, m0, mrows, w_off)) return;  // no barrier yet
+      W += w_off;
+    } else {
+      m0 = __builtin_amdgcn_readfirstlane((t % ntm) * kMT);
+      mrows = min(kMT, a.M - m0);
+    }
   }
-  const uint8_t* xbase = a.Xp + (size_t)m0 * xs;
-  const uint8_t* wbase = a.W + (size_t)n0 * ws_row;
-  const int mlast = a.M - 1 - m0, nlast = a.N - 1 - n0;
+  // grouped: rows are gathered, offsets from Xp itself (the host keeps the
+  // planar activation within 32-bit offsets)
+  const uint8_t* xbase = kGroup ? a.Xp : a.Xp + (size_t)m0 * xs;
+  const uint8_t* wbase = W + (size_t)n0 * ws_row;
+  const int mlast = mrows - 1, nlast = a.N - 1 - n0;
+  auto act_row = [&](int r) -> uint32_t {
+    if constexpr (kGroup)
+      return (uint32_t)group_act_row(a.grp, m0, r);
+    else
+      return (uint32_t)r;
+  };
 
   // Load plan per stage: 16 activation loads (1 KB = 4 tokens each), 4 dword
   // loads of the token scales (block pair kp of 64 tokens each), 70 weight
@@ -497,14 +533,14 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
   // last row.
   auto act_off = [&](int c) {
     const int q = 64 * c + lane, t = q >> 4, s = q & 15;
-    return (uint32_t)min(t, mlast) * xs + 16 * (uint32_t)(s ^ (t & 15));
+    return act_row(min(t, mlast)) * xs + 16 * (uint32_t)(s ^ (t & 15));
   };
   auto w_off = [&](int k) {
     const int q = 64 * k + lane, row = q / (kRowW / 4), part = q - (kRowW / 4) * row;
     return (uint32_t)min(row, nlast) * ws_row + 4 * (uint32_t)min(part, 33);
   };
   const uint32_t va0 = act_off(wave), va1 = act_off(wave + 8);
-  const uint32_t v2 = wave < 4 ? (uint32_t)min(lane, mlast) * xs + (uint32_t)a.K + 4 * wave : w_off(wave - 4);
+  const uint32_t v2 = wave < 4 ? act_row(min(lane, mlast)) * xs + (uint32_t)a.K + 4 * wave : w_off(wave - 4);
   uint32_t vw[9];
 #pragma unroll
   for (int i = 0; i < 9; ++i) vw[i] = w_off(min(wave + 8 * i + 4, kWLoads - 1));
@@ -616,8 +652,9 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
           make_float4(y[q][4 * r4], y[q][4 * r4 + 1], y[q][4 * r4 + 2], y[q][4 * r4 + 3]);
   __syncthreads();
   const int q = ph, th = q >> 1, ct = q & 1;
-  const int gm = m0 + 32 * th + col;
-  const bool v4 = (a.ldy & 3) == 0 && (reinterpret_cast<uintptr_t>(a.Y) & 15) == 0;
+  const int rr = 32 * th + col;
+  const bool v4 = (kGroup ? ((a.grp.y_s1 | a.grp.y_s2) & 3) == 0 : (a.ldy & 3) == 0) &&
+                  (reinterpret_cast<uintptr_t>(a.Y) & 15) == 0;
 #pragma unroll
   for (int r4 = 0; r4 < 4; ++r4) {
     float4 v = red[(((cp + 0) * 4 + q) * 4 + r4) * 64 + lane];
@@ -631,8 +668,8 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
     }
     // register r holds weight row 8*(r/4) + 4*h + r%4 of the tile
     const int gn = n0 + 64 * cp + 32 * ct + 8 * r4 + 4 * h;
-    if (gm < a.M) {
-      float* yr = a.Y + (size_t)gm * a.ldy;
+    if (rr < mrows) {
+      float* yr = a.Y + (kGroup ? group_dst_row(a.grp, m0, rr) : (long long)(m0 + rr) * a.ldy);
       if (v4 && gn + 3 < a.N) {
         *reinterpret_cast<float4*>(yr + gn) = v;
       } else {
@@ -651,12 +688,27 @@ constexpr int kMxLds = mx::kLds > q80_lds_bytes<WFmt::MXFP4>() ? mx::kLds : q80_
 
 // The block-scaled MFMA computes with GGML's tables; with any other tables
 // the workgroup runs the int8 body, which looks every value up.
+template <bool kGroup>
 __global__ void __launch_bounds__(kThreads, 1) mxfp4_gemm(GemmArgs a) {
   __shared__ __align__(16) uint8_t lds[kMxLds];
   if (__syncthreads_and(ggml_mxfp4_entry(a.codebook, a.scale, threadIdx.x)))
-    mx::scaled_body(a, lds);
+    mx::scaled_body<kGroup>(a, lds);
   else
-    q80_gemm_body<WFmt::MXFP4>(a, lds);
+    q80_gemm_body<WFmt::MXFP4, kGroup>(a, lds);
+}
+
+// Q8_0 quantization of M rows of X (ldx floats apart) into the planar layout
+template <WFmt F>
+void planar_pass(const float* X, size_t ldx, uint8_t* Xp, size_t M, size_t K, const int8_t* codebook,
+                 const float* scale) {
+  const long long nb = (long long)(M * K / 32);
+  const long long xs = (long long)(K + K / 16);
+  const long long waves = (nb + 7) / 8;
+  const int grid = (int)std::max<long long>(1, std::min<long long>((long long)cu_count() * 8, (waves + 3) / 4));
+  const bool a16 = aligned(X, 16) && ldx % 4 == 0;
+  q80_planar_kernel<F == WFmt::MXFP4><<<grid, 256, 0, current_stream()>>>(
+      X, (long long)ldx, a16, Xp, nb, (int)(K / 32), xs, codebook, scale);
+  check_launch();
 }
 
 template <WFmt F>
@@ -675,21 +727,14 @@ bool prefill_q80(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* co
       ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT) > (size_t)INT32_MAX)
     return false;
   if (F == WFmt::MXFP4 && (codebook == nullptr || scale == nullptr)) return false;
-  const long long nb = (long long)(M * K / 32);
-  const long long xs = (long long)(K + K / 16);
-  const long long waves = (nb + 7) / 8;
-  const int grid = (int)std::max<long long>(1, std::min<long long>((long long)cu_count() * 8, (waves + 3) / 4));
   const size_t ldx = M > 1 ? st.ldx : K;
-  const bool a16 = aligned(X, 16) && ldx % 4 == 0;
-  q80_planar_kernel<F == WFmt::MXFP4><<<grid, 256, 0, current_stream()>>>(
-      X, (long long)ldx, a16, Xq, nb, (int)(K / 32), xs, codebook, scale);
-  check_launch();
+  planar_pass<F>(X, ldx, Xq, M, K, codebook, scale);
   const size_t tiles = ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT);
-  GemmArgs ga{W, Xq, codebook, scale, Y, (int)N, (int)K, (int)M, ldw, (long long)st.ldy};
+  GemmArgs ga{W, Xq, codebook, scale, Y, (int)N, (int)K, (int)M, ldw, (long long)st.ldy, GroupTiles{}};
   if constexpr (F == WFmt::MXFP4) {
-    mxfp4_gemm<<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(ga);
+    mxfp4_gemm<false><<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(ga);
   } else {
-    q80_mfma_gemm<F><<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(ga);
+    q80_mfma_gemm<F, false><<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(ga);
   }
   check_launch();
   quantize_q8_0_rows(X, ldx, Xq, M, K);  // Xq ends in GGML's record layout
@@ -697,6 +742,57 @@ bool prefill_q80(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* co
 }
 
 }  // namespace
+
+// MUL_MAT_ID on the grouped GEMMs (Q4_0: fmt 0, MXFP4: fmt 1).  X rows
+// (token t, row j) at t * x_s2 + j * x_s1 floats are quantized into Xq
+// planar, then in GGML's records after the GEMM, as the dense path does.
+bool mul_mat_id_q80_grouped_ok(int fmt, const uint8_t* W, const float* X, const uint8_t* Xq, const float* Y,
+                               size_t N, size_t K, const RowStrides& st, const PairArgs& pr, int n_pairs,
+                               int n_tok, const void* ws, size_t ws_bytes, const int8_t* codebook,
+                               const float* scale) {
+  const size_t rb = K / 32 * (fmt == 0 ? kQ4_0Bytes : kMxfp4Bytes);
+  const size_t ldw = N > 1 ? st.ldw : rb;
+  const size_t xq_bytes = (size_t)n_tok * pr.ne11 * (K / 32) * kQ8_0Bytes;
+  return N > 0 && K > 0 && n_pairs > 0 && K % 256 == 0 && X != nullptr && aligned(X, 4) &&
+         aligned(W, 4) && ldw % 4 == 0 && (kNT - 1) * ldw + rb < ((size_t)1 << 32) &&
+         aligned(Xq, 16) && xq_bytes < ((size_t)1 << 32) && aligned(Y, 4) && aligned(ws, 16) &&
+         ws_bytes >= moe_group_bytes(n_pairs, pr.n_as) && pr.w_es % 4 == 0 &&
+         pr.n_as <= kMaxExperts && N <= (size_t)INT32_MAX && K <= (size_t)INT32_MAX &&
+         strides_ok(st, rb, 1, K, N, N, 1) && (fmt == 0 || (codebook != nullptr && scale != nullptr)) &&
+         (size_t)moe_tile_bound(n_pairs, pr.n_as) * ((N + kNT - 1) / kNT) <= (size_t)INT32_MAX;
+}
+
+void mul_mat_id_q80_grouped(int fmt, const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N,
+                            size_t K, const RowStrides& st, const PairArgs& pr, int n_pairs, int n_tok,
+                            void* ws, const int8_t* codebook, const float* scale) {
+  const size_t rb = K / 32 * (fmt == 0 ? kQ4_0Bytes : kMxfp4Bytes);
+  const size_t rows = (size_t)n_tok * pr.ne11, xs = K + K / 16;
+  // rows (t, j) of X at t * x_s2 + j * x_s1: one pass when they are evenly
+  // spaced, else one per token
+  auto each_plane = [&](auto&& pass, size_t row_bytes) {
+    if (pr.ne11 == 1) return pass(X, n_tok > 1 ? (size_t)pr.x_s2 : K, Xq, (size_t)n_tok);
+    if (n_tok == 1 || pr.x_s2 == (long long)pr.ne11 * pr.x_s1) return pass(X, (size_t)pr.x_s1, Xq, rows);
+    for (int t = 0; t < n_tok; ++t)
+      pass(X + (size_t)t * pr.x_s2, (size_t)pr.x_s1, Xq + (size_t)t * pr.ne11 * row_bytes, (size_t)pr.ne11);
+  };
+  each_plane([&](const float* x, size_t l, uint8_t* xp, size_t m) {
+    if (fmt == 0)
+      planar_pass<WFmt::Q4_0>(x, l, xp, m, K, nullptr, nullptr);
+    else
+      planar_pass<WFmt::MXFP4>(x, l, xp, m, K, codebook, scale);
+  }, xs);
+  const MoeGroups g = moe_group(pr, n_pairs, ws);
+  GemmArgs ga{W, Xq, codebook, scale, Y, (int)N, (int)K, kMT, N > 1 ? st.ldw : rb, 0, group_tiles(g, pr)};
+  const size_t wgs = (size_t)g.tmax * ((N + kNT - 1) / kNT);
+  if (fmt == 0)
+    q80_mfma_gemm<WFmt::Q4_0, true><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(ga);
+  else
+    mxfp4_gemm<true><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(ga);
+  check_launch();
+  // Xq ends in GGML's record layout
+  each_plane([&](const float* x, size_t l, uint8_t* xq, size_t m) { quantize_q8_0_rows(x, l, xq, m, K); },
+             (K / 32) * kQ8_0Bytes);
+}
 
 void mul_mat_q4_0(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
                   size_t M, const RowStrides& st) {
