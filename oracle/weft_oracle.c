@@ -38,6 +38,8 @@
 #define Q4_K_BYTES 144
 #define Q8_K_BYTES 292
 #define IQ2_XXS_BYTES 66
+#define Q6_K_BYTES 210
+#define GROUP_MAX_EPS 1e-15f
 
 static inline uint32_t f32_bits(float f) {
   uint32_t u;
@@ -471,6 +473,106 @@ void wo_quantize_row_iq2_xxs(const float *x, uint8_t *y, int64_t k) {
 
 /* quantize_row_q8_0_ref, ggml-quants.c:238-261: d = amax/127, q = roundf(x/d)
  * (round half away from zero), d stored as fp16. */
+/* make_qx_quants, ggml-quants.c:570-635 (qw == NULL), with the iteration
+ * over is = -9..9 of the candidate scales */
+static float make_qx(int n, int nmax, const float *x, int8_t *L, int rmse_type) {
+  float max = 0, amax = 0;
+  for (int i = 0; i < n; ++i) {
+    const float ax = fabsf(x[i]);
+    if (ax > amax) { amax = ax; max = x[i]; }
+  }
+  if (amax < GROUP_MAX_EPS) {
+    for (int i = 0; i < n; ++i) L[i] = 0;
+    return 0.f;
+  }
+  float iscale = -nmax / max;
+  float sumlx = 0, suml2 = 0;
+  for (int i = 0; i < n; ++i) {
+    int l = nearest_int(iscale * x[i]);
+    l = l < -nmax ? -nmax : l > nmax - 1 ? nmax - 1 : l;
+    L[i] = (int8_t)(l + nmax);
+    const float w = rmse_type == 1 ? x[i] * x[i] : 1.f;
+    sumlx += w * x[i] * l;
+    suml2 += w * l * l;
+  }
+  float scale = suml2 ? sumlx / suml2 : 0.0f;
+  float best = scale * sumlx;
+  for (int is = -9; is <= 9; ++is) {
+    if (is == 0) continue;
+    iscale = -(nmax + 0.1f * is) / max;
+    sumlx = suml2 = 0;
+    for (int i = 0; i < n; ++i) {
+      int l = nearest_int(iscale * x[i]);
+      l = l < -nmax ? -nmax : l > nmax - 1 ? nmax - 1 : l;
+      const float w = rmse_type == 1 ? x[i] * x[i] : 1.f;
+      sumlx += w * x[i] * l;
+      suml2 += w * l * l;
+    }
+    if (suml2 > 0 && sumlx * sumlx > best * suml2) {
+      for (int i = 0; i < n; ++i) {
+        int l = nearest_int(iscale * x[i]);
+        l = l < -nmax ? -nmax : l > nmax - 1 ? nmax - 1 : l;
+        L[i] = (int8_t)(l + nmax);
+      }
+      scale = sumlx / suml2;
+      best = scale * sumlx;
+    }
+  }
+  return scale;
+}
+
+/* quantize_row_q6_K_ref, ggml-quants.c:1811-1879 (input generator).
+ * Record: ql[128] | qh[64] | scales[16] (int8) | d (fp16). */
+void wo_quantize_row_q6_K(const float *x, uint8_t *y, int64_t k) {
+  const int64_t nb = k / QK_K;
+  int8_t L[QK_K];
+  float scales[QK_K / 16];
+  for (int64_t i = 0; i < nb; ++i, x += QK_K, y += Q6_K_BYTES) {
+    float max_scale = 0, max_abs_scale = 0;
+    for (int ib = 0; ib < QK_K / 16; ++ib) {
+      const float scale = make_qx(16, 32, x + 16 * ib, L + 16 * ib, 1);
+      scales[ib] = scale;
+      const float abs_scale = fabsf(scale);
+      if (abs_scale > max_abs_scale) {
+        max_abs_scale = abs_scale;
+        max_scale = scale;
+      }
+    }
+    if (max_abs_scale < GROUP_MAX_EPS) {
+      memset(y, 0, Q6_K_BYTES);
+      wr16(y + 208, wo_fp32_to_fp16(0.f));
+      continue;
+    }
+    const float iscale = -128.f / max_scale;
+    wr16(y + 208, wo_fp32_to_fp16(1 / iscale));
+    int8_t *sc = (int8_t *)(y + 192);
+    for (int ib = 0; ib < QK_K / 16; ++ib) {
+      const int v = nearest_int(iscale * scales[ib]);
+      sc[ib] = (int8_t)(v < 127 ? v : 127);
+    }
+    for (int j = 0; j < QK_K / 16; ++j) {
+      const float d = wo_fp16_to_fp32(rd16(y + 208)) * sc[j];
+      if (!d) continue;
+      for (int ii = 0; ii < 16; ++ii) {
+        int l = nearest_int(x[16 * j + ii] / d);
+        l = l < -32 ? -32 : l > 31 ? 31 : l;
+        L[16 * j + ii] = (int8_t)(l + 32);
+      }
+    }
+    uint8_t *ql = y, *qh = y + 128;
+    for (int j = 0; j < QK_K; j += 128, ql += 64, qh += 32) {
+      for (int l = 0; l < 32; ++l) {
+        const uint8_t q1 = L[j + l] & 0xF, q2 = L[j + l + 32] & 0xF;
+        const uint8_t q3 = L[j + l + 64] & 0xF, q4 = L[j + l + 96] & 0xF;
+        ql[l] = q1 | (q3 << 4);
+        ql[l + 32] = q2 | (q4 << 4);
+        qh[l] = (L[j + l] >> 4) | ((L[j + l + 32] >> 4) << 2) | ((L[j + l + 64] >> 4) << 4) |
+                ((L[j + l + 96] >> 4) << 6);
+      }
+    }
+  }
+}
+
 void wo_quantize_row_q8_0(const float *x, uint8_t *y, int64_t k) {
   const int64_t nb = k / QK8_0;
   for (int64_t i = 0; i < nb; ++i) {
@@ -722,6 +824,75 @@ float wo_vec_dot_iq2_xxs_q8_K(const uint8_t *w, const uint8_t *x, int64_t k) {
   return 0.125f * sumf;
 }
 
+/* dequantize_row_q6_K, ggml-quants.c:1881-1910: y = (d * sc) * q, two
+ * rounded products in this order */
+void wo_dequantize_row_q6_K(const uint8_t *x, float *y, int64_t k) {
+  const int64_t nb = k / QK_K;
+  for (int64_t i = 0; i < nb; ++i) {
+    const uint8_t *r = x + i * Q6_K_BYTES;
+    const float d = wo_fp16_to_fp32(rd16(r + 208));
+    const uint8_t *ql = r, *qh = r + 128;
+    const int8_t *sc = (const int8_t *)(r + 192);
+    for (int n = 0; n < QK_K; n += 128) {
+      for (int l = 0; l < 32; ++l) {
+        const int is = l / 16;
+        const int8_t q1 = (int8_t)((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
+        const int8_t q2 = (int8_t)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+        const int8_t q3 = (int8_t)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+        const int8_t q4 = (int8_t)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+        y[l] = d * sc[is] * q1;
+        y[l + 32] = d * sc[is + 2] * q2;
+        y[l + 64] = d * sc[is + 4] * q3;
+        y[l + 96] = d * sc[is + 6] * q4;
+      }
+      y += 128;
+      ql += 64;
+      qh += 32;
+      sc += 8;
+    }
+  }
+}
+
+/* q of element e (0..255) of a Q6_K record, in [-32, 31] */
+static inline int q6_value(const uint8_t *r, int e) {
+  const int h = e / 128, i = e % 128, qq = i / 32, l = i % 32;
+  const uint8_t b = r[64 * h + l + 32 * (qq & 1)];
+  const int nib = qq < 2 ? (b & 0xF) : (b >> 4);
+  const int hb = (r[128 + 32 * h + l] >> (2 * qq)) & 3;
+  return (nib | (hb << 4)) - 32;
+}
+
+/* ggml_vec_dot_q6_K_q8_K_generic, ggml-cpu/quants.c:800-853: int32 lanes
+ * aux32[8] per superblock, then sums[l] += (dw * dx) * aux32[l] */
+float wo_vec_dot_q6_K_q8_K(const uint8_t *w, const uint8_t *x, int64_t k) {
+  const int64_t nb = k / QK_K;
+  float sums[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int8_t aux8[QK_K];
+  for (int64_t i = 0; i < nb; ++i) {
+    const uint8_t *r = w + i * Q6_K_BYTES;
+    const uint8_t *xr = x + i * Q8_K_BYTES;
+    const int8_t *q8 = (const int8_t *)(xr + 4);
+    for (int e = 0; e < QK_K; ++e) aux8[e] = (int8_t)q6_value(r, e);
+    int32_t aux32[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const int8_t *a = aux8;
+    for (int j = 0; j < QK_K / 16; ++j) {
+      const int scale = ((const int8_t *)(r + 192))[j];
+      for (int half = 0; half < 2; ++half) {
+        int16_t aux16[8];
+        for (int l = 0; l < 8; ++l) aux16[l] = (int16_t)(q8[l] * a[l]);
+        for (int l = 0; l < 8; ++l) aux32[l] += scale * aux16[l];
+        q8 += 8;
+        a += 8;
+      }
+    }
+    const float d = wo_fp16_to_fp32(rd16(r + 208)) * rdf32(xr);
+    for (int l = 0; l < 8; ++l) sums[l] += d * aux32[l];
+  }
+  float sumf = 0;
+  for (int l = 0; l < 8; ++l) sumf += sums[l];
+  return sumf;
+}
+
 /* ------------------------------------------------------------------------
  * MUL_MAT driver and fp64 re-accumulation
  * ---------------------------------------------------------------------- */
@@ -731,6 +902,7 @@ size_t wo_weight_row_bytes(int fmt, int64_t k) {
   case WO_Q4_K: return (size_t)(k / 256) * Q4_K_BYTES;
   case WO_IQ2_XXS: return (size_t)(k / 256) * IQ2_XXS_BYTES;
   case WO_MXFP4: return (size_t)(k / 32) * MXFP4_BYTES;
+  case WO_Q6_K: return (size_t)(k / 256) * Q6_K_BYTES;
   }
   return 0;
 }
@@ -747,6 +919,7 @@ static vec_dot_fn select_vec_dot(int fmt) {
   case WO_Q4_K: return wo_vec_dot_q4_K_q8_K;
   case WO_IQ2_XXS: return wo_vec_dot_iq2_xxs_q8_K;
   case WO_MXFP4: return wo_vec_dot_mxfp4_q8_0;
+  case WO_Q6_K: return wo_vec_dot_q6_K_q8_K;
   }
   return 0;
 }
@@ -847,6 +1020,17 @@ int64_t wo_int_partials(int fmt, const uint8_t *w, const uint8_t *x, int64_t k, 
       }
       out[n++] = b;
     }
+  } else if (fmt == WO_Q6_K) {
+    const int64_t nb = k / QK_K;
+    for (int64_t i = 0; i < nb; ++i) {
+      const uint8_t *wr = w + i * Q6_K_BYTES;
+      const int8_t *q8 = (const int8_t *)(x + i * Q8_K_BYTES + 4);
+      for (int g = 0; g < 16; ++g) {
+        int32_t p = 0;
+        for (int l = 0; l < 16; ++l) p += q6_value(wr, 16 * g + l) * q8[16 * g + l];
+        out[n++] = p;
+      }
+    }
   }
   return n;
 }
@@ -877,6 +1061,18 @@ void wo_mul_mat_f64(int fmt, const uint8_t *W, const uint8_t *Xq, double *E, dou
             e += t;
             a += fabs(t);
           }
+        }
+      } else if (fmt == WO_Q6_K) {
+        const int64_t nb = K / QK_K;
+        for (int64_t i = 0; i < nb; ++i) {
+          const uint8_t *wr = w + i * Q6_K_BYTES;
+          const uint8_t *xr = x + i * Q8_K_BYTES;
+          wo_int_partials(fmt, wr, xr, QK_K, parts);
+          int64_t S = 0;
+          for (int g = 0; g < 16; ++g) S += (int64_t)((const int8_t *)(wr + 192))[g] * parts[g];
+          const double t = (double)wo_fp16_to_fp32(rd16(wr + 208)) * (double)rdf32(xr) * (double)S;
+          e += t;
+          a += fabs(t);
         }
       } else {
         const int64_t nb = K / QK_K;

@@ -102,9 +102,9 @@ def test_record_sizes_match_ggml_static_asserts():
             e = e.replace(name, str(env[name]))
         sizes[k] = eval(e, {"__builtins__": {}})  # arithmetic on literals only
     assert sizes == {"block_q4_0": 18, "block_mxfp4": 17, "block_q8_0": 34, "block_q4_K": 144,
-                     "block_q8_K": 292, "block_iq2_xxs": 66}
+                     "block_q8_K": 292, "block_iq2_xxs": 66, "block_q6_K": 210}
     assert {k: o.RECORD[k][1] for k in o.RECORD} == {
-        "q4_0": 18, "mxfp4": 17, "q8_0": 34, "q4_k": 144, "q8_k": 292, "iq2_xxs": 66}
+        "q4_0": 18, "mxfp4": 17, "q8_0": 34, "q4_k": 144, "q8_k": 292, "iq2_xxs": 66, "q6_k": 210}
 
 
 # ------------------------------------------------------------ dequantizers
@@ -176,6 +176,43 @@ def test_dequant_q4_k_brute_force():
         want.append([np.float32(d * sc[e // 32] * c - dm * m[e // 32]) for e, c in enumerate(codes)])
     w = np.frombuffer(b"".join(recs), np.uint8).reshape(len(recs), 144)
     got = o.dequantize("q4_k", w, 256)
+    assert np.array_equal(got.view(np.uint32), np.array(want, np.float32).view(np.uint32))
+
+
+def _q6k_record(codes, sc, dh):
+    """A Q6_K record from the Weft encoding (examples/formats/ggml.py:114-120):
+    ql u4[256] grouped(128) bit_layers(64, lo_first) -> element e of 128-group
+    h at byte 64 h + (e % 128) % 64, high nibble when e % 128 >= 64; qh u2[256]
+    grouped(128) bit_layers(32, lo_first) -> byte 128 + 32 h + (e % 128) % 32,
+    bits 2 ((e % 128) // 32); scales i8[16] grouped(16); d f16 last."""
+    b = bytearray(210)
+    for e, c in enumerate(codes):
+        h, i = e // 128, e % 128
+        b[64 * h + i % 64] |= (c & 0xF) << (4 * (i // 64))
+        b[128 + 32 * h + i % 32] |= (c >> 4) << (2 * (i // 32))
+    b[192:208] = np.array(sc, np.int8).tobytes()
+    b[208:210] = dh.to_bytes(2, "little")
+    return bytes(b)
+
+
+def test_dequant_q6_k_brute_force():
+    # examples/kernels/dequantize/q6_k.py: q = ql | qh << 4, q -= 32,
+    # y = f32(d) * f32(scale[e // 16]) * f32(q), products rounded left to right
+    rng = np.random.default_rng(9)
+    recs, want = [], []
+    for trial in range(640):
+        codes = [int(v) for v in rng.integers(0, 64, 256)]
+        if trial < 64:  # every code at every position
+            codes = [(trial + 13 * e) % 64 for e in range(256)]
+        sc = [int(v) for v in rng.integers(-128, 128, 16)]
+        if trial < 16:
+            sc = [-128, 127, -1, 0, 1, 64, -65, 3] * 2
+        dh = D16[trial % 6]
+        d = np.float32(np.uint16(dh).view(np.float16))
+        recs.append(_q6k_record(codes, sc, dh))
+        want.append([(d * np.float32(sc[e // 16])) * np.float32(c - 32) for e, c in enumerate(codes)])
+    w = np.frombuffer(b"".join(recs), np.uint8).reshape(len(recs), 210)
+    got = o.dequantize("q6_k", w, 256)
     assert np.array_equal(got.view(np.uint32), np.array(want, np.float32).view(np.uint32))
 
 
@@ -296,7 +333,7 @@ def _dequant_act(act, xq, k):
     return (q * d).reshape(xq.shape[0], k)
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "iq2_xxs", "mxfp4"])
+@pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "iq2_xxs", "mxfp4", "q6_k"])
 def test_mul_mat_against_independent_float64_path(fmt):
     n, k, m = 48, 2048, 3
     w = o.quantize(fmt, o.seeded_normal(31, (n, k), 0.02))
@@ -343,8 +380,27 @@ def test_int_partials_q4_k_match_dequantized_integers():
                                   for s in range(8)]
 
 
+def test_int_partials_q6_k_are_the_group_dots():
+    k = 512
+    w = o.quantize("q6_k", o.seeded_normal(45, (1, k), 0.02))
+    xq = o.quantize("q8_k", o.seeded_normal(46, (1, k)))
+    p = o.int_partials("q6_k", w, xq, k).reshape(-1, 16)
+    for b in range(k // 256):
+        rec = w[0, 210 * b:210 * (b + 1)]
+        codes = np.zeros(256, np.int64)
+        for e in range(256):  # the record address of _q6k_record, read back
+            h, i = e // 128, e % 128
+            lo = (int(rec[64 * h + i % 64]) >> (4 * (i // 64))) & 0xF
+            hi = (int(rec[128 + 32 * h + i % 32]) >> (2 * (i // 32))) & 3
+            codes[e] = (lo | hi << 4) - 32
+        xv = xq[0, 292 * b + 4:292 * b + 260].view(np.int8).astype(np.int64)
+        assert list(p[b]) == [int((codes[16 * g:16 * g + 16] * xv[16 * g:16 * g + 16]).sum())
+                              for g in range(16)]
+
+
 # ------------------------------------------------ weight quantizers (inputs)
-@pytest.mark.parametrize("fmt,bound", [("q4_0", 0.10), ("q4_k", 0.09), ("mxfp4", 0.13), ("iq2_xxs", 0.45)])
+@pytest.mark.parametrize("fmt,bound", [("q4_0", 0.10), ("q4_k", 0.09), ("mxfp4", 0.13), ("iq2_xxs", 0.45),
+                                       ("q6_k", 0.05)])
 def test_weight_quantizer_round_trip(fmt, bound):
     w = o.seeded_normal(51, (32, 4096), 0.02)
     d = o.dequantize(fmt, o.quantize(fmt, w), 4096)
