@@ -1,0 +1,72 @@
+"""Q6_K (an adjacent GGML format, ggml-common.h:349-358) through the C ABI on
+the GPU, against the pinned oracle: row dequantize bit-exact (any base
+alignment: the Weft encoding declares none), vec_dot and mul_mat within the
+fp64 re-accumulation bar, the Xq workspace bit-exact.  Extreme records:
+scales -128 / 127, the -32 / 31 codes, d = 0, and a zero activation block."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as o
+from tests.test_gpu_parity import SENTINEL, acts, assert_close, check_mul_mat, run_mul_mat, weights
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("n,k,w_off,y_off", [(64, 4096, 0, 0), (33, 768, 1, 1), (7, 256, 3, 2)])
+def test_dequant_q6_k(hip, n, k, w_off, y_off):
+    w = weights("q6_k", n, k)
+    total = n * k
+    y = hip.empty(4 * total, fill=SENTINEL, offset=4 * y_off)
+    hip.call("row_dequantize_q6_k", hip.to_dev(w, offset=w_off), y, total)
+    want = o.dequantize("q6_k", w, k).reshape(-1)
+    np.testing.assert_array_equal(y.numpy(np.float32).view(np.uint32), want.view(np.uint32))
+
+
+def extreme_records(n_rec):
+    """Records with every code at its extremes and the widest scales."""
+    rng = np.random.default_rng(17)
+    recs = rng.integers(0, 256, size=(n_rec, 210), dtype=np.uint8)
+    recs[0, :192] = 0x00                      # all codes 0 -> q = -32
+    recs[1, :192] = 0xFF                      # all codes 63 -> q = 31
+    recs[:, 192:208] = rng.choice(np.array([-128, 127, -1, 0, 1], np.int8), size=(n_rec, 16)).view(np.uint8)
+    recs[2, 208:210] = 0                      # d = 0
+    d = (rng.standard_normal(n_rec) * 1e-3).astype(np.float16).view(np.uint8).reshape(n_rec, 2)
+    recs[3:, 208:210] = d[3:]
+    return recs
+
+
+def test_vec_dot_q6_k(hip):
+    for k in (256, 4096, 14336):
+        w = weights("q6_k", 1, k, seed=3)
+        xq = o.quantize("q8_k", acts(1, k, seed=4))
+        y = hip.empty(4, fill=SENTINEL)
+        hip.call("quantized_vec_dot_q6_k_q8_k", hip.to_dev(w), hip.to_dev(xq), y, k)
+        e, a = o.mul_mat_f64("q6_k", w, xq, 1, k, 1)
+        assert_close(y.numpy(np.float32).reshape(1, 1), e, a, f"vec_dot q6_k K={k}")
+
+
+def test_vec_dot_q6_k_extreme_records(hip):
+    k = 16 * 256
+    w = extreme_records(16).reshape(1, -1)
+    x = acts(1, k, seed=8)
+    x[0, 512:768] = 0.0                       # an all-zero Q8_K block
+    xq = o.quantize("q8_k", x)
+    y = hip.empty(4, fill=SENTINEL)
+    hip.call("quantized_vec_dot_q6_k_q8_k", hip.to_dev(w), hip.to_dev(xq), y, k)
+    e, a = o.mul_mat_f64("q6_k", w, xq, 1, k, 1)
+    assert_close(y.numpy(np.float32).reshape(1, 1), e, a, "vec_dot q6_k extremes")
+
+
+@pytest.mark.parametrize("n,k,m", [(4096, 4096, 1), (11008, 4096, 1), (4096, 14336, 1), (300, 768, 3),
+                                   (65, 1024, 5), (1, 256, 1)])
+def test_decode_q6_k(hip, n, k, m):
+    w, x, xq, y = run_mul_mat(hip, "production_mul_mat_q6_k_decode", "q6_k", n, k, m)
+    check_mul_mat("q6_k", w, x, xq, y, n, k, m)
+
+
+def test_prefill_q6_k(hip):
+    n, k, m = 512, 4096, 64
+    w, x, xq, y = run_mul_mat(hip, "production_mul_mat_q6_k", "q6_k", n, k, m)
+    check_mul_mat("q6_k", w, x, xq, y, n, k, m)

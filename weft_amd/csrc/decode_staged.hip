@@ -1,12 +1,13 @@
 // Decode GEMV for the formats whose records are not 16-byte multiples:
 // Q4_0 x Q8_0 (18 B / 32), MXFP4 x Q8_0 (17 B / 32), IQ2_XXS x Q8_K
-// (66 B / 256); plus their single-output vec_dots.
+// (66 B / 256), Q6_K x Q8_K (210 B / 256); plus their single-output vec_dots.
 //
 // Semantics (GGML generic vec_dots, ggml-cpu/quants.c):
 //   Q4_0    :174-208  y = sum_b dw_b * dx_b * sum_32 (q-8) * x
 //   MXFP4   :247-276  y = sum_b dx_b * e8m0_half(e_b) * sum_32 kv[q] * x
 //   IQ2_XXS :855-895  y = 0.125 * sum_B dw * dx * sum_g (2 s_g + 1) *
 //                         sum_32 grid[idx] * sign * x
+//   Q6_K    :800-853  y = sum_B dw * dx * sum_g sc_g * sum_16 (q - 32) * x
 // and the Weft kernels examples/kernels/mul_mat/{q4_0_decode,mxfp4_decode,
 // iq2_xxs_decode}.py (quantize X into Xq, then one vec_dot per output).
 //
@@ -36,7 +37,7 @@ constexpr int kWaves = kThreads / kWave;
 constexpr int kMaxRowsPerPass = 4;
 constexpr int kWindow = 2304 + 32;  // per-wave LDS window (bytes), with slack
 
-enum class Fmt { Q4_0, MXFP4, IQ2_XXS };
+enum class Fmt { Q4_0, MXFP4, IQ2_XXS, Q6_K };
 
 template <Fmt F>
 struct Traits;
@@ -53,6 +54,11 @@ struct Traits<Fmt::MXFP4> {
 template <>
 struct Traits<Fmt::IQ2_XXS> {
   static constexpr int kElems = 256, kBytes = 66, kSegRecords = 32, kItemsPerRecord = 8;
+  static constexpr bool kQ8K = true;
+};
+template <>
+struct Traits<Fmt::Q6_K> {
+  static constexpr int kElems = 256, kBytes = 210, kSegRecords = 8, kItemsPerRecord = 8;
   static constexpr bool kQ8K = true;
 };
 
@@ -243,6 +249,47 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
             s = dot4(hi3, xh.w, s);
             acc[m] += (float)s * wscale * v.d[gb];
           }
+        } else if constexpr (F == Fmt::Q6_K) {
+          // item = (superblock, 32-element chunk g): half h = g / 4, quarter
+          // qq = g % 4; the chunk's 6-bit codes are the nibble 4 (qq / 2) of
+          // ql bytes 64 h + 32 (qq % 2) + l and bits 2 qq of qh bytes
+          // 128 + 32 h + l (l = 0..31); its two 16-groups scale by sc[2 g]
+          // and sc[2 g + 1]
+          const int sb = valid ? it >> 3 : 0, g = it & 7;
+          const int gsb = r0 + sb;
+          const int o = off0 + T::kBytes * sb;
+          const int h = g >> 2, qq = g & 3;
+          const int qlo = o + 64 * h + 32 * (qq & 1), qho = o + 128 + 32 * h;
+          const int nsh = 4 * (qq >> 1), hsh = 2 * qq;
+          const uint32_t sw = lds_u32(win, o + 192 + 2 * g);
+          const int sc0 = (int)(int8_t)(sw & 0xffu), sc1 = (int)(int8_t)((sw >> 8) & 0xffu);
+          const float dw = fp16_to_fp32(lds_u32(win, o + 208) & 0xffffu);
+          int wv[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const uint32_t q = ((lds_u32(win, qlo + 4 * j) >> nsh) & 0x0f0f0f0fu) |
+                               (((lds_u32(win, qho + 4 * j) >> hsh) & 0x03030303u) << 4);
+            wv[j] = (int)(((q | 0x80808080u) - 0x20202020u) ^ 0x80808080u);  // bytewise q - 32
+          }
+#pragma unroll
+          for (int m = 0; m < kMaxRowsPerPass; ++m) {
+            if (m >= a.mb) break;
+            const Q8KView v = q8k_view(act, K, m);
+            const int4 x0 = *reinterpret_cast<const int4*>(v.qs + 256 * gsb + 32 * g);
+            const int4 x1 = *reinterpret_cast<const int4*>(v.qs + 256 * gsb + 32 * g + 16);
+            int s0 = dot4(wv[0], x0.x, 0);
+            s0 = dot4(wv[1], x0.y, s0);
+            s0 = dot4(wv[2], x0.z, s0);
+            s0 = dot4(wv[3], x0.w, s0);
+            int s1 = dot4(wv[4], x1.x, 0);
+            s1 = dot4(wv[5], x1.y, s1);
+            s1 = dot4(wv[6], x1.z, s1);
+            s1 = dot4(wv[7], x1.w, s1);
+            // the superblock's exact int32 sum over its 8 chunks, then one
+            // fp32 term (|sum| <= 256 * 32 * 127 * 128 < 2^31)
+            const int bsum = sum8_of_sum4(sum4(valid ? sc0 * s0 + sc1 * s1 : 0));
+            if (valid && g == 0) acc[m] += (dw * v.d[gsb]) * (float)bsum;
+          }
         } else {  // IQ2_XXS: item = (superblock, 32-group); 8 lanes per superblock
           const int sb = valid ? it >> 3 : 0, g = it & 7;
           const int gsb = r0 + sb;
@@ -302,12 +349,12 @@ void launch(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_
   if (pr != nullptr) M = 1;  // one activation row per pair
   if (N == 0 || M == 0 || K == 0 || (pr != nullptr && n_pairs <= 0)) return;
   const size_t act_align = T::kQ8K ? 4 : 2;
-  const size_t w_align = F == Fmt::MXFP4 ? 1 : 2;
+  const size_t w_align = F == Fmt::MXFP4 || F == Fmt::Q6_K ? 1 : 2;
   if (K % T::kElems != 0 || W == nullptr || Y == nullptr || (X == nullptr && xq_in == nullptr) ||
       N > (size_t)INT32_MAX || K > (size_t)INT32_MAX || M > (size_t)INT32_MAX ||
       !aligned(W, w_align) || !aligned(Y, 4) || (X && !aligned(X, 4)) ||
       (xq_in && !aligned(xq_in, act_align)) || (xq_out && !aligned(xq_out, act_align)) ||
-      (F != Fmt::Q4_0 && (tab0 == nullptr || tab1 == nullptr)) ||
+      ((F == Fmt::MXFP4 || F == Fmt::IQ2_XXS) && (tab0 == nullptr || tab1 == nullptr)) ||
       (F == Fmt::IQ2_XXS && (!aligned(tab0, 4) || !aligned(tab1, 4))) ||
       (F == Fmt::MXFP4 && !aligned(tab1, 4)) ||
       !strides_ok(st, K / T::kElems * T::kBytes, w_align, K, N, N, M) ||
@@ -382,8 +429,14 @@ void decode_pairs(int fmt, const uint8_t* W, const float* X, const uint8_t* xq_i
   switch (fmt) {
     case 0: return launch<Fmt::Q4_0>(W, X, xq_in, xq_out, nullptr, nullptr, Y, N, K, 1, st, &pr, n_pairs);
     case 1: return launch<Fmt::MXFP4>(W, X, xq_in, xq_out, tab0, tab1, Y, N, K, 1, st, &pr, n_pairs);
+    case 3: return launch<Fmt::Q6_K>(W, X, xq_in, xq_out, nullptr, nullptr, Y, N, K, 1, st, &pr, n_pairs);
     default: return launch<Fmt::IQ2_XXS>(W, X, xq_in, xq_out, tab0, tab1, Y, N, K, 1, st, &pr, n_pairs);
   }
+}
+
+void decode_q6_k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
+                 size_t M, const RowStrides& st) {
+  launch<Fmt::Q6_K>(W, X, nullptr, Xq, nullptr, nullptr, Y, N, K, M, st);
 }
 
 void decode_quantized(int fmt, const uint8_t* W, const uint8_t* Xq, const int8_t* tab0,
@@ -392,6 +445,7 @@ void decode_quantized(int fmt, const uint8_t* W, const uint8_t* Xq, const int8_t
   switch (fmt) {
     case 0: return launch<Fmt::Q4_0>(W, nullptr, Xq, nullptr, nullptr, nullptr, Y, N, K, M, st);
     case 1: return launch<Fmt::MXFP4>(W, nullptr, Xq, nullptr, tab0, tab1, Y, N, K, M, st);
+    case 3: return launch<Fmt::Q6_K>(W, nullptr, Xq, nullptr, nullptr, nullptr, Y, N, K, M, st);
     default: return launch<Fmt::IQ2_XXS>(W, nullptr, Xq, nullptr, tab0, tab1, Y, N, K, M, st);
   }
 }
@@ -430,6 +484,26 @@ void quantized_vec_dot_mxfp4_q8_0(const uint8_t* W, const uint8_t* X, const int8
                                   const float* scale, float* Y, size_t K) {
   if (X == nullptr) return weft::set_error(hipErrorInvalidValue);
   weft::launch<weft::Fmt::MXFP4>(W, nullptr, X, nullptr, codebook, scale, Y, 1, K, 1, weft::packed(0, K, 1));
+}
+
+void production_mul_mat_q6_k_decode(const uint8_t* W, const float* X, uint8_t* Xq, float* Y,
+                                    size_t N, size_t K, size_t M) {
+  if (X == nullptr || Xq == nullptr) return weft::set_error(hipErrorInvalidValue);
+  weft::decode_q6_k(W, X, Xq, Y, N, K, M, weft::packed(K / 256 * weft::kQ6_KBytes, K, N));
+}
+
+// Q6_K prefill: the GEMV kernel at every M (the scales are per 16 elements
+// and int8 wide, so an exact int8-MFMA form needs the scaled weights split
+// into two operands per element; not built yet)
+void production_mul_mat_q6_k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N,
+                             size_t K, size_t M) {
+  if (X == nullptr || Xq == nullptr) return weft::set_error(hipErrorInvalidValue);
+  weft::decode_q6_k(W, X, Xq, Y, N, K, M, weft::packed(K / 256 * weft::kQ6_KBytes, K, N));
+}
+
+void quantized_vec_dot_q6_k_q8_k(const uint8_t* W, const uint8_t* X, float* Y, size_t K) {
+  if (X == nullptr) return weft::set_error(hipErrorInvalidValue);
+  weft::launch<weft::Fmt::Q6_K>(W, nullptr, X, nullptr, nullptr, nullptr, Y, 1, K, 1, weft::packed(0, K, 1));
 }
 
 void quantized_vec_dot_iq2_xxs_q8_k(const uint8_t* W, const uint8_t* X, const int8_t* grid,

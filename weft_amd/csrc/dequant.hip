@@ -1,10 +1,11 @@
-// Row dequantize: row_dequantize_{q4_0,q4_k,iq2_xxs,mxfp4}
+// Row dequantize: row_dequantize_{q4_0,q4_k,iq2_xxs,mxfp4,q6_k}
 // (examples/kernels/dequantize/*.py; GGML dequantize_row_* in
-// ggml-quants.c:401-419, :511-529, :1471-1493, :2416-2440).
+// ggml-quants.c:401-419, :511-529, :1471-1493, :2416-2440, :1881-1910).
 //
 // Every product here is exact in fp32 (at most 22 significant bits), and
 // Q4_K's single subtraction rounds once, so the outputs are bit-exact with
-// GGML regardless of contraction.
+// GGML regardless of contraction.  Q6_K's (d * sc) * q rounds at the second
+// product, which has no addend to contract with, so it is bit-exact too.
 //
 // HBM write-bound (Q4_K: 0.56 B read, 4 B written per element).  The mapping
 // is output-major: lane l of a wave writes elements 4l..4l+3 of a 256-element
@@ -120,6 +121,45 @@ __global__ void __launch_bounds__(kThreads) dq_32_kernel(const uint8_t* __restri
   }
 }
 
+// Q6_K (dequantize_row_q6_K, ggml-quants.c:1881-1910): lane l of a wave
+// writes elements e = 4l..4l+3 of a superblock; they share one ql word (half
+// h = e / 128, byte 64 h + e % 64, nibble (e % 128) / 64), one qh word (byte
+// 128 + 32 h + e % 32, bits 2 ((e % 128) / 32)) and one scale (e / 16).
+// y = (d * sc) * (q - 32): two fp32 products rounded in GGML's order.
+// Records are 210 bytes with no alignment (the Weft encoding declares none),
+// so every load is bytewise; U superblocks are in flight per wave.
+template <int U, bool Y16>
+__global__ void __launch_bounds__(kThreads) dq_q6k_kernel(const uint8_t* __restrict__ W,
+                                                          float* __restrict__ Y, long long nsb) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const long long wave = ((long long)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const long long nwaves = (long long)gridDim.x * blockDim.x / kWave;
+  const int e = 4 * lane, h = e >> 7, i = e & 127;
+  const int qlo = 64 * h + (i & 63), qls = 4 * (i >> 6);
+  const int qho = 128 + 32 * h + (i & 31), qhs = 2 * (i >> 5);
+  for (long long s0 = wave * U; s0 < nsb; s0 += nwaves * U) {
+    uint32_t ql[U], qh[U], dh[U];
+    int sc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint8_t* rec = W + min(s0 + u, nsb - 1) * kQ6_KBytes;  // clamped: a valid record
+      ql[u] = ld_u32_a1(rec + qlo);
+      qh[u] = ld_u32_a1(rec + qho);
+      sc[u] = (int)(int8_t)rec[192 + (e >> 4)];
+      dh[u] = (uint32_t)rec[208] | ((uint32_t)rec[209] << 8);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (s0 + u >= nsb) break;
+      const float dsc = fp16_to_fp32(dh[u]) * (float)sc[u];
+      const uint32_t q = ((ql[u] >> qls) & 0x0f0f0f0fu) | (((qh[u] >> qhs) & 0x03030303u) << 4);
+      store4<Y16>(Y + (s0 + u) * 256 + e, dsc * (float)((int)(q & 0xff) - 32),
+                  dsc * (float)((int)((q >> 8) & 0xff) - 32), dsc * (float)((int)((q >> 16) & 0xff) - 32),
+                  dsc * (float)((int)(q >> 24) - 32));
+    }
+  }
+}
+
 // IQ2_XXS: one wave per superblock; lane l -> elements 4l..4l+3
 template <bool Y16>
 __global__ void __launch_bounds__(kThreads) dq_iq2xxs_kernel(const uint8_t* __restrict__ W,
@@ -178,6 +218,20 @@ void row_dequantize_q4_k(const uint8_t* W, float* Y, size_t K) {
     dq_q4k_kernel<U, false, true><<<g, kThreads, 0, current_stream()>>>(W, Y, nsb);
   else
     dq_q4k_kernel<U, false, false><<<g, kThreads, 0, current_stream()>>>(W, Y, nsb);
+  check_launch();
+}
+
+void row_dequantize_q6_k(const uint8_t* W, float* Y, size_t K) {
+  using namespace weft;
+  if (K == 0) return;
+  if (K % 256 || bad(W, 1, Y)) return set_error(hipErrorInvalidValue);
+  const long long nsb = (long long)(K / 256);
+  constexpr int U = 4;
+  const int g = grid_for((nsb + U - 1) / U);
+  if (aligned(Y, 16))
+    dq_q6k_kernel<U, true><<<g, kThreads, 0, current_stream()>>>(W, Y, nsb);
+  else
+    dq_q6k_kernel<U, false><<<g, kThreads, 0, current_stream()>>>(W, Y, nsb);
   check_launch();
 }
 

@@ -55,12 +55,14 @@ _MM_MX = ("W", "X", "Xq", "codebook", "scale", "Y")
 _DECODE_GROUPS = {"Xq": "workspace", "Y": "output"}
 
 # wl.auto extents of the tiled prefill kernels (mul_mat/q4_0.py:17-22,
-# q4_k_staged.py:20-24, iq2_xxs_staged.py:43-48 and :80-83, mxfp4.py:21-25)
+# q4_k_staged.py:20-24, iq2_xxs_staged.py:43-48 and :80-83, mxfp4.py:21-25,
+# q6_k.py:17-21)
 _AUTO = {
     "production_mul_mat_q4_0": ("MC", "MR", "NC", "NR"),
     "production_mul_mat_q4_k_staged": ("KC", "MC", "MR", "NC"),
     "production_mul_mat_iq2_xxs_staged": ("KC", "MC", "MR", "NC", "NR"),
     "production_mul_mat_mxfp4": ("MC", "MR", "NC", "NR"),
+    "production_mul_mat_q6_k": ("MC", "MR", "NC", "NR"),
 }
 
 # (symbol, parameters, reference source, alias groups)
@@ -91,6 +93,10 @@ _DEFS = [
     ("production_mul_mat_mxfp4", _MM_MX, "examples/kernels/mul_mat/mxfp4.py:10-35", None),
     ("production_mul_mat_mxfp4_decode", _MM_MX, "examples/kernels/mul_mat/mxfp4_decode.py:10-23",
      _DECODE_GROUPS),
+    ("row_dequantize_q6_k", ("W", "Y"), "examples/kernels/dequantize/q6_k.py:8-15", None),
+    ("quantized_vec_dot_q6_k_q8_k", ("W", "X", "Y"), "examples/kernels/vec_dot/q6_k_q8_k.py:39-44", None),
+    ("production_mul_mat_q6_k", _MM, "examples/kernels/mul_mat/q6_k.py:9-37", _DECODE_GROUPS),
+    ("production_mul_mat_q6_k_decode", _MM, "examples/kernels/mul_mat/q6_k_decode.py:10-20", None),
     ("q4_k_q8_k_gemv", ("W", "X", "Y"), "examples/kernels/gemv/q4_k.py:8-26", None),
     ("q4_k_q8_k_gemv_groups4", ("W", "X", "Y"), "examples/kernels/gemv/q4_k_groups4.py:8-26", None),
     ("q4_k_q8_k_gemv_contract", ("W", "X", "Y"), "examples/kernels/gemv/q4_k_contract.py:8-26", None),
