@@ -11,10 +11,11 @@
 // and the Weft kernels examples/kernels/mul_mat/{q4_0_decode,mxfp4_decode,
 // iq2_xxs_decode}.py (quantize X into Xq, then one vec_dot per output).
 //
-// gfx950 mapping.  Records straddle 16-byte boundaries, so a wave streams a
-// segment of its row into a private LDS window with coalesced 16-byte loads
-// (1 KB per wave instruction) and lanes then pick their record out of LDS at
-// any byte offset with two aligned ds_read_b32 + v_alignbyte per word.  One
+// gfx950 mapping.  Records straddle 16-byte boundaries, so a wave streams
+// its rows segment by segment (up to ~2.3 KB) through a private LDS window:
+// coalesced 16-byte loads into registers, one segment ahead of the one being
+// computed, then into the window, where lanes pick their record out at any
+// byte offset with two aligned ds_read_b32 + v_alignbyte per word.  One
 // lane owns one 32-element block (Q4_0, MXFP4) or one 32-element group of an
 // IQ2_XXS superblock; its int8 products run on v_dot4_i32_i8 against the
 // quantized activation in LDS.  MXFP4's 16-entry codebook is looked up four
@@ -85,31 +86,51 @@ __device__ __forceinline__ uint32_t lds_u32(const char* base, int o) {
   return __builtin_amdgcn_alignbyte(w[1], w[0], (uint32_t)(o & 3));
 }
 
-// Copy bytes [p0, p1) of W into the wave's LDS window; returns the offset of
-// p0 inside the window.  16-byte loads from the 16-aligned address below p0;
-// a chunk that reaches outside [lo, hi) is read byte by byte, inside only.
-__device__ __forceinline__ int stage_bytes(char* win, const uint8_t* p0, const uint8_t* p1,
-                                           const uint8_t* lo, const uint8_t* hi, int lane) {
-  const uint8_t* a0 = reinterpret_cast<const uint8_t*>(reinterpret_cast<uintptr_t>(p0) & ~(uintptr_t)15);
-  const int nchunks = (int)((p1 - a0 + 15) >> 4);
-  for (int c = lane; c < nchunks; c += kWave) {
-    const uint8_t* src = a0 + 16 * c;
-    uint4 v;
-    if (src >= lo && src + 16 <= hi) {
-      v = *reinterpret_cast<const uint4*>(src);
-    } else {
-      uint32_t w[4] = {0, 0, 0, 0};
-      for (int i = 0; i < 16; ++i)
-        if (src + i >= lo && src + i < hi) w[i >> 2] |= (uint32_t)src[i] << (8 * (i & 3));
-      v = make_uint4(w[0], w[1], w[2], w[3]);
+// One segment of a row staged through registers, so the next segment's loads
+// are in flight while the current one is computed from LDS: fetch() issues
+// the 16-byte loads of bytes [p0, p1) (chunks reaching outside [lo, hi) are
+// read byte by byte, inside only), put() writes them into the wave's window
+// and returns the offset of p0 inside it.
+constexpr int kChunksPerLane = (kWindow / 16 + kWave - 1) / kWave;
+
+struct SegmentFetch {
+  uint4 c[kChunksPerLane];
+  int nchunks, off;
+
+  __device__ __forceinline__ void fetch(const uint8_t* p0, const uint8_t* p1, const uint8_t* lo,
+                                        const uint8_t* hi, int lane) {
+    const uint8_t* a0 = reinterpret_cast<const uint8_t*>(reinterpret_cast<uintptr_t>(p0) & ~(uintptr_t)15);
+    nchunks = (int)((p1 - a0 + 15) >> 4);
+    off = (int)(p0 - a0);
+#pragma unroll
+    for (int j = 0; j < kChunksPerLane; ++j) {
+      const int ch = lane + kWave * j;
+      const uint8_t* src = a0 + 16 * ch;
+      if (ch >= nchunks) {
+        c[j] = make_uint4(0, 0, 0, 0);
+      } else if (src >= lo && src + 16 <= hi) {
+        c[j] = *reinterpret_cast<const uint4*>(src);
+      } else {
+        uint32_t w[4] = {0, 0, 0, 0};
+        for (int i = 0; i < 16; ++i)
+          if (src + i >= lo && src + i < hi) w[i >> 2] |= (uint32_t)src[i] << (8 * (i & 3));
+        c[j] = make_uint4(w[0], w[1], w[2], w[3]);
+      }
     }
-    *reinterpret_cast<uint4*>(win + 16 * c) = v;
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  return (int)(p0 - a0);
-}
+
+  __device__ __forceinline__ int put(char* win, int lane) const {
+#pragma unroll
+    for (int j = 0; j < kChunksPerLane; ++j) {
+      const int ch = lane + kWave * j;
+      if (ch < nchunks) *reinterpret_cast<uint4*>(win + 16 * ch) = c[j];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    return off;
+  }
+};
 
 __device__ __forceinline__ void window_release() {
   // all lanes are done reading the window before it is overwritten
@@ -142,6 +163,7 @@ __device__ __forceinline__ int apply_signs(uint32_t g, uint32_t s) {
 template <Fmt F>
 __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
   using T = Traits<F>;
+  static_assert(T::kSegRecords * T::kBytes + 16 <= kWindow, "a segment fits the window");
   if (a.pair.ids != nullptr && !resolve_pair(a)) return;
   extern __shared__ __align__(16) char lds[];
   char* windows = lds;                             // kWaves * kWindow
@@ -195,16 +217,39 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
   const int row0 = blockIdx.x * a.rows_per_wg;
   const int row1 = min(a.N, row0 + a.rows_per_wg);
 
-  for (int row = row0 + wave; row < row1; row += nwaves) {
-    const uint8_t* wr = a.W + (size_t)row * rb;
-    float acc[kMaxRowsPerPass];
+  // this wave's (row, segment) sequence, one segment fetched ahead
+  const int nseg = (nrec + T::kSegRecords - 1) / T::kSegRecords;
+  const int my_rows = row0 + wave < row1 ? (row1 - row0 - wave + nwaves - 1) / nwaves : 0;
+  const int total = my_rows * nseg;
+  auto seg_span = [&](int si, const uint8_t*& p0, const uint8_t*& p1) {
+    const int ri = si / nseg, r0 = (si - ri * nseg) * T::kSegRecords;
+    const uint8_t* wr = a.W + (size_t)(row0 + wave + nwaves * ri) * rb;
+    p0 = wr + (size_t)r0 * T::kBytes;
+    p1 = wr + (size_t)min(r0 + T::kSegRecords, nrec) * T::kBytes;
+  };
+  SegmentFetch pf;
+  if (total > 0) {
+    const uint8_t *p0, *p1;
+    seg_span(0, p0, p1);
+    pf.fetch(p0, p1, wlo, whi, lane);
+  }
+  float acc[kMaxRowsPerPass];
+  for (int si = 0; si < total; ++si) {
+    const int ri = si / nseg, seg = si - ri * nseg;
+    const int row = row0 + wave + nwaves * ri;
+    const int r0 = seg * T::kSegRecords;
+    if (seg == 0) {
 #pragma unroll
-    for (int m = 0; m < kMaxRowsPerPass; ++m) acc[m] = 0.f;
-
-    for (int r0 = 0; r0 < nrec; r0 += T::kSegRecords) {
+      for (int m = 0; m < kMaxRowsPerPass; ++m) acc[m] = 0.f;
+    }
+    {
       const int nr = min(T::kSegRecords, nrec - r0);
-      const int off0 = stage_bytes(win, wr + (size_t)r0 * T::kBytes,
-                                   wr + (size_t)(r0 + nr) * T::kBytes, wlo, whi, lane);
+      const int off0 = pf.put(win, lane);
+      if (si + 1 < total) {
+        const uint8_t *p0, *p1;
+        seg_span(si + 1, p0, p1);
+        pf.fetch(p0, p1, wlo, whi, lane);
+      }
       const int items = nr * T::kItemsPerRecord;
       // wave-uniform trip count: the IQ2_XXS branch reduces across lanes
       for (int it0 = 0; it0 < items; it0 += kWave) {
@@ -331,12 +376,14 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
       }
       window_release();
     }
+    if (seg == nseg - 1) {
 #pragma unroll
-    for (int m = 0; m < kMaxRowsPerPass; ++m) {
-      if (m >= a.mb) break;
-      float tot = wave_sum_f(acc[m]);
-      if constexpr (F == Fmt::IQ2_XXS) tot *= 0.125f;
-      if (lane == 0) a.Y[(size_t)(a.m0 + m) * a.y_stride + row] = tot;
+      for (int m = 0; m < kMaxRowsPerPass; ++m) {
+        if (m >= a.mb) break;
+        float tot = wave_sum_f(acc[m]);
+        if constexpr (F == Fmt::IQ2_XXS) tot *= 0.125f;
+        if (lane == 0) a.Y[(size_t)(a.m0 + m) * a.y_stride + row] = tot;
+      }
     }
   }
 }
