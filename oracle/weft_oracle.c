@@ -39,6 +39,7 @@
 #define Q8_K_BYTES 292
 #define IQ2_XXS_BYTES 66
 #define Q6_K_BYTES 210
+#define Q5_K_BYTES 176
 #define GROUP_MAX_EPS 1e-15f
 
 static inline uint32_t f32_bits(float f) {
@@ -394,6 +395,75 @@ void wo_quantize_row_q4_K(const float *x, uint8_t *y, int64_t k) {
     for (int j = 0; j < QK_K; j += 64) {
       for (int l = 0; l < 32; ++l) q[l] = (uint8_t)(L[j + l] | (L[j + l + 32] << 4));
       q += 32;
+    }
+  }
+}
+
+/* quantize_row_q5_K_ref, ggml-quants.c:1586-1671 (input generator):
+ * record d | dmin | scales[12] | qh[32] | qs[128] */
+void wo_quantize_row_q5_K(const float *x, uint8_t *y, int64_t k) {
+  const int64_t nb = k / QK_K;
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < nb; ++i) {
+    uint8_t L[QK_K], Laux[32];
+    float weights[32], mins[QK_K / 32], scales[QK_K / 32];
+    const float *xb = x + i * QK_K;
+    uint8_t *rec = y + i * Q5_K_BYTES;
+    uint8_t *sc12 = rec + 4;
+    memset(sc12, 0, 12);
+    float max_scale = 0, max_min = 0;
+    for (int j = 0; j < QK_K / 32; ++j) {
+      float sum_x2 = 0;
+      for (int l = 0; l < 32; ++l) sum_x2 += xb[32 * j + l] * xb[32 * j + l];
+      const float av_x = sqrtf(sum_x2 / 32);
+      for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(xb[32 * j + l]);
+      scales[j] = make_qkx2(32, 31, xb + 32 * j, weights, L + 32 * j, &mins[j], Laux, -0.5f, 0.1f, 15);
+      if (scales[j] > max_scale) max_scale = scales[j];
+      if (mins[j] > max_min) max_min = mins[j];
+    }
+    const float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
+    const float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
+    for (int j = 0; j < QK_K / 32; ++j) {
+      uint8_t ls = (uint8_t)nearest_int(inv_scale * scales[j]);
+      uint8_t lm = (uint8_t)nearest_int(inv_min * mins[j]);
+      ls = ls < 63 ? ls : 63;
+      lm = lm < 63 ? lm : 63;
+      if (j < 4) {
+        sc12[j] = ls;
+        sc12[j + 4] = lm;
+      } else {
+        sc12[j + 4] = (uint8_t)((ls & 0xF) | ((lm & 0xF) << 4));
+        sc12[j - 4] |= (uint8_t)((ls >> 4) << 6);
+        sc12[j - 0] |= (uint8_t)((lm >> 4) << 6);
+      }
+    }
+    wr16(rec + 0, wo_fp32_to_fp16(max_scale / 63.f));
+    wr16(rec + 2, wo_fp32_to_fp16(max_min / 63.f));
+    for (int j = 0; j < QK_K / 32; ++j) {
+      uint8_t sc, m;
+      scale_min_k4(j, sc12, &sc, &m);
+      const float d = wo_fp16_to_fp32(rd16(rec)) * sc;
+      if (!d) continue;
+      const float dm = wo_fp16_to_fp32(rd16(rec + 2)) * m;
+      for (int ii = 0; ii < 32; ++ii) {
+        int l = nearest_int((xb[32 * j + ii] + dm) / d);
+        l = l < 0 ? 0 : (l > 31 ? 31 : l);
+        L[32 * j + ii] = (uint8_t)l;
+      }
+    }
+    uint8_t *qh = rec + 16, *ql = rec + 48;
+    memset(qh, 0, 32);
+    uint8_t m1 = 1, m2 = 2;
+    for (int n = 0; n < QK_K; n += 64) {
+      for (int j = 0; j < 32; ++j) {
+        int l1 = L[n + j], l2 = L[n + j + 32];
+        if (l1 > 15) { l1 -= 16; qh[j] |= m1; }
+        if (l2 > 15) { l2 -= 16; qh[j] |= m2; }
+        ql[j] = (uint8_t)(l1 | (l2 << 4));
+      }
+      m1 <<= 2;
+      m2 <<= 2;
+      ql += 32;
     }
   }
 }
@@ -853,6 +923,73 @@ void wo_dequantize_row_q6_K(const uint8_t *x, float *y, int64_t k) {
   }
 }
 
+/* dequantize_row_q5_K, ggml-quants.c:1673-1697: y = (d * sc) * q - dmin * m */
+void wo_dequantize_row_q5_K(const uint8_t *x, float *y, int64_t k) {
+  const int64_t nb = k / QK_K;
+  for (int64_t i = 0; i < nb; ++i) {
+    const uint8_t *r = x + i * Q5_K_BYTES;
+    const uint8_t *ql = r + 48, *qh = r + 16;
+    const float d = wo_fp16_to_fp32(rd16(r)), min = wo_fp16_to_fp32(rd16(r + 2));
+    int is = 0;
+    uint8_t sc, m, u1 = 1, u2 = 2;
+    for (int j = 0; j < QK_K; j += 64) {
+      scale_min_k4(is + 0, r + 4, &sc, &m);
+      const float d1 = d * sc, m1 = min * m;
+      scale_min_k4(is + 1, r + 4, &sc, &m);
+      const float d2 = d * sc, m2 = min * m;
+      for (int l = 0; l < 32; ++l) *y++ = d1 * ((ql[l] & 0xF) + (qh[l] & u1 ? 16 : 0)) - m1;
+      for (int l = 0; l < 32; ++l) *y++ = d2 * ((ql[l] >> 4) + (qh[l] & u2 ? 16 : 0)) - m2;
+      ql += 32;
+      is += 2;
+      u1 <<= 2;
+      u2 <<= 2;
+    }
+  }
+}
+
+/* q of element e (0..255) of a Q5_K record, in [0, 31] */
+static inline int q5_value(const uint8_t *r, int e) {
+  const int j = e / 64, half = (e % 64) / 32, l = e % 32;
+  const uint8_t b = r[48 + 32 * j + l];
+  return (half ? b >> 4 : b & 0xF) | (((r[16 + l] >> (2 * j + half)) & 1) << 4);
+}
+
+/* ggml_vec_dot_q5_K_q8_K_generic, ggml-cpu/quants.c:720-798 */
+float wo_vec_dot_q5_K_q8_K(const uint8_t *w, const uint8_t *x, int64_t k) {
+  const int64_t nb = k / QK_K;
+  float sums[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  float sumf = 0;
+  int8_t aux8[QK_K];
+  for (int64_t i = 0; i < nb; ++i) {
+    const uint8_t *r = w + i * Q5_K_BYTES;
+    const uint8_t *xr = x + i * Q8_K_BYTES;
+    const int8_t *q8 = (const int8_t *)(xr + 4);
+    for (int e = 0; e < QK_K; ++e) aux8[e] = (int8_t)q5_value(r, e);
+    uint8_t scales[8], mins[8];
+    for (int s = 0; s < 8; ++s) scale_min_k4(s, r + 4, &scales[s], &mins[s]);
+    int sumi = 0;
+    for (int j = 0; j < QK_K / 16; ++j) sumi += (int16_t)rd16(xr + 260 + 2 * j) * mins[j / 2];
+    int32_t aux32[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const int8_t *a = aux8;
+    for (int j = 0; j < QK_K / 32; ++j) {
+      const int32_t scale = scales[j];
+      for (int part = 0; part < 4; ++part) {
+        int16_t aux16[8];
+        for (int l = 0; l < 8; ++l) aux16[l] = (int16_t)(q8[l] * a[l]);
+        for (int l = 0; l < 8; ++l) aux32[l] += scale * aux16[l];
+        q8 += 8;
+        a += 8;
+      }
+    }
+    const float d = wo_fp16_to_fp32(rd16(r)) * rdf32(xr);
+    for (int l = 0; l < 8; ++l) sums[l] += d * aux32[l];
+    const float dmin = wo_fp16_to_fp32(rd16(r + 2)) * rdf32(xr);
+    sumf -= dmin * sumi;
+  }
+  for (int l = 0; l < 8; ++l) sumf += sums[l];
+  return sumf;
+}
+
 /* q of element e (0..255) of a Q6_K record, in [-32, 31] */
 static inline int q6_value(const uint8_t *r, int e) {
   const int h = e / 128, i = e % 128, qq = i / 32, l = i % 32;
@@ -903,6 +1040,7 @@ size_t wo_weight_row_bytes(int fmt, int64_t k) {
   case WO_IQ2_XXS: return (size_t)(k / 256) * IQ2_XXS_BYTES;
   case WO_MXFP4: return (size_t)(k / 32) * MXFP4_BYTES;
   case WO_Q6_K: return (size_t)(k / 256) * Q6_K_BYTES;
+  case WO_Q5_K: return (size_t)(k / 256) * Q5_K_BYTES;
   }
   return 0;
 }
@@ -920,6 +1058,7 @@ static vec_dot_fn select_vec_dot(int fmt) {
   case WO_IQ2_XXS: return wo_vec_dot_iq2_xxs_q8_K;
   case WO_MXFP4: return wo_vec_dot_mxfp4_q8_0;
   case WO_Q6_K: return wo_vec_dot_q6_K_q8_K;
+  case WO_Q5_K: return wo_vec_dot_q5_K_q8_K;
   }
   return 0;
 }
@@ -977,10 +1116,10 @@ int64_t wo_int_partials(int fmt, const uint8_t *w, const uint8_t *x, int64_t k, 
       }
       out[n++] = s;
     }
-  } else if (fmt == WO_Q4_K) {
+  } else if (fmt == WO_Q4_K || fmt == WO_Q5_K) {
     const int64_t nb = k / QK_K;
     for (int64_t i = 0; i < nb; ++i) {
-      const uint8_t *wr = w + i * Q4_K_BYTES;
+      const uint8_t *wr = w + i * (fmt == WO_Q4_K ? Q4_K_BYTES : Q5_K_BYTES);
       const uint8_t *xr = x + i * Q8_K_BYTES;
       const int8_t *q8 = (const int8_t *)(xr + 4);
       int32_t mn = 0;
@@ -990,7 +1129,7 @@ int64_t wo_int_partials(int fmt, const uint8_t *w, const uint8_t *x, int64_t k, 
         const uint8_t *q4 = wr + 16 + 32 * (s / 2);
         int32_t p = 0;
         for (int l = 0; l < 32; ++l) {
-          const int v = (s & 1) ? (q4[l] >> 4) : (q4[l] & 0xF);
+          const int v = fmt == WO_Q5_K ? q5_value(wr, 32 * s + l) : (s & 1) ? (q4[l] >> 4) : (q4[l] & 0xF);
           p += v * q8[32 * s + l];
         }
         out[n++] = p;
@@ -1077,12 +1216,12 @@ void wo_mul_mat_f64(int fmt, const uint8_t *W, const uint8_t *Xq, double *E, dou
       } else {
         const int64_t nb = K / QK_K;
         for (int64_t i = 0; i < nb; ++i) {
-          const uint8_t *wr = w + i * (fmt == WO_Q4_K ? Q4_K_BYTES : IQ2_XXS_BYTES);
+          const uint8_t *wr = w + i * (fmt == WO_Q4_K ? Q4_K_BYTES : fmt == WO_Q5_K ? Q5_K_BYTES : IQ2_XXS_BYTES);
           const uint8_t *xr = x + i * Q8_K_BYTES;
           wo_int_partials(fmt, wr, xr, QK_K, parts);
           const double dx = rdf32(xr);
           const double dw = wo_fp16_to_fp32(rd16(wr));
-          if (fmt == WO_Q4_K) {
+          if (fmt == WO_Q4_K || fmt == WO_Q5_K) {
             uint8_t sc, mm;
             int64_t S = 0;
             for (int s = 0; s < 8; ++s) {

@@ -32,6 +32,7 @@ enum wo_format {
   WO_IQ2_XXS = 2,
   WO_MXFP4 = 3,
   WO_Q6_K = 4,
+  WO_Q5_K = 5,
 };
 
 /* scalar conversions (ggml-impl.h:384-431, :477-495) */
@@ -54,6 +55,7 @@ void wo_quantize_row_q4_K(const float *x, uint8_t *y, int64_t k);
 void wo_quantize_row_mxfp4(const float *x, uint8_t *y, int64_t k);
 void wo_quantize_row_iq2_xxs(const float *x, uint8_t *y, int64_t k);
 void wo_quantize_row_q6_K(const float *x, uint8_t *y, int64_t k);
+void wo_quantize_row_q5_K(const float *x, uint8_t *y, int64_t k);
 
 /* activation quantizers (on the hot path) */
 void wo_quantize_row_q8_0(const float *x, uint8_t *y, int64_t k);
@@ -65,6 +67,7 @@ void wo_dequantize_row_q4_K(const uint8_t *x, float *y, int64_t k);
 void wo_dequantize_row_iq2_xxs(const uint8_t *x, float *y, int64_t k);
 void wo_dequantize_row_mxfp4(const uint8_t *x, float *y, int64_t k);
 void wo_dequantize_row_q6_K(const uint8_t *x, float *y, int64_t k);
+void wo_dequantize_row_q5_K(const uint8_t *x, float *y, int64_t k);
 
 /* generic vec_dots: w row (k elements) . quantized activation row */
 float wo_vec_dot_q4_0_q8_0(const uint8_t *w, const uint8_t *x, int64_t k);
@@ -72,6 +75,7 @@ float wo_vec_dot_q4_K_q8_K(const uint8_t *w, const uint8_t *x, int64_t k);
 float wo_vec_dot_iq2_xxs_q8_K(const uint8_t *w, const uint8_t *x, int64_t k);
 float wo_vec_dot_mxfp4_q8_0(const uint8_t *w, const uint8_t *x, int64_t k);
 float wo_vec_dot_q6_K_q8_K(const uint8_t *w, const uint8_t *x, int64_t k);
+float wo_vec_dot_q5_K_q8_K(const uint8_t *w, const uint8_t *x, int64_t k);
 
 /* Bytes of one encoded row of k elements for a weight format, or of the
  * activation format that pairs with it (Q8_0 for Q4_0/MXFP4, Q8_K else). */
@@ -95,7 +99,7 @@ void wo_mul_mat_f64(int fmt, const uint8_t *W, const uint8_t *Xq, double *E,
 
 /* Integer partials of one row pair, for exactness checks on tiny inputs:
  * Q4_0 / MXFP4 : one int32 per 32-block (P)
- * Q4_K         : per superblock, 8 sub-block sums P_s then the min sum Mn
+ * Q4_K / Q5_K  : per superblock, 8 sub-block sums P_s then the min sum Mn
  * IQ2_XXS      : one int32 per superblock (B = sum_g I_g * (2 s_g + 1))
  * Q6_K         : per superblock, the 16 group sums P_g (16 elements each)
  * returns the number of int32 written. */

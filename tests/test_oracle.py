@@ -102,9 +102,9 @@ def test_record_sizes_match_ggml_static_asserts():
             e = e.replace(name, str(env[name]))
         sizes[k] = eval(e, {"__builtins__": {}})  # arithmetic on literals only
     assert sizes == {"block_q4_0": 18, "block_mxfp4": 17, "block_q8_0": 34, "block_q4_K": 144,
-                     "block_q8_K": 292, "block_iq2_xxs": 66, "block_q6_K": 210}
+                     "block_q8_K": 292, "block_iq2_xxs": 66, "block_q6_K": 210, "block_q5_K": 176}
     assert {k: o.RECORD[k][1] for k in o.RECORD} == {
-        "q4_0": 18, "mxfp4": 17, "q8_0": 34, "q4_k": 144, "q8_k": 292, "iq2_xxs": 66, "q6_k": 210}
+        "q4_0": 18, "mxfp4": 17, "q8_0": 34, "q4_k": 144, "q8_k": 292, "iq2_xxs": 66, "q6_k": 210, "q5_k": 176}
 
 
 # ------------------------------------------------------------ dequantizers
@@ -213,6 +213,36 @@ def test_dequant_q6_k_brute_force():
         want.append([(d * np.float32(sc[e // 16])) * np.float32(c - 32) for e, c in enumerate(codes)])
     w = np.frombuffer(b"".join(recs), np.uint8).reshape(len(recs), 210)
     got = o.dequantize("q6_k", w, 256)
+    assert np.array_equal(got.view(np.uint32), np.array(want, np.float32).view(np.uint32))
+
+
+def test_dequant_q5_k_brute_force():
+    # Weft Q5_K (examples/formats/ggml.py:101-110): d, dmin, (sc, m) 6-bit x 8
+    # packed as Q4_K's, qh u1[256] bit_layers(32, lo_first) -> byte e % 32,
+    # bit e // 32; q u4[256] as Q4_K's; value d*sc*(q | qh << 4) - dmin*m
+    # (examples/kernels/dequantize/q5_k.py, functions/quantization.py:14-17)
+    rng = np.random.default_rng(11)
+    recs, want = [], []
+    for trial in range(600):
+        sc = [int(v) for v in rng.integers(0, 64, 8)]
+        m = [int(v) for v in rng.integers(0, 64, 8)]
+        codes = [int(v) for v in rng.integers(0, 32, 256)]
+        if trial < 64:  # every scale, min and code value in every position
+            sc = [(trial + 7 * s) % 64 for s in range(8)]
+            m = [(63 - trial + 5 * s) % 64 for s in range(8)]
+            codes = [(trial + 11 * e) % 32 for e in range(256)]
+        dh, mh = D16[trial % 6], D16[(trial + 3) % 6]
+        d = float(np.uint16(dh).view(np.float16))
+        dm = float(np.uint16(mh).view(np.float16))
+        qh, qs = bytearray(32), bytearray(128)
+        for e, c in enumerate(codes):
+            qs[32 * (e // 64) + e % 32] |= (c & 0xF) if e % 64 < 32 else (c & 0xF) << 4
+            qh[e % 32] |= (c >> 4) << (e // 32)
+        recs.append(dh.to_bytes(2, "little") + mh.to_bytes(2, "little") + _pack_q4k_scales(sc, m) +
+                    bytes(qh) + bytes(qs))
+        want.append([np.float32(d * sc[e // 32] * c - dm * m[e // 32]) for e, c in enumerate(codes)])
+    w = np.frombuffer(b"".join(recs), np.uint8).reshape(len(recs), 176)
+    got = o.dequantize("q5_k", w, 256)
     assert np.array_equal(got.view(np.uint32), np.array(want, np.float32).view(np.uint32))
 
 
@@ -333,7 +363,7 @@ def _dequant_act(act, xq, k):
     return (q * d).reshape(xq.shape[0], k)
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "iq2_xxs", "mxfp4", "q6_k"])
+@pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "iq2_xxs", "mxfp4", "q6_k", "q5_k"])
 def test_mul_mat_against_independent_float64_path(fmt):
     n, k, m = 48, 2048, 3
     w = o.quantize(fmt, o.seeded_normal(31, (n, k), 0.02))
@@ -400,7 +430,7 @@ def test_int_partials_q6_k_are_the_group_dots():
 
 # ------------------------------------------------ weight quantizers (inputs)
 @pytest.mark.parametrize("fmt,bound", [("q4_0", 0.10), ("q4_k", 0.09), ("mxfp4", 0.13), ("iq2_xxs", 0.45),
-                                       ("q6_k", 0.05)])
+                                       ("q6_k", 0.05), ("q5_k", 0.05)])
 def test_weight_quantizer_round_trip(fmt, bound):
     w = o.seeded_normal(51, (32, 4096), 0.02)
     d = o.dequantize(fmt, o.quantize(fmt, w), 4096)
