@@ -64,6 +64,8 @@ CASES = {
     # prefill entry runs the GEMV kernel (no MFMA form yet)
     "q6_k_decode": ("production_mul_mat_q6_k_decode", "q6_k", 11008, 4096, 1, "hbm"),
     "q6_k_prefill": ("production_mul_mat_q6_k", "q6_k", 4096, 4096, 512, "mfma"),
+    # adjacent format Q5_K (ggml-common.h:330-345), decode at the W_up shape
+    "q5_k_decode": ("production_mul_mat_q5_k_decode", "q5_k", 11008, 4096, 1, "hbm"),
     # GGML MUL_MAT_ID (MoE) prefill at a Mixtral-8x7B FFN shape: 8 experts of
     # 14336 x 4096 Q4_K, 2 experts per token, 512 tokens (the grouped GEMM)
     "q4_k_moe_prefill": ("weft_ggml_mul_mat_id", "q4_k", 14336, 4096, 512, "mfma"),

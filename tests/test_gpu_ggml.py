@@ -19,8 +19,10 @@ from weft_amd import ggml as G
 
 pytestmark = pytest.mark.gpu
 
-TYPE = {"q4_0": G.Q4_0, "q4_k": G.Q4_K, "iq2_xxs": G.IQ2_XXS, "mxfp4": G.MXFP4, "q6_k": G.Q6_K}
-VDT = {"q4_0": G.Q8_0, "mxfp4": G.Q8_0, "q4_k": G.Q8_K, "iq2_xxs": G.Q8_K, "q6_k": G.Q8_K}
+TYPE = {"q4_0": G.Q4_0, "q4_k": G.Q4_K, "iq2_xxs": G.IQ2_XXS, "mxfp4": G.MXFP4, "q6_k": G.Q6_K,
+        "q5_k": G.Q5_K}
+VDT = {"q4_0": G.Q8_0, "mxfp4": G.Q8_0, "q4_k": G.Q8_K, "iq2_xxs": G.Q8_K, "q6_k": G.Q8_K,
+       "q5_k": G.Q8_K}
 FMTS = list(TYPE)
 NAN = 0x7FC00001  # a quiet NaN the kernels never produce
 

@@ -1,6 +1,7 @@
 // Decode GEMV for the formats whose records are not 16-byte multiples:
 // Q4_0 x Q8_0 (18 B / 32), MXFP4 x Q8_0 (17 B / 32), IQ2_XXS x Q8_K
-// (66 B / 256), Q6_K x Q8_K (210 B / 256); plus their single-output vec_dots.
+// (66 B / 256), Q6_K x Q8_K (210 B / 256), Q5_K x Q8_K (176 B / 256); plus
+// their single-output vec_dots.
 //
 // Semantics (GGML generic vec_dots, ggml-cpu/quants.c):
 //   Q4_0    :174-208  y = sum_b dw_b * dx_b * sum_32 (q-8) * x
@@ -8,6 +9,8 @@
 //   IQ2_XXS :855-895  y = 0.125 * sum_B dw * dx * sum_g (2 s_g + 1) *
 //                         sum_32 grid[idx] * sign * x
 //   Q6_K    :800-853  y = sum_B dw * dx * sum_g sc_g * sum_16 (q - 32) * x
+//   Q5_K    :720-798  y = sum_B dx * (dw * sum_s sc_s * sum_32 q * x
+//                                    - dmin * sum_s m_s * bsum_s)
 // and the Weft kernels examples/kernels/mul_mat/{q4_0_decode,mxfp4_decode,
 // iq2_xxs_decode}.py (quantize X into Xq, then one vec_dot per output).
 //
@@ -38,7 +41,7 @@ constexpr int kWaves = kThreads / kWave;
 constexpr int kMaxRowsPerPass = 4;
 constexpr int kWindow = 2304 + 32;  // per-wave LDS window (bytes), with slack
 
-enum class Fmt { Q4_0, MXFP4, IQ2_XXS, Q6_K };
+enum class Fmt { Q4_0, MXFP4, IQ2_XXS, Q6_K, Q5_K };
 
 template <Fmt F>
 struct Traits;
@@ -60,6 +63,11 @@ struct Traits<Fmt::IQ2_XXS> {
 template <>
 struct Traits<Fmt::Q6_K> {
   static constexpr int kElems = 256, kBytes = 210, kSegRecords = 8, kItemsPerRecord = 8;
+  static constexpr bool kQ8K = true;
+};
+template <>
+struct Traits<Fmt::Q5_K> {
+  static constexpr int kElems = 256, kBytes = 176, kSegRecords = 8, kItemsPerRecord = 8;
   static constexpr bool kQ8K = true;
 };
 
@@ -84,6 +92,19 @@ struct Args {
 __device__ __forceinline__ uint32_t lds_u32(const char* base, int o) {
   const uint32_t* w = reinterpret_cast<const uint32_t*>(base + (o & ~3));
   return __builtin_amdgcn_alignbyte(w[1], w[0], (uint32_t)(o & 3));
+}
+
+// n consecutive 4-byte values from LDS byte offset o (any alignment): n + 1
+// aligned word reads and n byte-aligns (o + 4n + 3 inside the buffer)
+template <int n>
+__device__ __forceinline__ void lds_run(const char* base, int o, uint32_t (&v)[n]) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(base + (o & ~3));
+  const uint32_t sh = (uint32_t)(o & 3);
+  uint32_t t[n + 1];
+#pragma unroll
+  for (int i = 0; i <= n; ++i) t[i] = w[i];
+#pragma unroll
+  for (int i = 0; i < n; ++i) v[i] = __builtin_amdgcn_alignbyte(t[i + 1], t[i], sh);
 }
 
 // One segment of a row staged through registers, so the next segment's loads
@@ -294,6 +315,46 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
             s = dot4(hi3, xh.w, s);
             acc[m] += (float)s * wscale * v.d[gb];
           }
+        } else if constexpr (F == Fmt::Q5_K) {
+          // item = (superblock, 32-element sub-block s): the nibble half s % 2
+          // of qs bytes 48 + 32 (s / 2) + l and bit s of qh bytes 16 + l
+          const int sb = valid ? it >> 3 : 0, s = it & 7;
+          const int gsb = r0 + sb;
+          const int o = off0 + T::kBytes * sb;
+          uint32_t hd[4], qs[8], qh[8];
+          lds_run(win, o, hd);
+          lds_run(win, o + 48 + 32 * (s >> 1), qs);
+          lds_run(win, o + 16, qh);
+          int sc, mn;
+          q4k_scale_min(s, hd[1], hd[2], hd[3], sc, mn);
+          const float dw = fp16_to_fp32(hd[0] & 0xffffu), dmin = fp16_to_fp32(hd[0] >> 16);
+          const int nsh = 4 * (s & 1);
+          const uint32_t rot = (uint32_t)(s + 28) & 31u;  // bit s of each byte to bit 4
+          int wv[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            wv[j] = (int)(((qs[j] >> nsh) & 0x0f0f0f0fu) |
+                          (__builtin_amdgcn_alignbit(qh[j], qh[j], rot) & 0x10101010u));
+#pragma unroll
+          for (int m = 0; m < kMaxRowsPerPass; ++m) {
+            if (m >= a.mb) break;
+            const Q8KView v = q8k_view(act, K, m);
+            const int4 x0 = *reinterpret_cast<const int4*>(v.qs + 256 * gsb + 32 * s);
+            const int4 x1 = *reinterpret_cast<const int4*>(v.qs + 256 * gsb + 32 * s + 16);
+            int p = dot4(wv[0], x0.x, 0);
+            p = dot4(wv[1], x0.y, p);
+            p = dot4(wv[2], x0.z, p);
+            p = dot4(wv[3], x0.w, p);
+            p = dot4(wv[4], x1.x, p);
+            p = dot4(wv[5], x1.y, p);
+            p = dot4(wv[6], x1.z, p);
+            p = dot4(wv[7], x1.w, p);
+            // exact int32 S and Mn of the superblock over its 8 sub-blocks
+            // (|S| <= 256 * 31 * 127 * 63), then one fp32 term
+            const int S = sum8_of_sum4(sum4(valid ? sc * p : 0));
+            const int Mn = sum8_of_sum4(sum4(valid ? mn * v.bp[8 * gsb + s] : 0));
+            if (valid && s == 0) acc[m] += v.d[gsb] * (dw * (float)S - dmin * (float)Mn);
+          }
         } else if constexpr (F == Fmt::Q6_K) {
           // item = (superblock, 32-element chunk g): half h = g / 4, quarter
           // qq = g % 4; the chunk's 6-bit codes are the nibble 4 (qq / 2) of
@@ -309,11 +370,13 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
           const uint32_t sw = lds_u32(win, o + 192 + 2 * g);
           const int sc0 = (int)(int8_t)(sw & 0xffu), sc1 = (int)(int8_t)((sw >> 8) & 0xffu);
           const float dw = fp16_to_fp32(lds_u32(win, o + 208) & 0xffffu);
+          uint32_t ql[8], qh[8];
+          lds_run(win, qlo, ql);
+          lds_run(win, qho, qh);
           int wv[8];
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
-            const uint32_t q = ((lds_u32(win, qlo + 4 * j) >> nsh) & 0x0f0f0f0fu) |
-                               (((lds_u32(win, qho + 4 * j) >> hsh) & 0x03030303u) << 4);
+            const uint32_t q = ((ql[j] >> nsh) & 0x0f0f0f0fu) | (((qh[j] >> hsh) & 0x03030303u) << 4);
             wv[j] = (int)(((q | 0x80808080u) - 0x20202020u) ^ 0x80808080u);  // bytewise q - 32
           }
 #pragma unroll
@@ -477,6 +540,7 @@ void decode_pairs(int fmt, const uint8_t* W, const float* X, const uint8_t* xq_i
     case 0: return launch<Fmt::Q4_0>(W, X, xq_in, xq_out, nullptr, nullptr, Y, N, K, 1, st, &pr, n_pairs);
     case 1: return launch<Fmt::MXFP4>(W, X, xq_in, xq_out, tab0, tab1, Y, N, K, 1, st, &pr, n_pairs);
     case 3: return launch<Fmt::Q6_K>(W, X, xq_in, xq_out, nullptr, nullptr, Y, N, K, 1, st, &pr, n_pairs);
+    case 4: return launch<Fmt::Q5_K>(W, X, xq_in, xq_out, nullptr, nullptr, Y, N, K, 1, st, &pr, n_pairs);
     default: return launch<Fmt::IQ2_XXS>(W, X, xq_in, xq_out, tab0, tab1, Y, N, K, 1, st, &pr, n_pairs);
   }
 }
@@ -486,6 +550,11 @@ void decode_q6_k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t
   launch<Fmt::Q6_K>(W, X, nullptr, Xq, nullptr, nullptr, Y, N, K, M, st);
 }
 
+void decode_q5_k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
+                 size_t M, const RowStrides& st) {
+  launch<Fmt::Q5_K>(W, X, nullptr, Xq, nullptr, nullptr, Y, N, K, M, st);
+}
+
 void decode_quantized(int fmt, const uint8_t* W, const uint8_t* Xq, const int8_t* tab0,
                       const void* tab1, float* Y, size_t N, size_t K, size_t M,
                       const RowStrides& st) {
@@ -493,6 +562,7 @@ void decode_quantized(int fmt, const uint8_t* W, const uint8_t* Xq, const int8_t
     case 0: return launch<Fmt::Q4_0>(W, nullptr, Xq, nullptr, nullptr, nullptr, Y, N, K, M, st);
     case 1: return launch<Fmt::MXFP4>(W, nullptr, Xq, nullptr, tab0, tab1, Y, N, K, M, st);
     case 3: return launch<Fmt::Q6_K>(W, nullptr, Xq, nullptr, nullptr, nullptr, Y, N, K, M, st);
+    case 4: return launch<Fmt::Q5_K>(W, nullptr, Xq, nullptr, nullptr, nullptr, Y, N, K, M, st);
     default: return launch<Fmt::IQ2_XXS>(W, nullptr, Xq, nullptr, tab0, tab1, Y, N, K, M, st);
   }
 }
@@ -546,6 +616,24 @@ void production_mul_mat_q6_k(const uint8_t* W, const float* X, uint8_t* Xq, floa
                              size_t K, size_t M) {
   if (X == nullptr || Xq == nullptr) return weft::set_error(hipErrorInvalidValue);
   weft::decode_q6_k(W, X, Xq, Y, N, K, M, weft::packed(K / 256 * weft::kQ6_KBytes, K, N));
+}
+
+void production_mul_mat_q5_k_decode(const uint8_t* W, const float* X, uint8_t* Xq, float* Y,
+                                    size_t N, size_t K, size_t M) {
+  if (X == nullptr || Xq == nullptr) return weft::set_error(hipErrorInvalidValue);
+  weft::decode_q5_k(W, X, Xq, Y, N, K, M, weft::packed(K / 256 * weft::kQ5_KBytes, K, N));
+}
+
+// Q5_K prefill: the GEMV kernel at every M (no MFMA form yet)
+void production_mul_mat_q5_k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N,
+                             size_t K, size_t M) {
+  if (X == nullptr || Xq == nullptr) return weft::set_error(hipErrorInvalidValue);
+  weft::decode_q5_k(W, X, Xq, Y, N, K, M, weft::packed(K / 256 * weft::kQ5_KBytes, K, N));
+}
+
+void quantized_vec_dot_q5_k_q8_k(const uint8_t* W, const uint8_t* X, float* Y, size_t K) {
+  if (X == nullptr) return weft::set_error(hipErrorInvalidValue);
+  weft::launch<weft::Fmt::Q5_K>(W, nullptr, X, nullptr, nullptr, nullptr, Y, 1, K, 1, weft::packed(0, K, 1));
 }
 
 void quantized_vec_dot_q6_k_q8_k(const uint8_t* W, const uint8_t* X, float* Y, size_t K) {

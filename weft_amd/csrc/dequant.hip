@@ -1,6 +1,7 @@
-// Row dequantize: row_dequantize_{q4_0,q4_k,iq2_xxs,mxfp4,q6_k}
+// Row dequantize: row_dequantize_{q4_0,q4_k,iq2_xxs,mxfp4,q6_k,q5_k}
 // (examples/kernels/dequantize/*.py; GGML dequantize_row_* in
-// ggml-quants.c:401-419, :511-529, :1471-1493, :2416-2440, :1881-1910).
+// ggml-quants.c:401-419, :511-529, :1471-1493, :2416-2440, :1881-1910,
+// :1673-1697).
 //
 // Every product here is exact in fp32 (at most 22 significant bits), and
 // Q4_K's single subtraction rounds once, so the outputs are bit-exact with
@@ -160,6 +161,46 @@ __global__ void __launch_bounds__(kThreads) dq_q6k_kernel(const uint8_t* __restr
   }
 }
 
+// Q5_K (dequantize_row_q5_K, ggml-quants.c:1673-1697): as Q4_K, lane l
+// writing elements 4l..4l+3, with the fifth bit of each code from qh byte
+// e % 32, bit e / 32.  d * sc * q (<= 22 bits) and dmin * m are exact, the
+// subtraction rounds once: bit-exact.
+template <int U, bool Y16>
+__global__ void __launch_bounds__(kThreads) dq_q5k_kernel(const uint8_t* __restrict__ W,
+                                                          float* __restrict__ Y, long long nsb) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const long long wave = ((long long)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const long long nwaves = (long long)gridDim.x * blockDim.x / kWave;
+  const int g = lane >> 4;           // 64-element group
+  const int e = (lane & 15) * 4;     // offset inside the group
+  const int sub = 2 * g + (e >= 32); // 32-element sub-block
+  const int qoff = 48 + 32 * g + (e & 31), hoff = 16 + (e & 31);
+  const int shift = e >= 32 ? 4 : 0;
+  for (long long s0 = wave * U; s0 < nsb; s0 += nwaves * U) {
+    uint32_t hw[U][4], qs[U], qh[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint8_t* rec = W + min(s0 + u, nsb - 1) * kQ5_KBytes;  // clamped: a valid record
+#pragma unroll
+      for (int i = 0; i < 4; ++i) hw[u][i] = ld_u32_a2(rec + 4 * i);
+      qs[u] = ld_u32_a2(rec + qoff);
+      qh[u] = ld_u32_a2(rec + hoff);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (s0 + u >= nsb) break;
+      int sc, m;
+      q4k_scale_min(sub, hw[u][1], hw[u][2], hw[u][3], sc, m);
+      const float d = fp16_to_fp32(hw[u][0] & 0xffffu), dmin = fp16_to_fp32(hw[u][0] >> 16);
+      const float d1 = d * (float)sc, m1 = dmin * (float)m;
+      const uint32_t n = ((qs[u] >> shift) & 0x0f0f0f0fu) | (((qh[u] >> sub) & 0x01010101u) << 4);
+      store4<Y16>(Y + (s0 + u) * 256 + 4 * lane, d1 * (float)(n & 0xff) - m1,
+                  d1 * (float)((n >> 8) & 0xff) - m1, d1 * (float)((n >> 16) & 0xff) - m1,
+                  d1 * (float)(n >> 24) - m1);
+    }
+  }
+}
+
 // IQ2_XXS: one wave per superblock; lane l -> elements 4l..4l+3
 template <bool Y16>
 __global__ void __launch_bounds__(kThreads) dq_iq2xxs_kernel(const uint8_t* __restrict__ W,
@@ -218,6 +259,20 @@ void row_dequantize_q4_k(const uint8_t* W, float* Y, size_t K) {
     dq_q4k_kernel<U, false, true><<<g, kThreads, 0, current_stream()>>>(W, Y, nsb);
   else
     dq_q4k_kernel<U, false, false><<<g, kThreads, 0, current_stream()>>>(W, Y, nsb);
+  check_launch();
+}
+
+void row_dequantize_q5_k(const uint8_t* W, float* Y, size_t K) {
+  using namespace weft;
+  if (K == 0) return;
+  if (K % 256 || bad(W, 2, Y)) return set_error(hipErrorInvalidValue);
+  const long long nsb = (long long)(K / 256);
+  constexpr int U = 4;
+  const int g = grid_for((nsb + U - 1) / U);
+  if (aligned(Y, 16))
+    dq_q5k_kernel<U, true><<<g, kThreads, 0, current_stream()>>>(W, Y, nsb);
+  else
+    dq_q5k_kernel<U, false><<<g, kThreads, 0, current_stream()>>>(W, Y, nsb);
   check_launch();
 }
 

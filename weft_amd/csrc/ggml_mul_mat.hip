@@ -1,6 +1,6 @@
 // GGML's MUL_MAT op on the quantized mul_mat kernels: the contract of
 // ggml_compute_forward_mul_mat (ggml-cpu/ggml-cpu.c:1245-1443) for src0 of
-// type Q4_0, Q4_K, Q6_K, IQ2_XXS or MXFP4, so the kernels can sit under a
+// type Q4_0, Q4_K, Q5_K, Q6_K, IQ2_XXS or MXFP4, so the kernels can sit under a
 // ggml-style graph executor.
 //
 //   dst[i3, i2, i1, i0] = vec_dot(src0 row i0 of plane (i2 / r2, i3 / r3),
@@ -49,6 +49,7 @@ constexpr TypeInfo kTypes[] = {
     {WEFT_GGML_TYPE_Q4_0, 32, kQ4_0Bytes, WEFT_GGML_TYPE_Q8_0},
     {WEFT_GGML_TYPE_Q8_0, 32, kQ8_0Bytes, -1},
     {WEFT_GGML_TYPE_Q4_K, 256, kQ4_KBytes, WEFT_GGML_TYPE_Q8_K},
+    {WEFT_GGML_TYPE_Q5_K, 256, kQ5_KBytes, WEFT_GGML_TYPE_Q8_K},
     {WEFT_GGML_TYPE_Q6_K, 256, kQ6_KBytes, WEFT_GGML_TYPE_Q8_K},
     {WEFT_GGML_TYPE_Q8_K, 256, kQ8_KBytes, -1},
     {WEFT_GGML_TYPE_IQ2_XXS, 256, kIq2xxsBytes, WEFT_GGML_TYPE_Q8_K},
@@ -216,6 +217,7 @@ hipError_t mul_mat(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1, const
           case WEFT_GGML_TYPE_Q4_0: mul_mat_q4_0(W, X, Xq, Y, n, k, m, st); break;
           case WEFT_GGML_TYPE_Q4_K: mul_mat_q4k(W, X, Xq, Y, n, k, m, st); break;
           case WEFT_GGML_TYPE_Q6_K: decode_q6_k(W, X, Xq, Y, n, k, m, st); break;
+          case WEFT_GGML_TYPE_Q5_K: decode_q5_k(W, X, Xq, Y, n, k, m, st); break;
           case WEFT_GGML_TYPE_IQ2_XXS:
             mul_mat_iq2_xxs(W, X, Xq, tab->grid, tab->signs, Y, n, k, m, st);
             break;
@@ -226,6 +228,7 @@ hipError_t mul_mat(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1, const
           case WEFT_GGML_TYPE_Q4_0: decode_quantized(0, W, src1, nullptr, nullptr, Y, n, k, m, st); break;
           case WEFT_GGML_TYPE_Q4_K: mul_mat_q4k_quantized(W, src1, Y, n, k, m, st); break;
           case WEFT_GGML_TYPE_Q6_K: decode_quantized(3, W, src1, nullptr, nullptr, Y, n, k, m, st); break;
+          case WEFT_GGML_TYPE_Q5_K: decode_quantized(4, W, src1, nullptr, nullptr, Y, n, k, m, st); break;
           case WEFT_GGML_TYPE_IQ2_XXS:
             mul_mat_iq2_xxs_quantized(W, src1, tab->grid, tab->signs, Y, n, k, m, st);
             break;
@@ -341,6 +344,7 @@ hipError_t mul_mat_id(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1,
         }
         break;
       case WEFT_GGML_TYPE_Q6_K:
+      case WEFT_GGML_TYPE_Q5_K:
         break;  // no grouped GEMM: the pair GEMV below
       default: {  // Q4_0 / MXFP4: the GEMMs read a planar activation quantized from X
         const int fmt = s0->type == WEFT_GGML_TYPE_Q4_0 ? 0 : 1;
@@ -364,6 +368,9 @@ hipError_t mul_mat_id(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1,
       break;
     case WEFT_GGML_TYPE_Q6_K:
       decode_pairs(3, W, X, xq_in, xq_out, nullptr, nullptr, Y, (size_t)N, (size_t)K, st, pr, n_pairs);
+      break;
+    case WEFT_GGML_TYPE_Q5_K:
+      decode_pairs(4, W, X, xq_in, xq_out, nullptr, nullptr, Y, (size_t)N, (size_t)K, st, pr, n_pairs);
       break;
     case WEFT_GGML_TYPE_MXFP4:
       decode_pairs(1, W, X, xq_in, xq_out, tab->codebook, tab->scale, Y, (size_t)N, (size_t)K, st, pr,

@@ -129,7 +129,7 @@ const EncodingInfo kEncodings[] = {
     {"Q8_0", "uint8_t", 34, 32, 2},      {"Q8_K", "uint8_t", 292, 256, 4},
     {"IQ2_XXS", "uint8_t", 66, 256, 2},  {"MXFP4", "uint8_t", 17, 32, 1},
     {"I8X8", "uint8_t", 8, 8, 8},        {"Q4K_I[16]", "uint8_t", 144, 256, 16},
-    {"Q6_K", "uint8_t", 210, 256, 1},
+    {"Q6_K", "uint8_t", 210, 256, 1},    {"Q5_K", "uint8_t", 176, 256, 2},
     {"dense.f32", "float", 4, 1, 4},
     {"dense.i8", "int8_t", 1, 1, 1},
 };
@@ -181,6 +181,8 @@ std::vector<KernelSpec> kernel_specs() {
                "K"});
   k.push_back({"row_dequantize_q6_k",
                {{"W", "Q6_K", "K", false, nullptr}, {"Y", "dense.f32", "K", true, nullptr}}, "K"});
+  k.push_back({"row_dequantize_q5_k",
+               {{"W", "Q5_K", "K", false, nullptr}, {"Y", "dense.f32", "K", true, "output"}}, "K"});
   k.push_back({"q8_0_quantize",
                {{"X", "dense.f32", "K", false, nullptr}, {"Y", "Q8_0", "K", true, nullptr}}, "K"});
   k.push_back({"q8_K_quantize",
@@ -214,6 +216,11 @@ std::vector<KernelSpec> kernel_specs() {
                 {"X", "Q8_K", "K", false, nullptr},
                 {"Y", "dense.f32", "1", true, nullptr}},
                "K"});
+  k.push_back({"quantized_vec_dot_q5_k_q8_k",
+               {{"W", "Q5_K", "K", false, nullptr},
+                {"X", "Q8_K", "K", false, nullptr},
+                {"Y", "dense.f32", "1", true, nullptr}},
+               "K"});
   mm("production_mul_mat_q4_0", "Q4_0", "Q8_0", false, {});
   mm("production_mul_mat_q4_0_decode", "Q4_0", "Q8_0", false, {});
   mm("production_mul_mat_q4_k", "Q4_K", "Q8_K", false, {});
@@ -226,6 +233,8 @@ std::vector<KernelSpec> kernel_specs() {
   mm("production_mul_mat_mxfp4_decode", "MXFP4", "Q8_0", true, mx);
   mm("production_mul_mat_q6_k", "Q6_K", "Q8_K", true, {});
   mm("production_mul_mat_q6_k_decode", "Q6_K", "Q8_K", false, {});
+  mm("production_mul_mat_q5_k", "Q5_K", "Q8_K", false, {});
+  mm("production_mul_mat_q5_k_decode", "Q5_K", "Q8_K", false, {});
   for (const char* sym : {"q4_k_q8_k_gemv", "q4_k_q8_k_gemv_groups4", "q4_k_q8_k_gemv_contract"})
     k.push_back({sym,
                  {{"W", "Q4K_I[16]", "M,K", false, nullptr},

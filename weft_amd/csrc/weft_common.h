@@ -22,6 +22,7 @@ constexpr int kQ4_KElems = 256, kQ4_KBytes = 144;
 constexpr int kQ8_KElems = 256, kQ8_KBytes = 292;
 constexpr int kIq2xxsElems = 256, kIq2xxsBytes = 66;
 constexpr int kQ6_KElems = 256, kQ6_KBytes = 210;  // ql[128] qh[64] scales[16] d
+constexpr int kQ5_KElems = 256, kQ5_KBytes = 176;  // d dmin scales[12] qh[32] qs[128]
 
 // ---------------------------------------------------------------- numerics
 // IEEE binary16 -> binary32 with v_cvt_f32_f16.  Exact for every input

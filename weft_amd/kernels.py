@@ -56,13 +56,14 @@ _DECODE_GROUPS = {"Xq": "workspace", "Y": "output"}
 
 # wl.auto extents of the tiled prefill kernels (mul_mat/q4_0.py:17-22,
 # q4_k_staged.py:20-24, iq2_xxs_staged.py:43-48 and :80-83, mxfp4.py:21-25,
-# q6_k.py:17-21)
+# q6_k.py:17-21, q5_k.py:17-22)
 _AUTO = {
     "production_mul_mat_q4_0": ("MC", "MR", "NC", "NR"),
     "production_mul_mat_q4_k_staged": ("KC", "MC", "MR", "NC"),
     "production_mul_mat_iq2_xxs_staged": ("KC", "MC", "MR", "NC", "NR"),
     "production_mul_mat_mxfp4": ("MC", "MR", "NC", "NR"),
     "production_mul_mat_q6_k": ("MC", "MR", "NC", "NR"),
+    "production_mul_mat_q5_k": ("MC", "MR", "NC", "NR"),
 }
 
 # (symbol, parameters, reference source, alias groups)
@@ -97,6 +98,10 @@ _DEFS = [
     ("quantized_vec_dot_q6_k_q8_k", ("W", "X", "Y"), "examples/kernels/vec_dot/q6_k_q8_k.py:39-44", None),
     ("production_mul_mat_q6_k", _MM, "examples/kernels/mul_mat/q6_k.py:9-37", _DECODE_GROUPS),
     ("production_mul_mat_q6_k_decode", _MM, "examples/kernels/mul_mat/q6_k_decode.py:10-20", None),
+    ("row_dequantize_q5_k", ("W", "Y"), "examples/kernels/dequantize/q5_k.py:9-15", {"Y": "output"}),
+    ("quantized_vec_dot_q5_k_q8_k", ("W", "X", "Y"), "examples/kernels/vec_dot/q5_k_q8_k.py:34-38", None),
+    ("production_mul_mat_q5_k", _MM, "examples/kernels/mul_mat/q5_k.py:9-37", None),
+    ("production_mul_mat_q5_k_decode", _MM, "examples/kernels/mul_mat/q5_k_decode.py:10-20", None),
     ("q4_k_q8_k_gemv", ("W", "X", "Y"), "examples/kernels/gemv/q4_k.py:8-26", None),
     ("q4_k_q8_k_gemv_groups4", ("W", "X", "Y"), "examples/kernels/gemv/q4_k_groups4.py:8-26", None),
     ("q4_k_q8_k_gemv_contract", ("W", "X", "Y"), "examples/kernels/gemv/q4_k_contract.py:8-26", None),
