@@ -39,7 +39,11 @@ namespace {
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kMaxRowsPerPass = 4;
-constexpr int kWindow = 2304 + 32;  // per-wave LDS window (bytes), with slack
+// per-wave LDS window (bytes), with slack.  A wave keeps one segment in
+// flight while it computes the previous one, so the window sets the bytes in
+// flight per CU (16 waves x ~4.5 KB): with ~2 us of loaded HBM latency,
+// 2.3 KB windows held Q5_K / Q6_K near 2.3-2.7 TB/s.
+constexpr int kWindow = 4608 + 32;
 
 enum class Fmt { Q4_0, MXFP4, IQ2_XXS, Q6_K, Q5_K };
 
@@ -47,27 +51,27 @@ template <Fmt F>
 struct Traits;
 template <>
 struct Traits<Fmt::Q4_0> {
-  static constexpr int kElems = 32, kBytes = 18, kSegRecords = 128, kItemsPerRecord = 1;
+  static constexpr int kElems = 32, kBytes = 18, kSegRecords = 256, kItemsPerRecord = 1;
   static constexpr bool kQ8K = false;
 };
 template <>
 struct Traits<Fmt::MXFP4> {
-  static constexpr int kElems = 32, kBytes = 17, kSegRecords = 128, kItemsPerRecord = 1;
+  static constexpr int kElems = 32, kBytes = 17, kSegRecords = 256, kItemsPerRecord = 1;
   static constexpr bool kQ8K = false;
 };
 template <>
 struct Traits<Fmt::IQ2_XXS> {
-  static constexpr int kElems = 256, kBytes = 66, kSegRecords = 32, kItemsPerRecord = 8;
+  static constexpr int kElems = 256, kBytes = 66, kSegRecords = 64, kItemsPerRecord = 8;
   static constexpr bool kQ8K = true;
 };
 template <>
 struct Traits<Fmt::Q6_K> {
-  static constexpr int kElems = 256, kBytes = 210, kSegRecords = 8, kItemsPerRecord = 8;
+  static constexpr int kElems = 256, kBytes = 210, kSegRecords = 16, kItemsPerRecord = 8;
   static constexpr bool kQ8K = true;
 };
 template <>
 struct Traits<Fmt::Q5_K> {
-  static constexpr int kElems = 256, kBytes = 176, kSegRecords = 8, kItemsPerRecord = 8;
+  static constexpr int kElems = 256, kBytes = 176, kSegRecords = 16, kItemsPerRecord = 8;
   static constexpr bool kQ8K = true;
 };
 
@@ -206,6 +210,33 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
     for (int i = threadIdx.x; i < 256; i += blockDim.x)
       reinterpret_cast<float*>(tables)[i] = reinterpret_cast<const float*>(a.tab1)[i];
   }
+  char* win = windows + wave * kWindow;
+  const int nrec = K / T::kElems;
+  const size_t rb = a.ldw;
+  const uint8_t* wlo = a.W;
+  // end of the last row: staging windows are clamped to [wlo, whi)
+  const uint8_t* whi = a.W + (size_t)(a.N - 1) * rb + (size_t)nrec * T::kBytes;
+  const int row0 = blockIdx.x * a.rows_per_wg;
+  const int row1 = min(a.N, row0 + a.rows_per_wg);
+
+  // this wave's (row, segment) sequence, one segment fetched ahead
+  const int nseg = (nrec + T::kSegRecords - 1) / T::kSegRecords;
+  const int my_rows = row0 + wave < row1 ? (row1 - row0 - wave + nwaves - 1) / nwaves : 0;
+  const int total = my_rows * nseg;
+  auto seg_span = [&](int si, const uint8_t*& p0, const uint8_t*& p1) {
+    const int ri = si / nseg, r0 = (si - ri * nseg) * T::kSegRecords;
+    const uint8_t* wr = a.W + (size_t)(row0 + wave + nwaves * ri) * rb;
+    p0 = wr + (size_t)r0 * T::kBytes;
+    p1 = wr + (size_t)min(r0 + T::kSegRecords, nrec) * T::kBytes;
+  };
+  // the first segment's loads are issued before the activation is staged,
+  // so its HBM latency overlaps the quantization
+  SegmentFetch pf;
+  if (total > 0) {
+    const uint8_t *p0, *p1;
+    seg_span(0, p0, p1);
+    pf.fetch(p0, p1, wlo, whi, lane);
+  }
   if constexpr (T::kQ8K) {
     if (a.X != nullptr)
       stage_q8k_quantize(a.X, a.ldx, blockIdx.x == 0 ? a.xq_out : nullptr, K, a.m0, a.mb, act);
@@ -229,31 +260,6 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
     c3 = ld_u32_a1(cb + 12);
   }
 
-  char* win = windows + wave * kWindow;
-  const int nrec = K / T::kElems;
-  const size_t rb = a.ldw;
-  const uint8_t* wlo = a.W;
-  // end of the last row: staging windows are clamped to [wlo, whi)
-  const uint8_t* whi = a.W + (size_t)(a.N - 1) * rb + (size_t)nrec * T::kBytes;
-  const int row0 = blockIdx.x * a.rows_per_wg;
-  const int row1 = min(a.N, row0 + a.rows_per_wg);
-
-  // this wave's (row, segment) sequence, one segment fetched ahead
-  const int nseg = (nrec + T::kSegRecords - 1) / T::kSegRecords;
-  const int my_rows = row0 + wave < row1 ? (row1 - row0 - wave + nwaves - 1) / nwaves : 0;
-  const int total = my_rows * nseg;
-  auto seg_span = [&](int si, const uint8_t*& p0, const uint8_t*& p1) {
-    const int ri = si / nseg, r0 = (si - ri * nseg) * T::kSegRecords;
-    const uint8_t* wr = a.W + (size_t)(row0 + wave + nwaves * ri) * rb;
-    p0 = wr + (size_t)r0 * T::kBytes;
-    p1 = wr + (size_t)min(r0 + T::kSegRecords, nrec) * T::kBytes;
-  };
-  SegmentFetch pf;
-  if (total > 0) {
-    const uint8_t *p0, *p1;
-    seg_span(0, p0, p1);
-    pf.fetch(p0, p1, wlo, whi, lane);
-  }
   float acc[kMaxRowsPerPass];
   for (int si = 0; si < total; ++si) {
     const int ri = si / nseg, seg = si - ri * nseg;
