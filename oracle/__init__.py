@@ -20,16 +20,18 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libweft_oracle.so"
 
-Q4_0, Q4_K, IQ2_XXS, MXFP4, Q6_K, Q5_K = 0, 1, 2, 3, 4, 5
-FORMATS = {"q4_0": Q4_0, "q4_k": Q4_K, "iq2_xxs": IQ2_XXS, "mxfp4": MXFP4, "q6_k": Q6_K, "q5_k": Q5_K}
+Q4_0, Q4_K, IQ2_XXS, MXFP4, Q6_K, Q5_K, NVFP4 = 0, 1, 2, 3, 4, 5, 6
+FORMATS = {"q4_0": Q4_0, "q4_k": Q4_K, "iq2_xxs": IQ2_XXS, "mxfp4": MXFP4, "q6_k": Q6_K, "q5_k": Q5_K,
+           "nvfp4": NVFP4}
 
 # (elements per record, bytes per record)
 RECORD = {
     "q4_0": (32, 18), "mxfp4": (32, 17), "q8_0": (32, 34),
     "q4_k": (256, 144), "q8_k": (256, 292), "iq2_xxs": (256, 66), "q6_k": (256, 210),
-    "q5_k": (256, 176),
+    "q5_k": (256, 176), "nvfp4": (64, 36),
 }
-ACT_OF = {"q4_0": "q8_0", "mxfp4": "q8_0", "q4_k": "q8_k", "iq2_xxs": "q8_k", "q6_k": "q8_k", "q5_k": "q8_k"}
+ACT_OF = {"q4_0": "q8_0", "mxfp4": "q8_0", "q4_k": "q8_k", "iq2_xxs": "q8_k", "q6_k": "q8_k", "q5_k": "q8_k",
+          "nvfp4": "q8_0"}
 
 
 def build() -> Path:
@@ -65,6 +67,9 @@ def _declare(l: ctypes.CDLL) -> None:
         "wo_iq2xxs_grid": ([_P], None), "wo_ksigns_iq2xs": ([_P], None),
         "wo_signs_i8x8": ([_P], None), "wo_kvalues_mxfp4": ([_P], None),
         "wo_e8m0_half_table": ([_P], None),
+        "wo_ue4m3_to_fp32": ([ctypes.c_uint8], ctypes.c_float),
+        "wo_fp32_to_ue4m3": ([ctypes.c_float], ctypes.c_uint8),
+        "wo_ue4m3_table": ([_P], None),
         "wo_weight_row_bytes": ([ctypes.c_int, _I64], ctypes.c_size_t),
         "wo_act_row_bytes": ([ctypes.c_int, _I64], ctypes.c_size_t),
         "wo_mul_mat": ([ctypes.c_int, _P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int], None),
@@ -73,11 +78,12 @@ def _declare(l: ctypes.CDLL) -> None:
         "wo_int_partials": ([ctypes.c_int, _P, _P, _I64, _P], _I64),
         "wo_max_threads": ([], ctypes.c_int),
     }
-    for fmt in ("q4_0", "q4_K", "mxfp4", "iq2_xxs", "q6_K", "q5_K", "q8_0", "q8_K"):
+    for fmt in ("q4_0", "q4_K", "mxfp4", "iq2_xxs", "q6_K", "q5_K", "nvfp4", "q8_0", "q8_K"):
         sig[f"wo_quantize_row_{fmt}"] = ([_P, _P, _I64], None)
-    for fmt in ("q4_0", "q4_K", "mxfp4", "iq2_xxs", "q6_K", "q5_K"):
+    for fmt in ("q4_0", "q4_K", "mxfp4", "iq2_xxs", "q6_K", "q5_K", "nvfp4"):
         sig[f"wo_dequantize_row_{fmt}"] = ([_P, _P, _I64], None)
-    for name in ("q4_0_q8_0", "q4_K_q8_K", "iq2_xxs_q8_K", "mxfp4_q8_0", "q6_K_q8_K", "q5_K_q8_K"):
+    for name in ("q4_0_q8_0", "q4_K_q8_K", "iq2_xxs_q8_K", "mxfp4_q8_0", "q6_K_q8_K", "q5_K_q8_K",
+                 "nvfp4_q8_0"):
         sig[f"wo_vec_dot_{name}"] = ([_P, _P, _I64], ctypes.c_float)
     for name, (args, res) in sig.items():
         fn = getattr(l, name)
@@ -147,6 +153,13 @@ def e8m0_half_table() -> np.ndarray:
     return out
 
 
+def ue4m3_table() -> np.ndarray:
+    """ggml_ue4m3_to_fp32 of every byte (NVFP4 sub-block scales)."""
+    out = np.empty(256, np.float32)
+    lib().wo_ue4m3_table(_ptr(out))
+    return out
+
+
 # ----------------------------------------------------------------- quantizers
 def quantize(fmt: str, x: np.ndarray, out: np.ndarray | None = None) -> np.ndarray:
     """Quantize rows of fp32 ``x`` (..., K) into ``fmt`` records (uint8)."""
@@ -157,7 +170,7 @@ def quantize(fmt: str, x: np.ndarray, out: np.ndarray | None = None) -> np.ndarr
     if out is None:
         out = np.zeros(x.shape[:-1] + (rb,), np.uint8)
     name = {"q4_0": "q4_0", "q4_k": "q4_K", "mxfp4": "mxfp4", "iq2_xxs": "iq2_xxs",
-            "q6_k": "q6_K", "q5_k": "q5_K", "q8_0": "q8_0", "q8_k": "q8_K"}[fmt]
+            "q6_k": "q6_K", "q5_k": "q5_K", "nvfp4": "nvfp4", "q8_0": "q8_0", "q8_k": "q8_K"}[fmt]
     fn = getattr(lib(), f"wo_quantize_row_{name}")
     # one call over all rows: records never straddle rows
     fn(_ptr(x), _ptr(out), rows * k)
@@ -170,13 +183,14 @@ def dequantize(fmt: str, w: np.ndarray, k: int) -> np.ndarray:
     rb = record_bytes(fmt, k)
     rows = w.size // rb if rb else 0
     out = np.empty(w.shape[:-1] + (k,), np.float32)
-    name = {"q4_0": "q4_0", "q4_k": "q4_K", "mxfp4": "mxfp4", "iq2_xxs": "iq2_xxs", "q6_k": "q6_K", "q5_k": "q5_K"}[fmt]
+    name = {"q4_0": "q4_0", "q4_k": "q4_K", "mxfp4": "mxfp4", "iq2_xxs": "iq2_xxs", "q6_k": "q6_K", "q5_k": "q5_K",
+            "nvfp4": "nvfp4"}[fmt]
     getattr(lib(), f"wo_dequantize_row_{name}")(_ptr(w), _ptr(out), rows * k)
     return out
 
 
 _VEC_DOT = {"q4_0": "q4_0_q8_0", "q4_k": "q4_K_q8_K", "iq2_xxs": "iq2_xxs_q8_K",
-            "mxfp4": "mxfp4_q8_0", "q6_k": "q6_K_q8_K", "q5_k": "q5_K_q8_K"}
+            "mxfp4": "mxfp4_q8_0", "q6_k": "q6_K_q8_K", "q5_k": "q5_K_q8_K", "nvfp4": "nvfp4_q8_0"}
 
 
 def vec_dot(fmt: str, w: np.ndarray, x: np.ndarray, k: int) -> float:

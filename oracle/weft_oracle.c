@@ -40,6 +40,8 @@
 #define IQ2_XXS_BYTES 66
 #define Q6_K_BYTES 210
 #define Q5_K_BYTES 176
+#define QK_NVFP4 64
+#define NVFP4_BYTES 36
 #define GROUP_MAX_EPS 1e-15f
 
 static inline uint32_t f32_bits(float f) {
@@ -1031,6 +1033,123 @@ float wo_vec_dot_q6_K_q8_K(const uint8_t *w, const uint8_t *x, int64_t k) {
 }
 
 /* ------------------------------------------------------------------------
+ * NVFP4: 64-element records, four UE4M3 sub-block scales then 32 bytes of
+ * E2M1 codes; sub-block s holds elements 16 s + j (low nibble of byte
+ * 4 + 8 s + j) and 16 s + 8 + j (high nibble), j < 8.
+ * ---------------------------------------------------------------------- */
+
+/* ggml_ue4m3_to_fp32 (ggml-impl.h:502-515): E4M3 without sign, 0x00 and
+ * 0x7F read as zero, times one half (the E2M1 codebook is doubled). */
+float wo_ue4m3_to_fp32(uint8_t x) {
+  if (x == 0 || x == 0x7F) return 0.0f;
+  const int e = (x >> 3) & 0xF, m = x & 7;
+  const float raw = e == 0 ? ldexpf((float)m, -9) : ldexpf(1.0f + (float)m / 8.0f, e - 7);
+  return raw * 0.5f;
+}
+
+/* ggml_fp32_to_ue4m3 (ggml-impl.h:517-553): clamp to 448, round the
+ * mantissa to 3 bits on the next bit (ties up), subnormals m * 2^-9. */
+uint8_t wo_fp32_to_ue4m3(float x) {
+  if (!(x > 0.0f)) return 0;
+  if (x > 448.0f) x = 448.0f;
+  uint32_t b;
+  memcpy(&b, &x, 4);
+  int e = (int)((b >> 23) & 0xFF) - 127 + 7;
+  if (e <= 0) {
+    int m = (int)(x * 512.0f + 0.5f);
+    if (m > 7) m = 7;
+    return m < 1 ? 0 : (uint8_t)m;
+  }
+  if (e >= 15) return 0x7E;
+  int m = (int)((b >> 20) & 7) + (int)((b >> 19) & 1);
+  if (m > 7) {
+    m = 0;
+    if (++e >= 15) return 0x7E;
+  }
+  return (uint8_t)((e << 3) | m);
+}
+
+void wo_ue4m3_table(float out[256]) {
+  for (int c = 0; c < 256; ++c) out[c] = wo_ue4m3_to_fp32((uint8_t)c);
+}
+
+/* quantize_row_nvfp4_ref (ggml-quants.c:346-378) */
+void wo_quantize_row_nvfp4(const float *x, uint8_t *y, int64_t k) {
+  int8_t kv[16];
+  wo_kvalues_mxfp4(kv);
+  for (int64_t i = 0; i < k / QK_NVFP4; ++i) {
+    uint8_t *rec = y + i * NVFP4_BYTES;
+    for (int s = 0; s < 4; ++s) {
+      const float *xb = x + i * QK_NVFP4 + 16 * s;
+      float amax = 0.f;
+      for (int j = 0; j < 16; ++j)
+        if (amax < fabsf(xb[j])) amax = fabsf(xb[j]);
+      rec[s] = wo_fp32_to_ue4m3(amax / 6.0f);
+      const float d = wo_ue4m3_to_fp32(rec[s]);
+      for (int j = 0; j < 8; ++j) {
+        int best[2];
+        for (int h = 0; h < 2; ++h) {
+          const float v = xb[8 * h + j];
+          int bi = 0;
+          float be = fabsf(kv[0] * d - v);
+          for (int c = 1; c < 16; ++c) {
+            const float err = fabsf(kv[c] * d - v);
+            if (err < be) {
+              bi = c;
+              be = err;
+            }
+          }
+          best[h] = bi;
+        }
+        rec[4 + 8 * s + j] = (uint8_t)(best[0] | (best[1] << 4));
+      }
+    }
+  }
+}
+
+/* dequantize_row_nvfp4 (ggml-quants.c:531-552) */
+void wo_dequantize_row_nvfp4(const uint8_t *x, float *y, int64_t k) {
+  int8_t kv[16];
+  wo_kvalues_mxfp4(kv);
+  for (int64_t i = 0; i < k / QK_NVFP4; ++i) {
+    const uint8_t *rec = x + i * NVFP4_BYTES;
+    for (int s = 0; s < 4; ++s) {
+      const float d = wo_ue4m3_to_fp32(rec[s]);
+      float *yb = y + i * QK_NVFP4 + 16 * s;
+      for (int j = 0; j < 8; ++j) {
+        yb[j] = kv[rec[4 + 8 * s + j] & 0x0F] * d;
+        yb[j + 8] = kv[rec[4 + 8 * s + j] >> 4] * d;
+      }
+    }
+  }
+}
+
+/* ggml_vec_dot_nvfp4_q8_0_generic (ggml-cpu/quants.c:279-313): sub-block s
+ * of record i meets half s % 2 of Q8_0 block 2 i + s / 2. */
+float wo_vec_dot_nvfp4_q8_0(const uint8_t *w, const uint8_t *x, int64_t k) {
+  int8_t kv[16];
+  wo_kvalues_mxfp4(kv);
+  float sumf = 0.f;
+  for (int64_t i = 0; i < k / QK_NVFP4; ++i) {
+    const uint8_t *rec = w + i * NVFP4_BYTES;
+    for (int s = 0; s < 4; ++s) {
+      const uint8_t *xb = x + (2 * i + s / 2) * Q8_0_BYTES;
+      const int8_t *xq = (const int8_t *)(xb + 2) + 16 * (s % 2);
+      const float d = wo_ue4m3_to_fp32(rec[s]);
+      const float dy = wo_fp16_to_fp32(rd16(xb));
+      int lo = 0, hi = 0;
+      for (int j = 0; j < 8; ++j) {
+        const uint8_t q = rec[4 + 8 * s + j];
+        lo += xq[j] * kv[q & 0xF];
+        hi += xq[j + 8] * kv[q >> 4];
+      }
+      sumf += dy * d * (float)(lo + hi);
+    }
+  }
+  return sumf;
+}
+
+/* ------------------------------------------------------------------------
  * MUL_MAT driver and fp64 re-accumulation
  * ---------------------------------------------------------------------- */
 size_t wo_weight_row_bytes(int fmt, int64_t k) {
@@ -1041,12 +1160,13 @@ size_t wo_weight_row_bytes(int fmt, int64_t k) {
   case WO_MXFP4: return (size_t)(k / 32) * MXFP4_BYTES;
   case WO_Q6_K: return (size_t)(k / 256) * Q6_K_BYTES;
   case WO_Q5_K: return (size_t)(k / 256) * Q5_K_BYTES;
+  case WO_NVFP4: return (size_t)(k / QK_NVFP4) * NVFP4_BYTES;
   }
   return 0;
 }
 
 size_t wo_act_row_bytes(int fmt, int64_t k) {
-  if (fmt == WO_Q4_0 || fmt == WO_MXFP4) return (size_t)(k / 32) * Q8_0_BYTES;
+  if (fmt == WO_Q4_0 || fmt == WO_MXFP4 || fmt == WO_NVFP4) return (size_t)(k / 32) * Q8_0_BYTES;
   return (size_t)(k / 256) * Q8_K_BYTES;
 }
 
@@ -1059,6 +1179,7 @@ static vec_dot_fn select_vec_dot(int fmt) {
   case WO_MXFP4: return wo_vec_dot_mxfp4_q8_0;
   case WO_Q6_K: return wo_vec_dot_q6_K_q8_K;
   case WO_Q5_K: return wo_vec_dot_q5_K_q8_K;
+  case WO_NVFP4: return wo_vec_dot_nvfp4_q8_0;
   }
   return 0;
 }
@@ -1085,7 +1206,7 @@ void wo_mul_mat_q(int fmt, const uint8_t *W, const uint8_t *Xq, float *Y, int64_
 void wo_mul_mat(int fmt, const uint8_t *W, const float *X, uint8_t *Xq, float *Y, int64_t N,
                 int64_t K, int64_t M, int nthreads) {
   const size_t xrow = wo_act_row_bytes(fmt, K);
-  const int q80 = (fmt == WO_Q4_0 || fmt == WO_MXFP4);
+  const int q80 = (fmt == WO_Q4_0 || fmt == WO_MXFP4 || fmt == WO_NVFP4);
   if (nthreads <= 0) nthreads = wo_max_threads();
 #pragma omp parallel for num_threads(nthreads) schedule(static)
   for (int64_t m = 0; m < M; ++m) {
@@ -1115,6 +1236,22 @@ int64_t wo_int_partials(int fmt, const uint8_t *w, const uint8_t *x, int64_t k, 
         s += v0 * xq[j] + v1 * xq[j + 16];
       }
       out[n++] = s;
+    }
+  } else if (fmt == WO_NVFP4) {
+    /* one int32 per 16-element sub-block */
+    int8_t kv[16];
+    wo_kvalues_mxfp4(kv);
+    for (int64_t i = 0; i < k / QK_NVFP4; ++i) {
+      const uint8_t *rec = w + i * NVFP4_BYTES;
+      for (int s = 0; s < 4; ++s) {
+        const int8_t *xq = (const int8_t *)(x + (2 * i + s / 2) * Q8_0_BYTES + 2) + 16 * (s % 2);
+        int32_t p = 0;
+        for (int j = 0; j < 8; ++j) {
+          const uint8_t q = rec[4 + 8 * s + j];
+          p += xq[j] * kv[q & 0xF] + xq[j + 8] * kv[q >> 4];
+        }
+        out[n++] = p;
+      }
     }
   } else if (fmt == WO_Q4_K || fmt == WO_Q5_K) {
     const int64_t nb = k / QK_K;
@@ -1197,6 +1334,17 @@ void wo_mul_mat_f64(int fmt, const uint8_t *W, const uint8_t *Xq, double *E, dou
             const double dx = wo_fp16_to_fp32(rd16(x + (nbase + b) * Q8_0_BYTES));
             const double dw = fmt == WO_Q4_0 ? wo_fp16_to_fp32(rd16(wr)) : wo_e8m0_to_fp32_half(wr[0]);
             const double t = dw * dx * parts[b];
+            e += t;
+            a += fabs(t);
+          }
+        }
+      } else if (fmt == WO_NVFP4) {
+        for (int64_t i = 0; i < K / QK_NVFP4; ++i) {
+          const uint8_t *wr = w + i * NVFP4_BYTES;
+          wo_int_partials(fmt, wr, x + 2 * i * Q8_0_BYTES, QK_NVFP4, parts);
+          for (int s = 0; s < 4; ++s) {
+            const double dy = wo_fp16_to_fp32(rd16(x + (2 * i + s / 2) * Q8_0_BYTES));
+            const double t = (double)wo_ue4m3_to_fp32(wr[s]) * dy * parts[s];
             e += t;
             a += fabs(t);
           }

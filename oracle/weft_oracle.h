@@ -11,6 +11,7 @@
  * Record layouts (bytes, little endian), ggml-common.h:
  *   Q4_0    18 B / 32  : f16 d | u8 qs[16]                       (:184-189)
  *   MXFP4   17 B / 32  : u8 e  | u8 qs[16]                       (:204-209)
+ *   NVFP4   36 B / 64  : u8 d[4] (UE4M3) | u8 qs[32]            (:211-217)
  *   Q8_0    34 B / 32  : f16 d | i8 qs[32]                       (:241-246)
  *   Q4_K   144 B / 256 : f16 d | f16 dmin | u8 scales[12] | u8 qs[128]  (:317-328)
  *   Q8_K   292 B / 256 : f32 d | i8 qs[256] | i16 bsums[16]      (:361-366)
@@ -33,6 +34,7 @@ enum wo_format {
   WO_MXFP4 = 3,
   WO_Q6_K = 4,
   WO_Q5_K = 5,
+  WO_NVFP4 = 6,
 };
 
 /* scalar conversions (ggml-impl.h:384-431, :477-495) */
@@ -48,6 +50,9 @@ void wo_ksigns_iq2xs(uint8_t out[128]);  /* i | parity(i) << 7 */
 void wo_signs_i8x8(int8_t out[1024]);    /* 128 x 8 of +-1, the ABI's I8X8 sign table */
 void wo_kvalues_mxfp4(int8_t out[16]);   /* doubled e2m1 */
 void wo_e8m0_half_table(float out[256]);
+float wo_ue4m3_to_fp32(uint8_t x);       /* ggml_ue4m3_to_fp32, incl. the 1/2 */
+uint8_t wo_fp32_to_ue4m3(float x);
+void wo_ue4m3_table(float out[256]);
 
 /* weight quantizers (host-side input generators) */
 void wo_quantize_row_q4_0(const float *x, uint8_t *y, int64_t k);
@@ -56,6 +61,7 @@ void wo_quantize_row_mxfp4(const float *x, uint8_t *y, int64_t k);
 void wo_quantize_row_iq2_xxs(const float *x, uint8_t *y, int64_t k);
 void wo_quantize_row_q6_K(const float *x, uint8_t *y, int64_t k);
 void wo_quantize_row_q5_K(const float *x, uint8_t *y, int64_t k);
+void wo_quantize_row_nvfp4(const float *x, uint8_t *y, int64_t k);
 
 /* activation quantizers (on the hot path) */
 void wo_quantize_row_q8_0(const float *x, uint8_t *y, int64_t k);
@@ -68,6 +74,7 @@ void wo_dequantize_row_iq2_xxs(const uint8_t *x, float *y, int64_t k);
 void wo_dequantize_row_mxfp4(const uint8_t *x, float *y, int64_t k);
 void wo_dequantize_row_q6_K(const uint8_t *x, float *y, int64_t k);
 void wo_dequantize_row_q5_K(const uint8_t *x, float *y, int64_t k);
+void wo_dequantize_row_nvfp4(const uint8_t *x, float *y, int64_t k);
 
 /* generic vec_dots: w row (k elements) . quantized activation row */
 float wo_vec_dot_q4_0_q8_0(const uint8_t *w, const uint8_t *x, int64_t k);
@@ -76,6 +83,7 @@ float wo_vec_dot_iq2_xxs_q8_K(const uint8_t *w, const uint8_t *x, int64_t k);
 float wo_vec_dot_mxfp4_q8_0(const uint8_t *w, const uint8_t *x, int64_t k);
 float wo_vec_dot_q6_K_q8_K(const uint8_t *w, const uint8_t *x, int64_t k);
 float wo_vec_dot_q5_K_q8_K(const uint8_t *w, const uint8_t *x, int64_t k);
+float wo_vec_dot_nvfp4_q8_0(const uint8_t *w, const uint8_t *x, int64_t k);
 
 /* Bytes of one encoded row of k elements for a weight format, or of the
  * activation format that pairs with it (Q8_0 for Q4_0/MXFP4, Q8_K else). */

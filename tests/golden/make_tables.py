@@ -42,7 +42,8 @@ def main() -> int:
         "kvalues_mxfp4": table(common, "kvalues_mxfp4"),
         "record_size_asserts": {k: asserts[k].strip() for k in
                                 ("block_q4_0", "block_mxfp4", "block_q8_0", "block_q4_K",
-                                 "block_q8_K", "block_iq2_xxs", "block_q6_K", "block_q5_K") if k in asserts},
+                                 "block_q8_K", "block_iq2_xxs", "block_q6_K", "block_q5_K", "block_nvfp4")
+                                 if k in asserts},
     }
     OUT.write_text(json.dumps(out, indent=1) + "\n")
     print(f"wrote {OUT}")

@@ -94,7 +94,8 @@ def test_record_sizes_match_ggml_static_asserts():
     # sizeof expressions of ggml-common.h evaluated with QK4_0 = QK8_0 =
     # QK_MXFP4 = 32, QK_K = 256, K_SCALE_SIZE = 12, ggml_half = 2 bytes
     env = {"ggml_half": 2, "uint8_t": 1, "int16_t": 2, "uint16_t": 2, "float": 4,
-           "QK4_0": 32, "QK8_0": 32, "QK_MXFP4": 32, "QK_K": 256, "K_SCALE_SIZE": 12}
+           "QK4_0": 32, "QK8_0": 32, "QK_MXFP4": 32, "QK_K": 256, "K_SCALE_SIZE": 12,
+           "QK_NVFP4_SUB": 16, "QK_NVFP4": 64}
     sizes = {}
     for k, expr in GOLDEN["record_size_asserts"].items():
         e = expr.replace("sizeof", "")
@@ -102,9 +103,11 @@ def test_record_sizes_match_ggml_static_asserts():
             e = e.replace(name, str(env[name]))
         sizes[k] = eval(e, {"__builtins__": {}})  # arithmetic on literals only
     assert sizes == {"block_q4_0": 18, "block_mxfp4": 17, "block_q8_0": 34, "block_q4_K": 144,
-                     "block_q8_K": 292, "block_iq2_xxs": 66, "block_q6_K": 210, "block_q5_K": 176}
+                     "block_q8_K": 292, "block_iq2_xxs": 66, "block_q6_K": 210, "block_q5_K": 176,
+                     "block_nvfp4": 36}
     assert {k: o.RECORD[k][1] for k in o.RECORD} == {
-        "q4_0": 18, "mxfp4": 17, "q8_0": 34, "q4_k": 144, "q8_k": 292, "iq2_xxs": 66, "q6_k": 210, "q5_k": 176}
+        "q4_0": 18, "mxfp4": 17, "q8_0": 34, "q4_k": 144, "q8_k": 292, "iq2_xxs": 66, "q6_k": 210, "q5_k": 176,
+        "nvfp4": 36}
 
 
 # ------------------------------------------------------------ dequantizers
@@ -263,6 +266,111 @@ def test_dequant_mxfp4_brute_force():
     assert np.array_equal(o.dequantize("mxfp4", w, 32), np.array(want, np.float32))
 
 
+def _ue4m3_closed_form(c: int) -> float:
+    """UE4M3 from the E4M3 bit fields (exponent bias 7, 3 mantissa bits,
+    subnormals m * 2^-9), the sign bit ignored, times 1/2; 0x7F is zero."""
+    if c & 0x7F in (0, 0x7F):
+        return 0.0 if c != 0xFF else 0.5 * math.ldexp(1.875, 8)
+    e, m = (c >> 3) & 0xF, c & 7
+    return 0.5 * (math.ldexp(m, -9) if e == 0 else math.ldexp(1 + m / 8, e - 7))
+
+
+def test_ue4m3_decode_matches_e4m3():
+    import torch
+    tab = o.ue4m3_table()
+    e4m3 = torch.arange(0, 127, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+    # the torch E4M3FN decode for every finite positive code, halved
+    assert np.array_equal(tab[:127], (0.5 * e4m3).astype(np.float32))
+    assert tab[0x7F] == 0.0
+    assert [float(tab[c]) for c in range(256)] == [_ue4m3_closed_form(c) for c in range(256)]
+
+
+def test_ue4m3_encode_rounds_to_nearest_ties_up():
+    # GGML's encoder returns 0x7E (448) for any result in exponent 15, so the
+    # candidates are codes 1..0x77 plus 256 (code 0x78), which stands for 0x7E
+    raw = 2.0 * o.ue4m3_table()[1:0x79].astype(np.float64)   # codes 1..0x78, increasing
+    assert (np.diff(raw) > 0).all() and raw[-1] == 256.0
+    for c in range(1, 0x78):                                    # exact values round-trip
+        assert o.lib().wo_fp32_to_ue4m3(float(raw[c - 1])) == c
+    rng = np.random.default_rng(5)
+    xs = np.concatenate([np.exp(rng.uniform(np.log(1e-4), np.log(600.0), 4000)),
+                         (raw[:-1] + raw[1:]) / 2])             # every midpoint: ties go up
+    for x in xs.astype(np.float32):
+        x = float(x)
+        if 7.5 * 2.0 ** -9 <= x < 2.0 ** -6:
+            want = 7      # GGML's subnormal path caps m at 7 below the first normal
+        elif x >= 256.0:
+            want = 0x7E   # exponent 15: saturated
+        elif x < 0.5 * 2.0 ** -9:
+            want = 0
+        else:
+            err = np.abs(raw - x)
+            best = np.flatnonzero(err == err.min())
+            want = int(best[-1]) + 1
+            want = 0x7E if want == 0x78 else want
+        assert o.lib().wo_fp32_to_ue4m3(x) == want, x
+    assert o.lib().wo_fp32_to_ue4m3(0.0) == 0 and o.lib().wo_fp32_to_ue4m3(-1.0) == 0
+
+
+def test_dequant_nvfp4_brute_force():
+    # Weft NVFP4 (examples/formats/ggml.py:259-263): d u8[4], q u4[64]
+    # grouped(16) then bit_layers(8, lo_first): element e of sub-block s = e // 16,
+    # i = e % 16 sits in byte 4 + 8 s + i % 8, nibble i // 8; value kv[q] * ue4m3(d[s])
+    kv = GOLDEN["kvalues_mxfp4"]
+    rng = np.random.default_rng(13)
+    recs, want = [], []
+    for trial in range(300):
+        d = [int(v) for v in rng.integers(0, 256, 4)] if trial >= 64 else [(trial + 61 * s) % 256 for s in range(4)]
+        codes = [(trial + 7 * e) % 16 for e in range(64)]
+        b = bytearray(36)
+        b[0:4] = bytes(d)
+        for e, c in enumerate(codes):
+            s, i = divmod(e, 16)
+            b[4 + 8 * s + i % 8] |= c << (4 * (i // 8))
+        recs.append(bytes(b))
+        want.append([np.float32(kv[c] * _ue4m3_closed_form(d[e // 16])) for e, c in enumerate(codes)])
+    w = np.frombuffer(b"".join(recs), np.uint8).reshape(len(recs), 36)
+    assert np.array_equal(o.dequantize("nvfp4", w, 64).view(np.uint32), np.array(want, np.float32).view(np.uint32))
+
+
+def test_nvfp4_quantizer_picks_scale_and_nearest_codes():
+    kv = np.array(GOLDEN["kvalues_mxfp4"], np.float64)
+    x = o.seeded_normal(41, (8, 256), 0.02)
+    q = o.quantize("nvfp4", x).reshape(-1, 36)
+    xs = x.reshape(-1, 4, 16)
+    tab = o.ue4m3_table()
+    for r in range(q.shape[0]):
+        for s in range(4):
+            amax = np.float32(np.abs(xs[r, s]).max())
+            assert q[r, s] == o.lib().wo_fp32_to_ue4m3(float(np.float32(amax / np.float32(6.0))))
+            d = np.float32(tab[q[r, s]])
+            for i in range(16):
+                c = (q[r, 4 + 8 * s + i % 8] >> (4 * (i // 8))) & 0xF
+                err = np.abs((kv * d).astype(np.float32) - xs[r, s, i]).astype(np.float32)
+                assert c == int(np.argmin(err))   # first index among equal errors
+
+
+def test_int_partials_nvfp4_are_the_sub_block_dots():
+    k = 256
+    w = o.quantize("nvfp4", o.seeded_normal(42, (1, k), 0.02))
+    xq = o.quantize("q8_0", o.seeded_normal(43, (1, k)))
+    parts = np.zeros(k // 16, np.int32)
+    n = o.lib().wo_int_partials(o.NVFP4, o._ptr(w[0]), o._ptr(xq[0]), k, o._ptr(parts))
+    assert n == k // 16
+    kv = np.array(GOLDEN["kvalues_mxfp4"], np.int64)
+    tab = o.ue4m3_table()
+    codes = np.round(o.dequantize("nvfp4", w, k)[0].astype(np.float64) /
+                     np.repeat(tab[w[0].reshape(-1, 36)[:, :4].reshape(-1)], 16).astype(np.float64)
+                     .clip(min=1e-30))
+    xv = xq[0].reshape(-1, 34)[:, 2:].view(np.int8).reshape(-1).astype(np.int64)
+    scales = np.repeat(tab[w[0].reshape(-1, 36)[:, :4].reshape(-1)], 16)
+    codes = np.where(scales == 0, 0, codes).astype(np.int64)
+    assert set(np.unique(codes)) <= set(kv.tolist())
+    want = [int((codes[16 * g:16 * g + 16] * xv[16 * g:16 * g + 16]).sum()) for g in range(k // 16)]
+    got = [int(p) if tab[w[0].reshape(-1, 36)[g // 4, g % 4]] != 0 else 0 for g, p in enumerate(parts)]
+    assert got == want
+
+
 def test_dequant_iq2_xxs_brute_force():
     # examples/kernels/dequantize/iq2_xxs.py: per 32-group g, word pair
     # q[4g..4g+3]: metadata = q[4g+2] | q[4g+3] << 16; scale = d*(0.5 +
@@ -363,7 +471,7 @@ def _dequant_act(act, xq, k):
     return (q * d).reshape(xq.shape[0], k)
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "iq2_xxs", "mxfp4", "q6_k", "q5_k"])
+@pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "iq2_xxs", "mxfp4", "q6_k", "q5_k", "nvfp4"])
 def test_mul_mat_against_independent_float64_path(fmt):
     n, k, m = 48, 2048, 3
     w = o.quantize(fmt, o.seeded_normal(31, (n, k), 0.02))
@@ -430,7 +538,7 @@ def test_int_partials_q6_k_are_the_group_dots():
 
 # ------------------------------------------------ weight quantizers (inputs)
 @pytest.mark.parametrize("fmt,bound", [("q4_0", 0.10), ("q4_k", 0.09), ("mxfp4", 0.13), ("iq2_xxs", 0.45),
-                                       ("q6_k", 0.05), ("q5_k", 0.05)])
+                                       ("q6_k", 0.05), ("q5_k", 0.05), ("nvfp4", 0.11)])
 def test_weight_quantizer_round_trip(fmt, bound):
     w = o.seeded_normal(51, (32, 4096), 0.02)
     d = o.dequantize(fmt, o.quantize(fmt, w), 4096)
