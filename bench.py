@@ -66,6 +66,8 @@ CASES = {
     "q6_k_prefill": ("production_mul_mat_q6_k", "q6_k", 4096, 4096, 512, "mfma"),
     # adjacent format Q5_K (ggml-common.h:330-345), decode at the W_up shape
     "q5_k_decode": ("production_mul_mat_q5_k_decode", "q5_k", 11008, 4096, 1, "hbm"),
+    # adjacent format NVFP4 (ggml-common.h:211-217) at the W_up shape
+    "nvfp4_decode": ("production_mul_mat_nvfp4_decode", "nvfp4", 11008, 4096, 1, "hbm"),
     # GGML MUL_MAT_ID (MoE) prefill at a Mixtral-8x7B FFN shape: 8 experts of
     # 14336 x 4096 Q4_K, 2 experts per token, 512 tokens (the grouped GEMM)
     "q4_k_moe_prefill": ("weft_ggml_mul_mat_id", "q4_k", 14336, 4096, 512, "mfma"),
@@ -121,6 +123,7 @@ class Bench:
         self.tables = {
             "iq2_xxs": [self.dev_copy(o.iq2xxs_grid().view(np.int8)), self.dev_copy(o.signs_i8x8())],
             "mxfp4": [self.dev_copy(o.kvalues_mxfp4()), self.dev_copy(o.e8m0_half_table())],
+            "nvfp4": [self.dev_copy(o.kvalues_mxfp4()), self.dev_copy(o.ue4m3_table())],
         }
 
     def dev_copy(self, a: np.ndarray):

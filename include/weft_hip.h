@@ -73,6 +73,9 @@ void row_dequantize_mxfp4(const uint8_t *W, const int8_t *codebook, const float 
                           size_t K);
 /* examples/kernels/dequantize/q6_k.py:8-15; row_dequantize_runtime.cpp:222 */
 void row_dequantize_q6_k(const uint8_t *W, float *Y, size_t K);
+/* examples/kernels/dequantize/nvfp4.py:9-24; row_dequantize_runtime.cpp:287 */
+void row_dequantize_nvfp4(const uint8_t *W, const int8_t *codebook, const float *scale, float *Y,
+                          size_t K);
 /* examples/kernels/dequantize/q5_k.py:9-15; row_dequantize_runtime.cpp:217 */
 void row_dequantize_q5_k(const uint8_t *W, float *Y, size_t K);
 
@@ -95,6 +98,9 @@ void quantized_vec_dot_mxfp4_q8_0(const uint8_t *W, const uint8_t *X, const int8
                                   const float *scale, float *Y, size_t K);
 /* examples/kernels/vec_dot/q6_k_q8_k.py:8-44; vec_dot_runtime.cpp:263 */
 void quantized_vec_dot_q6_k_q8_k(const uint8_t *W, const uint8_t *X, float *Y, size_t K);
+/* examples/kernels/vec_dot/nvfp4_q8_0.py:9-38; vec_dot_runtime.cpp:367 */
+void quantized_vec_dot_nvfp4_q8_0(const uint8_t *W, const uint8_t *X, const int8_t *codebook,
+                                  const float *scale, float *Y, size_t K);
 /* examples/kernels/vec_dot/q5_k_q8_k.py:8-38; vec_dot_runtime.cpp:255 */
 void quantized_vec_dot_q5_k_q8_k(const uint8_t *W, const uint8_t *X, float *Y, size_t K);
 
@@ -141,6 +147,13 @@ void production_mul_mat_q6_k(const uint8_t *W, const float *X, uint8_t *Xq, floa
 /* examples/kernels/mul_mat/q6_k_decode.py:10-20; mul_mat_runtime.cpp:383 */
 void production_mul_mat_q6_k_decode(const uint8_t *W, const float *X, uint8_t *Xq, float *Y,
                                     size_t N, size_t K, size_t M);
+/* examples/kernels/mul_mat/nvfp4.py:10-43; mul_mat_runtime.cpp:582 */
+void production_mul_mat_nvfp4(const uint8_t *W, const float *X, uint8_t *Xq, const int8_t *codebook,
+                              const float *scale, float *Y, size_t N, size_t K, size_t M);
+/* examples/kernels/mul_mat/nvfp4_decode.py:10-23; mul_mat_runtime.cpp:579 */
+void production_mul_mat_nvfp4_decode(const uint8_t *W, const float *X, uint8_t *Xq,
+                                     const int8_t *codebook, const float *scale, float *Y,
+                                     size_t N, size_t K, size_t M);
 /* examples/kernels/mul_mat/q5_k.py:9-37; mul_mat_runtime.cpp:371 */
 void production_mul_mat_q5_k(const uint8_t *W, const float *X, uint8_t *Xq, float *Y, size_t N,
                              size_t K, size_t M);
@@ -177,7 +190,7 @@ void q4_k_q8_k_gemv_contract(const uint8_t *W, const uint8_t *X, float *Y, size_
 /* The quantized mul_mat behind GGML's MUL_MAT op, for a ggml-style graph
  * executor: ggml_compute_forward_mul_mat's contract
  * (source/c/ggml/llama.cpp/ggml/src/ggml-cpu/ggml-cpu.c:1245-1443) with
- * src0 of type Q4_0, Q4_K, Q5_K, Q6_K, IQ2_XXS or MXFP4, src1 F32 (quantized into wdata
+ * src0 of type Q4_0, Q4_K, Q5_K, Q6_K, IQ2_XXS, MXFP4 or NVFP4, src1 F32 (quantized into wdata
  * as GGML does) or already of src0's vec_dot type, dst F32; GGML's byte
  * strides and broadcast of src0 over src1's planes (ne12 / ne02, ne13 / ne03).
  * All data pointers are device pointers; the call is stream-ordered.
@@ -195,7 +208,8 @@ enum {
   WEFT_GGML_TYPE_Q6_K = 14,
   WEFT_GGML_TYPE_Q8_K = 15,
   WEFT_GGML_TYPE_IQ2_XXS = 16,
-  WEFT_GGML_TYPE_MXFP4 = 39
+  WEFT_GGML_TYPE_MXFP4 = 39,
+  WEFT_GGML_TYPE_NVFP4 = 40
 };
 
 /* the fields of struct ggml_tensor (ggml/include/ggml.h:667-692) MUL_MAT reads */

@@ -29,6 +29,7 @@ class Harness:
         self.signs_i8x8 = self.to_dev(o.signs_i8x8())
         self.codebook = self.to_dev(o.kvalues_mxfp4())
         self.scale = self.to_dev(o.e8m0_half_table())
+        self.ue4m3 = self.to_dev(o.ue4m3_table())
 
     # ------------------------------------------------------------ memory
     def to_dev(self, a: np.ndarray, offset: int = 0):

@@ -14,7 +14,8 @@ INVALID, NOT_SUPPORTED = 1, 801  # hipErrorInvalidValue, hipErrorNotSupported
 # ggml.c type_traits: (blck_size, type_size); ggml-cpu.c type_traits_cpu vec_dot_type
 TRAITS = {G.F32: (1, 4, -1), G.Q4_0: (32, 18, G.Q8_0), G.Q8_0: (32, 34, -1),
           G.Q4_K: (256, 144, G.Q8_K), G.Q8_K: (256, 292, -1), G.IQ2_XXS: (256, 66, G.Q8_K),
-          G.MXFP4: (32, 17, G.Q8_0), G.Q6_K: (256, 210, G.Q8_K), G.Q5_K: (256, 176, G.Q8_K)}
+          G.MXFP4: (32, 17, G.Q8_0), G.Q6_K: (256, 210, G.Q8_K), G.Q5_K: (256, 176, G.Q8_K),
+          G.NVFP4: (64, 36, G.Q8_0)}
 
 
 def test_type_traits_follow_ggml():
@@ -22,7 +23,7 @@ def test_type_traits_follow_ggml():
         assert (G.blck_size(t), G.type_size(t), G.vec_dot_type(t)) == (blck, size, vdt)
         assert G.row_size(t, 4096) == size * 4096 // blck
     assert G.row_size(G.Q4_K, 100) == 0  # not whole blocks (ggml_row_size asserts)
-    for other in (1, 3, 11, 40, 99):  # F16, Q4_1, Q3_K, NVFP4, unknown
+    for other in (1, 3, 11, 41, 99):  # F16, Q4_1, Q3_K, past the enum, unknown
         assert (G.type_size(other), G.blck_size(other), G.vec_dot_type(other)) == (0, 0, -1)
 
 

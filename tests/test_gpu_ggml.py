@@ -20,9 +20,9 @@ from weft_amd import ggml as G
 pytestmark = pytest.mark.gpu
 
 TYPE = {"q4_0": G.Q4_0, "q4_k": G.Q4_K, "iq2_xxs": G.IQ2_XXS, "mxfp4": G.MXFP4, "q6_k": G.Q6_K,
-        "q5_k": G.Q5_K}
+        "q5_k": G.Q5_K, "nvfp4": G.NVFP4}
 VDT = {"q4_0": G.Q8_0, "mxfp4": G.Q8_0, "q4_k": G.Q8_K, "iq2_xxs": G.Q8_K, "q6_k": G.Q8_K,
-       "q5_k": G.Q8_K}
+       "q5_k": G.Q8_K, "nvfp4": G.Q8_0}
 FMTS = list(TYPE)
 NAN = 0x7FC00001  # a quiet NaN the kernels never produce
 
@@ -102,7 +102,7 @@ def test_padded_rows(hip, fmt, m):
 def test_unaligned_row_pads(hip, fmt, m):
     # a 2-byte (1-byte for MXFP4) weight-row pad: rows keep only the Encoding
     # alignment, so the GEMV kernels take every size
-    run(hip, fmt, 512, 96, m, pad_w=1 if fmt in ("mxfp4", "q6_k") else 2, pad_x=1, pad_y=3)
+    run(hip, fmt, 512, 96, m, pad_w=1 if fmt in ("mxfp4", "q6_k", "nvfp4") else 2, pad_x=1, pad_y=3)
 
 
 @pytest.mark.parametrize("fmt", FMTS)
@@ -193,7 +193,7 @@ def test_mul_mat_id_tokens_and_invalid_ids(hip, fmt):
 @pytest.mark.parametrize("fmt", FMTS)
 def test_mul_mat_id_prequantized_and_strided(hip, fmt):
     ids = np.array([[1, 3, 0], [2, 2, 1]])
-    run_id(hip, fmt, 512, 64, 4, 3, 1, 2, ids, pad_w=1 if fmt in ("mxfp4", "q6_k") else 2, prequant=True)
+    run_id(hip, fmt, 512, 64, 4, 3, 1, 2, ids, pad_w=1 if fmt in ("mxfp4", "q6_k", "nvfp4") else 2, prequant=True)
 
 
 @pytest.mark.parametrize("fmt", FMTS)

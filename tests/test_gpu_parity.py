@@ -40,6 +40,8 @@ def tables(hip, fmt):
         return [hip.grid_i8x8, hip.signs_i8x8]
     if fmt == "mxfp4":
         return [hip.codebook, hip.scale]
+    if fmt == "nvfp4":
+        return [hip.codebook, hip.ue4m3]
     return []
 
 

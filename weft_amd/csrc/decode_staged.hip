@@ -9,6 +9,7 @@
 //   IQ2_XXS :855-895  y = 0.125 * sum_B dw * dx * sum_g (2 s_g + 1) *
 //                         sum_32 grid[idx] * sign * x
 //   Q6_K    :800-853  y = sum_B dw * dx * sum_g sc_g * sum_16 (q - 32) * x
+//   NVFP4   ggml-cpu/quants.c:279-313  y = sum_B sum_s dx * ue4m3(d_s) * sum_16 kv[q] * x
 //   Q5_K    :720-798  y = sum_B dx * (dw * sum_s sc_s * sum_32 q * x
 //                                    - dmin * sum_s m_s * bsum_s)
 // and the Weft kernels examples/kernels/mul_mat/{q4_0_decode,mxfp4_decode,
@@ -45,7 +46,7 @@ constexpr int kMaxRowsPerPass = 4;
 // 2.3 KB windows held Q5_K / Q6_K near 2.3-2.7 TB/s.
 constexpr int kWindow = 4608 + 32;
 
-enum class Fmt { Q4_0, MXFP4, IQ2_XXS, Q6_K, Q5_K };
+enum class Fmt { Q4_0, MXFP4, IQ2_XXS, Q6_K, Q5_K, NVFP4 };
 
 template <Fmt F>
 struct Traits;
@@ -68,6 +69,11 @@ template <>
 struct Traits<Fmt::Q6_K> {
   static constexpr int kElems = 256, kBytes = 210, kSegRecords = 16, kItemsPerRecord = 8;
   static constexpr bool kQ8K = true;
+};
+template <>
+struct Traits<Fmt::NVFP4> {
+  static constexpr int kElems = 64, kBytes = 36, kSegRecords = 128, kItemsPerRecord = 1;
+  static constexpr bool kQ8K = false;
 };
 template <>
 struct Traits<Fmt::Q5_K> {
@@ -206,7 +212,7 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
     for (int i = threadIdx.x; i < 256; i += blockDim.x)
       reinterpret_cast<uint32_t*>(tables + 2048)[i] =
           reinterpret_cast<const uint32_t*>(a.tab1)[i];
-  } else if constexpr (F == Fmt::MXFP4) {
+  } else if constexpr (F == Fmt::MXFP4 || F == Fmt::NVFP4) {
     for (int i = threadIdx.x; i < 256; i += blockDim.x)
       reinterpret_cast<float*>(tables)[i] = reinterpret_cast<const float*>(a.tab1)[i];
   }
@@ -251,7 +257,7 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
   __syncthreads();
 
   uint32_t c0 = 0, c1 = 0, c2 = 0, c3 = 0;
-  if constexpr (F == Fmt::MXFP4) {
+  if constexpr (F == Fmt::MXFP4 || F == Fmt::NVFP4) {
     // int8[16] codebook, any alignment: four little-endian words
     const uint8_t* cb = reinterpret_cast<const uint8_t*>(a.tab0);
     c0 = ld_u32_a1(cb);
@@ -320,6 +326,37 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
             s = dot4(hi2, xh.z, s);
             s = dot4(hi3, xh.w, s);
             acc[m] += (float)s * wscale * v.d[gb];
+          }
+        } else if constexpr (F == Fmt::NVFP4) {
+          if (!valid) continue;
+          // item = one 64-element record: sub-block s (16 elements) is the low
+          // then high nibbles of qs words 2 s, 2 s + 1 and meets half s % 2 of
+          // Q8_0 block 2 gb + s / 2
+          const int gb = r0 + it;
+          const int o = off0 + T::kBytes * it;
+          // one sub-block at a time: its two words decoded, then every row
+          // (decoding all eight words up front spilled at 128 VGPRs)
+          const uint32_t sw = lds_u32(win, o);
+          const float* tab = reinterpret_cast<const float*>(tables);
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            uint32_t q[2];
+            lds_run(win, o + 4 + 8 * s, q);
+            const int lo0 = lookup16(q[0], c0, c1, c2, c3), lo1 = lookup16(q[1], c0, c1, c2, c3);
+            const int hi0 = lookup16(q[0] >> 4, c0, c1, c2, c3), hi1 = lookup16(q[1] >> 4, c0, c1, c2, c3);
+            const float ws = tab[(sw >> (8 * s)) & 0xffu];
+            const int xb = 2 * gb + s / 2;
+#pragma unroll
+            for (int m = 0; m < kMaxRowsPerPass; ++m) {
+              if (m >= a.mb) break;
+              const Q80View v = q80_view(act, K, m);
+              const int4 x = *reinterpret_cast<const int4*>(v.qs + 32 * xb + 16 * (s % 2));
+              int p = dot4(lo0, x.x, 0);
+              p = dot4(lo1, x.y, p);
+              p = dot4(hi0, x.z, p);
+              p = dot4(hi1, x.w, p);
+              acc[m] += v.d[xb] * ws * (float)p;
+            }
           }
         } else if constexpr (F == Fmt::Q5_K) {
           // item = (superblock, 32-element sub-block s): the nibble half s % 2
@@ -465,14 +502,14 @@ void launch(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_
   if (pr != nullptr) M = 1;  // one activation row per pair
   if (N == 0 || M == 0 || K == 0 || (pr != nullptr && n_pairs <= 0)) return;
   const size_t act_align = T::kQ8K ? 4 : 2;
-  const size_t w_align = F == Fmt::MXFP4 || F == Fmt::Q6_K ? 1 : 2;
+  const size_t w_align = F == Fmt::MXFP4 || F == Fmt::Q6_K || F == Fmt::NVFP4 ? 1 : 2;
   if (K % T::kElems != 0 || W == nullptr || Y == nullptr || (X == nullptr && xq_in == nullptr) ||
       N > (size_t)INT32_MAX || K > (size_t)INT32_MAX || M > (size_t)INT32_MAX ||
       !aligned(W, w_align) || !aligned(Y, 4) || (X && !aligned(X, 4)) ||
       (xq_in && !aligned(xq_in, act_align)) || (xq_out && !aligned(xq_out, act_align)) ||
-      ((F == Fmt::MXFP4 || F == Fmt::IQ2_XXS) && (tab0 == nullptr || tab1 == nullptr)) ||
+      ((F == Fmt::MXFP4 || F == Fmt::NVFP4 || F == Fmt::IQ2_XXS) && (tab0 == nullptr || tab1 == nullptr)) ||
       (F == Fmt::IQ2_XXS && (!aligned(tab0, 4) || !aligned(tab1, 4))) ||
-      (F == Fmt::MXFP4 && !aligned(tab1, 4)) ||
+      ((F == Fmt::MXFP4 || F == Fmt::NVFP4) && !aligned(tab1, 4)) ||
       !strides_ok(st, K / T::kElems * T::kBytes, w_align, K, N, N, M) ||
       (pr != nullptr && pr->w_es % (long long)w_align != 0)) {
     set_error(hipErrorInvalidValue);
@@ -547,6 +584,7 @@ void decode_pairs(int fmt, const uint8_t* W, const float* X, const uint8_t* xq_i
     case 1: return launch<Fmt::MXFP4>(W, X, xq_in, xq_out, tab0, tab1, Y, N, K, 1, st, &pr, n_pairs);
     case 3: return launch<Fmt::Q6_K>(W, X, xq_in, xq_out, nullptr, nullptr, Y, N, K, 1, st, &pr, n_pairs);
     case 4: return launch<Fmt::Q5_K>(W, X, xq_in, xq_out, nullptr, nullptr, Y, N, K, 1, st, &pr, n_pairs);
+    case 5: return launch<Fmt::NVFP4>(W, X, xq_in, xq_out, tab0, tab1, Y, N, K, 1, st, &pr, n_pairs);
     default: return launch<Fmt::IQ2_XXS>(W, X, xq_in, xq_out, tab0, tab1, Y, N, K, 1, st, &pr, n_pairs);
   }
 }
@@ -561,6 +599,11 @@ void decode_q5_k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t
   launch<Fmt::Q5_K>(W, X, nullptr, Xq, nullptr, nullptr, Y, N, K, M, st);
 }
 
+void decode_nvfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
+                  const float* scale, float* Y, size_t N, size_t K, size_t M, const RowStrides& st) {
+  launch<Fmt::NVFP4>(W, X, nullptr, Xq, codebook, scale, Y, N, K, M, st);
+}
+
 void decode_quantized(int fmt, const uint8_t* W, const uint8_t* Xq, const int8_t* tab0,
                       const void* tab1, float* Y, size_t N, size_t K, size_t M,
                       const RowStrides& st) {
@@ -569,6 +612,7 @@ void decode_quantized(int fmt, const uint8_t* W, const uint8_t* Xq, const int8_t
     case 1: return launch<Fmt::MXFP4>(W, nullptr, Xq, nullptr, tab0, tab1, Y, N, K, M, st);
     case 3: return launch<Fmt::Q6_K>(W, nullptr, Xq, nullptr, nullptr, nullptr, Y, N, K, M, st);
     case 4: return launch<Fmt::Q5_K>(W, nullptr, Xq, nullptr, nullptr, nullptr, Y, N, K, M, st);
+    case 5: return launch<Fmt::NVFP4>(W, nullptr, Xq, nullptr, tab0, tab1, Y, N, K, M, st);
     default: return launch<Fmt::IQ2_XXS>(W, nullptr, Xq, nullptr, tab0, tab1, Y, N, K, M, st);
   }
 }
@@ -622,6 +666,27 @@ void production_mul_mat_q6_k(const uint8_t* W, const float* X, uint8_t* Xq, floa
                              size_t K, size_t M) {
   if (X == nullptr || Xq == nullptr) return weft::set_error(hipErrorInvalidValue);
   weft::decode_q6_k(W, X, Xq, Y, N, K, M, weft::packed(K / 256 * weft::kQ6_KBytes, K, N));
+}
+
+void production_mul_mat_nvfp4_decode(const uint8_t* W, const float* X, uint8_t* Xq,
+                                     const int8_t* codebook, const float* scale, float* Y, size_t N,
+                                     size_t K, size_t M) {
+  if (X == nullptr || Xq == nullptr) return weft::set_error(hipErrorInvalidValue);
+  weft::decode_nvfp4(W, X, Xq, codebook, scale, Y, N, K, M,
+                     weft::packed(K / 64 * weft::kNvfp4Bytes, K, N));
+}
+
+// NVFP4 prefill: the GEMV kernel at every M (no MFMA form yet)
+void production_mul_mat_nvfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
+                              const float* scale, float* Y, size_t N, size_t K, size_t M) {
+  production_mul_mat_nvfp4_decode(W, X, Xq, codebook, scale, Y, N, K, M);
+}
+
+void quantized_vec_dot_nvfp4_q8_0(const uint8_t* W, const uint8_t* X, const int8_t* codebook,
+                                  const float* scale, float* Y, size_t K) {
+  if (X == nullptr) return weft::set_error(hipErrorInvalidValue);
+  weft::launch<weft::Fmt::NVFP4>(W, nullptr, X, nullptr, codebook, scale, Y, 1, K, 1,
+                                 weft::packed(0, K, 1));
 }
 
 void production_mul_mat_q5_k_decode(const uint8_t* W, const float* X, uint8_t* Xq, float* Y,

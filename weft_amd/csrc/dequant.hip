@@ -1,7 +1,7 @@
-// Row dequantize: row_dequantize_{q4_0,q4_k,iq2_xxs,mxfp4,q6_k,q5_k}
+// Row dequantize: row_dequantize_{q4_0,q4_k,iq2_xxs,mxfp4,q6_k,q5_k,nvfp4}
 // (examples/kernels/dequantize/*.py; GGML dequantize_row_* in
 // ggml-quants.c:401-419, :511-529, :1471-1493, :2416-2440, :1881-1910,
-// :1673-1697).
+// :1673-1697, :531-552).
 //
 // Every product here is exact in fp32 (at most 22 significant bits), and
 // Q4_K's single subtraction rounds once, so the outputs are bit-exact with
@@ -119,6 +119,33 @@ __global__ void __launch_bounds__(kThreads) dq_32_kernel(const uint8_t* __restri
       for (int i = 0; i < 4; ++i) v[i] = (float)((int)((qs >> (8 * i + shift)) & 0xf) - 8) * d;
     }
     store4<Y16>(Y + b * 32 + 4 * p, v[0], v[1], v[2], v[3]);
+  }
+}
+
+// NVFP4 (dequantize_row_nvfp4, ggml-quants.c:531-552): 16 lanes per 36-byte
+// record, lane p writing elements 4p..4p+3 of sub-block s = p / 4: the low
+// (p % 4 < 2) or high nibbles of qs word 4 + 8 s + 4 (p % 2), times the
+// decoded UE4M3 scale scale[d[s]].  Records carry no alignment.
+template <bool Y16>
+__global__ void __launch_bounds__(kThreads) dq_nvfp4_kernel(const uint8_t* __restrict__ W,
+                                                            const int8_t* __restrict__ codebook,
+                                                            const float* __restrict__ scale,
+                                                            float* __restrict__ Y, long long nb) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const long long wave = ((long long)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const long long nwaves = (long long)gridDim.x * blockDim.x / kWave;
+  const int p = lane & 15, s = p >> 2;
+  const int shift = (p & 2) ? 4 : 0;
+  for (long long st = wave; 4 * st < nb; st += nwaves) {
+    const long long b = 4 * st + lane / 16;
+    if (b >= nb) continue;
+    const uint8_t* rec = W + b * kNvfp4Bytes;
+    const float d = scale[rec[s]];
+    const uint32_t qs = ld_u32_a1(rec + 4 + 8 * s + 4 * (p & 1));
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = (float)codebook[(qs >> (8 * i + shift)) & 0xf] * d;
+    store4<Y16>(Y + b * 64 + 4 * p, v[0], v[1], v[2], v[3]);
   }
 }
 
@@ -259,6 +286,21 @@ void row_dequantize_q4_k(const uint8_t* W, float* Y, size_t K) {
     dq_q4k_kernel<U, false, true><<<g, kThreads, 0, current_stream()>>>(W, Y, nsb);
   else
     dq_q4k_kernel<U, false, false><<<g, kThreads, 0, current_stream()>>>(W, Y, nsb);
+  check_launch();
+}
+
+void row_dequantize_nvfp4(const uint8_t* W, const int8_t* codebook, const float* scale, float* Y,
+                          size_t K) {
+  using namespace weft;
+  if (K == 0) return;
+  if (K % 64 || bad(W, 1, Y) || codebook == nullptr || scale == nullptr || !aligned(scale, 4))
+    return set_error(hipErrorInvalidValue);
+  const long long nb = (long long)(K / 64);
+  const int g = grid_for((nb + 3) / 4);
+  if (aligned(Y, 16))
+    dq_nvfp4_kernel<true><<<g, kThreads, 0, current_stream()>>>(W, codebook, scale, Y, nb);
+  else
+    dq_nvfp4_kernel<false><<<g, kThreads, 0, current_stream()>>>(W, codebook, scale, Y, nb);
   check_launch();
 }
 

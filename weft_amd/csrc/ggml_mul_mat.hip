@@ -1,6 +1,6 @@
 // GGML's MUL_MAT op on the quantized mul_mat kernels: the contract of
 // ggml_compute_forward_mul_mat (ggml-cpu/ggml-cpu.c:1245-1443) for src0 of
-// type Q4_0, Q4_K, Q5_K, Q6_K, IQ2_XXS or MXFP4, so the kernels can sit under a
+// type Q4_0, Q4_K, Q5_K, Q6_K, IQ2_XXS, MXFP4 or NVFP4, so the kernels can sit under a
 // ggml-style graph executor.
 //
 //   dst[i3, i2, i1, i0] = vec_dot(src0 row i0 of plane (i2 / r2, i3 / r3),
@@ -54,6 +54,7 @@ constexpr TypeInfo kTypes[] = {
     {WEFT_GGML_TYPE_Q8_K, 256, kQ8_KBytes, -1},
     {WEFT_GGML_TYPE_IQ2_XXS, 256, kIq2xxsBytes, WEFT_GGML_TYPE_Q8_K},
     {WEFT_GGML_TYPE_MXFP4, 32, kMxfp4Bytes, WEFT_GGML_TYPE_Q8_0},
+    {WEFT_GGML_TYPE_NVFP4, 64, kNvfp4Bytes, WEFT_GGML_TYPE_Q8_0},
 };
 
 constexpr int32_t kGgmlTypeI32 = 26;  // GGML_TYPE_I32
@@ -71,7 +72,8 @@ struct GgmlTables {
   int8_t grid[256 * 8];
   int8_t signs[128 * 8];
   int8_t codebook[16];
-  float scale[256];
+  float scale[256];  // E8M0 (MXFP4), ggml_e8m0_to_fp32_half
+  float ue4m3[256];  // UE4M3 (NVFP4), ggml_ue4m3_to_fp32 (ggml-impl.h:502-515)
 };
 
 constexpr uint16_t kGridCodes[256] = {
@@ -108,6 +110,12 @@ constexpr GgmlTables make_tables() {
   for (int i = 0; i < 16; ++i) t.codebook[i] = (int8_t)(i & 8 ? -kv[i & 7] : kv[i & 7]);
   for (int e = 0; e < 256; ++e)
     t.scale[e] = __builtin_bit_cast(float, e < 2 ? 0x00200000u << e : (uint32_t)(e - 1) << 23);
+  for (int c = 0; c < 256; ++c) {  // half of E4M3 without sign; 0x00 and 0x7F are zero
+    const int e = (c >> 3) & 15, m = c & 7;
+    t.ue4m3[c] = c == 0 || c == 0x7F ? 0.0f
+                 : e == 0            ? (float)m * (1.0f / 1024.0f)
+                                     : (float)(8 + m) * __builtin_bit_cast(float, (uint32_t)(116 + e) << 23);
+  }
   return t;
 }
 
@@ -183,7 +191,8 @@ hipError_t mul_mat(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1, const
     return fail(hipErrorNotSupported);  // quantized src1 rows must be packed
   }
   const GgmlTables* tab = nullptr;
-  if (s0->type == WEFT_GGML_TYPE_IQ2_XXS || s0->type == WEFT_GGML_TYPE_MXFP4) {
+  if (s0->type == WEFT_GGML_TYPE_IQ2_XXS || s0->type == WEFT_GGML_TYPE_MXFP4 ||
+      s0->type == WEFT_GGML_TYPE_NVFP4) {
     tab = device_tables();
     if (tab == nullptr) return fail(hipErrorInvalidDevice);
   }
@@ -218,6 +227,9 @@ hipError_t mul_mat(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1, const
           case WEFT_GGML_TYPE_Q4_K: mul_mat_q4k(W, X, Xq, Y, n, k, m, st); break;
           case WEFT_GGML_TYPE_Q6_K: decode_q6_k(W, X, Xq, Y, n, k, m, st); break;
           case WEFT_GGML_TYPE_Q5_K: decode_q5_k(W, X, Xq, Y, n, k, m, st); break;
+          case WEFT_GGML_TYPE_NVFP4:
+            decode_nvfp4(W, X, Xq, tab->codebook, tab->ue4m3, Y, n, k, m, st);
+            break;
           case WEFT_GGML_TYPE_IQ2_XXS:
             mul_mat_iq2_xxs(W, X, Xq, tab->grid, tab->signs, Y, n, k, m, st);
             break;
@@ -229,6 +241,9 @@ hipError_t mul_mat(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1, const
           case WEFT_GGML_TYPE_Q4_K: mul_mat_q4k_quantized(W, src1, Y, n, k, m, st); break;
           case WEFT_GGML_TYPE_Q6_K: decode_quantized(3, W, src1, nullptr, nullptr, Y, n, k, m, st); break;
           case WEFT_GGML_TYPE_Q5_K: decode_quantized(4, W, src1, nullptr, nullptr, Y, n, k, m, st); break;
+          case WEFT_GGML_TYPE_NVFP4:
+            decode_quantized(5, W, src1, tab->codebook, tab->ue4m3, Y, n, k, m, st);
+            break;
           case WEFT_GGML_TYPE_IQ2_XXS:
             mul_mat_iq2_xxs_quantized(W, src1, tab->grid, tab->signs, Y, n, k, m, st);
             break;
@@ -279,7 +294,8 @@ hipError_t mul_mat_id(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1,
     return fail(hipErrorNotSupported);  // quantized src1 rows must be packed
   }
   const GgmlTables* tab = nullptr;
-  if (s0->type == WEFT_GGML_TYPE_IQ2_XXS || s0->type == WEFT_GGML_TYPE_MXFP4) {
+  if (s0->type == WEFT_GGML_TYPE_IQ2_XXS || s0->type == WEFT_GGML_TYPE_MXFP4 ||
+      s0->type == WEFT_GGML_TYPE_NVFP4) {
     tab = device_tables();
     if (tab == nullptr) return fail(hipErrorInvalidDevice);
   }
@@ -345,6 +361,7 @@ hipError_t mul_mat_id(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1,
         break;
       case WEFT_GGML_TYPE_Q6_K:
       case WEFT_GGML_TYPE_Q5_K:
+      case WEFT_GGML_TYPE_NVFP4:
         break;  // no grouped GEMM: the pair GEMV below
       default: {  // Q4_0 / MXFP4: the GEMMs read a planar activation quantized from X
         const int fmt = s0->type == WEFT_GGML_TYPE_Q4_0 ? 0 : 1;
@@ -371,6 +388,10 @@ hipError_t mul_mat_id(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1,
       break;
     case WEFT_GGML_TYPE_Q5_K:
       decode_pairs(4, W, X, xq_in, xq_out, nullptr, nullptr, Y, (size_t)N, (size_t)K, st, pr, n_pairs);
+      break;
+    case WEFT_GGML_TYPE_NVFP4:
+      decode_pairs(5, W, X, xq_in, xq_out, tab->codebook, tab->ue4m3, Y, (size_t)N, (size_t)K, st, pr,
+                   n_pairs);
       break;
     case WEFT_GGML_TYPE_MXFP4:
       decode_pairs(1, W, X, xq_in, xq_out, tab->codebook, tab->scale, Y, (size_t)N, (size_t)K, st, pr,

@@ -45,11 +45,13 @@ void decode_q6_k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t
                  size_t M, const RowStrides& st);
 void decode_q5_k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
                  size_t M, const RowStrides& st);
+void decode_nvfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
+                  const float* scale, float* Y, size_t N, size_t K, size_t M, const RowStrides& st);
 
 // MUL_MAT_ID: the GEMV over every (token, slot) pair of pr, each with the
 // expert ids[t, s] selects (one activation row per pair; X quantized into
 // xq_out, or the quantized xq_in read).  Q4_K, and Q4_0 (fmt 0), MXFP4 (1),
-// IQ2_XXS (2), Q6_K (3), Q5_K (4).
+// IQ2_XXS (2), Q6_K (3), Q5_K (4), NVFP4 (5).
 void decode_q4k_pairs(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_out,
                       float* Y, size_t N, size_t K, const RowStrides& st, const PairArgs& pr,
                       int n_pairs);
@@ -99,7 +101,7 @@ bool mul_mat_id_iq2_grouped_ok(const uint8_t* W, size_t xq_bytes, const float* Y
 void mul_mat_id_iq2_grouped(const uint8_t* W, const uint8_t* Xq, const int8_t* grid, const int8_t* signs,
                             float* Y, size_t N, size_t K, const RowStrides& st, const PairArgs& pr,
                             int n_pairs, void* ws);
-// Q4_0 (fmt 0), MXFP4 (1), IQ2_XXS (2), Q6_K (3) or Q5_K (4) GEMV over an already quantized
+// Q4_0 (fmt 0), MXFP4 (1), IQ2_XXS (2), Q6_K (3), Q5_K (4) or NVFP4 (5) GEMV over an already quantized
 // activation (Q8_0 / Q8_0 / Q8_K records, read only)
 void decode_quantized(int fmt, const uint8_t* W, const uint8_t* Xq, const int8_t* tab0,
                       const void* tab1, float* Y, size_t N, size_t K, size_t M,

@@ -130,6 +130,7 @@ const EncodingInfo kEncodings[] = {
     {"IQ2_XXS", "uint8_t", 66, 256, 2},  {"MXFP4", "uint8_t", 17, 32, 1},
     {"I8X8", "uint8_t", 8, 8, 8},        {"Q4K_I[16]", "uint8_t", 144, 256, 16},
     {"Q6_K", "uint8_t", 210, 256, 1},    {"Q5_K", "uint8_t", 176, 256, 2},
+    {"NVFP4", "uint8_t", 36, 64, 1},
     {"dense.f32", "float", 4, 1, 4},
     {"dense.i8", "int8_t", 1, 1, 1},
 };
@@ -181,6 +182,16 @@ std::vector<KernelSpec> kernel_specs() {
                "K"});
   k.push_back({"row_dequantize_q6_k",
                {{"W", "Q6_K", "K", false, nullptr}, {"Y", "dense.f32", "K", true, nullptr}}, "K"});
+  k.push_back({"row_dequantize_nvfp4",
+               {{"W", "NVFP4", "K", false, nullptr}, mx[0], mx[1], {"Y", "dense.f32", "K", true, nullptr}},
+               "K"});
+  k.push_back({"quantized_vec_dot_nvfp4_q8_0",
+               {{"W", "NVFP4", "K", false, nullptr},
+                {"X", "Q8_0", "K", false, nullptr},
+                mx[0],
+                mx[1],
+                {"Y", "dense.f32", "1", true, nullptr}},
+               "K"});
   k.push_back({"row_dequantize_q5_k",
                {{"W", "Q5_K", "K", false, nullptr}, {"Y", "dense.f32", "K", true, "output"}}, "K"});
   k.push_back({"q8_0_quantize",
@@ -234,6 +245,8 @@ std::vector<KernelSpec> kernel_specs() {
   mm("production_mul_mat_q6_k", "Q6_K", "Q8_K", true, {});
   mm("production_mul_mat_q6_k_decode", "Q6_K", "Q8_K", false, {});
   mm("production_mul_mat_q5_k", "Q5_K", "Q8_K", false, {});
+  mm("production_mul_mat_nvfp4", "NVFP4", "Q8_0", false, mx);
+  mm("production_mul_mat_nvfp4_decode", "NVFP4", "Q8_0", false, mx);
   mm("production_mul_mat_q5_k_decode", "Q5_K", "Q8_K", false, {});
   for (const char* sym : {"q4_k_q8_k_gemv", "q4_k_q8_k_gemv_groups4", "q4_k_q8_k_gemv_contract"})
     k.push_back({sym,

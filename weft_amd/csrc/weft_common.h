@@ -23,6 +23,7 @@ constexpr int kQ8_KElems = 256, kQ8_KBytes = 292;
 constexpr int kIq2xxsElems = 256, kIq2xxsBytes = 66;
 constexpr int kQ6_KElems = 256, kQ6_KBytes = 210;  // ql[128] qh[64] scales[16] d
 constexpr int kQ5_KElems = 256, kQ5_KBytes = 176;  // d dmin scales[12] qh[32] qs[128]
+constexpr int kNvfp4Elems = 64, kNvfp4Bytes = 36;  // ue4m3 d[4] qs[32]
 
 // ---------------------------------------------------------------- numerics
 // IEEE binary16 -> binary32 with v_cvt_f32_f16.  Exact for every input

@@ -56,7 +56,7 @@ _DECODE_GROUPS = {"Xq": "workspace", "Y": "output"}
 
 # wl.auto extents of the tiled prefill kernels (mul_mat/q4_0.py:17-22,
 # q4_k_staged.py:20-24, iq2_xxs_staged.py:43-48 and :80-83, mxfp4.py:21-25,
-# q6_k.py:17-21, q5_k.py:17-22)
+# q6_k.py:17-21, q5_k.py:17-22, nvfp4.py:21-26)
 _AUTO = {
     "production_mul_mat_q4_0": ("MC", "MR", "NC", "NR"),
     "production_mul_mat_q4_k_staged": ("KC", "MC", "MR", "NC"),
@@ -64,6 +64,7 @@ _AUTO = {
     "production_mul_mat_mxfp4": ("MC", "MR", "NC", "NR"),
     "production_mul_mat_q6_k": ("MC", "MR", "NC", "NR"),
     "production_mul_mat_q5_k": ("MC", "MR", "NC", "NR"),
+    "production_mul_mat_nvfp4": ("MC", "MR", "NC", "NR"),
 }
 
 # (symbol, parameters, reference source, alias groups)
@@ -102,6 +103,11 @@ _DEFS = [
     ("quantized_vec_dot_q5_k_q8_k", ("W", "X", "Y"), "examples/kernels/vec_dot/q5_k_q8_k.py:34-38", None),
     ("production_mul_mat_q5_k", _MM, "examples/kernels/mul_mat/q5_k.py:9-37", None),
     ("production_mul_mat_q5_k_decode", _MM, "examples/kernels/mul_mat/q5_k_decode.py:10-20", None),
+    ("row_dequantize_nvfp4", ("W", "codebook", "scale", "Y"), "examples/kernels/dequantize/nvfp4.py:9-24", None),
+    ("quantized_vec_dot_nvfp4_q8_0", ("W", "X", "codebook", "scale", "Y"),
+     "examples/kernels/vec_dot/nvfp4_q8_0.py:29-38", None),
+    ("production_mul_mat_nvfp4", _MM_MX, "examples/kernels/mul_mat/nvfp4.py:10-43", None),
+    ("production_mul_mat_nvfp4_decode", _MM_MX, "examples/kernels/mul_mat/nvfp4_decode.py:10-23", None),
     ("q4_k_q8_k_gemv", ("W", "X", "Y"), "examples/kernels/gemv/q4_k.py:8-26", None),
     ("q4_k_q8_k_gemv_groups4", ("W", "X", "Y"), "examples/kernels/gemv/q4_k_groups4.py:8-26", None),
     ("q4_k_q8_k_gemv_contract", ("W", "X", "Y"), "examples/kernels/gemv/q4_k_contract.py:8-26", None),
