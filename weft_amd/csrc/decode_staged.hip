@@ -77,7 +77,7 @@ struct Traits<Fmt::NVFP4> {
 };
 template <>
 struct Traits<Fmt::Q5_K> {
-  static constexpr int kElems = 256, kBytes = 176, kSegRecords = 16, kItemsPerRecord = 8;
+  static constexpr int kElems = 256, kBytes = 176, kSegRecords = 16, kItemsPerRecord = 4;
   static constexpr bool kQ8K = true;
 };
 
@@ -359,44 +359,58 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
             }
           }
         } else if constexpr (F == Fmt::Q5_K) {
-          // item = (superblock, 32-element sub-block s): the nibble half s % 2
-          // of qs bytes 48 + 32 (s / 2) + l and bit s of qh bytes 16 + l
-          const int sb = valid ? it >> 3 : 0, s = it & 7;
+          // item = (superblock, 64-element group g): qs bytes 48 + 32 g + l
+          // hold sub-block 2 g in their low and 2 g + 1 in their high
+          // nibbles, bits 2 g and 2 g + 1 of qh bytes 16 + l the fifth bits;
+          // one header decode and one 4-lane reduction per two sub-blocks
+          const int sb = valid ? it >> 2 : 0, g = it & 3;
           const int gsb = r0 + sb;
           const int o = off0 + T::kBytes * sb;
           uint32_t hd[4], qs[8], qh[8];
           lds_run(win, o, hd);
-          lds_run(win, o + 48 + 32 * (s >> 1), qs);
+          lds_run(win, o + 48 + 32 * g, qs);
           lds_run(win, o + 16, qh);
-          int sc, mn;
-          q4k_scale_min(s, hd[1], hd[2], hd[3], sc, mn);
+          int sc0, mn0, sc1, mn1;
+          q4k_scale_min(2 * g, hd[1], hd[2], hd[3], sc0, mn0);
+          q4k_scale_min(2 * g + 1, hd[1], hd[2], hd[3], sc1, mn1);
           const float dw = fp16_to_fp32(hd[0] & 0xffffu), dmin = fp16_to_fp32(hd[0] >> 16);
-          const int nsh = 4 * (s & 1);
-          const uint32_t rot = (uint32_t)(s + 28) & 31u;  // bit s of each byte to bit 4
-          int wv[8];
+          // bit 2 g (2 g + 1) of each byte to bit 4
+          const uint32_t rot0 = (uint32_t)(2 * g + 28) & 31u, rot1 = (uint32_t)(2 * g + 29) & 31u;
+          int wl[8], wh[8];
 #pragma unroll
-          for (int j = 0; j < 8; ++j)
-            wv[j] = (int)(((qs[j] >> nsh) & 0x0f0f0f0fu) |
-                          (__builtin_amdgcn_alignbit(qh[j], qh[j], rot) & 0x10101010u));
+          for (int j = 0; j < 8; ++j) {
+            wl[j] = (int)((qs[j] & 0x0f0f0f0fu) | (__builtin_amdgcn_alignbit(qh[j], qh[j], rot0) & 0x10101010u));
+            wh[j] = (int)(((qs[j] >> 4) & 0x0f0f0f0fu) |
+                          (__builtin_amdgcn_alignbit(qh[j], qh[j], rot1) & 0x10101010u));
+          }
 #pragma unroll
           for (int m = 0; m < kMaxRowsPerPass; ++m) {
             if (m >= a.mb) break;
             const Q8KView v = q8k_view(act, K, m);
-            const int4 x0 = *reinterpret_cast<const int4*>(v.qs + 256 * gsb + 32 * s);
-            const int4 x1 = *reinterpret_cast<const int4*>(v.qs + 256 * gsb + 32 * s + 16);
-            int p = dot4(wv[0], x0.x, 0);
-            p = dot4(wv[1], x0.y, p);
-            p = dot4(wv[2], x0.z, p);
-            p = dot4(wv[3], x0.w, p);
-            p = dot4(wv[4], x1.x, p);
-            p = dot4(wv[5], x1.y, p);
-            p = dot4(wv[6], x1.z, p);
-            p = dot4(wv[7], x1.w, p);
-            // exact int32 S and Mn of the superblock over its 8 sub-blocks
+            const int4* xv = reinterpret_cast<const int4*>(v.qs + 256 * gsb + 64 * g);
+            const int4 x0 = xv[0], x1 = xv[1], x2 = xv[2], x3 = xv[3];
+            int p0 = dot4(wl[0], x0.x, 0);
+            p0 = dot4(wl[1], x0.y, p0);
+            p0 = dot4(wl[2], x0.z, p0);
+            p0 = dot4(wl[3], x0.w, p0);
+            p0 = dot4(wl[4], x1.x, p0);
+            p0 = dot4(wl[5], x1.y, p0);
+            p0 = dot4(wl[6], x1.z, p0);
+            p0 = dot4(wl[7], x1.w, p0);
+            int p1 = dot4(wh[0], x2.x, 0);
+            p1 = dot4(wh[1], x2.y, p1);
+            p1 = dot4(wh[2], x2.z, p1);
+            p1 = dot4(wh[3], x2.w, p1);
+            p1 = dot4(wh[4], x3.x, p1);
+            p1 = dot4(wh[5], x3.y, p1);
+            p1 = dot4(wh[6], x3.z, p1);
+            p1 = dot4(wh[7], x3.w, p1);
+            const int2 bp = *reinterpret_cast<const int2*>(v.bp + 8 * gsb + 2 * g);
+            // exact int32 S and Mn of the superblock over its 4 groups
             // (|S| <= 256 * 31 * 127 * 63), then one fp32 term
-            const int S = sum8_of_sum4(sum4(valid ? sc * p : 0));
-            const int Mn = sum8_of_sum4(sum4(valid ? mn * v.bp[8 * gsb + s] : 0));
-            if (valid && s == 0) acc[m] += v.d[gsb] * (dw * (float)S - dmin * (float)Mn);
+            const int S = sum4(valid ? sc0 * p0 + sc1 * p1 : 0);
+            const int Mn = sum4(valid ? mn0 * bp.x + mn1 * bp.y : 0);
+            if (valid && g == 0) acc[m] += v.d[gsb] * (dw * (float)S - dmin * (float)Mn);
           }
         } else if constexpr (F == Fmt::Q6_K) {
           // item = (superblock, 32-element chunk g): half h = g / 4, quarter
