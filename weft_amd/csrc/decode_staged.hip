@@ -67,7 +67,7 @@ struct Traits<Fmt::IQ2_XXS> {
 };
 template <>
 struct Traits<Fmt::Q6_K> {
-  static constexpr int kElems = 256, kBytes = 210, kSegRecords = 16, kItemsPerRecord = 8;
+  static constexpr int kElems = 256, kBytes = 210, kSegRecords = 16, kItemsPerRecord = 4;
   static constexpr bool kQ8K = true;
 };
 template <>
@@ -413,47 +413,58 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
             if (valid && g == 0) acc[m] += v.d[gsb] * (dw * (float)S - dmin * (float)Mn);
           }
         } else if constexpr (F == Fmt::Q6_K) {
-          // item = (superblock, 32-element chunk g): half h = g / 4, quarter
-          // qq = g % 4; the chunk's 6-bit codes are the nibble 4 (qq / 2) of
-          // ql bytes 64 h + 32 (qq % 2) + l and bits 2 qq of qh bytes
-          // 128 + 32 h + l (l = 0..31); its two 16-groups scale by sc[2 g]
-          // and sc[2 g + 1]
-          const int sb = valid ? it >> 3 : 0, g = it & 7;
+          // item = (superblock, 64 elements): chunks g0 = 4 h + c and
+          // g1 = g0 + 2 of half h (c = 0, 1) share ql bytes 64 h + 32 c + l
+          // (low / high nibble) and qh bytes 128 + 32 h + l (bits 2 c /
+          // 2 c + 4); chunk g's two 16-groups scale by sc[2 g], sc[2 g + 1]
+          const int sb = valid ? it >> 2 : 0, G = it & 3;
           const int gsb = r0 + sb;
           const int o = off0 + T::kBytes * sb;
-          const int h = g >> 2, qq = g & 3;
-          const int qlo = o + 64 * h + 32 * (qq & 1), qho = o + 128 + 32 * h;
-          const int nsh = 4 * (qq >> 1), hsh = 2 * qq;
-          const uint32_t sw = lds_u32(win, o + 192 + 2 * g);
-          const int sc0 = (int)(int8_t)(sw & 0xffu), sc1 = (int)(int8_t)((sw >> 8) & 0xffu);
+          const int h = G >> 1, c = G & 1;
+          const int g0 = 4 * h + c, g1 = g0 + 2;
+          uint32_t lq[8], hq[8];
+          lds_run(win, o + 64 * h + 32 * c, lq);
+          lds_run(win, o + 128 + 32 * h, hq);
+          const uint32_t sw0 = lds_u32(win, o + 192 + 2 * g0), sw1 = lds_u32(win, o + 192 + 2 * g1);
+          const int sc00 = (int)(int8_t)(sw0 & 0xffu), sc01 = (int)(int8_t)((sw0 >> 8) & 0xffu);
+          const int sc10 = (int)(int8_t)(sw1 & 0xffu), sc11 = (int)(int8_t)((sw1 >> 8) & 0xffu);
           const float dw = fp16_to_fp32(lds_u32(win, o + 208) & 0xffffu);
-          uint32_t ql[8], qh[8];
-          lds_run(win, qlo, ql);
-          lds_run(win, qho, qh);
-          int wv[8];
+          const int hs0 = 2 * c, hs1 = 2 * c + 4;
+          int w0[8], w1[8];
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
-            const uint32_t q = ((ql[j] >> nsh) & 0x0f0f0f0fu) | (((qh[j] >> hsh) & 0x03030303u) << 4);
-            wv[j] = (int)(((q | 0x80808080u) - 0x20202020u) ^ 0x80808080u);  // bytewise q - 32
+            const uint32_t q0 = (lq[j] & 0x0f0f0f0fu) | (((hq[j] >> hs0) & 0x03030303u) << 4);
+            const uint32_t q1 = ((lq[j] >> 4) & 0x0f0f0f0fu) | (((hq[j] >> hs1) & 0x03030303u) << 4);
+            w0[j] = (int)(((q0 | 0x80808080u) - 0x20202020u) ^ 0x80808080u);  // bytewise q - 32
+            w1[j] = (int)(((q1 | 0x80808080u) - 0x20202020u) ^ 0x80808080u);
           }
 #pragma unroll
           for (int m = 0; m < kMaxRowsPerPass; ++m) {
             if (m >= a.mb) break;
             const Q8KView v = q8k_view(act, K, m);
-            const int4 x0 = *reinterpret_cast<const int4*>(v.qs + 256 * gsb + 32 * g);
-            const int4 x1 = *reinterpret_cast<const int4*>(v.qs + 256 * gsb + 32 * g + 16);
-            int s0 = dot4(wv[0], x0.x, 0);
-            s0 = dot4(wv[1], x0.y, s0);
-            s0 = dot4(wv[2], x0.z, s0);
-            s0 = dot4(wv[3], x0.w, s0);
-            int s1 = dot4(wv[4], x1.x, 0);
-            s1 = dot4(wv[5], x1.y, s1);
-            s1 = dot4(wv[6], x1.z, s1);
-            s1 = dot4(wv[7], x1.w, s1);
-            // the superblock's exact int32 sum over its 8 chunks, then one
+            const int4* xa = reinterpret_cast<const int4*>(v.qs + 256 * gsb + 32 * g0);
+            const int4* xb = reinterpret_cast<const int4*>(v.qs + 256 * gsb + 32 * g1);
+            const int4 x0 = xa[0], x1 = xa[1], y0 = xb[0], y1 = xb[1];
+            int s00 = dot4(w0[0], x0.x, 0);
+            s00 = dot4(w0[1], x0.y, s00);
+            s00 = dot4(w0[2], x0.z, s00);
+            s00 = dot4(w0[3], x0.w, s00);
+            int s01 = dot4(w0[4], x1.x, 0);
+            s01 = dot4(w0[5], x1.y, s01);
+            s01 = dot4(w0[6], x1.z, s01);
+            s01 = dot4(w0[7], x1.w, s01);
+            int s10 = dot4(w1[0], y0.x, 0);
+            s10 = dot4(w1[1], y0.y, s10);
+            s10 = dot4(w1[2], y0.z, s10);
+            s10 = dot4(w1[3], y0.w, s10);
+            int s11 = dot4(w1[4], y1.x, 0);
+            s11 = dot4(w1[5], y1.y, s11);
+            s11 = dot4(w1[6], y1.z, s11);
+            s11 = dot4(w1[7], y1.w, s11);
+            // the superblock's exact int32 sum over its 4 items, then one
             // fp32 term (|sum| <= 256 * 32 * 127 * 128 < 2^31)
-            const int bsum = sum8_of_sum4(sum4(valid ? sc0 * s0 + sc1 * s1 : 0));
-            if (valid && g == 0) acc[m] += (dw * v.d[gsb]) * (float)bsum;
+            const int bsum = sum4(valid ? sc00 * s00 + sc01 * s01 + sc10 * s10 + sc11 * s11 : 0);
+            if (valid && G == 0) acc[m] += (dw * v.d[gsb]) * (float)bsum;
           }
         } else {  // IQ2_XXS: item = (superblock, 32-group); 8 lanes per superblock
           const int sb = valid ? it >> 3 : 0, g = it & 7;
