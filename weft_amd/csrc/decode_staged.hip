@@ -325,7 +325,10 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
             s = dot4(hi1, xh.y, s);
             s = dot4(hi2, xh.z, s);
             s = dot4(hi3, xh.w, s);
-            acc[m] += (float)s * wscale * v.d[gb];
+            if constexpr (F == Fmt::MXFP4)
+              acc[m] = ggml_scaled_term(acc[m], v.d[gb], wscale, (float)s);  // GGML's order
+            else
+              acc[m] += (float)s * wscale * v.d[gb];
           }
         } else if constexpr (F == Fmt::NVFP4) {
           if (!valid) continue;

@@ -469,6 +469,21 @@ constexpr int kSlot = kSW + kNT * kRowW;   // 35328
 constexpr int kLds = 4 * kSlot;            // 141312
 constexpr int kWLoads = kNT * kRowW / 256; // 70 wave-wide dword loads of weights
 static_assert(kNT * kRowW % 256 == 0, "whole wave-wide weight loads");
+
+// Exponents whose block terms the scaled MFMA reproduces.  GGML forms
+// d = fp16(dx) * 2^(e-128), then sumf + d * I, each step rounded
+// (ggml-cpu/quants.c:265-273); the MFMA forms 2^(e-128) * I exactly and one
+// FMA adds it times dx.  With |dx| in [2^-24, 65504] and
+// |I| <= 32 * 12 * 127 < 2^15.6:
+//   * e >= 26 keeps d and 2^(e-128) I normal, so both sides round the same
+//     real product once;
+//   * e <= 224 keeps |2^(e-128) I dx| < 2^128, so no finite product
+//     overflows (the FMA does not round its product: an overflow that GGML
+//     turns into inf before the add would be lost against an inf already in
+//     the sum).  An inf dx gives inf, or NaN for I = 0, on both sides.
+// Other exponents (e = 255, whose 2^127 has no E8M0 block-scale encoding,
+// included) take GGML's order.
+constexpr uint32_t kSafeLo = 26, kSafeHi = 224;
 static_assert(8 * 4 * 16 * 64 * 4 <= kLds, "partial sums fit the ring");
 
 // 16 bytes per lane from sbase + voff into [lds + 16 lane, +16)
@@ -485,6 +500,25 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 typedef int v8i __attribute__((ext_vector_type(8)));
+
+// y += dx * d for a tile whose MFMA applied the block scales
+__device__ __forceinline__ v16f fma_block(v16f y, v16f d, float dx) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) y[r] = fmaf(d[r], dx, y[r]);
+  return y;
+}
+
+// A tile computed at unit block scale (d = I / 2 exactly), combined in
+// GGML's order: register r holds weight row 8 (r / 4) + 4 h + r % 4 of the
+// tile, whose exponent the lane of that row holds in e.
+__device__ __attribute__((noinline)) v16f ggml_block_terms(v16f y, v16f d, float dx, uint32_t e, int h) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const uint32_t er = (uint32_t)__shfl((int)e, 8 * (r >> 2) + 4 * h + (r & 3), kWave);
+    y[r] = ggml_scaled_term(y[r], dx, e8m0_half(er), 2.f * d[r]);
+  }
+  return y;
+}
 
 template <bool kGroup>
 __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
@@ -561,11 +595,9 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
         lds_dma4_s(wb, vw[i], __builtin_amdgcn_readfirstlane(lds_addr(slot + kSW + 256 * (wave + 8 * i + 4))));
   };
 
-  float y[4][16];  // tile 2 * token half + column tile
+  v16f y[4];  // tile 2 * token half + column tile
 #pragma unroll
-  for (int q = 0; q < 4; ++q)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) y[q][r] = 0.f;
+  for (int q = 0; q < 4; ++q) y[q] = v16f{};
   const v16f fzero = {};
   const int x_scale = h ? 127 + 9 : 127 + 13;  // B block 0: hi plane (x16), block 1: lo plane
 
@@ -581,15 +613,20 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
       const int b4 = (off + 1) & ~3, sh = (off + 1) & 3;
       v8i wv[2];
       int wsc[2];
+      uint32_t ew[2];
+      bool exact[2];
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) {
         const uint8_t* wr = slot + kSW + kRowW * (64 * cp + 32 * ct + col);
         const uint32_t w0 = ld32(wr + b4), w1 = ld32(wr + b4 + 4), w2 = ld32(wr + b4 + 8),
                        w3 = ld32(wr + b4 + 12), w4 = ld32(wr + b4 + 16);
         const uint32_t e = __builtin_amdgcn_ubfe(ld32(wr + (off & ~3)), 8 * (off & 3), 8);
-        // e = 255 (2^127 in GGML's table) has no E8M0 block-scale encoding;
-        // GGML's quantizer never produces it from finite weights
-        wsc[ct] = (int)min(e, 254u);
+        // A tile whose 32 rows all have exponents in [kSafeLo, kSafeHi]
+        // takes e as the hardware block scale; otherwise the MFMA runs at
+        // unit scale and the block is combined in GGML's order below.
+        exact[ct] = __builtin_amdgcn_ballot_w64(e < kSafeLo || e > kSafeHi) != 0;
+        ew[ct] = e;
+        wsc[ct] = exact[ct] ? 127 : (int)e;
         wv[ct] = v8i{(int)__builtin_amdgcn_alignbyte(w1, w0, sh), (int)__builtin_amdgcn_alignbyte(w2, w1, sh),
                      (int)__builtin_amdgcn_alignbyte(w3, w2, sh), (int)__builtin_amdgcn_alignbyte(w4, w3, sh),
                      0, 0, 0, 0};
@@ -615,9 +652,13 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
         d[q] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wv[q & 1], xv[q >> 1], fzero, 4, 0, 0, wsc[q & 1], 0,
                                                                x_scale);
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) y[q][r] = fmaf(d[q][r], dx[q >> 1], y[q][r]);
+      for (int q = 0; q < 4; ++q) {
+        const int ct = q & 1;
+        if (exact[ct])
+          y[q] = ggml_block_terms(y[q], d[q], dx[q >> 1], ew[ct], h);
+        else
+          y[q] = fma_block(y[q], d[q], dx[q >> 1]);
+      }
     }
   };
 

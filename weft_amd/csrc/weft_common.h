@@ -344,6 +344,23 @@ __device__ __forceinline__ Q8_0Lane q80_quantize_8lanes(float4 x) {
   return r;
 }
 
+// ggml_e8m0_to_fp32_half (ggml-impl.h:477-495): 2^(e-128), e < 2 as fp32
+// subnormals
+__device__ __forceinline__ float e8m0_half(uint32_t e) {
+  return __uint_as_float(e < 2 ? 0x00200000u << e : (e - 1) << 23);
+}
+
+// One MXFP4 x Q8_0 block term added in GGML's order and rounding
+// (ggml-cpu/quants.c:265-273): d = fp16(dx) * ws, then acc + d * I, each
+// step rounded (so an overflow to inf, and inf * 0 = NaN, happen where
+// GGML's do).
+__device__ __forceinline__ float ggml_scaled_term(float acc, float dx, float ws, float i) {
+#pragma clang fp contract(off)
+  const float d = dx * ws;
+  const float t = d * i;
+  return acc + t;
+}
+
 __device__ __forceinline__ int pack4_i8(const int q[4]) {
   return (int)((uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
                ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24));
