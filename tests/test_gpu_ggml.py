@@ -211,3 +211,10 @@ def test_mul_mat_id_grouped_gemm(hip, fmt, ne11, prequant):
     ids[40, 0] = n_as
     run_id(hip, fmt, 1024, 300, n_as, n_ids, ne11, n_tok, ids, pad_w=16,
            pad_x=0 if prequant else 4, prequant=prequant)
+
+
+@pytest.mark.parametrize("k", [8192, 11008])
+def test_mul_mat_id_decode_long_rows(hip, k):
+    # batch-1 pairs with rows of two / three 4096-column steps: the
+    # split-step GEMV with its per-row partial sums, pair by pair
+    run_id(hip, "q4_k", k, 160, 4, 2, 1, 1, np.array([[3, 1]]))

@@ -208,8 +208,9 @@ __global__ void __launch_bounds__(NT) q4k_gemv_kernel(Q4KArgs a) {
 // streams in, instead of bursting all its requests up front and computing
 // after the last one lands.
 // RB = row buffers: 2 for the ping-pong walk above, 1 when the launch gives
-// every wave at most one row (long rows at NT = 1024, where a second buffer
-// would not fit the register budget).
+// every wave at most one row.  The library launches <1, 1024, 2> (K <= 4096);
+// longer rows go to q4k_gemv_ks_kernel, which splits a row's steps over
+// waves instead of holding every step's activation slice in one wave.
 template <int STEPS, int NT, int RB>
 __global__ void __launch_bounds__(NT) q4k_gemv_m1_kernel(Q4KArgs a) {
   static_assert(RB == 1 || RB == 2, "one or two row buffers");
@@ -349,6 +350,138 @@ __global__ void __launch_bounds__(NT) q4k_gemv_m1_kernel(Q4KArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Batch-1 kernel for rows longer than one step (4096 < K <= 4096 * KS), e.g.
+// config 3's W_down (K = 11008: 43 superblocks in 3 steps).  The waves of a
+// workgroup form groups of KS: wave w computes step w % KS of the rows of
+// group w / KS, so each wave keeps one step's activation slice in VGPRs and
+// walks its rows with the ping-pong lookahead of q4k_gemv_m1_kernel (rows
+// row_first + k * ngroups).  The KS partial sums of a row meet in LDS and
+// are added in step order once every wave is done.  Waves past the last
+// whole group quantize and wait at the barriers only.
+template <int KS, int NT>
+__global__ void __launch_bounds__(NT) q4k_gemv_ks_kernel(Q4KArgs a) {
+  if (a.pair.ids != nullptr && !resolve_pair(a)) return;
+  extern __shared__ __align__(16) char lds[];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  constexpr int nwaves = NT / kWave;
+  constexpr int ngroups = nwaves / KS;
+  const int K = a.K;
+  const int nsb = K >> 8;
+  const size_t rb = a.ldw;
+  const int st = wave % KS, grp = wave / KS;
+  const int lsb = lane >> 2, g = lane & 3;
+  // steps take ceil(nsb / KS) <= 16 consecutive superblocks each, so the
+  // last step is not left with a short tail (43 = 15 + 15 + 13)
+  const int spb = (nsb + KS - 1) / KS;
+  const int sb = st * spb + lsb;
+  const bool live = lsb < spb && sb < nsb;
+  const int off = min(sb, nsb - 1) * kQ4_KBytes;
+  const int row_base = blockIdx.x * a.rows_per_wg;
+  const int row_end = min(a.N, row_base + a.rows_per_wg);
+  const int row_first = row_base + grp;
+  const int nrows = grp < ngroups && row_first < row_end ? (row_end - row_first + ngroups - 1) / ngroups : 0;
+  // partial sums [row - row_base][step], after the activation row
+  float* part = reinterpret_cast<float*>(lds + q8k_lds_row_bytes(K));
+
+  Q8KStager16<(4 * KS + nwaves - 1) / nwaves> stager;
+  stager.prefetch(a.X, a.ldx, K, a.m0, 1);
+  __builtin_amdgcn_sched_barrier(0);
+
+  struct RowBuf {
+    uint4 h, qa, qc;
+  };
+  auto issue = [&](RowBuf& buf, int k) {
+    const int row = min(row_first + k * ngroups, a.N - 1);  // clamped: always a valid row
+    const uint8_t* sbp = a.W + (size_t)row * rb + off;
+    buf.h = *reinterpret_cast<const uint4*>(sbp);
+    buf.qa = *reinterpret_cast<const uint4*>(sbp + 16 + 32 * g);
+    buf.qc = *reinterpret_cast<const uint4*>(sbp + 32 + 32 * g);
+  };
+  RowBuf bufA, bufB;
+  issue(bufA, 0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  stager.finish(a.X, a.ldx, blockIdx.x == 0 ? a.xq_out : nullptr, K, a.m0, 1, lds);
+  __syncthreads();
+
+  int4 xl0, xl1, xh0, xh1;
+  float dx;
+  int bp0, bp1;
+  {
+    const Q8KView v = q8k_view(lds, K, 0);
+    const int sbc = min(sb, nsb - 1);
+    const int8_t* xb = v.qs + 256 * sbc + 64 * g;
+    xl0 = *reinterpret_cast<const int4*>(xb);
+    xl1 = *reinterpret_cast<const int4*>(xb + 16);
+    xh0 = *reinterpret_cast<const int4*>(xb + 32);
+    xh1 = *reinterpret_cast<const int4*>(xb + 48);
+    dx = live ? v.d[sbc] : 0.f;  // dead lanes contribute exactly 0
+    const int2 bp = *reinterpret_cast<const int2*>(v.bp + 8 * sbc + 2 * g);
+    bp0 = bp.x;
+    bp1 = bp.y;
+  }
+
+  auto compute = [&](const RowBuf& buf, int k) {
+    const uint4 h = buf.h;
+    const uint32_t scw = g < 2 ? (h.y & 0x3f3f3f3fu)
+                               : ((h.w & 0x0f0f0f0fu) | (((h.y >> 6) & 0x03030303u) << 4));
+    const uint32_t mnw = g < 2 ? (h.z & 0x3f3f3f3fu)
+                               : (((h.w >> 4) & 0x0f0f0f0fu) | (((h.z >> 6) & 0x03030303u) << 4));
+    const int sh = 16 * (g & 1);
+    const int sc_lo = (scw >> sh) & 0xff, sc_hi = (scw >> (sh + 8)) & 0xff;
+    const int m_lo = (mnw >> sh) & 0xff, m_hi = (mnw >> (sh + 8)) & 0xff;
+    const uint4 qa4 = buf.qa, qc4 = buf.qc;
+    int pl = dot4((int)(qa4.x & 0x0f0f0f0fu), xl0.x, 0);
+    pl = dot4((int)(qa4.y & 0x0f0f0f0fu), xl0.y, pl);
+    pl = dot4((int)(qa4.z & 0x0f0f0f0fu), xl0.z, pl);
+    pl = dot4((int)(qa4.w & 0x0f0f0f0fu), xl0.w, pl);
+    pl = dot4((int)(qc4.x & 0x0f0f0f0fu), xl1.x, pl);
+    pl = dot4((int)(qc4.y & 0x0f0f0f0fu), xl1.y, pl);
+    pl = dot4((int)(qc4.z & 0x0f0f0f0fu), xl1.z, pl);
+    pl = dot4((int)(qc4.w & 0x0f0f0f0fu), xl1.w, pl);
+    int ph = dot4((int)((qa4.x >> 4) & 0x0f0f0f0fu), xh0.x, 0);
+    ph = dot4((int)((qa4.y >> 4) & 0x0f0f0f0fu), xh0.y, ph);
+    ph = dot4((int)((qa4.z >> 4) & 0x0f0f0f0fu), xh0.z, ph);
+    ph = dot4((int)((qa4.w >> 4) & 0x0f0f0f0fu), xh0.w, ph);
+    ph = dot4((int)((qc4.x >> 4) & 0x0f0f0f0fu), xh1.x, ph);
+    ph = dot4((int)((qc4.y >> 4) & 0x0f0f0f0fu), xh1.y, ph);
+    ph = dot4((int)((qc4.z >> 4) & 0x0f0f0f0fu), xh1.z, ph);
+    ph = dot4((int)((qc4.w >> 4) & 0x0f0f0f0fu), xh1.w, ph);
+    const int S = __mul24(sc_lo, pl) + __mul24(sc_hi, ph);
+    const int Mn = __mul24(m_lo, bp0) + __mul24(m_hi, bp1);
+    const float dw = fp16_to_fp32(h.x & 0xffffu);
+    const float dmin = fp16_to_fp32(h.x >> 16);
+    const float tot = wave_sum_f(dx * (dw * (float)S - dmin * (float)Mn));
+    if (lane == 0) part[(row_first + k * ngroups - row_base) * KS + st] = tot;
+  };
+
+  // one row of lookahead, as in q4k_gemv_m1_kernel (deeper prefetch measured
+  // slower: the requests queue behind each other)
+  int k = 0;
+  for (; k + 2 < nrows; k += 2) {
+    issue(bufB, k + 1);
+    compute(bufA, k);
+    issue(bufA, k + 2);
+    compute(bufB, k + 1);
+  }
+  if (nrows - k == 2) {
+    issue(bufB, k + 1);
+    compute(bufA, k);
+    compute(bufB, k + 1);
+  } else if (nrows - k == 1) {
+    compute(bufA, k);
+  }
+  __syncthreads();
+  for (int r = threadIdx.x; r < row_end - row_base; r += NT) {
+    float y = part[r * KS];
+#pragma unroll
+    for (int s = 1; s < KS; ++s) y += part[r * KS + s];
+    a.Y[row_base + r] = y;
+  }
+}
+
 namespace {
 
 constexpr int kMaxRowsPerPass = 4;
@@ -403,15 +536,10 @@ void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t*
     }
   };
   if (M == 1 && X != nullptr && a16 && x16 && K <= 3 * 4096) {
-    // batch 1: the register-resident kernel.  One step per row (K <= 4096)
-    // runs 1024-thread workgroups, two per CU (62 VGPRs); longer rows keep
-    // three activation slices in VGPRs and run 512 threads, one per CU.
+    // batch 1: the register-resident kernels.  One step per row (K <= 4096)
+    // runs 1024-thread workgroups, two per CU (62 VGPRs); longer rows split
+    // each row's steps over a group of waves (q4k_gemv_ks_kernel).
     const int steps = (int)((K + 4095) / 4096);
-    // one row per wave at NT = 1024 (one workgroup per CU) when the rows are
-    // long and few enough: 16 waves share the activation quantization
-    const bool one_row = steps > 1 && N <= (size_t)cus * 16;
-    const int wgs = steps == 1 ? 2 * cus : cus;
-    const int rpw = one_row ? 16 : (int)((N + wgs - 1) / wgs);
     Q4KArgs a;
     a.W = W;
     a.X = X;
@@ -422,25 +550,36 @@ void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t*
     a.K = (int)K;
     a.m0 = 0;
     a.mb = 1;
-    a.rows_per_wg = rpw;
     a.y_stride = (long long)st.ldy;
     a.ldw = st.ldw;
     a.ldx = st.ldx;
-    const int g1 = (int)((N + rpw - 1) / rpw);
-    each(a, g1, [&](const Q4KArgs& b, dim3 g) {
-      if (steps == 1)
+    if (steps == 1) {
+      const int wgs = 2 * cus;
+      a.rows_per_wg = (int)((N + wgs - 1) / wgs);
+      const int g1 = (int)((N + a.rows_per_wg - 1) / a.rows_per_wg);
+      each(a, g1, [&](const Q4KArgs& b, dim3 g) {
         q4k_gemv_m1_kernel<1, 1024, 2><<<g, 1024, row_lds, current_stream()>>>(b);
-      else if (one_row && steps == 2)
-        q4k_gemv_m1_kernel<2, 1024, 1><<<g, 1024, row_lds, current_stream()>>>(b);
-      else if (one_row)
-        q4k_gemv_m1_kernel<3, 1024, 1><<<g, 1024, row_lds, current_stream()>>>(b);
-      else if (steps == 2)
-        q4k_gemv_m1_kernel<2, 512, 2><<<g, 512, row_lds, current_stream()>>>(b);
-      else
-        q4k_gemv_m1_kernel<3, 512, 2><<<g, 512, row_lds, current_stream()>>>(b);
-      check_launch();
-    });
-    return;
+        check_launch();
+      });
+      return;
+    }
+    // one workgroup per CU: every workgroup quantizes the whole activation,
+    // so more (smaller) workgroups only add that prologue (measured: 7.8 us
+    // at 768 threads x 256 for config 3's W_down, 9.6 us at 2 per CU)
+    const int wgs = cus;
+    a.rows_per_wg = (int)((N + wgs - 1) / wgs);
+    const int g1 = (int)((N + a.rows_per_wg - 1) / a.rows_per_wg);
+    const size_t lds = row_lds + (size_t)a.rows_per_wg * steps * sizeof(float);
+    if (lds <= lds_cap) {  // else the general kernel below
+      each(a, g1, [&](const Q4KArgs& b, dim3 g) {
+        if (steps == 2)
+          q4k_gemv_ks_kernel<2, 1024><<<g, 1024, lds, current_stream()>>>(b);
+        else
+          q4k_gemv_ks_kernel<3, 768><<<g, 768, lds, current_stream()>>>(b);
+        check_launch();
+      });
+      return;
+    }
   }
   for (size_t m0 = 0; m0 < M; m0 += mb_max) {
     Q4KArgs a;
