@@ -279,7 +279,7 @@ __global__ void __launch_bounds__(NT) q4k_gemv_m1_kernel(Q4KArgs a) {
       xl1[st] = *reinterpret_cast<const int4*>(xb + 16);
       xh0[st] = *reinterpret_cast<const int4*>(xb + 32);
       xh1[st] = *reinterpret_cast<const int4*>(xb + 48);
-      dx[st] = live[st] ? v.d[sb] : 0.f;  // dead lanes contribute exactly 0
+      dx[st] = v.d[sb];
       const int2 bp = *reinterpret_cast<const int2*>(v.bp + 8 * sb + 2 * g);
       bp0[st] = bp.x;
       bp1[st] = bp.y;
@@ -322,7 +322,9 @@ __global__ void __launch_bounds__(NT) q4k_gemv_m1_kernel(Q4KArgs a) {
       const int Mn = __mul24(m_lo, bp0[st]) + __mul24(m_hi, bp1[st]);
       const float dw = fp16_to_fp32(h.x & 0xffffu);
       const float dmin = fp16_to_fp32(h.x >> 16);
-      acc += dx[st] * (dw * (float)S - dmin * (float)Mn);
+      // lanes past the row's last superblock duplicate it: they add exactly 0
+      const float t = dx[st] * (dw * (float)S - dmin * (float)Mn);
+      acc += live[st] ? t : 0.f;
     }
     const float tot = wave_sum_f(acc);
     if (lane == 0) a.Y[row_first + k * nwaves] = tot;
@@ -417,7 +419,7 @@ __global__ void __launch_bounds__(NT) q4k_gemv_ks_kernel(Q4KArgs a) {
     xl1 = *reinterpret_cast<const int4*>(xb + 16);
     xh0 = *reinterpret_cast<const int4*>(xb + 32);
     xh1 = *reinterpret_cast<const int4*>(xb + 48);
-    dx = live ? v.d[sbc] : 0.f;  // dead lanes contribute exactly 0
+    dx = v.d[sbc];
     const int2 bp = *reinterpret_cast<const int2*>(v.bp + 8 * sbc + 2 * g);
     bp0 = bp.x;
     bp1 = bp.y;
@@ -453,7 +455,8 @@ __global__ void __launch_bounds__(NT) q4k_gemv_ks_kernel(Q4KArgs a) {
     const int Mn = __mul24(m_lo, bp0) + __mul24(m_hi, bp1);
     const float dw = fp16_to_fp32(h.x & 0xffffu);
     const float dmin = fp16_to_fp32(h.x >> 16);
-    const float tot = wave_sum_f(dx * (dw * (float)S - dmin * (float)Mn));
+    const float t = dx * (dw * (float)S - dmin * (float)Mn);
+    const float tot = wave_sum_f(live ? t : 0.f);  // dead lanes duplicate a live superblock
     if (lane == 0) part[(row_first + k * ngroups - row_base) * KS + st] = tot;
   };
 

@@ -543,6 +543,12 @@ void launch(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_
     set_error(hipErrorInvalidValue);
     return;
   }
+  if constexpr (F == Fmt::Q4_0 || F == Fmt::MXFP4) {
+    // batch 1: the register-resident kernel of decode_rec.hip when it applies
+    if (pr == nullptr && M == 1 && X != nullptr &&
+        decode_rec_m1(F == Fmt::MXFP4 ? 1 : 0, W, X, xq_out, tab0, static_cast<const float*>(tab1), Y, N, K, st))
+      return;
+  }
   const size_t row_lds = T::kQ8K ? q8k_lds_row_bytes((int)K) : q80_lds_row_bytes((int)K);
   const size_t fixed = (size_t)kWaves * kWindow + 3072;
   const size_t cap = max_lds_per_block();

@@ -48,6 +48,12 @@ void decode_q5_k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t
 void decode_nvfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
                   const float* scale, float* Y, size_t N, size_t K, size_t M, const RowStrides& st);
 
+// Batch-1 Q4_0 (fmt 0) / MXFP4 (fmt 1) GEMV with the records in VGPRs
+// (decode_rec.hip); false, with nothing launched, when the call does not
+// suit it (K > 4096, unaligned operands), for the caller's general kernel.
+bool decode_rec_m1(int fmt, const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
+                   const float* scale, float* Y, size_t N, size_t K, const RowStrides& st);
+
 // MUL_MAT_ID: the GEMV over every (token, slot) pair of pr, each with the
 // expert ids[t, s] selects (one activation row per pair; X quantized into
 // xq_out, or the quantized xq_in read).  Q4_K, and Q4_0 (fmt 0), MXFP4 (1),
