@@ -13,8 +13,8 @@ import pytest
 
 from weft_amd import _lib, kernels as K
 from weft_amd.diagnostics import DefinitionError, LanguageUseError
-from weft_amd.runtime import Buffer, CompilationError, CompileOptions, HipTarget
-from weft_amd.runtime.compiler import CompiledKernel, _Compiler
+from weft_amd.runtime import Buffer, CompilationError, CompileOptions, HipTarget, Toolchain
+from weft_amd.runtime.compiler import CompiledKernel, _Registry
 
 TARGET = HipTarget("gfx950", 64, 64, 0)
 
@@ -137,24 +137,18 @@ def test_definitions_match_library_and_cannot_be_called():
 def test_compile_options_are_validated():
     with pytest.raises(ValueError):
         CompileOptions(meta={"NC": 0})
-    comp = _Compiler.__new__(_Compiler)
-    comp.target, comp._cache = TARGET, {}
-    import threading
-    comp._lock = threading.RLock()
+    comp = _Registry(Toolchain(), TARGET)
     with pytest.raises(CompilationError, match="RISC-V"):
-        comp.compile(K.production_mul_mat_q4_k_decode, CompileOptions(lmul_eighths=16))
+        comp.resolve(K.production_mul_mat_q4_k_decode, CompileOptions(lmul_eighths=16))
     with pytest.raises(NotImplementedError):
-        comp.compile(K.production_mul_mat_q4_k_decode, CompileOptions(matrix_extension="ime"))
-    a = comp.compile(K.production_mul_mat_q4_k_decode, CompileOptions())
-    assert comp.compile(K.production_mul_mat_q4_k_decode, CompileOptions()) is a  # reuse
+        comp.resolve(K.production_mul_mat_q4_k_decode, CompileOptions(matrix_extension="ime"))
+    a = comp.resolve(K.production_mul_mat_q4_k_decode, CompileOptions())
+    assert comp.resolve(K.production_mul_mat_q4_k_decode, CompileOptions()) is a  # reuse
     assert dict(a.metadata["bindings"]) == {}
 
 
 def _compiler():
-    import threading
-    comp = _Compiler.__new__(_Compiler)
-    comp.target, comp._cache, comp._lock = TARGET, {}, threading.RLock()
-    return comp
+    return _Registry(Toolchain(), TARGET)
 
 
 def test_source_bindings_follow_the_reference_compiler():
@@ -166,24 +160,24 @@ def test_source_bindings_follow_the_reference_compiler():
     staged = K.production_mul_mat_q4_k_staged
     assert staged.source_bindings == ("KC", "MC", "MR", "NC")
     with pytest.raises(CompilationError, match="'KC' requires one concrete --meta binding"):
-        comp.compile(staged, CompileOptions())
+        comp.resolve(staged, CompileOptions())
     with pytest.raises(CompilationError, match="'MR' requires"):
-        comp.compile(staged, CompileOptions(meta={"NC": 64, "KC": 512, "MC": 8}))
+        comp.resolve(staged, CompileOptions(meta={"NC": 64, "KC": 512, "MC": 8}))
     # examples/kernels/mul_mat/tuning.json "mul-mat:k1 q4_k prefill"
     tuned = {"NC": 64, "KC": 512, "MC": 8, "MR": 2}
-    a = comp.compile(staged, CompileOptions(meta=tuned))
+    a = comp.resolve(staged, CompileOptions(meta=tuned))
     assert list(a.metadata["bindings"].items()) == sorted(tuned.items())
-    assert comp.compile(staged, CompileOptions(meta=dict(tuned))) is a
-    b = comp.compile(staged, CompileOptions(meta={**tuned, "MR": 4}))
+    assert comp.resolve(staged, CompileOptions(meta=dict(tuned))) is a
+    b = comp.resolve(staged, CompileOptions(meta={**tuned, "MR": 4}))
     assert b is not a and b.metadata["bindings"]["MR"] == 4
     # a kernel without auto extents records whatever it is given
-    d = comp.compile(K.production_mul_mat_q4_k_decode, CompileOptions(meta={"NC": 64}))
+    d = comp.resolve(K.production_mul_mat_q4_k_decode, CompileOptions(meta={"NC": 64}))
     assert dict(d.metadata["bindings"]) == {"NC": 64}
-    assert d is not comp.compile(K.production_mul_mat_q4_k_decode, CompileOptions())
+    assert d is not comp.resolve(K.production_mul_mat_q4_k_decode, CompileOptions())
     for name in ("production_mul_mat_q4_0", "production_mul_mat_mxfp4",
                  "production_mul_mat_iq2_xxs_staged"):
         with pytest.raises(CompilationError, match="requires one concrete"):
-            comp.compile(K.DEFINITIONS[name], CompileOptions())
+            comp.resolve(K.DEFINITIONS[name], CompileOptions())
 
 
 def test_buffer_inference_and_contiguity():
