@@ -8,30 +8,36 @@ included, exactly as the reference's timed mul_mat (weft-kernel-performance.csv:
 ``value`` is the algorithmic HBM bytes of the call (encoded W + fp32 X + Xq
 write + fp32 Y = 25,427,520 B) divided by the measured time per call, in GB/s.
 
-Inputs are seeded synthetic data (weights ~ N(0, 0.02^2) quantized with the
-GGML reference quantizers restated in oracle/, activations ~ N(0, 1)) resident
-in HBM before timing.  For the HBM-bound decode cases the weights are rotated
-over enough copies (> 2 x the 256 MB Infinity Cache) that every call streams
-them from HBM.  A timed region is K back-to-back calls on the library's stream
-between two HIP events, bracketed by device synchronisation.
+Inputs are seeded synthetic data (weights ~ N(0, 0.02^2) quantized on the host
+by oracle/'s restatement of GGML's reference quantizers -- for IQ2_XXS a
+nearest-grid generator, not GGML's quantize_iq2_xxs -- and activations
+~ N(0, 1)), resident in HBM before timing.  Every case rotates its weights
+over enough copies (> 2 x the 256 MB Infinity Cache) that each call reads
+them from HBM.  Each case is timed three ways on the library's stream:
+  * ``us``: K back-to-back calls between two HIP events (the headline);
+  * ``cold_us``: BASELINE.md's protocol -- 512 MiB written to flush the
+    caches, then one call between two events; median of 20;
+  * ``graph_us``: the same back-to-back calls replayed from a captured HIP
+    graph (launch cost of a serving loop that captures its steps).
+Floors measured in the same run: an empty launch back to back, and one
+streaming-read launch of the same weight bytes (library probes); for the
+prefill shapes, the vendor's plain int8 GEMM (hipBLASLt through
+torch._int_mm) of the same M x N x K.  ``kernels`` lists what one call
+launched (the library's launch log).
 
-Secondary figures (the other BASELINE.json configs) ride in the same JSON
-line under ``configs``: W_down decode, the Q4_0 / IQ2_XXS / MXFP4 decode GEMVs,
-the Q4_K row dequantize, and the prefill mul_mats (Q4_K config 4 at N=4096 and
-N=11008, MXFP4 config 5b, Q4_0 and IQ2_XXS at the same shape), the latter
-against the int8 MFMA peak, plus the derived Q4K_I[16] GEMV and GGML's
-MUL_MAT_ID at a Mixtral-8x7B expert shape (ops counted per (token, expert)
-pair).
-
-The CPU baseline is oracle/'s restatement of GGML's generic MUL_MAT path
-(quantize_row_q8_K_ref + ggml_vec_dot_q4_K_q8_K_generic, rows over OpenMP
-threads), timed on this host on the same decode workload.
+CPU baseline: oracle/'s restatement of GGML's MUL_MAT (quantize_row_q8_K_ref
++ ggml_vec_dot_q4_K_q8_K_generic) on the same decode call, with GGML's
+thread schedule over every host thread (``value``), and single-threaded
+under the reference's kernel protocol: one warmup, a 64 MiB eviction before
+each of 10 timed calls, median (doc/experiments/protocol.md:46-55).
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import platform
+import statistics
 import sys
 import time
 
@@ -41,8 +47,11 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-INT8_PEAK_TOPS = 5000.0
+INT8_PEAK_TOPS = 5000.0   # dense int8 MFMA
+FP8_PEAK_TOPS = 5000.0    # dense fp8 MFMA: the rate of an fp4 x fp8 f8f6f4 product
+FP4_PEAK_TOPS = 10100.0   # dense fp4 / fp6 MFMA
 MALL_BYTES = 256 << 20
+FLUSH_BYTES = 512 << 20
 
 # name: (symbol, format, N, K, M, bound)
 CASES = {
@@ -60,13 +69,10 @@ CASES = {
     "mxfp4_prefill": ("production_mul_mat_mxfp4", "mxfp4", 4096, 4096, 512, "mfma"),
     "q4_0_prefill": ("production_mul_mat_q4_0", "q4_0", 4096, 4096, 512, "mfma"),
     "iq2_xxs_prefill": ("production_mul_mat_iq2_xxs_staged", "iq2_xxs", 4096, 4096, 512, "mfma"),
-    # adjacent format Q6_K (ggml-common.h:349-358) at the W_up shape; its
-    # prefill entry runs the GEMV kernel (no MFMA form yet)
+    # adjacent formats at the W_up shape (ggml-common.h:330-358, :211-217)
     "q6_k_decode": ("production_mul_mat_q6_k_decode", "q6_k", 11008, 4096, 1, "hbm"),
     "q6_k_prefill": ("production_mul_mat_q6_k", "q6_k", 4096, 4096, 512, "mfma"),
-    # adjacent format Q5_K (ggml-common.h:330-345), decode at the W_up shape
     "q5_k_decode": ("production_mul_mat_q5_k_decode", "q5_k", 11008, 4096, 1, "hbm"),
-    # adjacent format NVFP4 (ggml-common.h:211-217) at the W_up shape
     "nvfp4_decode": ("production_mul_mat_nvfp4_decode", "nvfp4", 11008, 4096, 1, "hbm"),
     # GGML MUL_MAT_ID (MoE) prefill at a Mixtral-8x7B FFN shape: 8 experts of
     # 14336 x 4096 Q4_K, 2 experts per token, 512 tokens (the grouped GEMM)
@@ -82,8 +88,10 @@ def parse():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--cpu-seconds", type=float, default=10.0,
-                   help="wall-clock budget of the CPU baseline sample")
+                   help="wall-clock budget of the all-threads CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-extra", action="store_true",
+                   help="skip the cold / graph timings and the floors")
     p.add_argument("--cases", default="all",
                    help="comma-separated secondary cases to run (default all; 'none' for "
                         "the headline only): " + ",".join(c for c in CASES if c != HEADLINE))
@@ -108,6 +116,17 @@ def profiled_traffic(name: str):
     return None
 
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
 class Bench:
     def __init__(self):
         import torch
@@ -125,20 +144,23 @@ class Bench:
             "mxfp4": [self.dev_copy(o.kvalues_mxfp4()), self.dev_copy(o.e8m0_half_table())],
             "nvfp4": [self.dev_copy(o.kvalues_mxfp4()), self.dev_copy(o.ue4m3_table())],
         }
+        self.flush_buf = None
 
     def dev_copy(self, a: np.ndarray):
         return self.torch.from_numpy(np.ascontiguousarray(a)).to(self.dev)
 
+    def events(self):
+        return (self.torch.cuda.Event(enable_timing=True), self.torch.cuda.Event(enable_timing=True))
+
     def time_calls(self, launch, steps, warmup):
-        """launch(i) enqueues call i; returns seconds per call over `steps`,
-        from two HIP events on the stream the library launches on."""
+        """launch(i) enqueues call i; seconds per call over `steps`
+        back-to-back calls, from two HIP events on the library's stream."""
         torch = self.torch
         for i in range(warmup):
             launch(i)
         torch.cuda.synchronize()
         self._lib.check("warmup")
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
+        start, end = self.events()
         torch.cuda.synchronize()
         start.record(self.stream)
         for i in range(steps):
@@ -148,110 +170,236 @@ class Bench:
         self._lib.check("timed region")
         return start.elapsed_time(end) / 1e3 / steps
 
+    def time_cold(self, launch, reps=20):
+        """Median seconds of one call after the caches are flushed by writing
+        FLUSH_BYTES (BASELINE.md's headline protocol)."""
+        torch = self.torch
+        if self.flush_buf is None:
+            self.flush_buf = torch.empty(FLUSH_BYTES // 4, dtype=torch.float32, device=self.dev)
+        times = []
+        for i in range(reps):
+            self.flush_buf.fill_(float(i))
+            start, end = self.events()
+            start.record(self.stream)
+            launch(i)
+            end.record(self.stream)
+            torch.cuda.synchronize()
+            times.append(start.elapsed_time(end) / 1e3)
+        self._lib.check("cold calls")
+        return statistics.median(times)
 
-def run_case(b: Bench, name: str, steps: int, warmup: int) -> dict:
+    def time_graph(self, launch, calls=20, replays=5):
+        """Seconds per call when `calls` back-to-back calls are replayed from
+        one captured HIP graph."""
+        torch = self.torch
+        side = torch.cuda.Stream()
+        side.wait_stream(self.stream)
+        g = torch.cuda.CUDAGraph()
+        try:
+            with torch.cuda.stream(side):
+                self._lib.set_stream(side.cuda_stream)
+                with torch.cuda.graph(g, stream=side):
+                    for i in range(calls):
+                        launch(i)
+        finally:
+            self._lib.set_stream(self.stream.cuda_stream)
+        self._lib.check("graph capture")
+        g.replay()
+        torch.cuda.synchronize()
+        start, end = self.events()
+        start.record(self.stream)
+        for _ in range(replays):
+            g.replay()
+        end.record(self.stream)
+        torch.cuda.synchronize()
+        self._lib.check("graph replay")
+        return start.elapsed_time(end) / 1e3 / (calls * replays)
+
+    def floors(self, nbytes_list):
+        """Per-launch floors on this stream: an empty kernel back to back, and
+        the best single streaming-read launch of each byte count."""
+        torch = self.torch
+        lib = self.lib
+        out = {"empty_launch_us": round(self.time_calls(lambda i: lib.weft_hip_probe_empty(), 200, 20) * 1e6, 3)}
+        sink = torch.empty(1 << 16, dtype=torch.int32, device=self.dev)
+        reads = {}
+        for nbytes in nbytes_list:
+            n16 = (nbytes + 15) // 16 * 16
+            copies = max(2, int(np.ceil(2 * MALL_BYTES / n16)) + 1)
+            bufs = [torch.zeros(n16, dtype=torch.uint8, device=self.dev) for _ in range(copies)]
+            best = None
+            for grid in (256, 512, 1024, 2048):
+                sec = self.time_calls(lambda i: lib.weft_hip_probe_read(bufs[i % copies].data_ptr(), n16,
+                                                                        sink.data_ptr(), grid), 100, 10)
+                if best is None or sec < best[0]:
+                    best = (sec, grid)
+            reads[str(nbytes)] = {"us": round(best[0] * 1e6, 3), "GBs": round(nbytes / best[0] / 1e9, 1),
+                                  "grid": best[1]}
+            del bufs
+            torch.cuda.empty_cache()
+        out["stream_read"] = reads
+        return out
+
+    def vendor_int8_gemm(self, m, n, k):
+        """hipBLASLt's plain int8 GEMM (torch._int_mm) of the same shape:
+        seconds per call, back to back."""
+        torch = self.torch
+        a = torch.randint(-127, 128, (m, k), dtype=torch.int8, device=self.dev)
+        b = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=self.dev).t()
+        try:
+            for _ in range(3):
+                torch._int_mm(a, b)
+            torch.cuda.synchronize()
+            start, end = self.events()
+            start.record(self.stream)
+            for _ in range(20):
+                torch._int_mm(a, b)
+            end.record(self.stream)
+            torch.cuda.synchronize()
+            return start.elapsed_time(end) / 1e3 / 20
+        except RuntimeError:
+            return None
+
+
+def run_case(b: Bench, name: str, steps: int, warmup: int, extra: bool) -> dict:
     """Time one case; returns its figures (algorithmic bytes / ops, rate, roofline fraction)."""
     import oracle as o
     sym, fmt, n, k, m, bound = CASES[name]
     w = o.quantize(fmt, o.seeded_normal(1, (n, k), 0.02))
     torch = b.torch
-    copies = 1
-    if bound == "hbm":  # stream the weights from HBM on every call
-        copies = max(2, int(np.ceil(2 * MALL_BYTES / w.nbytes)) + 1)
-    wd = [b.dev_copy(w) for _ in range(copies)]
+    copies = max(2, int(np.ceil(2 * MALL_BYTES / w.nbytes)) + 1)
     fn = getattr(b.lib, sym)
-    if m == 0:  # row dequantize of the whole matrix
-        y = torch.empty(n * k, dtype=torch.float32, device=b.dev)
-
-        def launch(i):
-            fn(wd[i % copies].data_ptr(), y.data_ptr(), n * k)
-
-        nbytes = w.nbytes + 4 * n * k
-    elif m < 0:  # GEMV over the Q4K_I[16] layout: pack every copy once, outside the timing
-        packed = [torch.empty_like(t) for t in wd]
-        pack = getattr(b.lib, sym + "_W_pack")
-        for src, dst in zip(wd, packed):
-            pack(src.data_ptr(), dst.data_ptr(), n, k)
-        torch.cuda.synchronize()
-        b._lib.check(sym + "_W_pack")
-        wd = packed
-        xq = b.dev_copy(o.quantize("q8_k", o.seeded_normal(2, (1, k))))
-        y = torch.empty(n, dtype=torch.float32, device=b.dev)
-
-        def launch(i):
-            fn(wd[i % copies].data_ptr(), xq.data_ptr(), y.data_ptr(), n, k)
-
-        nbytes = w.nbytes + xq.numel() + 4 * n
-    elif sym == "weft_ggml_mul_mat_id":
-        # one quantized expert matrix copied MOE_EXPERTS times (the timing
-        # does not depend on the values); seeded top-MOE_USED choices per token
+    if sym == "weft_ggml_mul_mat_id":
+        # expert matrices copied from one quantized matrix (the timing does
+        # not depend on the values); the expert set itself is rotated
         from weft_amd import ggml as G
-        experts = b.dev_copy(np.concatenate([w] * MOE_EXPERTS))
-        del wd
-        wd = [experts]
+        bank = b.dev_copy(np.concatenate([w] * MOE_EXPERTS))
+        copies = max(2, int(np.ceil(2 * MALL_BYTES / bank.numel())) + 1)
+        wd = [bank] + [bank.clone() for _ in range(copies - 1)]
         rng = np.random.default_rng(3)
         ids_h = np.stack([rng.choice(MOE_EXPERTS, MOE_USED, replace=False) for _ in range(m)]).astype(np.int32)
         ids = b.dev_copy(ids_h)
         x = b.dev_copy(o.seeded_normal(2, (m, k)))
         y = torch.empty(m * MOE_USED * n, dtype=torch.float32, device=b.dev)
-        s0 = G.tensor(G.Q4_K, (k, n, MOE_EXPERTS), experts.data_ptr())
         s1 = G.tensor(G.F32, (k, 1, m), x.data_ptr())
         it = G.tensor(G.I32, (MOE_USED, m), ids.data_ptr())
         d = G.tensor(G.F32, (n, MOE_USED, m), y.data_ptr())
-        wsize = G.mul_mat_id_work_size(s0, s1, it)
+        s0s = [G.tensor(G.Q4_K, (k, n, MOE_EXPERTS), t.data_ptr()) for t in wd]
+        wsize = G.mul_mat_id_work_size(s0s[0], s1, it)
         work = torch.empty(wsize, dtype=torch.uint8, device=b.dev)
 
         def launch(i):
-            G.mul_mat_id(s0, s1, it, d, work.data_ptr(), wsize)
+            G.mul_mat_id(s0s[i % copies], s1, it, d, work.data_ptr(), wsize)
 
         nbytes = MOE_EXPERTS * w.nbytes + 4 * m * k + o.record_bytes("q8_k", k) * m + 4 * m * MOE_USED * n
         m *= MOE_USED  # products: one per (token, expert) pair
     else:
-        act = o.ACT_OF[fmt]
-        x = b.dev_copy(o.seeded_normal(2, (m, k)))
-        xq = torch.empty(o.record_bytes(act, k) * m, dtype=torch.uint8, device=b.dev)
-        y = torch.empty(m * n, dtype=torch.float32, device=b.dev)
-        tabs = [t.data_ptr() for t in b.tables.get(fmt, [])]
+        wd = [b.dev_copy(w) for _ in range(copies)]
+        if m == 0:  # row dequantize of the whole matrix
+            y = torch.empty(n * k, dtype=torch.float32, device=b.dev)
 
-        def launch(i):
-            fn(wd[i % copies].data_ptr(), x.data_ptr(), xq.data_ptr(), *tabs, y.data_ptr(), n, k, m)
+            def launch(i):
+                fn(wd[i % copies].data_ptr(), y.data_ptr(), n * k)
 
-        nbytes = w.nbytes + 4 * m * k + xq.numel() + 4 * m * n
+            nbytes = w.nbytes + 4 * n * k
+        elif m < 0:  # GEMV over the Q4K_I[16] layout: pack every copy once, outside the timing
+            packed = [torch.empty_like(t) for t in wd]
+            pack = getattr(b.lib, sym + "_W_pack")
+            for src, dst in zip(wd, packed):
+                pack(src.data_ptr(), dst.data_ptr(), n, k)
+            torch.cuda.synchronize()
+            b._lib.check(sym + "_W_pack")
+            wd = packed
+            xq = b.dev_copy(o.quantize("q8_k", o.seeded_normal(2, (1, k))))
+            y = torch.empty(n, dtype=torch.float32, device=b.dev)
+
+            def launch(i):
+                fn(wd[i % copies].data_ptr(), xq.data_ptr(), y.data_ptr(), n, k)
+
+            nbytes = w.nbytes + xq.numel() + 4 * n
+        else:
+            act = o.ACT_OF[fmt]
+            x = b.dev_copy(o.seeded_normal(2, (m, k)))
+            xq = torch.empty(o.record_bytes(act, k) * m, dtype=torch.uint8, device=b.dev)
+            y = torch.empty(m * n, dtype=torch.float32, device=b.dev)
+            tabs = [t.data_ptr() for t in b.tables.get(fmt, [])]
+
+            def launch(i):
+                fn(wd[i % copies].data_ptr(), x.data_ptr(), xq.data_ptr(), *tabs, y.data_ptr(), n, k, m)
+
+            nbytes = w.nbytes + 4 * m * k + xq.numel() + 4 * m * n
     if bound == "mfma":
-        steps, warmup = max(3, steps // 20), 3
+        steps, warmup = max(20, steps // 4), 3
+    b._lib.launch_log()
+    launch(0)
+    torch.cuda.synchronize()
+    log = b._lib.launch_log()
+    kernels = [f"{k} x{log.count(k)}" if log.count(k) > 1 else k for k in dict.fromkeys(log)]
     sec = b.time_calls(launch, steps, warmup)
-    del wd
-    torch.cuda.empty_cache()
     out = {"symbol": sym, "N": n, "K": k, "M": max(m, 1) if m < 0 else m, "us": round(sec * 1e6, 3),
            "algorithmic_bytes": int(nbytes), "GBs": round(nbytes / sec / 1e9, 2),
-           "weight_copies_rotated": copies, "steps": steps}
+           "weight_copies_rotated": copies, "steps": steps, "kernels": kernels}
+    if extra:
+        out["cold_us"] = round(b.time_cold(launch) * 1e6, 3)
+        out["graph_us"] = round(b.time_graph(launch) * 1e6, 3)
     if bound == "hbm":
         out["frac_hbm_peak"] = round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4)
     else:
-        tops = 2.0 * m * n * k / sec / 1e12
-        out.update({"ops": 2 * m * n * k, "TOPS": round(tops, 2),
-                    "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)})
+        ops = 2.0 * m * n * k
+        tops = ops / sec / 1e12
+        out.update({"ops": int(ops), "TOPS": round(tops, 2)})
+        if fmt == "mxfp4":
+            # fp4 weights x fp8 activation planes on the block-scaled MFMA
+            out["frac_fp8_rate"] = round(tops / FP8_PEAK_TOPS, 4)
+            out["frac_fp4_peak"] = round(tops / FP4_PEAK_TOPS, 4)
+        else:
+            out["frac_int8_peak"] = round(tops / INT8_PEAK_TOPS, 4)
+        if extra and sym != "weft_ggml_mul_mat_id":
+            vs = b.vendor_int8_gemm(m, n, k)
+            if vs is not None:
+                out["vendor_int8_gemm_us"] = round(vs * 1e6, 3)
+                out["vendor_int8_gemm_TOPS"] = round(ops / vs / 1e12, 2)
+    del wd
+    torch.cuda.empty_cache()
     return out
 
 
 def cpu_baseline(n, k, budget_s):
+    """GGML's MUL_MAT restated in oracle/ on the headline call: all threads
+    with GGML's schedule for ~budget_s, then one thread under the reference's
+    kernel protocol."""
     import oracle as o
     w = o.quantize("q4_k", o.seeded_normal(1, (n, k), 0.02))
     x = o.seeded_normal(2, (1, k))
+    nbytes = w.nbytes + 4 * k + (k // 256) * 292 + 4 * n
     threads = o.max_threads()
-    o.mul_mat("q4_k", w, x, n, k, 1, threads=threads)  # warmup
+    xq = np.zeros((1, o.record_bytes("q8_k", k)), np.uint8)
+    y = np.empty((1, n), np.float32)
+    o.mul_mat_ggml("q4_k", w, x, n, k, 1, threads=threads, xq=xq, y=y)  # warmup
     reps, t0 = 0, time.perf_counter()
     while True:
-        o.mul_mat("q4_k", w, x, n, k, 1, threads=threads)
+        o.mul_mat_ggml("q4_k", w, x, n, k, 1, threads=threads, xq=xq, y=y)
         reps += 1
         el = time.perf_counter() - t0
         if el >= budget_s or reps >= 100000:
             break
     per = el / reps
-    nbytes = w.nbytes + 4 * k + (k // 256) * 292 + 4 * n
+    # single thread: 1 warmup, 64 MiB eviction before each of 10 timed calls, median
+    evict = np.zeros(64 << 20, np.uint8)
+    o.mul_mat_ggml("q4_k", w, x, n, k, 1, threads=1, xq=xq, y=y)
+    singles = []
+    for _ in range(10):
+        o.evict(evict)
+        t = time.perf_counter()
+        o.mul_mat_ggml("q4_k", w, x, n, k, 1, threads=1, xq=xq, y=y)
+        singles.append(time.perf_counter() - t)
+    one = statistics.median(singles)
     return {"value": round(nbytes / per / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{reps} full decode calls (N={n}, K={k}, M=1) in {el:.1f} s, "
-                      f"{per * 1e3:.3f} ms/call, OpenMP over {threads} host threads"}
+            "sample": f"{reps} full decode calls (N={n}, K={k}, M=1) in {el:.1f} s, {per * 1e3:.3f} ms/call, "
+                      f"GGML's MUL_MAT thread schedule over {threads} host threads",
+            "single_thread": {"us": round(one * 1e6, 1), "GBs": round(nbytes / one / 1e9, 3),
+                              "protocol": "1 warmup, 64 MiB eviction before each of 10 calls, median"},
+            "cpu_model": cpu_model(), "nproc": os.cpu_count()}
 
 
 def main():
@@ -262,8 +410,9 @@ def main():
         sys.exit(2)
     b = Bench()
     steps, warmup = args.steps, args.warmup
+    extra = not args.no_extra
 
-    head = run_case(b, HEADLINE, steps, warmup)
+    head = run_case(b, HEADLINE, steps, warmup, extra)
     sec = head["us"] / 1e6
     gbs = head["GBs"]
     if args.cases == "all":
@@ -272,16 +421,30 @@ def main():
         names = []
     else:
         names = [c for c in args.cases.split(",") if c]
-    secondary = {name: run_case(b, name, steps, warmup) for name in names}
+    secondary = {name: run_case(b, name, steps, warmup, extra) for name in names}
+    floors = None
+    if extra:
+        byte_counts = sorted({head["algorithmic_bytes"]} |
+                             {v["algorithmic_bytes"] for v in secondary.values() if v.get("frac_hbm_peak")})
+        floors = b.floors(byte_counts)
     if args.calibrate_copy:
-        n = args.calibrate_copy << 20
-        src = b.torch.empty(n, dtype=b.torch.uint8, device=b.dev)
+        nb = args.calibrate_copy << 20
+        src = b.torch.empty(nb, dtype=b.torch.uint8, device=b.dev)
         dst = b.torch.empty_like(src)
         b.torch.cuda.synchronize()
         dst.copy_(src)
         b.torch.cuda.synchronize()
     cpu = None if args.no_cpu else cpu_baseline(11008, 4096, args.cpu_seconds)
 
+    roofline = {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": profiled_traffic("q4k_decode_w_up"),
+                "algorithmic_bytes": head["algorithmic_bytes"],
+                "kernel": head["kernels"][0] if len(head["kernels"]) == 1 else ",".join(head["kernels"])}
+    if floors is not None:
+        read = floors["stream_read"][str(head["algorithmic_bytes"])]
+        roofline["floor"] = {"empty_launch_us": floors["empty_launch_us"], "stream_read_us": read["us"],
+                             "stream_read_frac": round(read["GBs"] / HBM_PEAK_GBS, 4),
+                             "kernel_vs_read": round(head["us"] / read["us"], 3)}
     line = {
         "metric": "Q4_K mul_mat: decode GB/s (% of 8 TB/s) + prefill TOPS (% int8 MFMA peak)",
         "value": gbs,
@@ -294,18 +457,17 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic (seeded N(0,0.02) weights quantized by the oracle's GGML reference "
-                "quantizers, N(0,1) activations)",
+        "data": "synthetic (seeded N(0,0.02) weights quantized on the host by the oracle's restated GGML "
+                "reference quantizers, IQ2_XXS by a nearest-grid generator; N(0,1) activations)",
         "config": {"workload": "production_mul_mat_q4_k_decode, config 3 W_up: N=11008 K=4096 "
                                "M=1, Q8_K activation quantize inside the timed call",
                    "N": 11008, "K": 4096, "M": 1,
                    "weight_copies_rotated": head["weight_copies_rotated"]},
-        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": profiled_traffic("q4k_decode_w_up"),
-                     "algorithmic_bytes": head["algorithmic_bytes"],
-                     "kernel": "q4k_gemv_m1_kernel<1,1024,2>"},
+        "roofline": roofline,
         "cpu_baseline": cpu,
+        "headline_cold_us": head.get("cold_us"),
+        "headline_graph_us": head.get("graph_us"),
+        "floors": floors,
         "configs": secondary,
     }
     print(json.dumps(line))

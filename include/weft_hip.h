@@ -59,6 +59,16 @@ int weft_hip_device_arch(int dev, char *buf, size_t len);
  * "weft-hip-artifact", gfx_arch / wavefront_size in place of march / abi /
  * vlen_bits). */
 const char *weft_hip_artifact(void);
+/* Names of the kernels this thread launched since the last read, comma
+ * separated, copied into buf (len bytes with the NUL) and cleared; returns
+ * the log's length.  buf == NULL only returns the length. */
+size_t weft_hip_launch_log(char *buf, size_t len);
+/* Measurement probes on the current stream: an empty launch, and one launch
+ * that reads `bytes` (a multiple of 16, 16-byte aligned) of device memory
+ * with `grid` x 512 threads and writes one word per wave into sink
+ * (grid * 8 words). */
+void weft_hip_probe_empty(void);
+void weft_hip_probe_read(const void *src, size_t bytes, uint32_t *sink, int grid);
 
 /* ------------------------------------------------------ row dequantize */
 /* examples/kernels/dequantize/q4_0.py:9-13; repro row_dequantize_runtime.cpp:177 */

@@ -77,6 +77,8 @@ def _declare(l: ctypes.CDLL) -> None:
         "wo_mul_mat_f64": ([ctypes.c_int, _P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int], None),
         "wo_int_partials": ([ctypes.c_int, _P, _P, _I64, _P], _I64),
         "wo_max_threads": ([], ctypes.c_int),
+        "wo_mul_mat_ggml": ([ctypes.c_int, _P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int], None),
+        "wo_evict": ([_P, ctypes.c_size_t], None),
     }
     for fmt in ("q4_0", "q4_K", "mxfp4", "iq2_xxs", "q6_K", "q5_K", "nvfp4", "q8_0", "q8_K"):
         sig[f"wo_quantize_row_{fmt}"] = ([_P, _P, _I64], None)
@@ -209,6 +211,24 @@ def mul_mat(fmt: str, W: np.ndarray, X: np.ndarray, n: int, k: int, m: int,
     y = np.empty((m, n), np.float32)
     lib().wo_mul_mat(FORMATS[fmt], _ptr(W), _ptr(X), _ptr(xq), _ptr(y), n, k, m, threads)
     return xq, y
+
+
+def mul_mat_ggml(fmt: str, W: np.ndarray, X: np.ndarray, n: int, k: int, m: int,
+                 threads: int = 0, xq: np.ndarray | None = None, y: np.ndarray | None = None):
+    """GGML MUL_MAT with GGML's thread schedule (quantize split by blocks,
+    chunked rows from a shared counter): returns (Xq, Y)."""
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    if xq is None:
+        xq = np.zeros((m, record_bytes(ACT_OF[fmt], k)), np.uint8)
+    if y is None:
+        y = np.empty((m, n), np.float32)
+    lib().wo_mul_mat_ggml(FORMATS[fmt], _ptr(W), _ptr(X), _ptr(xq), _ptr(y), n, k, m, threads)
+    return xq, y
+
+
+def evict(buf: np.ndarray) -> None:
+    lib().wo_evict(_ptr(buf), buf.nbytes)
 
 
 def mul_mat_q(fmt: str, W: np.ndarray, Xq: np.ndarray, n: int, k: int, m: int,

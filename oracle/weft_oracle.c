@@ -1218,6 +1218,66 @@ void wo_mul_mat(int fmt, const uint8_t *W, const float *X, uint8_t *Xq, float *Y
   wo_mul_mat_q(fmt, W, Xq, Y, N, K, M, nthreads);
 }
 
+/* ggml_compute_forward_mul_mat's schedule, ggml-cpu/ggml-cpu.c:1313-1443
+ * (from_float split by blocks, ggml_barrier, chunk plan, shared counter) and
+ * ggml_compute_forward_mul_mat_one_chunk's 16 x 16 blocking, :1155-1243.
+ * 2-D case: ne1 = M activation rows, ne0 = N outputs per row. */
+void wo_mul_mat_ggml(int fmt, const uint8_t *W, const float *X, uint8_t *Xq, float *Y,
+                     int64_t N, int64_t K, int64_t M, int nthreads) {
+  const vec_dot_fn dot = select_vec_dot(fmt);
+  const int q80 = (fmt == WO_Q4_0 || fmt == WO_MXFP4 || fmt == WO_NVFP4);
+  const int64_t bs = q80 ? QK8_0 : QK_K;
+  const size_t blk_bytes = q80 ? Q8_0_BYTES : Q8_K_BYTES;
+  const size_t wrow = wo_weight_row_bytes(fmt, K), xrow = wo_act_row_bytes(fmt, K);
+  if (nthreads <= 0) nthreads = wo_max_threads();
+  _Atomic int64_t next_chunk = 0;
+#pragma omp parallel num_threads(nthreads)
+  {
+    const int nth = omp_get_num_threads(), ith = omp_get_thread_num();
+    const int64_t nb = K / bs;
+    for (int64_t m = 0; m < M; ++m) {
+      const int64_t b0 = ith * nb / nth, b1 = (ith + 1) * nb / nth;
+      if (b1 > b0) {
+        if (q80)
+          wo_quantize_row_q8_0(X + m * K + b0 * bs, Xq + m * xrow + b0 * blk_bytes, (b1 - b0) * bs);
+        else
+          wo_quantize_row_q8_K(X + m * K + b0 * bs, Xq + m * xrow + b0 * blk_bytes, (b1 - b0) * bs);
+      }
+    }
+    if (ith == 0) next_chunk = nth;  /* every thread starts at its own index */
+#pragma omp barrier
+    const int64_t nr0 = N, nr1 = M;
+    const int64_t chunk_size = (nr0 == 1 || nr1 == 1) ? 64 : 16;
+    int64_t nchunk0 = (nr0 + chunk_size - 1) / chunk_size;
+    int64_t nchunk1 = (nr1 + chunk_size - 1) / chunk_size;
+    if (nchunk0 * nchunk1 < (int64_t)nth * 4) {
+      nchunk0 = nr0 > nr1 ? nth : 1;
+      nchunk1 = nr0 > nr1 ? 1 : nth;
+    }
+    const int64_t dr0 = (nr0 + nchunk0 - 1) / nchunk0, dr1 = (nr1 + nchunk1 - 1) / nchunk1;
+    int64_t chunk = ith;
+    while (chunk < nchunk0 * nchunk1) {
+      const int64_t i0 = chunk % nchunk0, i1 = chunk / nchunk0;
+      const int64_t r0a = dr0 * i0, r0b = r0a + dr0 < nr0 ? r0a + dr0 : nr0;
+      const int64_t r1a = dr1 * i1, r1b = r1a + dr1 < nr1 ? r1a + dr1 : nr1;
+      float tmp[16];
+      for (int64_t bb1 = r1a; bb1 < r1b; bb1 += 16)
+        for (int64_t bb0 = r0a; bb0 < r0b; bb0 += 16)
+          for (int64_t r1 = bb1; r1 < bb1 + 16 && r1 < r1b; ++r1) {
+            int64_t r0 = bb0;
+            for (; r0 < bb0 + 16 && r0 < r0b; ++r0) tmp[r0 - bb0] = dot(W + r0 * wrow, Xq + r1 * xrow, K);
+            memcpy(Y + r1 * N + bb0, tmp, (size_t)(r0 - bb0) * sizeof(float));
+          }
+      if (nth >= nchunk0 * nchunk1) break;
+      chunk = __atomic_fetch_add(&next_chunk, 1, __ATOMIC_RELAXED);
+    }
+  }
+}
+
+void wo_evict(uint8_t *buf, size_t bytes) {
+  for (size_t i = 0; i < bytes; i += 64) buf[i] = (uint8_t)(buf[i] + 1);
+}
+
 int64_t wo_int_partials(int fmt, const uint8_t *w, const uint8_t *x, int64_t k, int32_t *out) {
   int64_t n = 0;
   if (fmt == WO_Q4_0 || fmt == WO_MXFP4) {

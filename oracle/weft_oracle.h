@@ -114,6 +114,21 @@ void wo_mul_mat_f64(int fmt, const uint8_t *W, const uint8_t *Xq, double *E,
 int64_t wo_int_partials(int fmt, const uint8_t *w, const uint8_t *x, int64_t k,
                         int32_t *out);
 
+/* GGML's threaded MUL_MAT as ggml_compute_forward_mul_mat schedules it
+ * (ggml-cpu/ggml-cpu.c:1313-1443) for a 2-D F32 src1: thread ith quantizes
+ * blocks [ith*nb/nth, (ith+1)*nb/nth) of every row, then all threads take
+ * chunks of dr0 weight rows x dr1 activation rows (chunk size 16, 64 when
+ * either side is a single row; one chunk per thread along the longer side
+ * when there are fewer than 4 chunks per thread), the first at their own
+ * index and the rest from a shared counter, and walk a chunk in 16 x 16
+ * blocks.  nthreads <= 0: all OpenMP threads. */
+void wo_mul_mat_ggml(int fmt, const uint8_t *W, const float *X, uint8_t *Xq,
+                     float *Y, int64_t N, int64_t K, int64_t M, int nthreads);
+
+/* Walk (read and write) `bytes` of `buf`: the reference timing protocol's
+ * cache eviction between timed calls (doc/experiments/protocol.md:46-55). */
+void wo_evict(uint8_t *buf, size_t bytes);
+
 /* Threads OpenMP would use by default (for reporting the CPU baseline). */
 int wo_max_threads(void);
 

@@ -60,6 +60,12 @@ def load() -> ctypes.CDLL:
             lib.weft_hip_device_count.restype = ctypes.c_int
             lib.weft_hip_device_arch.argtypes = [ctypes.c_int, ctypes.c_char_p, ctypes.c_size_t]
             lib.weft_hip_device_arch.restype = ctypes.c_int
+            lib.weft_hip_launch_log.argtypes = [ctypes.c_char_p, ctypes.c_size_t]
+            lib.weft_hip_launch_log.restype = ctypes.c_size_t
+            lib.weft_hip_probe_empty.argtypes = []
+            lib.weft_hip_probe_empty.restype = None
+            lib.weft_hip_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int]
+            lib.weft_hip_probe_read.restype = None
             _bind_ggml(lib)
             artifact = json.loads(lib.weft_hip_artifact())
             for kernel in artifact["kernels"]:
@@ -131,3 +137,12 @@ def synchronize() -> None:
     if code != 0:
         load().weft_hip_get_last_error()
         raise HipError(code, "synchronize")
+
+
+def launch_log() -> list[str]:
+    """Kernels this thread launched through the library since the last read."""
+    lib = load()
+    n = lib.weft_hip_launch_log(None, 0)
+    buf = ctypes.create_string_buffer(n + 1)
+    lib.weft_hip_launch_log(buf, n + 1)
+    return [k for k in buf.value.decode().split(",") if k]

@@ -562,7 +562,7 @@ void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t*
       const int g1 = (int)((N + a.rows_per_wg - 1) / a.rows_per_wg);
       each(a, g1, [&](const Q4KArgs& b, dim3 g) {
         q4k_gemv_m1_kernel<1, 1024, 2><<<g, 1024, row_lds, current_stream()>>>(b);
-        check_launch();
+        check_launch("q4k_gemv_m1_kernel");
       });
       return;
     }
@@ -579,7 +579,7 @@ void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t*
           q4k_gemv_ks_kernel<2, 1024><<<g, 1024, lds, current_stream()>>>(b);
         else
           q4k_gemv_ks_kernel<3, 768><<<g, 768, lds, current_stream()>>>(b);
-        check_launch();
+        check_launch("q4k_gemv_ks_kernel");
       });
       return;
     }
@@ -605,7 +605,7 @@ void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t*
         launch_one<1, NT>(a16, g, lds, b);
       else
         launch_one<kMaxRowsPerPass, NT>(a16, g, lds, b);
-      check_launch();
+      check_launch("q4k_gemv_kernel");
     });
   }
 }

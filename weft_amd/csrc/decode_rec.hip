@@ -270,7 +270,7 @@ bool decode_rec_m1(int fmt, const uint8_t* W, const float* X, uint8_t* Xq, const
     rec_gemv_m1_kernel<true><<<grid, kRecThreads, lds, current_stream()>>>(a);
   else
     rec_gemv_m1_kernel<false><<<grid, kRecThreads, lds, current_stream()>>>(a);
-  check_launch();
+  check_launch("rec_gemv_m1_kernel");
   return true;
 }
 

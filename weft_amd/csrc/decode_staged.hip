@@ -580,7 +580,7 @@ void launch(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_
     a.pair = PairArgs{};
     if (pr == nullptr) {
       staged_gemv_kernel<F><<<grid, kThreads, fixed + row_lds * a.mb, current_stream()>>>(a);
-      check_launch();
+      check_launch("staged_gemv_kernel");
       continue;
     }
     for (int p0 = 0; p0 < n_pairs; p0 += kMaxGridY) {
@@ -588,7 +588,7 @@ void launch(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_
       a.pair.pair0 = p0;
       const dim3 g((unsigned)grid, (unsigned)std::min(kMaxGridY, n_pairs - p0));
       staged_gemv_kernel<F><<<g, kThreads, fixed + row_lds, current_stream()>>>(a);
-      check_launch();
+      check_launch("staged_gemv_kernel");
     }
   }
 }

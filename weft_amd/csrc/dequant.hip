@@ -286,7 +286,7 @@ void row_dequantize_q4_k(const uint8_t* W, float* Y, size_t K) {
     dq_q4k_kernel<U, false, true><<<g, kThreads, 0, current_stream()>>>(W, Y, nsb);
   else
     dq_q4k_kernel<U, false, false><<<g, kThreads, 0, current_stream()>>>(W, Y, nsb);
-  check_launch();
+  check_launch("dq_q4k_kernel");
 }
 
 void row_dequantize_nvfp4(const uint8_t* W, const int8_t* codebook, const float* scale, float* Y,
@@ -301,7 +301,7 @@ void row_dequantize_nvfp4(const uint8_t* W, const int8_t* codebook, const float*
     dq_nvfp4_kernel<true><<<g, kThreads, 0, current_stream()>>>(W, codebook, scale, Y, nb);
   else
     dq_nvfp4_kernel<false><<<g, kThreads, 0, current_stream()>>>(W, codebook, scale, Y, nb);
-  check_launch();
+  check_launch("dq_nvfp4_kernel");
 }
 
 void row_dequantize_q5_k(const uint8_t* W, float* Y, size_t K) {
@@ -315,7 +315,7 @@ void row_dequantize_q5_k(const uint8_t* W, float* Y, size_t K) {
     dq_q5k_kernel<U, true><<<g, kThreads, 0, current_stream()>>>(W, Y, nsb);
   else
     dq_q5k_kernel<U, false><<<g, kThreads, 0, current_stream()>>>(W, Y, nsb);
-  check_launch();
+  check_launch("dq_q5k_kernel");
 }
 
 void row_dequantize_q6_k(const uint8_t* W, float* Y, size_t K) {
@@ -329,7 +329,7 @@ void row_dequantize_q6_k(const uint8_t* W, float* Y, size_t K) {
     dq_q6k_kernel<U, true><<<g, kThreads, 0, current_stream()>>>(W, Y, nsb);
   else
     dq_q6k_kernel<U, false><<<g, kThreads, 0, current_stream()>>>(W, Y, nsb);
-  check_launch();
+  check_launch("dq_q6k_kernel");
 }
 
 void row_dequantize_q4_0(const uint8_t* W, float* Y, size_t K) {
@@ -342,7 +342,7 @@ void row_dequantize_q4_0(const uint8_t* W, float* Y, size_t K) {
     dq_32_kernel<false, true><<<g, kThreads, 0, current_stream()>>>(W, nullptr, nullptr, Y, nb);
   else
     dq_32_kernel<false, false><<<g, kThreads, 0, current_stream()>>>(W, nullptr, nullptr, Y, nb);
-  check_launch();
+  check_launch("dq_32_kernel");
 }
 
 void row_dequantize_mxfp4(const uint8_t* W, const int8_t* codebook, const float* scale, float* Y,
@@ -357,7 +357,7 @@ void row_dequantize_mxfp4(const uint8_t* W, const int8_t* codebook, const float*
     dq_32_kernel<true, true><<<g, kThreads, 0, current_stream()>>>(W, codebook, scale, Y, nb);
   else
     dq_32_kernel<true, false><<<g, kThreads, 0, current_stream()>>>(W, codebook, scale, Y, nb);
-  check_launch();
+  check_launch("dq_32_kernel");
 }
 
 void row_dequantize_iq2_xxs(const uint8_t* W, const int8_t* grid, const int8_t* signs, float* Y,
@@ -371,7 +371,7 @@ void row_dequantize_iq2_xxs(const uint8_t* W, const int8_t* grid, const int8_t* 
     dq_iq2xxs_kernel<true><<<grid_for(nsb), kThreads, 0, current_stream()>>>(W, grid, signs, Y, nsb);
   else
     dq_iq2xxs_kernel<false><<<grid_for(nsb), kThreads, 0, current_stream()>>>(W, grid, signs, Y, nsb);
-  check_launch();
+  check_launch("dq_iq2xxs_kernel");
 }
 
 }  // extern "C"

@@ -270,7 +270,7 @@ void q4k_i16_pack(const uint8_t* source, uint8_t* target, size_t M, size_t K) {
   }
   q4k_i16_pack_kernel<<<(unsigned)blocks, 256, 0, current_stream()>>>(source, target, lines,
                                                                        (int)(K / 256));
-  check_launch();
+  check_launch("q4k_i16_pack_kernel");
 }
 
 void q4k_i16_gemv(const uint8_t* W, const uint8_t* X, float* Y, size_t M, size_t K) {
@@ -304,7 +304,7 @@ void q4k_i16_gemv(const uint8_t* W, const uint8_t* X, float* Y, size_t M, size_t
     case 8: q4k_i16_gemv_kernel<8><<<grid, 512, lds, current_stream()>>>(a); break;
     default: q4k_i16_gemv_kernel<16><<<grid, 1024, lds, current_stream()>>>(a); break;
   }
-  check_launch();
+  check_launch("q4k_i16_gemv_kernel");
 }
 
 }  // namespace

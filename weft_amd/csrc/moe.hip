@@ -80,7 +80,7 @@ MoeGroups moe_group(const PairArgs& pr, int n_pairs, void* ws) {
   m.pairs = m.tiles + 3 * (size_t)m.tmax;
   GroupArgs g{pr.ids, pr.ids_s0, pr.ids_s1, pr.n_ids, n_pairs, pr.n_as, m.tmax, m.ntiles, m.tiles, m.pairs};
   moe_group_kernel<<<1, kGroupThreads, 0, current_stream()>>>(g);
-  check_launch();
+  check_launch("moe_group_kernel");
   return m;
 }
 

@@ -297,7 +297,7 @@ void gemm_iq2(const uint8_t* W, const uint8_t* Xq, const int8_t* grid, const int
   GemmArgs ga{W, Xq, grid, signs, Y, (int)N, (int)K, (int)M, ldw, (long long)st.ldy, GroupTiles{}};
   const size_t tiles = ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT);
   iq2_mfma_gemm<false><<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(ga);
-  check_launch();
+  check_launch("iq2_mfma_gemm");
 }
 
 }  // namespace
@@ -323,7 +323,7 @@ void mul_mat_id_iq2_grouped(const uint8_t* W, const uint8_t* Xq, const int8_t* g
   GemmArgs ga{W, Xq, grid, signs, Y, (int)N, (int)K, kMT, ldw, 0, group_tiles(g, pr)};
   const size_t wgs = (size_t)g.tmax * ((N + kNT - 1) / kNT);
   iq2_mfma_gemm<true><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(ga);
-  check_launch();
+  check_launch("iq2_mfma_gemm");
 }
 
 void mul_mat_iq2_xxs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,

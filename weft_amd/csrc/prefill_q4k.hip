@@ -430,7 +430,7 @@ void gemm_q4k(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K,
   a.ldy = (long long)st.ldy;
   const size_t tiles = ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT);
   q4k_mfma_gemm<false><<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(a);
-  check_launch();
+  check_launch("q4k_mfma_gemm");
 }
 
 bool args_ok(const uint8_t* W, const void* Xq, const float* Y, size_t N, size_t K, size_t M,
@@ -479,7 +479,7 @@ void mul_mat_id_q4k_grouped(const uint8_t* W, const uint8_t* Xq, float* Y, size_
   a.grp = group_tiles(g, pr);
   const size_t wgs = (size_t)g.tmax * ((N + kNT - 1) / kNT);
   q4k_mfma_gemm<true><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(a);
-  check_launch();
+  check_launch("q4k_mfma_gemm");
 }
 
 void mul_mat_q4k_quantized(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K,

@@ -749,7 +749,7 @@ void planar_pass(const float* X, size_t ldx, uint8_t* Xp, size_t M, size_t K, co
   const bool a16 = aligned(X, 16) && ldx % 4 == 0;
   q80_planar_kernel<F == WFmt::MXFP4><<<grid, 256, 0, current_stream()>>>(
       X, (long long)ldx, a16, Xp, nb, (int)(K / 32), xs, codebook, scale);
-  check_launch();
+  check_launch("q80_planar_kernel");
 }
 
 template <WFmt F>
@@ -777,7 +777,7 @@ bool prefill_q80(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* co
   } else {
     q80_mfma_gemm<F, false><<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(ga);
   }
-  check_launch();
+  check_launch(F == WFmt::MXFP4 ? "mxfp4_gemm" : "q80_mfma_gemm");
   quantize_q8_0_rows(X, ldx, Xq, M, K);  // Xq ends in GGML's record layout
   return true;
 }
@@ -829,7 +829,7 @@ void mul_mat_id_q80_grouped(int fmt, const uint8_t* W, const float* X, uint8_t* 
     q80_mfma_gemm<WFmt::Q4_0, true><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(ga);
   else
     mxfp4_gemm<true><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(ga);
-  check_launch();
+  check_launch(fmt == 0 ? "q80_mfma_gemm" : "mxfp4_gemm");
   // Xq ends in GGML's record layout
   each_plane([&](const float* x, size_t l, uint8_t* xq, size_t m) { quantize_q8_0_rows(x, l, xq, m, K); },
              (K / 32) * kQ8_0Bytes);

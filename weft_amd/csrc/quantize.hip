@@ -124,7 +124,7 @@ void quantize_q8_k_rows(const float* X, size_t ldx, uint8_t* Y, size_t M, size_t
   const long long blocks = std::max<long long>(1, (nb + 15) / 16);
   q8k_quantize_kernel<<<(int)std::min<long long>(blocks, INT32_MAX), kThreads, 0, current_stream()>>>(
       X, Y, nb, xr, a16);
-  check_launch();
+  check_launch("q8k_quantize_kernel");
 }
 
 void quantize_q8_0_rows(const float* X, size_t ldx, uint8_t* Y, size_t M, size_t K) {
@@ -137,7 +137,7 @@ void quantize_q8_0_rows(const float* X, size_t ldx, uint8_t* Y, size_t M, size_t
   const XRows xr{flat ? 0 : (long long)(K / 32), (long long)ldx};
   const bool a16 = aligned(X, 16) && (flat || ldx % 4 == 0);
   q80_quantize_kernel<<<grid_for((nb + 7) / 8), kThreads, 0, current_stream()>>>(X, Y, nb, xr, a16);
-  check_launch();
+  check_launch("q80_quantize_kernel");
 }
 
 void quantize_q8_k(const float* X, uint8_t* Y, size_t K) { quantize_q8_k_rows(X, K, Y, 1, K); }

@@ -12,8 +12,9 @@ namespace weft {
 hipStream_t current_stream();
 // Record an error for the calling thread (first one wins until read).
 void set_error(hipError_t e);
-// Check the launch just made and record its error, if any.
-void check_launch();
+// Check the launch just made and record its error, if any; `kernel` names
+// it in the calling thread's launch log (weft_hip_launch_log).
+void check_launch(const char* kernel = nullptr);
 // The calling thread's recorded error, left in place.
 hipError_t pending_error();
 // Compute units of the current device (cached per device).

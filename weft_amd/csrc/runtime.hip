@@ -18,6 +18,7 @@ namespace weft {
 namespace {
 thread_local hipStream_t t_stream = nullptr;
 thread_local hipError_t t_error = hipSuccess;
+thread_local std::string t_launch_log;  // kernels launched since the log was last read
 
 struct DeviceFacts {
   int cus = 0;
@@ -53,7 +54,14 @@ void set_error(hipError_t e) {
   if (e != hipSuccess && t_error == hipSuccess) t_error = e;
 }
 
-void check_launch() { set_error(hipGetLastError()); }
+void check_launch(const char* kernel) {
+  const hipError_t e = hipGetLastError();
+  set_error(e);
+  if (kernel != nullptr && e == hipSuccess) {
+    if (!t_launch_log.empty()) t_launch_log += ',';
+    t_launch_log += kernel;
+  }
+}
 
 hipError_t pending_error() { return t_error; }
 
@@ -88,6 +96,17 @@ int weft_hip_synchronize(void) {
 
 const char* weft_hip_version(void) { return WEFT_HIP_VERSION_STRING; }
 
+size_t weft_hip_launch_log(char* buf, size_t len) {
+  const size_t n = weft::t_launch_log.size();
+  if (buf != nullptr && len > 0) {
+    const size_t c = n < len - 1 ? n : len - 1;
+    for (size_t i = 0; i < c; ++i) buf[i] = weft::t_launch_log[i];
+    buf[c] = 0;
+    weft::t_launch_log.clear();
+  }
+  return n;
+}
+
 int weft_hip_device_count(void) {
   int n = 0;
   const hipError_t e = hipGetDeviceCount(&n);
@@ -104,6 +123,57 @@ int weft_hip_device_arch(int dev, char* buf, size_t len) {
   for (; i + 1 < len && prop.gcnArchName[i] != 0; ++i) buf[i] = prop.gcnArchName[i];
   buf[i] = 0;
   return 0;
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------- measurement probes
+// Floors a caller measures beside the kernels on the same stream: an empty
+// launch (the per-launch cost of any kernel) and a plain streaming read of a
+// buffer (the best a single launch can do for that many bytes).
+namespace weft {
+namespace {
+
+__global__ void probe_empty_kernel() {}
+
+// grid-stride 16-byte loads, UNROLL in flight per lane, one 4-byte store
+// per wave (the decode kernels' store pattern)
+constexpr int kProbeUnroll = 4;
+__global__ void __launch_bounds__(512) probe_read_kernel(const uint4* __restrict__ src, size_t n16,
+                                                         uint32_t* __restrict__ sink) {
+  const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t nth = (size_t)gridDim.x * blockDim.x;
+  uint32_t acc = 0;
+  for (size_t i = tid; i < n16; i += nth * kProbeUnroll) {
+    uint4 v[kProbeUnroll];
+#pragma unroll
+    for (int u = 0; u < kProbeUnroll; ++u)
+      v[u] = i + u * nth < n16 ? src[i + u * nth] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < kProbeUnroll; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  for (int o = 32; o > 0; o >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, o, 64);
+  if ((threadIdx.x & 63) == 0) sink[tid >> 6] = acc;
+}
+
+}  // namespace
+}  // namespace weft
+
+extern "C" {
+
+void weft_hip_probe_empty(void) {
+  weft::probe_empty_kernel<<<1, 64, 0, weft::current_stream()>>>();
+  weft::check_launch("probe_empty_kernel");
+}
+
+void weft_hip_probe_read(const void* src, size_t bytes, uint32_t* sink, int grid) {
+  if (src == nullptr || sink == nullptr || grid <= 0 || bytes % 16 != 0 || !weft::aligned(src, 16)) {
+    weft::set_error(hipErrorInvalidValue);
+    return;
+  }
+  weft::probe_read_kernel<<<grid, 512, 0, weft::current_stream()>>>(static_cast<const uint4*>(src), bytes / 16,
+                                                                    sink);
+  weft::check_launch("probe_read_kernel");
 }
 
 }  // extern "C"
