@@ -255,6 +255,16 @@ size_t weft_ggml_mul_mat_id_work_size(const weft_ggml_tensor *src0, const weft_g
 int weft_ggml_mul_mat_id(const weft_ggml_tensor *src0, const weft_ggml_tensor *src1,
                          const weft_ggml_tensor *ids, const weft_ggml_tensor *dst, void *wdata,
                          size_t wsize);
+/* No counterpart in the reference.  weft_ggml_mul_mat_id for callers that
+ * cannot allocate (HIP graph capture, serving loops that forbid hipMalloc):
+ * the work buffer is a static device array the library holds per device
+ * (WEFT_GGML_NOALLOC_SCRATCH_BYTES), so the call allocates nothing.  A call
+ * whose work size (weft_ggml_mul_mat_id_work_size) exceeds it returns
+ * hipErrorOutOfMemory and launches nothing.  Calls that overlap on one
+ * device share the array and race. */
+#define WEFT_GGML_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int weft_ggml_mul_mat_id_noalloc(const weft_ggml_tensor *src0, const weft_ggml_tensor *src1,
+                                 const weft_ggml_tensor *ids, const weft_ggml_tensor *dst);
 
 #ifdef __cplusplus
 }

@@ -111,3 +111,62 @@ def test_invalid_call_records_an_error_without_a_device():
     lib.row_dequantize_q4_k(None, None, 100)
     assert lib.weft_hip_get_last_error() != 0
     assert lib.weft_hip_get_last_error() == 0
+
+
+# ----------------------------------------------- device variables of the library
+READELF = Path("/opt/rocm/llvm/bin/llvm-readelf")
+OBJCOPY = Path("/opt/rocm/llvm/bin/llvm-objcopy")
+
+
+def device_code_objects(so: Path) -> list[bytes]:
+    """The gfx950 code objects in the library's .hip_fatbin section (one
+    clang offload bundle per translation unit)."""
+    import struct
+    import subprocess
+    import tempfile
+    with tempfile.TemporaryDirectory() as tmp:
+        fat = Path(tmp) / "fatbin"
+        subprocess.run([str(OBJCOPY), f"--dump-section=.hip_fatbin={fat}", str(so), str(Path(tmp) / "x")],
+                       check=True, capture_output=True)
+        data = fat.read_bytes()
+    magic = b"__CLANG_OFFLOAD_BUNDLE__"
+    out = []
+    at = data.find(magic)
+    while at >= 0:
+        (count,) = struct.unpack_from("<Q", data, at + len(magic))
+        pos = at + len(magic) + 8
+        for _ in range(count):
+            off, size, tlen = struct.unpack_from("<QQQ", data, pos)
+            triple = data[pos + 24:pos + 24 + tlen].decode()
+            pos += 24 + tlen
+            if "gfx950" in triple:
+                out.append(data[at + off:at + off + size])
+        at = data.find(magic, at + 1)
+    return out
+
+
+@pytest.mark.skipif(not (READELF.exists() and OBJCOPY.exists()), reason="needs ROCm's llvm-readelf / llvm-objcopy")
+def test_host_registered_device_variables_exist_in_the_code_objects():
+    """Every __device__ variable the host side registers must survive in the
+    device code object: an internal const object that no kernel reads is
+    dropped there while the host still registers it, and the HIP runtime then
+    aborts the process at the first launch from that code object.  The
+    library's variables are the GGML tables and the no-allocation scratch."""
+    import subprocess
+    import tempfile
+    objects = device_code_objects(_lib.LIB_PATH)
+    assert objects
+    symbols = []
+    with tempfile.TemporaryDirectory() as tmp:
+        for i, co in enumerate(objects):
+            path = Path(tmp) / f"co{i}.o"
+            path.write_bytes(co)
+            res = subprocess.run([str(READELF), "--syms", "--wide", str(path)], check=True,
+                                 capture_output=True, text=True)
+            symbols += [line.split() for line in res.stdout.splitlines() if " OBJECT " in line]
+    found = {row[-1]: row for row in symbols}
+    for needle in ("g_weft_ggml_tables", "scratch"):
+        hits = [name for name in found if needle in name and not name.endswith(".kd")]
+        assert hits, f"device variable {needle} missing from the code objects"
+        for name in hits:
+            assert found[name][4] == "GLOBAL", f"{name} is not a global symbol of the code object"

@@ -96,7 +96,8 @@ def _bind_ggml(lib: ctypes.CDLL) -> None:
                             ("weft_ggml_mul_mat_work_size", [vp, vp], sz),
                             ("weft_ggml_mul_mat", [vp, vp, vp, vp, sz], ctypes.c_int),
                             ("weft_ggml_mul_mat_id_work_size", [vp, vp, vp], sz),
-                            ("weft_ggml_mul_mat_id", [vp, vp, vp, vp, vp, sz], ctypes.c_int)):
+                            ("weft_ggml_mul_mat_id", [vp, vp, vp, vp, vp, sz], ctypes.c_int),
+                            ("weft_ggml_mul_mat_id_noalloc", [vp, vp, vp, vp], ctypes.c_int)):
         fn = getattr(lib, name)
         fn.argtypes, fn.restype = args, res
 

@@ -143,6 +143,40 @@ const GgmlTables* device_tables() {
   return addr[dev];
 }
 
+// The work buffer of weft_ggml_mul_mat_id_noalloc: one copy per device, held
+// until the process ends.  Host code never names it past the lookup below:
+// there the name is a host-side stand-in, and each device's copy lives at
+// the address hipGetSymbolAddress returns with that device current.  Every
+// call on a device shares its copy (a call's quantized src1 and expert
+// grouping are written in full before they are read, so nothing needs to
+// start at zero); calls that overlap on one device race on it.
+static __device__ __align__(256) uint8_t scratch[WEFT_GGML_NOALLOC_SCRATCH_BYTES];
+
+// Device address of the current device's scratch, resolved on the first call
+// on that device; null (and the error recorded) if the lookup fails.
+uint8_t* noalloc_scratch() {
+  static std::mutex mu;
+  static std::vector<uint8_t*> addr;
+  int dev = 0;
+  const hipError_t ge = hipGetDevice(&dev);
+  if (ge != hipSuccess) {
+    set_error(ge);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if ((int)addr.size() <= dev) addr.resize(dev + 1, nullptr);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) {
+      set_error(e);
+      return nullptr;
+    }
+    addr[dev] = static_cast<uint8_t*>(p);
+  }
+  return addr[dev];
+}
+
 // ---------------------------------------------------------------- the op
 size_t row_size(const TypeInfo* t, int64_t ne) { return t->size * (size_t)(ne / t->blck); }
 
@@ -452,6 +486,15 @@ int weft_ggml_mul_mat_id(const weft_ggml_tensor* src0, const weft_ggml_tensor* s
                          const weft_ggml_tensor* ids, const weft_ggml_tensor* dst, void* wdata,
                          size_t wsize) {
   return (int)weft::mul_mat_id(src0, src1, ids, dst, wdata, wsize);
+}
+
+int weft_ggml_mul_mat_id_noalloc(const weft_ggml_tensor* src0, const weft_ggml_tensor* src1,
+                                 const weft_ggml_tensor* ids, const weft_ggml_tensor* dst) {
+  const size_t need = weft_ggml_mul_mat_id_work_size(src0, src1, ids);
+  if (need > WEFT_GGML_NOALLOC_SCRATCH_BYTES) return (int)weft::fail(hipErrorOutOfMemory);
+  uint8_t* ws = weft::noalloc_scratch();
+  if (ws == nullptr) return (int)weft::pending_error();
+  return (int)weft::mul_mat_id(src0, src1, ids, dst, ws, need);
 }
 
 size_t weft_ggml_mul_mat_work_size(const weft_ggml_tensor* src0, const weft_ggml_tensor* src1) {

@@ -79,3 +79,19 @@ def mul_mat_id(src0: Tensor, src1: Tensor, ids: Tensor, dst: Tensor, wdata: int 
     if code != 0:
         lib.weft_hip_get_last_error()
         raise _lib.HipError(code, "weft_ggml_mul_mat_id")
+
+
+# the library's per-device work buffer of mul_mat_id_noalloc (weft_hip.h)
+NOALLOC_SCRATCH_BYTES = 32 << 20
+
+
+def mul_mat_id_noalloc(src0: Tensor, src1: Tensor, ids: Tensor, dst: Tensor) -> None:
+    """MUL_MAT_ID without a caller work buffer: the library's per-device
+    scratch stands in for it (calls that overlap on one device race)."""
+    lib = _lib.load()
+    code = lib.weft_ggml_mul_mat_id_noalloc(ctypes.byref(src0), ctypes.byref(src1), ctypes.byref(ids),
+                                            ctypes.byref(dst))
+    if code != 0:
+        lib.weft_hip_get_last_error()
+        raise _lib.HipError(code, "weft_ggml_mul_mat_id_noalloc")
+
