@@ -262,23 +262,90 @@ def test_prefill_q4_k_config4_n4096(hip):
     check_mul_mat("q4_k", w, x, xq, y, n, k, m)
 
 
-def test_prefill_q4_k_config4_n11008_sampled(hip):
-    """BASELINE config 4 (N=11008): Xq in full, Y on 256 seeded columns."""
+def test_prefill_q4_k_config4_n11008(hip):
+    """BASELINE config 4 (N=11008): 512 tokens x 11008, every output."""
     n, k, m = 11008, 4096, 512
     w, x, xq, y = run_mul_mat(hip, "production_mul_mat_q4_k_staged", "q4_k", n, k, m)
-    cols = np.sort(np.random.default_rng(5).choice(n, 256, replace=False))
-    check_mul_mat("q4_k", w, x, xq, y, n, k, m, cols=cols)
+    check_mul_mat("q4_k", w, x, xq, y, n, k, m)
 
 
 @pytest.mark.parametrize("fmt", ["mxfp4", "q4_0", "iq2_xxs"])
-def test_prefill_config5b_sampled(hip, fmt):
+def test_prefill_config5b(hip, fmt):
     """BASELINE config 5b (MXFP4, 512 x 4096 x 4096; Q4_0 and IQ2_XXS at the
-    same shape): Xq in full, Y on 256 seeded columns."""
+    same shape): every output."""
     n = k = 4096
     m = 512
     w, x, xq, y = run_mul_mat(hip, MM_PREFILL[fmt], fmt, n, k, m)
-    cols = np.sort(np.random.default_rng(6).choice(n, 256, replace=False))
-    check_mul_mat(fmt, w, x, xq, y, n, k, m, cols=cols)
+    check_mul_mat(fmt, w, x, xq, y, n, k, m)
+
+
+@pytest.mark.parametrize("symbol,fmt", [("production_mul_mat_q4_k", "q4_k"),
+                                        ("production_mul_mat_iq2_xxs", "iq2_xxs")])
+def test_prefill_unstaged_entry_points(hip, symbol, fmt):
+    """The reference's unstaged mul_mat symbols (mul_mat/q4_k.py,
+    mul_mat/iq2_xxs.py) share the staged kernels; one call each."""
+    n, k, m = 384, 2048, 80
+    w, x, xq, y = run_mul_mat(hip, symbol, fmt, n, k, m)
+    check_mul_mat(fmt, w, x, xq, y, n, k, m)
+
+
+# ------------------------------------------------ crafted records, prefill
+FP16_EDGES = np.array([0x0000, 0x8000, 0x0001, 0x03FF, 0x0400, 0x7BFF, 0xFBFF, 0x3C00, 0x2E66, 0xB1A0],
+                      np.uint16)  # zeros, subnormals, smallest normal, +-max, ordinary values
+
+
+def crafted_q4_k(n, k, rng):
+    rec = rng.integers(0, 256, size=(n, k // 256, 144), dtype=np.uint8)
+    d = rng.choice(FP16_EDGES, size=(n, k // 256))
+    dmin = rng.choice(FP16_EDGES, size=(n, k // 256))
+    rec[:, :, 0:2] = d.view(np.uint8).reshape(n, k // 256, 2)
+    rec[:, :, 2:4] = dmin.view(np.uint8).reshape(n, k // 256, 2)
+    rec[0::7, :, 4:16] = 0xFF  # every sub-block: sc = m = 63
+    rec[3::11, :, 16:] = 0xFF  # every nibble 15
+    return rec.reshape(n, -1)
+
+
+def crafted_q4_0(n, k, rng):
+    rec = rng.integers(0, 256, size=(n, k // 32, 18), dtype=np.uint8)
+    rec[:, :, 0:2] = rng.choice(FP16_EDGES, size=(n, k // 32)).view(np.uint8).reshape(n, k // 32, 2)
+    rec[5::9, :, 2:] = 0x00  # q - 8 = -8 everywhere
+    return rec.reshape(n, -1)
+
+
+def crafted_iq2_xxs(n, k, rng):
+    rec = rng.integers(0, 256, size=(n, k // 256, 66), dtype=np.uint8)
+    rec[:, :, 0:2] = rng.choice(FP16_EDGES, size=(n, k // 256)).view(np.uint8).reshape(n, k // 256, 2)
+    words = rec[:, :, 2:].copy().view(np.uint32)  # (n, nsb, 16): pairs of (grid idx, signs | scale << 28)
+    words[:, :, 1::2] |= np.uint32(0xF0000000)  # s = 15 in every group ...
+    words[2::5, :, 1::2] &= np.uint32(0x0FFFFFFF)  # ... except some rows with s = 0
+    rec[:, :, 2:] = words.view(np.uint8).reshape(n, k // 256, 64)
+    return rec.reshape(n, -1)
+
+
+def crafted_acts_q8k(m, k, rng):
+    x = o.seeded_normal(int(rng.integers(1 << 30)), (m, k))
+    x[:, 256:512] = 0.0            # an all-zero Q8_K block in every row
+    x[1, :] = 0.0                  # an all-zero row
+    x[2, ::256] = 1e4              # a dominant first element per superblock
+    x[3, 7::256] = -127.0          # a negative maximum
+    return x
+
+
+@pytest.mark.parametrize("fmt,make", [("q4_k", crafted_q4_k), ("q4_0", crafted_q4_0),
+                                      ("iq2_xxs", crafted_iq2_xxs)])
+def test_prefill_crafted_records(hip, fmt, make):
+    """The MFMA prefill GEMMs on records no quantizer emits: d / dmin zero,
+    negative zero, subnormal, the smallest normal and +-65504; Q4_K sub-blocks
+    with sc = m = 63 and all-15 nibbles; Q4_0 blocks of q - 8 = -8; IQ2_XXS
+    groups with scale 15 and 0; activations with all-zero Q8_K blocks and
+    rows, a dominant element and a negative maximum."""
+    rng = np.random.default_rng(77)
+    n, k, m = 256, 1024, 64
+    w = make(n, k, rng)
+    x = crafted_acts_q8k(m, k, rng)
+    print(f"crafted prefill {fmt}", flush=True)
+    w, x, xq, y = run_mul_mat(hip, MM_PREFILL[fmt], fmt, n, k, m, w=w, x=x)
+    check_mul_mat(fmt, w, x, xq, y, n, k, m)
 
 
 def test_prefill_mxfp4_crafted_scales(hip):

@@ -546,6 +546,82 @@ def test_weight_quantizer_round_trip(fmt, bound):
     assert rel < bound
 
 
+def _k_scale_min(s: np.ndarray, j: int):
+    """get_scale_min_k4 (ggml-quants.c:822-829) over records' 12 scale bytes."""
+    if j < 4:
+        return s[..., j] & 63, s[..., j + 4] & 63
+    return ((s[..., j + 4] & 0xF) | ((s[..., j - 4] >> 6) << 4),
+            (s[..., j + 4] >> 4) | ((s[..., j] >> 6) << 4))
+
+
+def _codes_k(fmt: str, rec: np.ndarray) -> np.ndarray:
+    """The integer codes of Q4_K / Q5_K / Q6_K records (element order),
+    read from the byte layouts of ggml-common.h."""
+    e = np.arange(256)
+    if fmt in ("q4_k", "q5_k"):
+        qs = rec[:, -128:]
+        low = qs[:, 32 * (e // 64) + e % 32]
+        q = np.where((e % 64) < 32, low & 0xF, low >> 4).astype(np.int32)
+        if fmt == "q5_k":
+            qh = rec[:, 16:48]
+            q += ((qh[:, e % 32] >> (e // 32)) & 1).astype(np.int32) << 4
+        return q
+    ql, qh = rec[:, :128], rec[:, 128:192]
+    h, r = e // 128, e % 128
+    lo = ql[:, 64 * h + r % 64]
+    q = np.where(r < 64, lo & 0xF, lo >> 4).astype(np.int32)
+    q |= ((qh[:, 32 * h + r % 32] >> (2 * (r // 32))) & 3).astype(np.int32) << 4
+    return q
+
+
+def _nearest_int(v: np.ndarray) -> np.ndarray:
+    return np.rint(v.astype(np.float32)).astype(np.int64)  # RNE, as GGML's 1.5 * 2^23 trick
+
+
+@pytest.mark.parametrize("fmt", ["q4_k", "q5_k", "q6_k"])
+def test_k_quantizer_codes_are_nearest_given_the_record(fmt):
+    """What GGML's reference quantizers' last pass fixes, checked on the
+    oracle's records: with the record's own fp16 d (and dmin) and 6-bit
+    (Q6_K: int8) scales, every code of a sub-block with a non-zero scale is
+    nearest_int((x + dmin m) / (d sc)) clamped to the code range
+    (quantize_row_q4_K_ref ggml-quants.c:1448-1459, _q5_K_ref :1635-1646,
+    _q6_K_ref :1849-1859).  Weights of the tests' generator plus rows with a
+    zero sub-block, a constant row and an outlier."""
+    x = o.seeded_normal(53, (24, 1024), 0.02)
+    x[1, 64:96] = 0.0
+    x[2, :] = 0.01
+    x[3, 500] = 0.9
+    rb = o.RECORD[fmt][1]
+    rec = o.quantize(fmt, x).reshape(-1, rb)
+    xs = x.reshape(-1, 256).astype(np.float32)
+    codes = _codes_k(fmt, rec)
+    f16 = lambda b: b.copy().view(np.float16).astype(np.float32)[..., 0]  # noqa: E731
+    checked = 0
+    if fmt == "q6_k":
+        d = f16(rec[:, 208:210])
+        sc = rec[:, 192:208].view(np.int8).astype(np.float32)
+        for j in range(16):
+            dj = (d * sc[:, j]).astype(np.float32)
+            live = dj != 0
+            v = xs[live, 16 * j:16 * j + 16] / dj[live, None]
+            want = np.clip(_nearest_int(v), -32, 31) + 32
+            assert (codes[live, 16 * j:16 * j + 16] == want).all(), f"sub-block {j}"
+            checked += int(live.sum())
+    else:
+        d, dmin = f16(rec[:, 0:2]), f16(rec[:, 2:4])
+        top = 15 if fmt == "q4_k" else 31
+        for j in range(8):
+            sc, m = _k_scale_min(rec[:, 4:16], j)
+            dj = (d * sc.astype(np.float32)).astype(np.float32)
+            dm = (dmin * m.astype(np.float32)).astype(np.float32)
+            live = dj != 0
+            v = (xs[live, 32 * j:32 * j + 32] + dm[live, None]) / dj[live, None]
+            want = np.clip(_nearest_int(v), 0, top)
+            assert (codes[live, 32 * j:32 * j + 32] == want).all(), f"sub-block {j}"
+            checked += int(live.sum())
+    assert checked > 0.9 * xs.shape[0] * (16 if fmt == "q6_k" else 8)
+
+
 def test_q4_0_quantizer_error_is_half_a_step():
     w = o.seeded_normal(52, (16, 1024), 0.02)
     q = o.quantize("q4_0", w).reshape(-1, 18)
