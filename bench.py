@@ -77,6 +77,9 @@ CASES = {
     # GGML MUL_MAT_ID (MoE) prefill at a Mixtral-8x7B FFN shape: 8 experts of
     # 14336 x 4096 Q4_K, 2 experts per token, 512 tokens (the grouped GEMM)
     "q4_k_moe_prefill": ("weft_ggml_mul_mat_id", "q4_k", 14336, 4096, 512, "mfma"),
+    # GGML MUL_MAT with src1 already in Q8_K: the Q4_K GEMM alone, no quantize pass
+    "q4_k_prefill_n4096_q8k_src1": ("weft_ggml_mul_mat", "q4_k", 4096, 4096, 512, "mfma"),
+    "q4_k_prefill_n11008_q8k_src1": ("weft_ggml_mul_mat", "q4_k", 11008, 4096, 512, "mfma"),
 }
 MOE_EXPERTS, MOE_USED = 8, 2
 HEADLINE = "q4_k_decode_w_up"
@@ -293,6 +296,19 @@ def run_case(b: Bench, name: str, steps: int, warmup: int, extra: bool) -> dict:
 
         nbytes = MOE_EXPERTS * w.nbytes + 4 * m * k + o.record_bytes("q8_k", k) * m + 4 * m * MOE_USED * n
         m *= MOE_USED  # products: one per (token, expert) pair
+    elif sym == "weft_ggml_mul_mat":
+        from weft_amd import ggml as G
+        wd = [b.dev_copy(w) for _ in range(copies)]
+        xq = b.dev_copy(o.quantize("q8_k", o.seeded_normal(2, (m, k))))
+        y = torch.empty(m * n, dtype=torch.float32, device=b.dev)
+        s0s = [G.tensor(G.Q4_K, (k, n), t.data_ptr()) for t in wd]
+        s1 = G.tensor(G.Q8_K, (k, m), xq.data_ptr())
+        d = G.tensor(G.F32, (n, m), y.data_ptr())
+
+        def launch(i):
+            G.mul_mat(s0s[i % copies], s1, d)
+
+        nbytes = w.nbytes + xq.numel() + 4 * m * n
     else:
         wd = [b.dev_copy(w) for _ in range(copies)]
         if m == 0:  # row dequantize of the whole matrix
