@@ -26,6 +26,7 @@
 // token scales are loaded by one wave per parity and transposed to fp32
 // [block][token] so the combine reads four tokens with one instruction.
 #include <algorithm>
+#include <type_traits>
 
 #include "kernels.h"
 #include "runtime.h"
@@ -199,19 +200,21 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
   // per-block token scales of this parity's stage: wave wcol == 0, token = lane
   const uint8_t* dsrc = a.Xp + (size_t)act_row(min(lane, mrows - 1)) * xs + a.K;
 
+  // LDS byte addresses as integers from one wave-uniform base: no per-use
+  // generic-to-LDS pointer casts (their null checks on VALU do not compile)
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
   auto issue = [&](int pair, uint8_t* ring) {
     const int st = min(2 * pair + par, nst - 1);
-    uint8_t* stage = ring + par * kStage;
+    const uint32_t stage = lds0 + (uint32_t)(ring - lds) + par * kStage;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      lds_dma16(asrc[i] + 256 * (size_t)st,
-                __builtin_amdgcn_readfirstlane(lds_addr(stage + 1024 * (wcol + 4 * i))));
+      lds_dma16(asrc[i] + 256 * (size_t)st, stage + 1024 * (wcol + 4 * i));
 #pragma unroll
     for (int i = 0; i < kWPerWave; ++i) {
       const int k = wcol + 4 * i;
       const int q = 64 * k + lane, row = q / kWD, part = q - kWD * row;
       const uint8_t* g = W + (size_t)min(n0 + row, a.N - 1) * ws_row + (size_t)st * kRB + 4 * part;
-      lds_dma4(g, __builtin_amdgcn_readfirstlane(lds_addr(stage + kAQ + 256 * k)));
+      lds_dma4(g, stage + kAQ + 256 * k);
     }
   };
   uint4 dxraw = make_uint4(0, 0, 0, 0);
@@ -510,11 +513,13 @@ __device__ __forceinline__ v16f fma_block(v16f y, v16f d, float dx) {
 
 // A tile computed at unit block scale (d = I / 2 exactly), combined in
 // GGML's order: register r holds weight row 8 (r / 4) + 4 h + r % 4 of the
-// tile, whose exponent the lane of that row holds in e.
-__device__ __attribute__((noinline)) v16f ggml_block_terms(v16f y, v16f d, float dx, uint32_t e, int h) {
+// tile, whose exponent byte sits at LDS address e0 + kRowW (8 (r / 4) + r % 4)
+// (e0: the exponent of row 4 h).
+__device__ __forceinline__ v16f ggml_block_terms(v16f y, v16f d, float dx, uint32_t e0) {
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    const uint32_t er = (uint32_t)__shfl((int)e, 8 * (r >> 2) + 4 * h + (r & 3), kWave);
+    const uint32_t er =
+        *(const __attribute__((address_space(3))) uint8_t*)(size_t)(e0 + kRowW * (8 * (r >> 2) + (r & 3)));
     y[r] = ggml_scaled_term(y[r], dx, e8m0_half(er), 2.f * d[r]);
   }
   return y;
@@ -579,20 +584,23 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
 #pragma unroll
   for (int i = 0; i < 9; ++i) vw[i] = w_off(min(wave + 8 * i + 4, kWLoads - 1));
 
+  // LDS byte addresses as integers from one wave-uniform base: no per-use
+  // generic-to-LDS pointer casts (their null checks on VALU do not compile)
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
   auto issue = [&](int st) {
-    uint8_t* slot = lds + (st & 3) * kSlot;
+    const uint32_t slot = lds0 + (uint32_t)(st & 3) * kSlot;
     const uint8_t* xb = xbase + 256 * (size_t)st;
     const uint8_t* wb = wbase + 136 * (size_t)st;
-    dma16_s(xb, va0, __builtin_amdgcn_readfirstlane(lds_addr(slot + 1024 * wave)));
-    dma16_s(xb, va1, __builtin_amdgcn_readfirstlane(lds_addr(slot + 1024 * (wave + 8))));
+    dma16_s(xb, va0, slot + 1024 * wave);
+    dma16_s(xb, va1, slot + 1024 * (wave + 8));
     if (wave < 4)
-      lds_dma4_s(xbase + 16 * (size_t)st, v2, __builtin_amdgcn_readfirstlane(lds_addr(slot + kSD + 256 * wave)));
+      lds_dma4_s(xbase + 16 * (size_t)st, v2, slot + kSD + 256 * wave);
     else
-      lds_dma4_s(wb, v2, __builtin_amdgcn_readfirstlane(lds_addr(slot + kSW + 256 * (wave - 4))));
+      lds_dma4_s(wb, v2, slot + kSW + 256 * (wave - 4));
 #pragma unroll
     for (int i = 0; i < 9; ++i)
       if (i < 8 || wave < 2)
-        lds_dma4_s(wb, vw[i], __builtin_amdgcn_readfirstlane(lds_addr(slot + kSW + 256 * (wave + 8 * i + 4))));
+        lds_dma4_s(wb, vw[i], slot + kSW + 256 * (wave + 8 * i + 4));
   };
 
   v16f y[4];  // tile 2 * token half + column tile
@@ -601,9 +609,16 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
   const v16f fzero = {};
   const int x_scale = h ? 127 + 9 : 127 + 13;  // B block 0: hi plane (x16), block 1: lo plane
 
-  // blocks 2 ph and 2 ph + 1 of stage st
-  auto stage = [&](int st) {
+  // blocks 2 ph and 2 ph + 1 of stage st.  kExact false: every tile takes
+  // its exponent e as the hardware block scale, and `out` collects whether
+  // any e lies outside [kSafeLo, kSafeHi] (the results are then discarded).
+  // kExact true: a column tile whose 32 rows all have exponents in range
+  // does the same; otherwise (wave-uniform) its MFMA runs at unit scale and
+  // the block is combined in GGML's order.
+  auto stage = [&](int st, auto exact_tag, bool& out) {
+    constexpr bool kExact = decltype(exact_tag)::value;
     const uint8_t* slot = lds + (st & 3) * kSlot;
+    const uint32_t slot_lds = lds0 + (uint32_t)(st & 3) * kSlot;
 #pragma unroll
     for (int bi = 0; bi < 2; ++bi) {
       const int b = 2 * ph + bi;
@@ -613,19 +628,18 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
       const int b4 = (off + 1) & ~3, sh = (off + 1) & 3;
       v8i wv[2];
       int wsc[2];
-      uint32_t ew[2];
-      bool exact[2];
+      bool exact[2] = {false, false};
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) {
         const uint8_t* wr = slot + kSW + kRowW * (64 * cp + 32 * ct + col);
         const uint32_t w0 = ld32(wr + b4), w1 = ld32(wr + b4 + 4), w2 = ld32(wr + b4 + 8),
                        w3 = ld32(wr + b4 + 12), w4 = ld32(wr + b4 + 16);
         const uint32_t e = __builtin_amdgcn_ubfe(ld32(wr + (off & ~3)), 8 * (off & 3), 8);
-        // A tile whose 32 rows all have exponents in [kSafeLo, kSafeHi]
-        // takes e as the hardware block scale; otherwise the MFMA runs at
-        // unit scale and the block is combined in GGML's order below.
-        exact[ct] = __builtin_amdgcn_ballot_w64(e < kSafeLo || e > kSafeHi) != 0;
-        ew[ct] = e;
+        const bool unsafe = e - kSafeLo > kSafeHi - kSafeLo;  // unsigned
+        if constexpr (kExact)
+          exact[ct] = __builtin_amdgcn_ballot_w64(unsafe) != 0;
+        else
+          out |= unsafe;
         wsc[ct] = exact[ct] ? 127 : (int)e;
         wv[ct] = v8i{(int)__builtin_amdgcn_alignbyte(w1, w0, sh), (int)__builtin_amdgcn_alignbyte(w2, w1, sh),
                      (int)__builtin_amdgcn_alignbyte(w3, w2, sh), (int)__builtin_amdgcn_alignbyte(w4, w3, sh),
@@ -654,32 +668,45 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int ct = q & 1;
-        if (exact[ct])
-          y[q] = ggml_block_terms(y[q], d[q], dx[q >> 1], ew[ct], h);
+        if (kExact && exact[ct])  // wave-uniform
+          y[q] = ggml_block_terms(y[q], d[q], dx[q >> 1], slot_lds + kSW + kRowW * (64 * cp + 32 * ct + 4 * h) + off);
         else
           y[q] = fma_block(y[q], d[q], dx[q >> 1]);
       }
     }
   };
 
-  // Two stages per barrier: the direct loads of the next pair go out right
-  // after the barrier, into the slots the previous pair used, so each wave
-  // waits for all of its own loads (vmcnt 0) at the top of a pair.
-  issue(0);
-  if (nst > 1) issue(1);
-  int st = 0;
-  for (; st + 1 < nst; st += 2) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    lds_barrier();  // the pair is in for every wave; the previous pair's slots are free
-    if (st + 2 < nst) issue(st + 2);
-    if (st + 3 < nst) issue(st + 3);
-    stage(st);
-    stage(st + 1);
-  }
-  if (st < nst) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    lds_barrier();
-    stage(st);
+  // The K loop.  Two stages per barrier: the direct loads of the next pair
+  // go out right after the barrier, into the slots the previous pair used,
+  // so each wave waits for all of its own loads (vmcnt 0) at the top of a
+  // pair.
+  auto kloop = [&](auto exact_tag, bool& out) {
+    issue(0);
+    if (nst > 1) issue(1);
+    int st = 0;
+    for (; st + 1 < nst; st += 2) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      lds_barrier();  // the pair is in for every wave; the previous pair's slots are free
+      if (st + 2 < nst) issue(st + 2);
+      if (st + 3 < nst) issue(st + 3);
+      stage(st, exact_tag, out);
+      stage(st + 1, exact_tag, out);
+    }
+    if (st < nst) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      lds_barrier();
+      stage(st, exact_tag, out);
+    }
+  };
+  // Weights quantized by GGML keep every exponent in range, and the loop
+  // without per-tile branches runs once.  A workgroup that met an exponent
+  // out of range runs the K loop again with GGML's order for those tiles.
+  bool out = false;
+  kloop(std::integral_constant<bool, false>{}, out);
+  if (__syncthreads_or(out)) {  // also: every wave is done with the ring
+#pragma unroll
+    for (int q = 0; q < 4; ++q) y[q] = v16f{};
+    kloop(std::integral_constant<bool, true>{}, out);
   }
 
   // partial sums of the four K phases -> LDS; wave (cp, p) finishes tile p
