@@ -78,6 +78,8 @@ CASES = {
     # 14336 x 4096 Q4_K, 2 experts per token, 512 tokens (the grouped GEMM)
     "q4_k_moe_prefill": ("weft_ggml_mul_mat_id", "q4_k", 14336, 4096, 512, "mfma"),
     # GGML MUL_MAT with src1 already in Q8_K: the Q4_K GEMM alone, no quantize pass
+    # the same prefill from the persisted Q4K_I[16] interleave (packed outside the timing)
+    "q4_k_persistent_prefill_n4096": ("production_mul_mat_q4_k_persistent", "q4_k", 4096, 4096, 512, "mfma"),
     "q4_k_prefill_n4096_q8k_src1": ("weft_ggml_mul_mat", "q4_k", 4096, 4096, 512, "mfma"),
     "q4_k_prefill_n11008_q8k_src1": ("weft_ggml_mul_mat", "q4_k", 11008, 4096, 512, "mfma"),
 }
@@ -333,6 +335,22 @@ def run_case(b: Bench, name: str, steps: int, warmup: int, extra: bool) -> dict:
                 fn(wd[i % copies].data_ptr(), xq.data_ptr(), y.data_ptr(), n, k)
 
             nbytes = w.nbytes + xq.numel() + 4 * n
+        elif sym.endswith("_persistent"):  # Q4K_I[16] weights, shapes in the artifact's order M, K, N
+            packed = [torch.empty_like(t) for t in wd]
+            pack = getattr(b.lib, sym + "_W_pack")
+            for src, dst in zip(wd, packed):
+                pack(src.data_ptr(), dst.data_ptr(), n, k)
+            torch.cuda.synchronize()
+            b._lib.check(sym + "_W_pack")
+            wd = packed
+            x = b.dev_copy(o.seeded_normal(2, (m, k)))
+            xq = torch.empty(o.record_bytes("q8_k", k) * m, dtype=torch.uint8, device=b.dev)
+            y = torch.empty(m * n, dtype=torch.float32, device=b.dev)
+
+            def launch(i):
+                fn(wd[i % copies].data_ptr(), x.data_ptr(), xq.data_ptr(), y.data_ptr(), m, k, n)
+
+            nbytes = w.nbytes + 4 * m * k + xq.numel() + 4 * m * n
         else:
             act = o.ACT_OF[fmt]
             x = b.dev_copy(o.seeded_normal(2, (m, k)))

@@ -133,6 +133,19 @@ void production_mul_mat_q4_k_decode(const uint8_t *W, const float *X, uint8_t *X
 /* examples/kernels/mul_mat/q4_k_staged.py:9-37; mul_mat_runtime.cpp:350-354 */
 void production_mul_mat_q4_k_staged(const uint8_t *W, const float *X, uint8_t *Xq, float *Y,
                                     size_t N, size_t K, size_t M);
+/* examples/kernels/mul_mat/q4_k_persistent.py:10-31; mul_mat_runtime.cpp:338-347, :807-808.
+ * W is the Q4K_I[16] interleave of an N x K Q4_K matrix (N a multiple of 16;
+ * layout as for q4_k_q8_k_gemv below), made by _W_pack from row-major Q4_K
+ * (device pointers, target 16-byte aligned).  The artifact-phase functions
+ * take the derive builder's shape names (examples/formats/ggml.py:286-290):
+ * their M is the weight's row count, the kernel's N.  The kernel's shape
+ * parameters come in the artifact's order M, K, N (the builder's symbols
+ * first), M being the activation's rows. */
+size_t production_mul_mat_q4_k_persistent_W_packed_size(size_t M, size_t K);
+void production_mul_mat_q4_k_persistent_W_pack(const uint8_t *source, uint8_t *target, size_t M,
+                                               size_t K);
+void production_mul_mat_q4_k_persistent(const uint8_t *W, const float *X, uint8_t *Xq, float *Y,
+                                        size_t M, size_t K, size_t N);
 /* examples/kernels/mul_mat/iq2_xxs.py; mul_mat_runtime.cpp:472 */
 void production_mul_mat_iq2_xxs(const uint8_t *W, const float *X, uint8_t *Xq, const int8_t *grid,
                                 const int8_t *signs, float *Y, size_t N, size_t K, size_t M);

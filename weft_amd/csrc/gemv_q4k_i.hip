@@ -244,9 +244,14 @@ __global__ void __launch_bounds__(256) q4k_i16_pack_kernel(const uint8_t* __rest
   *reinterpret_cast<uint4*>(dst + 16 * t) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+}  // namespace
+
+namespace {
 bool gemv_shape_ok(size_t M, size_t K) {
   return K % 256 == 0 && M % kCohort == 0 && M <= (size_t)INT32_MAX && K <= (size_t)INT32_MAX;
 }
+
+}  // namespace
 
 size_t q4k_i16_packed_size(size_t M, size_t K) {
   if (!gemv_shape_ok(M, K)) {
@@ -307,7 +312,6 @@ void q4k_i16_gemv(const uint8_t* W, const uint8_t* X, float* Y, size_t M, size_t
   check_launch("q4k_i16_gemv_kernel");
 }
 
-}  // namespace
 }  // namespace weft
 
 extern "C" {

@@ -120,6 +120,17 @@ void mul_mat_q4k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t
 void mul_mat_q4k_quantized(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K,
                            size_t M, const RowStrides& st);
 
+// Q4_K mul_mat over the persisted 16-row interleave Q4K_I[16] (N a multiple
+// of 16): GEMM on the cohort blocks for M >= 16, interleaved GEMV per row.
+void mul_mat_q4k_persistent(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t M,
+                            size_t K, size_t N);
+
+// Q4K_I[16] layout: byte size, device repack from row-major Q4_K, and the
+// GEMV of one Q8_K activation row (M weight rows); errors go to set_error.
+size_t q4k_i16_packed_size(size_t M, size_t K);
+void q4k_i16_pack(const uint8_t* source, uint8_t* target, size_t M, size_t K);
+void q4k_i16_gemv(const uint8_t* W, const uint8_t* X, float* Y, size_t M, size_t K);
+
 // Q4_0 / MXFP4 mul_mat for any M: int8-MFMA GEMM for prefill shapes, GEMV otherwise.
 void mul_mat_q4_0(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
                   size_t M, const RowStrides& st);

@@ -90,6 +90,8 @@ constexpr int kStage = kAQ + kAX + kWT;        // 38912
 constexpr int kAQSlots = kAQ / 1024;           // 17
 constexpr int kAXSlots = kAX / 1024;           // 3
 constexpr int kSlots = kStage / 1024;          // 38 wave-wide 1 KB loads per superblock
+constexpr int kCohortBlock = 16 * kQ4_KBytes;  // 2304: one superblock of a 16-row interleaved cohort
+static_assert(kWT == (kNT / 16) * kCohortBlock, "a weight stage is eight cohort blocks");
 static_assert(kAQ % 1024 == 0 && kAX % 1024 == 0 && kStage % 1024 == 0,
               "every region is a whole number of wave loads");
 static_assert(4 * 32 * 64 * 4 <= 2 * kStage, "reduction buffer fits one ring slot");
@@ -145,7 +147,22 @@ __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
 }
 __device__ __forceinline__ float bf16_lo_to_f32(uint32_t p) { return __uint_as_float(p << 16); }
 
-template <bool kGroup>
+// Eight bytes of row (lane % 16) from eight consecutive 16-byte lines of an
+// interleaved cohort block: lane i of each 16-lane group addresses byte 8 i
+// of the group's 128-byte window and receives row i's byte from each line.
+__device__ __forceinline__ uint2 tr8(uint32_t lds_byte_addr) {
+  typedef int v2i __attribute__((ext_vector_type(2)));
+  typedef __attribute__((address_space(3))) v2i lds_v2i;
+  const v2i v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(size_t)lds_byte_addr);
+  return make_uint2((uint32_t)v.x, (uint32_t)v.y);
+}
+
+// kIlv: W is the 16-row interleave Q4K_I[16] (superblock b of rows 16c ..
+// 16c + 15 is the 2304-byte block (c * nsb + b) * 2304 whose byte 16 j + r is
+// byte j of row 16c + r's record).  A stage then holds the tile's eight
+// cohort blocks as they lie in memory, and each MFMA wave reads its rows'
+// header and nibble bytes transposed (tr8); everything else is the same.
+template <bool kGroup, bool kIlv = false>
 __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
   __shared__ __align__(16) uint8_t ring[4 * kStage];  // [pair slot][parity]
   __shared__ __align__(16) uint32_t zero16[4];
@@ -188,6 +205,9 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
   };
   const int nsb = a.K >> 8;
   const int npair = (nsb + 1) >> 1;
+  // LDS byte addresses as integers from one wave-uniform base (no per-lane
+  // generic-to-LDS pointer casts)
+  const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(ring));
 
   if (wave >= kMfmaWaves) {
     // ---------------------------------------------------------- loader wave
@@ -209,6 +229,11 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
         const int q = 64 * (k - kAQSlots) + lane, r = q / 3, e = q - 3 * r;
         o = (uint32_t)(kGroup ? act_row(min(r, mrows - 1)) : min(r, mrows - 1)) * xrb +
             (e == 0 ? 0 : 244 + 16 * e);
+      } else if constexpr (kIlv) {
+        // line q of the eight 144-line cohort blocks; cohorts past N repeat
+        // the last one (N is a multiple of 16)
+        const int q = 64 * (k - kAQSlots - kAXSlots) + lane, i = q / 144, line = q - 144 * i;
+        o = (uint32_t)(min(n0 + 16 * i, a.N - 16) - n0) * wrb + 16 * line;
       } else {
         const int q = 64 * (k - kAQSlots - kAXSlots) + lane, row = q / 9, part = q - 9 * row;
         o = (uint32_t)(min(n0 + row, a.N - 1) - n0) * wrb + 16 * part;
@@ -217,13 +242,12 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
     }
     auto issue = [&](int pair) {
       const int b = min(2 * pair + par, nsb - 1);
-      uint8_t* stage = ring + (2 * (pair & 1) + par) * kStage;
+      const uint32_t stage = ring_lds + (uint32_t)(2 * (pair & 1) + par) * kStage;
       const uint8_t* xb = xbase + (size_t)b * kQ8_KBytes;
-      const uint8_t* wb = wbase + (size_t)b * kQ4_KBytes;
+      const uint8_t* wb = wbase + (size_t)b * (kIlv ? kCohortBlock : kQ4_KBytes);
 #pragma unroll
       for (int k = 0; k < kSlots; ++k)
-        lds_dma16(k < kAQSlots + kAXSlots ? xb : wb, voff[k],
-                  __builtin_amdgcn_readfirstlane(lds_addr(stage + 1024 * k)));
+        lds_dma16(k < kAQSlots + kAXSlots ? xb : wb, voff[k], stage + 1024 * k);
     };
     // In place in the landed stage, token t = lane: the 16 bsums become f16
     // (min-term A operand) and the 16-byte d chunk becomes the token-scale
@@ -279,8 +303,18 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
     const uint8_t* AQ = stage + kAQRow * col + 16 * kg;          // + 8704 t + 32 s
     const uint8_t* AX = stage + kAQ + 48 * col;                   // + 1536 t
     const uint8_t* wrow = stage + kAQ + kAX + (32 * wcol + col) * kQ4_KBytes;
+    // interleaved: this lane's cohort block and the byte of its row in the
+    // first line of a 16-lane group's window
+    const uint32_t wtr = ring_lds + (uint32_t)(2 * (pair & 1) + par) * kStage + kAQ + kAX +
+                         (uint32_t)(2 * wcol + (col >> 4)) * kCohortBlock + 8 * (lane & 15);
 
-    const uint4 h = *reinterpret_cast<const uint4*>(wrow);
+    uint4 h;
+    if constexpr (kIlv) {
+      const uint2 h0 = tr8(wtr), h1 = tr8(wtr + 128);
+      h = make_uint4(h0.x, h0.y, h1.x, h1.y);
+    } else {
+      h = *reinterpret_cast<const uint4*>(wrow);
+    }
     const float dw = fp16_to_fp32(h.x & 0xffffu);
     const float dmin = fp16_to_fp32(h.x >> 16);
     const bool dz = dw == 0.f;
@@ -309,7 +343,14 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
     for (int t = 0; t < 2; ++t) acur[t] = *reinterpret_cast<const v4i*>(AQ + 32 * kAQRow * t);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const uint4 q = *reinterpret_cast<const uint4*>(wrow + 16 + 32 * g + 16 * kg);
+      uint4 q;
+      if constexpr (kIlv) {
+        const uint32_t ql = wtr + 16 * (16 + 32 * g + 16 * kg);
+        const uint2 q0 = tr8(ql), q1 = tr8(ql + 128);
+        q = make_uint4(q0.x, q0.y, q1.x, q1.y);
+      } else {
+        q = *reinterpret_cast<const uint4*>(wrow + 16 + 32 * g + 16 * kg);
+      }
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
         const int s = 2 * g + hf;
@@ -416,6 +457,7 @@ bool gemm_q4k_ok(const uint8_t* W, size_t N, size_t K, size_t M, const RowStride
          ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT) <= (size_t)INT32_MAX;
 }
 
+template <bool kIlv = false>
 void gemm_q4k(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K, size_t M,
               const RowStrides& st) {
   const size_t rb = K / 256 * kQ4_KBytes;
@@ -429,7 +471,7 @@ void gemm_q4k(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K,
   a.ldw = (uint32_t)(N > 1 ? st.ldw : rb);
   a.ldy = (long long)st.ldy;
   const size_t tiles = ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT);
-  q4k_mfma_gemm<false><<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(a);
+  q4k_mfma_gemm<false, kIlv><<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(a);
   check_launch("q4k_mfma_gemm");
 }
 
@@ -480,6 +522,29 @@ void mul_mat_id_q4k_grouped(const uint8_t* W, const uint8_t* Xq, float* Y, size_
   const size_t wgs = (size_t)g.tmax * ((N + kNT - 1) / kNT);
   q4k_mfma_gemm<true><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(a);
   check_launch("q4k_mfma_gemm");
+}
+
+// production_mul_mat_q4_k_persistent: W is the Q4K_I[16] interleave of an
+// N x K Q4_K matrix (N a multiple of 16), X is M x K, all packed.  X is
+// quantized into Xq (Q8_K), then the GEMM reads the cohort blocks for M >= 16
+// and the interleaved GEMV runs once per activation row below that.
+void mul_mat_q4k_persistent(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t M,
+                            size_t K, size_t N) {
+  if (N == 0 || M == 0 || K == 0) return;
+  const size_t rb = K / 256 * kQ4_KBytes, xrb = K / 256 * kQ8_KBytes;
+  const RowStrides st = packed(rb, K, N);
+  if (K % 256 != 0 || N % 16 != 0 || W == nullptr || X == nullptr || Xq == nullptr ||
+      Y == nullptr || !aligned(W, 16) || !aligned(Xq, 4) || !aligned(Y, 4) || !aligned(X, 4) ||
+      !strides_ok(st, rb, 16, K, N, N, M)) {
+    set_error(hipErrorInvalidValue);
+    return;
+  }
+  quantize_q8_k_rows(X, K, Xq, M, K);
+  if (M >= 16 && gemm_q4k_ok(W, N, K, M, st)) {
+    gemm_q4k<true>(W, Xq, Y, N, K, M, st);
+  } else {
+    for (size_t m = 0; m < M; ++m) q4k_i16_gemv(W, Xq + m * xrb, Y + m * N, N, K);
+  }
 }
 
 void mul_mat_q4k_quantized(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K,

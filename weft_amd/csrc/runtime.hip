@@ -318,6 +318,12 @@ std::vector<KernelSpec> kernel_specs() {
   mm("production_mul_mat_nvfp4", "NVFP4", "Q8_0", false, mx);
   mm("production_mul_mat_nvfp4_decode", "NVFP4", "Q8_0", false, mx);
   mm("production_mul_mat_q5_k_decode", "Q5_K", "Q8_K", false, {});
+  k.push_back({"production_mul_mat_q4_k_persistent",
+               {{"W", "Q4K_I[16]", "N,K", false, nullptr},
+                {"X", "dense.f32", "M,K", false, nullptr},
+                {"Xq", "Q8_K", "M,K", true, nullptr},
+                {"Y", "dense.f32", "M,N", true, nullptr}},
+               "M,K,N"});
   for (const char* sym : {"q4_k_q8_k_gemv", "q4_k_q8_k_gemv_groups4", "q4_k_q8_k_gemv_contract"})
     k.push_back({sym,
                  {{"W", "Q4K_I[16]", "M,K", false, nullptr},

@@ -108,6 +108,7 @@ _DEFS = [
      "examples/kernels/vec_dot/nvfp4_q8_0.py:29-38", None),
     ("production_mul_mat_nvfp4", _MM_MX, "examples/kernels/mul_mat/nvfp4.py:10-43", None),
     ("production_mul_mat_nvfp4_decode", _MM_MX, "examples/kernels/mul_mat/nvfp4_decode.py:10-23", None),
+    ("production_mul_mat_q4_k_persistent", _MM, "examples/kernels/mul_mat/q4_k_persistent.py:10-31", None),
     ("q4_k_q8_k_gemv", ("W", "X", "Y"), "examples/kernels/gemv/q4_k.py:8-26", None),
     ("q4_k_q8_k_gemv_groups4", ("W", "X", "Y"), "examples/kernels/gemv/q4_k_groups4.py:8-26", None),
     ("q4_k_q8_k_gemv_contract", ("W", "X", "Y"), "examples/kernels/gemv/q4_k_contract.py:8-26", None),
