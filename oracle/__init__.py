@@ -20,18 +20,18 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libweft_oracle.so"
 
-Q4_0, Q4_K, IQ2_XXS, MXFP4, Q6_K, Q5_K, NVFP4 = 0, 1, 2, 3, 4, 5, 6
+Q4_0, Q4_K, IQ2_XXS, MXFP4, Q6_K, Q5_K, NVFP4, Q4_1, IQ2_XS = 0, 1, 2, 3, 4, 5, 6, 7, 8
 FORMATS = {"q4_0": Q4_0, "q4_k": Q4_K, "iq2_xxs": IQ2_XXS, "mxfp4": MXFP4, "q6_k": Q6_K, "q5_k": Q5_K,
-           "nvfp4": NVFP4}
+           "nvfp4": NVFP4, "q4_1": Q4_1, "iq2_xs": IQ2_XS}
 
 # (elements per record, bytes per record)
 RECORD = {
     "q4_0": (32, 18), "mxfp4": (32, 17), "q8_0": (32, 34),
     "q4_k": (256, 144), "q8_k": (256, 292), "iq2_xxs": (256, 66), "q6_k": (256, 210),
-    "q5_k": (256, 176), "nvfp4": (64, 36),
+    "q5_k": (256, 176), "nvfp4": (64, 36), "q4_1": (32, 20), "q8_1": (32, 36), "iq2_xs": (256, 74),
 }
 ACT_OF = {"q4_0": "q8_0", "mxfp4": "q8_0", "q4_k": "q8_k", "iq2_xxs": "q8_k", "q6_k": "q8_k", "q5_k": "q8_k",
-          "nvfp4": "q8_0"}
+          "nvfp4": "q8_0", "q4_1": "q8_1", "iq2_xs": "q8_k"}
 
 
 def build() -> Path:
@@ -64,7 +64,7 @@ def _declare(l: ctypes.CDLL) -> None:
         "wo_e8m0_to_fp32_half": ([ctypes.c_uint8], ctypes.c_float),
         "wo_fp16_to_fp32_array": ([_P, _P, _I64], None),
         "wo_fp32_to_fp16_array": ([_P, _P, _I64], None),
-        "wo_iq2xxs_grid": ([_P], None), "wo_ksigns_iq2xs": ([_P], None),
+        "wo_iq2xxs_grid": ([_P], None), "wo_ksigns_iq2xs": ([_P], None), "wo_iq2xs_grid": ([_P], None),
         "wo_signs_i8x8": ([_P], None), "wo_kvalues_mxfp4": ([_P], None),
         "wo_e8m0_half_table": ([_P], None),
         "wo_ue4m3_to_fp32": ([ctypes.c_uint8], ctypes.c_float),
@@ -80,12 +80,12 @@ def _declare(l: ctypes.CDLL) -> None:
         "wo_mul_mat_ggml": ([ctypes.c_int, _P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int], None),
         "wo_evict": ([_P, ctypes.c_size_t], None),
     }
-    for fmt in ("q4_0", "q4_K", "mxfp4", "iq2_xxs", "q6_K", "q5_K", "nvfp4", "q8_0", "q8_K"):
+    for fmt in ("q4_0", "q4_K", "mxfp4", "iq2_xxs", "q6_K", "q5_K", "nvfp4", "q8_0", "q8_K", "q4_1", "q8_1"):
         sig[f"wo_quantize_row_{fmt}"] = ([_P, _P, _I64], None)
-    for fmt in ("q4_0", "q4_K", "mxfp4", "iq2_xxs", "q6_K", "q5_K", "nvfp4"):
+    for fmt in ("q4_0", "q4_K", "mxfp4", "iq2_xxs", "q6_K", "q5_K", "nvfp4", "q4_1", "iq2_xs"):
         sig[f"wo_dequantize_row_{fmt}"] = ([_P, _P, _I64], None)
     for name in ("q4_0_q8_0", "q4_K_q8_K", "iq2_xxs_q8_K", "mxfp4_q8_0", "q6_K_q8_K", "q5_K_q8_K",
-                 "nvfp4_q8_0"):
+                 "nvfp4_q8_0", "q4_1_q8_1", "iq2_xs_q8_K"):
         sig[f"wo_vec_dot_{name}"] = ([_P, _P, _I64], ctypes.c_float)
     for name, (args, res) in sig.items():
         fn = getattr(l, name)
@@ -131,6 +131,13 @@ def iq2xxs_grid() -> np.ndarray:
     return out
 
 
+def iq2xs_grid() -> np.ndarray:
+    """iq2xs_grid (ggml-common.h:617-746) as 512 x 8 bytes."""
+    out = np.empty(4096, np.uint8)
+    lib().wo_iq2xs_grid(_ptr(out))
+    return out
+
+
 def ksigns_iq2xs() -> np.ndarray:
     out = np.empty(128, np.uint8)
     lib().wo_ksigns_iq2xs(_ptr(out))
@@ -171,8 +178,11 @@ def quantize(fmt: str, x: np.ndarray, out: np.ndarray | None = None) -> np.ndarr
     rb = record_bytes(fmt, k)
     if out is None:
         out = np.zeros(x.shape[:-1] + (rb,), np.uint8)
+    if fmt == "iq2_xs":
+        raise ValueError("no IQ2_XS weight quantizer: tests use random_records('iq2_xs', ...)")
     name = {"q4_0": "q4_0", "q4_k": "q4_K", "mxfp4": "mxfp4", "iq2_xxs": "iq2_xxs",
-            "q6_k": "q6_K", "q5_k": "q5_K", "nvfp4": "nvfp4", "q8_0": "q8_0", "q8_k": "q8_K"}[fmt]
+            "q6_k": "q6_K", "q5_k": "q5_K", "nvfp4": "nvfp4", "q8_0": "q8_0", "q8_k": "q8_K",
+            "q4_1": "q4_1", "q8_1": "q8_1"}[fmt]
     fn = getattr(lib(), f"wo_quantize_row_{name}")
     # one call over all rows: records never straddle rows
     fn(_ptr(x), _ptr(out), rows * k)
@@ -186,13 +196,14 @@ def dequantize(fmt: str, w: np.ndarray, k: int) -> np.ndarray:
     rows = w.size // rb if rb else 0
     out = np.empty(w.shape[:-1] + (k,), np.float32)
     name = {"q4_0": "q4_0", "q4_k": "q4_K", "mxfp4": "mxfp4", "iq2_xxs": "iq2_xxs", "q6_k": "q6_K", "q5_k": "q5_K",
-            "nvfp4": "nvfp4"}[fmt]
+            "nvfp4": "nvfp4", "q4_1": "q4_1", "iq2_xs": "iq2_xs"}[fmt]
     getattr(lib(), f"wo_dequantize_row_{name}")(_ptr(w), _ptr(out), rows * k)
     return out
 
 
 _VEC_DOT = {"q4_0": "q4_0_q8_0", "q4_k": "q4_K_q8_K", "iq2_xxs": "iq2_xxs_q8_K",
-            "mxfp4": "mxfp4_q8_0", "q6_k": "q6_K_q8_K", "q5_k": "q5_K_q8_K", "nvfp4": "nvfp4_q8_0"}
+            "mxfp4": "mxfp4_q8_0", "q6_k": "q6_K_q8_K", "q5_k": "q5_K_q8_K", "nvfp4": "nvfp4_q8_0",
+            "q4_1": "q4_1_q8_1", "iq2_xs": "iq2_xs_q8_K"}
 
 
 def vec_dot(fmt: str, w: np.ndarray, x: np.ndarray, k: int) -> float:
@@ -270,6 +281,19 @@ def interleave_rows(w: np.ndarray, n: int, k: int, rows: int = 16) -> np.ndarray
         raise ValueError("Q4K_I needs whole row cohorts and whole superblocks")
     src = np.ascontiguousarray(w, dtype=np.uint8).reshape(n // rows, rows, nsb, 144)
     return np.ascontiguousarray(src.transpose(0, 2, 3, 1)).reshape(-1)
+
+
+def random_records(fmt: str, n: int, k: int, seed: int = 0) -> np.ndarray:
+    """Rows of records with random payload bytes and a moderate fp16 scale
+    (every byte pattern of these formats is a valid record).  The input
+    generator for IQ2_XS, whose GGML quantizer (an importance-weighted grid
+    search) is not restated here."""
+    rng = np.random.default_rng(seed)
+    nrec = k // RECORD[fmt][0]
+    rec = rng.integers(0, 256, size=(n, nrec, RECORD[fmt][1]), dtype=np.uint8)
+    d = fp32_to_fp16(rng.uniform(1e-4, 2e-3, size=(n, nrec)).astype(np.float32))
+    rec[:, :, 0:2] = d.view(np.uint8).reshape(n, nrec, 2)
+    return rec.reshape(n, -1)
 
 
 def max_threads() -> int:

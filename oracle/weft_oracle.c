@@ -42,6 +42,9 @@
 #define Q5_K_BYTES 176
 #define QK_NVFP4 64
 #define NVFP4_BYTES 36
+#define Q4_1_BYTES 20
+#define Q8_1_BYTES 36
+#define IQ2_XS_BYTES 74
 #define GROUP_MAX_EPS 1e-15f
 
 static inline uint32_t f32_bits(float f) {
@@ -163,6 +166,50 @@ void wo_iq2xxs_grid(uint8_t out[2048]) {
   static const uint8_t lane_value[4] = {0x08, 0x19, 0x2b, 0x00};
   for (int i = 0; i < 256; ++i)
     for (int j = 0; j < 8; ++j) out[8 * i + j] = lane_value[(kIq2xxsCodes[i] >> (2 * j)) & 3];
+}
+
+/* iq2xs_grid (ggml-common.h:617-746): 512 entries of 8 magnitudes in
+ * {0x08, 0x19, 0x2b}, here as two bits per lane (0, 1, 2), lane 0 in the low
+ * bits; the codes ascend with the table index. */
+static const uint16_t kIq2xsCodes[512] = {
+        0,     2,     5,     8,    10,    17,    20,    22,    25,    32,    34,    37,    40,    65,    68,    70,
+       73,    80,    82,    85,    88,    97,   100,   128,   130,   133,   136,   145,   148,   153,   160,   257,
+      260,   262,   265,   272,   274,   277,   280,   282,   289,   292,   320,   322,   325,   328,   337,   340,
+      352,   360,   385,   388,   400,   512,   514,   517,   520,   529,   532,   544,   577,   580,   592,   597,
+      640,   650,  1025,  1028,  1030,  1033,  1040,  1042,  1045,  1048,  1057,  1060,  1088,  1090,  1093,  1096,
+     1105,  1108,  1110,  1120,  1153,  1156,  1168,  1280,  1282,  1285,  1288,  1297,  1300,  1312,  1345,  1348,
+     1360,  1377,  1408,  1537,  1540,  1552,  1574,  1600,  1602,  1668,  2048,  2050,  2053,  2056,  2058,  2065,
+     2068,  2080,  2085,  2113,  2116,  2128,  2136,  2176,  2208,  2218,  2305,  2308,  2320,  2368,  2433,  2441,
+     2560,  2592,  2600,  2710,  2720,  4097,  4100,  4102,  4105,  4112,  4114,  4117,  4120,  4129,  4132,  4160,
+     4162,  4165,  4168,  4177,  4180,  4192,  4202,  4225,  4228,  4240,  4352,  4354,  4357,  4360,  4369,  4372,
+     4384,  4417,  4420,  4432,  4480,  4500,  4502,  4609,  4612,  4614,  4624,  4672,  4704,  5120,  5122,  5125,
+     5128,  5137,  5140,  5152,  5185,  5188,  5193,  5200,  5220,  5248,  5377,  5380,  5392,  5440,  5632,  5652,
+     5705,  6145,  6148,  6160,  6162,  6208,  6228,  6278,  6400,  6405,  6502,  6737,  6825,  8192,  8194,  8197,
+     8200,  8202,  8209,  8212,  8224,  8257,  8260,  8272,  8320,  8352,  8449,  8452,  8464,  8512,  8520,  8549,
+     8704,  8738,  8832,  8872,  9217,  9220,  9232,  9257,  9280,  9472,  9537,  9554,  9625,  9729,  9754,  9894,
+    10240, 10248, 10250, 10272, 10325, 10376, 10402, 10600, 10640, 10760, 10784, 10882, 10888, 10890, 16385, 16388,
+    16390, 16393, 16400, 16402, 16405, 16408, 16417, 16420, 16448, 16450, 16453, 16456, 16458, 16465, 16468, 16480,
+    16485, 16513, 16516, 16528, 16640, 16642, 16645, 16648, 16657, 16660, 16672, 16705, 16708, 16720, 16768, 16773,
+    16802, 16897, 16900, 16912, 16914, 16937, 16960, 17408, 17410, 17413, 17416, 17425, 17428, 17433, 17440, 17473,
+    17476, 17488, 17536, 17556, 17665, 17668, 17680, 17700, 17728, 17818, 17920, 17930, 17988, 18000, 18433, 18436,
+    18448, 18496, 18501, 18516, 18530, 18688, 18705, 18756, 18768, 18793, 18948, 20480, 20482, 20485, 20488, 20497,
+    20500, 20512, 20520, 20545, 20548, 20560, 20608, 20737, 20740, 20752, 20757, 20800, 20802, 20992, 21060, 21162,
+    21505, 21508, 21520, 21537, 21568, 21600, 21633, 21665, 21760, 21768, 21888, 21896, 22049, 22120, 22177, 22528,
+    22548, 22593, 22608, 22681, 22810, 22848, 22850, 23173, 24577, 24580, 24592, 24640, 24660, 24674, 24710, 24745,
+    24832, 25124, 25162, 25234, 25600, 25622, 25872, 25920, 25925, 26020, 26625, 26730, 26917, 27142, 27220, 27234,
+    32768, 32770, 32773, 32776, 32785, 32788, 32800, 32810, 32833, 32836, 32848, 32896, 32898, 32936, 32938, 33025,
+    33028, 33030, 33040, 33088, 33105, 33113, 33280, 33312, 33408, 33410, 33440, 33448, 33793, 33796, 33808, 33810,
+    33813, 33856, 33888, 33929, 34048, 34116, 34213, 34328, 34410, 34816, 34824, 34853, 34906, 34944, 34946, 34984,
+    35078, 35362, 35456, 35464, 35478, 35496, 36865, 36868, 36880, 36928, 36950, 36996, 37120, 37154, 37220, 37462,
+    37513, 37888, 37893, 37956, 37968, 37976, 38185, 38288, 38290, 38465, 38993, 39078, 39241, 39445, 39520, 40960,
+    40962, 40968, 40970, 40992, 41002, 41120, 41297, 41305, 41382, 41472, 41474, 41480, 41514, 41600, 41632, 42048,
+    42133, 42597, 42648, 43018, 43040, 43042, 43048, 43168, 43176, 43268, 43396, 43398, 43560, 43562, 43665, 43690,
+};
+
+void wo_iq2xs_grid(uint8_t out[4096]) {
+  static const uint8_t lane_value[4] = {0x08, 0x19, 0x2b, 0x00};
+  for (int i = 0; i < 512; ++i)
+    for (int j = 0; j < 8; ++j) out[8 * i + j] = lane_value[(kIq2xsCodes[i] >> (2 * j)) & 3];
 }
 
 void wo_ksigns_iq2xs(uint8_t out[128]) {
@@ -659,6 +706,53 @@ void wo_quantize_row_q8_0(const float *x, uint8_t *y, int64_t k) {
   }
 }
 
+/* quantize_row_q4_1_ref, ggml-quants.c:112-146: d = (max - min) / 15,
+ * m = min, q = MIN(15, (int8_t)((x - min) * id + 0.5f)). */
+void wo_quantize_row_q4_1(const float *x, uint8_t *y, int64_t k) {
+  const int64_t nb = k / 32;
+  for (int64_t i = 0; i < nb; ++i) {
+    const float *xb = x + i * 32;
+    uint8_t *rec = y + i * Q4_1_BYTES;
+    float min = 3.402823466e+38f, max = -3.402823466e+38f;
+    for (int j = 0; j < 32; ++j) {
+      if (xb[j] < min) min = xb[j];
+      if (xb[j] > max) max = xb[j];
+    }
+    const float d = (max - min) / 15;
+    const float id = d ? 1.0f / d : 0.0f;
+    wr16(rec, wo_fp32_to_fp16(d));
+    wr16(rec + 2, wo_fp32_to_fp16(min));
+    for (int j = 0; j < 16; ++j) {
+      const float x0 = (xb[j] - min) * id, x1 = (xb[16 + j] - min) * id;
+      const int v0 = (int8_t)(x0 + 0.5f), v1 = (int8_t)(x1 + 0.5f);
+      const uint8_t q0 = (uint8_t)(v0 < 15 ? v0 : 15), q1 = (uint8_t)(v1 < 15 ? v1 : 15);
+      rec[4 + j] = (uint8_t)(q0 | (q1 << 4));
+    }
+  }
+}
+
+/* quantize_row_q8_1_ref, ggml-quants.c:264-295: Q8_0's d and roundf codes,
+ * plus s = fp16(sum(q) * d) with the fp32 d. */
+void wo_quantize_row_q8_1(const float *x, uint8_t *y, int64_t k) {
+  const int64_t nb = k / 32;
+  for (int64_t i = 0; i < nb; ++i) {
+    const float *xb = x + i * 32;
+    uint8_t *rec = y + i * Q8_1_BYTES;
+    float amax = 0.0f;
+    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(xb[j]));
+    const float d = amax / 127;
+    const float id = d ? 1.0f / d : 0.0f;
+    wr16(rec, wo_fp32_to_fp16(d));
+    int sum = 0;
+    for (int j = 0; j < 32; ++j) {
+      const int8_t q = (int8_t)roundf(xb[j] * id);
+      rec[4 + j] = (uint8_t)q;
+      sum += q;
+    }
+    wr16(rec + 2, wo_fp32_to_fp16(sum * d));
+  }
+}
+
 /* quantize_row_q8_K_ref, ggml-quants.c:2696-2733: the signed value at the
  * first index of the largest |x| sets iscale = -127/max; q = RNE(iscale*x)
  * capped at 127; bsums = sums of 16; d = 1/iscale.  An all-zero block writes
@@ -711,6 +805,41 @@ void wo_dequantize_row_q4_0(const uint8_t *x, float *y, int64_t k) {
       const int x1 = (rec[2 + j] >> 4) - 8;
       y[i * QK4_0 + j] = x0 * d;
       y[i * QK4_0 + j + QK4_0 / 2] = x1 * d;
+    }
+  }
+}
+
+/* dequantize_row_q4_1, ggml-quants.c:421-439 */
+void wo_dequantize_row_q4_1(const uint8_t *x, float *y, int64_t k) {
+  const int64_t nb = k / 32;
+  for (int64_t i = 0; i < nb; ++i) {
+    const uint8_t *rec = x + i * Q4_1_BYTES;
+    const float d = wo_fp16_to_fp32(rd16(rec)), m = wo_fp16_to_fp32(rd16(rec + 2));
+    for (int j = 0; j < 16; ++j) {
+      y[i * 32 + j] = (rec[4 + j] & 0x0F) * d + m;
+      y[i * 32 + j + 16] = (rec[4 + j] >> 4) * d + m;
+    }
+  }
+}
+
+/* dequantize_row_iq2_xs, ggml-quants.c:2444-2467 */
+void wo_dequantize_row_iq2_xs(const uint8_t *x, float *y, int64_t k) {
+  uint8_t grid[4096], ks[128];
+  wo_iq2xs_grid(grid);
+  wo_ksigns_iq2xs(ks);
+  const int64_t nb = k / QK_K;
+  for (int64_t i = 0; i < nb; ++i) {
+    const uint8_t *rec = x + i * IQ2_XS_BYTES;
+    const float d = wo_fp16_to_fp32(rd16(rec));
+    for (int ib32 = 0; ib32 < 8; ++ib32) {
+      const uint8_t sc = rec[66 + ib32];
+      const float db[2] = {d * (0.5f + (sc & 0xf)) * 0.25f, d * (0.5f + (sc >> 4)) * 0.25f};
+      for (int l = 0; l < 4; ++l) {
+        const uint16_t q = rd16(rec + 2 + 2 * (4 * ib32 + l));
+        const uint8_t *g = grid + 8 * (q & 511);
+        const uint8_t signs = ks[q >> 9];
+        for (int j = 0; j < 8; ++j) *y++ = db[l / 2] * g[j] * (signs & (1 << j) ? -1.f : 1.f);
+      }
     }
   }
 }
@@ -799,6 +928,59 @@ float wo_vec_dot_q4_0_q8_0(const uint8_t *w, const uint8_t *x, int64_t k) {
     sumf += sumi * wo_fp16_to_fp32(rd16(wr)) * wo_fp16_to_fp32(rd16(xr));
   }
   return sumf;
+}
+
+/* ggml_vec_dot_q4_1_q8_1_generic, ggml-cpu/quants.c:211-245 */
+float wo_vec_dot_q4_1_q8_1(const uint8_t *w, const uint8_t *x, int64_t k) {
+  const int64_t nb = k / 32;
+  float sumf = 0;
+  for (int64_t ib = 0; ib < nb; ++ib) {
+    const uint8_t *wr = w + ib * Q4_1_BYTES;
+    const uint8_t *xr = x + ib * Q8_1_BYTES;
+    const int8_t *xq = (const int8_t *)(xr + 4);
+    int sumi0 = 0, sumi1 = 0;
+    for (int j = 0; j < 16; ++j) {
+      sumi0 += (wr[4 + j] & 0x0F) * xq[j];
+      sumi1 += (wr[4 + j] >> 4) * xq[j + 16];
+    }
+    const int sumi = sumi0 + sumi1;
+    sumf += (wo_fp16_to_fp32(rd16(wr)) * wo_fp16_to_fp32(rd16(xr))) * sumi +
+            wo_fp16_to_fp32(rd16(wr + 2)) * wo_fp16_to_fp32(rd16(xr + 2));
+  }
+  return sumf;
+}
+
+/* ggml_vec_dot_iq2_xs_q8_K_generic, ggml-cpu/quants.c:897-946 */
+float wo_vec_dot_iq2_xs_q8_K(const uint8_t *w, const uint8_t *x, int64_t k) {
+  uint8_t grid[4096], ks[128];
+  wo_iq2xs_grid(grid);
+  wo_ksigns_iq2xs(ks);
+  const int64_t nb = k / QK_K;
+  float sumf = 0.f;
+  for (int64_t i = 0; i < nb; ++i) {
+    const uint8_t *wr = w + i * IQ2_XS_BYTES;
+    const uint8_t *xr = x + i * Q8_K_BYTES;
+    const float d = wo_fp16_to_fp32(rd16(wr)) * rdf32(xr);
+    const int8_t *q8 = (const int8_t *)(xr + 4);
+    int32_t bsum = 0;
+    for (int ib32 = 0; ib32 < 8; ++ib32) {
+      const uint8_t sc = wr[66 + ib32];
+      const int ls[2] = {2 * (sc & 0xf) + 1, 2 * (sc >> 4) + 1};
+      for (int h = 0; h < 2; ++h) {
+        int32_t sumi = 0;
+        for (int l = 2 * h; l < 2 * h + 2; ++l) {
+          const uint16_t q = rd16(wr + 2 + 2 * (4 * ib32 + l));
+          const uint8_t *g = grid + 8 * (q & 511);
+          const uint8_t signs = ks[q >> 9];
+          for (int j = 0; j < 8; ++j) sumi += g[j] * q8[j] * (signs & (1 << j) ? -1 : 1);
+          q8 += 8;
+        }
+        bsum += sumi * ls[h];
+      }
+    }
+    sumf += d * bsum;
+  }
+  return 0.125f * sumf;
 }
 
 /* ggml_vec_dot_mxfp4_q8_0_generic, ggml-cpu/quants.c:247-276 */
@@ -1161,11 +1343,14 @@ size_t wo_weight_row_bytes(int fmt, int64_t k) {
   case WO_Q6_K: return (size_t)(k / 256) * Q6_K_BYTES;
   case WO_Q5_K: return (size_t)(k / 256) * Q5_K_BYTES;
   case WO_NVFP4: return (size_t)(k / QK_NVFP4) * NVFP4_BYTES;
+  case WO_Q4_1: return (size_t)(k / 32) * Q4_1_BYTES;
+  case WO_IQ2_XS: return (size_t)(k / 256) * IQ2_XS_BYTES;
   }
   return 0;
 }
 
 size_t wo_act_row_bytes(int fmt, int64_t k) {
+  if (fmt == WO_Q4_1) return (size_t)(k / 32) * Q8_1_BYTES;
   if (fmt == WO_Q4_0 || fmt == WO_MXFP4 || fmt == WO_NVFP4) return (size_t)(k / 32) * Q8_0_BYTES;
   return (size_t)(k / 256) * Q8_K_BYTES;
 }
@@ -1180,8 +1365,20 @@ static vec_dot_fn select_vec_dot(int fmt) {
   case WO_Q6_K: return wo_vec_dot_q6_K_q8_K;
   case WO_Q5_K: return wo_vec_dot_q5_K_q8_K;
   case WO_NVFP4: return wo_vec_dot_nvfp4_q8_0;
+  case WO_Q4_1: return wo_vec_dot_q4_1_q8_1;
+  case WO_IQ2_XS: return wo_vec_dot_iq2_xs_q8_K;
   }
   return 0;
+}
+
+/* the activation quantizer of a weight format: Q8_0, Q8_1 or Q8_K rows */
+static void quantize_act(int fmt, const float *x, uint8_t *y, int64_t k) {
+  if (fmt == WO_Q4_1)
+    wo_quantize_row_q8_1(x, y, k);
+  else if (fmt == WO_Q4_0 || fmt == WO_MXFP4 || fmt == WO_NVFP4)
+    wo_quantize_row_q8_0(x, y, k);
+  else
+    wo_quantize_row_q8_K(x, y, k);
 }
 
 int wo_max_threads(void) {
@@ -1206,15 +1403,9 @@ void wo_mul_mat_q(int fmt, const uint8_t *W, const uint8_t *Xq, float *Y, int64_
 void wo_mul_mat(int fmt, const uint8_t *W, const float *X, uint8_t *Xq, float *Y, int64_t N,
                 int64_t K, int64_t M, int nthreads) {
   const size_t xrow = wo_act_row_bytes(fmt, K);
-  const int q80 = (fmt == WO_Q4_0 || fmt == WO_MXFP4 || fmt == WO_NVFP4);
   if (nthreads <= 0) nthreads = wo_max_threads();
 #pragma omp parallel for num_threads(nthreads) schedule(static)
-  for (int64_t m = 0; m < M; ++m) {
-    if (q80)
-      wo_quantize_row_q8_0(X + m * K, Xq + m * xrow, K);
-    else
-      wo_quantize_row_q8_K(X + m * K, Xq + m * xrow, K);
-  }
+  for (int64_t m = 0; m < M; ++m) quantize_act(fmt, X + m * K, Xq + m * xrow, K);
   wo_mul_mat_q(fmt, W, Xq, Y, N, K, M, nthreads);
 }
 
@@ -1225,9 +1416,9 @@ void wo_mul_mat(int fmt, const uint8_t *W, const float *X, uint8_t *Xq, float *Y
 void wo_mul_mat_ggml(int fmt, const uint8_t *W, const float *X, uint8_t *Xq, float *Y,
                      int64_t N, int64_t K, int64_t M, int nthreads) {
   const vec_dot_fn dot = select_vec_dot(fmt);
-  const int q80 = (fmt == WO_Q4_0 || fmt == WO_MXFP4 || fmt == WO_NVFP4);
+  const int q80 = (fmt == WO_Q4_0 || fmt == WO_MXFP4 || fmt == WO_NVFP4 || fmt == WO_Q4_1);
   const int64_t bs = q80 ? QK8_0 : QK_K;
-  const size_t blk_bytes = q80 ? Q8_0_BYTES : Q8_K_BYTES;
+  const size_t blk_bytes = fmt == WO_Q4_1 ? Q8_1_BYTES : q80 ? Q8_0_BYTES : Q8_K_BYTES;
   const size_t wrow = wo_weight_row_bytes(fmt, K), xrow = wo_act_row_bytes(fmt, K);
   if (nthreads <= 0) nthreads = wo_max_threads();
   _Atomic int64_t next_chunk = 0;
@@ -1237,12 +1428,7 @@ void wo_mul_mat_ggml(int fmt, const uint8_t *W, const float *X, uint8_t *Xq, flo
     const int64_t nb = K / bs;
     for (int64_t m = 0; m < M; ++m) {
       const int64_t b0 = ith * nb / nth, b1 = (ith + 1) * nb / nth;
-      if (b1 > b0) {
-        if (q80)
-          wo_quantize_row_q8_0(X + m * K + b0 * bs, Xq + m * xrow + b0 * blk_bytes, (b1 - b0) * bs);
-        else
-          wo_quantize_row_q8_K(X + m * K + b0 * bs, Xq + m * xrow + b0 * blk_bytes, (b1 - b0) * bs);
-      }
+      if (b1 > b0) quantize_act(fmt, X + m * K + b0 * bs, Xq + m * xrow + b0 * blk_bytes, (b1 - b0) * bs);
     }
     if (ith == 0) next_chunk = nth;  /* every thread starts at its own index */
 #pragma omp barrier
@@ -1296,6 +1482,33 @@ int64_t wo_int_partials(int fmt, const uint8_t *w, const uint8_t *x, int64_t k, 
         s += v0 * xq[j] + v1 * xq[j + 16];
       }
       out[n++] = s;
+    }
+  } else if (fmt == WO_Q4_1) {
+    for (int64_t ib = 0; ib < k / 32; ++ib) {
+      const uint8_t *qs = w + ib * Q4_1_BYTES + 4;
+      const int8_t *xq = (const int8_t *)(x + ib * Q8_1_BYTES + 4);
+      int32_t s = 0;
+      for (int j = 0; j < 16; ++j) s += (qs[j] & 0xF) * xq[j] + (qs[j] >> 4) * xq[j + 16];
+      out[n++] = s;
+    }
+  } else if (fmt == WO_IQ2_XS) {
+    /* one int32 per 16-element half group: the partial its 4-bit scale
+     * multiplies */
+    uint8_t grid[4096], ks[128];
+    wo_iq2xs_grid(grid);
+    wo_ksigns_iq2xs(ks);
+    for (int64_t i = 0; i < k / QK_K; ++i) {
+      const uint8_t *wr = w + i * IQ2_XS_BYTES;
+      const int8_t *q8 = (const int8_t *)(x + i * Q8_K_BYTES + 4);
+      for (int h = 0; h < 16; ++h) {
+        int32_t s = 0;
+        for (int l = 2 * h; l < 2 * h + 2; ++l) {
+          const uint16_t q = rd16(wr + 2 + 2 * l);
+          for (int j = 0; j < 8; ++j)
+            s += grid[8 * (q & 511) + j] * q8[8 * l + j] * ((ks[q >> 9] >> j) & 1 ? -1 : 1);
+        }
+        out[n++] = s;
+      }
     }
   } else if (fmt == WO_NVFP4) {
     /* one int32 per 16-element sub-block */
@@ -1382,7 +1595,31 @@ void wo_mul_mat_f64(int fmt, const uint8_t *W, const uint8_t *Xq, double *E, dou
       const uint8_t *w = W + n * wrow;
       const uint8_t *x = Xq + m * xrow;
       double e = 0, a = 0;
-      if (fmt == WO_Q4_0 || fmt == WO_MXFP4) {
+      if (fmt == WO_Q4_1) {
+        for (int64_t base = 0; base < K; base += 8192) {
+          const int64_t kk = K - base < 8192 ? K - base : 8192;
+          const int64_t nbase = base / 32;
+          const int64_t np = wo_int_partials(fmt, w + nbase * Q4_1_BYTES, x + nbase * Q8_1_BYTES, kk, parts);
+          for (int64_t b = 0; b < np; ++b) {
+            const uint8_t *wr = w + (nbase + b) * Q4_1_BYTES, *xr = x + (nbase + b) * Q8_1_BYTES;
+            const double t1 = (double)wo_fp16_to_fp32(rd16(wr)) * wo_fp16_to_fp32(rd16(xr)) * parts[b];
+            const double t2 = (double)wo_fp16_to_fp32(rd16(wr + 2)) * wo_fp16_to_fp32(rd16(xr + 2));
+            e += t1 + t2;
+            a += fabs(t1) + fabs(t2);
+          }
+        }
+      } else if (fmt == WO_IQ2_XS) {
+        for (int64_t i = 0; i < K / QK_K; ++i) {
+          const uint8_t *wr = w + i * IQ2_XS_BYTES;
+          const uint8_t *xr = x + i * Q8_K_BYTES;
+          wo_int_partials(fmt, wr, xr, QK_K, parts);
+          int64_t S = 0;
+          for (int h = 0; h < 16; ++h) S += (int64_t)(2 * ((wr[66 + h / 2] >> (4 * (h & 1))) & 0xf) + 1) * parts[h];
+          const double t = 0.125 * wo_fp16_to_fp32(rd16(wr)) * (double)rdf32(xr) * (double)S;
+          e += t;
+          a += fabs(t);
+        }
+      } else if (fmt == WO_Q4_0 || fmt == WO_MXFP4) {
         for (int64_t base = 0; base < K; base += 8192) {
           const int64_t kk = K - base < 8192 ? K - base : 8192;
           const int64_t nbase = base / 32;

@@ -35,6 +35,8 @@ enum wo_format {
   WO_Q6_K = 4,
   WO_Q5_K = 5,
   WO_NVFP4 = 6,
+  WO_Q4_1 = 7,
+  WO_IQ2_XS = 8,
 };
 
 /* scalar conversions (ggml-impl.h:384-431, :477-495) */
@@ -49,6 +51,7 @@ void wo_iq2xxs_grid(uint8_t out[2048]);  /* 256 x 8 magnitudes {8,25,43} */
 void wo_ksigns_iq2xs(uint8_t out[128]);  /* i | parity(i) << 7 */
 void wo_signs_i8x8(int8_t out[1024]);    /* 128 x 8 of +-1, the ABI's I8X8 sign table */
 void wo_kvalues_mxfp4(int8_t out[16]);   /* doubled e2m1 */
+void wo_iq2xs_grid(uint8_t out[4096]);   /* 512 x 8 magnitudes {8,25,43} */
 void wo_e8m0_half_table(float out[256]);
 float wo_ue4m3_to_fp32(uint8_t x);       /* ggml_ue4m3_to_fp32, incl. the 1/2 */
 uint8_t wo_fp32_to_ue4m3(float x);
@@ -62,10 +65,12 @@ void wo_quantize_row_iq2_xxs(const float *x, uint8_t *y, int64_t k);
 void wo_quantize_row_q6_K(const float *x, uint8_t *y, int64_t k);
 void wo_quantize_row_q5_K(const float *x, uint8_t *y, int64_t k);
 void wo_quantize_row_nvfp4(const float *x, uint8_t *y, int64_t k);
+void wo_quantize_row_q4_1(const float *x, uint8_t *y, int64_t k);
 
 /* activation quantizers (on the hot path) */
 void wo_quantize_row_q8_0(const float *x, uint8_t *y, int64_t k);
 void wo_quantize_row_q8_K(const float *x, uint8_t *y, int64_t k);
+void wo_quantize_row_q8_1(const float *x, uint8_t *y, int64_t k);
 
 /* row dequantizers */
 void wo_dequantize_row_q4_0(const uint8_t *x, float *y, int64_t k);
@@ -75,6 +80,8 @@ void wo_dequantize_row_mxfp4(const uint8_t *x, float *y, int64_t k);
 void wo_dequantize_row_q6_K(const uint8_t *x, float *y, int64_t k);
 void wo_dequantize_row_q5_K(const uint8_t *x, float *y, int64_t k);
 void wo_dequantize_row_nvfp4(const uint8_t *x, float *y, int64_t k);
+void wo_dequantize_row_q4_1(const uint8_t *x, float *y, int64_t k);
+void wo_dequantize_row_iq2_xs(const uint8_t *x, float *y, int64_t k);
 
 /* generic vec_dots: w row (k elements) . quantized activation row */
 float wo_vec_dot_q4_0_q8_0(const uint8_t *w, const uint8_t *x, int64_t k);
@@ -84,6 +91,8 @@ float wo_vec_dot_mxfp4_q8_0(const uint8_t *w, const uint8_t *x, int64_t k);
 float wo_vec_dot_q6_K_q8_K(const uint8_t *w, const uint8_t *x, int64_t k);
 float wo_vec_dot_q5_K_q8_K(const uint8_t *w, const uint8_t *x, int64_t k);
 float wo_vec_dot_nvfp4_q8_0(const uint8_t *w, const uint8_t *x, int64_t k);
+float wo_vec_dot_q4_1_q8_1(const uint8_t *w, const uint8_t *x, int64_t k);
+float wo_vec_dot_iq2_xs_q8_K(const uint8_t *w, const uint8_t *x, int64_t k);
 
 /* Bytes of one encoded row of k elements for a weight format, or of the
  * activation format that pairs with it (Q8_0 for Q4_0/MXFP4, Q8_K else). */

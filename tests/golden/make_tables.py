@@ -4,7 +4,7 @@ The tables are data the record formats are defined by; they are read here as
 text (nothing of the reference is imported or executed) from
   source/c/ggml/llama.cpp/ggml/src/ggml-common.h
     kmask_iq2xs (:499-501), ksigns_iq2xs (:503-512), iq2xxs_grid (:550-615),
-    kvalues_mxfp4 (:1116-1118)
+    iq2xs_grid (:617-746), kvalues_mxfp4 (:1116-1118)
 and the record sizes from the static_asserts next to each block struct.
 Run in the build container:  python tests/golden/make_tables.py
 """
@@ -39,10 +39,12 @@ def main() -> int:
         "kmask_iq2xs": table(common, "kmask_iq2xs"),
         "ksigns_iq2xs": table(common, "ksigns_iq2xs"),
         "iq2xxs_grid": [f"{v:016x}" for v in table(common, "iq2xxs_grid")],
+        "iq2xs_grid": [f"{v:016x}" for v in table(common, "iq2xs_grid")],
         "kvalues_mxfp4": table(common, "kvalues_mxfp4"),
         "record_size_asserts": {k: asserts[k].strip() for k in
                                 ("block_q4_0", "block_mxfp4", "block_q8_0", "block_q4_K",
-                                 "block_q8_K", "block_iq2_xxs", "block_q6_K", "block_q5_K", "block_nvfp4")
+                                 "block_q8_K", "block_iq2_xxs", "block_q6_K", "block_q5_K", "block_nvfp4",
+                                 "block_q4_1", "block_q8_1", "block_iq2_xs")
                                  if k in asserts},
     }
     OUT.write_text(json.dumps(out, indent=1) + "\n")

@@ -77,6 +77,13 @@ def test_iq2xxs_grid_matches_ggml_table():
     assert set(np.unique(o.iq2xxs_grid())) == {0x08, 0x19, 0x2b}
 
 
+def test_iq2xs_grid_matches_ggml_table():
+    want = np.array([int(x, 16) for x in GOLDEN["iq2xs_grid"]], np.uint64)
+    got = o.iq2xs_grid().view(np.uint64)
+    assert np.array_equal(got, want)
+    assert set(np.unique(o.iq2xs_grid())) == {0x08, 0x19, 0x2b}
+
+
 def test_sign_tables_match_ggml():
     assert list(o.ksigns_iq2xs()) == GOLDEN["ksigns_iq2xs"]
     kmask = GOLDEN["kmask_iq2xs"]
@@ -95,7 +102,7 @@ def test_record_sizes_match_ggml_static_asserts():
     # QK_MXFP4 = 32, QK_K = 256, K_SCALE_SIZE = 12, ggml_half = 2 bytes
     env = {"ggml_half": 2, "uint8_t": 1, "int16_t": 2, "uint16_t": 2, "float": 4,
            "QK4_0": 32, "QK8_0": 32, "QK_MXFP4": 32, "QK_K": 256, "K_SCALE_SIZE": 12,
-           "QK_NVFP4_SUB": 16, "QK_NVFP4": 64}
+           "QK_NVFP4_SUB": 16, "QK_NVFP4": 64, "QK4_1": 32, "QK8_1": 32}
     sizes = {}
     for k, expr in GOLDEN["record_size_asserts"].items():
         e = expr.replace("sizeof", "")
@@ -104,10 +111,10 @@ def test_record_sizes_match_ggml_static_asserts():
         sizes[k] = eval(e, {"__builtins__": {}})  # arithmetic on literals only
     assert sizes == {"block_q4_0": 18, "block_mxfp4": 17, "block_q8_0": 34, "block_q4_K": 144,
                      "block_q8_K": 292, "block_iq2_xxs": 66, "block_q6_K": 210, "block_q5_K": 176,
-                     "block_nvfp4": 36}
+                     "block_nvfp4": 36, "block_q4_1": 20, "block_q8_1": 36, "block_iq2_xs": 74}
     assert {k: o.RECORD[k][1] for k in o.RECORD} == {
         "q4_0": 18, "mxfp4": 17, "q8_0": 34, "q4_k": 144, "q8_k": 292, "iq2_xxs": 66, "q6_k": 210, "q5_k": 176,
-        "nvfp4": 36}
+        "nvfp4": 36, "q4_1": 20, "q8_1": 36, "iq2_xs": 74}
 
 
 # ------------------------------------------------------------ dequantizers
@@ -138,6 +145,57 @@ def test_dequant_q4_0_brute_force():
     w = np.frombuffer(b"".join(recs), np.uint8).reshape(len(recs), 18)
     got = o.dequantize("q4_0", w, 32)
     assert np.array_equal(got, np.array(want, np.float32))
+
+
+def test_dequant_q4_1_brute_force():
+    # Weft Q4_1: f16 d, f16 m, q: u4[32] like Q4_0; value q * d + m
+    # (examples/kernels/dequantize/q4_1.py, functions/quantization.py:10-11)
+    recs, want = [], []
+    for i, dh in enumerate(D16):
+        mh = D16[(i + 2) % len(D16)]
+        d = float(np.uint16(dh).view(np.float16))
+        m = float(np.uint16(mh).view(np.float16))
+        for pos in range(32):
+            for q in range(16):
+                codes = [(pos * 5 + j * 7 + q) % 16 for j in range(32)]
+                codes[pos] = q
+                b = bytearray(20)
+                b[0:2] = dh.to_bytes(2, "little")
+                b[2:4] = mh.to_bytes(2, "little")
+                for j in range(16):
+                    b[4 + j] = codes[j] | (codes[j + 16] << 4)
+                recs.append(bytes(b))
+                want.append([np.float32(np.float32(c * np.float32(d)) + np.float32(m)) for c in codes])
+    w = np.frombuffer(b"".join(recs), np.uint8).reshape(len(recs), 20)
+    got = o.dequantize("q4_1", w, 32)
+    assert np.array_equal(got, np.array(want, np.float32))
+
+
+def test_dequant_iq2_xs_brute_force():
+    # examples/kernels/dequantize/iq2_xs.py: per 32-group g, scale byte
+    # scales[g] (low nibble: entries 0-1, high: entries 2-3) gives
+    # d * (0.5 + s) * 0.25; entry l's u16 word q[4g + l]: grid row = bits
+    # 0-8, sign row = bits 9-15.
+    grid = np.array([int(x, 16) for x in GOLDEN["iq2xs_grid"]], np.uint64).view(np.uint8).reshape(512, 8)
+    ks = GOLDEN["ksigns_iq2xs"]
+    rng = np.random.default_rng(4)
+    raw = rng.integers(0, 256, (200, 74), dtype=np.uint8)
+    raw[:, 0:2] = np.array([np.uint16(D16[i % 6]) for i in range(200)], np.uint16).view(np.uint8).reshape(200, 2)
+    want = np.zeros((200, 256), np.float32)
+    for r in range(200):
+        d = np.float32(raw[r, 0:2].view(np.float16)[0])
+        q = raw[r, 2:66].view(np.uint16)
+        for gi in range(8):
+            sb = int(raw[r, 66 + gi])
+            scales = [np.float32(np.float32(d * np.float32(0.5 + (sb & 15))) * np.float32(0.25)),
+                      np.float32(np.float32(d * np.float32(0.5 + (sb >> 4))) * np.float32(0.25))]
+            for l in range(4):
+                word = int(q[4 * gi + l])
+                idx, sgn = word & 511, ks[word >> 9]
+                for j in range(8):
+                    s = np.float32(-1.0 if sgn & (1 << j) else 1.0)
+                    want[r, 32 * gi + 8 * l + j] = np.float32(scales[l // 2] * np.float32(grid[idx, j])) * s
+    assert np.array_equal(o.dequantize("iq2_xs", raw, 256).view(np.uint32), want.view(np.uint32))
 
 
 def _pack_q4k_scales(sc, m):
@@ -435,6 +493,40 @@ def test_q8_k_known_answers():
     assert not z[:260].any() and (z[260:] == sentinel).all()
 
 
+def test_q8_1_known_answers():
+    # quantize_row_q8_1_ref (ggml-quants.c:264-295): Q8_0's d and codes, and
+    # s = fp16(sum(q) * d) with the fp32 d
+    x = np.zeros(64, np.float32)
+    x[0] = 127.0
+    x[1:8] = [0.5, 1.5, 2.5, -0.5, -2.5, 3.5, 126.5]
+    x[32:64] = np.linspace(-3.0, 1.0, 32, dtype=np.float32)
+    y = o.quantize("q8_1", x)
+    assert y[0:2].view(np.uint16)[0] == 0x3C00
+    q0 = [127, 1, 2, 3, -1, -3, 4, 127]
+    assert list(y[4:12].view(np.int8)) == q0
+    assert y[2:4].view(np.float16)[0] == np.float16(sum(q0))
+    # the second block's codes are Q8_0's, its sum is rounded once to fp16
+    q80 = o.quantize("q8_0", x[32:])
+    assert np.array_equal(y[40:72], q80[2:34]) and np.array_equal(y[36:38], q80[0:2])
+    d2 = np.float32(3.0) / np.float32(127)
+    tot = int(y[40:72].view(np.int8).astype(int).sum())
+    assert y[38:40].view(np.uint16)[0] == np.float16(np.float32(tot) * d2).view(np.uint16)
+    assert not o.quantize("q8_1", np.zeros(32, np.float32)).any()
+
+
+def test_q4_1_quantizer_known_answer():
+    # quantize_row_q4_1_ref (ggml-quants.c:112-146): a block spanning
+    # [min, min + 15 d] on the code grid comes back code for code
+    d, mn = np.float32(0.25), np.float32(-1.0)
+    codes = np.array([(5 * j + 3) % 16 for j in range(32)])
+    codes[0], codes[1] = 0, 15
+    x = (mn + codes * d).astype(np.float32)
+    y = o.quantize("q4_1", x)
+    assert y[0:2].view(np.float16)[0] == np.float16(d) and y[2:4].view(np.float16)[0] == np.float16(mn)
+    got = np.concatenate([y[4:20] & 0xF, y[4:20] >> 4])
+    assert np.array_equal(got, codes)
+
+
 @pytest.mark.parametrize("act", ["q8_0", "q8_k"])
 def test_q8_invariants(act):
     x = o.seeded_normal(21, (64, 1024))
@@ -465,21 +557,36 @@ def _dequant_act(act, xq, k):
     if act == "q8_0":
         d = recs[:, 0:2].copy().view(np.float16).astype(np.float64)
         q = recs[:, 2:].view(np.int8).astype(np.float64)
+    elif act == "q8_1":
+        d = recs[:, 0:2].copy().view(np.float16).astype(np.float64)
+        q = recs[:, 4:].view(np.int8).astype(np.float64)
     else:
         d = recs[:, 0:4].copy().view(np.float32).astype(np.float64)
         q = recs[:, 4:260].view(np.int8).astype(np.float64)
     return (q * d).reshape(xq.shape[0], k)
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "iq2_xxs", "mxfp4", "q6_k", "q5_k", "nvfp4"])
+@pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "iq2_xxs", "mxfp4", "q6_k", "q5_k", "nvfp4", "q4_1", "iq2_xs"])
 def test_mul_mat_against_independent_float64_path(fmt):
     n, k, m = 48, 2048, 3
-    w = o.quantize(fmt, o.seeded_normal(31, (n, k), 0.02))
+    if fmt == "iq2_xs":
+        w = o.random_records(fmt, n, k, seed=31)
+    else:
+        w = o.quantize(fmt, o.seeded_normal(31, (n, k), 0.02))
     x = o.seeded_normal(32, (m, k))
     xq, y = o.mul_mat(fmt, w, x, n, k, m)
     e, a = o.mul_mat_f64(fmt, w, xq, n, k, m)
     # independent: dequantize both operands (pinned above) and multiply
     ref = _dequant_act(o.ACT_OF[fmt], xq, k) @ o.dequantize(fmt, w, k).astype(np.float64).T
+    if fmt == "q4_1":
+        # Q4_1's min term uses Q8_1's s (fp16 of sum(q) * fp32 d), not the
+        # dequantized activation: replace that part of the reference
+        xr = xq.reshape(m, -1, 36)
+        s = xr[:, :, 2:4].copy().view(np.float16)[..., 0].astype(np.float64)
+        dx = xr[:, :, 0:2].copy().view(np.float16)[..., 0].astype(np.float64)
+        qsum = xr[:, :, 4:].view(np.int8).astype(np.float64).sum(axis=2)
+        wm = w.reshape(n, -1, 20)[:, :, 2:4].copy().view(np.float16)[..., 0].astype(np.float64)
+        ref += s @ wm.T - (dx * qsum) @ wm.T
     assert np.allclose(e, ref, rtol=1e-12, atol=1e-12 * np.abs(ref).max())
     assert o.within_tolerance(y, e, a).all()
     # a wrong sign or a dropped min term would not be near: check the bound bites
