@@ -88,12 +88,19 @@ void row_dequantize_nvfp4(const uint8_t *W, const int8_t *codebook, const float 
                           size_t K);
 /* examples/kernels/dequantize/q5_k.py:9-15; row_dequantize_runtime.cpp:217 */
 void row_dequantize_q5_k(const uint8_t *W, float *Y, size_t K);
+/* examples/kernels/dequantize/q4_1.py:9-13; row_dequantize_runtime.cpp:182 */
+void row_dequantize_q4_1(const uint8_t *W, float *Y, size_t K);
+/* examples/kernels/dequantize/iq2_xs.py:9-75; row_dequantize_runtime.cpp:242 */
+void row_dequantize_iq2_xs(const uint8_t *W, const int8_t *grid, const int8_t *signs, float *Y,
+                           size_t K);
 
 /* ------------------------------------------------ activation quantize */
 /* examples/kernels/quantize/q8_0.py:26-28; repro q8_quantize_runtime.cpp:25 */
 void q8_0_quantize(const float *X, uint8_t *Y, size_t K);
 /* examples/kernels/quantize/q8_k.py:38-40; repro q8_quantize_runtime.cpp:26 */
 void q8_K_quantize(const float *X, uint8_t *Y, size_t K);
+/* examples/kernels/quantize/q8_1.py:28-30; repro q8_quantize_runtime.cpp:18, :43 */
+void q8_1_quantize(const float *X, uint8_t *Y, size_t K);
 
 /* ------------------------------------------------------------ vec_dot */
 /* examples/kernels/vec_dot/q4_0_q8_0.py:8-23; repro vec_dot_runtime.cpp:191 */
@@ -113,6 +120,11 @@ void quantized_vec_dot_nvfp4_q8_0(const uint8_t *W, const uint8_t *X, const int8
                                   const float *scale, float *Y, size_t K);
 /* examples/kernels/vec_dot/q5_k_q8_k.py:8-38; vec_dot_runtime.cpp:255 */
 void quantized_vec_dot_q5_k_q8_k(const uint8_t *W, const uint8_t *X, float *Y, size_t K);
+/* examples/kernels/vec_dot/q4_1_q8_1.py:8-29; vec_dot_runtime.cpp:199 */
+void quantized_vec_dot_q4_1_q8_1(const uint8_t *W, const uint8_t *X, float *Y, size_t K);
+/* examples/kernels/vec_dot/iq2_xs_q8_k.py:9-45; vec_dot_runtime.cpp:295 */
+void quantized_vec_dot_iq2_xs_q8_k(const uint8_t *W, const uint8_t *X, const int8_t *grid,
+                                   const int8_t *signs, float *Y, size_t K);
 
 /* --------------------------------------------------- production mul_mat */
 /* W (N x K) encoded, X (M x K) fp32, Xq (M x K) written with the
@@ -164,6 +176,19 @@ void production_mul_mat_mxfp4(const uint8_t *W, const float *X, uint8_t *Xq, con
 void production_mul_mat_mxfp4_decode(const uint8_t *W, const float *X, uint8_t *Xq,
                                      const int8_t *codebook, const float *scale, float *Y,
                                      size_t N, size_t K, size_t M);
+/* examples/kernels/mul_mat/q4_1.py:9-30; mul_mat_runtime.cpp:235-236 */
+void production_mul_mat_q4_1(const uint8_t *W, const float *X, uint8_t *Xq, float *Y, size_t N,
+                             size_t K, size_t M);
+/* examples/kernels/mul_mat/q4_1_decode.py:10-20; mul_mat_runtime.cpp:232-233 */
+void production_mul_mat_q4_1_decode(const uint8_t *W, const float *X, uint8_t *Xq, float *Y,
+                                    size_t N, size_t K, size_t M);
+/* examples/kernels/mul_mat/iq2_xs.py:26-56; mul_mat_runtime.cpp:446-447 */
+void production_mul_mat_iq2_xs(const uint8_t *W, const float *X, uint8_t *Xq, const int8_t *grid,
+                               const int8_t *signs, float *Y, size_t N, size_t K, size_t M);
+/* examples/kernels/mul_mat/iq2_xs_staged.py:29-75; mul_mat_runtime.cpp:443-444 */
+void production_mul_mat_iq2_xs_staged(const uint8_t *W, const float *X, uint8_t *Xq,
+                                      const int8_t *grid, const int8_t *signs, float *Y, size_t N,
+                                      size_t K, size_t M);
 /* examples/kernels/mul_mat/q6_k.py:9-37; mul_mat_runtime.cpp:386 */
 void production_mul_mat_q6_k(const uint8_t *W, const float *X, uint8_t *Xq, float *Y, size_t N,
                              size_t K, size_t M);
@@ -225,12 +250,15 @@ void q4_k_q8_k_gemv_contract(const uint8_t *W, const uint8_t *X, float *Y, size_
 enum {
   WEFT_GGML_TYPE_F32 = 0,
   WEFT_GGML_TYPE_Q4_0 = 2,
+  WEFT_GGML_TYPE_Q4_1 = 3,
   WEFT_GGML_TYPE_Q8_0 = 8,
+  WEFT_GGML_TYPE_Q8_1 = 9,
   WEFT_GGML_TYPE_Q4_K = 12,
   WEFT_GGML_TYPE_Q5_K = 13,
   WEFT_GGML_TYPE_Q6_K = 14,
   WEFT_GGML_TYPE_Q8_K = 15,
   WEFT_GGML_TYPE_IQ2_XXS = 16,
+  WEFT_GGML_TYPE_IQ2_XS = 17,
   WEFT_GGML_TYPE_MXFP4 = 39,
   WEFT_GGML_TYPE_NVFP4 = 40
 };

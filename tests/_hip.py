@@ -26,6 +26,7 @@ class Harness:
         self._lib = _lib
         _lib.set_stream(torch.cuda.current_stream().cuda_stream)
         self.grid_i8x8 = self.to_dev(o.iq2xxs_grid().view(np.int8))
+        self.grid_xs_i8x8 = self.to_dev(o.iq2xs_grid().view(np.int8))
         self.signs_i8x8 = self.to_dev(o.signs_i8x8())
         self.codebook = self.to_dev(o.kvalues_mxfp4())
         self.scale = self.to_dev(o.e8m0_half_table())

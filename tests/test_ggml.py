@@ -15,7 +15,8 @@ INVALID, NOT_SUPPORTED = 1, 801  # hipErrorInvalidValue, hipErrorNotSupported
 TRAITS = {G.F32: (1, 4, -1), G.Q4_0: (32, 18, G.Q8_0), G.Q8_0: (32, 34, -1),
           G.Q4_K: (256, 144, G.Q8_K), G.Q8_K: (256, 292, -1), G.IQ2_XXS: (256, 66, G.Q8_K),
           G.MXFP4: (32, 17, G.Q8_0), G.Q6_K: (256, 210, G.Q8_K), G.Q5_K: (256, 176, G.Q8_K),
-          G.NVFP4: (64, 36, G.Q8_0)}
+          G.NVFP4: (64, 36, G.Q8_0), G.Q4_1: (32, 20, G.Q8_1), G.Q8_1: (32, 36, -1),
+          G.IQ2_XS: (256, 74, G.Q8_K)}
 
 
 def test_type_traits_follow_ggml():
@@ -23,7 +24,7 @@ def test_type_traits_follow_ggml():
         assert (G.blck_size(t), G.type_size(t), G.vec_dot_type(t)) == (blck, size, vdt)
         assert G.row_size(t, 4096) == size * 4096 // blck
     assert G.row_size(G.Q4_K, 100) == 0  # not whole blocks (ggml_row_size asserts)
-    for other in (1, 3, 11, 41, 99):  # F16, Q4_1, Q3_K, past the enum, unknown
+    for other in (1, 6, 11, 41, 99):  # F16, Q5_0, Q3_K, past the enum, unknown
         assert (G.type_size(other), G.blck_size(other), G.vec_dot_type(other)) == (0, 0, -1)
 
 
@@ -80,7 +81,7 @@ def test_asserts_become_invalid_value():
 
 def test_types_outside_the_path_are_not_supported():
     s0, s1, d = ok_args()
-    assert call(G.tensor(3, (512, 64), data=1 << 20, nb=[20, 320, 0, 0]), s1, d) == NOT_SUPPORTED
+    assert call(G.tensor(6, (512, 64), data=1 << 20, nb=[22, 352, 0, 0]), s1, d) == NOT_SUPPORTED  # Q5_0
     assert call(s0, G.tensor(G.Q8_0, (512, 4), data=2 << 20), d) == NOT_SUPPORTED  # not Q4_K's vec_dot type
     assert call(s0, s1, G.tensor(G.Q8_K, (64, 4), data=3 << 20, nb=[4, 256, 1024, 1024])) == NOT_SUPPORTED
     # a quantized src1 is read in place: its rows must be packed records
@@ -128,5 +129,5 @@ def test_mul_mat_id_asserts_become_invalid_value():
     assert call_id(s0, s1, ids, G.tensor(G.F32, (64, 3, 3), data=3 << 20)) == INVALID  # dst ne1
     assert call_id(G.tensor(G.Q4_K, (512, 64, 8, 2), data=1 << 20), s1, ids, d) == INVALID  # 4-d src0
     assert call_id(s0, s1, ids, d, wsize=G.row_size(G.Q8_K, 512 * 3) - 1) == INVALID
-    assert call_id(G.tensor(3, (512, 64, 8), data=1 << 20, nb=[20, 320, 320 * 64, 0]), s1, ids,
+    assert call_id(G.tensor(6, (512, 64, 8), data=1 << 20, nb=[22, 352, 352 * 64, 0]), s1, ids,
                    d) == NOT_SUPPORTED

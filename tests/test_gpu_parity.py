@@ -38,6 +38,8 @@ def acts(m: int, k: int, seed: int = 2) -> np.ndarray:
 def tables(hip, fmt):
     if fmt == "iq2_xxs":
         return [hip.grid_i8x8, hip.signs_i8x8]
+    if fmt == "iq2_xs":
+        return [hip.grid_xs_i8x8, hip.signs_i8x8]
     if fmt == "mxfp4":
         return [hip.codebook, hip.scale]
     if fmt == "nvfp4":

@@ -325,4 +325,84 @@ __device__ inline void stage_q80_load(const uint8_t* __restrict__ xq, int K, int
   }
 }
 
+// ---------------------------------------------------------------- Q8_1
+// LDS image of one Q8_1 activation row: int8 qs[K] | float d[K/32] |
+// float s[K/32] (the fp16 d and s widened to fp32, as the vec_dot reads them)
+struct Q81View {
+  int8_t* qs;
+  float* d;
+  float* s;
+};
+
+__host__ __device__ inline size_t q81_lds_row_bytes(int K) {
+  return ((size_t)K + 8 * (size_t)(K / 32) + 15) & ~(size_t)15;
+}
+
+__device__ inline Q81View q81_view(char* base, int K, int m) {
+  char* p = base + (size_t)m * q81_lds_row_bytes(K);
+  Q81View v;
+  v.qs = reinterpret_cast<int8_t*>(p);
+  v.d = reinterpret_cast<float*>(p + K);
+  v.s = v.d + K / 32;
+  return v;
+}
+
+// as stage_q80_quantize, plus each block's s (quantize_row_q8_1_ref)
+__device__ inline void stage_q81_quantize(const float* __restrict__ X, size_t ldx,
+                                          uint8_t* __restrict__ xq_out, int K, int m0, int mb,
+                                          char* lds) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int nwaves = blockDim.x / kWave;
+  const int nb = K / 32;
+  const int steps = (nb + 7) / 8;
+  const bool a16 = x_rows_a16(X, ldx);
+  for (int idx = wave; idx < mb * steps; idx += nwaves) {
+    const int m = idx / steps, st = idx - m * steps;
+    const int b = 8 * st + lane / 8;
+    const bool live = b < nb;  // uniform per 8-lane group
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live) x = load_x4(X + (size_t)(m0 + m) * ldx + 32 * b + 4 * (lane & 7), a16);
+    const Q8_0Lane r = q80_quantize_8lanes(x);
+    const uint32_t sh = q81_sum_half(r);
+    if (!live) continue;
+    const Q81View v = q81_view(lds, K, m);
+    const int packed = pack4_i8(r.q);
+    reinterpret_cast<int*>(v.qs + 32 * b)[lane & 7] = packed;
+    if ((lane & 7) == 0) {
+      v.d[b] = fp16_to_fp32(r.dh);
+      v.s[b] = fp16_to_fp32(sh);
+    }
+    if (xq_out != nullptr) {
+      uint8_t* rec = xq_out + ((size_t)(m0 + m) * nb + b) * kQ8_1Bytes;
+      uint16_t* q16 = reinterpret_cast<uint16_t*>(rec + 4 + 4 * (lane & 7));
+      q16[0] = (uint16_t)((uint32_t)packed & 0xffffu);
+      q16[1] = (uint16_t)((uint32_t)packed >> 16);
+      if ((lane & 7) == 0) {
+        reinterpret_cast<uint16_t*>(rec)[0] = (uint16_t)r.dh;
+        reinterpret_cast<uint16_t*>(rec)[1] = (uint16_t)sh;
+      }
+    }
+  }
+}
+
+__device__ inline void stage_q81_load(const uint8_t* __restrict__ xq, int K, int m0, int mb,
+                                      char* lds) {
+  const int nb = K / 32;
+  const int total = mb * nb * 8;  // 8 lanes per block
+  for (int i = threadIdx.x; i < total; i += blockDim.x) {
+    const int m = i / (nb * 8);
+    const int rem = i - m * nb * 8;
+    const int b = rem >> 3, part = rem & 7;
+    const uint8_t* rec = xq + ((size_t)(m0 + m) * nb + b) * kQ8_1Bytes;
+    const Q81View v = q81_view(lds, K, m);
+    const uint16_t* q16 = reinterpret_cast<const uint16_t*>(rec + 4 + 4 * part);
+    reinterpret_cast<int*>(v.qs + 32 * b)[part] = (int)((uint32_t)q16[0] | ((uint32_t)q16[1] << 16));
+    if (part == 0) {
+      v.d[b] = fp16_to_fp32(reinterpret_cast<const uint16_t*>(rec)[0]);
+      v.s[b] = fp16_to_fp32(reinterpret_cast<const uint16_t*>(rec)[1]);
+    }
+  }
+}
+
 }  // namespace weft

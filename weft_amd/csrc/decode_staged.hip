@@ -1,7 +1,8 @@
 // Decode GEMV for the formats whose records are not 16-byte multiples:
 // Q4_0 x Q8_0 (18 B / 32), MXFP4 x Q8_0 (17 B / 32), IQ2_XXS x Q8_K
-// (66 B / 256), Q6_K x Q8_K (210 B / 256), Q5_K x Q8_K (176 B / 256); plus
-// their single-output vec_dots.
+// (66 B / 256), Q6_K x Q8_K (210 B / 256), Q5_K x Q8_K (176 B / 256),
+// NVFP4 x Q8_0 (36 B / 64), Q4_1 x Q8_1 (20 B / 32), IQ2_XS x Q8_K
+// (74 B / 256); plus their single-output vec_dots.
 //
 // Semantics (GGML generic vec_dots, ggml-cpu/quants.c):
 //   Q4_0    :174-208  y = sum_b dw_b * dx_b * sum_32 (q-8) * x
@@ -12,6 +13,9 @@
 //   NVFP4   ggml-cpu/quants.c:279-313  y = sum_B sum_s dx * ue4m3(d_s) * sum_16 kv[q] * x
 //   Q5_K    :720-798  y = sum_B dx * (dw * sum_s sc_s * sum_32 q * x
 //                                    - dmin * sum_s m_s * bsum_s)
+//   Q4_1    :211-245  y = sum_b (dw_b dx_b) sum_32 q x + m_b s_b
+//   IQ2_XS  :897-946  y = 0.125 * sum_B dw * dx * sum_h (2 s_h + 1) *
+//                         sum_16 grid[idx] * sign * x   (h: 16-element halves)
 // and the Weft kernels examples/kernels/mul_mat/{q4_0_decode,mxfp4_decode,
 // iq2_xxs_decode}.py (quantize X into Xq, then one vec_dot per output).
 //
@@ -46,7 +50,7 @@ constexpr int kMaxRowsPerPass = 4;
 // 2.3 KB windows held Q5_K / Q6_K near 2.3-2.7 TB/s.
 constexpr int kWindow = 4608 + 32;
 
-enum class Fmt { Q4_0, MXFP4, IQ2_XXS, Q6_K, Q5_K, NVFP4 };
+enum class Fmt { Q4_0, MXFP4, IQ2_XXS, Q6_K, Q5_K, NVFP4, Q4_1, IQ2_XS };
 
 template <Fmt F>
 struct Traits;
@@ -80,6 +84,29 @@ struct Traits<Fmt::Q5_K> {
   static constexpr int kElems = 256, kBytes = 176, kSegRecords = 16, kItemsPerRecord = 4;
   static constexpr bool kQ8K = true;
 };
+
+template <>
+struct Traits<Fmt::Q4_1> {
+  static constexpr int kElems = 32, kBytes = 20, kSegRecords = 224, kItemsPerRecord = 1;
+  static constexpr bool kQ8K = false;
+};
+template <>
+struct Traits<Fmt::IQ2_XS> {
+  static constexpr int kElems = 256, kBytes = 74, kSegRecords = 56, kItemsPerRecord = 8;
+  static constexpr bool kQ8K = true;
+};
+
+// Q4_1 pairs with the Q8_1 activation (block sums s), every other 32-element
+// format with Q8_0
+template <Fmt F>
+constexpr bool act_q81() {
+  return F == Fmt::Q4_1;
+}
+// LDS for lookup tables: IQ2_XS's 512 x 8 grid and 128 x 8 signs, else 3 KB
+template <Fmt F>
+constexpr int table_bytes() {
+  return F == Fmt::IQ2_XS ? 5120 : 3072;
+}
 
 struct Args {
   const uint8_t* W;
@@ -198,8 +225,8 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
   if (a.pair.ids != nullptr && !resolve_pair(a)) return;
   extern __shared__ __align__(16) char lds[];
   char* windows = lds;                             // kWaves * kWindow
-  char* tables = windows + kWaves * kWindow;       // 3 KB of tables
-  char* act = tables + 3072;                       // activation rows
+  char* tables = windows + kWaves * kWindow;       // lookup tables
+  char* act = tables + table_bytes<F>();           // activation rows
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int nwaves = blockDim.x / kWave;
@@ -211,6 +238,13 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
       reinterpret_cast<uint32_t*>(tables)[i] = reinterpret_cast<const uint32_t*>(a.tab0)[i];
     for (int i = threadIdx.x; i < 256; i += blockDim.x)
       reinterpret_cast<uint32_t*>(tables + 2048)[i] =
+          reinterpret_cast<const uint32_t*>(a.tab1)[i];
+  } else if constexpr (F == Fmt::IQ2_XS) {
+    // grid I8X8[512x8] then signs I8X8[128x8]
+    for (int i = threadIdx.x; i < 1024; i += blockDim.x)
+      reinterpret_cast<uint32_t*>(tables)[i] = reinterpret_cast<const uint32_t*>(a.tab0)[i];
+    for (int i = threadIdx.x; i < 256; i += blockDim.x)
+      reinterpret_cast<uint32_t*>(tables + 4096)[i] =
           reinterpret_cast<const uint32_t*>(a.tab1)[i];
   } else if constexpr (F == Fmt::MXFP4 || F == Fmt::NVFP4) {
     for (int i = threadIdx.x; i < 256; i += blockDim.x)
@@ -248,6 +282,11 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
       stage_q8k_quantize(a.X, a.ldx, blockIdx.x == 0 ? a.xq_out : nullptr, K, a.m0, a.mb, act);
     else
       stage_q8k_load(a.xq_in, K, a.m0, a.mb, act);
+  } else if constexpr (act_q81<F>()) {
+    if (a.X != nullptr)
+      stage_q81_quantize(a.X, a.ldx, blockIdx.x == 0 ? a.xq_out : nullptr, K, a.m0, a.mb, act);
+    else
+      stage_q81_load(a.xq_in, K, a.m0, a.mb, act);
   } else {
     if (a.X != nullptr)
       stage_q80_quantize(a.X, a.ldx, blockIdx.x == 0 ? a.xq_out : nullptr, K, a.m0, a.mb, act);
@@ -329,6 +368,77 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
               acc[m] = ggml_scaled_term(acc[m], v.d[gb], wscale, (float)s);  // GGML's order
             else
               acc[m] += (float)s * wscale * v.d[gb];
+          }
+        } else if constexpr (F == Fmt::Q4_1) {
+          if (!valid) continue;
+          // one 32-element block per lane: unsigned nibbles against Q8_1,
+          // GGML's (dw dx) sumi + m s per block (ggml-cpu/quants.c:211-245)
+          const int gb = r0 + it;
+          const int o = off0 + T::kBytes * it;
+          const uint32_t hd = lds_u32(win, o);
+          const float dw = fp16_to_fp32(hd & 0xffffu), mw = fp16_to_fp32(hd >> 16);
+          uint32_t q[4];
+          lds_run(win, o + 4, q);
+          const int lo0 = (int)(q[0] & 0x0f0f0f0fu), lo1 = (int)(q[1] & 0x0f0f0f0fu);
+          const int lo2 = (int)(q[2] & 0x0f0f0f0fu), lo3 = (int)(q[3] & 0x0f0f0f0fu);
+          const int hi0 = (int)((q[0] >> 4) & 0x0f0f0f0fu), hi1 = (int)((q[1] >> 4) & 0x0f0f0f0fu);
+          const int hi2 = (int)((q[2] >> 4) & 0x0f0f0f0fu), hi3 = (int)((q[3] >> 4) & 0x0f0f0f0fu);
+#pragma unroll
+          for (int m = 0; m < kMaxRowsPerPass; ++m) {
+            if (m >= a.mb) break;
+            const Q81View v = q81_view(act, K, m);
+            const int4 xl = *reinterpret_cast<const int4*>(v.qs + 32 * gb);
+            const int4 xh = *reinterpret_cast<const int4*>(v.qs + 32 * gb + 16);
+            int p = dot4(lo0, xl.x, 0);
+            p = dot4(lo1, xl.y, p);
+            p = dot4(lo2, xl.z, p);
+            p = dot4(lo3, xl.w, p);
+            p = dot4(hi0, xh.x, p);
+            p = dot4(hi1, xh.y, p);
+            p = dot4(hi2, xh.z, p);
+            p = dot4(hi3, xh.w, p);
+            acc[m] += (dw * v.d[gb]) * (float)p + mw * v.s[gb];
+          }
+        } else if constexpr (F == Fmt::IQ2_XS) {
+          // item = (superblock, 32-group g); 8 lanes per superblock.  Entry
+          // l's u16 word: grid row bits 0-8, sign row bits 9-15; entries 0-1
+          // take scale nibble low, 2-3 high (ggml-cpu/quants.c:897-946)
+          const int sb = valid ? it >> 3 : 0, g = it & 7;
+          const int gsb = r0 + sb;
+          const int o = off0 + T::kBytes * sb;
+          const float dw = fp16_to_fp32(lds_u32(win, o) & 0xffffu);
+          uint32_t q[2];
+          lds_run(win, o + 2 + 8 * g, q);
+          const uint32_t sc = lds_u32(win, o + 66 + g) & 0xffu;
+          const uint2* grid = reinterpret_cast<const uint2*>(tables);
+          const uint2* sgn = reinterpret_cast<const uint2*>(tables + 4096);
+          int wv[8];
+#pragma unroll
+          for (int l = 0; l < 4; ++l) {
+            const uint32_t word = (q[l >> 1] >> (16 * (l & 1))) & 0xffffu;
+            const uint2 gv = grid[word & 511u];
+            const uint2 sv = sgn[word >> 9];
+            wv[2 * l] = apply_signs(gv.x, sv.x);
+            wv[2 * l + 1] = apply_signs(gv.y, sv.y);
+          }
+          const int ls1 = 2 * (int)(sc & 15u) + 1, ls2 = 2 * (int)(sc >> 4) + 1;
+#pragma unroll
+          for (int m = 0; m < kMaxRowsPerPass; ++m) {
+            if (m >= a.mb) break;
+            const Q8KView v = q8k_view(act, K, m);
+            const int4 x0 = *reinterpret_cast<const int4*>(v.qs + 256 * gsb + 32 * g);
+            const int4 x1 = *reinterpret_cast<const int4*>(v.qs + 256 * gsb + 32 * g + 16);
+            int s0 = dot4(wv[0], x0.x, 0);
+            s0 = dot4(wv[1], x0.y, s0);
+            s0 = dot4(wv[2], x0.z, s0);
+            s0 = dot4(wv[3], x0.w, s0);
+            int s1 = dot4(wv[4], x1.x, 0);
+            s1 = dot4(wv[5], x1.y, s1);
+            s1 = dot4(wv[6], x1.z, s1);
+            s1 = dot4(wv[7], x1.w, s1);
+            // the superblock's integer sum over its 8 groups, then one fp32 term
+            const int bsum = sum8_of_sum4(sum4(valid ? s0 * ls1 + s1 * ls2 : 0));
+            if (valid && g == 0) acc[m] += (dw * v.d[gsb]) * (float)bsum;
           }
         } else if constexpr (F == Fmt::NVFP4) {
           if (!valid) continue;
@@ -515,7 +625,7 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
       for (int m = 0; m < kMaxRowsPerPass; ++m) {
         if (m >= a.mb) break;
         float tot = wave_sum_f(acc[m]);
-        if constexpr (F == Fmt::IQ2_XXS) tot *= 0.125f;
+        if constexpr (F == Fmt::IQ2_XXS || F == Fmt::IQ2_XS) tot *= 0.125f;
         if (lane == 0) a.Y[(size_t)(a.m0 + m) * a.y_stride + row] = tot;
       }
     }
@@ -531,12 +641,13 @@ void launch(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_
   if (N == 0 || M == 0 || K == 0 || (pr != nullptr && n_pairs <= 0)) return;
   const size_t act_align = T::kQ8K ? 4 : 2;
   const size_t w_align = F == Fmt::MXFP4 || F == Fmt::Q6_K || F == Fmt::NVFP4 ? 1 : 2;
+  constexpr bool kGrid = F == Fmt::IQ2_XXS || F == Fmt::IQ2_XS;
   if (K % T::kElems != 0 || W == nullptr || Y == nullptr || (X == nullptr && xq_in == nullptr) ||
       N > (size_t)INT32_MAX || K > (size_t)INT32_MAX || M > (size_t)INT32_MAX ||
       !aligned(W, w_align) || !aligned(Y, 4) || (X && !aligned(X, 4)) ||
       (xq_in && !aligned(xq_in, act_align)) || (xq_out && !aligned(xq_out, act_align)) ||
-      ((F == Fmt::MXFP4 || F == Fmt::NVFP4 || F == Fmt::IQ2_XXS) && (tab0 == nullptr || tab1 == nullptr)) ||
-      (F == Fmt::IQ2_XXS && (!aligned(tab0, 4) || !aligned(tab1, 4))) ||
+      ((F == Fmt::MXFP4 || F == Fmt::NVFP4 || kGrid) && (tab0 == nullptr || tab1 == nullptr)) ||
+      (kGrid && (!aligned(tab0, 4) || !aligned(tab1, 4))) ||
       ((F == Fmt::MXFP4 || F == Fmt::NVFP4) && !aligned(tab1, 4)) ||
       !strides_ok(st, K / T::kElems * T::kBytes, w_align, K, N, N, M) ||
       (pr != nullptr && pr->w_es % (long long)w_align != 0)) {
@@ -549,8 +660,10 @@ void launch(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_
         decode_rec_m1(F == Fmt::MXFP4 ? 1 : 0, W, X, xq_out, tab0, static_cast<const float*>(tab1), Y, N, K, st))
       return;
   }
-  const size_t row_lds = T::kQ8K ? q8k_lds_row_bytes((int)K) : q80_lds_row_bytes((int)K);
-  const size_t fixed = (size_t)kWaves * kWindow + 3072;
+  const size_t row_lds = T::kQ8K ? q8k_lds_row_bytes((int)K)
+                         : act_q81<F>() ? q81_lds_row_bytes((int)K)
+                                        : q80_lds_row_bytes((int)K);
+  const size_t fixed = (size_t)kWaves * kWindow + table_bytes<F>();
   const size_t cap = max_lds_per_block();
   if (fixed + row_lds > cap) {
     set_error(hipErrorInvalidValue);
@@ -619,8 +732,20 @@ void decode_pairs(int fmt, const uint8_t* W, const float* X, const uint8_t* xq_i
     case 3: return launch<Fmt::Q6_K>(W, X, xq_in, xq_out, nullptr, nullptr, Y, N, K, 1, st, &pr, n_pairs);
     case 4: return launch<Fmt::Q5_K>(W, X, xq_in, xq_out, nullptr, nullptr, Y, N, K, 1, st, &pr, n_pairs);
     case 5: return launch<Fmt::NVFP4>(W, X, xq_in, xq_out, tab0, tab1, Y, N, K, 1, st, &pr, n_pairs);
+    case 6: return launch<Fmt::Q4_1>(W, X, xq_in, xq_out, nullptr, nullptr, Y, N, K, 1, st, &pr, n_pairs);
+    case 7: return launch<Fmt::IQ2_XS>(W, X, xq_in, xq_out, tab0, tab1, Y, N, K, 1, st, &pr, n_pairs);
     default: return launch<Fmt::IQ2_XXS>(W, X, xq_in, xq_out, tab0, tab1, Y, N, K, 1, st, &pr, n_pairs);
   }
+}
+
+void decode_q4_1(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
+                 size_t M, const RowStrides& st) {
+  launch<Fmt::Q4_1>(W, X, nullptr, Xq, nullptr, nullptr, Y, N, K, M, st);
+}
+
+void decode_iq2_xs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,
+                   const int8_t* signs, float* Y, size_t N, size_t K, size_t M, const RowStrides& st) {
+  launch<Fmt::IQ2_XS>(W, X, nullptr, Xq, grid, signs, Y, N, K, M, st);
 }
 
 void decode_q6_k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
@@ -647,6 +772,8 @@ void decode_quantized(int fmt, const uint8_t* W, const uint8_t* Xq, const int8_t
     case 3: return launch<Fmt::Q6_K>(W, nullptr, Xq, nullptr, nullptr, nullptr, Y, N, K, M, st);
     case 4: return launch<Fmt::Q5_K>(W, nullptr, Xq, nullptr, nullptr, nullptr, Y, N, K, M, st);
     case 5: return launch<Fmt::NVFP4>(W, nullptr, Xq, nullptr, tab0, tab1, Y, N, K, M, st);
+    case 6: return launch<Fmt::Q4_1>(W, nullptr, Xq, nullptr, nullptr, nullptr, Y, N, K, M, st);
+    case 7: return launch<Fmt::IQ2_XS>(W, nullptr, Xq, nullptr, tab0, tab1, Y, N, K, M, st);
     default: return launch<Fmt::IQ2_XXS>(W, nullptr, Xq, nullptr, tab0, tab1, Y, N, K, M, st);
   }
 }
@@ -744,6 +871,23 @@ void quantized_vec_dot_q5_k_q8_k(const uint8_t* W, const uint8_t* X, float* Y, s
 void quantized_vec_dot_q6_k_q8_k(const uint8_t* W, const uint8_t* X, float* Y, size_t K) {
   if (X == nullptr) return weft::set_error(hipErrorInvalidValue);
   weft::launch<weft::Fmt::Q6_K>(W, nullptr, X, nullptr, nullptr, nullptr, Y, 1, K, 1, weft::packed(0, K, 1));
+}
+
+void production_mul_mat_q4_1_decode(const uint8_t* W, const float* X, uint8_t* Xq, float* Y,
+                                    size_t N, size_t K, size_t M) {
+  if (X == nullptr || Xq == nullptr) return weft::set_error(hipErrorInvalidValue);
+  weft::decode_q4_1(W, X, Xq, Y, N, K, M, weft::packed(K / 32 * weft::kQ4_1Bytes, K, N));
+}
+
+void quantized_vec_dot_q4_1_q8_1(const uint8_t* W, const uint8_t* X, float* Y, size_t K) {
+  if (X == nullptr) return weft::set_error(hipErrorInvalidValue);
+  weft::launch<weft::Fmt::Q4_1>(W, nullptr, X, nullptr, nullptr, nullptr, Y, 1, K, 1, weft::packed(0, K, 1));
+}
+
+void quantized_vec_dot_iq2_xs_q8_k(const uint8_t* W, const uint8_t* X, const int8_t* grid,
+                                   const int8_t* signs, float* Y, size_t K) {
+  if (X == nullptr) return weft::set_error(hipErrorInvalidValue);
+  weft::launch<weft::Fmt::IQ2_XS>(W, nullptr, X, nullptr, grid, signs, Y, 1, K, 1, weft::packed(0, K, 1));
 }
 
 void quantized_vec_dot_iq2_xxs_q8_k(const uint8_t* W, const uint8_t* X, const int8_t* grid,

@@ -1,4 +1,4 @@
-// Row dequantize: row_dequantize_{q4_0,q4_k,iq2_xxs,mxfp4,q6_k,q5_k,nvfp4}
+// Row dequantize: row_dequantize_{q4_0,q4_k,iq2_xxs,mxfp4,q6_k,q5_k,nvfp4,q4_1,iq2_xs}
 // (examples/kernels/dequantize/*.py; GGML dequantize_row_* in
 // ggml-quants.c:401-419, :511-529, :1471-1493, :2416-2440, :1881-1910,
 // :1673-1697, :531-552).
@@ -257,6 +257,62 @@ __global__ void __launch_bounds__(kThreads) dq_iq2xxs_kernel(const uint8_t* __re
   }
 }
 
+// Q4_1 (dequantize_row_q4_1, ggml-quants.c:421-439): 8 lanes per 32-block;
+// q * d rounded, then + m rounded, as the C expression states
+template <bool Y16>
+__global__ void __launch_bounds__(kThreads) dq_q41_kernel(const uint8_t* __restrict__ W,
+                                                          float* __restrict__ Y, long long nb) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & (kWave - 1);
+  const long long wave = ((long long)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const long long nwaves = (long long)gridDim.x * blockDim.x / kWave;
+  const int p = lane & 7;
+  const int shift = p >= 4 ? 4 : 0;
+  const long long steps = (nb + 7) / 8;
+  for (long long st = wave; st < steps; st += nwaves) {
+    const long long b = 8 * st + lane / 8;
+    if (b >= nb) continue;
+    const uint8_t* rec = W + b * kQ4_1Bytes;
+    const float d = fp16_to_fp32(ld_u16(rec)), m = fp16_to_fp32(ld_u16(rec + 2));
+    const uint32_t qs = ld_u32_a2(rec + 4 + 4 * (p & 3));
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = (float)((qs >> (8 * i + shift)) & 0xf) * d + m;
+    store4<Y16>(Y + b * 32 + 4 * p, v[0], v[1], v[2], v[3]);
+  }
+}
+
+// IQ2_XS (dequantize_row_iq2_xs, ggml-quants.c:2444-2467): one wave per
+// superblock, lane l -> elements 4l..4l+3 of 8-element entry c = l / 2:
+// grid row = bits 0-8 of u16 word c, sign row = bits 9-15, scale nibble
+// c % 4 < 2 ? low : high of scales[c / 4], db = (d (0.5 + s)) 0.25
+template <bool Y16>
+__global__ void __launch_bounds__(kThreads) dq_iq2xs_kernel(const uint8_t* __restrict__ W,
+                                                            const int8_t* __restrict__ grid,
+                                                            const int8_t* __restrict__ signs,
+                                                            float* __restrict__ Y, long long nsb) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const long long wave = ((long long)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const long long nwaves = (long long)gridDim.x * blockDim.x / kWave;
+  const int c = lane >> 1, h = lane & 1;
+  for (long long s = wave; s < nsb; s += nwaves) {
+    const uint8_t* rec = W + s * kIq2xsBytes;
+    const float d = fp16_to_fp32(ld_u16(rec));
+    const uint32_t word = ld_u16(rec + 2 + 2 * c);
+    const uint32_t sb = rec[66 + (c >> 2)];
+    const uint32_t sc = (c & 3) < 2 ? sb & 0xfu : sb >> 4;
+    const float db = d * (0.5f + (float)sc) * 0.25f;
+    const int gi = (int)(word & 511u), si = (int)(word >> 9);
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = 4 * h + i;
+      v[i] = (float)((int)grid[8 * gi + j] * (int)signs[8 * si + j]) * db;
+    }
+    store4<Y16>(Y + s * 256 + 4 * lane, v[0], v[1], v[2], v[3]);
+  }
+}
+
 int grid_for(long long waves_needed) {
   const long long per_block = kThreads / kWave;
   const long long cap = (long long)cu_count() * 16;
@@ -372,6 +428,33 @@ void row_dequantize_iq2_xxs(const uint8_t* W, const int8_t* grid, const int8_t* 
   else
     dq_iq2xxs_kernel<false><<<grid_for(nsb), kThreads, 0, current_stream()>>>(W, grid, signs, Y, nsb);
   check_launch("dq_iq2xxs_kernel");
+}
+
+void row_dequantize_q4_1(const uint8_t* W, float* Y, size_t K) {
+  using namespace weft;
+  if (K == 0) return;
+  if (K % 32 || bad(W, 2, Y)) return set_error(hipErrorInvalidValue);
+  const long long nb = (long long)(K / 32);
+  const int g = grid_for((nb + 7) / 8);
+  if (aligned(Y, 16))
+    dq_q41_kernel<true><<<g, kThreads, 0, current_stream()>>>(W, Y, nb);
+  else
+    dq_q41_kernel<false><<<g, kThreads, 0, current_stream()>>>(W, Y, nb);
+  check_launch("dq_q41_kernel");
+}
+
+void row_dequantize_iq2_xs(const uint8_t* W, const int8_t* grid, const int8_t* signs, float* Y,
+                           size_t K) {
+  using namespace weft;
+  if (K == 0) return;
+  if (K % 256 || bad(W, 2, Y) || grid == nullptr || signs == nullptr)
+    return set_error(hipErrorInvalidValue);
+  const long long nsb = (long long)(K / 256);
+  if (aligned(Y, 16))
+    dq_iq2xs_kernel<true><<<grid_for(nsb), kThreads, 0, current_stream()>>>(W, grid, signs, Y, nsb);
+  else
+    dq_iq2xs_kernel<false><<<grid_for(nsb), kThreads, 0, current_stream()>>>(W, grid, signs, Y, nsb);
+  check_launch("dq_iq2xs_kernel");
 }
 
 }  // extern "C"

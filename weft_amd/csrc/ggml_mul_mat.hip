@@ -55,6 +55,9 @@ constexpr TypeInfo kTypes[] = {
     {WEFT_GGML_TYPE_IQ2_XXS, 256, kIq2xxsBytes, WEFT_GGML_TYPE_Q8_K},
     {WEFT_GGML_TYPE_MXFP4, 32, kMxfp4Bytes, WEFT_GGML_TYPE_Q8_0},
     {WEFT_GGML_TYPE_NVFP4, 64, kNvfp4Bytes, WEFT_GGML_TYPE_Q8_0},
+    {WEFT_GGML_TYPE_Q4_1, 32, kQ4_1Bytes, WEFT_GGML_TYPE_Q8_1},
+    {WEFT_GGML_TYPE_Q8_1, 32, kQ8_1Bytes, -1},
+    {WEFT_GGML_TYPE_IQ2_XS, 256, kIq2xsBytes, WEFT_GGML_TYPE_Q8_K},
 };
 
 constexpr int32_t kGgmlTypeI32 = 26;  // GGML_TYPE_I32
@@ -74,6 +77,7 @@ struct GgmlTables {
   int8_t codebook[16];
   float scale[256];  // E8M0 (MXFP4), ggml_e8m0_to_fp32_half
   float ue4m3[256];  // UE4M3 (NVFP4), ggml_ue4m3_to_fp32 (ggml-impl.h:502-515)
+  int8_t grid_xs[512 * 8];  // iq2xs_grid (ggml-common.h:617-746)
 };
 
 constexpr uint16_t kGridCodes[256] = {
@@ -95,11 +99,49 @@ constexpr uint16_t kGridCodes[256] = {
     37248, 37445, 37888, 37922, 37956, 38225, 39041, 39200, 40962, 41040, 41093, 41225, 41472, 42008, 43088, 43268,
 };
 
+// iq2xs_grid as two bits per lane (0x08, 0x19, 0x2b -> 0, 1, 2), lane 0 lowest
+constexpr uint16_t kGridXsCodes[512] = {
+        0,     2,     5,     8,    10,    17,    20,    22,    25,    32,    34,    37,    40,    65,    68,    70,
+       73,    80,    82,    85,    88,    97,   100,   128,   130,   133,   136,   145,   148,   153,   160,   257,
+      260,   262,   265,   272,   274,   277,   280,   282,   289,   292,   320,   322,   325,   328,   337,   340,
+      352,   360,   385,   388,   400,   512,   514,   517,   520,   529,   532,   544,   577,   580,   592,   597,
+      640,   650,  1025,  1028,  1030,  1033,  1040,  1042,  1045,  1048,  1057,  1060,  1088,  1090,  1093,  1096,
+     1105,  1108,  1110,  1120,  1153,  1156,  1168,  1280,  1282,  1285,  1288,  1297,  1300,  1312,  1345,  1348,
+     1360,  1377,  1408,  1537,  1540,  1552,  1574,  1600,  1602,  1668,  2048,  2050,  2053,  2056,  2058,  2065,
+     2068,  2080,  2085,  2113,  2116,  2128,  2136,  2176,  2208,  2218,  2305,  2308,  2320,  2368,  2433,  2441,
+     2560,  2592,  2600,  2710,  2720,  4097,  4100,  4102,  4105,  4112,  4114,  4117,  4120,  4129,  4132,  4160,
+     4162,  4165,  4168,  4177,  4180,  4192,  4202,  4225,  4228,  4240,  4352,  4354,  4357,  4360,  4369,  4372,
+     4384,  4417,  4420,  4432,  4480,  4500,  4502,  4609,  4612,  4614,  4624,  4672,  4704,  5120,  5122,  5125,
+     5128,  5137,  5140,  5152,  5185,  5188,  5193,  5200,  5220,  5248,  5377,  5380,  5392,  5440,  5632,  5652,
+     5705,  6145,  6148,  6160,  6162,  6208,  6228,  6278,  6400,  6405,  6502,  6737,  6825,  8192,  8194,  8197,
+     8200,  8202,  8209,  8212,  8224,  8257,  8260,  8272,  8320,  8352,  8449,  8452,  8464,  8512,  8520,  8549,
+     8704,  8738,  8832,  8872,  9217,  9220,  9232,  9257,  9280,  9472,  9537,  9554,  9625,  9729,  9754,  9894,
+    10240, 10248, 10250, 10272, 10325, 10376, 10402, 10600, 10640, 10760, 10784, 10882, 10888, 10890, 16385, 16388,
+    16390, 16393, 16400, 16402, 16405, 16408, 16417, 16420, 16448, 16450, 16453, 16456, 16458, 16465, 16468, 16480,
+    16485, 16513, 16516, 16528, 16640, 16642, 16645, 16648, 16657, 16660, 16672, 16705, 16708, 16720, 16768, 16773,
+    16802, 16897, 16900, 16912, 16914, 16937, 16960, 17408, 17410, 17413, 17416, 17425, 17428, 17433, 17440, 17473,
+    17476, 17488, 17536, 17556, 17665, 17668, 17680, 17700, 17728, 17818, 17920, 17930, 17988, 18000, 18433, 18436,
+    18448, 18496, 18501, 18516, 18530, 18688, 18705, 18756, 18768, 18793, 18948, 20480, 20482, 20485, 20488, 20497,
+    20500, 20512, 20520, 20545, 20548, 20560, 20608, 20737, 20740, 20752, 20757, 20800, 20802, 20992, 21060, 21162,
+    21505, 21508, 21520, 21537, 21568, 21600, 21633, 21665, 21760, 21768, 21888, 21896, 22049, 22120, 22177, 22528,
+    22548, 22593, 22608, 22681, 22810, 22848, 22850, 23173, 24577, 24580, 24592, 24640, 24660, 24674, 24710, 24745,
+    24832, 25124, 25162, 25234, 25600, 25622, 25872, 25920, 25925, 26020, 26625, 26730, 26917, 27142, 27220, 27234,
+    32768, 32770, 32773, 32776, 32785, 32788, 32800, 32810, 32833, 32836, 32848, 32896, 32898, 32936, 32938, 33025,
+    33028, 33030, 33040, 33088, 33105, 33113, 33280, 33312, 33408, 33410, 33440, 33448, 33793, 33796, 33808, 33810,
+    33813, 33856, 33888, 33929, 34048, 34116, 34213, 34328, 34410, 34816, 34824, 34853, 34906, 34944, 34946, 34984,
+    35078, 35362, 35456, 35464, 35478, 35496, 36865, 36868, 36880, 36928, 36950, 36996, 37120, 37154, 37220, 37462,
+    37513, 37888, 37893, 37956, 37968, 37976, 38185, 38288, 38290, 38465, 38993, 39078, 39241, 39445, 39520, 40960,
+    40962, 40968, 40970, 40992, 41002, 41120, 41297, 41305, 41382, 41472, 41474, 41480, 41514, 41600, 41632, 42048,
+    42133, 42597, 42648, 43018, 43040, 43042, 43048, 43168, 43176, 43268, 43396, 43398, 43560, 43562, 43665, 43690,
+};
+
 constexpr GgmlTables make_tables() {
   GgmlTables t{};
   constexpr int8_t lane_value[4] = {0x08, 0x19, 0x2b, 0x00};
   for (int i = 0; i < 256; ++i)
     for (int j = 0; j < 8; ++j) t.grid[8 * i + j] = lane_value[(kGridCodes[i] >> (2 * j)) & 3];
+  for (int i = 0; i < 512; ++i)
+    for (int j = 0; j < 8; ++j) t.grid_xs[8 * i + j] = lane_value[(kGridXsCodes[i] >> (2 * j)) & 3];
   for (int i = 0; i < 128; ++i) {
     int parity = 0;
     for (int b = 0; b < 7; ++b) parity ^= (i >> b) & 1;
@@ -226,7 +268,7 @@ hipError_t mul_mat(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1, const
   }
   const GgmlTables* tab = nullptr;
   if (s0->type == WEFT_GGML_TYPE_IQ2_XXS || s0->type == WEFT_GGML_TYPE_MXFP4 ||
-      s0->type == WEFT_GGML_TYPE_NVFP4) {
+      s0->type == WEFT_GGML_TYPE_NVFP4 || s0->type == WEFT_GGML_TYPE_IQ2_XS) {
     tab = device_tables();
     if (tab == nullptr) return fail(hipErrorInvalidDevice);
   }
@@ -267,6 +309,10 @@ hipError_t mul_mat(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1, const
           case WEFT_GGML_TYPE_IQ2_XXS:
             mul_mat_iq2_xxs(W, X, Xq, tab->grid, tab->signs, Y, n, k, m, st);
             break;
+          case WEFT_GGML_TYPE_Q4_1: mul_mat_q4_1(W, X, Xq, Y, n, k, m, st); break;
+          case WEFT_GGML_TYPE_IQ2_XS:
+            decode_iq2_xs(W, X, Xq, tab->grid_xs, tab->signs, Y, n, k, m, st);
+            break;
           default: mul_mat_mxfp4(W, X, Xq, tab->codebook, tab->scale, Y, n, k, m, st); break;
         }
       } else {
@@ -280,6 +326,10 @@ hipError_t mul_mat(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1, const
             break;
           case WEFT_GGML_TYPE_IQ2_XXS:
             mul_mat_iq2_xxs_quantized(W, src1, tab->grid, tab->signs, Y, n, k, m, st);
+            break;
+          case WEFT_GGML_TYPE_Q4_1: decode_quantized(6, W, src1, nullptr, nullptr, Y, n, k, m, st); break;
+          case WEFT_GGML_TYPE_IQ2_XS:
+            decode_quantized(7, W, src1, tab->grid_xs, tab->signs, Y, n, k, m, st);
             break;
           default: decode_quantized(1, W, src1, tab->codebook, tab->scale, Y, n, k, m, st); break;
         }
@@ -329,7 +379,7 @@ hipError_t mul_mat_id(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1,
   }
   const GgmlTables* tab = nullptr;
   if (s0->type == WEFT_GGML_TYPE_IQ2_XXS || s0->type == WEFT_GGML_TYPE_MXFP4 ||
-      s0->type == WEFT_GGML_TYPE_NVFP4) {
+      s0->type == WEFT_GGML_TYPE_NVFP4 || s0->type == WEFT_GGML_TYPE_IQ2_XS) {
     tab = device_tables();
     if (tab == nullptr) return fail(hipErrorInvalidDevice);
   }
@@ -396,6 +446,8 @@ hipError_t mul_mat_id(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1,
       case WEFT_GGML_TYPE_Q6_K:
       case WEFT_GGML_TYPE_Q5_K:
       case WEFT_GGML_TYPE_NVFP4:
+      case WEFT_GGML_TYPE_Q4_1:
+      case WEFT_GGML_TYPE_IQ2_XS:
         break;  // no grouped GEMM: the pair GEMV below
       default: {  // Q4_0 / MXFP4: the GEMMs read a planar activation quantized from X
         const int fmt = s0->type == WEFT_GGML_TYPE_Q4_0 ? 0 : 1;
@@ -429,6 +481,13 @@ hipError_t mul_mat_id(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1,
       break;
     case WEFT_GGML_TYPE_MXFP4:
       decode_pairs(1, W, X, xq_in, xq_out, tab->codebook, tab->scale, Y, (size_t)N, (size_t)K, st, pr,
+                   n_pairs);
+      break;
+    case WEFT_GGML_TYPE_Q4_1:
+      decode_pairs(6, W, X, xq_in, xq_out, nullptr, nullptr, Y, (size_t)N, (size_t)K, st, pr, n_pairs);
+      break;
+    case WEFT_GGML_TYPE_IQ2_XS:
+      decode_pairs(7, W, X, xq_in, xq_out, tab->grid_xs, tab->signs, Y, (size_t)N, (size_t)K, st, pr,
                    n_pairs);
       break;
     default:

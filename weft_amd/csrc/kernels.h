@@ -57,7 +57,7 @@ bool decode_rec_m1(int fmt, const uint8_t* W, const float* X, uint8_t* Xq, const
 // MUL_MAT_ID: the GEMV over every (token, slot) pair of pr, each with the
 // expert ids[t, s] selects (one activation row per pair; X quantized into
 // xq_out, or the quantized xq_in read).  Q4_K, and Q4_0 (fmt 0), MXFP4 (1),
-// IQ2_XXS (2), Q6_K (3), Q5_K (4), NVFP4 (5).
+// IQ2_XXS (2), Q6_K (3), Q5_K (4), NVFP4 (5), Q4_1 (6), IQ2_XS (7).
 void decode_q4k_pairs(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_out,
                       float* Y, size_t N, size_t K, const RowStrides& st, const PairArgs& pr,
                       int n_pairs);
@@ -107,11 +107,18 @@ bool mul_mat_id_iq2_grouped_ok(const uint8_t* W, size_t xq_bytes, const float* Y
 void mul_mat_id_iq2_grouped(const uint8_t* W, const uint8_t* Xq, const int8_t* grid, const int8_t* signs,
                             float* Y, size_t N, size_t K, const RowStrides& st, const PairArgs& pr,
                             int n_pairs, void* ws);
-// Q4_0 (fmt 0), MXFP4 (1), IQ2_XXS (2), Q6_K (3), Q5_K (4) or NVFP4 (5) GEMV over an already quantized
-// activation (Q8_0 / Q8_0 / Q8_K records, read only)
+// Q4_0 (fmt 0), MXFP4 (1), IQ2_XXS (2), Q6_K (3), Q5_K (4), NVFP4 (5), Q4_1 (6) or
+// IQ2_XS (7) GEMV over an already quantized activation (Q8_0, Q8_1 or Q8_K
+// records, read only)
 void decode_quantized(int fmt, const uint8_t* W, const uint8_t* Xq, const int8_t* tab0,
                       const void* tab1, float* Y, size_t N, size_t K, size_t M,
                       const RowStrides& st);
+
+// Q4_1 x Q8_1 and IQ2_XS x Q8_K decode GEMVs (quantize X in-kernel, write Xq, any M)
+void decode_q4_1(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
+                 size_t M, const RowStrides& st);
+void decode_iq2_xs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,
+                   const int8_t* signs, float* Y, size_t N, size_t K, size_t M, const RowStrides& st);
 
 // Q4_K mul_mat for any M: int8-MFMA GEMM for prefill shapes, GEMV otherwise.
 void mul_mat_q4k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
@@ -136,6 +143,9 @@ void mul_mat_q4_0(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_
                   size_t M, const RowStrides& st);
 void mul_mat_mxfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
                    const float* scale, float* Y, size_t N, size_t K, size_t M, const RowStrides& st);
+// Q4_1 x Q8_1: the Q4_0 GEMM body with each block's m * s term, GEMV otherwise
+void mul_mat_q4_1(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
+                  size_t M, const RowStrides& st);
 
 // IQ2_XXS mul_mat for any M: int8-MFMA GEMM for prefill shapes, GEMV otherwise.
 void mul_mat_iq2_xxs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,
@@ -151,5 +161,6 @@ void quantize_q8_k(const float* X, uint8_t* Y, size_t K);
 void quantize_q8_0(const float* X, uint8_t* Y, size_t K);
 void quantize_q8_k_rows(const float* X, size_t ldx, uint8_t* Y, size_t M, size_t K);
 void quantize_q8_0_rows(const float* X, size_t ldx, uint8_t* Y, size_t M, size_t K);
+void quantize_q8_1_rows(const float* X, size_t ldx, uint8_t* Y, size_t M, size_t K);
 
 }  // namespace weft

@@ -41,7 +41,7 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
-enum class WFmt { Q4_0, MXFP4 };
+enum class WFmt { Q4_0, MXFP4, Q4_1 };
 
 template <WFmt F>
 struct WTraits;
@@ -55,6 +55,18 @@ struct WTraits<WFmt::MXFP4> {
   static constexpr int kRec = kMxfp4Bytes;  // 17
   static constexpr int kHdr = 1;            // e8m0 e, then 16 nibble bytes
 };
+template <>
+struct WTraits<WFmt::Q4_1> {
+  static constexpr int kRec = kQ4_1Bytes;  // 20
+  static constexpr int kHdr = 4;           // fp16 d, fp16 m, then 16 nibble bytes
+};
+
+// Planar activation row bytes: K int8, K/32 fp16 scales d, and for Q4_1's
+// Q8_1 activation K/32 fp16 block sums s (the size of the caller's Xq row)
+template <WFmt F>
+constexpr size_t planar_row_bytes(size_t K) {
+  return K + K / 16 + (F == WFmt::Q4_1 ? K / 16 : 0);
+}
 
 constexpr int kMT = 64;        // tokens per workgroup tile
 constexpr int kNT = 128;       // weight rows per workgroup tile
@@ -115,10 +127,11 @@ __device__ __forceinline__ uint32_t lookup16(uint32_t n, uint32_t c0, uint32_t c
 }
 
 // LDS bytes of the int8 GEMM body: two ring slots of two stages, the token
-// scales, the MXFP4 scale table
+// scales (fp32), Q4_1's token block sums (fp16), the MXFP4 scale table
 template <WFmt F>
 constexpr int q80_lds_bytes() {
-  return 4 * (kAQ + kNT * 8 * WTraits<F>::kRec) + 2 * 2 * 8 * kMT * 4 + 256 * 4;
+  return 4 * (kAQ + kNT * 8 * WTraits<F>::kRec) + 2 * 2 * 8 * kMT * 4 +
+         (F == WFmt::Q4_1 ? 2 * 2 * 8 * kMT * 2 : 0) + (F == WFmt::MXFP4 ? 256 * 4 : 0);
 }
 
 template <WFmt F, bool kGroup>
@@ -138,8 +151,13 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
   uint8_t* ring0 = lds;
   uint8_t* ring1 = lds + 2 * kStage;
   float(*adt)[2][8 * kMT] = reinterpret_cast<float(*)[2][8 * kMT]>(lds + 4 * kStage);  // [slot][parity][block][token]
+  // Q4_1: the tokens' fp16 block sums [slot][parity][block][token]; MXFP4: scale table
+  uint16_t(*ast)[2][8 * kMT] = reinterpret_cast<uint16_t(*)[2][8 * kMT]>(lds + 4 * kStage + 2 * 2 * 8 * kMT * 4);
   float* scl = reinterpret_cast<float*>(lds + 4 * kStage) + 2 * 2 * 8 * kMT;
-  static_assert(q80_lds_bytes<F>() == 4 * kStage + 2 * 2 * 8 * kMT * 4 + 256 * 4, "LDS carve");
+  static_assert(q80_lds_bytes<F>() == 4 * kStage + 2 * 2 * 8 * kMT * 4 +
+                                          (F == WFmt::Q4_1 ? 2 * 2 * 8 * kMT * 2 : 0) +
+                                          (F == WFmt::MXFP4 ? 256 * 4 : 0),
+                "LDS carve");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -147,7 +165,7 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
   const int par = wave >> 2, wcol = wave & 3;
   const int col = lane & 31, kg = lane >> 5;
   const int nst = a.K >> 8;                         // stages (8 blocks each)
-  const size_t xs = (size_t)a.K + (size_t)a.K / 16;  // planar activation row stride
+  const size_t xs = planar_row_bytes<F>((size_t)a.K);  // planar activation row stride
   const size_t ws_row = a.ldw;
 
   // XCD-aware tile order (workgroups are dealt round-robin to 8 XCDs);
@@ -217,16 +235,23 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
       lds_dma4(g, stage + kAQ + 256 * k);
     }
   };
-  uint4 dxraw = make_uint4(0, 0, 0, 0);
+  uint4 dxraw = make_uint4(0, 0, 0, 0), sraw = make_uint4(0, 0, 0, 0);
   auto load_dx = [&](int pair) {
     const int st = min(2 * pair + par, nst - 1);
     dxraw = *reinterpret_cast<const uint4*>(dsrc + 16 * (size_t)st);
+    if constexpr (F == WFmt::Q4_1) sraw = *reinterpret_cast<const uint4*>(dsrc + a.K / 16 + 16 * (size_t)st);
   };
   auto store_dx = [&](int slot) {
     float* d = &adt[slot][par][0];
     const uint32_t w[4] = {dxraw.x, dxraw.y, dxraw.z, dxraw.w};
 #pragma unroll
     for (int j = 0; j < 8; ++j) d[j * kMT + lane] = fp16_to_fp32((w[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+    if constexpr (F == WFmt::Q4_1) {
+      uint16_t* sv = &ast[slot][par][0];
+      const uint32_t u[4] = {sraw.x, sraw.y, sraw.z, sraw.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sv[j * kMT + lane] = (uint16_t)(u[j >> 1] >> (16 * (j & 1)));
+    }
   };
 
   v16i I[2];
@@ -252,6 +277,7 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
       const uint8_t* AQ = stage;
       const uint8_t* wrow = stage + kAQ + (32 * wcol + col) * kRB;
       const float* dxs = &adt[pair & 1][par][0];
+      const uint16_t* sxs = &ast[pair & 1][par][0];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         // raw record j of this lane's weight row: header, then 16 nibble bytes
@@ -268,8 +294,12 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
           q3 = __builtin_amdgcn_alignbyte(w4, w3, sh);
         }
         // header byte(s) just before the nibbles
-        float wsc;
-        if constexpr (F == WFmt::Q4_0) {
+        float wsc, wmin = 0.f;
+        if constexpr (F == WFmt::Q4_1) {
+          const uint32_t hd = ld32(wrow + T::kRec * j);  // records are 4-byte aligned here
+          wsc = fp16_to_fp32(hd & 0xffffu);
+          wmin = fp16_to_fp32(hd >> 16);
+        } else if constexpr (F == WFmt::Q4_0) {
           const uint32_t dbits = sh >= 2 ? (w0 & 0xffffu) : (ld32(wrow + b4 - 4) >> 16);
           wsc = fp16_to_fp32(dbits);
         } else {
@@ -284,6 +314,8 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
         for (int i = 0; i < 4; ++i) {
           if constexpr (F == WFmt::Q4_0)
             bv[i] = (int)(((n[i] | 0x80808080u) - 0x08080808u) ^ 0x80808080u);  // q - 8 per byte
+          else if constexpr (F == WFmt::Q4_1)
+            bv[i] = (int)n[i];  // q in 0..15
           else
             bv[i] = (int)lookup16(n[i], c0, c1, c2, c3);
         }
@@ -300,10 +332,22 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
           for (int r4 = 0; r4 < 4; ++r4) {
             const float4 d4 = *reinterpret_cast<const float4*>(dxs + j * kMT + 32 * t + 8 * r4 + 4 * kg);
             const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+            if constexpr (F == WFmt::Q4_1) {
+              // (dw dx) I + m s per block (ggml-cpu/quants.c:241)
+              const uint2 s4 = *reinterpret_cast<const uint2*>(sxs + j * kMT + 32 * t + 8 * r4 + 4 * kg);
+              const float sv[4] = {fp16_to_fp32(s4.x & 0xffffu), fp16_to_fp32(s4.x >> 16),
+                                   fp16_to_fp32(s4.y & 0xffffu), fp16_to_fp32(s4.y >> 16)};
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const int r = 4 * r4 + q;
-              y[t][r] += (dv[q] * wsc) * (float)I[t][r];
+              for (int q = 0; q < 4; ++q) {
+                const int r = 4 * r4 + q;
+                y[t][r] += (dv[q] * wsc) * (float)I[t][r] + wmin * sv[q];
+              }
+            } else {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                const int r = 4 * r4 + q;
+                y[t][r] += (dv[q] * wsc) * (float)I[t][r];
+              }
             }
           }
       }
@@ -382,7 +426,10 @@ __device__ __forceinline__ bool ggml_mxfp4_entry(const int8_t* codebook, const f
 // For the MXFP4 block-scaled GEMM (kMx, and the caller passed GGML's tables)
 // the int8 values are stored as sign and magnitude and in that GEMM's K
 // order: byte 2i of a block holds element i, byte 2i + 1 element i + 16.
-template <bool kMx>
+//
+// kS (Q4_1's Q8_1 activation): the block sums s = fp16(sum(q) * d) follow
+// the scales, K/32 fp16 more per row.
+template <bool kMx, bool kS = false>
 __global__ void __launch_bounds__(256) q80_planar_kernel(const float* __restrict__ X, long long ldx,
                                                          bool a16, uint8_t* __restrict__ Xp,
                                                          long long nb, int bpr, long long xs,
@@ -400,6 +447,8 @@ __global__ void __launch_bounds__(256) q80_planar_kernel(const float* __restrict
     float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
     if (live) x = ldx4(X + row * ldx + 32 * blk + 4 * (lane & 7), a16);
     const Q8_0Lane r = q80_quantize_8lanes(x);
+    uint32_t sh = 0;
+    if constexpr (kS) sh = q81_sum_half(r);
     uint32_t word = (uint32_t)pack4_i8(r.q);
     int at = 4 * (lane & 7);
     if (kord) {
@@ -417,6 +466,7 @@ __global__ void __launch_bounds__(256) q80_planar_kernel(const float* __restrict
     uint8_t* rp = Xp + row * xs;
     *reinterpret_cast<uint32_t*>(rp + 32 * blk + at) = word;
     if ((lane & 7) == 0) *reinterpret_cast<uint16_t*>(rp + (long long)bpr * 32 + 2 * blk) = (uint16_t)r.dh;
+    if (kS && (lane & 7) == 0) *reinterpret_cast<uint16_t*>(rp + (long long)bpr * 34 + 2 * blk) = (uint16_t)sh;
   }
 }
 
@@ -770,11 +820,11 @@ template <WFmt F>
 void planar_pass(const float* X, size_t ldx, uint8_t* Xp, size_t M, size_t K, const int8_t* codebook,
                  const float* scale) {
   const long long nb = (long long)(M * K / 32);
-  const long long xs = (long long)(K + K / 16);
+  const long long xs = (long long)planar_row_bytes<F>(K);
   const long long waves = (nb + 7) / 8;
   const int grid = (int)std::max<long long>(1, std::min<long long>((long long)cu_count() * 8, (waves + 3) / 4));
   const bool a16 = aligned(X, 16) && ldx % 4 == 0;
-  q80_planar_kernel<F == WFmt::MXFP4><<<grid, 256, 0, current_stream()>>>(
+  q80_planar_kernel<F == WFmt::MXFP4, F == WFmt::Q4_1><<<grid, 256, 0, current_stream()>>>(
       X, (long long)ldx, a16, Xp, nb, (int)(K / 32), xs, codebook, scale);
   check_launch("q80_planar_kernel");
 }
@@ -805,7 +855,11 @@ bool prefill_q80(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* co
     q80_mfma_gemm<F, false><<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(ga);
   }
   check_launch(F == WFmt::MXFP4 ? "mxfp4_gemm" : "q80_mfma_gemm");
-  quantize_q8_0_rows(X, ldx, Xq, M, K);  // Xq ends in GGML's record layout
+  // Xq ends in GGML's record layout
+  if constexpr (F == WFmt::Q4_1)
+    quantize_q8_1_rows(X, ldx, Xq, M, K);
+  else
+    quantize_q8_0_rows(X, ldx, Xq, M, K);
   return true;
 }
 
@@ -868,6 +922,14 @@ void mul_mat_q4_0(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_
   if (W == nullptr || X == nullptr || Xq == nullptr || Y == nullptr ||
       !prefill_q80<WFmt::Q4_0>(W, X, Xq, nullptr, nullptr, Y, N, K, M, st))
     decode_q4_0(W, X, Xq, Y, N, K, M, st);
+}
+
+void mul_mat_q4_1(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
+                  size_t M, const RowStrides& st) {
+  if (N == 0 || M == 0 || K == 0) return decode_q4_1(W, X, Xq, Y, N, K, M, st);
+  if (W == nullptr || X == nullptr || Xq == nullptr || Y == nullptr ||
+      !prefill_q80<WFmt::Q4_1>(W, X, Xq, nullptr, nullptr, Y, N, K, M, st))
+    decode_q4_1(W, X, Xq, Y, N, K, M, st);
 }
 
 void mul_mat_mxfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,

@@ -1,7 +1,8 @@
-// Standalone activation quantizers q8_0_quantize and q8_K_quantize
-// (examples/kernels/quantize/q8_0.py:26-28, q8_k.py:38-40), bit-exact with
-// GGML's quantize_row_q8_0_ref / quantize_row_q8_K_ref
-// (ggml-quants.c:238-261, :2696-2733).
+// Standalone activation quantizers q8_0_quantize, q8_K_quantize and
+// q8_1_quantize (examples/kernels/quantize/q8_0.py:26-28, q8_k.py:38-40,
+// q8_1.py:28-30), bit-exact with GGML's quantize_row_q8_0_ref /
+// quantize_row_q8_K_ref / quantize_row_q8_1_ref (ggml-quants.c:238-261,
+// :2696-2733, :264-295).
 //
 // HBM-bound (read 4 B, write ~1.1 B per element).  Q8_K: 16 lanes per
 // superblock, lane p owns x[16p..16p+15] (four 16-byte loads), so the
@@ -103,6 +104,35 @@ __global__ void __launch_bounds__(kThreads) q80_quantize_kernel(const float* __r
   }
 }
 
+// Q8_1: Q8_0's lanes plus the block's s; the 36-byte records are 2-byte
+// aligned, so the codes go out as halfwords
+__global__ void __launch_bounds__(kThreads) q81_quantize_kernel(const float* __restrict__ X,
+                                                                uint8_t* __restrict__ Y, long long nb,
+                                                                XRows xr, bool a16) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const long long wave = ((long long)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const long long nwaves = (long long)gridDim.x * blockDim.x / kWave;
+  const long long steps = (nb + 7) / 8;
+  for (long long st = wave; st < steps; st += nwaves) {
+    const long long b = 8 * st + lane / 8;
+    const bool live = b < nb;
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live) x = ldx4(xr.at(X, b, 32) + 4 * (lane & 7), a16);
+    const Q8_0Lane r = q80_quantize_8lanes(x);
+    const uint32_t sh = q81_sum_half(r);
+    if (!live) continue;
+    uint8_t* rec = Y + b * kQ8_1Bytes;
+    const uint32_t packed = (uint32_t)pack4_i8(r.q);
+    uint16_t* q16 = reinterpret_cast<uint16_t*>(rec + 4 + 4 * (lane & 7));
+    q16[0] = (uint16_t)(packed & 0xffffu);
+    q16[1] = (uint16_t)(packed >> 16);
+    if ((lane & 7) == 0) {
+      reinterpret_cast<uint16_t*>(rec)[0] = (uint16_t)r.dh;
+      reinterpret_cast<uint16_t*>(rec)[1] = (uint16_t)sh;
+    }
+  }
+}
+
 int grid_for(long long waves_needed) {
   const long long per_block = kThreads / kWave;
   const long long cap = (long long)cu_count() * 8;  // 8 workgroups (32 waves) per CU
@@ -140,6 +170,19 @@ void quantize_q8_0_rows(const float* X, size_t ldx, uint8_t* Y, size_t M, size_t
   check_launch("q80_quantize_kernel");
 }
 
+void quantize_q8_1_rows(const float* X, size_t ldx, uint8_t* Y, size_t M, size_t K) {
+  if (K == 0 || M == 0) return;
+  if (K % 32 || X == nullptr || Y == nullptr || !aligned(X, 4) || !aligned(Y, 2) ||
+      (M > 1 && ldx < K))
+    return set_error(hipErrorInvalidValue);
+  const bool flat = M == 1 || ldx == K;
+  const long long nb = (long long)(M * (K / 32));
+  const XRows xr{flat ? 0 : (long long)(K / 32), (long long)ldx};
+  const bool a16 = aligned(X, 16) && (flat || ldx % 4 == 0);
+  q81_quantize_kernel<<<grid_for((nb + 7) / 8), kThreads, 0, current_stream()>>>(X, Y, nb, xr, a16);
+  check_launch("q81_quantize_kernel");
+}
+
 void quantize_q8_k(const float* X, uint8_t* Y, size_t K) { quantize_q8_k_rows(X, K, Y, 1, K); }
 
 void quantize_q8_0(const float* X, uint8_t* Y, size_t K) { quantize_q8_0_rows(X, K, Y, 1, K); }
@@ -151,5 +194,7 @@ extern "C" {
 void q8_0_quantize(const float* X, uint8_t* Y, size_t K) { weft::quantize_q8_0(X, Y, K); }
 
 void q8_K_quantize(const float* X, uint8_t* Y, size_t K) { weft::quantize_q8_k(X, Y, K); }
+
+void q8_1_quantize(const float* X, uint8_t* Y, size_t K) { weft::quantize_q8_1_rows(X, K, Y, 1, K); }
 
 }  // extern "C"

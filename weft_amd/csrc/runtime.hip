@@ -201,6 +201,8 @@ const EncodingInfo kEncodings[] = {
     {"I8X8", "uint8_t", 8, 8, 8},        {"Q4K_I[16]", "uint8_t", 144, 256, 16},
     {"Q6_K", "uint8_t", 210, 256, 1},    {"Q5_K", "uint8_t", 176, 256, 2},
     {"NVFP4", "uint8_t", 36, 64, 1},
+    {"Q4_1", "uint8_t", 20, 32, 2},      {"Q8_1", "uint8_t", 36, 32, 2},
+    {"IQ2_XS", "uint8_t", 74, 256, 2},
     {"dense.f32", "float", 4, 1, 4},
     {"dense.i8", "int8_t", 1, 1, 1},
 };
@@ -324,6 +326,35 @@ std::vector<KernelSpec> kernel_specs() {
                 {"Xq", "Q8_K", "M,K", true, nullptr},
                 {"Y", "dense.f32", "M,N", true, nullptr}},
                "M,K,N"});
+  k.push_back({"row_dequantize_q4_1",
+               {{"W", "Q4_1", "K", false, nullptr}, {"Y", "dense.f32", "K", true, nullptr}}, "K"});
+  k.push_back({"row_dequantize_iq2_xs",
+               {{"W", "IQ2_XS", "K", false, nullptr},
+                {"grid", "dense.i8", "4096", false, nullptr},
+                {"signs", "dense.i8", "1024", false, nullptr},
+                {"Y", "dense.f32", "K", true, nullptr}},
+               "K"});
+  k.push_back({"q8_1_quantize",
+               {{"X", "dense.f32", "K", false, nullptr}, {"Y", "Q8_1", "K", true, nullptr}}, "K"});
+  k.push_back({"quantized_vec_dot_q4_1_q8_1",
+               {{"W", "Q4_1", "K", false, nullptr},
+                {"X", "Q8_1", "K", false, nullptr},
+                {"Y", "dense.f32", "1", true, nullptr}},
+               "K"});
+  const std::vector<ArgSpec> iq2xs = {{"grid", "I8X8", "512,8", false, nullptr},
+                                      {"signs", "I8X8", "128,8", false, nullptr}};
+  k.push_back({"quantized_vec_dot_iq2_xs_q8_k",
+               {{"W", "IQ2_XS", "K", false, nullptr},
+                {"X", "Q8_K", "K", false, nullptr},
+                iq2xs[0],
+                iq2xs[1],
+                {"Y", "dense.f32", "1", true, nullptr}},
+               "K"});
+  mm("production_mul_mat_q4_1", "Q4_1", "Q8_1", true, {});
+  mm("production_mul_mat_q4_1_decode", "Q4_1", "Q8_1", true, {});
+  mm("production_mul_mat_iq2_xs", "IQ2_XS", "Q8_K", true, iq2xs);
+  mm("production_mul_mat_iq2_xs_staged", "IQ2_XS", "Q8_K", false,
+     {{"grid", "dense.i8", "4096", false, nullptr}, {"signs", "dense.i8", "1024", false, nullptr}});
   for (const char* sym : {"q4_k_q8_k_gemv", "q4_k_q8_k_gemv_groups4", "q4_k_q8_k_gemv_contract"})
     k.push_back({sym,
                  {{"W", "Q4K_I[16]", "M,K", false, nullptr},

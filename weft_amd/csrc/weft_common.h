@@ -24,6 +24,9 @@ constexpr int kIq2xxsElems = 256, kIq2xxsBytes = 66;
 constexpr int kQ6_KElems = 256, kQ6_KBytes = 210;  // ql[128] qh[64] scales[16] d
 constexpr int kQ5_KElems = 256, kQ5_KBytes = 176;  // d dmin scales[12] qh[32] qs[128]
 constexpr int kNvfp4Elems = 64, kNvfp4Bytes = 36;  // ue4m3 d[4] qs[32]
+constexpr int kQ4_1Elems = 32, kQ4_1Bytes = 20;    // d m qs[16]
+constexpr int kQ8_1Elems = 32, kQ8_1Bytes = 36;    // d s qs[32]
+constexpr int kIq2xsElems = 256, kIq2xsBytes = 74; // d qs[32] (u16) scales[8]
 
 // ---------------------------------------------------------------- numerics
 // IEEE binary16 -> binary32 with v_cvt_f32_f16.  Exact for every input
@@ -342,6 +345,17 @@ __device__ __forceinline__ Q8_0Lane q80_quantize_8lanes(float4 x) {
   r.d = d;
   r.dh = fp32_to_fp16(d);
   return r;
+}
+
+// Q8_1's block sum term (quantize_row_q8_1_ref, ggml-quants.c:264-295):
+// s = fp16(sum(q) * d) with the fp32 d, over the 8 lanes of a block (every
+// lane of the wave calls this)
+__device__ __forceinline__ uint32_t q81_sum_half(const Q8_0Lane& r) {
+  int t = r.q[0] + r.q[1] + r.q[2] + r.q[3];
+  t += __shfl_xor(t, 1, kWave);
+  t += __shfl_xor(t, 2, kWave);
+  t += __shfl_xor(t, 4, kWave);
+  return fp32_to_fp16((float)t * r.d);
 }
 
 // ggml_e8m0_to_fp32_half (ggml-impl.h:477-495): 2^(e-128), e < 2 as fp32

@@ -16,6 +16,7 @@ from . import _lib
 
 # enum ggml_type (ggml/include/ggml.h:389-431), the types of this path
 F32, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K, IQ2_XXS, I32, MXFP4, NVFP4 = 0, 2, 8, 12, 13, 14, 15, 16, 26, 39, 40
+Q4_1, Q8_1, IQ2_XS = 3, 9, 17
 
 
 class Tensor(ctypes.Structure):

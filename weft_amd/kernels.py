@@ -65,6 +65,9 @@ _AUTO = {
     "production_mul_mat_q6_k": ("MC", "MR", "NC", "NR"),
     "production_mul_mat_q5_k": ("MC", "MR", "NC", "NR"),
     "production_mul_mat_nvfp4": ("MC", "MR", "NC", "NR"),
+    "production_mul_mat_q4_1": ("MC", "MR", "NC", "NR"),
+    "production_mul_mat_iq2_xs": ("NR",),
+    "production_mul_mat_iq2_xs_staged": ("KC", "MC", "MR", "NC", "NR"),
 }
 
 # (symbol, parameters, reference source, alias groups)
@@ -109,6 +112,16 @@ _DEFS = [
     ("production_mul_mat_nvfp4", _MM_MX, "examples/kernels/mul_mat/nvfp4.py:10-43", None),
     ("production_mul_mat_nvfp4_decode", _MM_MX, "examples/kernels/mul_mat/nvfp4_decode.py:10-23", None),
     ("production_mul_mat_q4_k_persistent", _MM, "examples/kernels/mul_mat/q4_k_persistent.py:10-31", None),
+    ("row_dequantize_q4_1", ("W", "Y"), "examples/kernels/dequantize/q4_1.py:9-13", None),
+    ("row_dequantize_iq2_xs", ("W", "grid", "signs", "Y"), "examples/kernels/dequantize/iq2_xs.py:9-75", None),
+    ("q8_1_quantize", ("X", "Y"), "examples/kernels/quantize/q8_1.py:28-30", None),
+    ("quantized_vec_dot_q4_1_q8_1", ("W", "X", "Y"), "examples/kernels/vec_dot/q4_1_q8_1.py:8-29", None),
+    ("quantized_vec_dot_iq2_xs_q8_k", ("W", "X", "grid", "signs", "Y"),
+     "examples/kernels/vec_dot/iq2_xs_q8_k.py:9-45", None),
+    ("production_mul_mat_q4_1", _MM, "examples/kernels/mul_mat/q4_1.py:9-30", _DECODE_GROUPS),
+    ("production_mul_mat_q4_1_decode", _MM, "examples/kernels/mul_mat/q4_1_decode.py:10-20", _DECODE_GROUPS),
+    ("production_mul_mat_iq2_xs", _MM_IQ2, "examples/kernels/mul_mat/iq2_xs.py:26-56", _DECODE_GROUPS),
+    ("production_mul_mat_iq2_xs_staged", _MM_IQ2, "examples/kernels/mul_mat/iq2_xs_staged.py:29-75", None),
     ("q4_k_q8_k_gemv", ("W", "X", "Y"), "examples/kernels/gemv/q4_k.py:8-26", None),
     ("q4_k_q8_k_gemv_groups4", ("W", "X", "Y"), "examples/kernels/gemv/q4_k_groups4.py:8-26", None),
     ("q4_k_q8_k_gemv_contract", ("W", "X", "Y"), "examples/kernels/gemv/q4_k_contract.py:8-26", None),
