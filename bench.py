@@ -8,10 +8,11 @@ included, exactly as the reference's timed mul_mat (weft-kernel-performance.csv:
 ``value`` is the algorithmic HBM bytes of the call (encoded W + fp32 X + Xq
 write + fp32 Y = 25,427,520 B) divided by the measured time per call, in GB/s.
 
-Inputs are seeded synthetic data (weights ~ N(0, 0.02^2) quantized on the host
-by oracle/'s restatement of GGML's reference quantizers -- for IQ2_XXS a
-nearest-grid generator, not GGML's quantize_iq2_xxs -- and activations
-~ N(0, 1)), resident in HBM before timing.  Every case rotates its weights
+Inputs are seeded synthetic data, resident in HBM before timing: weight
+records of random payload bytes with their scale fields at the magnitudes
+GGML's quantizers give an N(0, 0.02^2) matrix (the kernels' time does not
+depend on the values), activations ~ N(0, 1), pre-quantized activations by
+the library's own q8_K_quantize.  Only the CPU baseline below uses oracle/.  Every case rotates its weights
 over enough copies (> 2 x the 256 MB Infinity Cache) that each call reads
 them from HBM.  Each case is timed three ways on the library's stream:
   * ``us``: K back-to-back calls between two HIP events (the headline);
@@ -74,6 +75,10 @@ CASES = {
     "q6_k_prefill": ("production_mul_mat_q6_k", "q6_k", 4096, 4096, 512, "mfma"),
     "q5_k_decode": ("production_mul_mat_q5_k_decode", "q5_k", 11008, 4096, 1, "hbm"),
     "nvfp4_decode": ("production_mul_mat_nvfp4_decode", "nvfp4", 11008, 4096, 1, "hbm"),
+    "q4_1_decode": ("production_mul_mat_q4_1_decode", "q4_1", 11008, 4096, 1, "hbm"),
+    "q4_1_prefill": ("production_mul_mat_q4_1", "q4_1", 4096, 4096, 512, "mfma"),
+    "iq2_xs_decode": ("production_mul_mat_iq2_xs", "iq2_xs", 4096, 4096, 1, "hbm"),
+    "iq2_xs_prefill": ("production_mul_mat_iq2_xs_staged", "iq2_xs", 4096, 4096, 512, "mfma"),
     # GGML MUL_MAT_ID (MoE) prefill at a Mixtral-8x7B FFN shape: 8 experts of
     # 14336 x 4096 Q4_K, 2 experts per token, 512 tokens (the grouped GEMM)
     "q4_k_moe_prefill": ("weft_ggml_mul_mat_id", "q4_k", 14336, 4096, 512, "mfma"),
@@ -106,6 +111,75 @@ def parse():
     return p.parse_args()
 
 
+# (elements, bytes) per record of the GGML formats (ggml-common.h block structs)
+RECORD = {"q4_0": (32, 18), "q4_1": (32, 20), "mxfp4": (32, 17), "q8_0": (32, 34), "q8_1": (32, 36),
+          "q4_k": (256, 144), "q5_k": (256, 176), "q6_k": (256, 210), "q8_k": (256, 292),
+          "iq2_xxs": (256, 66), "iq2_xs": (256, 74), "nvfp4": (64, 36)}
+ACT_OF = {"q4_0": "q8_0", "mxfp4": "q8_0", "nvfp4": "q8_0", "q4_1": "q8_1"}  # others: Q8_K
+
+
+def record_bytes(fmt: str, k: int) -> int:
+    elems, nbytes = RECORD[fmt]
+    return k // elems * nbytes
+
+
+def seeded_normal(seed: int, shape, sigma: float = 1.0) -> np.ndarray:
+    rng = np.random.Generator(np.random.PCG64(seed))
+    return (rng.standard_normal(size=shape, dtype=np.float64) * sigma).astype(np.float32)
+
+
+def synthetic_weights(fmt: str, n: int, k: int, seed: int = 1) -> np.ndarray:
+    """n rows of fmt records: random payload bytes, and the scale fields at
+    the magnitudes GGML's quantizers give an N(0, 0.02) matrix (every byte
+    pattern is a valid record of these formats, and the kernels' time does
+    not depend on the values; MXFP4 exponents stay in the range the
+    block-scaled MFMA takes directly)."""
+    rng = np.random.default_rng(seed)
+    elems, nbytes = RECORD[fmt]
+    nrec = k // elems
+    rec = rng.integers(0, 256, size=(n, nrec, nbytes), dtype=np.uint8)
+
+    def f16(lo, hi, at):
+        v = rng.uniform(lo, hi, size=(n, nrec)).astype(np.float16)
+        rec[:, :, at:at + 2] = v.view(np.uint8).reshape(n, nrec, 2)
+
+    if fmt in ("q4_0", "iq2_xxs", "iq2_xs"):
+        f16(2e-3, 8e-3, 0)
+    elif fmt == "q4_1":
+        f16(4e-3, 8e-3, 0)
+        f16(-6e-2, -3e-2, 2)
+    elif fmt in ("q4_k", "q5_k"):
+        f16(1e-4, 3e-4, 0)
+        f16(1e-4, 3e-4, 2)
+    elif fmt == "q6_k":
+        f16(2e-5, 6e-5, 208)
+    elif fmt == "mxfp4":
+        rec[:, :, 0] = rng.integers(118, 123, size=(n, nrec), dtype=np.uint8)
+    elif fmt == "nvfp4":
+        rec[:, :, 0:4] = rng.integers(0x20, 0x40, size=(n, nrec, 4), dtype=np.uint8)
+    return rec.reshape(n, -1)
+
+
+def ggml_tables() -> dict:
+    """The lookup tables the ABI passes to IQ2_XXS / IQ2_XS / MXFP4 / NVFP4
+    kernels: grids from the GGML table fixture (ggml-common.h's text), the
+    rest from their definitions."""
+    with open(os.path.join(ROOT, "tests", "golden", "ggml_tables.json")) as f:
+        t = json.load(f)
+    grid = np.array([int(h, 16) for h in t["iq2xxs_grid"]], np.uint64).view(np.int8)
+    grid_xs = np.array([int(h, 16) for h in t["iq2xs_grid"]], np.uint64).view(np.int8)
+    ks = np.array(t["ksigns_iq2xs"], np.int64)
+    signs = np.where((ks[:, None] >> np.arange(8)[None, :]) & 1, -1, 1).astype(np.int8).reshape(-1)
+    kv = np.array(t["kvalues_mxfp4"], np.int8)
+    e = np.arange(256, dtype=np.uint32)
+    e8m0 = np.where(e < 2, np.uint32(0x00200000) << e, (e - 1) << 23).astype(np.uint32).view(np.float32)
+    c = np.arange(256)
+    ex, mant = (c >> 3) & 15, c & 7
+    ue4m3 = np.where(ex == 0, mant / 1024.0, (8 + mant) * np.ldexp(1.0, ex.astype(np.int32) - 11)).astype(np.float32)
+    ue4m3[[0, 0x7F]] = 0.0
+    return {"iq2_xxs": [grid, signs], "iq2_xs": [grid_xs, signs], "mxfp4": [kv, e8m0], "nvfp4": [kv, ue4m3]}
+
+
 def profiled_traffic(name: str):
     """HBM bytes per launch measured by the FETCH_SIZE / WRITE_SIZE counter
     runs recorded in profiles/<name>.md (scaled against a known-size copy),
@@ -136,7 +210,6 @@ class Bench:
     def __init__(self):
         import torch
 
-        import oracle as o
         from weft_amd import _lib
         self.torch = torch
         self.lib = _lib.load()
@@ -144,15 +217,21 @@ class Bench:
         self.dev = torch.device("cuda:0")
         self.stream = torch.cuda.current_stream()
         _lib.set_stream(self.stream.cuda_stream)
-        self.tables = {
-            "iq2_xxs": [self.dev_copy(o.iq2xxs_grid().view(np.int8)), self.dev_copy(o.signs_i8x8())],
-            "mxfp4": [self.dev_copy(o.kvalues_mxfp4()), self.dev_copy(o.e8m0_half_table())],
-            "nvfp4": [self.dev_copy(o.kvalues_mxfp4()), self.dev_copy(o.ue4m3_table())],
-        }
+        self.tables = {fmt: [self.dev_copy(a) for a in arrs] for fmt, arrs in ggml_tables().items()}
         self.flush_buf = None
 
     def dev_copy(self, a: np.ndarray):
         return self.torch.from_numpy(np.ascontiguousarray(a)).to(self.dev)
+
+    def q8k(self, x: np.ndarray):
+        """Q8_K records of the rows of x, by the library's q8_K_quantize."""
+        m, k = x.shape
+        xd = self.dev_copy(x)
+        out = self.torch.empty(record_bytes("q8_k", k) * m, dtype=self.torch.uint8, device=self.dev)
+        self.lib.q8_K_quantize(xd.data_ptr(), out.data_ptr(), m * k)
+        self.torch.cuda.synchronize()
+        self._lib.check("q8_K_quantize")
+        return out
 
     def events(self):
         return (self.torch.cuda.Event(enable_timing=True), self.torch.cuda.Event(enable_timing=True))
@@ -268,9 +347,8 @@ class Bench:
 
 def run_case(b: Bench, name: str, steps: int, warmup: int, extra: bool) -> dict:
     """Time one case; returns its figures (algorithmic bytes / ops, rate, roofline fraction)."""
-    import oracle as o
     sym, fmt, n, k, m, bound = CASES[name]
-    w = o.quantize(fmt, o.seeded_normal(1, (n, k), 0.02))
+    w = synthetic_weights(fmt, n, k)
     torch = b.torch
     copies = max(2, int(np.ceil(2 * MALL_BYTES / w.nbytes)) + 1)
     fn = getattr(b.lib, sym)
@@ -284,7 +362,7 @@ def run_case(b: Bench, name: str, steps: int, warmup: int, extra: bool) -> dict:
         rng = np.random.default_rng(3)
         ids_h = np.stack([rng.choice(MOE_EXPERTS, MOE_USED, replace=False) for _ in range(m)]).astype(np.int32)
         ids = b.dev_copy(ids_h)
-        x = b.dev_copy(o.seeded_normal(2, (m, k)))
+        x = b.dev_copy(seeded_normal(2, (m, k)))
         y = torch.empty(m * MOE_USED * n, dtype=torch.float32, device=b.dev)
         s1 = G.tensor(G.F32, (k, 1, m), x.data_ptr())
         it = G.tensor(G.I32, (MOE_USED, m), ids.data_ptr())
@@ -296,12 +374,12 @@ def run_case(b: Bench, name: str, steps: int, warmup: int, extra: bool) -> dict:
         def launch(i):
             G.mul_mat_id(s0s[i % copies], s1, it, d, work.data_ptr(), wsize)
 
-        nbytes = MOE_EXPERTS * w.nbytes + 4 * m * k + o.record_bytes("q8_k", k) * m + 4 * m * MOE_USED * n
+        nbytes = MOE_EXPERTS * w.nbytes + 4 * m * k + record_bytes("q8_k", k) * m + 4 * m * MOE_USED * n
         m *= MOE_USED  # products: one per (token, expert) pair
     elif sym == "weft_ggml_mul_mat":
         from weft_amd import ggml as G
         wd = [b.dev_copy(w) for _ in range(copies)]
-        xq = b.dev_copy(o.quantize("q8_k", o.seeded_normal(2, (m, k))))
+        xq = b.q8k(seeded_normal(2, (m, k)))
         y = torch.empty(m * n, dtype=torch.float32, device=b.dev)
         s0s = [G.tensor(G.Q4_K, (k, n), t.data_ptr()) for t in wd]
         s1 = G.tensor(G.Q8_K, (k, m), xq.data_ptr())
@@ -328,7 +406,7 @@ def run_case(b: Bench, name: str, steps: int, warmup: int, extra: bool) -> dict:
             torch.cuda.synchronize()
             b._lib.check(sym + "_W_pack")
             wd = packed
-            xq = b.dev_copy(o.quantize("q8_k", o.seeded_normal(2, (1, k))))
+            xq = b.q8k(seeded_normal(2, (1, k)))
             y = torch.empty(n, dtype=torch.float32, device=b.dev)
 
             def launch(i):
@@ -343,8 +421,8 @@ def run_case(b: Bench, name: str, steps: int, warmup: int, extra: bool) -> dict:
             torch.cuda.synchronize()
             b._lib.check(sym + "_W_pack")
             wd = packed
-            x = b.dev_copy(o.seeded_normal(2, (m, k)))
-            xq = torch.empty(o.record_bytes("q8_k", k) * m, dtype=torch.uint8, device=b.dev)
+            x = b.dev_copy(seeded_normal(2, (m, k)))
+            xq = torch.empty(record_bytes("q8_k", k) * m, dtype=torch.uint8, device=b.dev)
             y = torch.empty(m * n, dtype=torch.float32, device=b.dev)
 
             def launch(i):
@@ -352,9 +430,9 @@ def run_case(b: Bench, name: str, steps: int, warmup: int, extra: bool) -> dict:
 
             nbytes = w.nbytes + 4 * m * k + xq.numel() + 4 * m * n
         else:
-            act = o.ACT_OF[fmt]
-            x = b.dev_copy(o.seeded_normal(2, (m, k)))
-            xq = torch.empty(o.record_bytes(act, k) * m, dtype=torch.uint8, device=b.dev)
+            act = ACT_OF.get(fmt, "q8_k")
+            x = b.dev_copy(seeded_normal(2, (m, k)))
+            xq = torch.empty(record_bytes(act, k) * m, dtype=torch.uint8, device=b.dev)
             y = torch.empty(m * n, dtype=torch.float32, device=b.dev)
             tabs = [t.data_ptr() for t in b.tables.get(fmt, [])]
 
@@ -491,8 +569,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic (seeded N(0,0.02) weights quantized on the host by the oracle's restated GGML "
-                "reference quantizers, IQ2_XXS by a nearest-grid generator; N(0,1) activations)",
+        "data": "synthetic (weight records of random payload bytes with scale fields at the magnitudes "
+                "an N(0,0.02) matrix quantizes to; seeded N(0,1) activations)",
         "config": {"workload": "production_mul_mat_q4_k_decode, config 3 W_up: N=11008 K=4096 "
                                "M=1, Q8_K activation quantize inside the timed call",
                    "N": 11008, "K": 4096, "M": 1,
