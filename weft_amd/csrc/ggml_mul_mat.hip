@@ -311,7 +311,7 @@ hipError_t mul_mat(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1, const
             break;
           case WEFT_GGML_TYPE_Q4_1: mul_mat_q4_1(W, X, Xq, Y, n, k, m, st); break;
           case WEFT_GGML_TYPE_IQ2_XS:
-            decode_iq2_xs(W, X, Xq, tab->grid_xs, tab->signs, Y, n, k, m, st);
+            mul_mat_iq2_xs(W, X, Xq, tab->grid_xs, tab->signs, Y, n, k, m, st);
             break;
           default: mul_mat_mxfp4(W, X, Xq, tab->codebook, tab->scale, Y, n, k, m, st); break;
         }
@@ -329,7 +329,7 @@ hipError_t mul_mat(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1, const
             break;
           case WEFT_GGML_TYPE_Q4_1: decode_quantized(6, W, src1, nullptr, nullptr, Y, n, k, m, st); break;
           case WEFT_GGML_TYPE_IQ2_XS:
-            decode_quantized(7, W, src1, tab->grid_xs, tab->signs, Y, n, k, m, st);
+            mul_mat_iq2_xs_quantized(W, src1, tab->grid_xs, tab->signs, Y, n, k, m, st);
             break;
           default: decode_quantized(1, W, src1, tab->codebook, tab->scale, Y, n, k, m, st); break;
         }

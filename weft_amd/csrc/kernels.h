@@ -151,6 +151,11 @@ void mul_mat_q4_1(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_
 void mul_mat_iq2_xxs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,
                      const int8_t* signs, float* Y, size_t N, size_t K, size_t M,
                      const RowStrides& st);
+// IQ2_XS mul_mat for any M: the IQ2 GEMM with per-16 scales for prefill shapes, GEMV otherwise.
+void mul_mat_iq2_xs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid, const int8_t* signs,
+                    float* Y, size_t N, size_t K, size_t M, const RowStrides& st);
+void mul_mat_iq2_xs_quantized(const uint8_t* W, const uint8_t* Xq, const int8_t* grid, const int8_t* signs,
+                              float* Y, size_t N, size_t K, size_t M, const RowStrides& st);
 void mul_mat_iq2_xxs_quantized(const uint8_t* W, const uint8_t* Xq, const int8_t* grid,
                                const int8_t* signs, float* Y, size_t N, size_t K, size_t M,
                                const RowStrides& st);

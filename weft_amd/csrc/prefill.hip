@@ -63,11 +63,10 @@ void production_mul_mat_q4_1(const uint8_t* W, const float* X, uint8_t* Xq, floa
   weft::mul_mat_q4_1(W, X, Xq, Y, N, K, M, weft::packed(K / 32 * weft::kQ4_1Bytes, K, N));
 }
 
-// IQ2_XS: the GEMV kernel at every M (no MFMA form yet)
 void production_mul_mat_iq2_xs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,
                                const int8_t* signs, float* Y, size_t N, size_t K, size_t M) {
   if (X == nullptr || Xq == nullptr) return weft::set_error(hipErrorInvalidValue);
-  weft::decode_iq2_xs(W, X, Xq, grid, signs, Y, N, K, M, weft::packed(K / 256 * weft::kIq2xsBytes, K, N));
+  weft::mul_mat_iq2_xs(W, X, Xq, grid, signs, Y, N, K, M, weft::packed(K / 256 * weft::kIq2xsBytes, K, N));
 }
 
 void production_mul_mat_iq2_xs_staged(const uint8_t* W, const float* X, uint8_t* Xq,

@@ -1,5 +1,7 @@
 // IQ2_XXS x Q8_K prefill GEMM on int8 MFMA (production_mul_mat_iq2_xxs,
-// production_mul_mat_iq2_xxs_staged; examples/kernels/mul_mat/iq2_xxs_staged.py:9-97).
+// production_mul_mat_iq2_xxs_staged; examples/kernels/mul_mat/iq2_xxs_staged.py:9-97),
+// and its IQ2_XS variant (production_mul_mat_iq2_xs{,_staged};
+// examples/kernels/mul_mat/iq2_xs.py:26-56, iq2_xs_staged.py:29-75).
 //
 //   Y[m, n] = 1/8 * sum_b dw[n,b] * dx[m,b] * sum_g ls[n,b,g] * I[m,n,b,g]
 //   I = sum_{k in group g} q8[m,k] * grid[idx][j] * sign      (exact int32)
@@ -35,14 +37,22 @@ constexpr int kMT = 64;        // tokens per workgroup tile
 constexpr int kNT = 128;       // weight rows per workgroup tile
 constexpr int kThreads = 512;  // 8 waves: 4 column groups x 2 superblock parities
 constexpr int kAQ = kMT * 256;                    // activation int8 of one superblock
-constexpr int kPairB = 2 * kIq2xxsBytes;          // 132 weight bytes per row and pair
-constexpr int kWT = kNT * kPairB;                 // 16896
-constexpr int kSlot = 2 * kAQ + kWT;              // one ring slot: both parities + weights
-constexpr int kSlotAlloc = kSlot + 16;            // slack: a group read may run 4 bytes past row 127
-constexpr int kWD = kPairB / 4;                   // 33 dwords per row and pair
-constexpr int kWSlots = kNT * kWD / 64;           // 66 wave-wide dword loads per pair
-static_assert(kNT * kWD % 64 == 0, "weight pair tile is whole wave loads");
-static_assert(4 * 32 * 64 * 4 <= kSlot, "reduction buffer fits one ring slot");
+
+// Per format (kXs: IQ2_XS, else IQ2_XXS): record bytes and the weight tile
+// of a superblock pair (4-byte aligned: 132 / 148 bytes per row).
+template <bool kXs>
+struct Tile {
+  static constexpr int kRec = kXs ? kIq2xsBytes : kIq2xxsBytes;  // 74 / 66
+  static constexpr int kPairB = 2 * kRec;
+  static constexpr int kWT = kNT * kPairB;                      // 18944 / 16896
+  static constexpr int kSlot = 2 * kAQ + kWT;                   // one ring slot: both parities + weights
+  static constexpr int kSlotAlloc = kSlot + 16;                 // slack: a read may run past row 127
+  static constexpr int kWD = kPairB / 4;                        // 37 / 33 dwords per row and pair
+  static constexpr int kWSlots = kNT * kWD / 64;                // 74 / 66 wave-wide dword loads
+  static constexpr int kGrid = kXs ? 512 : 256;                 // grid entries
+  static_assert(kNT * kWD % 64 == 0, "weight pair tile is whole wave loads");
+  static_assert(4 * 32 * 64 * 4 <= kSlot, "reduction buffer fits one ring slot");
+};
 
 struct GemmArgs {
   const uint8_t* W;
@@ -90,12 +100,20 @@ __device__ __forceinline__ uint32_t apply_signs(uint32_t g, uint32_t s) {
   return (g ^ m) + (m & 0x01010101u);
 }
 
-template <bool kGroup>
+// kXs (IQ2_XS, ggml-cpu/quants.c:897-946): u16 entries (grid row bits 0-8,
+// sign row bits 9-15) and a 4-bit scale per 16-element half, s_lo for
+// entries 0-1 and s_hi for 2-3 of each 32-group (scale byte 66 + g).  A
+// 32-group's MFMA runs twice with the weight operand of one half (the lanes
+// kg of the other half hold zeros), and each product tile takes its half's
+// 2 s + 1 in the same exact int32 multiply-add.
+template <bool kGroup, bool kXs = false>
 __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
-  __shared__ __align__(16) uint8_t ring0[kSlotAlloc];
-  __shared__ __align__(16) uint8_t ring1[kSlotAlloc];
+  using TT = Tile<kXs>;
+  constexpr int kPairB = TT::kPairB, kWD = TT::kWD, kWSlots = TT::kWSlots;
+  __shared__ __align__(16) uint8_t ring0[TT::kSlotAlloc];
+  __shared__ __align__(16) uint8_t ring1[TT::kSlotAlloc];
   __shared__ __align__(16) float dxs[2][2][kMT];  // [slot][parity][token]
-  __shared__ __align__(16) uint8_t tgrid[256 * 8];
+  __shared__ __align__(16) uint8_t tgrid[TT::kGrid * 8];
   __shared__ __align__(16) uint8_t tsign[128 * 8];
 
   const int tid = threadIdx.x;
@@ -134,7 +152,7 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
       return m0 + r;
   };
 
-  for (int i = tid; i < 256 * 8; i += kThreads) tgrid[i] = (uint8_t)a.grid[i];
+  for (int i = tid; i < TT::kGrid * 8; i += kThreads) tgrid[i] = (uint8_t)a.grid[i];
   for (int i = tid; i < 128 * 8; i += kThreads) tsign[i] = (uint8_t)a.signs[i];
 
   // activation int8 of superblock 2*pair + par: 16 wave-wide 16-byte loads, 4 per wave
@@ -147,12 +165,16 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
   }
   const uint8_t* dsrc = a.Xq + (size_t)act_row(min(lane, mrows - 1)) * xrb;  // Q8_K d of token lane
 
+  // LDS byte addresses of the two ring slots, formed once from wave-uniform
+  // pointers (no per-load generic-to-LDS casts)
+  const uint32_t ring_lds[2] = {(uint32_t)__builtin_amdgcn_readfirstlane(lds_addr(ring0)),
+                                (uint32_t)__builtin_amdgcn_readfirstlane(lds_addr(ring1))};
   auto issue = [&](int pair, uint8_t* ring) {
     const int b = 2 * pair + par;
+    const uint32_t base = ring == ring0 ? ring_lds[0] : ring_lds[1];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      lds_dma16(asrc[i] + (size_t)b * kQ8_KBytes,
-                __builtin_amdgcn_readfirstlane(lds_addr(ring + par * kAQ + 1024 * (wcol + 4 * i))));
+      lds_dma16(asrc[i] + (size_t)b * kQ8_KBytes, base + par * kAQ + 1024 * (wcol + 4 * i));
     // weight pair: 66 dword loads over the 8 waves
 #pragma unroll
     for (int i = 0; i < (kWSlots + 7) / 8; ++i) {
@@ -160,7 +182,7 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
       if (k < kWSlots) {
         const int q = 64 * k + lane, row = q / kWD, part = q - kWD * row;
         const uint8_t* g = W + (size_t)min(n0 + row, a.N - 1) * wrb + (size_t)pair * kPairB + 4 * part;
-        lds_dma4(g, __builtin_amdgcn_readfirstlane(lds_addr(ring + 2 * kAQ + 256 * k)));
+        lds_dma4(g, base + 2 * kAQ + 256 * k);
       }
     }
   };
@@ -169,7 +191,7 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
     dxr = *reinterpret_cast<const float*>(dsrc + (size_t)(2 * pair + par) * kQ8_KBytes);
   };
 
-  v16i I[2], acc[2];
+  v16i I[2], I2[2], acc[2];
   v16f y[2];
 #pragma unroll
   for (int t = 0; t < 2; ++t)
@@ -177,7 +199,7 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
     for (int r = 0; r < 16; ++r) y[t][r] = 0.f;
   const v16i zero = {};
   const int sw = col & 15;
-  const int sb0 = par * kIq2xxsBytes;  // this parity's record within the pair: 0 or 66
+  const int sb0 = par * TT::kRec;  // this parity's record within the pair: 0 or 66 / 74
 
   auto step = [&](int pair, const uint8_t* cur, uint8_t* nxt) {
     __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of this pair have landed
@@ -196,8 +218,47 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
     const float dw = fp16_to_fp32(par ? dword0 >> 16 : dword0 & 0xffffu);
     const int sh = 2 - 2 * par;  // byte offset of group data (rec + 2 + 8g) in its dword
     const uint8_t* gbase = rec + 2 - sh;  // 4-byte aligned
+    // IQ2_XS: the 8 scale bytes at rec + 66 (byte offset 2 - 2 par in its dword)
+    uint32_t scl0 = 0, scl1 = 0;
+    if constexpr (kXs) {
+      const uint8_t* sbase = rec + 66 - sh;  // 4-byte aligned
+      const uint32_t s0w = ld32(sbase), s1w = ld32(sbase + 4), s2w = ld32(sbase + 8);
+      scl0 = __builtin_amdgcn_alignbyte(s1w, s0w, sh);
+      scl1 = __builtin_amdgcn_alignbyte(s2w, s1w, sh);
+    }
 #pragma unroll
     for (int g = 0; g < 8; ++g) {
+      if constexpr (kXs) {
+        const uint32_t w0 = ld32(gbase + 8 * g), w1 = ld32(gbase + 8 * g + 4), w2 = ld32(gbase + 8 * g + 8);
+        // this lane's 16 elements: entries 2kg, 2kg + 1 = one u16 pair
+        const uint32_t ew = kg ? __builtin_amdgcn_alignbyte(w2, w1, sh) : __builtin_amdgcn_alignbyte(w1, w0, sh);
+        const uint32_t e0 = ew & 0xffffu, e1 = ew >> 16;
+        const uint2 g0 = *reinterpret_cast<const uint2*>(tgrid + 8 * (e0 & 511u));
+        const uint2 g1 = *reinterpret_cast<const uint2*>(tgrid + 8 * (e1 & 511u));
+        const uint2 z0 = *reinterpret_cast<const uint2*>(tsign + 8 * (e0 >> 9));
+        const uint2 z1 = *reinterpret_cast<const uint2*>(tsign + 8 * (e1 >> 9));
+        const v4i bv = {(int)apply_signs(g0.x, z0.x), (int)apply_signs(g0.y, z0.y),
+                        (int)apply_signs(g1.x, z1.x), (int)apply_signs(g1.y, z1.y)};
+        const v4i bz = {};
+        const uint32_t sb = ((g < 4 ? scl0 : scl1) >> (8 * (g & 3))) & 0xffu;
+        const int ls_lo = 2 * (int)(sb & 15u) + 1, ls_hi = 2 * (int)(sb >> 4) + 1;
+        const int chunk = (2 * g + kg) ^ sw;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const v4i av = *reinterpret_cast<const v4i*>(AQ + (32 * t + col) * 256 + 16 * chunk);
+          I[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, kg ? bz : bv, zero, 0, 0, 0);
+          I2[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, kg ? bv : bz, zero, 0, 0, 0);
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            int v = __mul24(I[t][r], ls_lo) + __mul24(I2[t][r], ls_hi) + (g == 0 ? 0 : acc[t][r]);
+            pin(v);
+            acc[t][r] = v;
+          }
+        continue;
+      }
       const uint32_t w0 = ld32(gbase + 8 * g), w1 = ld32(gbase + 8 * g + 4), w2 = ld32(gbase + 8 * g + 8);
       const uint32_t idx = __builtin_amdgcn_alignbyte(w1, w0, sh);   // 4 grid indices
       const uint32_t meta = __builtin_amdgcn_alignbyte(w2, w1, sh);  // 4 x 7-bit signs, 4-bit s
@@ -279,25 +340,28 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
 }
 
 
+template <bool kXs = false>
 bool gemm_iq2_ok(const uint8_t* W, const void* Xq, const float* Y, const int8_t* grid,
                  const int8_t* signs, size_t N, size_t K, size_t M, const RowStrides& st) {
   // MFMA path: prefill shapes with an even number of superblocks per row and
   // 4-byte aligned weight rows; the GEMV kernels take everything else
-  const size_t ldw = N > 1 ? st.ldw : K / 256 * kIq2xxsBytes;
+  constexpr size_t kRec = Tile<kXs>::kRec;
+  const size_t ldw = N > 1 ? st.ldw : K / 256 * kRec;
   return M >= 16 && N > 0 && K > 0 && K % 512 == 0 && W != nullptr && Xq != nullptr &&
          Y != nullptr && grid != nullptr && signs != nullptr && aligned(W, 4) && ldw % 4 == 0 &&
          aligned(Xq, 4) && aligned(Y, 4) && N <= (size_t)INT32_MAX && K <= (size_t)INT32_MAX &&
-         M <= (size_t)INT32_MAX && strides_ok(st, K / 256 * kIq2xxsBytes, 2, K, N, N, M) &&
+         M <= (size_t)INT32_MAX && strides_ok(st, K / 256 * kRec, 2, K, N, N, M) &&
          ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT) <= (size_t)INT32_MAX;
 }
 
+template <bool kXs = false>
 void gemm_iq2(const uint8_t* W, const uint8_t* Xq, const int8_t* grid, const int8_t* signs, float* Y,
               size_t N, size_t K, size_t M, const RowStrides& st) {
-  const size_t ldw = N > 1 ? st.ldw : K / 256 * kIq2xxsBytes;
+  const size_t ldw = N > 1 ? st.ldw : K / 256 * Tile<kXs>::kRec;
   GemmArgs ga{W, Xq, grid, signs, Y, (int)N, (int)K, (int)M, ldw, (long long)st.ldy, GroupTiles{}};
   const size_t tiles = ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT);
-  iq2_mfma_gemm<false><<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(ga);
-  check_launch("iq2_mfma_gemm");
+  iq2_mfma_gemm<false, kXs><<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(ga);
+  check_launch(kXs ? "iq2xs_mfma_gemm" : "iq2_mfma_gemm");
 }
 
 }  // namespace
@@ -333,6 +397,22 @@ void mul_mat_iq2_xxs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t
     return decode_iq2_xxs(W, X, Xq, grid, signs, Y, N, K, M, st);
   quantize_q8_k_rows(X, st.ldx, Xq, M, K);
   gemm_iq2(W, Xq, grid, signs, Y, N, K, M, st);
+}
+
+// IQ2_XS: the same GEMM with per-half scales (M >= 16, K % 512 == 0), the GEMV otherwise
+void mul_mat_iq2_xs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid, const int8_t* signs,
+                    float* Y, size_t N, size_t K, size_t M, const RowStrides& st) {
+  if (X == nullptr || !aligned(X, 4) || !gemm_iq2_ok<true>(W, Xq, Y, grid, signs, N, K, M, st))
+    return decode_iq2_xs(W, X, Xq, grid, signs, Y, N, K, M, st);
+  quantize_q8_k_rows(X, st.ldx, Xq, M, K);
+  gemm_iq2<true>(W, Xq, grid, signs, Y, N, K, M, st);
+}
+
+void mul_mat_iq2_xs_quantized(const uint8_t* W, const uint8_t* Xq, const int8_t* grid, const int8_t* signs,
+                              float* Y, size_t N, size_t K, size_t M, const RowStrides& st) {
+  if (!gemm_iq2_ok<true>(W, Xq, Y, grid, signs, N, K, M, st))
+    return decode_quantized(7, W, Xq, grid, signs, Y, N, K, M, st);
+  gemm_iq2<true>(W, Xq, grid, signs, Y, N, K, M, st);
 }
 
 void mul_mat_iq2_xxs_quantized(const uint8_t* W, const uint8_t* Xq, const int8_t* grid,
