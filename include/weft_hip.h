@@ -45,6 +45,14 @@ extern "C" {
 /* No counterpart in the reference (its kernels are synchronous host C). */
 int weft_hip_set_stream(void *stream);   /* hipStream_t; thread-local */
 void *weft_hip_get_stream(void);
+/* Source tile bindings of the calling thread (CompileOptions.meta; no
+ * counterpart in the generated C, where they are compile-time constants):
+ * "NC" = weight rows per workgroup and "MR" = activation rows per pass
+ * (1..4) of the GEMV kernels; 0 unsets.  Returns 1 when the name has a
+ * launch knob here, 0 otherwise (the MFMA GEMMs' 64 x 128 tiles are fixed).
+ * weft_hip_clear_tile_bindings unsets every binding. */
+int weft_hip_set_tile_binding(const char *name, size_t value);
+void weft_hip_clear_tile_bindings(void);
 int weft_hip_get_last_error(void);       /* hipError_t, then cleared */
 const char *weft_hip_error_string(int code);
 int weft_hip_synchronize(void);          /* hipStreamSynchronize(current) */

@@ -113,6 +113,24 @@ def test_invalid_call_records_an_error_without_a_device():
     assert lib.weft_hip_get_last_error() == 0
 
 
+def test_tile_bindings_accept_the_gemv_knobs_only():
+    """NC and MR retile the GEMV launches; other meta names have no gfx950
+    knob (0, no error); a value above INT32_MAX or no name is an error."""
+    lib = _lib.load()
+    try:
+        assert lib.weft_hip_set_tile_binding(b"NC", 64) == 1
+        assert lib.weft_hip_set_tile_binding(b"MR", 2) == 1
+        for name in (b"KC", b"MC", b"NR", b"nc", b""):
+            assert lib.weft_hip_set_tile_binding(name, 8) == 0
+        assert lib.weft_hip_get_last_error() == 0
+        lib.weft_hip_set_tile_binding(b"NC", 1 << 31)
+        assert lib.weft_hip_get_last_error() != 0
+        lib.weft_hip_set_tile_binding(None, 1)
+        assert lib.weft_hip_get_last_error() != 0
+    finally:
+        lib.weft_hip_clear_tile_bindings()
+
+
 # ----------------------------------------------- device variables of the library
 READELF = Path("/opt/rocm/llvm/bin/llvm-readelf")
 OBJCOPY = Path("/opt/rocm/llvm/bin/llvm-objcopy")

@@ -84,3 +84,35 @@ def test_jit_staged_prefill_with_the_reference_tuning_bindings(torch_dev):
     assert np.array_equal(xq_t.cpu().numpy().reshape(m, -1), want_xq)
     e, a = o.mul_mat_f64("q4_k", w, want_xq, n, k, m)
     assert o.within_tolerance(y_t.cpu().numpy(), e, a).all()
+
+
+@pytest.mark.parametrize("definition,fmt", [(K.production_mul_mat_q5_k, "q5_k"),
+                                            (K.production_mul_mat_q4_k_staged, "q4_k")])
+def test_tile_bindings_retile_the_gemv_launches(torch_dev, definition, fmt):
+    """NC (weight rows per workgroup) and MR (activation rows per pass) reach
+    the GEMV kernels: MR = 1 launches one pass per activation row, MR = 4 one
+    per four; the outputs are bit-identical (each output is one wave's dot
+    whatever the tiling) and within the oracle's bar."""
+    from weft_amd import _lib
+    torch, dev = torch_dev
+    n, k, m = 300, 1024, 8  # M < 16: the GEMV path of every prefill entry point
+    w = o.quantize(fmt, o.seeded_normal(65, (n, k), 0.02))
+    x = o.seeded_normal(66, (m, k))
+    outs, launches = [], []
+    for meta in ({"NC": 7, "KC": 512, "MC": 8, "MR": 1, "NR": 2}, {"NC": 64, "KC": 512, "MC": 8, "MR": 4, "NR": 2}):
+        fn = compile(definition, options=CompileOptions(meta=meta))
+        assert dict(fn.metadata["bindings"]) == dict(sorted(meta.items()))
+        xq_t = torch.zeros(m * (k // 256) * 292, dtype=torch.uint8, device=dev)
+        y_t = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+        _lib.launch_log()
+        fn(Buffer(torch.from_numpy(w).to(dev), shape=(n, k), encoding=fmt.upper()),
+           torch.from_numpy(x).to(dev), Buffer(xq_t, shape=(m, k), encoding="Q8_K"), y_t)
+        launches.append([name for name in _lib.launch_log() if "gemv" in name])
+        outs.append(y_t.cpu().numpy())
+        want_xq = o.quantize("q8_k", x)
+        assert np.array_equal(xq_t.cpu().numpy().reshape(m, -1), want_xq)
+        e, a = o.mul_mat_f64(fmt, w, want_xq, n, k, m)
+        assert o.within_tolerance(outs[-1], e, a).all()
+    assert len(launches[0]) == m and len(launches[1]) == m // 4, launches
+    np.testing.assert_array_equal(outs[0], outs[1])
+    assert _lib.load().weft_hip_set_tile_binding(b"NR", 2) == 0  # no GEMV knob

@@ -55,6 +55,10 @@ def load() -> ctypes.CDLL:
             lib.weft_hip_set_stream.argtypes = [ctypes.c_void_p]
             lib.weft_hip_set_stream.restype = ctypes.c_int
             lib.weft_hip_get_stream.restype = ctypes.c_void_p
+            lib.weft_hip_set_tile_binding.argtypes = [ctypes.c_char_p, ctypes.c_size_t]
+            lib.weft_hip_set_tile_binding.restype = ctypes.c_int
+            lib.weft_hip_clear_tile_bindings.argtypes = []
+            lib.weft_hip_clear_tile_bindings.restype = None
             lib.weft_hip_get_last_error.restype = ctypes.c_int
             lib.weft_hip_synchronize.restype = ctypes.c_int
             lib.weft_hip_device_count.restype = ctypes.c_int

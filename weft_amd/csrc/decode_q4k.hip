@@ -519,9 +519,11 @@ void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t*
     return;
   }
   constexpr int NT = 1024;
-  const int mb_max = (int)std::min<size_t>(kMaxRowsPerPass, lds_cap / row_lds);
+  const TileBindings& tb = tile_bindings();
+  int mb_max = (int)std::min<size_t>(kMaxRowsPerPass, lds_cap / row_lds);
+  if (tb.mr > 0) mb_max = std::min(mb_max, tb.mr);
   const int cus = cu_count();
-  const int rows_per_wg = (int)((N + cus - 1) / cus);
+  const int rows_per_wg = tb.nc > 0 ? (int)std::min<size_t>(N, (size_t)tb.nc) : (int)((N + cus - 1) / cus);
   const int grid = (int)((N + rows_per_wg - 1) / rows_per_wg);
   const bool a16 = aligned(W, 16) && (N == 1 || st.ldw % 16 == 0) && (pr == nullptr || pr->w_es % 16 == 0);
   const bool x16 = aligned(X, 16) && (pr == nullptr || (pr->x_s1 % 4 == 0 && pr->x_s2 % 4 == 0));
@@ -558,7 +560,7 @@ void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t*
     a.ldx = st.ldx;
     if (steps == 1) {
       const int wgs = 2 * cus;
-      a.rows_per_wg = (int)((N + wgs - 1) / wgs);
+      a.rows_per_wg = tb.nc > 0 ? rows_per_wg : (int)((N + wgs - 1) / wgs);
       const int g1 = (int)((N + a.rows_per_wg - 1) / a.rows_per_wg);
       each(a, g1, [&](const Q4KArgs& b, dim3 g) {
         q4k_gemv_m1_kernel<1, 1024, 2><<<g, 1024, row_lds, current_stream()>>>(b);
@@ -570,7 +572,7 @@ void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t*
     // so more (smaller) workgroups only add that prologue (measured: 7.8 us
     // at 768 threads x 256 for config 3's W_down, 9.6 us at 2 per CU)
     const int wgs = cus;
-    a.rows_per_wg = (int)((N + wgs - 1) / wgs);
+    a.rows_per_wg = tb.nc > 0 ? rows_per_wg : (int)((N + wgs - 1) / wgs);
     const int g1 = (int)((N + a.rows_per_wg - 1) / a.rows_per_wg);
     const size_t lds = row_lds + (size_t)a.rows_per_wg * steps * sizeof(float);
     if (lds <= lds_cap) {  // else the general kernel below

@@ -669,9 +669,11 @@ void launch(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_
     set_error(hipErrorInvalidValue);
     return;
   }
-  const int mb_max = (int)std::min<size_t>(kMaxRowsPerPass, (cap - fixed) / row_lds);
+  const TileBindings& tb = tile_bindings();
+  int mb_max = (int)std::min<size_t>(kMaxRowsPerPass, (cap - fixed) / row_lds);
+  if (tb.mr > 0) mb_max = std::min(mb_max, tb.mr);
   const int cus = cu_count();
-  const int rows_per_wg = (int)((N + cus - 1) / cus);
+  const int rows_per_wg = tb.nc > 0 ? (int)std::min<size_t>(N, (size_t)tb.nc) : (int)((N + cus - 1) / cus);
   const int grid = (int)((N + rows_per_wg - 1) / rows_per_wg);
   for (size_t m0 = 0; m0 < M; m0 += mb_max) {
     Args a;

@@ -17,6 +17,14 @@ void set_error(hipError_t e);
 void check_launch(const char* kernel = nullptr);
 // The calling thread's recorded error, left in place.
 hipError_t pending_error();
+// The calling thread's source tile bindings (weft_hip_set_tile_binding;
+// 0 = unset): nc = weight rows per workgroup and mr = activation rows per
+// pass of the GEMV kernels.  The MFMA GEMMs' tiles are fixed.
+struct TileBindings {
+  int nc = 0, mr = 0;
+};
+const TileBindings& tile_bindings();
+
 // Compute units of the current device (cached per device).
 int cu_count();
 // Largest dynamic LDS a workgroup may request on the current device.

@@ -19,6 +19,7 @@ namespace {
 thread_local hipStream_t t_stream = nullptr;
 thread_local hipError_t t_error = hipSuccess;
 thread_local std::string t_launch_log;  // kernels launched since the log was last read
+thread_local TileBindings t_tiles;
 
 struct DeviceFacts {
   int cus = 0;
@@ -65,6 +66,8 @@ void check_launch(const char* kernel) {
 
 hipError_t pending_error() { return t_error; }
 
+const TileBindings& tile_bindings() { return t_tiles; }
+
 int cu_count() { return facts().cus; }
 
 size_t max_lds_per_block() { return facts().lds; }
@@ -79,6 +82,25 @@ int weft_hip_set_stream(void* stream) {
 }
 
 void* weft_hip_get_stream(void) { return reinterpret_cast<void*>(weft::t_stream); }
+
+int weft_hip_set_tile_binding(const char* name, size_t value) {
+  if (name == nullptr || value > (size_t)INT32_MAX) {
+    weft::set_error(hipErrorInvalidValue);
+    return 0;
+  }
+  const std::string n(name);
+  if (n == "NC") {
+    weft::t_tiles.nc = (int)value;
+    return 1;
+  }
+  if (n == "MR") {
+    weft::t_tiles.mr = (int)value;
+    return 1;
+  }
+  return 0;  // a binding without a gfx950 launch knob
+}
+
+void weft_hip_clear_tile_bindings(void) { weft::t_tiles = weft::TileBindings{}; }
 
 int weft_hip_get_last_error(void) {
   const hipError_t e = weft::t_error;

@@ -239,6 +239,9 @@ class CompiledKernel:
         self._plan = _AbiPlan(self.metadata, definition, target)
         self._lib = _lib
         self._entry = getattr(_lib.load(), self.metadata["symbol"])
+        # the source bindings, set on the library's calling thread for each
+        # call (weft_hip_set_tile_binding: NC / MR retile the GEMV launches)
+        self._tiles = tuple((name.encode(), value) for name, value in self.metadata["bindings"].items())
         self._lock = threading.RLock()
 
     @property
@@ -251,7 +254,13 @@ class CompiledKernel:
                 raise RuntimeError("the compiled kernel has been closed")
             self.target.check_execution()
             pointers, shapes = self._plan.bind(args, dict(kwargs))
-            self._entry(*map(ctypes.c_void_p, pointers), *shapes)
+            lib = self._lib.load()
+            for name, value in self._tiles:
+                lib.weft_hip_set_tile_binding(name, value)
+            try:
+                self._entry(*map(ctypes.c_void_p, pointers), *shapes)
+            finally:
+                lib.weft_hip_clear_tile_bindings()
             self._lib.check(self.metadata["symbol"])
             if self.synchronize:
                 self._lib.synchronize()
@@ -278,9 +287,9 @@ class _Registry:
             if getattr(options, name) != default:
                 raise CompilationError(f"RISC-V physical binding {name} has no gfx950 meaning")
         # every wl.auto extent needs one concrete binding; other names are
-        # recorded (lib/Target/ConvertWeftToRISCV.cpp:730-745).  The gfx950
-        # kernels' tiles are their own, so a binding names the artifact, it
-        # does not retile it.
+        # recorded (lib/Target/ConvertWeftToRISCV.cpp:730-745).  On gfx950
+        # NC (weight rows per workgroup) and MR (activation rows per pass)
+        # retile the GEMV launches; the MFMA GEMMs keep their 64 x 128 tile.
         missing = [name for name in definition.source_bindings if name not in options.meta]
         if missing:
             raise CompilationError(f"source auto parameter '{missing[0]}' requires one concrete --meta binding")
