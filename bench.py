@@ -74,6 +74,7 @@ CASES = {
     "q6_k_decode": ("production_mul_mat_q6_k_decode", "q6_k", 11008, 4096, 1, "hbm"),
     "q6_k_prefill": ("production_mul_mat_q6_k", "q6_k", 4096, 4096, 512, "mfma"),
     "q5_k_decode": ("production_mul_mat_q5_k_decode", "q5_k", 11008, 4096, 1, "hbm"),
+    "q5_k_prefill": ("production_mul_mat_q5_k", "q5_k", 4096, 4096, 512, "mfma"),
     "nvfp4_decode": ("production_mul_mat_nvfp4_decode", "nvfp4", 11008, 4096, 1, "hbm"),
     "q4_1_decode": ("production_mul_mat_q4_1_decode", "q4_1", 11008, 4096, 1, "hbm"),
     "q4_1_prefill": ("production_mul_mat_q4_1", "q4_1", 4096, 4096, 512, "mfma"),

@@ -74,7 +74,29 @@ def test_decode_q5_k(hip, n, k, m):
     check_mul_mat("q5_k", w, x, xq, y, n, k, m)
 
 
-def test_prefill_q5_k(hip):
-    n, k, m = 512, 4096, 64
+@pytest.mark.parametrize("n,k,m", [(4096, 4096, 512), (512, 4096, 64), (144, 1024, 70), (300, 768, 17),
+                                   (129, 256, 40), (64, 512, 15)])
+def test_prefill_q5_k(hip, n, k, m):
+    """M >= 16 runs the int8-MFMA GEMM (odd superblock counts, ragged weight
+    and token tiles included); M = 15 takes the GEMV."""
     w, x, xq, y = run_mul_mat(hip, "production_mul_mat_q5_k", "q5_k", n, k, m)
+    check_mul_mat("q5_k", w, x, xq, y, n, k, m)
+
+
+def test_prefill_q5_k_extreme_records(hip):
+    """The MFMA GEMM on whole rows of 0 and 31 codes, scales and mins at 63,
+    d = 0 with dmin kept, against activations with an all-zero Q8_K block and
+    an all-zero token."""
+    n, k, m = 160, 2048, 48
+    w = extreme_records(n * k // 256).reshape(n, k // 256, 176)
+    w[5, :, 16:176] = 0x00
+    w[9, :, 16:176] = 0xFF
+    w[9, :, 4:16] = 0xFF
+    w[17, :, 0:2] = 0
+    w[18, 2, 0:4] = 0                         # d = dmin = 0
+    w = np.ascontiguousarray(w.reshape(n, -1))
+    x = acts(m, k, seed=9).copy()
+    x[4, 256:512] = 0.0
+    x[7] = 0.0
+    w, x, xq, y = run_mul_mat(hip, "production_mul_mat_q5_k", "q5_k", n, k, m, w=w, x=x)
     check_mul_mat("q5_k", w, x, xq, y, n, k, m)

@@ -66,7 +66,32 @@ def test_decode_q6_k(hip, n, k, m):
     check_mul_mat("q6_k", w, x, xq, y, n, k, m)
 
 
-def test_prefill_q6_k(hip):
-    n, k, m = 512, 4096, 64
+@pytest.mark.parametrize("n,k,m", [(4096, 4096, 512), (512, 4096, 64), (144, 1024, 70), (129, 2048, 17),
+                                   (300, 768, 40), (64, 512, 15)])
+def test_prefill_q6_k(hip, n, k, m):
+    """M >= 16 with K a multiple of 512 runs the int8-MFMA GEMM (ragged
+    weight and token tiles included); K = 768 and M = 15 take the GEMV."""
     w, x, xq, y = run_mul_mat(hip, "production_mul_mat_q6_k", "q6_k", n, k, m)
+    check_mul_mat("q6_k", w, x, xq, y, n, k, m)
+
+
+def test_prefill_q6_k_extreme_records(hip):
+    """The MFMA GEMM on whole rows of -32 and 31 codes, scales drawn from
+    {-128, 127, -1, 0, 1}, d = 0 and subnormal d, against activations with
+    an all-zero Q8_K block and an all-zero token."""
+    n, k, m = 160, 2048, 48
+    rng = np.random.default_rng(29)
+    w = extreme_records(n * k // 256).reshape(n, k // 256, 210)
+    d = (rng.standard_normal((n, k // 256)) * 1e-2).astype(np.float16)
+    w[:, :, 208:210] = d.view(np.uint8).reshape(n, k // 256, 2)
+    w[5, :, :192] = 0x00                      # q = -32 everywhere
+    w[9, :, :192] = 0xFF                      # q = 31 everywhere
+    w[9, :, 192:208] = np.array(-128, np.int8).view(np.uint8)
+    w[17, 3, 208:210] = 0                     # d = 0
+    w[18, :, 208:210] = np.array([1, 0], np.uint8)  # smallest subnormal d
+    w = np.ascontiguousarray(w.reshape(n, -1))
+    x = acts(m, k, seed=9).copy()
+    x[4, 256:512] = 0.0
+    x[7] = 0.0
+    w, x, xq, y = run_mul_mat(hip, "production_mul_mat_q6_k", "q6_k", n, k, m, w=w, x=x)
     check_mul_mat("q6_k", w, x, xq, y, n, k, m)

@@ -822,13 +822,11 @@ void production_mul_mat_q6_k_decode(const uint8_t* W, const float* X, uint8_t* X
   weft::decode_q6_k(W, X, Xq, Y, N, K, M, weft::packed(K / 256 * weft::kQ6_KBytes, K, N));
 }
 
-// Q6_K prefill: the GEMV kernel at every M (the scales are per 16 elements
-// and int8 wide, so an exact int8-MFMA form needs the scaled weights split
-// into two operands per element; not built yet)
+// Q6_K mul_mat: the int8-MFMA GEMM for prefill shapes, the GEMV otherwise
 void production_mul_mat_q6_k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N,
                              size_t K, size_t M) {
   if (X == nullptr || Xq == nullptr) return weft::set_error(hipErrorInvalidValue);
-  weft::decode_q6_k(W, X, Xq, Y, N, K, M, weft::packed(K / 256 * weft::kQ6_KBytes, K, N));
+  weft::mul_mat_q6k(W, X, Xq, Y, N, K, M, weft::packed(K / 256 * weft::kQ6_KBytes, K, N));
 }
 
 void production_mul_mat_nvfp4_decode(const uint8_t* W, const float* X, uint8_t* Xq,
@@ -858,11 +856,11 @@ void production_mul_mat_q5_k_decode(const uint8_t* W, const float* X, uint8_t* X
   weft::decode_q5_k(W, X, Xq, Y, N, K, M, weft::packed(K / 256 * weft::kQ5_KBytes, K, N));
 }
 
-// Q5_K prefill: the GEMV kernel at every M (no MFMA form yet)
+// Q5_K mul_mat: the int8-MFMA GEMM for prefill shapes, the GEMV otherwise
 void production_mul_mat_q5_k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N,
                              size_t K, size_t M) {
   if (X == nullptr || Xq == nullptr) return weft::set_error(hipErrorInvalidValue);
-  weft::decode_q5_k(W, X, Xq, Y, N, K, M, weft::packed(K / 256 * weft::kQ5_KBytes, K, N));
+  weft::mul_mat_q5k(W, X, Xq, Y, N, K, M, weft::packed(K / 256 * weft::kQ5_KBytes, K, N));
 }
 
 void quantized_vec_dot_q5_k_q8_k(const uint8_t* W, const uint8_t* X, float* Y, size_t K) {

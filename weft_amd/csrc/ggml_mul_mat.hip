@@ -301,8 +301,8 @@ hipError_t mul_mat(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1, const
         switch (s0->type) {
           case WEFT_GGML_TYPE_Q4_0: mul_mat_q4_0(W, X, Xq, Y, n, k, m, st); break;
           case WEFT_GGML_TYPE_Q4_K: mul_mat_q4k(W, X, Xq, Y, n, k, m, st); break;
-          case WEFT_GGML_TYPE_Q6_K: decode_q6_k(W, X, Xq, Y, n, k, m, st); break;
-          case WEFT_GGML_TYPE_Q5_K: decode_q5_k(W, X, Xq, Y, n, k, m, st); break;
+          case WEFT_GGML_TYPE_Q6_K: mul_mat_q6k(W, X, Xq, Y, n, k, m, st); break;
+          case WEFT_GGML_TYPE_Q5_K: mul_mat_q5k(W, X, Xq, Y, n, k, m, st); break;
           case WEFT_GGML_TYPE_NVFP4:
             decode_nvfp4(W, X, Xq, tab->codebook, tab->ue4m3, Y, n, k, m, st);
             break;
@@ -319,8 +319,8 @@ hipError_t mul_mat(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1, const
         switch (s0->type) {
           case WEFT_GGML_TYPE_Q4_0: decode_quantized(0, W, src1, nullptr, nullptr, Y, n, k, m, st); break;
           case WEFT_GGML_TYPE_Q4_K: mul_mat_q4k_quantized(W, src1, Y, n, k, m, st); break;
-          case WEFT_GGML_TYPE_Q6_K: decode_quantized(3, W, src1, nullptr, nullptr, Y, n, k, m, st); break;
-          case WEFT_GGML_TYPE_Q5_K: decode_quantized(4, W, src1, nullptr, nullptr, Y, n, k, m, st); break;
+          case WEFT_GGML_TYPE_Q6_K: mul_mat_q6k_quantized(W, src1, Y, n, k, m, st); break;
+          case WEFT_GGML_TYPE_Q5_K: mul_mat_q5k_quantized(W, src1, Y, n, k, m, st); break;
           case WEFT_GGML_TYPE_NVFP4:
             decode_quantized(5, W, src1, tab->codebook, tab->ue4m3, Y, n, k, m, st);
             break;
@@ -444,7 +444,15 @@ hipError_t mul_mat_id(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1,
         }
         break;
       case WEFT_GGML_TYPE_Q6_K:
-      case WEFT_GGML_TYPE_Q5_K:
+      case WEFT_GGML_TYPE_Q5_K: {
+        const bool q6 = s0->type == WEFT_GGML_TYPE_Q6_K;
+        if (mul_mat_id_kq_grouped_ok(q6, W, xq_bytes, Y, n, k, st, pr, n_pairs, ws, ws_bytes)) {
+          quantize_q8k();
+          mul_mat_id_kq_grouped(q6, W, xq, Y, n, k, st, pr, n_pairs, ws);
+          return pending_error();
+        }
+        break;
+      }
       case WEFT_GGML_TYPE_NVFP4:
       case WEFT_GGML_TYPE_Q4_1:
       case WEFT_GGML_TYPE_IQ2_XS:

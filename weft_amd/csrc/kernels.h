@@ -160,6 +160,23 @@ void mul_mat_iq2_xxs_quantized(const uint8_t* W, const uint8_t* Xq, const int8_t
                                const int8_t* signs, float* Y, size_t N, size_t K, size_t M,
                                const RowStrides& st);
 
+// Q6_K / Q5_K mul_mat for any M: int8-MFMA GEMM for prefill shapes, GEMV
+// otherwise; _quantized: over an already quantized Q8_K activation.
+void mul_mat_q6k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K, size_t M,
+                 const RowStrides& st);
+void mul_mat_q5k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K, size_t M,
+                 const RowStrides& st);
+void mul_mat_q6k_quantized(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K, size_t M,
+                           const RowStrides& st);
+void mul_mat_q5k_quantized(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K, size_t M,
+                           const RowStrides& st);
+// Q6_K (q6) / Q5_K MUL_MAT_ID on the grouped MFMA GEMM over quantized Q8_K rows
+bool mul_mat_id_kq_grouped_ok(bool q6, const uint8_t* W, size_t xq_bytes, const float* Y, size_t N, size_t K,
+                              const RowStrides& st, const PairArgs& pr, int n_pairs, const void* ws,
+                              size_t ws_bytes);
+void mul_mat_id_kq_grouped(bool q6, const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K,
+                           const RowStrides& st, const PairArgs& pr, int n_pairs, void* ws);
+
 // Activation quantizers over K contiguous values, and over M rows of K
 // values ldx floats apart (records written contiguously).
 void quantize_q8_k(const float* X, uint8_t* Y, size_t K);
