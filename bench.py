@@ -76,6 +76,7 @@ CASES = {
     "q5_k_decode": ("production_mul_mat_q5_k_decode", "q5_k", 11008, 4096, 1, "hbm"),
     "q5_k_prefill": ("production_mul_mat_q5_k", "q5_k", 4096, 4096, 512, "mfma"),
     "nvfp4_decode": ("production_mul_mat_nvfp4_decode", "nvfp4", 11008, 4096, 1, "hbm"),
+    "nvfp4_prefill": ("production_mul_mat_nvfp4", "nvfp4", 4096, 4096, 512, "mfma"),
     "q4_1_decode": ("production_mul_mat_q4_1_decode", "q4_1", 11008, 4096, 1, "hbm"),
     "q4_1_prefill": ("production_mul_mat_q4_1", "q4_1", 4096, 4096, 512, "mfma"),
     "iq2_xs_decode": ("production_mul_mat_iq2_xs", "iq2_xs", 4096, 4096, 1, "hbm"),

@@ -74,7 +74,24 @@ def test_decode_nvfp4(hip, n, k, m):
     check_mul_mat("nvfp4", w, x, xq, y, n, k, m)
 
 
-def test_prefill_nvfp4(hip):
-    n, k, m = 512, 4096, 64
+@pytest.mark.parametrize("n,k,m", [(4096, 4096, 512), (512, 4096, 64), (144, 768, 70), (129, 256, 17),
+                                   (300, 320, 40), (64, 512, 15)])
+def test_prefill_nvfp4(hip, n, k, m):
+    """M >= 16 with K a multiple of 256 runs the int8-MFMA GEMM (ragged
+    weight and token tiles included); K = 320 and M = 15 take the GEMV."""
     w, x, xq, y = run_mul_mat(hip, "production_mul_mat_nvfp4", "nvfp4", n, k, m)
+    check_mul_mat("nvfp4", w, x, xq, y, n, k, m)
+
+
+def test_prefill_nvfp4_extreme_records(hip):
+    """The MFMA GEMM on rows that cycle through all 256 UE4M3 scale bytes
+    (0x00 and 0x7F read as zero, subnormals, 448) and every code, against
+    activations with an all-zero Q8_0 block and an all-zero token."""
+    n, k, m = 128, 4096, 40
+    recs = extreme_records()                  # 64 records = one row of K = 4096
+    w = np.stack([np.roll(recs, 5 * r, axis=0) for r in range(n)]).reshape(n, -1)
+    x = acts(m, k, seed=9).copy()
+    x[4, 64:96] = 0.0
+    x[7] = 0.0
+    w, x, xq, y = run_mul_mat(hip, "production_mul_mat_nvfp4", "nvfp4", n, k, m, w=w, x=x)
     check_mul_mat("nvfp4", w, x, xq, y, n, k, m)

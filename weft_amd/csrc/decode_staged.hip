@@ -837,10 +837,11 @@ void production_mul_mat_nvfp4_decode(const uint8_t* W, const float* X, uint8_t* 
                      weft::packed(K / 64 * weft::kNvfp4Bytes, K, N));
 }
 
-// NVFP4 prefill: the GEMV kernel at every M (no MFMA form yet)
+// NVFP4 mul_mat: the int8-MFMA GEMM for prefill shapes, the GEMV otherwise
 void production_mul_mat_nvfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
                               const float* scale, float* Y, size_t N, size_t K, size_t M) {
-  production_mul_mat_nvfp4_decode(W, X, Xq, codebook, scale, Y, N, K, M);
+  if (X == nullptr || Xq == nullptr) return weft::set_error(hipErrorInvalidValue);
+  weft::mul_mat_nvfp4(W, X, Xq, codebook, scale, Y, N, K, M, weft::packed(K / 64 * weft::kNvfp4Bytes, K, N));
 }
 
 void quantized_vec_dot_nvfp4_q8_0(const uint8_t* W, const uint8_t* X, const int8_t* codebook,

@@ -304,7 +304,7 @@ hipError_t mul_mat(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1, const
           case WEFT_GGML_TYPE_Q6_K: mul_mat_q6k(W, X, Xq, Y, n, k, m, st); break;
           case WEFT_GGML_TYPE_Q5_K: mul_mat_q5k(W, X, Xq, Y, n, k, m, st); break;
           case WEFT_GGML_TYPE_NVFP4:
-            decode_nvfp4(W, X, Xq, tab->codebook, tab->ue4m3, Y, n, k, m, st);
+            mul_mat_nvfp4(W, X, Xq, tab->codebook, tab->ue4m3, Y, n, k, m, st);
             break;
           case WEFT_GGML_TYPE_IQ2_XXS:
             mul_mat_iq2_xxs(W, X, Xq, tab->grid, tab->signs, Y, n, k, m, st);
@@ -453,14 +453,13 @@ hipError_t mul_mat_id(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1,
         }
         break;
       }
-      case WEFT_GGML_TYPE_NVFP4:
       case WEFT_GGML_TYPE_Q4_1:
       case WEFT_GGML_TYPE_IQ2_XS:
         break;  // no grouped GEMM: the pair GEMV below
-      default: {  // Q4_0 / MXFP4: the GEMMs read a planar activation quantized from X
-        const int fmt = s0->type == WEFT_GGML_TYPE_Q4_0 ? 0 : 1;
+      default: {  // Q4_0 / MXFP4 / NVFP4: the GEMMs read a planar activation quantized from X
+        const int fmt = s0->type == WEFT_GGML_TYPE_Q4_0 ? 0 : s0->type == WEFT_GGML_TYPE_MXFP4 ? 1 : 2;
         const int8_t* cb = fmt ? tab->codebook : nullptr;
-        const float* sc = fmt ? tab->scale : nullptr;
+        const float* sc = fmt == 1 ? tab->scale : fmt == 2 ? tab->ue4m3 : nullptr;
         if (quantize && mul_mat_id_q80_grouped_ok(fmt, W, X, xq_out, Y, n, k, st, pr, n_pairs,
                                                   (int)n_tok, ws, ws_bytes, cb, sc)) {
           mul_mat_id_q80_grouped(fmt, W, X, xq_out, Y, n, k, st, pr, n_pairs, (int)n_tok, ws, cb, sc);

@@ -90,7 +90,7 @@ bool mul_mat_id_q4k_grouped_ok(const uint8_t* W, size_t xq_bytes, const float* Y
                                size_t ws_bytes);
 void mul_mat_id_q4k_grouped(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K,
                             const RowStrides& st, const PairArgs& pr, int n_pairs, void* ws);
-// Q4_0 (fmt 0) / MXFP4 (fmt 1) MUL_MAT_ID on the grouped MFMA GEMMs: src1
+// Q4_0 (fmt 0) / MXFP4 (fmt 1) / NVFP4 (fmt 2) MUL_MAT_ID on the grouped MFMA GEMMs: src1
 // rows (token t, row j) at t * pr.x_s2 + j * pr.x_s1 floats, quantized into
 // Xq (planar for the GEMM, GGML's records at the end).
 bool mul_mat_id_q80_grouped_ok(int fmt, const uint8_t* W, const float* X, const uint8_t* Xq, const float* Y,
@@ -160,6 +160,9 @@ void mul_mat_iq2_xxs_quantized(const uint8_t* W, const uint8_t* Xq, const int8_t
                                const int8_t* signs, float* Y, size_t N, size_t K, size_t M,
                                const RowStrides& st);
 
+// NVFP4 mul_mat for any M: the Q8_0 int8-MFMA GEMM for prefill shapes, GEMV otherwise
+void mul_mat_nvfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
+                   const float* ue4m3, float* Y, size_t N, size_t K, size_t M, const RowStrides& st);
 // Q6_K / Q5_K mul_mat for any M: int8-MFMA GEMM for prefill shapes, GEMV
 // otherwise; _quantized: over an already quantized Q8_K activation.
 void mul_mat_q6k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K, size_t M,

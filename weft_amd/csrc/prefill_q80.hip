@@ -1,10 +1,14 @@
-// Q4_0 / MXFP4 x Q8_0 prefill GEMM on int8 MFMA (production_mul_mat_q4_0,
-// examples/kernels/mul_mat/q4_0.py:9-30; production_mul_mat_mxfp4,
-// examples/kernels/mul_mat/mxfp4.py:10-35).
+// Q4_0 / MXFP4 / NVFP4 x Q8_0 and Q4_1 x Q8_1 prefill GEMMs on int8 MFMA
+// (production_mul_mat_q4_0, examples/kernels/mul_mat/q4_0.py:9-30;
+// production_mul_mat_mxfp4, mxfp4.py:10-35; production_mul_mat_nvfp4,
+// nvfp4.py:10-43; production_mul_mat_q4_1, q4_1.py:9-10).
 //
 //   Y[m, n] = sum_b dx[m,b] * ws[n,b] * I[m,n,b],   I = sum_{k in b} q8[m,k] * w[n,k]
 //   Q4_0:  w = q - 8,            ws = fp16 d        (ggml-cpu/quants.c:174-208)
 //   MXFP4: w = codebook[q],      ws = scale[e]      (ggml-cpu/quants.c:247-276)
+//   NVFP4: w = codebook[q], a UE4M3 scale per 16-element half of the block
+//          (ggml-cpu/quants.c:279-313): the block's MFMA runs twice with the
+//          weight operand of one half, Y += dx * (ws_lo I_lo + ws_hi I_hi)
 // One v_mfma_i32_32x32x32_i8 per 32x32 tile and 32-block gives I exactly; the
 // two per-block scales are applied in fp32 on VALU (3 instructions per
 // output and block), which is what bounds these kernels.
@@ -41,7 +45,7 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
-enum class WFmt { Q4_0, MXFP4, Q4_1 };
+enum class WFmt { Q4_0, MXFP4, Q4_1, NVFP4 };
 
 template <WFmt F>
 struct WTraits;
@@ -59,6 +63,13 @@ template <>
 struct WTraits<WFmt::Q4_1> {
   static constexpr int kRec = kQ4_1Bytes;  // 20
   static constexpr int kHdr = 4;           // fp16 d, fp16 m, then 16 nibble bytes
+};
+// NVFP4: a 36-byte record covers two 32-blocks (4 UE4M3 scales, then 8 code
+// bytes per 16-element sub-block); kRec is the bytes per 32 elements
+template <>
+struct WTraits<WFmt::NVFP4> {
+  static constexpr int kRec = kNvfp4Bytes / 2;  // 18
+  static constexpr int kHdr = 4;
 };
 
 // Planar activation row bytes: K int8, K/32 fp16 scales d, and for Q4_1's
@@ -127,11 +138,15 @@ __device__ __forceinline__ uint32_t lookup16(uint32_t n, uint32_t c0, uint32_t c
 }
 
 // LDS bytes of the int8 GEMM body: two ring slots of two stages, the token
-// scales (fp32), Q4_1's token block sums (fp16), the MXFP4 scale table
+// scales (fp32), Q4_1's token block sums (fp16), the MXFP4 / UE4M3 scale table
+template <WFmt F>
+constexpr bool has_table() {
+  return F == WFmt::MXFP4 || F == WFmt::NVFP4;
+}
 template <WFmt F>
 constexpr int q80_lds_bytes() {
   return 4 * (kAQ + kNT * 8 * WTraits<F>::kRec) + 2 * 2 * 8 * kMT * 4 +
-         (F == WFmt::Q4_1 ? 2 * 2 * 8 * kMT * 2 : 0) + (F == WFmt::MXFP4 ? 256 * 4 : 0);
+         (F == WFmt::Q4_1 ? 2 * 2 * 8 * kMT * 2 : 0) + (has_table<F>() ? 256 * 4 : 0);
 }
 
 template <WFmt F, bool kGroup>
@@ -156,7 +171,7 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
   float* scl = reinterpret_cast<float*>(lds + 4 * kStage) + 2 * 2 * 8 * kMT;
   static_assert(q80_lds_bytes<F>() == 4 * kStage + 2 * 2 * 8 * kMT * 4 +
                                           (F == WFmt::Q4_1 ? 2 * 2 * 8 * kMT * 2 : 0) +
-                                          (F == WFmt::MXFP4 ? 256 * 4 : 0),
+                                          (has_table<F>() ? 256 * 4 : 0),
                 "LDS carve");
 
   const int tid = threadIdx.x;
@@ -195,7 +210,7 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
   };
 
   uint32_t c0 = 0, c1 = 0, c2 = 0, c3 = 0;
-  if constexpr (F == WFmt::MXFP4) {
+  if constexpr (has_table<F>()) {
     // int8[16] codebook at any alignment: four little-endian words
     uint32_t w[4];
 #pragma unroll
@@ -280,6 +295,41 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
       const uint16_t* sxs = &ast[pair & 1][par][0];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
+        if constexpr (F == WFmt::NVFP4) {
+          // block j is half j % 2 of record j / 2: sub-blocks 2 (j % 2) + kg;
+          // this lane's 16 elements are the low nibbles of its sub-block's 8
+          // code bytes, then their high nibbles
+          const uint8_t* rec = wrow + 36 * (j >> 1);
+          const uint32_t sc4 = ld32(rec);
+          const uint32_t u0 = ld32(rec + 4 + 16 * (j & 1) + 8 * kg), u1 = ld32(rec + 8 + 16 * (j & 1) + 8 * kg);
+          const float wlo = scl[(sc4 >> (16 * (j & 1))) & 0xffu], whi = scl[(sc4 >> (16 * (j & 1) + 8)) & 0xffu];
+          const v4i bv = {(int)lookup16(u0 & 0x0f0f0f0fu, c0, c1, c2, c3),
+                          (int)lookup16(u1 & 0x0f0f0f0fu, c0, c1, c2, c3),
+                          (int)lookup16((u0 >> 4) & 0x0f0f0f0fu, c0, c1, c2, c3),
+                          (int)lookup16((u1 >> 4) & 0x0f0f0f0fu, c0, c1, c2, c3)};
+          const v4i bz = {};
+          const int chunk = (2 * j + kg) ^ sw;
+          v16i I2[2];
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const v4i av = *reinterpret_cast<const v4i*>(AQ + (32 * t + col) * 256 + 16 * chunk);
+            I[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, kg ? bz : bv, zero, 0, 0, 0);
+            I2[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, kg ? bv : bz, zero, 0, 0, 0);
+          }
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+              const float4 d4 = *reinterpret_cast<const float4*>(dxs + j * kMT + 32 * t + 8 * r4 + 4 * kg);
+              const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                const int r = 4 * r4 + q;
+                y[t][r] += dv[q] * (wlo * (float)I[t][r] + whi * (float)I2[t][r]);
+              }
+            }
+          continue;
+        }
         // raw record j of this lane's weight row: header, then 16 nibble bytes
         const int off = T::kRec * j + T::kHdr;  // first nibble byte
         const int sh = off & 3, b4 = off - sh;
@@ -844,7 +894,7 @@ bool prefill_q80(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* co
       !strides_ok(st, rb, 1, K, N, N, M) ||
       ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT) > (size_t)INT32_MAX)
     return false;
-  if (F == WFmt::MXFP4 && (codebook == nullptr || scale == nullptr)) return false;
+  if (has_table<F>() && (codebook == nullptr || scale == nullptr)) return false;
   const size_t ldx = M > 1 ? st.ldx : K;
   planar_pass<F>(X, ldx, Xq, M, K, codebook, scale);
   const size_t tiles = ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT);
@@ -854,7 +904,7 @@ bool prefill_q80(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* co
   } else {
     q80_mfma_gemm<F, false><<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(ga);
   }
-  check_launch(F == WFmt::MXFP4 ? "mxfp4_gemm" : "q80_mfma_gemm");
+  check_launch(F == WFmt::MXFP4 ? "mxfp4_gemm" : F == WFmt::NVFP4 ? "nvfp4_mfma_gemm" : "q80_mfma_gemm");
   // Xq ends in GGML's record layout
   if constexpr (F == WFmt::Q4_1)
     quantize_q8_1_rows(X, ldx, Xq, M, K);
@@ -865,14 +915,14 @@ bool prefill_q80(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* co
 
 }  // namespace
 
-// MUL_MAT_ID on the grouped GEMMs (Q4_0: fmt 0, MXFP4: fmt 1).  X rows
+// MUL_MAT_ID on the grouped GEMMs (Q4_0: fmt 0, MXFP4: fmt 1, NVFP4: fmt 2).  X rows
 // (token t, row j) at t * x_s2 + j * x_s1 floats are quantized into Xq
 // planar, then in GGML's records after the GEMM, as the dense path does.
 bool mul_mat_id_q80_grouped_ok(int fmt, const uint8_t* W, const float* X, const uint8_t* Xq, const float* Y,
                                size_t N, size_t K, const RowStrides& st, const PairArgs& pr, int n_pairs,
                                int n_tok, const void* ws, size_t ws_bytes, const int8_t* codebook,
                                const float* scale) {
-  const size_t rb = K / 32 * (fmt == 0 ? kQ4_0Bytes : kMxfp4Bytes);
+  const size_t rb = K / 32 * (fmt == 0 ? kQ4_0Bytes : fmt == 1 ? kMxfp4Bytes : kNvfp4Bytes / 2);
   const size_t ldw = N > 1 ? st.ldw : rb;
   const size_t xq_bytes = (size_t)n_tok * pr.ne11 * (K / 32) * kQ8_0Bytes;
   return N > 0 && K > 0 && n_pairs > 0 && K % 256 == 0 && X != nullptr && aligned(X, 4) &&
@@ -887,7 +937,7 @@ bool mul_mat_id_q80_grouped_ok(int fmt, const uint8_t* W, const float* X, const 
 void mul_mat_id_q80_grouped(int fmt, const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N,
                             size_t K, const RowStrides& st, const PairArgs& pr, int n_pairs, int n_tok,
                             void* ws, const int8_t* codebook, const float* scale) {
-  const size_t rb = K / 32 * (fmt == 0 ? kQ4_0Bytes : kMxfp4Bytes);
+  const size_t rb = K / 32 * (fmt == 0 ? kQ4_0Bytes : fmt == 1 ? kMxfp4Bytes : kNvfp4Bytes / 2);
   const size_t rows = (size_t)n_tok * pr.ne11, xs = K + K / 16;
   // rows (t, j) of X at t * x_s2 + j * x_s1: one pass when they are evenly
   // spaced, else one per token
@@ -898,19 +948,21 @@ void mul_mat_id_q80_grouped(int fmt, const uint8_t* W, const float* X, uint8_t* 
       pass(X + (size_t)t * pr.x_s2, (size_t)pr.x_s1, Xq + (size_t)t * pr.ne11 * row_bytes, (size_t)pr.ne11);
   };
   each_plane([&](const float* x, size_t l, uint8_t* xp, size_t m) {
-    if (fmt == 0)
-      planar_pass<WFmt::Q4_0>(x, l, xp, m, K, nullptr, nullptr);
-    else
+    if (fmt == 1)
       planar_pass<WFmt::MXFP4>(x, l, xp, m, K, codebook, scale);
+    else
+      planar_pass<WFmt::Q4_0>(x, l, xp, m, K, nullptr, nullptr);  // the plain int8 planar layout
   }, xs);
   const MoeGroups g = moe_group(pr, n_pairs, ws);
   GemmArgs ga{W, Xq, codebook, scale, Y, (int)N, (int)K, kMT, N > 1 ? st.ldw : rb, 0, group_tiles(g, pr)};
   const size_t wgs = (size_t)g.tmax * ((N + kNT - 1) / kNT);
   if (fmt == 0)
     q80_mfma_gemm<WFmt::Q4_0, true><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(ga);
-  else
+  else if (fmt == 1)
     mxfp4_gemm<true><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(ga);
-  check_launch(fmt == 0 ? "q80_mfma_gemm" : "mxfp4_gemm");
+  else
+    q80_mfma_gemm<WFmt::NVFP4, true><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(ga);
+  check_launch(fmt == 0 ? "q80_mfma_gemm" : fmt == 1 ? "mxfp4_gemm" : "nvfp4_mfma_gemm");
   // Xq ends in GGML's record layout
   each_plane([&](const float* x, size_t l, uint8_t* xq, size_t m) { quantize_q8_0_rows(x, l, xq, m, K); },
              (K / 32) * kQ8_0Bytes);
@@ -930,6 +982,14 @@ void mul_mat_q4_1(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_
   if (W == nullptr || X == nullptr || Xq == nullptr || Y == nullptr ||
       !prefill_q80<WFmt::Q4_1>(W, X, Xq, nullptr, nullptr, Y, N, K, M, st))
     decode_q4_1(W, X, Xq, Y, N, K, M, st);
+}
+
+void mul_mat_nvfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
+                   const float* ue4m3, float* Y, size_t N, size_t K, size_t M, const RowStrides& st) {
+  if (N == 0 || M == 0 || K == 0) return decode_nvfp4(W, X, Xq, codebook, ue4m3, Y, N, K, M, st);
+  if (W == nullptr || X == nullptr || Xq == nullptr || Y == nullptr ||
+      !prefill_q80<WFmt::NVFP4>(W, X, Xq, codebook, ue4m3, Y, N, K, M, st))
+    decode_nvfp4(W, X, Xq, codebook, ue4m3, Y, N, K, M, st);
 }
 
 void mul_mat_mxfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
