@@ -20,11 +20,19 @@ from weft_amd import ggml as G
 pytestmark = pytest.mark.gpu
 
 TYPE = {"q4_0": G.Q4_0, "q4_k": G.Q4_K, "iq2_xxs": G.IQ2_XXS, "mxfp4": G.MXFP4, "q6_k": G.Q6_K,
-        "q5_k": G.Q5_K, "nvfp4": G.NVFP4}
+        "q5_k": G.Q5_K, "nvfp4": G.NVFP4, "q4_1": G.Q4_1, "iq2_xs": G.IQ2_XS}
 VDT = {"q4_0": G.Q8_0, "mxfp4": G.Q8_0, "q4_k": G.Q8_K, "iq2_xxs": G.Q8_K, "q6_k": G.Q8_K,
-       "q5_k": G.Q8_K, "nvfp4": G.Q8_0}
+       "q5_k": G.Q8_K, "nvfp4": G.Q8_0, "q4_1": G.Q8_1, "iq2_xs": G.Q8_K}
 FMTS = list(TYPE)
 NAN = 0x7FC00001  # a quiet NaN the kernels never produce
+
+
+def make_weights(fmt, n, k, seed):
+    """GGML-quantized N(0, 0.02) rows; IQ2_XS (no quantizer restated) as
+    random records."""
+    if fmt == "iq2_xs":
+        return o.random_records(fmt, n, k, seed=seed)
+    return o.quantize(fmt, o.seeded_normal(seed, (n, k), 0.02))
 
 
 def run(hip, fmt, k, n, m, planes0=(1, 1), planes1=(1, 1), pad_w=0, pad_x=0, pad_y=0,
@@ -36,8 +44,7 @@ def run(hip, fmt, k, n, m, planes0=(1, 1), planes1=(1, 1), pad_w=0, pad_x=0, pad
     act = o.ACT_OF[fmt]
     rq = o.record_bytes(act, k)
     # src0: ne03 x ne02 planes of n rows, each row followed by pad_w bytes
-    w = np.stack([o.quantize(fmt, o.seeded_normal(seed + p, (n, k), 0.02))
-                  for p in range(ne02 * ne03)]).reshape(ne03, ne02, n, rb)
+    w = np.stack([make_weights(fmt, n, k, seed + p) for p in range(ne02 * ne03)]).reshape(ne03, ne02, n, rb)
     w_host = np.full((ne03, ne02, n, rb + pad_w), 0x5A, np.uint8)
     w_host[..., :rb] = w
     x = o.seeded_normal(seed + 100, (ne13, ne12, m, k))
@@ -129,7 +136,7 @@ def run_id(hip, fmt, k, n, n_as, n_ids, ne11, n_tok, ids, pad_w=0, pad_x=0, preq
     rb = o.record_bytes(fmt, k)
     act = o.ACT_OF[fmt]
     rq = o.record_bytes(act, k)
-    w = np.stack([o.quantize(fmt, o.seeded_normal(seed + e, (n, k), 0.02)) for e in range(n_as)])
+    w = np.stack([make_weights(fmt, n, k, seed + e) for e in range(n_as)])
     w_host = np.full((n_as, n, rb + pad_w), 0x5A, np.uint8)
     w_host[..., :rb] = w
     x = o.seeded_normal(seed + 500, (n_tok, ne11, k))
@@ -202,15 +209,21 @@ def test_mul_mat_id_prequantized_and_strided(hip, fmt):
 def test_mul_mat_id_grouped_gemm(hip, fmt, ne11, prequant):
     """Many pairs per expert: the device groups the pairs by expert and the
     grouped MFMA GEMMs run them (ragged tiles, one expert unused, invalid ids
-    skipped).  A pre-quantized Q8_0 src1 takes the pair GEMV (the Q4_0 / MXFP4
-    GEMMs read a planar activation quantized from F32)."""
+    skipped).  A pre-quantized Q8_0 / Q8_1 src1 takes the pair GEMV (the
+    Q4_0 / MXFP4 / NVFP4 / Q4_1 GEMMs read a planar activation quantized from
+    F32); the launch log shows which ran."""
+    from weft_amd import _lib
     rng = np.random.default_rng(5)
     n_tok, n_ids, n_as = 70, 4, 8
     ids = rng.integers(0, n_as - 1, size=(n_tok, n_ids))  # expert 7 never chosen
     ids[3, 2] = -1
     ids[40, 0] = n_as
+    _lib.launch_log()
     run_id(hip, fmt, 1024, 300, n_as, n_ids, ne11, n_tok, ids, pad_w=16,
            pad_x=0 if prequant else 4, prequant=prequant)
+    launched = _lib.launch_log()
+    gemv = prequant and o.ACT_OF[fmt] in ("q8_0", "q8_1")
+    assert any("gemm" in name for name in launched) != gemv, launched
 
 
 @pytest.mark.parametrize("k", [8192, 11008])

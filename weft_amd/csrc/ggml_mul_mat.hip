@@ -436,13 +436,17 @@ hipError_t mul_mat_id(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1,
         }
         break;
       case WEFT_GGML_TYPE_IQ2_XXS:
-        if (mul_mat_id_iq2_grouped_ok(W, xq_bytes, Y, tab->grid, tab->signs, n, k, st, pr, n_pairs, ws,
+      case WEFT_GGML_TYPE_IQ2_XS: {
+        const bool xs = s0->type == WEFT_GGML_TYPE_IQ2_XS;
+        const int8_t* grid = xs ? tab->grid_xs : tab->grid;
+        if (mul_mat_id_iq2_grouped_ok(xs, W, xq_bytes, Y, grid, tab->signs, n, k, st, pr, n_pairs, ws,
                                       ws_bytes)) {
           quantize_q8k();
-          mul_mat_id_iq2_grouped(W, xq, tab->grid, tab->signs, Y, n, k, st, pr, n_pairs, ws);
+          mul_mat_id_iq2_grouped(xs, W, xq, grid, tab->signs, Y, n, k, st, pr, n_pairs, ws);
           return pending_error();
         }
         break;
+      }
       case WEFT_GGML_TYPE_Q6_K:
       case WEFT_GGML_TYPE_Q5_K: {
         const bool q6 = s0->type == WEFT_GGML_TYPE_Q6_K;
@@ -453,12 +457,12 @@ hipError_t mul_mat_id(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1,
         }
         break;
       }
-      case WEFT_GGML_TYPE_Q4_1:
-      case WEFT_GGML_TYPE_IQ2_XS:
-        break;  // no grouped GEMM: the pair GEMV below
-      default: {  // Q4_0 / MXFP4 / NVFP4: the GEMMs read a planar activation quantized from X
-        const int fmt = s0->type == WEFT_GGML_TYPE_Q4_0 ? 0 : s0->type == WEFT_GGML_TYPE_MXFP4 ? 1 : 2;
-        const int8_t* cb = fmt ? tab->codebook : nullptr;
+      default: {  // Q4_0 / MXFP4 / NVFP4 / Q4_1: the GEMMs read a planar activation quantized from X
+        const int fmt = s0->type == WEFT_GGML_TYPE_Q4_0    ? 0
+                        : s0->type == WEFT_GGML_TYPE_MXFP4 ? 1
+                        : s0->type == WEFT_GGML_TYPE_NVFP4 ? 2
+                                                           : 3;
+        const int8_t* cb = fmt == 1 || fmt == 2 ? tab->codebook : nullptr;
         const float* sc = fmt == 1 ? tab->scale : fmt == 2 ? tab->ue4m3 : nullptr;
         if (quantize && mul_mat_id_q80_grouped_ok(fmt, W, X, xq_out, Y, n, k, st, pr, n_pairs,
                                                   (int)n_tok, ws, ws_bytes, cb, sc)) {

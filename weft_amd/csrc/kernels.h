@@ -90,7 +90,8 @@ bool mul_mat_id_q4k_grouped_ok(const uint8_t* W, size_t xq_bytes, const float* Y
                                size_t ws_bytes);
 void mul_mat_id_q4k_grouped(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K,
                             const RowStrides& st, const PairArgs& pr, int n_pairs, void* ws);
-// Q4_0 (fmt 0) / MXFP4 (fmt 1) / NVFP4 (fmt 2) MUL_MAT_ID on the grouped MFMA GEMMs: src1
+// Q4_0 (fmt 0) / MXFP4 (fmt 1) / NVFP4 (fmt 2) / Q4_1 (fmt 3, Q8_1 activation)
+// MUL_MAT_ID on the grouped MFMA GEMMs: src1
 // rows (token t, row j) at t * pr.x_s2 + j * pr.x_s1 floats, quantized into
 // Xq (planar for the GEMM, GGML's records at the end).
 bool mul_mat_id_q80_grouped_ok(int fmt, const uint8_t* W, const float* X, const uint8_t* Xq, const float* Y,
@@ -100,11 +101,11 @@ bool mul_mat_id_q80_grouped_ok(int fmt, const uint8_t* W, const float* X, const 
 void mul_mat_id_q80_grouped(int fmt, const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N,
                             size_t K, const RowStrides& st, const PairArgs& pr, int n_pairs, int n_tok,
                             void* ws, const int8_t* codebook, const float* scale);
-// IQ2_XXS MUL_MAT_ID on the grouped MFMA GEMM over quantized Q8_K rows
-bool mul_mat_id_iq2_grouped_ok(const uint8_t* W, size_t xq_bytes, const float* Y, const int8_t* grid,
+// IQ2_XXS / IQ2_XS (xs) MUL_MAT_ID on the grouped MFMA GEMM over quantized Q8_K rows
+bool mul_mat_id_iq2_grouped_ok(bool xs, const uint8_t* W, size_t xq_bytes, const float* Y, const int8_t* grid,
                                const int8_t* signs, size_t N, size_t K, const RowStrides& st,
                                const PairArgs& pr, int n_pairs, const void* ws, size_t ws_bytes);
-void mul_mat_id_iq2_grouped(const uint8_t* W, const uint8_t* Xq, const int8_t* grid, const int8_t* signs,
+void mul_mat_id_iq2_grouped(bool xs, const uint8_t* W, const uint8_t* Xq, const int8_t* grid, const int8_t* signs,
                             float* Y, size_t N, size_t K, const RowStrides& st, const PairArgs& pr,
                             int n_pairs, void* ws);
 // Q4_0 (fmt 0), MXFP4 (1), IQ2_XXS (2), Q6_K (3), Q5_K (4), NVFP4 (5), Q4_1 (6) or

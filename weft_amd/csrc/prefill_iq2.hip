@@ -366,10 +366,10 @@ void gemm_iq2(const uint8_t* W, const uint8_t* Xq, const int8_t* grid, const int
 
 }  // namespace
 
-bool mul_mat_id_iq2_grouped_ok(const uint8_t* W, size_t xq_bytes, const float* Y, const int8_t* grid,
+bool mul_mat_id_iq2_grouped_ok(bool xs, const uint8_t* W, size_t xq_bytes, const float* Y, const int8_t* grid,
                                const int8_t* signs, size_t N, size_t K, const RowStrides& st,
                                const PairArgs& pr, int n_pairs, const void* ws, size_t ws_bytes) {
-  const size_t rb = K / 256 * kIq2xxsBytes;
+  const size_t rb = K / 256 * (xs ? kIq2xsBytes : kIq2xxsBytes);
   const size_t ldw = N > 1 ? st.ldw : rb;
   return N > 0 && n_pairs > 0 && K > 0 && K % 512 == 0 && W != nullptr && Y != nullptr &&
          grid != nullptr && signs != nullptr && aligned(W, 4) && ldw % 4 == 0 && aligned(Y, 4) &&
@@ -379,15 +379,20 @@ bool mul_mat_id_iq2_grouped_ok(const uint8_t* W, size_t xq_bytes, const float* Y
          (size_t)moe_tile_bound(n_pairs, pr.n_as) * ((N + kNT - 1) / kNT) <= (size_t)INT32_MAX;
 }
 
-void mul_mat_id_iq2_grouped(const uint8_t* W, const uint8_t* Xq, const int8_t* grid, const int8_t* signs,
+void mul_mat_id_iq2_grouped(bool xs, const uint8_t* W, const uint8_t* Xq, const int8_t* grid, const int8_t* signs,
                             float* Y, size_t N, size_t K, const RowStrides& st, const PairArgs& pr,
                             int n_pairs, void* ws) {
   const MoeGroups g = moe_group(pr, n_pairs, ws);
-  const size_t ldw = N > 1 ? st.ldw : K / 256 * kIq2xxsBytes;
+  const size_t ldw = N > 1 ? st.ldw : K / 256 * (xs ? kIq2xsBytes : kIq2xxsBytes);
   GemmArgs ga{W, Xq, grid, signs, Y, (int)N, (int)K, kMT, ldw, 0, group_tiles(g, pr)};
   const size_t wgs = (size_t)g.tmax * ((N + kNT - 1) / kNT);
-  iq2_mfma_gemm<true><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(ga);
-  check_launch("iq2_mfma_gemm");
+  if (xs) {
+    iq2_mfma_gemm<true, true><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(ga);
+    check_launch("iq2xs_mfma_gemm");
+  } else {
+    iq2_mfma_gemm<true><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(ga);
+    check_launch("iq2_mfma_gemm");
+  }
 }
 
 void mul_mat_iq2_xxs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,

@@ -915,30 +915,32 @@ bool prefill_q80(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* co
 
 }  // namespace
 
-// MUL_MAT_ID on the grouped GEMMs (Q4_0: fmt 0, MXFP4: fmt 1, NVFP4: fmt 2).  X rows
+// MUL_MAT_ID on the grouped GEMMs (Q4_0: fmt 0, MXFP4: fmt 1, NVFP4: fmt 2,
+// Q4_1: fmt 3, whose activation is Q8_1).  X rows
 // (token t, row j) at t * x_s2 + j * x_s1 floats are quantized into Xq
 // planar, then in GGML's records after the GEMM, as the dense path does.
 bool mul_mat_id_q80_grouped_ok(int fmt, const uint8_t* W, const float* X, const uint8_t* Xq, const float* Y,
                                size_t N, size_t K, const RowStrides& st, const PairArgs& pr, int n_pairs,
                                int n_tok, const void* ws, size_t ws_bytes, const int8_t* codebook,
                                const float* scale) {
-  const size_t rb = K / 32 * (fmt == 0 ? kQ4_0Bytes : fmt == 1 ? kMxfp4Bytes : kNvfp4Bytes / 2);
+  const size_t rb = K / 32 * (fmt == 0 ? kQ4_0Bytes : fmt == 1 ? kMxfp4Bytes : fmt == 2 ? kNvfp4Bytes / 2 : kQ4_1Bytes);
   const size_t ldw = N > 1 ? st.ldw : rb;
-  const size_t xq_bytes = (size_t)n_tok * pr.ne11 * (K / 32) * kQ8_0Bytes;
+  const size_t xq_bytes = (size_t)n_tok * pr.ne11 * (K / 32) * (fmt == 3 ? kQ8_1Bytes : kQ8_0Bytes);
   return N > 0 && K > 0 && n_pairs > 0 && K % 256 == 0 && X != nullptr && aligned(X, 4) &&
          aligned(W, 4) && ldw % 4 == 0 && (kNT - 1) * ldw + rb < ((size_t)1 << 32) &&
          aligned(Xq, 16) && xq_bytes < ((size_t)1 << 32) && aligned(Y, 4) && aligned(ws, 16) &&
          ws_bytes >= moe_group_bytes(n_pairs, pr.n_as) && pr.w_es % 4 == 0 &&
          pr.n_as <= kMaxExperts && N <= (size_t)INT32_MAX && K <= (size_t)INT32_MAX &&
-         strides_ok(st, rb, 1, K, N, N, 1) && (fmt == 0 || (codebook != nullptr && scale != nullptr)) &&
+         strides_ok(st, rb, 1, K, N, N, 1) && (fmt == 0 || fmt == 3 || (codebook != nullptr && scale != nullptr)) &&
          (size_t)moe_tile_bound(n_pairs, pr.n_as) * ((N + kNT - 1) / kNT) <= (size_t)INT32_MAX;
 }
 
 void mul_mat_id_q80_grouped(int fmt, const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N,
                             size_t K, const RowStrides& st, const PairArgs& pr, int n_pairs, int n_tok,
                             void* ws, const int8_t* codebook, const float* scale) {
-  const size_t rb = K / 32 * (fmt == 0 ? kQ4_0Bytes : fmt == 1 ? kMxfp4Bytes : kNvfp4Bytes / 2);
-  const size_t rows = (size_t)n_tok * pr.ne11, xs = K + K / 16;
+  const size_t rb = K / 32 * (fmt == 0 ? kQ4_0Bytes : fmt == 1 ? kMxfp4Bytes : fmt == 2 ? kNvfp4Bytes / 2 : kQ4_1Bytes);
+  const size_t rows = (size_t)n_tok * pr.ne11;
+  const size_t xs = fmt == 3 ? planar_row_bytes<WFmt::Q4_1>(K) : planar_row_bytes<WFmt::Q4_0>(K);
   // rows (t, j) of X at t * x_s2 + j * x_s1: one pass when they are evenly
   // spaced, else one per token
   auto each_plane = [&](auto&& pass, size_t row_bytes) {
@@ -950,6 +952,8 @@ void mul_mat_id_q80_grouped(int fmt, const uint8_t* W, const float* X, uint8_t* 
   each_plane([&](const float* x, size_t l, uint8_t* xp, size_t m) {
     if (fmt == 1)
       planar_pass<WFmt::MXFP4>(x, l, xp, m, K, codebook, scale);
+    else if (fmt == 3)
+      planar_pass<WFmt::Q4_1>(x, l, xp, m, K, nullptr, nullptr);
     else
       planar_pass<WFmt::Q4_0>(x, l, xp, m, K, nullptr, nullptr);  // the plain int8 planar layout
   }, xs);
@@ -960,12 +964,18 @@ void mul_mat_id_q80_grouped(int fmt, const uint8_t* W, const float* X, uint8_t* 
     q80_mfma_gemm<WFmt::Q4_0, true><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(ga);
   else if (fmt == 1)
     mxfp4_gemm<true><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(ga);
-  else
+  else if (fmt == 2)
     q80_mfma_gemm<WFmt::NVFP4, true><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(ga);
-  check_launch(fmt == 0 ? "q80_mfma_gemm" : fmt == 1 ? "mxfp4_gemm" : "nvfp4_mfma_gemm");
+  else
+    q80_mfma_gemm<WFmt::Q4_1, true><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(ga);
+  check_launch(fmt == 1 ? "mxfp4_gemm" : fmt == 2 ? "nvfp4_mfma_gemm" : "q80_mfma_gemm");
   // Xq ends in GGML's record layout
-  each_plane([&](const float* x, size_t l, uint8_t* xq, size_t m) { quantize_q8_0_rows(x, l, xq, m, K); },
-             (K / 32) * kQ8_0Bytes);
+  if (fmt == 3)
+    each_plane([&](const float* x, size_t l, uint8_t* xq, size_t m) { quantize_q8_1_rows(x, l, xq, m, K); },
+               (K / 32) * kQ8_1Bytes);
+  else
+    each_plane([&](const float* x, size_t l, uint8_t* xq, size_t m) { quantize_q8_0_rows(x, l, xq, m, K); },
+               (K / 32) * kQ8_0Bytes);
 }
 
 void mul_mat_q4_0(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
