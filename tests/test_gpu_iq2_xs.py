@@ -52,11 +52,12 @@ def test_vec_dot_iq2_xs(hip):
 
 @pytest.mark.parametrize("symbol", ["production_mul_mat_iq2_xs", "production_mul_mat_iq2_xs_staged"])
 @pytest.mark.parametrize("n,k,m", [(4096, 4096, 1), (4096, 14336, 1), (300, 768, 3), (65, 1024, 5),
-                                   (1, 256, 1), (512, 4096, 64), (200, 1536, 70), (129, 1024, 17),
-                                   (4096, 4096, 512)])
+                                   (1, 256, 1), (1, 512, 1), (17, 1024, 1), (5000, 2048, 1),
+                                   (512, 4096, 64), (200, 1536, 70), (129, 1024, 17), (4096, 4096, 512)])
 def test_mul_mat_iq2_xs(hip, symbol, n, k, m):
     """M >= 16 with K a multiple of 512 runs the MFMA GEMM (the IQ2 GEMM with
-    per-16 scales), every other shape the GEMV."""
+    per-16 scales), M = 1 with K <= 4096 a multiple of 512 the batch-1
+    kernel, every other shape the staged GEMV."""
     w = weights(n, k)
     w, x, xq, y = run_mul_mat(hip, symbol, "iq2_xs", n, k, m, w=w)
     check_mul_mat("iq2_xs", w, x, xq, y, n, k, m)

@@ -333,6 +333,21 @@ def crafted_acts_q8k(m, k, rng):
     return x
 
 
+@pytest.mark.parametrize("n,k", [(1, 512), (17, 1024), (300, 2048), (5000, 4096), (4097, 4096)])
+def test_decode_iq2_xxs_batch1(hip, n, k):
+    """The batch-1 IQ2_XXS kernel (records in VGPRs, K <= 4096 with an even
+    superblock count): one row, rows past a wave's share, idle lanes for
+    K < 4096, a row count that leaves the last workgroup short; crafted
+    records (d at the fp16 edges, s = 15 and s = 0) against activations with
+    a zero block."""
+    rng = np.random.default_rng(n + k)
+    w = crafted_iq2_xxs(n, k, rng)
+    x = acts(1, k, seed=13).copy()
+    x[0, 256:512] = 0.0
+    w, x, xq, y = run_mul_mat(hip, MM_DECODE["iq2_xxs"], "iq2_xxs", n, k, 1, w=w, x=x)
+    check_mul_mat("iq2_xxs", w, x, xq, y, n, k, 1)
+
+
 @pytest.mark.parametrize("fmt,make", [("q4_k", crafted_q4_k), ("q4_0", crafted_q4_0),
                                       ("iq2_xxs", crafted_iq2_xxs)])
 def test_prefill_crafted_records(hip, fmt, make):

@@ -660,6 +660,12 @@ void launch(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_
         decode_rec_m1(F == Fmt::MXFP4 ? 1 : 0, W, X, xq_out, tab0, static_cast<const float*>(tab1), Y, N, K, st))
       return;
   }
+  if constexpr (kGrid) {
+    // batch 1: the register-resident kernel of decode_iq2.hip when it applies
+    if (pr == nullptr && M == 1 && X != nullptr &&
+        decode_iq2_m1(F == Fmt::IQ2_XS, W, X, xq_out, tab0, static_cast<const int8_t*>(tab1), Y, N, K, st))
+      return;
+  }
   const size_t row_lds = T::kQ8K ? q8k_lds_row_bytes((int)K)
                          : act_q81<F>() ? q81_lds_row_bytes((int)K)
                                         : q80_lds_row_bytes((int)K);
