@@ -43,6 +43,7 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
 enum class WFmt { Q4_0, MXFP4, Q4_1, NVFP4 };
@@ -167,6 +168,7 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
   uint8_t* ring1 = lds + 2 * kStage;
   float(*adt)[2][8 * kMT] = reinterpret_cast<float(*)[2][8 * kMT]>(lds + 4 * kStage);  // [slot][parity][block][token]
   // Q4_1: the tokens' fp16 block sums [slot][parity][block][token]; MXFP4: scale table
+  // [slot][parity][token][block]
   uint16_t(*ast)[2][8 * kMT] = reinterpret_cast<uint16_t(*)[2][8 * kMT]>(lds + 4 * kStage + 2 * 2 * 8 * kMT * 4);
   float* scl = reinterpret_cast<float*>(lds + 4 * kStage) + 2 * 2 * 8 * kMT;
   static_assert(q80_lds_bytes<F>() == 4 * kStage + 2 * 2 * 8 * kMT * 4 +
@@ -261,12 +263,8 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
     const uint32_t w[4] = {dxraw.x, dxraw.y, dxraw.z, dxraw.w};
 #pragma unroll
     for (int j = 0; j < 8; ++j) d[j * kMT + lane] = fp16_to_fp32((w[j >> 1] >> (16 * (j & 1))) & 0xffffu);
-    if constexpr (F == WFmt::Q4_1) {
-      uint16_t* sv = &ast[slot][par][0];
-      const uint32_t u[4] = {sraw.x, sraw.y, sraw.z, sraw.w};
-#pragma unroll
-      for (int j = 0; j < 8; ++j) sv[j * kMT + lane] = (uint16_t)(u[j >> 1] >> (16 * (j & 1)));
-    }
+    if constexpr (F == WFmt::Q4_1)  // the token's eight fp16 block sums, token-major
+      *reinterpret_cast<uint4*>(&ast[slot][par][8 * lane]) = sraw;
   };
 
   v16i I[2];
@@ -344,11 +342,10 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
           q3 = __builtin_amdgcn_alignbyte(w4, w3, sh);
         }
         // header byte(s) just before the nibbles
-        float wsc, wmin = 0.f;
+        float wsc;
         if constexpr (F == WFmt::Q4_1) {
           const uint32_t hd = ld32(wrow + T::kRec * j);  // records are 4-byte aligned here
           wsc = fp16_to_fp32(hd & 0xffffu);
-          wmin = fp16_to_fp32(hd >> 16);
         } else if constexpr (F == WFmt::Q4_0) {
           const uint32_t dbits = sh >= 2 ? (w0 & 0xffffu) : (ld32(wrow + b4 - 4) >> 16);
           wsc = fp16_to_fp32(dbits);
@@ -382,24 +379,28 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
           for (int r4 = 0; r4 < 4; ++r4) {
             const float4 d4 = *reinterpret_cast<const float4*>(dxs + j * kMT + 32 * t + 8 * r4 + 4 * kg);
             const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
-            if constexpr (F == WFmt::Q4_1) {
-              // (dw dx) I + m s per block (ggml-cpu/quants.c:241)
-              const uint2 s4 = *reinterpret_cast<const uint2*>(sxs + j * kMT + 32 * t + 8 * r4 + 4 * kg);
-              const float sv[4] = {fp16_to_fp32(s4.x & 0xffffu), fp16_to_fp32(s4.x >> 16),
-                                   fp16_to_fp32(s4.y & 0xffffu), fp16_to_fp32(s4.y >> 16)};
 #pragma unroll
-              for (int q = 0; q < 4; ++q) {
-                const int r = 4 * r4 + q;
-                y[t][r] += (dv[q] * wsc) * (float)I[t][r] + wmin * sv[q];
-              }
-            } else {
-#pragma unroll
-              for (int q = 0; q < 4; ++q) {
-                const int r = 4 * r4 + q;
-                y[t][r] += (dv[q] * wsc) * (float)I[t][r];
-              }
+            for (int q = 0; q < 4; ++q) {
+              const int r = 4 * r4 + q;
+              y[t][r] += (dv[q] * wsc) * (float)I[t][r];
             }
           }
+      }
+      if constexpr (F == WFmt::Q4_1) {
+        // Q4_1's min term, m s per block (ggml-cpu/quants.c:241), for the
+        // stage's eight blocks at once: one f16 MFMA per tile (K = 8 blocks)
+        // of the tokens' fp16 block sums against the rows' fp16 mins, added
+        // into y.  Both are fp16, so every product is exact in fp32.
+        const uint8_t* mrec = wrow + T::kRec * 4 * kg;  // blocks 4 kg .. 4 kg + 3 of this lane's row
+        const uint32_t h0 = ld32(mrec), h1 = ld32(mrec + T::kRec), h2 = ld32(mrec + 2 * T::kRec),
+                       h3 = ld32(mrec + 3 * T::kRec);
+        const uint2 bm = make_uint2(__builtin_amdgcn_perm(h1, h0, 0x07060302u), __builtin_amdgcn_perm(h3, h2, 0x07060302u));
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const uint2 am = *reinterpret_cast<const uint2*>(sxs + 8 * (32 * t + col) + 4 * kg);
+          y[t] = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, am), __builtin_bit_cast(v4h, bm), y[t],
+                                                     0, 0, 0);
+        }
       }
     }
     if (refill && wcol == 0) store_dx((pair + 1) & 1);  // slot last read a pair ago
