@@ -14,7 +14,9 @@ GGML's quantizers give an N(0, 0.02^2) matrix (the kernels' time does not
 depend on the values), activations ~ N(0, 1), pre-quantized activations by
 the library's own q8_K_quantize.  Only the CPU baseline below uses oracle/.  Every case rotates its weights
 over enough copies (> 2 x the 256 MB Infinity Cache) that each call reads
-them from HBM.  Each case is timed three ways on the library's stream:
+them from HBM; the write-bound row dequantize rotates its outputs as well
+(``one_output_us``: the same calls into one output buffer).  Each case is
+timed three ways on the library's stream:
   * ``us``: K back-to-back calls between two HIP events (the headline);
   * ``cold_us``: BASELINE.md's protocol -- 512 MiB written to flush the
     caches, then one call between two events; median of 20;
@@ -394,9 +396,16 @@ def run_case(b: Bench, name: str, steps: int, warmup: int, extra: bool) -> dict:
     else:
         wd = [b.dev_copy(w) for _ in range(copies)]
         if m == 0:  # row dequantize of the whole matrix
-            y = torch.empty(n * k, dtype=torch.float32, device=b.dev)
+            # write-bound: the outputs rotate too, past the Infinity Cache,
+            # so that no call writes into lines a previous call left cached
+            ycopies = max(2, int(np.ceil(2 * MALL_BYTES / (4 * n * k))) + 1)
+            ys = [torch.empty(n * k, dtype=torch.float32, device=b.dev) for _ in range(ycopies)]
+            y = ys[0]
 
             def launch(i):
+                fn(wd[i % copies].data_ptr(), ys[i % ycopies].data_ptr(), n * k)
+
+            def launch_one_output(i):
                 fn(wd[i % copies].data_ptr(), y.data_ptr(), n * k)
 
             nbytes = w.nbytes + 4 * n * k
@@ -453,6 +462,11 @@ def run_case(b: Bench, name: str, steps: int, warmup: int, extra: bool) -> dict:
     out = {"symbol": sym, "N": n, "K": k, "M": max(m, 1) if m < 0 else m, "us": round(sec * 1e6, 3),
            "algorithmic_bytes": int(nbytes), "GBs": round(nbytes / sec / 1e9, 2),
            "weight_copies_rotated": copies, "steps": steps, "kernels": kernels}
+    if m == 0:
+        out["output_copies_rotated"] = ycopies
+        # the same calls writing one output buffer (180 MB at config 2, part
+        # of which the Infinity Cache keeps between calls)
+        out["one_output_us"] = round(b.time_calls(launch_one_output, steps, warmup) * 1e6, 3)
     if extra:
         out["cold_us"] = round(b.time_cold(launch) * 1e6, 3)
         out["graph_us"] = round(b.time_graph(launch) * 1e6, 3)
