@@ -68,10 +68,24 @@ def test_vec_dot_nvfp4_extreme_records(hip):
 
 
 @pytest.mark.parametrize("n,k,m", [(4096, 4096, 1), (11008, 4096, 1), (4096, 14336, 1), (300, 768, 3),
-                                   (65, 1024, 5), (1, 64, 1)])
+                                   (65, 1024, 5), (1, 64, 1), (17, 1024, 1), (5000, 2048, 1)])
 def test_decode_nvfp4(hip, n, k, m):
+    """M = 1 with K <= 4096 a multiple of 64 runs the batch-1 kernel (records
+    in VGPRs), every other shape the staged GEMV."""
     w, x, xq, y = run_mul_mat(hip, "production_mul_mat_nvfp4_decode", "nvfp4", n, k, m)
     check_mul_mat("nvfp4", w, x, xq, y, n, k, m)
+
+
+def test_decode_nvfp4_batch1_extreme_records(hip):
+    """The batch-1 kernel on rows cycling through all 256 UE4M3 scale bytes
+    and every code, against an activation with an all-zero Q8_0 block."""
+    n, k = 96, 4096
+    recs = extreme_records()
+    w = np.stack([np.roll(recs, 3 * r, axis=0) for r in range(n)]).reshape(n, -1)
+    x = acts(1, k, seed=15).copy()
+    x[0, 32:64] = 0.0
+    w, x, xq, y = run_mul_mat(hip, "production_mul_mat_nvfp4_decode", "nvfp4", n, k, 1, w=w, x=x)
+    check_mul_mat("nvfp4", w, x, xq, y, n, k, 1)
 
 
 @pytest.mark.parametrize("n,k,m", [(4096, 4096, 512), (512, 4096, 64), (144, 768, 70), (129, 256, 17),

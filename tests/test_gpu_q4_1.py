@@ -73,10 +73,22 @@ def test_vec_dot_q4_1(hip):
 
 
 @pytest.mark.parametrize("n,k,m", [(4096, 4096, 1), (11008, 4096, 1), (4096, 14336, 1), (300, 768, 3),
-                                   (65, 1024, 5), (1, 32, 1)])
+                                   (65, 1024, 5), (1, 32, 1), (1, 64, 1), (17, 1024, 1), (5000, 2048, 1)])
 def test_decode_q4_1(hip, n, k, m):
+    """M = 1 with K <= 4096 a multiple of 64 runs the batch-1 kernel (records
+    in VGPRs), every other shape the staged GEMV."""
     w, x, xq, y = run_mul_mat(hip, "production_mul_mat_q4_1_decode", "q4_1", n, k, m)
     check_mul_mat("q4_1", w, x, xq, y, n, k, m)
+
+
+def test_decode_q4_1_batch1_crafted_records(hip):
+    rng = np.random.default_rng(81)
+    n, k = 300, 4096
+    w = crafted_q4_1(n, k, rng)
+    x = acts(1, k, seed=14).copy()
+    x[0, 64:96] = 0.0  # an all-zero Q8_1 block (d = s = 0)
+    w, x, xq, y = run_mul_mat(hip, "production_mul_mat_q4_1_decode", "q4_1", n, k, 1, w=w, x=x)
+    check_mul_mat("q4_1", w, x, xq, y, n, k, 1)
 
 
 @pytest.mark.parametrize("n,k,m", [(4096, 4096, 512), (300, 512, 37), (129, 768, 16), (200, 1536, 70),

@@ -654,10 +654,11 @@ void launch(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_
     set_error(hipErrorInvalidValue);
     return;
   }
-  if constexpr (F == Fmt::Q4_0 || F == Fmt::MXFP4) {
+  if constexpr (F == Fmt::Q4_0 || F == Fmt::MXFP4 || F == Fmt::NVFP4 || F == Fmt::Q4_1) {
     // batch 1: the register-resident kernel of decode_rec.hip when it applies
+    constexpr int kRecFmt = F == Fmt::MXFP4 ? 1 : F == Fmt::NVFP4 ? 5 : F == Fmt::Q4_1 ? 6 : 0;
     if (pr == nullptr && M == 1 && X != nullptr &&
-        decode_rec_m1(F == Fmt::MXFP4 ? 1 : 0, W, X, xq_out, tab0, static_cast<const float*>(tab1), Y, N, K, st))
+        decode_rec_m1(kRecFmt, W, X, xq_out, tab0, static_cast<const float*>(tab1), Y, N, K, st))
       return;
   }
   if constexpr (kGrid) {

@@ -48,7 +48,7 @@ void decode_q5_k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t
 void decode_nvfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
                   const float* scale, float* Y, size_t N, size_t K, size_t M, const RowStrides& st);
 
-// Batch-1 Q4_0 (fmt 0) / MXFP4 (fmt 1) GEMV with the records in VGPRs
+// Batch-1 Q4_0 (fmt 0) / MXFP4 (1) / NVFP4 (5) / Q4_1 (6) GEMV with the records in VGPRs
 // (decode_rec.hip); false, with nothing launched, when the call does not
 // suit it (K > 4096, unaligned operands), for the caller's general kernel.
 bool decode_rec_m1(int fmt, const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
