@@ -68,10 +68,28 @@ def test_vec_dot_q5_k_extreme_records(hip):
 
 
 @pytest.mark.parametrize("n,k,m", [(4096, 4096, 1), (11008, 4096, 1), (4096, 14336, 1), (300, 768, 3),
-                                   (65, 1024, 5), (1, 256, 1)])
+                                   (65, 1024, 5), (1, 256, 1), (17, 1024, 1), (5000, 2048, 1), (33, 768, 1)])
 def test_decode_q5_k(hip, n, k, m):
+    """M = 1 with K <= 4096 runs the batch-1 kernel (records in VGPRs),
+    every other shape the staged GEMV."""
     w, x, xq, y = run_mul_mat(hip, "production_mul_mat_q5_k_decode", "q5_k", n, k, m)
     check_mul_mat("q5_k", w, x, xq, y, n, k, m)
+
+
+def test_decode_q5_k_batch1_extreme_records(hip):
+    """The batch-1 kernel on rows of 0 and 31 codes, scales and mins at 63,
+    d = 0 with dmin kept, against an activation with an all-zero Q8_K block."""
+    n, k = 160, 4096
+    w = extreme_records(n * k // 256).reshape(n, k // 256, 176)
+    w[5, :, 16:176] = 0x00
+    w[9, :, 16:176] = 0xFF
+    w[9, :, 4:16] = 0xFF
+    w[17, :, 0:2] = 0
+    w = np.ascontiguousarray(w.reshape(n, -1))
+    x = acts(1, k, seed=16).copy()
+    x[0, 512:768] = 0.0
+    w, x, xq, y = run_mul_mat(hip, "production_mul_mat_q5_k_decode", "q5_k", n, k, 1, w=w, x=x)
+    check_mul_mat("q5_k", w, x, xq, y, n, k, 1)
 
 
 @pytest.mark.parametrize("n,k,m", [(4096, 4096, 512), (512, 4096, 64), (144, 1024, 70), (300, 768, 17),
