@@ -60,10 +60,32 @@ def test_vec_dot_q6_k_extreme_records(hip):
 
 
 @pytest.mark.parametrize("n,k,m", [(4096, 4096, 1), (11008, 4096, 1), (4096, 14336, 1), (300, 768, 3),
-                                   (65, 1024, 5), (1, 256, 1)])
+                                   (65, 1024, 5), (1, 256, 1), (1, 512, 1), (17, 1024, 1), (5000, 2048, 1)])
 def test_decode_q6_k(hip, n, k, m):
+    """M = 1 with K <= 4096 a multiple of 512 runs the batch-1 kernel
+    (records in VGPRs, odd superblocks at a 2-byte offset), every other
+    shape the staged GEMV."""
     w, x, xq, y = run_mul_mat(hip, "production_mul_mat_q6_k_decode", "q6_k", n, k, m)
     check_mul_mat("q6_k", w, x, xq, y, n, k, m)
+
+
+def test_decode_q6_k_batch1_extreme_records(hip):
+    """The batch-1 kernel on rows of -32 and 31 codes, scales from
+    {-128, 127, -1, 0, 1}, d = 0, against an activation with an all-zero
+    Q8_K block."""
+    n, k = 160, 4096
+    rng = np.random.default_rng(31)
+    w = extreme_records(n * k // 256).reshape(n, k // 256, 210)
+    d = (rng.standard_normal((n, k // 256)) * 1e-2).astype(np.float16)
+    w[:, :, 208:210] = d.view(np.uint8).reshape(n, k // 256, 2)
+    w[5, :, :192] = 0x00
+    w[9, :, :192] = 0xFF
+    w[17, 3, 208:210] = 0
+    w = np.ascontiguousarray(w.reshape(n, -1))
+    x = acts(1, k, seed=17).copy()
+    x[0, 256:512] = 0.0
+    w, x, xq, y = run_mul_mat(hip, "production_mul_mat_q6_k_decode", "q6_k", n, k, 1, w=w, x=x)
+    check_mul_mat("q6_k", w, x, xq, y, n, k, 1)
 
 
 @pytest.mark.parametrize("n,k,m", [(4096, 4096, 512), (512, 4096, 64), (144, 1024, 70), (129, 2048, 17),

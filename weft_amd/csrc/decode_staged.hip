@@ -665,6 +665,10 @@ void launch(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_
     // batch 1: the register-resident kernel of decode_q5k.hip when it applies
     if (pr == nullptr && M == 1 && X != nullptr && decode_q5k_m1(W, X, xq_out, Y, N, K, st)) return;
   }
+  if constexpr (F == Fmt::Q6_K) {
+    // batch 1: the register-resident kernel of decode_q6k.hip when it applies
+    if (pr == nullptr && M == 1 && X != nullptr && decode_q6k_m1(W, X, xq_out, Y, N, K, st)) return;
+  }
   if constexpr (kGrid) {
     // batch 1: the register-resident kernel of decode_iq2.hip when it applies
     if (pr == nullptr && M == 1 && X != nullptr &&

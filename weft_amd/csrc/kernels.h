@@ -58,6 +58,10 @@ bool decode_rec_m1(int fmt, const uint8_t* W, const float* X, uint8_t* Xq, const
 // not 16-byte aligned).
 bool decode_q5k_m1(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
                    const RowStrides& st);
+// Batch-1 Q6_K GEMV with the records in VGPRs (decode_q6k.hip); false when
+// the call does not suit it (K > 4096, an odd superblock count, unaligned).
+bool decode_q6k_m1(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
+                   const RowStrides& st);
 // Batch-1 IQ2_XXS / IQ2_XS (xs) GEMV with the records in VGPRs (decode_iq2.hip);
 // false, with nothing launched, when the call does not suit it (K > 4096,
 // an odd superblock count, unaligned operands).
