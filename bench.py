@@ -200,14 +200,23 @@ def profiled_traffic(name: str):
 
 
 def cpu_model() -> str:
+    """The host CPU's identity as /proc/cpuinfo gives it (model name, family,
+    model and stepping, clock, whether AVX-512 is present)."""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if not line.strip():
+                    break  # the first processor's block
+                key, _, val = line.partition(":")
+                fields[key.strip()] = val.strip()
     except OSError:
-        pass
-    return platform.processor() or "unknown"
+        return platform.processor() or "unknown"
+    name = fields.get("model name", platform.processor() or "unknown")
+    ident = "/".join(fields.get(k, "?") for k in ("cpu family", "model", "stepping"))
+    avx512 = "avx512f" in fields.get("flags", "").split()
+    mhz = fields.get("cpu MHz")
+    return f"{name} (family/model/stepping {ident}{', ' + mhz + ' MHz' if mhz else ''}, avx512f {'yes' if avx512 else 'no'})"
 
 
 class Bench:
