@@ -116,3 +116,31 @@ def test_tile_bindings_retile_the_gemv_launches(torch_dev, definition, fmt):
     assert len(launches[0]) == m and len(launches[1]) == m // 4, launches
     np.testing.assert_array_equal(outs[0], outs[1])
     assert _lib.load().weft_hip_set_tile_binding(b"NR", 2) == 0  # no GEMV knob
+
+
+@pytest.mark.parametrize("definition,fmt", [(K.production_mul_mat_q5_k_decode, "q5_k"),
+                                            (K.production_mul_mat_q6_k_decode, "q6_k"),
+                                            (K.production_mul_mat_q4_1_decode, "q4_1")])
+def test_tile_binding_nc_reaches_the_batch1_kernels(torch_dev, definition, fmt):
+    """NC sets the weight rows per workgroup of the batch-1 kernels too:
+    NC = 3 and NC = 200 give bit-identical rows (each one wave's dot)."""
+    from weft_amd import _lib
+    torch, dev = torch_dev
+    n, k = 1000, 2048
+    w = o.quantize(fmt, o.seeded_normal(67, (n, k), 0.02))
+    x = o.seeded_normal(68, (1, k))
+    act = o.ACT_OF[fmt]
+    outs = []
+    for nc in (3, 200):
+        fn = compile(definition, options=CompileOptions(meta={"NC": nc}))
+        xq_t = torch.zeros(o.record_bytes(act, k), dtype=torch.uint8, device=dev)
+        y_t = torch.full((1, n), float("nan"), dtype=torch.float32, device=dev)
+        _lib.launch_log()
+        fn(Buffer(torch.from_numpy(w).to(dev), shape=(n, k), encoding=fmt.upper()),
+           torch.from_numpy(x).to(dev), Buffer(xq_t, shape=(1, k), encoding=act.upper()), y_t)
+        assert len(_lib.launch_log()) == 1
+        outs.append(y_t.cpu().numpy())
+        want_xq = o.quantize(act, x)
+        e, a = o.mul_mat_f64(fmt, w, want_xq, n, k, 1)
+        assert o.within_tolerance(outs[-1], e, a).all()
+    np.testing.assert_array_equal(outs[0], outs[1])

@@ -201,7 +201,9 @@ bool decode_iq2_m1(bool xs, const uint8_t* W, const float* X, uint8_t* Xq, const
   a.Y = Y;
   a.N = (int)N;
   a.K = (int)K;
-  a.rows_per_wg = (int)((N + wgs - 1) / wgs);
+  // a CompileOptions NC binding sets the weight rows per workgroup
+  const int nc = tile_bindings().nc;
+  a.rows_per_wg = nc > 0 ? (int)std::min<size_t>(N, (size_t)nc) : (int)((N + wgs - 1) / wgs);
   a.ldw = ldw;
   const int g = (int)((N + a.rows_per_wg - 1) / a.rows_per_wg);
   const size_t lds = (xs ? 4096 : 2048) + 1024 + q8k_lds_row_bytes((int)K);

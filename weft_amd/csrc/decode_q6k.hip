@@ -196,7 +196,9 @@ bool decode_q6k_m1(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size
   a.Y = Y;
   a.N = (int)N;
   a.K = (int)K;
-  a.rows_per_wg = (int)((N + wgs - 1) / wgs);
+  // a CompileOptions NC binding sets the weight rows per workgroup
+  const int nc = tile_bindings().nc;
+  a.rows_per_wg = nc > 0 ? (int)std::min<size_t>(N, (size_t)nc) : (int)((N + wgs - 1) / wgs);
   a.ldw = ldw;
   const int grid = (int)((N + a.rows_per_wg - 1) / a.rows_per_wg);
   q6k_gemv_m1_kernel<<<grid, kThreads, q8k_lds_row_bytes((int)K), current_stream()>>>(a);

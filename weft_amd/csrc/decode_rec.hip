@@ -322,7 +322,9 @@ bool decode_rec_m1(int fmt, const uint8_t* W, const float* X, uint8_t* Xq, const
   a.Y = Y;
   a.N = (int)N;
   a.K = (int)K;
-  a.rows_per_wg = (int)((N + wgs - 1) / wgs);
+  // a CompileOptions NC binding sets the weight rows per workgroup
+  const int nc = tile_bindings().nc;
+  a.rows_per_wg = nc > 0 ? (int)std::min<size_t>(N, (size_t)nc) : (int)((N + wgs - 1) / wgs);
   a.ldw = ldw;
   const int grid = (int)((N + a.rows_per_wg - 1) / a.rows_per_wg);
   const size_t lds = 1024 + (fmt == 6 ? q81_lds_row_bytes((int)K) : q80_lds_row_bytes((int)K));
