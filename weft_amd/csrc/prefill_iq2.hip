@@ -22,6 +22,7 @@
 
 #include "kernels.h"
 #include "runtime.h"
+#include "tile_store.h"
 #include "weft_common.h"
 #include "weft_hip.h"
 
@@ -51,7 +52,7 @@ struct Tile {
   static constexpr int kWSlots = kNT * kWD / 64;                // 74 / 66 wave-wide dword loads
   static constexpr int kGrid = kXs ? 512 : 256;                 // grid entries
   static_assert(kNT * kWD % 64 == 0, "weight pair tile is whole wave loads");
-  static_assert(4 * 32 * 64 * 4 <= kSlot, "reduction buffer fits one ring slot");
+  static_assert(kTilePlaneBytes <= kSlot, "an output plane fits one ring slot");
 };
 
 struct GemmArgs {
@@ -313,30 +314,18 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
     if (pair + 1 < npair) step(pair + 1, ring1, ring0);
   }
 
-  // odd-parity partial sums -> LDS -> even waves, one ordered add per output
+  // both parities' partial sums -> two LDS planes (reusing the ring) -> Y
   __syncthreads();
-  float* red = reinterpret_cast<float*>(ring0) + wcol * (32 * 64) + lane;
-  if (par == 1) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) red[(16 * t + r) * 64] = y[t][r];
-  }
+  float* even_plane = reinterpret_cast<float*>(ring0);
+  float* odd_plane = reinterpret_cast<float*>(ring1);
+  tile_partials_to_lds(y, wcol, lane, par ? odd_plane : even_plane);
   __syncthreads();
-  if (par == 1) return;
-  const int gn = n0 + 32 * wcol + col;
-  if (gn < a.N) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int rr = 32 * t + 8 * (r >> 2) + 4 * kg + (r & 3);
-        if (rr < mrows) {
-          const long long yrow = kGroup ? group_dst_row(a.grp, m0, rr) : (long long)(m0 + rr) * a.ldy;
-          a.Y[yrow + gn] = 0.125f * (y[t][r] + red[(16 * t + r) * 64]);
-        }
-      }
-  }
+  tile_store_from_lds(
+      wave, lane, even_plane, odd_plane, mrows, min(kNT, a.N - n0),
+      [&](int rr) {
+        return a.Y + (kGroup ? group_dst_row(a.grp, m0, rr) : (long long)(m0 + rr) * a.ldy) + n0;
+      },
+      [](float e, float o) { return 0.125f * (e + o); });
 }
 
 

@@ -32,13 +32,14 @@
 // aligned for odd b, so its row is staged from the dword holding its first
 // byte (54 dwords, 216 bytes per LDS row) and the odd superblocks read with
 // a 2-byte alignment; the even/odd slots are the two instantiations of the
-// step.  The odd half's partial sums are added to the even half's through
-// LDS at the end, so every output is written once, in a fixed order.
+// step.  Both halves' partial sums meet in LDS at the end and every output
+// is written once, even + odd, with 16-byte stores (tile_store.h).
 #include <algorithm>
 #include <type_traits>
 
 #include "kernels.h"
 #include "runtime.h"
+#include "tile_store.h"
 #include "weft_common.h"
 #include "weft_hip.h"
 
@@ -69,7 +70,7 @@ struct KTile {
   static constexpr int kSlot = kAQ + kBS + kWT;              // 44,032 / 40,960
   static constexpr int kWSlots = kNT * kLoadD / 64;          // 108 / 88 wave-wide dword loads
   static_assert(kNT * kLoadD % 64 == 0, "weight tile is whole wave loads");
-  static_assert(4 * 2 * 16 * 64 * 4 <= kSlot, "reduction buffer fits one ring slot");
+  static_assert(kTilePlaneBytes <= kSlot, "an output plane fits one ring slot");
 };
 
 struct GemmArgs {
@@ -345,30 +346,18 @@ __global__ void __launch_bounds__(kThreads, 1) kq_mfma_gemm(GemmArgs a) {
     if (b + 1 < nsb) step(b + 1, ring1, 0, std::integral_constant<int, k6 ? 2 : 0>{});
   }
 
-  // odd-half partial sums -> LDS -> even waves, one ordered add per output
+  // both parities' partial sums -> two LDS planes (reusing the ring) -> Y
   __syncthreads();
-  float* red = reinterpret_cast<float*>(ring0) + wcol * (32 * 64) + lane;
-  if (h == 1) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) red[(16 * t + r) * 64] = y[t][r];
-  }
+  float* even_plane = reinterpret_cast<float*>(ring0);
+  float* odd_plane = reinterpret_cast<float*>(ring1);
+  tile_partials_to_lds(y, wcol, lane, h ? odd_plane : even_plane);
   __syncthreads();
-  if (h == 1) return;
-  const int gn = n0 + 32 * wcol + col;
-  if (gn < a.N) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int rr = 32 * t + 8 * (r >> 2) + 4 * kg + (r & 3);
-        if (rr < mrows) {
-          const long long yrow = kGroup ? group_dst_row(a.grp, m0, rr) : (long long)(m0 + rr) * a.ldy;
-          a.Y[yrow + gn] = y[t][r] + red[(16 * t + r) * 64];
-        }
-      }
-  }
+  tile_store_from_lds(
+      wave, lane, even_plane, odd_plane, mrows, min(kNT, a.N - n0),
+      [&](int rr) {
+        return a.Y + (kGroup ? group_dst_row(a.grp, m0, rr) : (long long)(m0 + rr) * a.ldy) + n0;
+      },
+      [](float e, float o) { return e + o; });
 }
 
 // MFMA path: prefill shapes with 4-byte aligned weight rows; Q6_K also needs

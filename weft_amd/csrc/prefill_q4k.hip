@@ -38,9 +38,9 @@
 // a global memory instruction.  Once a pair has landed, each loader rewrites
 // its stage's per-token data in place, once for all four column groups: the
 // bsums become f16 and the token scale becomes the outer product's bf16
-// operand.  One barrier per pair hands the filled ring slots over.  Odd
-// partial sums are added to the even waves' through LDS at the end: every
-// output is written once, in a fixed order.
+// operand.  One barrier per pair hands the filled ring slots over.  At the
+// end both parities' partial sums meet in LDS and every output is written
+// once, even + odd, with 16-byte stores (tile_store.h).
 //
 // LDS per superblock stage (38,912 B; 2 pairs = 4 stages):
 //   AQ  64 rows x 17 16-byte chunks: the 16 chunks of qs, then one pad chunk,
@@ -63,6 +63,7 @@
 
 #include "kernels.h"
 #include "runtime.h"
+#include "tile_store.h"
 #include "weft_common.h"
 #include "weft_hip.h"
 
@@ -94,7 +95,7 @@ constexpr int kCohortBlock = 16 * kQ4_KBytes;  // 2304: one superblock of a 16-r
 static_assert(kWT == (kNT / 16) * kCohortBlock, "a weight stage is eight cohort blocks");
 static_assert(kAQ % 1024 == 0 && kAX % 1024 == 0 && kStage % 1024 == 0,
               "every region is a whole number of wave loads");
-static_assert(4 * 32 * 64 * 4 <= 2 * kStage, "reduction buffer fits one ring slot");
+static_assert(2 * kTilePlaneBytes <= 4 * kStage, "the output planes fit the ring");
 
 struct GemmArgs {
   const uint8_t* W;
@@ -415,35 +416,20 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
       }
   }
 
-  // odd-parity partial sums -> LDS (reusing the stages) -> even waves
+  // both parities' partial sums -> two LDS planes (reusing the ring) -> Y
   __syncthreads();
-  float* red = reinterpret_cast<float*>(ring) + wcol * (32 * 64) + lane;
-  if (par == 1) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) red[(16 * t + r) * 64] = y[t][r];
-  }
+  float* planes = reinterpret_cast<float*>(ring);
+  tile_partials_to_lds(y, wcol, lane, planes + par * (kTilePlaneBytes / 4));
   __syncthreads();
-  if (par == 1) return;
-  // store: for a fixed register the 32 lanes of a half cover 32 consecutive columns
-  const int gn = n0 + 32 * wcol + col;
-  if (gn < a.N) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int rr = 32 * t + 8 * (r >> 2) + 4 * kg + (r & 3);
-        if (rr < mrows) {
-          const float v = y[t][r] + red[(16 * t + r) * 64];
-          if constexpr (kGroup) {
-            a.Y[group_dst_row(a.grp, m0, rr) + gn] = v;
-          } else {
-            a.Y[(size_t)(m0 + rr) * a.ldy + gn] = v;
-          }
-        }
-      }
-  }
+  tile_store_from_lds(
+      wave, lane, planes, planes + kTilePlaneBytes / 4, mrows, min(kNT, a.N - n0),
+      [&](int rr) {
+        if constexpr (kGroup)
+          return a.Y + group_dst_row(a.grp, m0, rr) + n0;
+        else
+          return a.Y + (size_t)(m0 + rr) * a.ldy + n0;
+      },
+      [](float e, float o) { return e + o; });
 }
 
 // The GEMM over an already quantized activation.  Weight rows must be

@@ -34,6 +34,7 @@
 
 #include "kernels.h"
 #include "runtime.h"
+#include "tile_store.h"
 #include "weft_common.h"
 #include "weft_hip.h"
 
@@ -160,7 +161,7 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
   constexpr int kWSlots = kNT * kWD / 64;    // 72 / 68 wave-wide dword loads
   constexpr int kWPerWave = kWSlots / 4;     // 18 / 17
   static_assert(kNT * kWD % 256 == 0, "weight slots split evenly over four waves");
-  static_assert(4 * 32 * 64 * 4 <= 2 * kStage, "reduction buffer fits one ring slot");
+  static_assert(kTilePlaneBytes <= 2 * kStage, "an output plane fits one ring half");
 
   // two ring slots; a slot being filled by direct loads never aliases the
   // slot being read
@@ -416,30 +417,18 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
     if (pair + 1 < npair) step(pair + 1, ring1, ring0);
   }
 
-  // odd-parity partial sums -> LDS -> even waves, one ordered add per output
+  // both parities' partial sums -> two LDS planes (reusing the ring) -> Y
   __syncthreads();
-  float* red = reinterpret_cast<float*>(ring0) + wcol * (32 * 64) + lane;
-  if (par == 1) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) red[(16 * t + r) * 64] = y[t][r];
-  }
+  float* even_plane = reinterpret_cast<float*>(ring0);
+  float* odd_plane = reinterpret_cast<float*>(ring1);
+  tile_partials_to_lds(y, wcol, lane, par ? odd_plane : even_plane);
   __syncthreads();
-  if (par == 1) return;
-  const int gn = n0 + 32 * wcol + col;
-  if (gn < a.N) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int rr = 32 * t + 8 * (r >> 2) + 4 * kg + (r & 3);
-        if (rr < mrows) {
-          const long long yrow = kGroup ? group_dst_row(a.grp, m0, rr) : (long long)(m0 + rr) * a.ldy;
-          a.Y[yrow + gn] = y[t][r] + red[(16 * t + r) * 64];
-        }
-      }
-  }
+  tile_store_from_lds(
+      wave, lane, even_plane, odd_plane, mrows, min(kNT, a.N - n0),
+      [&](int rr) {
+        return a.Y + (kGroup ? group_dst_row(a.grp, m0, rr) : (long long)(m0 + rr) * a.ldy) + n0;
+      },
+      [](float e, float o) { return e + o; });
 }
 
 template <WFmt F, bool kGroup>

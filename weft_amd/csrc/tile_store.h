@@ -1,0 +1,78 @@
+// Output stage shared by the 64 x 128 MFMA prefill GEMMs (prefill_q4k.hip,
+// prefill_kq.hip, prefill_iq2.hip, prefill_q80.hip's int8 body).
+//
+// Each of the eight MFMA waves ends the K loop with the partial sums of one
+// parity (superblocks, half superblocks or stages of that parity: w >> 2)
+// for the tile's columns 32 (w & 3) .. + 31, in two 32 x 32 accumulators:
+// register r of tile t holds row 32 t + 8 (r / 4) + 4 kg + r % 4 and column
+// lane % 32 (kg = lane / 32).  Storing that layout straight to Y costs one
+// 4-byte store instruction per register, 128 per workgroup, and the last
+// stores of every workgroup meet in one burst at the end of the launch.
+// Here both parities' partials go to LDS as two row-major 64 x 128 planes,
+// then every MFMA wave adds them (even + odd, the order the kernels always
+// used) and stores 16 contiguous bytes per lane: four rows per instruction,
+// 32 store instructions per workgroup.
+#pragma once
+
+#include <cstdint>
+
+#include <hip/hip_runtime.h>
+
+namespace weft {
+
+// floats per plane row: rows 4 apart (the kg halves of one register) start
+// 32 banks apart, and rows stay 16-byte aligned
+constexpr int kTilePlaneLd = 136;
+constexpr int kTilePlaneBytes = 64 * kTilePlaneLd * 4;  // 34,816
+
+typedef float tile_v16f __attribute__((ext_vector_type(16)));
+
+// Partial sums of this wave's parity into its plane (plane = the LDS plane
+// of the wave's parity, 16-byte aligned, kTilePlaneBytes).  Every wave
+// reading the K loop's LDS must have passed a barrier first.
+__device__ inline void tile_partials_to_lds(const tile_v16f (&y)[2], int wcol, int lane, float* plane) {
+  const int col = 32 * wcol + (lane & 31), kg = lane >> 5;
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = 32 * t + 8 * (r >> 2) + 4 * kg + (r & 3);
+      plane[row * kTilePlaneLd + col] = y[t][r];
+    }
+}
+
+// After a barrier that follows every wave's tile_partials_to_lds: wave w
+// (0..7) stores tile rows 4 w + lane / 16 and 32 + 4 w + lane / 16, columns
+// 4 (lane % 16) + 64 k (k = 0, 1), as fin(even, odd) per value.  Rows past
+// mrows and columns past ncols are not written; row_ptr(rr) is the address
+// of tile row rr's first column in Y.  A row segment that is not 16-byte
+// aligned, or not wholly inside ncols, is stored value by value.
+template <class RowPtr, class Fin>
+__device__ inline void tile_store_from_lds(int wave, int lane, const float* even, const float* odd,
+                                           int mrows, int ncols, RowPtr row_ptr, Fin fin) {
+  const int c0 = 4 * (lane & 15);
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int rr = 32 * p + 4 * wave + (lane >> 4);
+    if (rr >= mrows) continue;
+    float* dst = row_ptr(rr);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int c = c0 + 64 * k;
+      const float4 e = *reinterpret_cast<const float4*>(even + rr * kTilePlaneLd + c);
+      const float4 o = *reinterpret_cast<const float4*>(odd + rr * kTilePlaneLd + c);
+      const float4 v = make_float4(fin(e.x, o.x), fin(e.y, o.y), fin(e.z, o.z), fin(e.w, o.w));
+      float* d = dst + c;
+      if (c + 3 < ncols && (reinterpret_cast<uintptr_t>(d) & 15u) == 0) {
+        *reinterpret_cast<float4*>(d) = v;
+      } else {
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (c + i < ncols) d[i] = vv[i];
+      }
+    }
+  }
+}
+
+}  // namespace weft
