@@ -42,6 +42,13 @@
 // end both parities' partial sums meet in LDS and every output is written
 // once, even + odd, with 16-byte stores (tile_store.h).
 //
+// Launch: at most one workgroup per CU (the ring takes its LDS), each walking
+// a share of the tiles.  The pairs of a workgroup's tiles form one stream
+// through the ring, so the next tile's first superblocks load while the
+// current tile finishes and stores (measured at 512 x 4096 x 11008: a
+// tile's K loop takes 18-19.5 us and its output stage ~1.9 us; only a
+// workgroup's first tile waits for its first pair, ~2.9 us).
+//
 // LDS per superblock stage (38,912 B; 2 pairs = 4 stages):
 //   AQ  64 rows x 17 16-byte chunks: the 16 chunks of qs, then one pad chunk,
 //       so row r starts at 272 r and the 8 lanes of an A-operand read (8
@@ -55,10 +62,10 @@
 // Grouped mode (kGroup, GGML's MUL_MAT_ID, ggml-cpu/ggml-cpu.c:1454-1698):
 // the (token, slot) pairs are grouped by expert on the device
 // (moe_group_kernel: a pair list per expert and a table of 64-row tiles), and
-// workgroup (tile, column block) runs the same GEMM on its tile's pairs: the
+// each (tile, column block) runs the same GEMM on its tile's pairs: the
 // loader gathers their activation rows through the pair list, W is the
-// tile's expert matrix, and each output goes to the pair's dst row.  Tiles
-// past the device's tile count exit at once.
+// tile's expert matrix, and each output goes to the pair's dst row.  Tile
+// slots past the device's tile count are skipped.
 #include <algorithm>
 
 #include "kernels.h"
@@ -95,7 +102,7 @@ constexpr int kCohortBlock = 16 * kQ4_KBytes;  // 2304: one superblock of a 16-r
 static_assert(kWT == (kNT / 16) * kCohortBlock, "a weight stage is eight cohort blocks");
 static_assert(kAQ % 1024 == 0 && kAX % 1024 == 0 && kStage % 1024 == 0,
               "every region is a whole number of wave loads");
-static_assert(2 * kTilePlaneBytes <= 4 * kStage, "the output planes fit the ring");
+static_assert(2 * kTilePlaneBytes <= 2 * kStage, "the output planes fit one ring slot");
 
 struct GemmArgs {
   const uint8_t* W;
@@ -105,6 +112,14 @@ struct GemmArgs {
   uint32_t ldw;   // bytes between weight rows (a tile's 128 rows stay in 32-bit offsets)
   long long ldy;  // floats between output rows
   GroupTiles grp;  // grouped (MUL_MAT_ID) mode
+};
+
+// One 64 x 128 output tile: first activation row (grouped: pair-list index),
+// activation rows present, first weight row, weight byte offset (grouped:
+// the expert's matrix).
+struct Tile {
+  int m0, mrows, n0;
+  long long w_off;
 };
 
 // Direct global->LDS load of 16 bytes per lane: lane l reads sbase + voff
@@ -172,38 +187,37 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
   if (tid < 4) zero16[tid] = 0u;
-  int m0, n0;
-  int mrows;  // activation rows of this tile (the last row repeats past them)
-  const uint8_t* W = a.W;
-  if constexpr (kGroup) {
-    // m0 indexes the pair list.  XCD-aware order as below: an expert's
-    // consecutive tiles on one column block meet in one XCD's L2.
-    const int T = a.grp.tmax * ((a.N + kNT - 1) / kNT);
-    const int L = blockIdx.x, x = L & 7, j = L >> 3;
-    const int t = x * (T >> 3) + min(x, T & 7) + j;
-    long long w_off;
-    if (!group_tile(a.grp, t % a.grp.tmax, m0, mrows, w_off)) return;  // no barrier yet
-    W += w_off;
-    n0 = (t / a.grp.tmax) * kNT;
-  } else {
-    const int ntm = (a.M + kMT - 1) / kMT;
-    const int T = ntm * ((a.N + kNT - 1) / kNT);
-    const int L = blockIdx.x, x = L & 7, j = L >> 3;
-    const int t = x * (T >> 3) + min(x, T & 7) + j;
-    m0 = (t % ntm) * kMT;
-    n0 = (t / ntm) * kNT;
-    mrows = min(kMT, a.M - m0);
-  }
-  m0 = __builtin_amdgcn_readfirstlane(m0);
-  n0 = __builtin_amdgcn_readfirstlane(n0);
-  mrows = __builtin_amdgcn_readfirstlane(mrows);
-  // activation row of tile row r (r < mrows)
-  auto act_row = [&](int r) -> int {
-    if constexpr (kGroup)
-      return group_act_row(a.grp, m0, r);
-    else
-      return m0 + r;
+  // Tile t of the launch: m-tile fastest (dense) or expert tile fastest
+  // (grouped: m0 then indexes the pair list).  False for a grouped tile past
+  // the device's tile count.  Every wave enumerates the same tiles.
+  const int ntn = (a.N + kNT - 1) / kNT;
+  const int ntm = kGroup ? a.grp.tmax : (a.M + kMT - 1) / kMT;
+  auto tile_info = [&](int t, Tile& ti) -> bool {
+    if constexpr (kGroup) {
+      if (!group_tile(a.grp, t % ntm, ti.m0, ti.mrows, ti.w_off)) return false;
+    } else {
+      ti.m0 = (t % ntm) * kMT;
+      ti.mrows = min(kMT, a.M - ti.m0);
+      ti.w_off = 0;
+    }
+    ti.n0 = (t / ntm) * kNT;
+    ti.m0 = __builtin_amdgcn_readfirstlane(ti.m0);
+    ti.mrows = __builtin_amdgcn_readfirstlane(ti.mrows);
+    ti.n0 = __builtin_amdgcn_readfirstlane(ti.n0);
+    return true;
   };
+  // XCD-aware persistent schedule: workgroups are dispatched round-robin over
+  // the eight XCDs, so XCD x = blockIdx % 8 takes one contiguous chunk
+  // [c0, c1) of the tile order (consecutive tiles share a weight block, or an
+  // expert's rows, in that XCD's L2), and its P workgroups walk the chunk with
+  // stride P.  With one workgroup per tile every workgroup takes exactly tile
+  // c0 + blockIdx / 8.
+  const int T = ntm * ntn;
+  const int xcd = blockIdx.x & 7;
+  const int c0 = xcd * (T >> 3) + min(xcd, T & 7);
+  const int c1 = (xcd + 1) * (T >> 3) + min(xcd + 1, T & 7);
+  const int P = ((int)gridDim.x - xcd + 7) >> 3;
+  const int t_first = c0 + (int)(blockIdx.x >> 3);
   const int nsb = a.K >> 8;
   const int npair = (nsb + 1) >> 1;
   // LDS byte addresses as integers from one wave-uniform base (no per-lane
@@ -215,35 +229,47 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
     const int par = wave - kMfmaWaves;
     const uint32_t wrb = a.ldw;
     const uint32_t xrb = (uint32_t)nsb * kQ8_KBytes;
-    // grouped: rows are gathered, offsets from Xq itself (the host keeps
-    // the quantized activation within 32-bit offsets)
-    const uint8_t* xbase = kGroup ? a.Xq : a.Xq + (size_t)m0 * xrb;
-    const uint8_t* wbase = W + (size_t)n0 * wrb;
+    const uint8_t* xbase = a.Xq;
+    const uint8_t* wbase = a.W;
     uint32_t voff[kSlots];
+    // bases and per-lane offsets of tile ti's loads
+    auto setup = [&](const Tile& ti) {
+      // grouped: rows are gathered, offsets from Xq itself (the host keeps
+      // the quantized activation within 32-bit offsets)
+      xbase = kGroup ? a.Xq : a.Xq + (size_t)ti.m0 * xrb;
+      wbase = a.W + ti.w_off + (size_t)ti.n0 * wrb;
+      // activation row of tile row r (r < mrows)
+      auto act_row = [&](int r) -> int {
+        if constexpr (kGroup)
+          return group_act_row(a.grp, ti.m0, r);
+        else
+          return r;
+      };
 #pragma unroll
-    for (int k = 0; k < kSlots; ++k) {
-      uint32_t o;
-      if (k < kAQSlots) {
-        const int q = 64 * k + lane, r = q / 17, c = min(q - 17 * r, 15);
-        o = (uint32_t)(kGroup ? act_row(min(r, mrows - 1)) : min(r, mrows - 1)) * xrb + 4 + 16 * c;
-      } else if (k < kAQSlots + kAXSlots) {
-        const int q = 64 * (k - kAQSlots) + lane, r = q / 3, e = q - 3 * r;
-        o = (uint32_t)(kGroup ? act_row(min(r, mrows - 1)) : min(r, mrows - 1)) * xrb +
-            (e == 0 ? 0 : 244 + 16 * e);
-      } else if constexpr (kIlv) {
-        // line q of the eight 144-line cohort blocks; cohorts past N repeat
-        // the last one (N is a multiple of 16)
-        const int q = 64 * (k - kAQSlots - kAXSlots) + lane, i = q / 144, line = q - 144 * i;
-        o = (uint32_t)(min(n0 + 16 * i, a.N - 16) - n0) * wrb + 16 * line;
-      } else {
-        const int q = 64 * (k - kAQSlots - kAXSlots) + lane, row = q / 9, part = q - 9 * row;
-        o = (uint32_t)(min(n0 + row, a.N - 1) - n0) * wrb + 16 * part;
+      for (int k = 0; k < kSlots; ++k) {
+        uint32_t o;
+        if (k < kAQSlots) {
+          const int q = 64 * k + lane, r = q / 17, c = min(q - 17 * r, 15);
+          o = (uint32_t)act_row(min(r, ti.mrows - 1)) * xrb + 4 + 16 * c;
+        } else if (k < kAQSlots + kAXSlots) {
+          const int q = 64 * (k - kAQSlots) + lane, r = q / 3, e = q - 3 * r;
+          o = (uint32_t)act_row(min(r, ti.mrows - 1)) * xrb + (e == 0 ? 0 : 244 + 16 * e);
+        } else if constexpr (kIlv) {
+          // line q of the eight 144-line cohort blocks; cohorts past N repeat
+          // the last one (N is a multiple of 16)
+          const int q = 64 * (k - kAQSlots - kAXSlots) + lane, i = q / 144, line = q - 144 * i;
+          o = (uint32_t)(min(ti.n0 + 16 * i, a.N - 16) - ti.n0) * wrb + 16 * line;
+        } else {
+          const int q = 64 * (k - kAQSlots - kAXSlots) + lane, row = q / 9, part = q - 9 * row;
+          o = (uint32_t)(min(ti.n0 + row, a.N - 1) - ti.n0) * wrb + 16 * part;
+        }
+        voff[k] = o;
       }
-      voff[k] = o;
-    }
-    auto issue = [&](int pair) {
+    };
+    // superblock 2 pair + par of the current tile into ring slot `slot`
+    auto issue = [&](int pair, int slot) {
       const int b = min(2 * pair + par, nsb - 1);
-      const uint32_t stage = ring_lds + (uint32_t)(2 * (pair & 1) + par) * kStage;
+      const uint32_t stage = ring_lds + (uint32_t)(2 * slot + par) * kStage;
       const uint8_t* xb = xbase + (size_t)b * kQ8_KBytes;
       const uint8_t* wb = wbase + (size_t)b * (kIlv ? kCohortBlock : kQ4_KBytes);
 #pragma unroll
@@ -254,8 +280,8 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
     // (min-term A operand) and the 16-byte d chunk becomes the token-scale
     // operand of the dx (x) dw outer product: bf16 pairs (h,h), (m,m), (l,l),
     // 0 with d = h + m + l to 2^-24.
-    auto convert = [&](int pair) {
-      uint8_t* ax = ring + (2 * (pair & 1) + par) * kStage + kAQ + 48 * lane;
+    auto convert = [&](int slot) {
+      uint8_t* ax = ring + (2 * slot + par) * kStage + kAQ + 48 * lane;
       const uint4 dch = *reinterpret_cast<const uint4*>(ax);
       const uint4 b0 = *reinterpret_cast<const uint4*>(ax + 16);
       const uint4 b1 = *reinterpret_cast<const uint4*>(ax + 32);
@@ -271,16 +297,44 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
       *reinterpret_cast<uint4*>(ax + 32) =
           make_uint4(i16x2_to_f16x2(b1.x), i16x2_to_f16x2(b1.y), i16x2_to_f16x2(b1.z), i16x2_to_f16x2(b1.w));
     };
-    issue(0);
-    for (int pair = 0; pair < npair; ++pair) {
-      __builtin_amdgcn_s_waitcnt(0);  // this pair's stage has landed
-      convert(pair);
-      __syncthreads();                // hand it over; the slot of pair - 1 is free
-      if (pair + 1 < npair) issue(pair + 1);
+    // The pairs of all this workgroup's tiles form one stream over the two
+    // ring slots (pair g in slot g & 1): at the last pair of a tile the next
+    // tile's first pair is issued, so its loads overlap this tile's last
+    // pair and output stage.  Per tile: one barrier per pair, then the two
+    // barriers of the output stage, as the MFMA waves.
+    Tile ti;
+    int t = t_first;
+    while (t < c1 && !tile_info(t, ti)) t += P;
+    if (t >= c1) return;  // no tile: the MFMA waves find none either
+    setup(ti);
+    issue(0, 0);
+    int g = 0;
+    for (;;) {
+      Tile tn;
+      int u = t + P;
+      while (u < c1 && !tile_info(u, tn)) u += P;
+      const bool more = u < c1;
+      for (int pair = 0; pair + 1 < npair; ++pair, ++g) {
+        __builtin_amdgcn_s_waitcnt(0);  // this pair's stage has landed
+        convert(g & 1);
+        __syncthreads();                // hand it over; the slot of pair g - 1 is free
+        issue(pair + 1, (g + 1) & 1);
+      }
+      // the tile's last pair; the next tile's offsets are formed only here
+      // (formed before the loop they would hold a second set of registers)
+      __builtin_amdgcn_s_waitcnt(0);
+      convert(g & 1);
+      __syncthreads();
+      if (more) {
+        setup(tn);
+        issue(0, (g + 1) & 1);
+      }
+      ++g;
+      __syncthreads();  // the output stage's barriers
+      __syncthreads();
+      if (!more) return;
+      t = u;
     }
-    __syncthreads();  // the epilogue's barriers
-    __syncthreads();
-    return;
   }
 
   // ------------------------------------------------------------ MFMA wave
@@ -290,146 +344,152 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
 
   v16i lo[2], hi[2];
   v16f y[2];
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) y[t][r] = 0.f;
-
   const v16i zero = {};
   const v16f fzero = {};
-  for (int pair = 0; pair < npair; ++pair) {
-    __syncthreads();  // the loaders have staged and converted this pair
-    if (2 * pair + par >= nsb) continue;  // odd nsb: the last pair has one superblock
-    const uint8_t* stage = ring + (2 * (pair & 1) + par) * kStage;
-    const uint8_t* AQ = stage + kAQRow * col + 16 * kg;          // + 8704 t + 32 s
-    const uint8_t* AX = stage + kAQ + 48 * col;                   // + 1536 t
-    const uint8_t* wrow = stage + kAQ + kAX + (32 * wcol + col) * kQ4_KBytes;
-    // interleaved: this lane's cohort block and the byte of its row in the
-    // first line of a 16-lane group's window
-    const uint32_t wtr = ring_lds + (uint32_t)(2 * (pair & 1) + par) * kStage + kAQ + kAX +
-                         (uint32_t)(2 * wcol + (col >> 4)) * kCohortBlock + 8 * (lane & 15);
-
-    uint4 h;
-    if constexpr (kIlv) {
-      const uint2 h0 = tr8(wtr), h1 = tr8(wtr + 128);
-      h = make_uint4(h0.x, h0.y, h1.x, h1.y);
-    } else {
-      h = *reinterpret_cast<const uint4*>(wrow);
-    }
-    const float dw = fp16_to_fp32(h.x & 0xffffu);
-    const float dmin = fp16_to_fp32(h.x >> 16);
-    const bool dz = dw == 0.f;
-    const uint32_t sc03 = dz ? 0u : h.y & 0x3f3f3f3fu;
-    const uint32_t sc47 = dz ? 0u : (h.w & 0x0f0f0f0fu) | (((h.y >> 6) & 0x03030303u) << 4);
-    const float f = dz ? dmin : dw;
-    const float nr = dz ? -1.f : -(dmin * __builtin_amdgcn_rcpf(dw));
-    // per sub-block pair, the b (= sc & 7) and a (= sc >> 3) multipliers in
-    // the two 16-bit halves of one register
-    uint32_t cb[4], ca[4];
-    {
-      const uint32_t b03 = sc03 & 0x07070707u, a03 = (sc03 >> 3) & 0x07070707u;
-      const uint32_t b47 = sc47 & 0x07070707u, a47 = (sc47 >> 3) & 0x07070707u;
-      cb[0] = __builtin_amdgcn_perm(0u, b03, 0x0c010c00u);
-      cb[1] = __builtin_amdgcn_perm(0u, b03, 0x0c030c02u);
-      cb[2] = __builtin_amdgcn_perm(0u, b47, 0x0c010c00u);
-      cb[3] = __builtin_amdgcn_perm(0u, b47, 0x0c030c02u);
-      ca[0] = __builtin_amdgcn_perm(0u, a03, 0x0c010c00u);
-      ca[1] = __builtin_amdgcn_perm(0u, a03, 0x0c030c02u);
-      ca[2] = __builtin_amdgcn_perm(0u, a47, 0x0c010c00u);
-      ca[3] = __builtin_amdgcn_perm(0u, a47, 0x0c030c02u);
-    }
-
-    v4i acur[2], anxt[2];
+  int g = 0;  // pairs consumed over this workgroup's tiles: pair g sits in ring slot g & 1
+  for (int t = t_first; t < c1; t += P) {
+    Tile ti;
+    if (!tile_info(t, ti)) continue;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) acur[t] = *reinterpret_cast<const v4i*>(AQ + 32 * kAQRow * t);
+    for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      uint4 q;
+      for (int r = 0; r < 16; ++r) y[t2][r] = 0.f;
+    for (int pair = 0; pair < npair; ++pair, ++g) {
+      __syncthreads();  // the loaders have staged and converted this pair
+      if (2 * pair + par >= nsb) continue;  // odd nsb: the last pair has one superblock
+      const uint8_t* stage = ring + (2 * (g & 1) + par) * kStage;
+      const uint8_t* AQ = stage + kAQRow * col + 16 * kg;          // + 8704 t + 32 s
+      const uint8_t* AX = stage + kAQ + 48 * col;                   // + 1536 t
+      const uint8_t* wrow = stage + kAQ + kAX + (32 * wcol + col) * kQ4_KBytes;
+      // interleaved: this lane's cohort block and the byte of its row in the
+      // first line of a 16-lane group's window
+      const uint32_t wtr = ring_lds + (uint32_t)(2 * (g & 1) + par) * kStage + kAQ + kAX +
+                           (uint32_t)(2 * wcol + (col >> 4)) * kCohortBlock + 8 * (lane & 15);
+
+      uint4 h;
       if constexpr (kIlv) {
-        const uint32_t ql = wtr + 16 * (16 + 32 * g + 16 * kg);
-        const uint2 q0 = tr8(ql), q1 = tr8(ql + 128);
-        q = make_uint4(q0.x, q0.y, q1.x, q1.y);
+        const uint2 h0 = tr8(wtr), h1 = tr8(wtr + 128);
+        h = make_uint4(h0.x, h0.y, h1.x, h1.y);
       } else {
-        q = *reinterpret_cast<const uint4*>(wrow + 16 + 32 * g + 16 * kg);
+        h = *reinterpret_cast<const uint4*>(wrow);
       }
+      const float dw = fp16_to_fp32(h.x & 0xffffu);
+      const float dmin = fp16_to_fp32(h.x >> 16);
+      const bool dz = dw == 0.f;
+      const uint32_t sc03 = dz ? 0u : h.y & 0x3f3f3f3fu;
+      const uint32_t sc47 = dz ? 0u : (h.w & 0x0f0f0f0fu) | (((h.y >> 6) & 0x03030303u) << 4);
+      const float f = dz ? dmin : dw;
+      const float nr = dz ? -1.f : -(dmin * __builtin_amdgcn_rcpf(dw));
+      // per sub-block pair, the b (= sc & 7) and a (= sc >> 3) multipliers in
+      // the two 16-bit halves of one register
+      uint32_t cb[4], ca[4];
+      {
+        const uint32_t b03 = sc03 & 0x07070707u, a03 = (sc03 >> 3) & 0x07070707u;
+        const uint32_t b47 = sc47 & 0x07070707u, a47 = (sc47 >> 3) & 0x07070707u;
+        cb[0] = __builtin_amdgcn_perm(0u, b03, 0x0c010c00u);
+        cb[1] = __builtin_amdgcn_perm(0u, b03, 0x0c030c02u);
+        cb[2] = __builtin_amdgcn_perm(0u, b47, 0x0c010c00u);
+        cb[3] = __builtin_amdgcn_perm(0u, b47, 0x0c030c02u);
+        ca[0] = __builtin_amdgcn_perm(0u, a03, 0x0c010c00u);
+        ca[1] = __builtin_amdgcn_perm(0u, a03, 0x0c030c02u);
+        ca[2] = __builtin_amdgcn_perm(0u, a47, 0x0c010c00u);
+        ca[3] = __builtin_amdgcn_perm(0u, a47, 0x0c030c02u);
+      }
+
+      v4i acur[2], anxt[2];
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        const int s = 2 * g + hf;
-        if (s < 7) {
+      for (int t = 0; t < 2; ++t) acur[t] = *reinterpret_cast<const v4i*>(AQ + 32 * kAQRow * t);
 #pragma unroll
-          for (int t = 0; t < 2; ++t)
-            anxt[t] = *reinterpret_cast<const v4i*>(AQ + 32 * kAQRow * t + 32 * (s + 1));
+      for (int g = 0; g < 4; ++g) {
+        uint4 q;
+        if constexpr (kIlv) {
+          const uint32_t ql = wtr + 16 * (16 + 32 * g + 16 * kg);
+          const uint2 q0 = tr8(ql), q1 = tr8(ql + 128);
+          q = make_uint4(q0.x, q0.y, q1.x, q1.y);
+        } else {
+          q = *reinterpret_cast<const uint4*>(wrow + 16 + 32 * g + 16 * kg);
         }
-        const uint32_t n0w = hf ? (q.x >> 4) & 0x0f0f0f0fu : q.x & 0x0f0f0f0fu;
-        const uint32_t n1w = hf ? (q.y >> 4) & 0x0f0f0f0fu : q.y & 0x0f0f0f0fu;
-        const uint32_t n2w = hf ? (q.z >> 4) & 0x0f0f0f0fu : q.z & 0x0f0f0f0fu;
-        const uint32_t n3w = hf ? (q.w >> 4) & 0x0f0f0f0fu : q.w & 0x0f0f0f0fu;
-        const v2u16 pb = __builtin_bit_cast(v2u16, cb[s >> 1]);
-        const v2u16 pa = __builtin_bit_cast(v2u16, ca[s >> 1]);
-        const v2u16 mb = (s & 1) ? __builtin_shufflevector(pb, pb, 1, 1) : __builtin_shufflevector(pb, pb, 0, 0);
-        const v2u16 ma = (s & 1) ? __builtin_shufflevector(pa, pa, 1, 1) : __builtin_shufflevector(pa, pa, 0, 0);
-        auto mul = [](uint32_t n, v2u16 m) {
-          return (int)__builtin_bit_cast(uint32_t, __builtin_bit_cast(v2u16, n) * m);
-        };
-        const v4i b_lo = {mul(n0w, mb), mul(n1w, mb), mul(n2w, mb), mul(n3w, mb)};
-        const v4i b_hi = {mul(n0w, ma), mul(n1w, ma), mul(n2w, ma), mul(n3w, ma)};
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const int s = 2 * g + hf;
+          if (s < 7) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+              anxt[t] = *reinterpret_cast<const v4i*>(AQ + 32 * kAQRow * t + 32 * (s + 1));
+          }
+          const uint32_t n0w = hf ? (q.x >> 4) & 0x0f0f0f0fu : q.x & 0x0f0f0f0fu;
+          const uint32_t n1w = hf ? (q.y >> 4) & 0x0f0f0f0fu : q.y & 0x0f0f0f0fu;
+          const uint32_t n2w = hf ? (q.z >> 4) & 0x0f0f0f0fu : q.z & 0x0f0f0f0fu;
+          const uint32_t n3w = hf ? (q.w >> 4) & 0x0f0f0f0fu : q.w & 0x0f0f0f0fu;
+          const v2u16 pb = __builtin_bit_cast(v2u16, cb[s >> 1]);
+          const v2u16 pa = __builtin_bit_cast(v2u16, ca[s >> 1]);
+          const v2u16 mb = (s & 1) ? __builtin_shufflevector(pb, pb, 1, 1) : __builtin_shufflevector(pb, pb, 0, 0);
+          const v2u16 ma = (s & 1) ? __builtin_shufflevector(pa, pa, 1, 1) : __builtin_shufflevector(pa, pa, 0, 0);
+          auto mul = [](uint32_t n, v2u16 m) {
+            return (int)__builtin_bit_cast(uint32_t, __builtin_bit_cast(v2u16, n) * m);
+          };
+          const v4i b_lo = {mul(n0w, mb), mul(n1w, mb), mul(n2w, mb), mul(n3w, mb)};
+          const v4i b_hi = {mul(n0w, ma), mul(n1w, ma), mul(n2w, ma), mul(n3w, ma)};
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            lo[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(acur[t], b_lo, s == 0 ? zero : lo[t], 0, 0, 0);
+            hi[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(acur[t], b_hi, s == 0 ? zero : hi[t], 0, 0, 0);
+          }
+#pragma unroll
+          for (int t = 0; t < 2; ++t) acur[t] = anxt[t];
+        }
+      }
+
+      // min term (f16: converted bsums x duplicated mins) and the dx (x) f
+      // outer product (bf16: token-scale splits x f = f_h + f_l, exact)
+      v16f mn[2], qd[2];
+      {
+        const uint32_t mn03 = h.z & 0x3f3f3f3fu;
+        const uint32_t mn47 = ((h.w >> 4) & 0x0f0f0f0fu) | (((h.z >> 6) & 0x03030303u) << 4);
+        const uint32_t mw = kg ? mn47 : mn03;
+        const v4i bm = {(int)dup_byte_f16x2(mw, 0), (int)dup_byte_f16x2(mw, 1),
+                        (int)dup_byte_f16x2(mw, 2), (int)dup_byte_f16x2(mw, 3)};
+        const uint32_t pfh = pk_bf16(f, f);
+        const uint32_t pf = kg ? 0u : pk_bf16(f, f - bf16_lo_to_f32(pfh));
+        const v4i bq = {(int)pf, (int)pf, (int)pf, 0};
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-          lo[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(acur[t], b_lo, s == 0 ? zero : lo[t], 0, 0, 0);
-          hi[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(acur[t], b_hi, s == 0 ? zero : hi[t], 0, 0, 0);
+          const v4i am = *reinterpret_cast<const v4i*>(AX + 1536 * t + 16 + 16 * kg);
+          mn[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, am),
+                                                        __builtin_bit_cast(v8h, bm), fzero, 0, 0, 0);
+          const uint32_t qaddr = kg ? zaddr : lds_addr(AX + 1536 * t);
+          const v4i aq = *(const __attribute__((address_space(3))) v4i*)(size_t)qaddr;
+          qd[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aq),
+                                                         __builtin_bit_cast(v8bf, bq), fzero, 0, 0, 0);
         }
-#pragma unroll
-        for (int t = 0; t < 2; ++t) acur[t] = anxt[t];
       }
+      // y += (dx f) (lo + 8 hi - r Mn)
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float d = fmaf(mn[t][r], nr, (float)(lo[t][r] + 8 * hi[t][r]));
+          y[t][r] = fmaf(d, qd[t][r], y[t][r]);
+        }
     }
 
-    // min term (f16: converted bsums x duplicated mins) and the dx (x) f
-    // outer product (bf16: token-scale splits x f = f_h + f_l, exact)
-    v16f mn[2], qd[2];
-    {
-      const uint32_t mn03 = h.z & 0x3f3f3f3fu;
-      const uint32_t mn47 = ((h.w >> 4) & 0x0f0f0f0fu) | (((h.z >> 6) & 0x03030303u) << 4);
-      const uint32_t mw = kg ? mn47 : mn03;
-      const v4i bm = {(int)dup_byte_f16x2(mw, 0), (int)dup_byte_f16x2(mw, 1),
-                      (int)dup_byte_f16x2(mw, 2), (int)dup_byte_f16x2(mw, 3)};
-      const uint32_t pfh = pk_bf16(f, f);
-      const uint32_t pf = kg ? 0u : pk_bf16(f, f - bf16_lo_to_f32(pfh));
-      const v4i bq = {(int)pf, (int)pf, (int)pf, 0};
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const v4i am = *reinterpret_cast<const v4i*>(AX + 1536 * t + 16 + 16 * kg);
-        mn[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, am),
-                                                      __builtin_bit_cast(v8h, bm), fzero, 0, 0, 0);
-        const uint32_t qaddr = kg ? zaddr : lds_addr(AX + 1536 * t);
-        const v4i aq = *(const __attribute__((address_space(3))) v4i*)(size_t)qaddr;
-        qd[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aq),
-                                                       __builtin_bit_cast(v8bf, bq), fzero, 0, 0, 0);
-      }
-    }
-    // y += (dx f) (lo + 8 hi - r Mn)
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float d = fmaf(mn[t][r], nr, (float)(lo[t][r] + 8 * hi[t][r]));
-        y[t][r] = fmaf(d, qd[t][r], y[t][r]);
-      }
+    // Both parities' partial sums -> two LDS planes in the slot of the tile's
+    // last pair (the other slot may already be receiving the next tile) -> Y.
+    // The first barrier: every wave is done reading that slot.
+    __syncthreads();
+    float* planes = reinterpret_cast<float*>(ring + 2 * ((g - 1) & 1) * kStage);
+    tile_partials_to_lds(y, wcol, lane, planes + par * (kTilePlaneBytes / 4));
+    __syncthreads();
+    tile_store_from_lds(
+        wave, lane, planes, planes + kTilePlaneBytes / 4, ti.mrows, min(kNT, a.N - ti.n0),
+        [&](int rr) {
+          if constexpr (kGroup)
+            return a.Y + group_dst_row(a.grp, ti.m0, rr) + ti.n0;
+          else
+            return a.Y + (size_t)(ti.m0 + rr) * a.ldy + ti.n0;
+        },
+        [](float e, float o) { return e + o; });
   }
-
-  // both parities' partial sums -> two LDS planes (reusing the ring) -> Y
-  __syncthreads();
-  float* planes = reinterpret_cast<float*>(ring);
-  tile_partials_to_lds(y, wcol, lane, planes + par * (kTilePlaneBytes / 4));
-  __syncthreads();
-  tile_store_from_lds(
-      wave, lane, planes, planes + kTilePlaneBytes / 4, mrows, min(kNT, a.N - n0),
-      [&](int rr) {
-        if constexpr (kGroup)
-          return a.Y + group_dst_row(a.grp, m0, rr) + n0;
-        else
-          return a.Y + (size_t)(m0 + rr) * a.ldy + n0;
-      },
-      [](float e, float o) { return e + o; });
 }
 
 // The GEMM over an already quantized activation.  Weight rows must be
@@ -456,8 +516,11 @@ void gemm_q4k(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K,
   a.M = (int)M;
   a.ldw = (uint32_t)(N > 1 ? st.ldw : rb);
   a.ldy = (long long)st.ldy;
+  // one workgroup per CU at most (the ring takes the CU's LDS); each walks
+  // its share of the tiles
   const size_t tiles = ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT);
-  q4k_mfma_gemm<false, kIlv><<<dim3((unsigned)tiles), kThreads, 0, current_stream()>>>(a);
+  const size_t wgs = std::min(tiles, (size_t)cu_count());
+  q4k_mfma_gemm<false, kIlv><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(a);
   check_launch("q4k_mfma_gemm");
 }
 
@@ -505,7 +568,8 @@ void mul_mat_id_q4k_grouped(const uint8_t* W, const uint8_t* Xq, float* Y, size_
   a.M = kMT;
   a.ldw = (uint32_t)(N > 1 ? st.ldw : rb);
   a.grp = group_tiles(g, pr);
-  const size_t wgs = (size_t)g.tmax * ((N + kNT - 1) / kNT);
+  const size_t tiles = (size_t)g.tmax * ((N + kNT - 1) / kNT);
+  const size_t wgs = std::min(tiles, (size_t)cu_count());
   q4k_mfma_gemm<true><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(a);
   check_launch("q4k_mfma_gemm");
 }
