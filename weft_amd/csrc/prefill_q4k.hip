@@ -64,8 +64,8 @@
 // (moe_group_kernel: a pair list per expert and a table of 64-row tiles), and
 // each (tile, column block) runs the same GEMM on its tile's pairs: the
 // loader gathers their activation rows through the pair list, W is the
-// tile's expert matrix, and each output goes to the pair's dst row.  Tile
-// slots past the device's tile count are skipped.
+// tile's expert matrix, and each output goes to the pair's dst row.  The
+// workgroups walk the device's tile count (launched for the host's bound).
 #include <algorithm>
 
 #include "kernels.h"
@@ -188,10 +188,12 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
   if (tid < 4) zero16[tid] = 0u;
   // Tile t of the launch: m-tile fastest (dense) or expert tile fastest
-  // (grouped: m0 then indexes the pair list).  False for a grouped tile past
-  // the device's tile count.  Every wave enumerates the same tiles.
+  // (grouped: m0 then indexes the pair list, and the tiles are the device's
+  // tile count, not the host's bound, so the schedule below spreads only real
+  // tiles).  Every wave enumerates the same tiles.
   const int ntn = (a.N + kNT - 1) / kNT;
-  const int ntm = kGroup ? a.grp.tmax : (a.M + kMT - 1) / kMT;
+  const int ntm =
+      kGroup ? min(__builtin_amdgcn_readfirstlane(*a.grp.ntiles), a.grp.tmax) : (a.M + kMT - 1) / kMT;
   auto tile_info = [&](int t, Tile& ti) -> bool {
     if constexpr (kGroup) {
       if (!group_tile(a.grp, t % ntm, ti.m0, ti.mrows, ti.w_off)) return false;
