@@ -271,6 +271,16 @@ def test_prefill_q4_k_config4_n11008(hip):
     check_mul_mat("q4_k", w, x, xq, y, n, k, m)
 
 
+@pytest.mark.parametrize("n,k,m", [(32900, 768, 70), (16500, 1536, 130)])
+def test_prefill_q4_k_several_tiles_per_workgroup(hip, n, k, m):
+    # more 64 x 128 tiles than a launch has workgroups (one per CU), so each
+    # workgroup walks several: partial last token and weight tiles, an odd
+    # superblock count (K = 768) and an odd pair count (K = 1536) across the
+    # tile boundaries of the ring
+    w, x, xq, y = run_mul_mat(hip, "production_mul_mat_q4_k_staged", "q4_k", n, k, m)
+    check_mul_mat("q4_k", w, x, xq, y, n, k, m)
+
+
 @pytest.mark.parametrize("fmt", ["mxfp4", "q4_0", "iq2_xxs"])
 def test_prefill_config5b(hip, fmt):
     """BASELINE config 5b (MXFP4, 512 x 4096 x 4096; Q4_0 and IQ2_XXS at the

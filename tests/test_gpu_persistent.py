@@ -72,7 +72,7 @@ def test_persistent_matches_fp64(hip, n, k, m):
     check(w, x, xq, y, n, k, m)
 
 
-@pytest.mark.parametrize("n,k,m", [(4096, 4096, 512), (144, 768, 70)])
+@pytest.mark.parametrize("n,k,m", [(4096, 4096, 512), (144, 768, 70), (32784, 768, 70)])
 def test_persistent_gemm_equals_row_major_gemm(hip, n, k, m):
     w = o.quantize("q4_k", o.seeded_normal(5, (n, k), 0.02))
     x = o.seeded_normal(6, (m, k))
