@@ -240,10 +240,14 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
       // the quantized activation within 32-bit offsets)
       xbase = kGroup ? a.Xq : a.Xq + (size_t)ti.m0 * xrb;
       wbase = a.W + ti.w_off + (size_t)ti.n0 * wrb;
-      // activation row of tile row r (r < mrows)
+      // activation row of tile row r (r < mrows); grouped: lane r looks up
+      // row r once and the other lanes fetch it by cross-lane permute (one
+      // pair-list load and division per lane instead of one per offset)
+      int lane_row = 0;
+      if constexpr (kGroup) lane_row = group_act_row(a.grp, ti.m0, min(lane, ti.mrows - 1));
       auto act_row = [&](int r) -> int {
         if constexpr (kGroup)
-          return group_act_row(a.grp, ti.m0, r);
+          return __shfl(lane_row, r);
         else
           return r;
       };
@@ -482,11 +486,24 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
     float* planes = reinterpret_cast<float*>(ring + 2 * ((g - 1) & 1) * kStage);
     tile_partials_to_lds(y, wcol, lane, planes + par * (kTilePlaneBytes / 4));
     __syncthreads();
+    // grouped: lane r looks up the dst row of tile row r; the two rows this
+    // lane stores are fetched by cross-lane permute here, where every lane
+    // is active (inside the store's row checks some lanes are not)
+    long long dst_lo = 0, dst_hi = 0;
+    if constexpr (kGroup) {
+      const long long own = group_dst_row(a.grp, ti.m0, min(lane, ti.mrows - 1));
+      auto fetch = [&](int src) {
+        return (long long)(((uint64_t)(uint32_t)__shfl((int)(own >> 32), src) << 32) |
+                           (uint32_t)__shfl((int)(own & 0xffffffff), src));
+      };
+      dst_lo = fetch(tile_store_row(wave, lane, 0));
+      dst_hi = fetch(tile_store_row(wave, lane, 1));
+    }
     tile_store_from_lds(
         wave, lane, planes, planes + kTilePlaneBytes / 4, ti.mrows, min(kNT, a.N - ti.n0),
         [&](int rr) {
           if constexpr (kGroup)
-            return a.Y + group_dst_row(a.grp, ti.m0, rr) + ti.n0;
+            return a.Y + (rr < 32 ? dst_lo : dst_hi) + ti.n0;
           else
             return a.Y + (size_t)(ti.m0 + rr) * a.ldy + ti.n0;
         },

@@ -41,6 +41,10 @@ __device__ inline void tile_partials_to_lds(const tile_v16f (&y)[2], int wcol, i
     }
 }
 
+// The tile row that lane `lane` of wave `wave` stores in pass p (0, 1) of
+// tile_store_from_lds.
+__device__ inline int tile_store_row(int wave, int lane, int p) { return 32 * p + 4 * wave + (lane >> 4); }
+
 // After a barrier that follows every wave's tile_partials_to_lds: wave w
 // (0..7) stores tile rows 4 w + lane / 16 and 32 + 4 w + lane / 16, columns
 // 4 (lane % 16) + 64 k (k = 0, 1), as fin(even, odd) per value.  Rows past
@@ -53,7 +57,7 @@ __device__ inline void tile_store_from_lds(int wave, int lane, const float* even
   const int c0 = 4 * (lane & 15);
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
-    const int rr = 32 * p + 4 * wave + (lane >> 4);
+    const int rr = tile_store_row(wave, lane, p);
     if (rr >= mrows) continue;
     float* dst = row_ptr(rr);
 #pragma unroll
