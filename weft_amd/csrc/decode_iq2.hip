@@ -14,7 +14,8 @@
 // aligned dword below them: a record is 2-byte aligned), the superblock's d
 // and, for IQ2_XS, the two groups' scale bytes.  Its 64 activation values
 // (the same for every row) are read from LDS into VGPRs once.  Grid rows and
-// sign bytes come from LDS tables; products run on v_dot4_i32_i8.  A
+// sign masks (the +-1 sign table turned into 0xff / 0x00 byte masks as it
+// is staged) come from LDS tables; products run on v_dot4_i32_i8.  A
 // superblock's exact integer sum is the sum over its four lanes (DPP), then
 // one fp32 term per superblock and a wave sum per row.  A wave walks its
 // rows with one row of lookahead.  The activation is quantized in every
@@ -46,10 +47,13 @@ struct Iq2Args {
   size_t ldw;
 };
 
-// negate the bytes of g whose sign byte in s is -1 (bit 7 set): bytes of g
-// are in [0, 43], so (b ^ 0xff) + 1 never carries into the next byte
-__device__ __forceinline__ int iq2_signed(uint32_t g, uint32_t s) {
-  const uint32_t m = ((s >> 7) & 0x01010101u) * 0xffu;
+// four +-1 sign bytes -> byte masks (0xff where -1, bit 7 set), as the sign
+// table is held in LDS
+__device__ __forceinline__ uint32_t iq2_sign_mask(uint32_t s) { return ((s >> 7) & 0x01010101u) * 0xffu; }
+
+// negate the bytes of g whose mask byte in m is 0xff: bytes of g are in
+// [0, 43], so (b ^ 0xff) + 1 never carries into the next byte
+__device__ __forceinline__ int iq2_negate(uint32_t g, uint32_t m) {
   return (int)((g ^ m) + (m & 0x01010101u));
 }
 
@@ -105,7 +109,7 @@ __global__ void __launch_bounds__(kThreads) iq2_gemv_m1_kernel(Iq2Args a) {
   for (int i = threadIdx.x; i < kGridBytes / 4; i += kThreads)
     reinterpret_cast<uint32_t*>(tgrid)[i] = reinterpret_cast<const uint32_t*>(a.grid)[i];
   for (int i = threadIdx.x; i < 256; i += kThreads)
-    reinterpret_cast<uint32_t*>(tsign)[i] = reinterpret_cast<const uint32_t*>(a.signs)[i];
+    reinterpret_cast<uint32_t*>(tsign)[i] = iq2_sign_mask(reinterpret_cast<const uint32_t*>(a.signs)[i]);
   stager.finish(a.X, (size_t)K, blockIdx.x == 0 ? a.xq_out : nullptr, K, 0, 1, act);
   __syncthreads();
 
@@ -143,8 +147,8 @@ __global__ void __launch_bounds__(kThreads) iq2_gemv_m1_kernel(Iq2Args a) {
           gv = grid[(q[2 * u] >> (8 * l)) & 0xffu];
           sv = sgn[(q[2 * u + 1] >> (7 * l)) & 127u];
         }
-        part[l >> 1] = dot4(iq2_signed(gv.x, sv.x), xv[2 * l], part[l >> 1]);
-        part[l >> 1] = dot4(iq2_signed(gv.y, sv.y), xv[2 * l + 1], part[l >> 1]);
+        part[l >> 1] = dot4(iq2_negate(gv.x, sv.x), xv[2 * l], part[l >> 1]);
+        part[l >> 1] = dot4(iq2_negate(gv.y, sv.y), xv[2 * l + 1], part[l >> 1]);
       }
       if constexpr (kXs) {
         const uint32_t sb8 = (buf.s >> (8 * u)) & 0xffu;
