@@ -212,9 +212,12 @@ __device__ __forceinline__ int lookup16(uint32_t n, uint32_t c0, uint32_t c1, ui
   return (int)((hi & mask) | (lo & ~mask));
 }
 
-// negate the bytes of g (grid magnitudes 8..43) where the sign byte is -1
-__device__ __forceinline__ int apply_signs(uint32_t g, uint32_t s) {
-  const uint32_t m = ((s >> 7) & 0x01010101u) * 0xffu;
+// four +-1 sign bytes -> byte masks (0xff where -1), as the sign table is
+// staged in LDS
+__device__ __forceinline__ uint32_t sign_mask4(uint32_t s) { return ((s >> 7) & 0x01010101u) * 0xffu; }
+
+// negate the bytes of g (grid magnitudes 8..43) where the mask byte is 0xff
+__device__ __forceinline__ int apply_signs(uint32_t g, uint32_t m) {
   return (int)((g ^ m) + (m & 0x01010101u));
 }
 
@@ -233,19 +236,19 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
   const int K = a.K;
 
   if constexpr (F == Fmt::IQ2_XXS) {
-    // grid I8X8[256x8] then signs I8X8[128x8]
+    // grid I8X8[256x8] then signs I8X8[128x8] as byte masks
     for (int i = threadIdx.x; i < 512; i += blockDim.x)
       reinterpret_cast<uint32_t*>(tables)[i] = reinterpret_cast<const uint32_t*>(a.tab0)[i];
     for (int i = threadIdx.x; i < 256; i += blockDim.x)
       reinterpret_cast<uint32_t*>(tables + 2048)[i] =
-          reinterpret_cast<const uint32_t*>(a.tab1)[i];
+          sign_mask4(reinterpret_cast<const uint32_t*>(a.tab1)[i]);
   } else if constexpr (F == Fmt::IQ2_XS) {
-    // grid I8X8[512x8] then signs I8X8[128x8]
+    // grid I8X8[512x8] then signs I8X8[128x8] as byte masks
     for (int i = threadIdx.x; i < 1024; i += blockDim.x)
       reinterpret_cast<uint32_t*>(tables)[i] = reinterpret_cast<const uint32_t*>(a.tab0)[i];
     for (int i = threadIdx.x; i < 256; i += blockDim.x)
       reinterpret_cast<uint32_t*>(tables + 4096)[i] =
-          reinterpret_cast<const uint32_t*>(a.tab1)[i];
+          sign_mask4(reinterpret_cast<const uint32_t*>(a.tab1)[i]);
   } else if constexpr (F == Fmt::MXFP4 || F == Fmt::NVFP4) {
     for (int i = threadIdx.x; i < 256; i += blockDim.x)
       reinterpret_cast<float*>(tables)[i] = reinterpret_cast<const float*>(a.tab1)[i];

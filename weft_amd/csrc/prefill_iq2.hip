@@ -94,10 +94,10 @@ __device__ __forceinline__ uint32_t ld32(const uint8_t* p) {
 // live.  (It emits nothing, so the compiler still places the wait states a
 // VALU read of an MFMA result needs.)
 __device__ __forceinline__ void pin(int& v) { asm volatile("" : "+v"(v)); }
-// negate the bytes of g whose sign byte in s is -1 (bit 7 set): bytes of g
+// negate the bytes of g whose mask byte in m is 0xff (the sign table is
+// staged in LDS as byte masks: 0xff where the +-1 byte is -1): bytes of g
 // are in [0, 43], so (b ^ 0xff) + 1 never carries into the next byte
-__device__ __forceinline__ uint32_t apply_signs(uint32_t g, uint32_t s) {
-  const uint32_t m = ((s >> 7) & 0x01010101u) * 0xffu;
+__device__ __forceinline__ uint32_t apply_signs(uint32_t g, uint32_t m) {
   return (g ^ m) + (m & 0x01010101u);
 }
 
@@ -154,7 +154,7 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
   };
 
   for (int i = tid; i < TT::kGrid * 8; i += kThreads) tgrid[i] = (uint8_t)a.grid[i];
-  for (int i = tid; i < 128 * 8; i += kThreads) tsign[i] = (uint8_t)a.signs[i];
+  for (int i = tid; i < 128 * 8; i += kThreads) tsign[i] = a.signs[i] < 0 ? 0xffu : 0u;  // byte masks
 
   // activation int8 of superblock 2*pair + par: 16 wave-wide 16-byte loads, 4 per wave
   const uint8_t* asrc[4];
