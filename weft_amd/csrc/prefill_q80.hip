@@ -45,6 +45,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
 enum class WFmt { Q4_0, MXFP4, Q4_1, NVFP4 };
@@ -270,6 +271,7 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
 
   v16i I[2];
   v16f y[2];
+  const v16f fzero = {};
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -343,13 +345,13 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
           q3 = __builtin_amdgcn_alignbyte(w4, w3, sh);
         }
         // header byte(s) just before the nibbles
-        float wsc;
+        float wsc = 0.f;
+        uint32_t wbits = 0;  // Q4_0 / Q4_1: the fp16 scale's bits
         if constexpr (F == WFmt::Q4_1) {
           const uint32_t hd = ld32(wrow + T::kRec * j);  // records are 4-byte aligned here
-          wsc = fp16_to_fp32(hd & 0xffffu);
+          wbits = hd & 0xffffu;
         } else if constexpr (F == WFmt::Q4_0) {
-          const uint32_t dbits = sh >= 2 ? (w0 & 0xffffu) : (ld32(wrow + b4 - 4) >> 16);
-          wsc = fp16_to_fp32(dbits);
+          wbits = sh >= 2 ? (w0 & 0xffffu) : (ld32(wrow + b4 - 4) >> 16);
         } else {
           const uint32_t e = sh >= 1 ? ((w0 >> (8 * (sh - 1))) & 0xffu) : (ld32(wrow + b4 - 4) >> 24);
           wsc = scl[e];
@@ -373,19 +375,41 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
           const v4i av = *reinterpret_cast<const v4i*>(AQ + (32 * t + col) * 256 + 16 * chunk);
           I[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, zero, 0, 0, 0);
         }
-        // y += (dx * ws) * I; register r of a tile holds token 8*(r/4) + 4*kg + r%4
+        if constexpr (F == WFmt::Q4_0 || F == WFmt::Q4_1) {
+          // y += (dx dw) I with the factor dx dw of every output from one f16
+          // MFMA per tile as an outer product: K slot 0 holds the token's dx
+          // and the row's dw (both fp16, so each product is exact in fp32,
+          // as the VALU product it replaces), every other slot 0
+          // (operands as raw bits: the kg half's slots are zero without a branch)
+          const uint32_t kmask = kg ? 0u : 0xffffu;
+          const v2u bq = {wbits & kmask, 0u};
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+          for (int t = 0; t < 2; ++t) {
+            const _Float16 dxh = (_Float16)dxs[j * kMT + 32 * t + col];
+            const v2u aq = {(uint32_t)__builtin_bit_cast(uint16_t, dxh) & kmask, 0u};
+            const v16f qd = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, aq), __builtin_bit_cast(v4h, bq),
+                                                                fzero, 0, 0, 0);
 #pragma unroll
-          for (int r4 = 0; r4 < 4; ++r4) {
-            const float4 d4 = *reinterpret_cast<const float4*>(dxs + j * kMT + 32 * t + 8 * r4 + 4 * kg);
-            const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const int r = 4 * r4 + q;
-              y[t][r] += (dv[q] * wsc) * (float)I[t][r];
-            }
+            for (int r = 0; r < 16; ++r) y[t][r] = fmaf(qd[r], (float)I[t][r], y[t][r]);
           }
+          // keep the blocks' factor MFMAs in block order (hoisted, their
+          // results would hold registers across the whole stage)
+          __builtin_amdgcn_sched_barrier(0);
+        } else {
+          // y += (dx * ws) * I; register r of a tile holds token 8*(r/4) + 4*kg + r%4
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+              const float4 d4 = *reinterpret_cast<const float4*>(dxs + j * kMT + 32 * t + 8 * r4 + 4 * kg);
+              const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                const int r = 4 * r4 + q;
+                y[t][r] += (dv[q] * wsc) * (float)I[t][r];
+              }
+            }
+        }
       }
       if constexpr (F == WFmt::Q4_1) {
         // Q4_1's min term, m s per block (ggml-cpu/quants.c:241), for the
