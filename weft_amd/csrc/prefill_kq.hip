@@ -50,6 +50,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
 constexpr int kMT = 64;        // tokens per workgroup tile
@@ -124,7 +125,9 @@ __global__ void __launch_bounds__(kThreads, 1) kq_mfma_gemm(GemmArgs a) {
   constexpr int kRowB = TT::kRowB, kLoadD = TT::kLoadD, kWSlots = TT::kWSlots;
   __shared__ __align__(16) uint8_t ring0[TT::kSlot];
   __shared__ __align__(16) uint8_t ring1[TT::kSlot];
-  __shared__ __align__(16) float dxs[2][kMT];  // [slot][token]
+  // [slot][token]: the token's Q8_K d as the bf16 parts of the outer-product
+  // factor MFMA ((h,h), (m,m), (l,l), 0)
+  __shared__ __align__(16) uint4 dxq[2][kMT];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -220,7 +223,7 @@ __global__ void __launch_bounds__(kThreads, 1) kq_mfma_gemm(GemmArgs a) {
     }
     const uint8_t* AQ = cur;
     const uint8_t* row = cur + kAQ + TT::kBS + (32 * wcol + col) * kRowB;  // this lane's weight row
-    const float* dx = &dxs[b & 1][0];
+    const uint4* dxb = &dxq[b & 1][0];
     float dw, dmin = 0.f;
     v16f mn[2];
     if constexpr (k6) {
@@ -318,28 +321,42 @@ __global__ void __launch_bounds__(kThreads, 1) kq_mfma_gemm(GemmArgs a) {
         mn[t] = __builtin_amdgcn_mfma_f32_32x32x8f16(am, bm, fz, 0, 0, 0);
       }
     }
-    // y += (dw dx) * acc [- (dmin dx) * Mn]; register r of a tile holds token
-    // 8 (r / 4) + 4 kg + r % 4
+    // y += (dx dw) acc [- (dx dmin) Mn]: the factors of every output from a
+    // bf16 outer-product MFMA per tile (token d = h + m + l against the
+    // row's fp16 scale = f_h + f_l, K slots 0-5 of the kg = 0 lanes; the
+    // kg = 1 lanes' slots are zero), then two VALU operations per output
+    const uint32_t kz = kg ? 0u : 0xffffffffu;
+    const uint32_t pw = bf16_split2(dw) & kz;
+    const v4i bw = {(int)pw, (int)pw, (int)pw, 0};
+    v4i bm = {};
+    if constexpr (!k6) {
+      const uint32_t pm = bf16_split2(dmin) & kz;
+      bm = (v4i){(int)pm, (int)pm, (int)pm, 0};
+    }
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < 2; ++t) {
+      const uint4 d4 = dxb[32 * t + col];
+      const v4i aq = {(int)(d4.x & kz), (int)(d4.y & kz), (int)(d4.z & kz), 0};
+      const v16f fz = {};
+      const v16f qw = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aq),
+                                                             __builtin_bit_cast(v8bf, bw), fz, 0, 0, 0);
+      if constexpr (k6) {
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const float4 d4 = *reinterpret_cast<const float4*>(dx + 32 * t + 8 * r4 + 4 * kg);
-        const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+        for (int r = 0; r < 16; ++r) y[t][r] = fmaf(qw[r], (float)acc[t][r], y[t][r]);
+      } else {
+        const v16f qm = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aq),
+                                                               __builtin_bit_cast(v8bf, bm), fz, 0, 0, 0);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int r = 4 * r4 + q;
-          y[t][r] += (dw * dv[q]) * (float)acc[t][r];
-          if constexpr (!k6) y[t][r] -= (dmin * dv[q]) * mn[t][r];
-        }
+        for (int r = 0; r < 16; ++r) y[t][r] = fmaf(-qm[r], mn[t][r], fmaf(qw[r], (float)acc[t][r], y[t][r]));
       }
-    if (refill && wave == 0) dxs[(b + 1) & 1][lane] = dxr;  // slot last read a superblock ago
+    }
+    if (refill && wave == 0) dxq[(b + 1) & 1][lane] = bf16_split3(dxr);  // slot last read a superblock ago
   };
 
   issue(0, 0);
   if (wave == 0) {
     load_dx(0);
-    dxs[0][lane] = dxr;
+    dxq[0][lane] = bf16_split3(dxr);
   }
   for (int b = 0; b < nsb; b += 2) {
     step(b, ring0, 1, std::integral_constant<int, 0>{});

@@ -155,13 +155,6 @@ __device__ __forceinline__ uint32_t dup_byte_f16x2(uint32_t w, int i) {
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
-// fp32 -> two bf16 (round to nearest even) packed low | high << 16
-__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
-  typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
-  const v2bf v = {(__bf16)lo, (__bf16)hi};
-  return __builtin_bit_cast(uint32_t, v);
-}
-__device__ __forceinline__ float bf16_lo_to_f32(uint32_t p) { return __uint_as_float(p << 16); }
 
 // Eight bytes of row (lane % 16) from eight consecutive 16-byte lines of an
 // interleaved cohort block: lane i of each 16-lane group addresses byte 8 i

@@ -36,6 +36,31 @@ __device__ __forceinline__ float fp16_to_fp32(uint32_t h) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
+// fp32 -> two bf16 (round to nearest even) packed low | high << 16, and the
+// low one back as fp32.  An outer-product factor dx * f is formed on a bf16
+// MFMA from dx = h + m + l (bf16 parts, exact to 2^-24 relative) and an fp16
+// f = f_h + f_l (exactly two bf16 parts): six exact products summed in fp32.
+__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
+  typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+  const v2bf v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ float bf16_lo_to_f32(uint32_t p) { return __uint_as_float(p << 16); }
+
+// the token-side operand of that product: (h,h), (m,m), (l,l), 0 for d
+__device__ __forceinline__ uint4 bf16_split3(float d) {
+  const uint32_t ph = pk_bf16(d, d);
+  const float r1 = d - bf16_lo_to_f32(ph);
+  const uint32_t pm = pk_bf16(r1, r1);
+  const float r2 = r1 - bf16_lo_to_f32(pm);
+  return make_uint4(ph, pm, pk_bf16(r2, r2), 0u);
+}
+
+// the row-side operand: (f_h, f_l) for an fp16 value f, three times, then 0
+__device__ __forceinline__ uint32_t bf16_split2(float f) {
+  return pk_bf16(f, f - bf16_lo_to_f32(pk_bf16(f, f)));
+}
+
 // IEEE binary32 -> binary16, round to nearest even; NaN -> 0x7E00 (sign
 // kept), as GGML's software conversion (ggml-impl.h:407-431).
 __device__ __forceinline__ uint32_t fp32_to_fp16(float f) {
