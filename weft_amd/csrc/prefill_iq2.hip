@@ -32,6 +32,7 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
 constexpr int kMT = 64;        // tokens per workgroup tile
@@ -113,7 +114,9 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
   constexpr int kPairB = TT::kPairB, kWD = TT::kWD, kWSlots = TT::kWSlots;
   __shared__ __align__(16) uint8_t ring0[TT::kSlotAlloc];
   __shared__ __align__(16) uint8_t ring1[TT::kSlotAlloc];
-  __shared__ __align__(16) float dxs[2][2][kMT];  // [slot][parity][token]
+  // [slot][parity][token]: the token's Q8_K d as the bf16 parts of the
+  // outer-product factor MFMA ((h,h), (m,m), (l,l), 0)
+  __shared__ __align__(16) uint4 dxq[2][2][kMT];
   __shared__ __align__(16) uint8_t tgrid[TT::kGrid * 8];
   __shared__ __align__(16) uint8_t tsign[128 * 8];
 
@@ -212,7 +215,7 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
     }
     const uint8_t* AQ = cur + par * kAQ;
     const uint8_t* rec = cur + 2 * kAQ + (32 * wcol + col) * kPairB + sb0;
-    const float* dx = &dxs[pair & 1][par][0];
+    const uint4* dxb = &dxq[pair & 1][par][0];
     // fp16 d: bytes 0-1 of the record (rec is 4-byte aligned for parity 0,
     // 2 past an aligned dword for parity 1)
     const uint32_t dword0 = ld32(rec - 2 * par);
@@ -288,26 +291,30 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
           acc[t][r] = v;
         }
     }
-    // y += (dw * dx) * acc; register r of a tile holds token 8*(r/4) + 4*kg + r%4
+    // y += (dx dw) acc: the factor of every output from a bf16 outer-product
+    // MFMA per tile (token d = h + m + l against the row's fp16 dw = f_h +
+    // f_l in K slots 0-5 of the kg = 0 lanes), then two VALU operations per
+    // output
+    const uint32_t kz = kg ? 0u : 0xffffffffu;
+    const uint32_t pw = bf16_split2(dw) & kz;
+    const v4i bw = {(int)pw, (int)pw, (int)pw, 0};
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < 2; ++t) {
+      const uint4 d4 = dxb[32 * t + col];
+      const v4i aq = {(int)(d4.x & kz), (int)(d4.y & kz), (int)(d4.z & kz), 0};
+      const v16f fz = {};
+      const v16f qw = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aq),
+                                                             __builtin_bit_cast(v8bf, bw), fz, 0, 0, 0);
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const float4 d4 = *reinterpret_cast<const float4*>(dx + 32 * t + 8 * r4 + 4 * kg);
-        const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int r = 4 * r4 + q;
-          y[t][r] += (dw * dv[q]) * (float)acc[t][r];
-        }
-      }
-    if (refill && wcol == 0) dxs[(pair + 1) & 1][par][lane] = dxr;  // slot last read a pair ago
+      for (int r = 0; r < 16; ++r) y[t][r] = fmaf(qw[r], (float)acc[t][r], y[t][r]);
+    }
+    if (refill && wcol == 0) dxq[(pair + 1) & 1][par][lane] = bf16_split3(dxr);  // slot last read a pair ago
   };
 
   issue(0, ring0);
   if (wcol == 0) {
     load_dx(0);
-    dxs[0][par][lane] = dxr;
+    dxq[0][par][lane] = bf16_split3(dxr);
   }
   for (int pair = 0; pair < npair; pair += 2) {
     step(pair, ring0, ring1);
