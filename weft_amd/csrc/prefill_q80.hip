@@ -10,8 +10,11 @@
 //          (ggml-cpu/quants.c:279-313): the block's MFMA runs twice with the
 //          weight operand of one half, Y += dx * (ws_lo I_lo + ws_hi I_hi)
 // One v_mfma_i32_32x32x32_i8 per 32x32 tile and 32-block gives I exactly; the
-// two per-block scales are applied in fp32 on VALU (3 instructions per
-// output and block), which is what bounds these kernels.
+// two per-block scales are applied in fp32 on VALU, which is what bounds
+// these kernels.  Q4_0 / Q4_1: the factor dx ws of every output comes from
+// one f16 outer-product MFMA per tile and block (both scales are fp16, the
+// product exact in fp32), then convert and FMA: 2 VALU instructions per
+// output and block; NVFP4 and the MXFP4 table body: 3.
 //
 // Activation layout.  A Q8_0 record is 34 bytes at 2-byte alignment, which
 // cannot feed 16-byte operand reads.  The activation is therefore quantized
