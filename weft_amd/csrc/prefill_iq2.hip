@@ -10,14 +10,15 @@
 // operand bytes are +-{8, 25, 43}); the small integer group scale folds in
 // with one v_mad_i32_i24 per output, exact in int32 (|I| < 2^18, ls <= 31,
 // eight groups < 2^26), and the fp32 combine runs once per superblock on the
-// same integer GGML converts.
+// same integer GGML converts, its factor dx dw from a bf16 outer-product
+// MFMA per tile (as in the K-quant GEMMs).
 //
 // Tiling as in the Q4_K prefill: 64 tokens x 128 weight rows per workgroup,
 // 8 waves (superblock parity x 4 column groups), each wave two 32x32 tiles.
 // A 66-byte record is only 2-byte aligned, so the weight rows of a superblock
 // PAIR (132 bytes, 4-byte aligned when K/256 is even) are staged together;
 // each parity reads its half with aligned dword reads and byte alignment.
-// Grid and sign tables live in LDS.
+// Grid and sign tables live in LDS, the signs as byte masks (0xff per -1).
 #include <algorithm>
 
 #include "kernels.h"

@@ -23,6 +23,11 @@
 // int8 (|bsum| <= 2032) and the mins 6-bit, so both are exact f16 operands
 // and the fp32 result is exact (|Mn| < 2^21).
 //
+// The superblock's fp32 factors dx dw (and dx dmin) of every output come from
+// one bf16 outer-product MFMA per tile each (dx = h + m + l in bf16 parts
+// against the fp16 scale's two bf16 parts: six exact products summed in
+// fp32), so the combine is a convert and one FMA per output (two for Q5_K).
+//
 // Tiling: 64 tokens x 128 weight rows per workgroup, 8 waves; wave w takes
 // weight rows 32 (w % 4) .. +31 and the half superblock w / 4 (elements
 // 128 h .. +127: Q6_K's ql/qh half, Q5_K's groups 4h .. 4h+3) for all 64
