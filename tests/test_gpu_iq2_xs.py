@@ -4,7 +4,9 @@ bit-exact, vec_dot and mul_mat within the fp64 re-accumulation bar, the Xq
 workspace bit-exact Q8_K.  Weights are random records with a moderate fp16
 d (GGML's IQ2_XS quantizer, an importance-weighted grid search, is not
 restated; every byte pattern is a valid record), plus records with both
-scale nibbles at 0 and 15 and d = 0."""
+scale nibbles at 0 and 15 and d = 0, and corner records (grid and sign
+indices at 0 and at their maxima, subnormal and large d) for the MFMA GEMM
+and the batch-1 kernel."""
 from __future__ import annotations
 
 import numpy as np
@@ -80,3 +82,45 @@ def test_ggml_mul_mat_iq2_xs(hip):
     xq = o.quantize("q8_k", x)
     e, a = o.mul_mat_f64("iq2_xs", w, xq, n, k, m)
     assert_close(yd.numpy(np.float32).reshape(m, n), e, a, "MUL_MAT iq2_xs")
+
+
+def extreme_weights(n, k, seed=23):
+    """Records at the format's corners: every grid index and sign index at
+    0 and at its maximum (qs = 0x0000 / 0xFFFF: grid entry 511, sign entry
+    127), both scale nibbles 0 and 15, d = 0, the smallest subnormal d and
+    d = 2^15, mixed with random records."""
+    w = weights(n, k, seed=seed).reshape(n, k // 256, 74)
+    rng = np.random.default_rng(seed)
+    d = (rng.standard_normal((n, k // 256)) * 1e-2).astype(np.float16)
+    w[:, :, 0:2] = d.view(np.uint8).reshape(n, k // 256, 2)
+    w[3, :, 2:66] = 0x00                        # grid 0, sign 0 everywhere
+    w[4, :, 2:66] = 0xFF                        # grid 511, sign 127 everywhere
+    w[4, :, 66:74] = 0xFF
+    w[5, 1, 0:2] = 0                            # d = 0
+    w[6, :, 0:2] = np.array([1, 0], np.uint8)   # smallest subnormal d
+    w[7, :, 0:2] = np.array([2.0 ** 15], np.float16).view(np.uint8)
+    return np.ascontiguousarray(w.reshape(n, -1))
+
+
+def test_prefill_iq2_xs_extreme_records(hip):
+    """The MFMA GEMM (per-16 scales, sign masks from LDS, the dx dw factor
+    from a bf16 outer-product MFMA) on corner records, against activations
+    with an all-zero Q8_K block and an all-zero token."""
+    n, k, m = 160, 2048, 48
+    w = extreme_weights(n, k)
+    x = acts(m, k, seed=9).copy()
+    x[4, 256:512] = 0.0
+    x[7] = 0.0
+    w, x, xq, y = run_mul_mat(hip, "production_mul_mat_iq2_xs", "iq2_xs", n, k, m, w=w, x=x)
+    check_mul_mat("iq2_xs", w, x, xq, y, n, k, m)
+
+
+def test_decode_iq2_xs_batch1_extreme_records(hip):
+    """The batch-1 kernel on the same corner records, against an activation
+    with an all-zero Q8_K block."""
+    n, k = 160, 4096
+    w = extreme_weights(n, k, seed=29)
+    x = acts(1, k, seed=17).copy()
+    x[0, 256:512] = 0.0
+    w, x, xq, y = run_mul_mat(hip, "production_mul_mat_iq2_xs", "iq2_xs", n, k, 1, w=w, x=x)
+    check_mul_mat("iq2_xs", w, x, xq, y, n, k, 1)
