@@ -23,8 +23,9 @@
  * Record layouts are GGML's (source/c/ggml/llama.cpp/ggml/src/ggml-common.h):
  *   Q4_0 18 B/32, MXFP4 17 B/32, Q8_0 34 B/32, Q4_K 144 B/256,
  *   Q8_K 292 B/256, IQ2_XXS 66 B/256.
- * Table arguments: grid = I8X8[256x8] iq2xxs grid magnitudes, signs =
- * I8X8[128x8] of +-1, codebook = int8[16] doubled E2M1, scale = fp32[256]
+ * Table arguments: grid = I8X8[256x8] iq2xxs grid magnitudes (GGML's
+ * tables hold 8, 25 and 43 only; the kernels negate grid bytes in place
+ * and need every byte in [1, 127]), signs = I8X8[128x8] of +-1, codebook = int8[16] doubled E2M1, scale = fp32[256]
  * e8m0 "half" scales (examples/repro/weft/mul_mat_runtime.cpp:151-159).
  *
  * Reference citations are relative to the Weft repository root.

@@ -51,8 +51,10 @@ struct Iq2Args {
 // table is held in LDS
 __device__ __forceinline__ uint32_t iq2_sign_mask(uint32_t s) { return ((s >> 7) & 0x01010101u) * 0xffu; }
 
-// negate the bytes of g whose mask byte in m is 0xff: bytes of g are in
-// [0, 43], so (b ^ 0xff) + 1 never carries into the next byte
+// negate the bytes of g whose mask byte in m is 0xff: bytes of g are grid
+// magnitudes, 8, 25 or 43 in GGML's tables, and for b in [1, 127]
+// (b ^ 0xff) + 1 = 256 - b never carries into the next byte (a byte of 0
+// would)
 __device__ __forceinline__ int iq2_negate(uint32_t g, uint32_t m) {
   return (int)((g ^ m) + (m & 0x01010101u));
 }

@@ -216,7 +216,9 @@ __device__ __forceinline__ int lookup16(uint32_t n, uint32_t c0, uint32_t c1, ui
 // staged in LDS
 __device__ __forceinline__ uint32_t sign_mask4(uint32_t s) { return ((s >> 7) & 0x01010101u) * 0xffu; }
 
-// negate the bytes of g (grid magnitudes 8..43) where the mask byte is 0xff
+// negate the bytes of g where the mask byte is 0xff: bytes of g are grid
+// magnitudes (8, 25 or 43 in GGML's tables), and for b in [1, 127]
+// (b ^ 0xff) + 1 never carries into the next byte (a byte of 0 would)
 __device__ __forceinline__ int apply_signs(uint32_t g, uint32_t m) {
   return (int)((g ^ m) + (m & 0x01010101u));
 }

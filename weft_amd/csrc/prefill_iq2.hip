@@ -97,8 +97,10 @@ __device__ __forceinline__ uint32_t ld32(const uint8_t* p) {
 // VALU read of an MFMA result needs.)
 __device__ __forceinline__ void pin(int& v) { asm volatile("" : "+v"(v)); }
 // negate the bytes of g whose mask byte in m is 0xff (the sign table is
-// staged in LDS as byte masks: 0xff where the +-1 byte is -1): bytes of g
-// are in [0, 43], so (b ^ 0xff) + 1 never carries into the next byte
+// staged in LDS as byte masks: 0xff where the +-1 byte is -1).  Bytes of g
+// are grid magnitudes, 8, 25 or 43 in GGML's tables: for b in [1, 127],
+// (b ^ 0xff) + 1 = 256 - b never carries into the next byte (a byte of 0
+// would)
 __device__ __forceinline__ uint32_t apply_signs(uint32_t g, uint32_t m) {
   return (g ^ m) + (m & 0x01010101u);
 }
