@@ -129,11 +129,11 @@ __global__ void __launch_bounds__(kThreads) q6k_gemv_m1_kernel(Q6Args a) {
   auto compute = [&](const RowBuf& buf, int k) {
     uint32_t ql[16], qh[8];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) ql[i] = sh ? __builtin_amdgcn_alignbyte(buf.ql[i + 1], buf.ql[i], 2) : buf.ql[i];
+    for (int i = 0; i < 16; ++i) ql[i] = __builtin_amdgcn_alignbyte(buf.ql[i + 1], buf.ql[i], sh);  // sh 0 or 2
 #pragma unroll
-    for (int i = 0; i < 8; ++i) qh[i] = sh ? __builtin_amdgcn_alignbyte(buf.qh[i + 1], buf.qh[i], 2) : buf.qh[i];
-    const uint32_t sc4 = sh ? __builtin_amdgcn_alignbyte(buf.sc[1], buf.sc[0], 2) : buf.sc[0];
-    const float dw = fp16_to_fp32(sh ? buf.d >> 16 : buf.d & 0xffffu);
+    for (int i = 0; i < 8; ++i) qh[i] = __builtin_amdgcn_alignbyte(buf.qh[i + 1], buf.qh[i], sh);
+    const uint32_t sc4 = __builtin_amdgcn_alignbyte(buf.sc[1], buf.sc[0], sh);
+    const float dw = fp16_to_fp32((buf.d >> (8 * sh)) & 0xffffu);
     // part a: ql[0 .. 31] with qh bits hsh .. hsh + 1; part b: ql[32 .. 63]
     // with bits hsh + 2 .. hsh + 3 (element l of both parts reads qh[l])
     int P[4] = {0, 0, 0, 0};
