@@ -104,14 +104,21 @@ __global__ void __launch_bounds__(kThreads) iq2_gemv_m1_kernel(Iq2Args a) {
     buf.h = *reinterpret_cast<const uint32_t*>(rp + hoff);
     if constexpr (kXs) buf.s = *reinterpret_cast<const uint16_t*>(rp + soff);
   };
+  // the tables next, one dword per thread: they are needed with the
+  // activation, so they do not queue behind the weight rows
+  static_assert(kGridBytes / 4 <= kThreads, "one grid dword per thread");
+  const int ti = threadIdx.x;
+  uint32_t tg = 0, ts = 0;
+  if (ti < kGridBytes / 4) tg = reinterpret_cast<const uint32_t*>(a.grid)[ti];
+  if (ti < 256) ts = reinterpret_cast<const uint32_t*>(a.signs)[ti];
+  __builtin_amdgcn_sched_barrier(0);
+
   RowBuf bufA, bufB;
   issue(bufA, 0);
   __builtin_amdgcn_sched_barrier(0);
 
-  for (int i = threadIdx.x; i < kGridBytes / 4; i += kThreads)
-    reinterpret_cast<uint32_t*>(tgrid)[i] = reinterpret_cast<const uint32_t*>(a.grid)[i];
-  for (int i = threadIdx.x; i < 256; i += kThreads)
-    reinterpret_cast<uint32_t*>(tsign)[i] = iq2_sign_mask(reinterpret_cast<const uint32_t*>(a.signs)[i]);
+  if (ti < kGridBytes / 4) reinterpret_cast<uint32_t*>(tgrid)[ti] = tg;
+  if (ti < 256) reinterpret_cast<uint32_t*>(tsign)[ti] = iq2_sign_mask(ts);
   stager.finish(a.X, (size_t)K, blockIdx.x == 0 ? a.xq_out : nullptr, K, 0, 1, act);
   __syncthreads();
 

@@ -119,12 +119,19 @@ __global__ void __launch_bounds__(kRecThreads) rec_gemv_m1_kernel(RecArgs a) {
       buf.w[8] = *reinterpret_cast<const uint32_t*>(p + 32);
     }
   };
+  // the scale table next (one entry per thread): it is needed with the
+  // activation, so it does not queue behind the weight rows
+  float tsc = 0.f;
+  if constexpr (kTab)
+    if (threadIdx.x < 256) tsc = a.scale[threadIdx.x];
+  __builtin_amdgcn_sched_barrier(0);
+
   RowBuf bufA, bufB;
   issue(bufA, 0);
   __builtin_amdgcn_sched_barrier(0);
 
   if constexpr (kTab)
-    for (int i = threadIdx.x; i < 256; i += kRecThreads) tab[i] = a.scale[i];
+    if (threadIdx.x < 256) tab[threadIdx.x] = tsc;
   {
     const Q8_0Lane r = q80_quantize_8lanes(xv);
     uint32_t sh16 = 0;
