@@ -159,9 +159,6 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
       return m0 + r;
   };
 
-  for (int i = tid; i < TT::kGrid * 8; i += kThreads) tgrid[i] = (uint8_t)a.grid[i];
-  for (int i = tid; i < 128 * 8; i += kThreads) tsign[i] = a.signs[i] < 0 ? 0xffu : 0u;  // byte masks
-
   // activation int8 of superblock 2*pair + par: 16 wave-wide 16-byte loads, 4 per wave
   const uint8_t* asrc[4];
 #pragma unroll
@@ -315,6 +312,9 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
   };
 
   issue(0, ring0);
+  // the tables after the first stage's loads: their round trip overlaps it
+  for (int i = tid; i < TT::kGrid * 8; i += kThreads) tgrid[i] = (uint8_t)a.grid[i];
+  for (int i = tid; i < 128 * 8; i += kThreads) tsign[i] = a.signs[i] < 0 ? 0xffu : 0u;  // byte masks
   if (wcol == 0) {
     load_dx(0);
     dxq[0][par][lane] = bf16_split3(dxr);
