@@ -17,7 +17,9 @@ over enough copies (> 2 x the 256 MB Infinity Cache) that each call reads
 them from HBM; the write-bound row dequantize rotates its outputs as well
 (``one_output_us``: the same calls into one output buffer).  Each case is
 timed three ways on the library's stream:
-  * ``us``: K back-to-back calls between two HIP events (the headline);
+  * ``us``: windows of K back-to-back calls, each window between two HIP
+    events; the per-call time of the median window of 10 (``us_min`` /
+    ``us_max``: the fastest and slowest window), the headline;
   * ``cold_us``: BASELINE.md's protocol -- 512 MiB written to flush the
     caches, then one call between two events; median of 20;
   * ``graph_us``: the same back-to-back calls replayed from a captured HIP
@@ -29,10 +31,16 @@ torch._int_mm) of the same M x N x K.  ``kernels`` lists what one call
 launched (the library's launch log).
 
 CPU baseline: oracle/'s restatement of GGML's MUL_MAT (quantize_row_q8_K_ref
-+ ggml_vec_dot_q4_K_q8_K_generic) on the same decode call, with GGML's
-thread schedule over every host thread (``value``), and single-threaded
-under the reference's kernel protocol: one warmup, a 64 MiB eviction before
-each of 10 timed calls, median (doc/experiments/protocol.md:46-55).
++ ggml_vec_dot_q4_K_q8_K_generic) on the same decode call, built on the host
+that runs it with -march=native, with GGML's thread schedule over every host
+thread (``value``), and single-threaded under the reference's kernel
+protocol: one warmup, a 64 MiB eviction before each of 10 timed calls,
+median (doc/experiments/protocol.md:46-55).
+
+Output: one JSON line.  ``adjacent`` (the formats beside the north star, in
+brief) comes before ``configs`` (BASELINE.json's configs 1-5b in full), so
+the end of the line, which is what a log tail keeps, holds the BASELINE
+configs.
 """
 from __future__ import annotations
 
@@ -94,13 +102,25 @@ CASES = {
 }
 MOE_EXPERTS, MOE_USED = 8, 2
 HEADLINE = "q4_k_decode_w_up"
+# BASELINE.json configs (label: case), reported in full and last
+BASELINE_CASES = {
+    "1_q4_0_decode": "q4_0_decode",
+    "2_q4_k_dequant": "q4_k_dequant",
+    "3_q4_k_decode_w_up": "q4_k_decode_w_up",
+    "3_q4_k_decode_w_down": "q4_k_decode_w_down",
+    "4_q4_k_prefill_n4096": "q4_k_prefill_n4096",
+    "4_q4_k_prefill_n11008": "q4_k_prefill_n11008",
+    "5a_iq2_xxs_decode": "iq2_xxs_decode",
+    "5b_mxfp4_prefill": "mxfp4_prefill",
+}
+WINDOWS = 10  # timed windows per case; the median window is reported
 
 
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=200)
-    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--steps", type=int, default=50, help="calls per timed window")
+    p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="wall-clock budget of the all-threads CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
@@ -249,23 +269,29 @@ class Bench:
     def events(self):
         return (self.torch.cuda.Event(enable_timing=True), self.torch.cuda.Event(enable_timing=True))
 
-    def time_calls(self, launch, steps, warmup):
-        """launch(i) enqueues call i; seconds per call over `steps`
-        back-to-back calls, from two HIP events on the library's stream."""
+    def time_calls(self, launch, steps, warmup, windows=WINDOWS):
+        """launch(i) enqueues call i.  After `warmup` calls, `windows` windows
+        of `steps` back-to-back calls, each between two HIP events on the
+        library's stream with a synchronize on both sides; returns the
+        seconds per call of the median, fastest and slowest window."""
         torch = self.torch
         for i in range(warmup):
             launch(i)
         torch.cuda.synchronize()
         self._lib.check("warmup")
-        start, end = self.events()
-        torch.cuda.synchronize()
-        start.record(self.stream)
-        for i in range(steps):
-            launch(warmup + i)
-        end.record(self.stream)
-        torch.cuda.synchronize()
+        per, i = [], warmup
+        for _ in range(windows):
+            start, end = self.events()
+            torch.cuda.synchronize()
+            start.record(self.stream)
+            for _ in range(steps):
+                launch(i)
+                i += 1
+            end.record(self.stream)
+            torch.cuda.synchronize()
+            per.append(start.elapsed_time(end) / 1e3 / steps)
         self._lib.check("timed region")
-        return start.elapsed_time(end) / 1e3 / steps
+        return statistics.median(per), min(per), max(per)
 
     def time_cold(self, launch, reps=20):
         """Median seconds of one call after the caches are flushed by writing
@@ -312,26 +338,41 @@ class Bench:
         self._lib.check("graph replay")
         return start.elapsed_time(end) / 1e3 / (calls * replays)
 
-    def floors(self, nbytes_list):
+    def floors(self, nbytes_list, sweep_bytes):
         """Per-launch floors on this stream: an empty kernel back to back, and
-        the best single streaming-read launch of each byte count."""
+        the fastest single streaming-read launch of each byte count.  For
+        sweep_bytes the read probe is swept over every shape it has (threads
+        per workgroup, 16-byte loads in flight per lane, nontemporal or not,
+        grid-stride or one contiguous chunk per workgroup) and grid size; the
+        other byte counts try the five best shapes of that sweep.  The best
+        shape is then timed like a case (median of the windows)."""
         torch = self.torch
         lib = self.lib
-        out = {"empty_launch_us": round(self.time_calls(lambda i: lib.weft_hip_probe_empty(), 200, 20) * 1e6, 3)}
+        out = {"empty_launch_us": round(self.time_calls(lambda i: lib.weft_hip_probe_empty(), 100, 20)[0] * 1e6, 3)}
         sink = torch.empty(1 << 16, dtype=torch.int32, device=self.dev)
-        reads = {}
-        for nbytes in nbytes_list:
+        shapes = [(t, u, f) for t in (256, 512, 1024) for u in (1, 2, 4, 8, 16) for f in (0, 1, 2, 3)]
+        grids = (256, 512, 1024, 2048)
+        reads, ranked = {}, None
+        for nbytes in sorted(nbytes_list, key=lambda nb: nb != sweep_bytes):
             n16 = (nbytes + 15) // 16 * 16
             copies = max(2, int(np.ceil(2 * MALL_BYTES / n16)) + 1)
             bufs = [torch.zeros(n16, dtype=torch.uint8, device=self.dev) for _ in range(copies)]
-            best = None
-            for grid in (256, 512, 1024, 2048):
-                sec = self.time_calls(lambda i: lib.weft_hip_probe_read(bufs[i % copies].data_ptr(), n16,
-                                                                        sink.data_ptr(), grid), 100, 10)
-                if best is None or sec < best[0]:
-                    best = (sec, grid)
-            reads[str(nbytes)] = {"us": round(best[0] * 1e6, 3), "GBs": round(nbytes / best[0] / 1e9, 1),
-                                  "grid": best[1]}
+            tried = []
+            for shape in (shapes if ranked is None else ranked[:5]):
+                for grid in grids:
+                    t, u, f = shape
+                    sec = self.time_calls(lambda i: lib.weft_hip_probe_read_shape(
+                        bufs[i % copies].data_ptr(), n16, sink.data_ptr(), grid, t, u, f), 20, 5, windows=3)[0]
+                    tried.append((sec, shape, grid))
+            tried.sort()
+            if ranked is None:
+                ranked = list(dict.fromkeys(shape for _, shape, _ in tried))
+            _, (t, u, f), grid = tried[0]
+            sec = self.time_calls(lambda i: lib.weft_hip_probe_read_shape(
+                bufs[i % copies].data_ptr(), n16, sink.data_ptr(), grid, t, u, f), 50, 10)[0]
+            reads[str(nbytes)] = {"us": round(sec * 1e6, 3), "GBs": round(nbytes / sec / 1e9, 1),
+                                  "grid": grid, "threads": t, "unroll": u, "nontemporal": bool(f & 1),
+                                  "blocked": bool(f & 2), "launch_shapes_tried": len(tried)}
             del bufs
             torch.cuda.empty_cache()
         out["stream_read"] = reads
@@ -347,13 +388,16 @@ class Bench:
             for _ in range(3):
                 torch._int_mm(a, b)
             torch.cuda.synchronize()
-            start, end = self.events()
-            start.record(self.stream)
-            for _ in range(20):
-                torch._int_mm(a, b)
-            end.record(self.stream)
-            torch.cuda.synchronize()
-            return start.elapsed_time(end) / 1e3 / 20
+            per = []
+            for _ in range(WINDOWS):
+                start, end = self.events()
+                start.record(self.stream)
+                for _ in range(20):
+                    torch._int_mm(a, b)
+                end.record(self.stream)
+                torch.cuda.synchronize()
+                per.append(start.elapsed_time(end) / 1e3 / 20)
+            return statistics.median(per)
         except RuntimeError:
             return None
 
@@ -460,22 +504,22 @@ def run_case(b: Bench, name: str, steps: int, warmup: int, extra: bool) -> dict:
                 fn(wd[i % copies].data_ptr(), x.data_ptr(), xq.data_ptr(), *tabs, y.data_ptr(), n, k, m)
 
             nbytes = w.nbytes + 4 * m * k + xq.numel() + 4 * m * n
-    if bound == "mfma":
-        steps, warmup = max(20, steps // 4), 3
+    warmup = max(3, warmup if bound == "hbm" else warmup // 4)
     b._lib.launch_log()
     launch(0)
     torch.cuda.synchronize()
     log = b._lib.launch_log()
     kernels = [f"{k} x{log.count(k)}" if log.count(k) > 1 else k for k in dict.fromkeys(log)]
-    sec = b.time_calls(launch, steps, warmup)
+    sec, lo, hi = b.time_calls(launch, steps, warmup)
     out = {"symbol": sym, "N": n, "K": k, "M": max(m, 1) if m < 0 else m, "us": round(sec * 1e6, 3),
+           "us_min": round(lo * 1e6, 3), "us_max": round(hi * 1e6, 3),
            "algorithmic_bytes": int(nbytes), "GBs": round(nbytes / sec / 1e9, 2),
-           "weight_copies_rotated": copies, "steps": steps, "kernels": kernels}
+           "weight_copies_rotated": copies, "kernels": kernels}
     if m == 0:
         out["output_copies_rotated"] = ycopies
         # the same calls writing one output buffer (180 MB at config 2, part
         # of which the Infinity Cache keeps between calls)
-        out["one_output_us"] = round(b.time_calls(launch_one_output, steps, warmup) * 1e6, 3)
+        out["one_output_us"] = round(b.time_calls(launch_one_output, steps, warmup)[0] * 1e6, 3)
     if extra:
         out["cold_us"] = round(b.time_cold(launch) * 1e6, 3)
         out["graph_us"] = round(b.time_graph(launch) * 1e6, 3)
@@ -506,6 +550,7 @@ def cpu_baseline(n, k, budget_s):
     with GGML's schedule for ~budget_s, then one thread under the reference's
     kernel protocol."""
     import oracle as o
+    build = o.use_native()
     w = o.quantize("q4_k", o.seeded_normal(1, (n, k), 0.02))
     x = o.seeded_normal(2, (1, k))
     nbytes = w.nbytes + 4 * k + (k // 256) * 292 + 4 * n
@@ -536,14 +581,20 @@ def cpu_baseline(n, k, budget_s):
                       f"GGML's MUL_MAT thread schedule over {threads} host threads",
             "single_thread": {"us": round(one * 1e6, 1), "GBs": round(nbytes / one / 1e9, 3),
                               "protocol": "1 warmup, 64 MiB eviction before each of 10 calls, median"},
-            "cpu_model": cpu_model(), "nproc": os.cpu_count()}
+            "cpu_model": cpu_model(), "nproc": os.cpu_count(), "build": "gcc " + build}
+
+
+def brief(case: dict) -> dict:
+    """The figures of an adjacent-format case kept in the output line."""
+    keep = ("us", "us_min", "us_max", "GBs", "TOPS", "frac_hbm_peak", "frac_int8_peak", "graph_us")
+    return {k: case[k] for k in keep if k in case}
 
 
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1",
-                          "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU figures are not part of it "
+                                   "(--gpus must be 1)", "n_gpus": args.gpus}))
         sys.exit(2)
     b = Bench()
     steps, warmup = args.steps, args.warmup
@@ -558,12 +609,17 @@ def main():
         names = []
     else:
         names = [c for c in args.cases.split(",") if c]
-    secondary = {name: run_case(b, name, steps, warmup, extra) for name in names}
+    results = {HEADLINE: head}
+    results.update({name: run_case(b, name, steps, warmup, extra) for name in names})
     floors = None
     if extra:
-        byte_counts = sorted({head["algorithmic_bytes"]} |
-                             {v["algorithmic_bytes"] for v in secondary.values() if v.get("frac_hbm_peak")})
-        floors = b.floors(byte_counts)
+        byte_counts = sorted({v["algorithmic_bytes"] for v in results.values() if v.get("frac_hbm_peak")})
+        floors = b.floors(byte_counts, head["algorithmic_bytes"])
+        for v in results.values():
+            read = floors["stream_read"].get(str(v["algorithmic_bytes"])) if v.get("frac_hbm_peak") else None
+            if read is not None:
+                v["read_floor_us"] = read["us"]
+                v["vs_read_floor"] = round(v["us"] / read["us"], 3)
     if args.calibrate_copy:
         nb = args.calibrate_copy << 20
         src = b.torch.empty(nb, dtype=b.torch.uint8, device=b.dev)
@@ -582,6 +638,7 @@ def main():
         roofline["floor"] = {"empty_launch_us": floors["empty_launch_us"], "stream_read_us": read["us"],
                              "stream_read_frac": round(read["GBs"] / HBM_PEAK_GBS, 4),
                              "kernel_vs_read": round(head["us"] / read["us"], 3)}
+    labels = {case: label for label, case in BASELINE_CASES.items()}
     line = {
         "metric": "Q4_K mul_mat: decode GB/s (% of 8 TB/s) + prefill TOPS (% int8 MFMA peak)",
         "value": gbs,
@@ -599,13 +656,13 @@ def main():
         "config": {"workload": "production_mul_mat_q4_k_decode, config 3 W_up: N=11008 K=4096 "
                                "M=1, Q8_K activation quantize inside the timed call",
                    "N": 11008, "K": 4096, "M": 1,
-                   "weight_copies_rotated": head["weight_copies_rotated"]},
+                   "weight_copies_rotated": head["weight_copies_rotated"],
+                   "timing": f"median of {WINDOWS} windows of {steps} back-to-back calls (HIP events)"},
         "roofline": roofline,
         "cpu_baseline": cpu,
-        "headline_cold_us": head.get("cold_us"),
-        "headline_graph_us": head.get("graph_us"),
         "floors": floors,
-        "configs": secondary,
+        "adjacent": {name: brief(v) for name, v in results.items() if name not in labels},
+        "configs": {labels[name]: results[name] for name in CASES if name in labels and name in results},
     }
     print(json.dumps(line))
 

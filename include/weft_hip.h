@@ -68,9 +68,14 @@ int weft_hip_device_arch(int dev, char *buf, size_t len);
  * "weft-hip-artifact", gfx_arch / wavefront_size in place of march / abi /
  * vlen_bits). */
 const char *weft_hip_artifact(void);
-/* Names of the kernels this thread launched since the last read, comma
- * separated, copied into buf (len bytes with the NUL) and cleared; returns
- * the log's length.  buf == NULL only returns the length. */
+/* Launch log of the calling thread, a debugging and measurement aid that is
+ * off by default: weft_hip_set_launch_log(1) turns it on (0 turns it off and
+ * empties it) and returns the previous setting.  While on, the names of the
+ * kernels this thread launches are appended, keeping at most the last 4096
+ * bytes.  weft_hip_launch_log copies the names since the last read, comma
+ * separated, into buf (len bytes with the NUL) and clears them; it returns
+ * the log's length, and buf == NULL only returns the length. */
+int weft_hip_set_launch_log(int enable);
 size_t weft_hip_launch_log(char *buf, size_t len);
 /* Measurement probes on the current stream: an empty launch, and one launch
  * that reads `bytes` (a multiple of 16, 16-byte aligned) of device memory
@@ -78,6 +83,13 @@ size_t weft_hip_launch_log(char *buf, size_t len);
  * (grid * 8 words). */
 void weft_hip_probe_empty(void);
 void weft_hip_probe_read(const void *src, size_t bytes, uint32_t *sink, int grid);
+/* The same read in another shape: `threads` per workgroup (64..1024, a
+ * multiple of 64), `unroll` 16-byte loads in flight per lane (1, 2, 4, 8,
+ * 16), flags bit 0 = nontemporal loads, bit 1 = each workgroup reads one
+ * contiguous chunk instead of the grid striding over the buffer; sink holds
+ * grid * threads / 64 words.  weft_hip_probe_read is (512, 4, 0). */
+void weft_hip_probe_read_shape(const void *src, size_t bytes, uint32_t *sink, int grid, int threads,
+                               int unroll, int flags);
 
 /* ------------------------------------------------------ row dequantize */
 /* examples/kernels/dequantize/q4_0.py:9-13; repro row_dequantize_runtime.cpp:177 */
@@ -310,8 +322,12 @@ int weft_ggml_mul_mat_id(const weft_ggml_tensor *src0, const weft_ggml_tensor *s
  * the work buffer is a static device array the library holds per device
  * (WEFT_GGML_NOALLOC_SCRATCH_BYTES), so the call allocates nothing.  A call
  * whose work size (weft_ggml_mul_mat_id_work_size) exceeds it returns
- * hipErrorOutOfMemory and launches nothing.  Calls that overlap on one
- * device share the array and race. */
+ * hipErrorOutOfMemory and launches nothing.  Not safe from more than one
+ * stream of a device: every call on a device uses the same array, so calls
+ * that can overlap (issued by two threads, on two streams, or from two
+ * captured graphs replayed concurrently) corrupt each other's quantized src1
+ * and expert grouping without any error.  Calls on one stream are ordered
+ * and safe. */
 #define WEFT_GGML_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
 int weft_ggml_mul_mat_id_noalloc(const weft_ggml_tensor *src0, const weft_ggml_tensor *src1,
                                  const weft_ggml_tensor *ids, const weft_ggml_tensor *dst);

@@ -41,6 +41,26 @@ def build() -> Path:
 
 
 _lib = None
+NATIVE_PATH = HERE / "libweft_oracle_native.so"
+BUILD_FLAGS = "-O3 -march=x86-64-v3 -ffp-contract=off -fopenmp"
+NATIVE_FLAGS = "-O3 -march=native -ffp-contract=off -fopenmp"
+
+
+def use_native() -> str:
+    """Switch this process to the oracle built for the running machine's own
+    ISA (``make native``, built here if missing) and return its flags; on a
+    failed build keep the portable library and return its flags."""
+    global _lib
+    try:
+        subprocess.run(["make", "-s", "-C", str(HERE), "native"], check=True,
+                       stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL)
+        l = ctypes.CDLL(str(NATIVE_PATH))
+    except (OSError, subprocess.CalledProcessError):
+        lib()
+        return BUILD_FLAGS
+    _declare(l)
+    _lib = l
+    return NATIVE_FLAGS
 
 
 def lib() -> ctypes.CDLL:

@@ -113,6 +113,20 @@ def test_invalid_call_records_an_error_without_a_device():
     assert lib.weft_hip_get_last_error() == 0
 
 
+def test_launch_log_is_off_until_a_thread_turns_it_on():
+    """A drop-in caller that never reads the log keeps nothing: the log is
+    off by default and turning it off empties it."""
+    lib = _lib.load()
+    was = lib.weft_hip_set_launch_log(0)
+    try:
+        assert lib.weft_hip_set_launch_log(0) == 0
+        assert lib.weft_hip_launch_log(None, 0) == 0
+        assert lib.weft_hip_set_launch_log(1) == 0
+        assert lib.weft_hip_set_launch_log(1) == 1
+    finally:
+        lib.weft_hip_set_launch_log(was)
+
+
 def test_tile_bindings_accept_the_gemv_knobs_only():
     """NC and MR retile the GEMV launches; other meta names have no gfx950
     knob (0, no error); a value above INT32_MAX or no name is an error."""

@@ -144,3 +144,30 @@ def test_tile_binding_nc_reaches_the_batch1_kernels(torch_dev, definition, fmt):
         e, a = o.mul_mat_f64(fmt, w, want_xq, n, k, 1)
         assert o.within_tolerance(outs[-1], e, a).all()
     np.testing.assert_array_equal(outs[0], outs[1])
+
+
+def test_launch_log_stays_bounded_without_a_reader(torch_dev):
+    """The launch log keeps nothing while off and at most its last 4096 bytes
+    of names while on, however many launches go unread."""
+    torch, _ = torch_dev
+    from weft_amd import _lib
+    lib = _lib.load()
+    _lib.set_stream(torch.cuda.current_stream().cuda_stream)
+    was = lib.weft_hip_set_launch_log(0)
+    try:
+        for _ in range(2000):
+            lib.weft_hip_probe_empty()
+        torch.cuda.synchronize()
+        _lib.check("probe_empty")
+        assert lib.weft_hip_launch_log(None, 0) == 0
+        lib.weft_hip_set_launch_log(1)
+        for _ in range(2000):
+            lib.weft_hip_probe_empty()
+        torch.cuda.synchronize()
+        _lib.check("probe_empty")
+        n = lib.weft_hip_launch_log(None, 0)
+        assert 3000 < n <= 4096
+        names = _lib.launch_log()
+        assert names and set(names) == {"probe_empty_kernel"}
+    finally:
+        lib.weft_hip_set_launch_log(was)

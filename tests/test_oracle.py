@@ -595,6 +595,23 @@ def test_mul_mat_against_independent_float64_path(fmt):
     assert o.vec_dot(fmt, w[5], xq[1], k) == y[1, 5]
 
 
+@pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "iq2_xxs", "mxfp4"])
+@pytest.mark.parametrize("n,m", [(1, 1), (37, 1), (61, 5), (130, 17)])
+def test_ggml_scheduled_mul_mat_equals_the_pinned_mul_mat(fmt, n, m):
+    """The CPU baseline's MUL_MAT with GGML's thread schedule (wo_mul_mat_ggml,
+    ggml-cpu.c:1245-1443) gives the pinned wo_mul_mat's Xq and Y bit for bit,
+    at 1, 2 and every thread, on ragged N and M: the schedule only splits the
+    work, every output is the same vec_dot."""
+    k = 1024
+    w = o.quantize(fmt, o.seeded_normal(71, (n, k), 0.02))
+    x = o.seeded_normal(72, (m, k))
+    xq, y = o.mul_mat(fmt, w, x, n, k, m)
+    for threads in (1, 2, o.max_threads()):
+        gxq, gy = o.mul_mat_ggml(fmt, w, x, n, k, m, threads=threads)
+        assert np.array_equal(gxq, xq)
+        assert np.array_equal(gy.view(np.uint32), y.view(np.uint32))
+
+
 def test_int_partials_q4_0_are_the_block_dots():
     k = 512
     w = o.quantize("q4_0", o.seeded_normal(41, (1, k), 0.02))

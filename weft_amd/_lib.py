@@ -64,12 +64,17 @@ def load() -> ctypes.CDLL:
             lib.weft_hip_device_count.restype = ctypes.c_int
             lib.weft_hip_device_arch.argtypes = [ctypes.c_int, ctypes.c_char_p, ctypes.c_size_t]
             lib.weft_hip_device_arch.restype = ctypes.c_int
+            lib.weft_hip_set_launch_log.argtypes = [ctypes.c_int]
+            lib.weft_hip_set_launch_log.restype = ctypes.c_int
             lib.weft_hip_launch_log.argtypes = [ctypes.c_char_p, ctypes.c_size_t]
             lib.weft_hip_launch_log.restype = ctypes.c_size_t
             lib.weft_hip_probe_empty.argtypes = []
             lib.weft_hip_probe_empty.restype = None
             lib.weft_hip_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int]
             lib.weft_hip_probe_read.restype = None
+            lib.weft_hip_probe_read_shape.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                                      ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+            lib.weft_hip_probe_read_shape.restype = None
             _bind_ggml(lib)
             artifact = json.loads(lib.weft_hip_artifact())
             for kernel in artifact["kernels"]:
@@ -145,8 +150,11 @@ def synchronize() -> None:
 
 
 def launch_log() -> list[str]:
-    """Kernels this thread launched through the library since the last read."""
+    """Kernels this thread launched through the library since the last read.
+    The library keeps the log only once a thread asks for it, so the first
+    call turns it on for this thread (and returns what is there: nothing)."""
     lib = load()
+    lib.weft_hip_set_launch_log(1)
     n = lib.weft_hip_launch_log(None, 0)
     buf = ctypes.create_string_buffer(n + 1)
     lib.weft_hip_launch_log(buf, n + 1)

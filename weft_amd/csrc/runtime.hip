@@ -18,7 +18,13 @@ namespace weft {
 namespace {
 thread_local hipStream_t t_stream = nullptr;
 thread_local hipError_t t_error = hipSuccess;
-thread_local std::string t_launch_log;  // kernels launched since the log was last read
+// Kernels launched since the log was last read.  Off unless this thread
+// turned it on (weft_hip_set_launch_log); when on, it keeps at most the last
+// kLaunchLogCap bytes of names, so a caller that never reads it holds a
+// bounded amount of host memory.
+constexpr size_t kLaunchLogCap = 4096;
+thread_local bool t_log_on = false;
+thread_local std::string t_launch_log;
 thread_local TileBindings t_tiles;
 
 struct DeviceFacts {
@@ -58,9 +64,16 @@ void set_error(hipError_t e) {
 void check_launch(const char* kernel) {
   const hipError_t e = hipGetLastError();
   set_error(e);
-  if (kernel != nullptr && e == hipSuccess) {
+  if (t_log_on && kernel != nullptr && e == hipSuccess) {
     if (!t_launch_log.empty()) t_launch_log += ',';
     t_launch_log += kernel;
+    if (t_launch_log.size() > kLaunchLogCap) {
+      // drop whole names from the front
+      size_t cut = t_launch_log.size() - kLaunchLogCap;
+      const size_t comma = t_launch_log.find(',', cut);
+      cut = comma == std::string::npos ? t_launch_log.size() : comma + 1;
+      t_launch_log.erase(0, cut);
+    }
   }
 }
 
@@ -118,6 +131,13 @@ int weft_hip_synchronize(void) {
 
 const char* weft_hip_version(void) { return WEFT_HIP_VERSION_STRING; }
 
+int weft_hip_set_launch_log(int enable) {
+  const int was = weft::t_log_on ? 1 : 0;
+  weft::t_log_on = enable != 0;
+  if (!weft::t_log_on) weft::t_launch_log.clear();
+  return was;
+}
+
 size_t weft_hip_launch_log(char* buf, size_t len) {
   const size_t n = weft::t_launch_log.size();
   if (buf != nullptr && len > 0) {
@@ -158,24 +178,59 @@ namespace {
 
 __global__ void probe_empty_kernel() {}
 
-// grid-stride 16-byte loads, UNROLL in flight per lane, one 4-byte store
-// per wave (the decode kernels' store pattern)
-constexpr int kProbeUnroll = 4;
-__global__ void __launch_bounds__(512) probe_read_kernel(const uint4* __restrict__ src, size_t n16,
-                                                         uint32_t* __restrict__ sink) {
-  const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const size_t nth = (size_t)gridDim.x * blockDim.x;
+// 16-byte loads, U in flight per lane, one 4-byte store per wave (the
+// decode kernels' store pattern).  kBlocked: workgroup b reads one
+// contiguous chunk of the buffer (as a decode workgroup reads its rows);
+// otherwise the whole grid strides over it.  kNT: nontemporal loads.
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+template <int U, bool kNT, bool kBlocked>
+__global__ void __launch_bounds__(1024) probe_read_kernel(const v4u* __restrict__ src, size_t n16,
+                                                          uint32_t* __restrict__ sink) {
+  size_t first, end, stride;
+  if constexpr (kBlocked) {
+    const size_t chunk = (n16 + gridDim.x - 1) / gridDim.x;
+    first = (size_t)blockIdx.x * chunk + threadIdx.x;
+    end = min(n16, (size_t)(blockIdx.x + 1) * chunk);
+    stride = blockDim.x;
+  } else {
+    first = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    end = n16;
+    stride = (size_t)gridDim.x * blockDim.x;
+  }
   uint32_t acc = 0;
-  for (size_t i = tid; i < n16; i += nth * kProbeUnroll) {
-    uint4 v[kProbeUnroll];
+  for (size_t i = first; i < end; i += stride * U) {
+    v4u v[U];
 #pragma unroll
-    for (int u = 0; u < kProbeUnroll; ++u)
-      v[u] = i + u * nth < n16 ? src[i + u * nth] : make_uint4(0, 0, 0, 0);
+    for (int u = 0; u < U; ++u) {
+      const size_t j = i + u * stride;
+      if (j < end) {
+        if constexpr (kNT)
+          v[u] = __builtin_nontemporal_load(src + j);
+        else
+          v[u] = src[j];
+      } else {
+        v[u] = (v4u){0u, 0u, 0u, 0u};
+      }
+    }
 #pragma unroll
-    for (int u = 0; u < kProbeUnroll; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
   }
   for (int o = 32; o > 0; o >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, o, 64);
-  if ((threadIdx.x & 63) == 0) sink[tid >> 6] = acc;
+  if ((threadIdx.x & 63) == 0) sink[((size_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6] = acc;
+}
+
+template <int U>
+bool launch_probe(bool nt, bool blocked, int grid, int threads, const v4u* src, size_t n16, uint32_t* sink) {
+  hipStream_t s = current_stream();
+  if (nt && blocked)
+    probe_read_kernel<U, true, true><<<grid, threads, 0, s>>>(src, n16, sink);
+  else if (nt)
+    probe_read_kernel<U, true, false><<<grid, threads, 0, s>>>(src, n16, sink);
+  else if (blocked)
+    probe_read_kernel<U, false, true><<<grid, threads, 0, s>>>(src, n16, sink);
+  else
+    probe_read_kernel<U, false, false><<<grid, threads, 0, s>>>(src, n16, sink);
+  return true;
 }
 
 }  // namespace
@@ -188,14 +243,29 @@ void weft_hip_probe_empty(void) {
   weft::check_launch("probe_empty_kernel");
 }
 
-void weft_hip_probe_read(const void* src, size_t bytes, uint32_t* sink, int grid) {
-  if (src == nullptr || sink == nullptr || grid <= 0 || bytes % 16 != 0 || !weft::aligned(src, 16)) {
+void weft_hip_probe_read_shape(const void* src, size_t bytes, uint32_t* sink, int grid, int threads,
+                               int unroll, int flags) {
+  if (src == nullptr || sink == nullptr || grid <= 0 || bytes % 16 != 0 || !weft::aligned(src, 16) ||
+      threads <= 0 || threads > 1024 || threads % 64 != 0 || (flags & ~3) != 0) {
     weft::set_error(hipErrorInvalidValue);
     return;
   }
-  weft::probe_read_kernel<<<grid, 512, 0, weft::current_stream()>>>(static_cast<const uint4*>(src), bytes / 16,
-                                                                    sink);
+  const auto* p = static_cast<const weft::v4u*>(src);
+  const bool nt = flags & 1, blocked = flags & 2;
+  const size_t n16 = bytes / 16;
+  switch (unroll) {
+    case 1: weft::launch_probe<1>(nt, blocked, grid, threads, p, n16, sink); break;
+    case 2: weft::launch_probe<2>(nt, blocked, grid, threads, p, n16, sink); break;
+    case 4: weft::launch_probe<4>(nt, blocked, grid, threads, p, n16, sink); break;
+    case 8: weft::launch_probe<8>(nt, blocked, grid, threads, p, n16, sink); break;
+    case 16: weft::launch_probe<16>(nt, blocked, grid, threads, p, n16, sink); break;
+    default: weft::set_error(hipErrorInvalidValue); return;
+  }
   weft::check_launch("probe_read_kernel");
+}
+
+void weft_hip_probe_read(const void* src, size_t bytes, uint32_t* sink, int grid) {
+  weft_hip_probe_read_shape(src, bytes, sink, grid, 512, 4, 0);
 }
 
 }  // extern "C"
