@@ -49,9 +49,12 @@ void *weft_hip_get_stream(void);
 /* Source tile bindings of the calling thread (CompileOptions.meta; no
  * counterpart in the generated C, where they are compile-time constants):
  * "NC" = weight rows per workgroup and "MR" = activation rows per pass
- * (1..4) of the GEMV kernels; 0 unsets.  Returns 1 when the name has a
- * launch knob here, 0 otherwise (the MFMA GEMMs' 64 x 128 tiles are fixed).
- * weft_hip_clear_tile_bindings unsets every binding. */
+ * (1..4) of the GEMV kernels; for the Q4_K prefill GEMM (M >= 16 of
+ * production_mul_mat_q4_k_staged / production_mul_mat_q4_k) "NC" = weight
+ * rows per tile (<= 64: 64, else 128) and "MC" = activation rows per tile
+ * (<= 32: 32, else 64); 0 unsets.  Returns 1 when the name has a launch
+ * knob here, 0 otherwise (KC, NR and the other MFMA GEMMs' fixed 64 x 128
+ * tiles).  weft_hip_clear_tile_bindings unsets every binding. */
 int weft_hip_set_tile_binding(const char *name, size_t value);
 void weft_hip_clear_tile_bindings(void);
 int weft_hip_get_last_error(void);       /* hipError_t, then cleared */

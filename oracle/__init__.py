@@ -316,6 +316,59 @@ def random_records(fmt: str, n: int, k: int, seed: int = 0) -> np.ndarray:
     return rec.reshape(n, -1)
 
 
+def iq2_tables_mul_mat_f64(fmt: str, W: np.ndarray, Xq: np.ndarray, n: int, k: int, m: int,
+                           grid: np.ndarray, signs: np.ndarray):
+    """fp64 re-accumulation (E, A) of IQ2_XXS / IQ2_XS rows against Q8_K rows
+    with CALLER tables, as the reference's kernels state it for any I8X8
+    grid and sign table: each weight byte is grid * sign as i8 x i8 -> i8,
+    wrapping modulo 256 (examples/kernels/vec_dot/iq2_xxs_q8_k.py:25-45,
+    examples/functions/quantization.py:71-83: equal element types are not
+    promoted, python/weft/frontend/compiler.py:1276-1292); those bytes are
+    dotted with the Q8_K bytes in int32 per grid entry pair of one scale
+    (IQ2_XXS: a 32-group with 2 s + 1, s = the group word's top 4 bits;
+    IQ2_XS: a 16-element half with 2 s + 1 from its scale nibble), then
+    fp16 d * Q8_K d * 0.125 per superblock.  GGML's generic vec_dots
+    (ggml-cpu/quants.c:855-946) are the same function on GGML's tables.
+    Numpy, small shapes (tests only).  E = sum of the superblock terms, A =
+    sum of their magnitudes (oracle.within_tolerance), as wo_mul_mat_f64."""
+    xs = fmt == "iq2_xs"
+    rec = 74 if xs else 66
+    nsb = k // 256
+    g8 = np.asarray(grid, np.int8).reshape(-1, 8)
+    s8 = np.asarray(signs, np.int8).reshape(128, 8)
+    Wr = np.ascontiguousarray(W, np.uint8).reshape(n, nsb, rec)
+    Xr = np.ascontiguousarray(Xq, np.uint8).reshape(m, nsb, 292)
+    dw = fp16_to_fp32(Wr[:, :, 0:2].copy().view(np.uint16)[..., 0]).astype(np.float64)    # (n, nsb)
+    dx = Xr[:, :, 0:4].copy().view(np.float32)[..., 0].astype(np.float64)              # (m, nsb)
+    xq = Xr[:, :, 4:260].view(np.int8).astype(np.int64).reshape(m, nsb, 16, 16)        # 16 halves of 16
+    words = Wr[:, :, 2:66].copy().view(np.uint16).astype(np.int64)                     # (n, nsb, 32)
+    if xs:
+        gi = words & 511                                                                # entry e: elements 8e..
+        si = words >> 9
+        sc = Wr[:, :, 66:74].astype(np.int64)
+        ls = np.stack([sc & 15, sc >> 4], axis=-1).reshape(n, nsb, 16)                  # per 16-half
+    else:
+        w4 = words.reshape(n, nsb, 8, 4)
+        idx = w4[..., 0] | (w4[..., 1] << 16)
+        meta = w4[..., 2] | (w4[..., 3] << 16)
+        gi = np.stack([(idx >> (8 * l)) & 255 for l in range(4)], axis=-1).reshape(n, nsb, 32)
+        si = np.stack([(meta >> (7 * l)) & 127 for l in range(4)], axis=-1).reshape(n, nsb, 32)
+        ls = np.repeat(meta >> 28, 2, axis=-1)                                          # per 16-half
+    # i8 x i8 -> i8 (wraps), then widened: (n, nsb, 32 entries, 8)
+    wb = (g8[gi].astype(np.int16) * s8[si].astype(np.int16)).astype(np.int8).astype(np.int64)
+    wb = wb.reshape(n, nsb, 16, 16)
+    # integer sums per 16-element half: (m, n, nsb, 16)
+    part = np.einsum("msjt,nsjt->mnsj", xq, wb)
+    term = part * (2 * ls[None] + 1)
+    if not xs:  # one scale per 32-group: the two halves' integer sum times 2 s + 1
+        term = (part[..., 0::2] + part[..., 1::2]) * (2 * ls[None, ..., 0::2] + 1)
+    block = term.sum(axis=3)                                    # each superblock's exact integer sum
+    scale = 0.125 * dw[None, :, :] * dx[:, None, :]                                     # (m, n, nsb)
+    e = (scale * block).sum(axis=2)
+    a = np.abs(scale * block).sum(axis=2)
+    return e, a
+
+
 def max_threads() -> int:
     return int(lib().wo_max_threads())
 

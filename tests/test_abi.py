@@ -127,14 +127,16 @@ def test_launch_log_is_off_until_a_thread_turns_it_on():
         lib.weft_hip_set_launch_log(was)
 
 
-def test_tile_bindings_accept_the_gemv_knobs_only():
-    """NC and MR retile the GEMV launches; other meta names have no gfx950
-    knob (0, no error); a value above INT32_MAX or no name is an error."""
+def test_tile_bindings_accept_the_launch_knobs_only():
+    """NC and MR retile the GEMV launches, NC and MC the Q4_K GEMM's tiles;
+    other meta names have no gfx950 knob (0, no error); a value above
+    INT32_MAX or no name is an error."""
     lib = _lib.load()
     try:
         assert lib.weft_hip_set_tile_binding(b"NC", 64) == 1
         assert lib.weft_hip_set_tile_binding(b"MR", 2) == 1
-        for name in (b"KC", b"MC", b"NR", b"nc", b""):
+        assert lib.weft_hip_set_tile_binding(b"MC", 32) == 1
+        for name in (b"KC", b"NR", b"nc", b""):
             assert lib.weft_hip_set_tile_binding(name, 8) == 0
         assert lib.weft_hip_get_last_error() == 0
         lib.weft_hip_set_tile_binding(b"NC", 1 << 31)

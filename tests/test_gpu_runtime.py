@@ -118,6 +118,41 @@ def test_tile_bindings_retile_the_gemv_launches(torch_dev, definition, fmt):
     assert _lib.load().weft_hip_set_tile_binding(b"NR", 2) == 0  # no GEMV knob
 
 
+def test_tile_bindings_choose_the_q4k_gemm_tiling(torch_dev):
+    """MC and NC reach the Q4_K prefill GEMM as its tile (activation rows x
+    weight rows per workgroup tile, examples/kernels/mul_mat/q4_k_staged.py:
+    20-24): each binding launches its own tiling and workgroup count (the
+    launch log), and every tiling gives the same outputs bit for bit (each
+    output is one wave's superblock chain in a fixed order) within the
+    oracle's bar."""
+    from weft_amd import _lib
+    torch, dev = torch_dev
+    n, k, m = 300, 1024, 80  # ragged tiles on both axes
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    w = o.quantize("q4_k", o.seeded_normal(67, (n, k), 0.02))
+    x = o.seeded_normal(68, (m, k))
+    want_xq = o.quantize("q8_k", x)
+    e, a = o.mul_mat_f64("q4_k", w, want_xq, n, k, m)
+    outs = []
+    for mc, nc in ((64, 128), (32, 128), (64, 64), (32, 64), (8, 64)):
+        fn = compile(K.production_mul_mat_q4_k_staged, options=CompileOptions(meta={"NC": nc, "KC": 512, "MC": mc, "MR": 2}))
+        assert fn.metadata["bindings_without_launch_knob"] == ("KC",)
+        xq_t = torch.zeros(m * (k // 256) * 292, dtype=torch.uint8, device=dev)
+        y_t = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+        _lib.launch_log()
+        fn(Buffer(torch.from_numpy(w).to(dev), shape=(n, k), encoding="Q4_K"),
+           torch.from_numpy(x).to(dev), Buffer(xq_t, shape=(m, k), encoding="Q8_K"), y_t)
+        gemm = [name for name in _lib.launch_log() if name.startswith("q4k_mfma_gemm")]
+        mt, nt = (32 if mc <= 32 else 64), (64 if nc <= 64 else 128)
+        tiles = -(-m // mt) * -(-n // nt)
+        assert gemm == [f"q4k_mfma_gemm_{mt}x{nt}/{min(tiles, cus)}"], gemm
+        assert np.array_equal(xq_t.cpu().numpy().reshape(m, -1), want_xq)
+        outs.append(y_t.cpu().numpy())
+        assert o.within_tolerance(outs[-1], e, a).all()
+    for y in outs[1:]:
+        np.testing.assert_array_equal(y.view(np.uint32), outs[0].view(np.uint32))
+
+
 @pytest.mark.parametrize("definition,fmt", [(K.production_mul_mat_q5_k_decode, "q5_k"),
                                             (K.production_mul_mat_q6_k_decode, "q6_k"),
                                             (K.production_mul_mat_q4_1_decode, "q4_1")])

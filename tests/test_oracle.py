@@ -612,6 +612,47 @@ def test_ggml_scheduled_mul_mat_equals_the_pinned_mul_mat(fmt, n, m):
         assert np.array_equal(gy.view(np.uint32), y.view(np.uint32))
 
 
+@pytest.mark.parametrize("fmt", ["iq2_xxs", "iq2_xs"])
+def test_iq2_caller_table_oracle_is_the_ggml_function_on_ggml_tables(fmt):
+    """oracle.iq2_tables_mul_mat_f64 with GGML's grid and sign tables is the
+    pinned wo_mul_mat_f64 (GGML's generic vec_dot), E and A exactly."""
+    n, k, m = 13, 1024, 3
+    w = o.random_records(fmt, n, k, seed=91) if fmt == "iq2_xs" else \
+        o.quantize(fmt, o.seeded_normal(91, (n, k), 0.02))
+    xq = o.quantize("q8_k", o.seeded_normal(92, (m, k)))
+    grid = (o.iq2xs_grid() if fmt == "iq2_xs" else o.iq2xxs_grid()).view(np.int8)
+    e, a = o.mul_mat_f64(fmt, w, xq, n, k, m)
+    e2, a2 = o.iq2_tables_mul_mat_f64(fmt, w, xq, n, k, m, grid, o.signs_i8x8())
+    np.testing.assert_array_equal(e2, e)
+    np.testing.assert_array_equal(a2, a)
+
+
+@pytest.mark.parametrize("fmt", ["iq2_xxs", "iq2_xs"])
+def test_iq2_caller_table_oracle_known_answer(fmt):
+    """One superblock, worked by hand: grid row 3 = (-56, 1, 0, 127, -128,
+    -1, 2, 10) against sign row 5 = (3, -1, 7, 2, -1, 1, 0, -128) in i8
+    arithmetic gives bytes (88, -1, 0, -2, -128, -1, 0, 0) (-168, 254, 128
+    and -1280 wrap modulo 256); against x = 1..8 that is -568; scale nibble
+    2 -> times 5; d = 1, dx = 0.5, times 0.125: -177.5."""
+    grid = np.zeros((512 if fmt == "iq2_xs" else 256, 8), np.int8)
+    grid[3] = (-56, 1, 0, 127, -128, -1, 2, 10)
+    signs = np.zeros((128, 8), np.int8)
+    signs[5] = (3, -1, 7, 2, -1, 1, 0, -128)
+    rec = np.zeros(74 if fmt == "iq2_xs" else 66, np.uint8)
+    rec[0:2] = np.array([1.0], np.float16).view(np.uint8)
+    if fmt == "iq2_xs":
+        rec[2:4] = np.array([3 | (5 << 9)], np.uint16).view(np.uint8)  # entry 0: grid 3, sign 5
+        rec[66] = 2                                                    # elements 0-15: 2 s + 1 = 5
+    else:
+        rec[2] = 3                                                     # group 0, entry 0: grid 3
+        rec[6:10] = np.array([5 | (2 << 28)], np.uint32).view(np.uint8)  # sign row 5, s = 2
+    xq = np.zeros(292, np.uint8)
+    xq[0:4] = np.array([0.5], np.float32).view(np.uint8)
+    xq[4:12] = np.arange(1, 9, dtype=np.int8).view(np.uint8)
+    e, a = o.iq2_tables_mul_mat_f64(fmt, rec[None], xq[None], 1, 256, 1, grid, signs)
+    assert e[0, 0] == -177.5 and a[0, 0] == 177.5
+
+
 def test_int_partials_q4_0_are_the_block_dots():
     k = 512
     w = o.quantize("q4_0", o.seeded_normal(41, (1, k), 0.02))

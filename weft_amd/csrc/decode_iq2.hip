@@ -15,13 +15,17 @@
 // and, for IQ2_XS, the two groups' scale bytes.  Its 64 activation values
 // (the same for every row) are read from LDS into VGPRs once.  Grid rows and
 // sign masks (the +-1 sign table turned into 0xff / 0x00 byte masks as it
-// is staged) come from LDS tables; products run on v_dot4_i32_i8.  A
+// is staged) come from LDS tables; products run on v_dot4_i32_i8.  Tables
+// outside the masks' precondition (a sign byte other than +-1, a grid byte
+// of 0) are detected as they are staged and take the i8 byte product of
+// grid and sign instead (weft_common.h).  A
 // superblock's exact integer sum is the sum over its four lanes (DPP), then
 // one fp32 term per superblock and a wave sum per row.  A wave walks its
 // rows with one row of lookahead.  The activation is quantized in every
 // workgroup (16 lanes per superblock, bit-exact with quantize_row_q8_K_ref);
 // workgroup 0 writes Xq, so the mul_mat is one launch.
 #include <algorithm>
+#include <type_traits>
 
 #include "activation.h"
 #include "kernels.h"
@@ -51,10 +55,9 @@ struct Iq2Args {
 // table is held in LDS
 __device__ __forceinline__ uint32_t iq2_sign_mask(uint32_t s) { return ((s >> 7) & 0x01010101u) * 0xffu; }
 
-// negate the bytes of g whose mask byte in m is 0xff: bytes of g are grid
-// magnitudes, 8, 25 or 43 in GGML's tables, and for b in [1, 127]
-// (b ^ 0xff) + 1 = 256 - b never carries into the next byte (a byte of 0
-// would)
+// negate the bytes of g whose mask byte in m is 0xff: for a byte b != 0,
+// (b ^ 0xff) + 1 = 256 - b never carries into the next byte (GGML's
+// magnitudes are 8, 25 and 43; a table with a 0 byte takes mul8x4)
 __device__ __forceinline__ int iq2_negate(uint32_t g, uint32_t m) {
   return (int)((g ^ m) + (m & 0x01010101u));
 }
@@ -65,8 +68,9 @@ __global__ void __launch_bounds__(kThreads) iq2_gemv_m1_kernel(Iq2Args a) {
   constexpr int kGridBytes = kXs ? 4096 : 2048;
   extern __shared__ __align__(16) char lds[];
   char* tgrid = lds;
-  char* tsign = lds + kGridBytes;
-  char* act = lds + kGridBytes + 1024;  // Q8_K activation row
+  char* tsign = lds + kGridBytes;         // sign rows as byte masks
+  char* traw = lds + kGridBytes + 1024;   // sign rows as given
+  char* act = lds + kGridBytes + 2048;    // Q8_K activation row
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int K = a.K;
@@ -118,9 +122,15 @@ __global__ void __launch_bounds__(kThreads) iq2_gemv_m1_kernel(Iq2Args a) {
   __builtin_amdgcn_sched_barrier(0);
 
   if (ti < kGridBytes / 4) reinterpret_cast<uint32_t*>(tgrid)[ti] = tg;
-  if (ti < 256) reinterpret_cast<uint32_t*>(tsign)[ti] = iq2_sign_mask(ts);
+  if (ti < 256) {
+    reinterpret_cast<uint32_t*>(tsign)[ti] = iq2_sign_mask(ts);
+    reinterpret_cast<uint32_t*>(traw)[ti] = ts;
+  }
+  // the tables take the mask path when every workgroup thread's words meet
+  // its precondition (the same answer in every workgroup)
+  const bool bad = (ti < kGridBytes / 4 && !iq2_grid_word_ok(tg)) || (ti < 256 && !iq2_sign_word_ok(ts));
   stager.finish(a.X, (size_t)K, blockIdx.x == 0 ? a.xq_out : nullptr, K, 0, 1, act);
-  __syncthreads();
+  const bool canon = __builtin_amdgcn_readfirstlane(__syncthreads_or(bad)) == 0;  // wave-uniform
 
   // this lane's 64 activation values and its superblock's scale
   int4 xa[4];
@@ -132,9 +142,12 @@ __global__ void __launch_bounds__(kThreads) iq2_gemv_m1_kernel(Iq2Args a) {
     dx = v.d[sb];
   }
   const uint2* grid = reinterpret_cast<const uint2*>(tgrid);
-  const uint2* sgn = reinterpret_cast<const uint2*>(tsign);
 
-  auto compute = [&](const RowBuf& buf, int k) {
+  // kGen: any int8 tables, each weight byte the i8 product grid * sign;
+  // otherwise the sign masks' negate
+  auto compute = [&](const RowBuf& buf, int k, auto gen) {
+    constexpr bool kGen = decltype(gen)::value;
+    const uint2* sgn = reinterpret_cast<const uint2*>(kGen ? traw : tsign);
     uint32_t q[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) q[i] = dsh ? __builtin_amdgcn_alignbyte(buf.w[i + 1], buf.w[i], 2) : buf.w[i];
@@ -156,8 +169,10 @@ __global__ void __launch_bounds__(kThreads) iq2_gemv_m1_kernel(Iq2Args a) {
           gv = grid[(q[2 * u] >> (8 * l)) & 0xffu];
           sv = sgn[(q[2 * u + 1] >> (7 * l)) & 127u];
         }
-        part[l >> 1] = dot4(iq2_negate(gv.x, sv.x), xv[2 * l], part[l >> 1]);
-        part[l >> 1] = dot4(iq2_negate(gv.y, sv.y), xv[2 * l + 1], part[l >> 1]);
+        const int w0 = kGen ? (int)mul8x4(gv.x, sv.x) : iq2_negate(gv.x, sv.x);
+        const int w1 = kGen ? (int)mul8x4(gv.y, sv.y) : iq2_negate(gv.y, sv.y);
+        part[l >> 1] = dot4(w0, xv[2 * l], part[l >> 1]);
+        part[l >> 1] = dot4(w1, xv[2 * l + 1], part[l >> 1]);
       }
       if constexpr (kXs) {
         const uint32_t sb8 = (buf.s >> (8 * u)) & 0xffu;
@@ -173,20 +188,26 @@ __global__ void __launch_bounds__(kThreads) iq2_gemv_m1_kernel(Iq2Args a) {
     if (lane == 0) a.Y[row_first + k * kWaves] = 0.125f * tot;
   };
 
-  int k = 0;
-  for (; k + 2 < nrows; k += 2) {
-    issue(bufB, k + 1);
-    compute(bufA, k);
-    issue(bufA, k + 2);
-    compute(bufB, k + 1);
-  }
-  if (nrows - k == 2) {
-    issue(bufB, k + 1);
-    compute(bufA, k);
-    compute(bufB, k + 1);
-  } else if (nrows - k == 1) {
-    compute(bufA, k);
-  }
+  auto rows = [&](auto gen) {
+    int k = 0;
+    for (; k + 2 < nrows; k += 2) {
+      issue(bufB, k + 1);
+      compute(bufA, k, gen);
+      issue(bufA, k + 2);
+      compute(bufB, k + 1, gen);
+    }
+    if (nrows - k == 2) {
+      issue(bufB, k + 1);
+      compute(bufA, k, gen);
+      compute(bufB, k + 1, gen);
+    } else if (nrows - k == 1) {
+      compute(bufA, k, gen);
+    }
+  };
+  if (canon)
+    rows(std::false_type{});
+  else
+    rows(std::true_type{});
 }
 
 }  // namespace
@@ -219,7 +240,7 @@ bool decode_iq2_m1(bool xs, const uint8_t* W, const float* X, uint8_t* Xq, const
   a.rows_per_wg = nc > 0 ? (int)std::min<size_t>(N, (size_t)nc) : (int)((N + wgs - 1) / wgs);
   a.ldw = ldw;
   const int g = (int)((N + a.rows_per_wg - 1) / a.rows_per_wg);
-  const size_t lds = (xs ? 4096 : 2048) + 1024 + q8k_lds_row_bytes((int)K);
+  const size_t lds = (xs ? 4096 : 2048) + 2048 + q8k_lds_row_bytes((int)K);
   if (xs)
     iq2_gemv_m1_kernel<true><<<g, kThreads, lds, current_stream()>>>(a);
   else

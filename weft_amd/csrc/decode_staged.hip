@@ -105,7 +105,7 @@ constexpr bool act_q81() {
 // LDS for lookup tables: IQ2_XS's 512 x 8 grid and 128 x 8 signs, else 3 KB
 template <Fmt F>
 constexpr int table_bytes() {
-  return F == Fmt::IQ2_XS ? 5120 : 3072;
+  return F == Fmt::IQ2_XS ? 6144 : F == Fmt::IQ2_XXS ? 4096 : 3072;
 }
 
 struct Args {
@@ -216,9 +216,9 @@ __device__ __forceinline__ int lookup16(uint32_t n, uint32_t c0, uint32_t c1, ui
 // staged in LDS
 __device__ __forceinline__ uint32_t sign_mask4(uint32_t s) { return ((s >> 7) & 0x01010101u) * 0xffu; }
 
-// negate the bytes of g where the mask byte is 0xff: bytes of g are grid
-// magnitudes (8, 25 or 43 in GGML's tables), and for b in [1, 127]
-// (b ^ 0xff) + 1 never carries into the next byte (a byte of 0 would)
+// negate the bytes of g where the mask byte is 0xff: for a byte b != 0,
+// (b ^ 0xff) + 1 never carries into the next byte (tables with a 0 grid
+// byte or a sign other than +-1 take mul8x4, weft_common.h)
 __device__ __forceinline__ int apply_signs(uint32_t g, uint32_t m) {
   return (int)((g ^ m) + (m & 0x01010101u));
 }
@@ -237,20 +237,22 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
   const int nwaves = blockDim.x / kWave;
   const int K = a.K;
 
-  if constexpr (F == Fmt::IQ2_XXS) {
-    // grid I8X8[256x8] then signs I8X8[128x8] as byte masks
-    for (int i = threadIdx.x; i < 512; i += blockDim.x)
-      reinterpret_cast<uint32_t*>(tables)[i] = reinterpret_cast<const uint32_t*>(a.tab0)[i];
-    for (int i = threadIdx.x; i < 256; i += blockDim.x)
-      reinterpret_cast<uint32_t*>(tables + 2048)[i] =
-          sign_mask4(reinterpret_cast<const uint32_t*>(a.tab1)[i]);
-  } else if constexpr (F == Fmt::IQ2_XS) {
-    // grid I8X8[512x8] then signs I8X8[128x8] as byte masks
-    for (int i = threadIdx.x; i < 1024; i += blockDim.x)
-      reinterpret_cast<uint32_t*>(tables)[i] = reinterpret_cast<const uint32_t*>(a.tab0)[i];
-    for (int i = threadIdx.x; i < 256; i += blockDim.x)
-      reinterpret_cast<uint32_t*>(tables + 4096)[i] =
-          sign_mask4(reinterpret_cast<const uint32_t*>(a.tab1)[i]);
+  // IQ2: the grid, then the sign rows as byte masks, then as given; `bad`
+  // marks a table word outside the masks' precondition (weft_common.h)
+  bool bad = false;
+  if constexpr (F == Fmt::IQ2_XXS || F == Fmt::IQ2_XS) {
+    constexpr int kGridWords = F == Fmt::IQ2_XS ? 1024 : 512;
+    for (int i = threadIdx.x; i < kGridWords; i += blockDim.x) {
+      const uint32_t g = reinterpret_cast<const uint32_t*>(a.tab0)[i];
+      reinterpret_cast<uint32_t*>(tables)[i] = g;
+      bad |= !iq2_grid_word_ok(g);
+    }
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) {
+      const uint32_t sg = reinterpret_cast<const uint32_t*>(a.tab1)[i];
+      reinterpret_cast<uint32_t*>(tables + 4 * kGridWords)[i] = sign_mask4(sg);
+      reinterpret_cast<uint32_t*>(tables + 4 * kGridWords + 1024)[i] = sg;
+      bad |= !iq2_sign_word_ok(sg);
+    }
   } else if constexpr (F == Fmt::MXFP4 || F == Fmt::NVFP4) {
     for (int i = threadIdx.x; i < 256; i += blockDim.x)
       reinterpret_cast<float*>(tables)[i] = reinterpret_cast<const float*>(a.tab1)[i];
@@ -298,7 +300,8 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
     else
       stage_q80_load(a.xq_in, K, a.m0, a.mb, act);
   }
-  __syncthreads();
+  // IQ2 tables within the masks' precondition (the same in every workgroup)
+  const bool canon = __builtin_amdgcn_readfirstlane(__syncthreads_or(bad)) == 0;  // wave-uniform
 
   uint32_t c0 = 0, c1 = 0, c2 = 0, c3 = 0;
   if constexpr (F == Fmt::MXFP4 || F == Fmt::NVFP4) {
@@ -416,15 +419,15 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
           lds_run(win, o + 2 + 8 * g, q);
           const uint32_t sc = lds_u32(win, o + 66 + g) & 0xffu;
           const uint2* grid = reinterpret_cast<const uint2*>(tables);
-          const uint2* sgn = reinterpret_cast<const uint2*>(tables + 4096);
+          const uint2* sgn = reinterpret_cast<const uint2*>(tables + (canon ? 4096 : 5120));
           int wv[8];
 #pragma unroll
           for (int l = 0; l < 4; ++l) {
             const uint32_t word = (q[l >> 1] >> (16 * (l & 1))) & 0xffffu;
             const uint2 gv = grid[word & 511u];
             const uint2 sv = sgn[word >> 9];
-            wv[2 * l] = apply_signs(gv.x, sv.x);
-            wv[2 * l + 1] = apply_signs(gv.y, sv.y);
+            wv[2 * l] = canon ? apply_signs(gv.x, sv.x) : (int)mul8x4(gv.x, sv.x);
+            wv[2 * l + 1] = canon ? apply_signs(gv.y, sv.y) : (int)mul8x4(gv.y, sv.y);
           }
           const int ls1 = 2 * (int)(sc & 15u) + 1, ls2 = 2 * (int)(sc >> 4) + 1;
 #pragma unroll
@@ -592,14 +595,14 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
           const uint32_t idx = lds_u32(win, o + 2 + 8 * g);
           const uint32_t meta = lds_u32(win, o + 6 + 8 * g);
           const uint2* grid = reinterpret_cast<const uint2*>(tables);
-          const uint2* sgn = reinterpret_cast<const uint2*>(tables + 2048);
+          const uint2* sgn = reinterpret_cast<const uint2*>(tables + (canon ? 2048 : 3072));
           int wv[8];
 #pragma unroll
           for (int l = 0; l < 4; ++l) {
             const uint2 gv = grid[(idx >> (8 * l)) & 0xffu];
             const uint2 sv = sgn[(meta >> (7 * l)) & 127u];
-            wv[2 * l] = apply_signs(gv.x, sv.x);
-            wv[2 * l + 1] = apply_signs(gv.y, sv.y);
+            wv[2 * l] = canon ? apply_signs(gv.x, sv.x) : (int)mul8x4(gv.x, sv.x);
+            wv[2 * l + 1] = canon ? apply_signs(gv.y, sv.y) : (int)mul8x4(gv.y, sv.y);
           }
           const int ls = 2 * (int)(meta >> 28) + 1;
 #pragma unroll

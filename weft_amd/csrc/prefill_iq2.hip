@@ -20,6 +20,7 @@
 // each parity reads its half with aligned dword reads and byte alignment.
 // Grid and sign tables live in LDS, the signs as byte masks (0xff per -1).
 #include <algorithm>
+#include <type_traits>
 
 #include "kernels.h"
 #include "runtime.h"
@@ -72,16 +73,18 @@ struct GemmArgs {
 // Direct global->LDS loads; lane l writes [lds + size*l, +size).  Inline asm
 // keeps the compiler from making unrelated LDS reads wait for them; the
 // kernel waits (s_waitcnt) itself.  Nothing else in this kernel uses M0.
+// `lds` is wave-uniform; readfirstlane states it, so it is an SGPR operand
+// in every instantiation.
 __device__ __forceinline__ void lds_dma16(const uint8_t* g, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
                :
-               : "s"(lds), "v"(g)
+               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g)
                : "memory", "m0");
 }
 __device__ __forceinline__ void lds_dma4(const uint8_t* g, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
                :
-               : "s"(lds), "v"(g)
+               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g)
                : "memory", "m0");
 }
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -97,12 +100,20 @@ __device__ __forceinline__ uint32_t ld32(const uint8_t* p) {
 // VALU read of an MFMA result needs.)
 __device__ __forceinline__ void pin(int& v) { asm volatile("" : "+v"(v)); }
 // negate the bytes of g whose mask byte in m is 0xff (the sign table is
-// staged in LDS as byte masks: 0xff where the +-1 byte is -1).  Bytes of g
-// are grid magnitudes, 8, 25 or 43 in GGML's tables: for b in [1, 127],
-// (b ^ 0xff) + 1 = 256 - b never carries into the next byte (a byte of 0
-// would)
+// staged in LDS as byte masks: 0xff where the +-1 byte is -1): for a byte
+// b != 0, (b ^ 0xff) + 1 = 256 - b never carries into the next byte (GGML's
+// grid magnitudes are 8, 25 and 43)
 __device__ __forceinline__ uint32_t apply_signs(uint32_t g, uint32_t m) {
   return (g ^ m) + (m & 0x01010101u);
+}
+// four weight bytes: the masks' negate, or (tables outside its
+// precondition) the i8 products of grid and sign bytes
+template <class Gen>
+__device__ __forceinline__ uint32_t sign8(uint32_t g, uint32_t z, Gen) {
+  if constexpr (Gen::value)
+    return mul8x4(g, z);
+  else
+    return apply_signs(g, z);
 }
 
 // kXs (IQ2_XS, ggml-cpu/quants.c:897-946): u16 entries (grid row bits 0-8,
@@ -121,7 +132,8 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
   // outer-product factor MFMA ((h,h), (m,m), (l,l), 0)
   __shared__ __align__(16) uint4 dxq[2][2][kMT];
   __shared__ __align__(16) uint8_t tgrid[TT::kGrid * 8];
-  __shared__ __align__(16) uint8_t tsign[128 * 8];
+  __shared__ __align__(16) uint8_t tsign[128 * 8];  // sign rows as byte masks
+  __shared__ __align__(16) uint8_t traw[128 * 8];   // sign rows as given
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -205,7 +217,11 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
   const int sw = col & 15;
   const int sb0 = par * TT::kRec;  // this parity's record within the pair: 0 or 66 / 74
 
-  auto step = [&](int pair, const uint8_t* cur, uint8_t* nxt) {
+  // kGen: any int8 tables, each weight byte the i8 product grid * sign;
+  // otherwise the sign masks' negate
+  auto step = [&](int pair, const uint8_t* cur, uint8_t* nxt, auto gen) {
+    constexpr bool kGen = decltype(gen)::value;
+    const uint8_t* tsg = kGen ? traw : tsign;
     __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of this pair have landed
     __syncthreads();                // everyone's; the previous pair is consumed
     const bool refill = pair + 1 < npair;
@@ -239,10 +255,10 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
         const uint32_t e0 = ew & 0xffffu, e1 = ew >> 16;
         const uint2 g0 = *reinterpret_cast<const uint2*>(tgrid + 8 * (e0 & 511u));
         const uint2 g1 = *reinterpret_cast<const uint2*>(tgrid + 8 * (e1 & 511u));
-        const uint2 z0 = *reinterpret_cast<const uint2*>(tsign + 8 * (e0 >> 9));
-        const uint2 z1 = *reinterpret_cast<const uint2*>(tsign + 8 * (e1 >> 9));
-        const v4i bv = {(int)apply_signs(g0.x, z0.x), (int)apply_signs(g0.y, z0.y),
-                        (int)apply_signs(g1.x, z1.x), (int)apply_signs(g1.y, z1.y)};
+        const uint2 z0 = *reinterpret_cast<const uint2*>(tsg + 8 * (e0 >> 9));
+        const uint2 z1 = *reinterpret_cast<const uint2*>(tsg + 8 * (e1 >> 9));
+        const v4i bv = {(int)sign8(g0.x, z0.x, gen), (int)sign8(g0.y, z0.y, gen),
+                        (int)sign8(g1.x, z1.x, gen), (int)sign8(g1.y, z1.y, gen)};
         const v4i bz = {};
         const uint32_t sb = ((g < 4 ? scl0 : scl1) >> (8 * (g & 3))) & 0xffu;
         const int ls_lo = 2 * (int)(sb & 15u) + 1, ls_hi = 2 * (int)(sb >> 4) + 1;
@@ -271,10 +287,10 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
       const uint32_t s0 = (meta >> (14 * kg)) & 127u, s1 = (meta >> (14 * kg + 7)) & 127u;
       const uint2 g0 = *reinterpret_cast<const uint2*>(tgrid + 8 * i0);
       const uint2 g1 = *reinterpret_cast<const uint2*>(tgrid + 8 * i1);
-      const uint2 z0 = *reinterpret_cast<const uint2*>(tsign + 8 * s0);
-      const uint2 z1 = *reinterpret_cast<const uint2*>(tsign + 8 * s1);
-      const v4i bv = {(int)apply_signs(g0.x, z0.x), (int)apply_signs(g0.y, z0.y),
-                      (int)apply_signs(g1.x, z1.x), (int)apply_signs(g1.y, z1.y)};
+      const uint2 z0 = *reinterpret_cast<const uint2*>(tsg + 8 * s0);
+      const uint2 z1 = *reinterpret_cast<const uint2*>(tsg + 8 * s1);
+      const v4i bv = {(int)sign8(g0.x, z0.x, gen), (int)sign8(g0.y, z0.y, gen),
+                      (int)sign8(g1.x, z1.x, gen), (int)sign8(g1.y, z1.y, gen)};
       const int ls = 2 * (int)(meta >> 28) + 1;
       const int chunk = (2 * g + kg) ^ sw;
 #pragma unroll
@@ -312,17 +328,36 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
   };
 
   issue(0, ring0);
-  // the tables after the first stage's loads: their round trip overlaps it
-  for (int i = tid; i < TT::kGrid * 8; i += kThreads) tgrid[i] = (uint8_t)a.grid[i];
-  for (int i = tid; i < 128 * 8; i += kThreads) tsign[i] = a.signs[i] < 0 ? 0xffu : 0u;  // byte masks
+  // the tables after the first stage's loads: their round trip overlaps it.
+  // `bad` marks a grid byte of 0 or a sign byte other than +-1 (weft_common.h)
+  bool bad = false;
+  for (int i = tid; i < TT::kGrid * 8; i += kThreads) {
+    const int8_t gb = a.grid[i];
+    tgrid[i] = (uint8_t)gb;
+    bad |= gb == 0;
+  }
+  for (int i = tid; i < 128 * 8; i += kThreads) {
+    const int8_t sb = a.signs[i];
+    tsign[i] = sb < 0 ? 0xffu : 0u;  // byte masks
+    traw[i] = (uint8_t)sb;
+    bad |= sb != 1 && sb != -1;
+  }
+  // the same in every workgroup; wave-uniform, so the branch below is scalar
+  const bool canon = __builtin_amdgcn_readfirstlane(__syncthreads_or(bad)) == 0;
   if (wcol == 0) {
     load_dx(0);
     dxq[0][par][lane] = bf16_split3(dxr);
   }
-  for (int pair = 0; pair < npair; pair += 2) {
-    step(pair, ring0, ring1);
-    if (pair + 1 < npair) step(pair + 1, ring1, ring0);
-  }
+  auto run = [&](auto gen) {
+    for (int pair = 0; pair < npair; pair += 2) {
+      step(pair, ring0, ring1, gen);
+      if (pair + 1 < npair) step(pair + 1, ring1, ring0, gen);
+    }
+  };
+  if (canon)
+    run(std::false_type{});
+  else
+    run(std::true_type{});
 
   // both parities' partial sums -> two LDS planes (reusing the ring) -> Y
   __syncthreads();

@@ -67,6 +67,7 @@
 // tile's expert matrix, and each output goes to the pair's dst row.  The
 // workgroups walk the device's tile count (launched for the host's bound).
 #include <algorithm>
+#include <cstdio>
 
 #include "kernels.h"
 #include "runtime.h"
@@ -85,24 +86,40 @@ typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
-constexpr int kMT = 64;          // tokens per workgroup tile
-constexpr int kNT = 128;         // weight rows per workgroup tile
-constexpr int kMfmaWaves = 8;    // 4 column groups x 2 superblock parities
-constexpr int kLoaders = 2;      // loader waves, one per parity
-constexpr int kThreads = 64 * (kMfmaWaves + kLoaders);
+constexpr int kLoaders = 2;                    // loader waves, one per parity
 constexpr int kAQRow = 272;                    // 16 qs chunks + 1 pad chunk
-constexpr int kAQ = kMT * kAQRow;              // 17408
-constexpr int kAX = kMT * 48;                  // 3072
-constexpr int kWT = kNT * kQ4_KBytes;          // 18432
-constexpr int kStage = kAQ + kAX + kWT;        // 38912
-constexpr int kAQSlots = kAQ / 1024;           // 17
-constexpr int kAXSlots = kAX / 1024;           // 3
-constexpr int kSlots = kStage / 1024;          // 38 wave-wide 1 KB loads per superblock
 constexpr int kCohortBlock = 16 * kQ4_KBytes;  // 2304: one superblock of a 16-row interleaved cohort
-static_assert(kWT == (kNT / 16) * kCohortBlock, "a weight stage is eight cohort blocks");
-static_assert(kAQ % 1024 == 0 && kAX % 1024 == 0 && kStage % 1024 == 0,
-              "every region is a whole number of wave loads");
-static_assert(2 * kTilePlaneBytes <= 2 * kStage, "the output planes fit one ring slot");
+
+constexpr int round_kb(int b) { return (b + 1023) / 1024 * 1024; }
+
+// A workgroup tile of kMT tokens x kNT weight rows (kMT 32 or 64, kNT 64 or
+// 128): kNT / 32 column groups x 2 superblock parities of MFMA waves, each
+// wave kMT tokens x 32 rows (kMT / 32 accumulator tiles sharing one weight
+// operand), and the two loader waves.  The default and fastest at prefill
+// sizes is 64 x 128; the others serve CompileOptions.meta's MC / NC and
+// small M.
+template <int kMT_, int kNT_>
+struct Tiling {
+  static constexpr int kMT = kMT_;
+  static constexpr int kNT = kNT_;
+  static constexpr int kCols = kNT / 32;          // column groups
+  static constexpr int kT2 = kMT / 32;            // token tiles per wave
+  static constexpr int kMfmaWaves = 2 * kCols;
+  static constexpr int kThreads = 64 * (kMfmaWaves + kLoaders);
+  static constexpr int kAQ = round_kb(kMT * kAQRow);  // 17408 at 64 tokens
+  static constexpr int kAX = round_kb(kMT * 48);      // 3072
+  static constexpr int kWT = kNT * kQ4_KBytes;        // 18432 at 128 rows
+  static constexpr int kStage = kAQ + kAX + kWT;      // 38912
+  static constexpr int kAQSlots = kAQ / 1024;
+  static constexpr int kAXSlots = kAX / 1024;
+  static constexpr int kSlots = kStage / 1024;        // wave-wide 1 KB loads per superblock
+  static constexpr int kPlaneBytes = tile_plane_bytes<kMT, kNT>();
+  static_assert((kMT == 32 || kMT == 64) && (kNT == 64 || kNT == 128), "supported tilings");
+  static_assert(kWT == (kNT / 16) * kCohortBlock, "a weight stage is whole cohort blocks");
+  static_assert(kWT % 1024 == 0, "every region is a whole number of wave loads");
+  static_assert(2 * kPlaneBytes <= 2 * kStage, "the output planes fit one ring slot");
+};
+typedef Tiling<64, 128> DefaultTiling;
 
 struct GemmArgs {
   const uint8_t* W;
@@ -171,8 +188,13 @@ __device__ __forceinline__ uint2 tr8(uint32_t lds_byte_addr) {
 // byte j of row 16c + r's record).  A stage then holds the tile's eight
 // cohort blocks as they lie in memory, and each MFMA wave reads its rows'
 // header and nibble bytes transposed (tr8); everything else is the same.
-template <bool kGroup, bool kIlv = false>
-__global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
+template <bool kGroup, bool kIlv = false, class TL = DefaultTiling>
+__global__ void __launch_bounds__(TL::kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
+  constexpr int kMT = TL::kMT, kNT = TL::kNT, kCols = TL::kCols, kT2 = TL::kT2;
+  constexpr int kMfmaWaves = TL::kMfmaWaves, kStage = TL::kStage;
+  constexpr int kAQ = TL::kAQ, kAX = TL::kAX, kAQSlots = TL::kAQSlots, kAXSlots = TL::kAXSlots;
+  constexpr int kSlots = TL::kSlots;
+  static_assert(!kGroup || (kMT == 64 && kNT == 128), "grouped mode runs the 64 x 128 tile");
   __shared__ __align__(16) uint8_t ring[4 * kStage];  // [pair slot][parity]
   __shared__ __align__(16) uint32_t zero16[4];
 
@@ -280,6 +302,7 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
     // operand of the dx (x) dw outer product: bf16 pairs (h,h), (m,m), (l,l),
     // 0 with d = h + m + l to 2^-24.
     auto convert = [&](int slot) {
+      if (lane >= kMT) return;  // past the tile's tokens: the region's padding
       uint8_t* ax = ring + (2 * slot + par) * kStage + kAQ + 48 * lane;
       const uint4 dch = *reinterpret_cast<const uint4*>(ax);
       const uint4 b0 = *reinterpret_cast<const uint4*>(ax + 16);
@@ -337,12 +360,12 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
   }
 
   // ------------------------------------------------------------ MFMA wave
-  const int par = wave >> 2, wcol = wave & 3;  // superblock parity, column group
+  const int par = wave / kCols, wcol = wave % kCols;  // superblock parity, column group
   const int col = lane & 31, kg = lane >> 5;
   const uint32_t zaddr = lds_addr(zero16);
 
-  v16i lo[2], hi[2];
-  v16f y[2];
+  v16i lo[kT2], hi[kT2];
+  v16f y[kT2];
   const v16i zero = {};
   const v16f fzero = {};
   int g = 0;  // pairs consumed over this workgroup's tiles: pair g sits in ring slot g & 1
@@ -350,7 +373,7 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
     Tile ti;
     if (!tile_info(t, ti)) continue;
 #pragma unroll
-    for (int t2 = 0; t2 < 2; ++t2)
+    for (int t2 = 0; t2 < kT2; ++t2)
 #pragma unroll
       for (int r = 0; r < 16; ++r) y[t2][r] = 0.f;
     for (int pair = 0; pair < npair; ++pair, ++g) {
@@ -395,9 +418,9 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
         ca[3] = __builtin_amdgcn_perm(0u, a47, 0x0c030c02u);
       }
 
-      v4i acur[2], anxt[2];
+      v4i acur[kT2], anxt[kT2];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) acur[t] = *reinterpret_cast<const v4i*>(AQ + 32 * kAQRow * t);
+      for (int t = 0; t < kT2; ++t) acur[t] = *reinterpret_cast<const v4i*>(AQ + 32 * kAQRow * t);
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         uint4 q;
@@ -413,7 +436,7 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
           const int s = 2 * g + hf;
           if (s < 7) {
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+            for (int t = 0; t < kT2; ++t)
               anxt[t] = *reinterpret_cast<const v4i*>(AQ + 32 * kAQRow * t + 32 * (s + 1));
           }
           const uint32_t n0w = hf ? (q.x >> 4) & 0x0f0f0f0fu : q.x & 0x0f0f0f0fu;
@@ -430,18 +453,18 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
           const v4i b_lo = {mul(n0w, mb), mul(n1w, mb), mul(n2w, mb), mul(n3w, mb)};
           const v4i b_hi = {mul(n0w, ma), mul(n1w, ma), mul(n2w, ma), mul(n3w, ma)};
 #pragma unroll
-          for (int t = 0; t < 2; ++t) {
+          for (int t = 0; t < kT2; ++t) {
             lo[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(acur[t], b_lo, s == 0 ? zero : lo[t], 0, 0, 0);
             hi[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(acur[t], b_hi, s == 0 ? zero : hi[t], 0, 0, 0);
           }
 #pragma unroll
-          for (int t = 0; t < 2; ++t) acur[t] = anxt[t];
+          for (int t = 0; t < kT2; ++t) acur[t] = anxt[t];
         }
       }
 
       // min term (f16: converted bsums x duplicated mins) and the dx (x) f
       // outer product (bf16: token-scale splits x f = f_h + f_l, exact)
-      v16f mn[2], qd[2];
+      v16f mn[kT2], qd[kT2];
       {
         const uint32_t mn03 = h.z & 0x3f3f3f3fu;
         const uint32_t mn47 = ((h.w >> 4) & 0x0f0f0f0fu) | (((h.z >> 6) & 0x03030303u) << 4);
@@ -452,7 +475,7 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
         const uint32_t pf = kg ? 0u : pk_bf16(f, f - bf16_lo_to_f32(pfh));
         const v4i bq = {(int)pf, (int)pf, (int)pf, 0};
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int t = 0; t < kT2; ++t) {
           const v4i am = *reinterpret_cast<const v4i*>(AX + 1536 * t + 16 + 16 * kg);
           mn[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, am),
                                                         __builtin_bit_cast(v8h, bm), fzero, 0, 0, 0);
@@ -464,7 +487,7 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
       }
       // y += (dx f) (lo + 8 hi - r Mn)
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < kT2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const float d = fmaf(mn[t][r], nr, (float)(lo[t][r] + 8 * hi[t][r]));
@@ -477,7 +500,7 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
     // The first barrier: every wave is done reading that slot.
     __syncthreads();
     float* planes = reinterpret_cast<float*>(ring + 2 * ((g - 1) & 1) * kStage);
-    tile_partials_to_lds(y, wcol, lane, planes + par * (kTilePlaneBytes / 4));
+    tile_partials_to_lds_t<kT2, kNT>(y, wcol, lane, planes + par * (TL::kPlaneBytes / 4));
     __syncthreads();
     // grouped: lane r looks up the dst row of tile row r; the two rows this
     // lane stores are fetched by cross-lane permute here, where every lane
@@ -492,8 +515,8 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
       dst_lo = fetch(tile_store_row(wave, lane, 0));
       dst_hi = fetch(tile_store_row(wave, lane, 1));
     }
-    tile_store_from_lds(
-        wave, lane, planes, planes + kTilePlaneBytes / 4, ti.mrows, min(kNT, a.N - ti.n0),
+    tile_store_from_lds_t<kMT, kNT, kMfmaWaves>(
+        wave, lane, planes, planes + TL::kPlaneBytes / 4, ti.mrows, min(kNT, a.N - ti.n0),
         [&](int rr) {
           if constexpr (kGroup)
             return a.Y + (rr < 32 ? dst_lo : dst_hi) + ti.n0;
@@ -505,14 +528,47 @@ __global__ void __launch_bounds__(kThreads, 1) q4k_mfma_gemm(GemmArgs a) {
 }
 
 // The GEMM over an already quantized activation.  Weight rows must be
-// 4-byte aligned (dword direct-to-LDS loads) and a tile's 128 rows must stay
-// within 32-bit offsets.
+// 4-byte aligned (dword direct-to-LDS loads) and a tile's rows (up to 128)
+// must stay within 32-bit offsets.
 bool gemm_q4k_ok(const uint8_t* W, size_t N, size_t K, size_t M, const RowStrides& st) {
   const size_t rb = K / 256 * kQ4_KBytes;
   const size_t ldw = N > 1 ? st.ldw : rb;
-  return aligned(W, 4) && ldw % 4 == 0 && (kNT - 1) * ldw + rb < ((size_t)1 << 32) &&
+  return aligned(W, 4) && ldw % 4 == 0 && (DefaultTiling::kNT - 1) * ldw + rb < ((size_t)1 << 32) &&
          N <= (size_t)INT32_MAX && K <= (size_t)INT32_MAX && M <= (size_t)INT32_MAX &&
-         ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT) <= (size_t)INT32_MAX;
+         ((N + 63) / 64) * ((M + 31) / 32) <= (size_t)INT32_MAX;
+}
+
+// The tiling of a dense launch.  CompileOptions.meta's bindings, when set
+// on the calling thread, choose it as the reference's loop extents do
+// (examples/kernels/mul_mat/q4_k_staged.py:20-24): MC activation rows per
+// tile (<= 32: 32-token tiles, else 64), NC weight rows per tile (<= 64:
+// 64-row tiles, else 128).  Unbound: 32-token tiles for M <= 32, 64-row
+// tiles when 128-row ones would leave more than half of the CUs idle.
+struct GemmShape {
+  int mt, nt;
+};
+GemmShape gemm_q4k_shape(size_t N, size_t M) {
+  const TileBindings& tb = tile_bindings();
+  const int mt = tb.mc > 0 ? (tb.mc <= 32 ? 32 : 64) : (M <= 32 ? 32 : 64);
+  int nt = 128;
+  if (tb.nc > 0)
+    nt = tb.nc <= 64 ? 64 : 128;
+  else if (((N + 127) / 128) * ((M + mt - 1) / mt) * 2 < (size_t)cu_count())
+    nt = 64;
+  return {mt, nt};
+}
+
+template <bool kIlv, class TL>
+void launch_gemm_q4k(const GemmArgs& a, size_t N, size_t M) {
+  // one workgroup per CU at most (the ring takes the CU's LDS); each walks
+  // its share of the tiles
+  const size_t tiles = ((N + TL::kNT - 1) / TL::kNT) * ((M + TL::kMT - 1) / TL::kMT);
+  const unsigned wgs = (unsigned)std::min(tiles, (size_t)cu_count());
+  q4k_mfma_gemm<false, kIlv, TL><<<dim3(wgs), TL::kThreads, 0, current_stream()>>>(a);
+  // the launch log names the tiling and the workgroup count
+  char name[48] = "q4k_mfma_gemm";
+  if (launch_log_enabled()) snprintf(name, sizeof(name), "q4k_mfma_gemm_%dx%d/%u", TL::kMT, TL::kNT, wgs);
+  check_launch(name);
 }
 
 template <bool kIlv = false>
@@ -528,12 +584,19 @@ void gemm_q4k(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K,
   a.M = (int)M;
   a.ldw = (uint32_t)(N > 1 ? st.ldw : rb);
   a.ldy = (long long)st.ldy;
-  // one workgroup per CU at most (the ring takes the CU's LDS); each walks
-  // its share of the tiles
-  const size_t tiles = ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT);
-  const size_t wgs = std::min(tiles, (size_t)cu_count());
-  q4k_mfma_gemm<false, kIlv><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(a);
-  check_launch("q4k_mfma_gemm");
+  if constexpr (kIlv) {
+    launch_gemm_q4k<true, DefaultTiling>(a, N, M);  // the persisted layout has no bindings
+  } else {
+    const GemmShape sh = gemm_q4k_shape(N, M);
+    if (sh.mt == 64 && sh.nt == 128)
+      launch_gemm_q4k<false, Tiling<64, 128>>(a, N, M);
+    else if (sh.mt == 32 && sh.nt == 128)
+      launch_gemm_q4k<false, Tiling<32, 128>>(a, N, M);
+    else if (sh.mt == 64)
+      launch_gemm_q4k<false, Tiling<64, 64>>(a, N, M);
+    else
+      launch_gemm_q4k<false, Tiling<32, 64>>(a, N, M);
+  }
 }
 
 bool args_ok(const uint8_t* W, const void* Xq, const float* Y, size_t N, size_t K, size_t M,
@@ -563,8 +626,8 @@ bool mul_mat_id_q4k_grouped_ok(const uint8_t* W, size_t xq_bytes, const float* Y
   return N > 0 && K > 0 && n_pairs > 0 && K % 256 == 0 && pr.n_as <= kMaxExperts &&
          xq_bytes < ((size_t)1 << 32) && aligned(Y, 4) && aligned(ws, 16) &&
          ws_bytes >= moe_group_bytes(n_pairs, pr.n_as) && pr.w_es % 4 == 0 &&
-         gemm_q4k_ok(W, N, K, kMT, st) && strides_ok(st, rb, 2, K, N, N, 1) &&
-         (size_t)moe_tile_bound(n_pairs, pr.n_as) * ((N + kNT - 1) / kNT) <= (size_t)INT32_MAX;
+         gemm_q4k_ok(W, N, K, DefaultTiling::kMT, st) && strides_ok(st, rb, 2, K, N, N, 1) &&
+         (size_t)moe_tile_bound(n_pairs, pr.n_as) * ((N + 127) / 128) <= (size_t)INT32_MAX;
 }
 
 void mul_mat_id_q4k_grouped(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K,
@@ -577,13 +640,13 @@ void mul_mat_id_q4k_grouped(const uint8_t* W, const uint8_t* Xq, float* Y, size_
   a.Y = Y;
   a.N = (int)N;
   a.K = (int)K;
-  a.M = kMT;
+  a.M = DefaultTiling::kMT;
   a.ldw = (uint32_t)(N > 1 ? st.ldw : rb);
   a.grp = group_tiles(g, pr);
-  const size_t tiles = (size_t)g.tmax * ((N + kNT - 1) / kNT);
+  const size_t tiles = (size_t)g.tmax * ((N + DefaultTiling::kNT - 1) / DefaultTiling::kNT);
   const size_t wgs = std::min(tiles, (size_t)cu_count());
-  q4k_mfma_gemm<true><<<dim3((unsigned)wgs), kThreads, 0, current_stream()>>>(a);
-  check_launch("q4k_mfma_gemm");
+  q4k_mfma_gemm<true><<<dim3((unsigned)wgs), DefaultTiling::kThreads, 0, current_stream()>>>(a);
+  check_launch("q4k_mfma_gemm_grouped");
 }
 
 // production_mul_mat_q4_k_persistent: W is the Q4K_I[16] interleave of an

@@ -17,11 +17,14 @@ void set_error(hipError_t e);
 void check_launch(const char* kernel = nullptr);
 // The calling thread's recorded error, left in place.
 hipError_t pending_error();
+// Whether the calling thread keeps a launch log (weft_hip_set_launch_log).
+bool launch_log_enabled();
 // The calling thread's source tile bindings (weft_hip_set_tile_binding;
 // 0 = unset): nc = weight rows per workgroup and mr = activation rows per
-// pass of the GEMV kernels.  The MFMA GEMMs' tiles are fixed.
+// pass of the GEMV kernels; the Q4_K MFMA GEMM takes nc as weight rows and
+// mc as activation rows per tile (64 / 128 and 32 / 64).
 struct TileBindings {
-  int nc = 0, mr = 0;
+  int nc = 0, mr = 0, mc = 0;
 };
 const TileBindings& tile_bindings();
 

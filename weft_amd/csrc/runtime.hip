@@ -79,6 +79,8 @@ void check_launch(const char* kernel) {
 
 hipError_t pending_error() { return t_error; }
 
+bool launch_log_enabled() { return t_log_on; }
+
 const TileBindings& tile_bindings() { return t_tiles; }
 
 int cu_count() { return facts().cus; }
@@ -108,6 +110,10 @@ int weft_hip_set_tile_binding(const char* name, size_t value) {
   }
   if (n == "MR") {
     weft::t_tiles.mr = (int)value;
+    return 1;
+  }
+  if (n == "MC") {
+    weft::t_tiles.mc = (int)value;
     return 1;
   }
   return 0;  // a binding without a gfx950 launch knob

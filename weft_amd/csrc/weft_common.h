@@ -400,6 +400,32 @@ __device__ __forceinline__ float ggml_scaled_term(float acc, float dx, float ws,
   return acc + t;
 }
 
+// IQ2 lookup tables (IQ2_XXS / IQ2_XS grid and sign rows, I8X8).  The
+// reference multiplies a grid byte by its sign byte as i8 x i8 -> i8
+// (examples/kernels/vec_dot/iq2_xxs_q8_k.py:39, functions/quantization.py:77:
+// equal element types are not promoted, python/weft/frontend/compiler.py:
+// 1276-1292), so the product wraps modulo 256.  The fast kernels take signs
+// as byte masks and negate with (g ^ 0xff) + 1, which is that product
+// exactly when every sign byte is +1 or -1 and no grid byte is 0 (a 0 byte
+// would carry into its neighbour); GGML's tables (magnitudes 8, 25, 43 and
+// +-1 signs) meet it.  Other tables take the byte product below.
+__device__ __forceinline__ bool iq2_grid_word_ok(uint32_t g) {
+  return ((g - 0x01010101u) & ~g & 0x80808080u) == 0u;  // no zero byte
+}
+__device__ __forceinline__ bool iq2_sign_word_ok(uint32_t s) {
+  const uint32_t m = ((s >> 7) & 0x01010101u) * 0xffu;
+  return s == (m | 0x01010101u);  // every byte 0x01 or 0xff
+}
+// four i8 x i8 -> i8 products, byte by byte, modulo 256
+__device__ __forceinline__ uint32_t mul8x4(uint32_t g, uint32_t s) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  const u16x2 lo = __builtin_bit_cast(u16x2, g & 0x00ff00ffu) * __builtin_bit_cast(u16x2, s & 0x00ff00ffu);
+  const u16x2 hi =
+      __builtin_bit_cast(u16x2, (g >> 8) & 0x00ff00ffu) * __builtin_bit_cast(u16x2, (s >> 8) & 0x00ff00ffu);
+  // bytes 0 and 2 of each product: lo.b0, hi.b0, lo.b2, hi.b2
+  return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, hi), __builtin_bit_cast(uint32_t, lo), 0x06020400u);
+}
+
 __device__ __forceinline__ int pack4_i8(const int q[4]) {
   return (int)((uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
                ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24));

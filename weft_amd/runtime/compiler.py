@@ -230,8 +230,18 @@ class CompiledKernel:
         if metadata["gfx_arch"] != target.gfx_arch:
             raise CompilationError("compiled artifact disagrees with its discovered target")
         # the artifact records the source bindings it was built for, sorted by
-        # name (lib/Target/ConvertWeftToRISCV.cpp:944-954)
-        self.metadata = _immutable(dict(metadata, bindings=dict(sorted(options.meta.items()))))
+        # name (lib/Target/ConvertWeftToRISCV.cpp:944-954), and which of them
+        # no gfx950 launch takes (the library answers per name: NC / MR tile
+        # the GEMVs, NC / MC the Q4_K GEMM; KC, NR and the rest are recorded
+        # only)
+        lib = _lib.load()
+        inert = []
+        for name in sorted(options.meta):
+            if not lib.weft_hip_set_tile_binding(name.encode(), 1):
+                inert.append(name)
+        lib.weft_hip_clear_tile_bindings()
+        self.metadata = _immutable(dict(metadata, bindings=dict(sorted(options.meta.items())),
+                                        bindings_without_launch_knob=tuple(inert)))
         self.target = target
         self.options = options
         self.definition = definition
@@ -240,7 +250,8 @@ class CompiledKernel:
         self._lib = _lib
         self._entry = getattr(_lib.load(), self.metadata["symbol"])
         # the source bindings, set on the library's calling thread for each
-        # call (weft_hip_set_tile_binding: NC / MR retile the GEMV launches)
+        # call (weft_hip_set_tile_binding: NC / MR retile the GEMV launches,
+        # NC / MC the Q4_K GEMM's tiles)
         self._tiles = tuple((name.encode(), value) for name, value in self.metadata["bindings"].items())
         self._lock = threading.RLock()
 
@@ -289,7 +300,8 @@ class _Registry:
         # every wl.auto extent needs one concrete binding; other names are
         # recorded (lib/Target/ConvertWeftToRISCV.cpp:730-745).  On gfx950
         # NC (weight rows per workgroup) and MR (activation rows per pass)
-        # retile the GEMV launches; the MFMA GEMMs keep their 64 x 128 tile.
+        # retile the GEMV launches, NC and MC the Q4_K GEMM's tile; the other
+        # MFMA GEMMs keep their 64 x 128 tile.
         missing = [name for name in definition.source_bindings if name not in options.meta]
         if missing:
             raise CompilationError(f"source auto parameter '{missing[0]}' requires one concrete --meta binding")
