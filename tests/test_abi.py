@@ -204,3 +204,33 @@ def test_host_registered_device_variables_exist_in_the_code_objects():
         assert hits, f"device variable {needle} missing from the code objects"
         for name in hits:
             assert found[name][4] == "GLOBAL", f"{name} is not a global symbol of the code object"
+
+
+@pytest.mark.skipif(not (READELF.exists() and OBJCOPY.exists()), reason="needs ROCm's llvm-readelf / llvm-objcopy")
+def test_no_kernel_spills_to_scratch():
+    """Every kernel keeps its state in registers and LDS: a kernel whose
+    accumulators went to scratch memory (a private segment) runs tens of
+    times slower.  The code objects' kernel metadata states each kernel's
+    private segment; the one tolerated is the grouped (MUL_MAT_ID) Q4_K
+    GEMM's 12-byte spill of two VGPRs."""
+    import re
+    import subprocess
+    import tempfile
+    objects = device_code_objects(_lib.LIB_PATH)
+    assert objects
+    sizes = {}
+    with tempfile.TemporaryDirectory() as tmp:
+        for i, co in enumerate(objects):
+            path = Path(tmp) / f"co{i}.o"
+            path.write_bytes(co)
+            res = subprocess.run([str(READELF), "--notes", "--wide", str(path)], check=True,
+                                 capture_output=True, text=True)
+            for block in re.split(r"\n\s+- \.", res.stdout):
+                name = re.search(r"\.name:\s+(\S+)", block)
+                seg = re.search(r"\.private_segment_fixed_size:\s+(\d+)", block)
+                if name and seg:
+                    sizes[name.group(1)] = int(seg.group(1))
+    assert len(sizes) > 50
+    spilled = {k: v for k, v in sizes.items() if v > 0}
+    allowed = {k: v for k, v in spilled.items() if "q4k_mfma_gemm" in k and "ILb1E" in k and v <= 16}
+    assert spilled == allowed, spilled

@@ -128,9 +128,11 @@ __global__ void __launch_bounds__(kThreads) iq2_gemv_m1_kernel(Iq2Args a) {
   }
   // the tables take the mask path when every workgroup thread's words meet
   // its precondition (the same answer in every workgroup)
-  const bool bad = (ti < kGridBytes / 4 && !iq2_grid_word_ok(tg)) || (ti < 256 && !iq2_sign_word_ok(ts));
+  __shared__ uint32_t tflag[kWaves];
+  iq2_flag_wave(tflag, (ti < kGridBytes / 4 && !iq2_grid_word_ok(tg)) || (ti < 256 && !iq2_sign_word_ok(ts)));
   stager.finish(a.X, (size_t)K, blockIdx.x == 0 ? a.xq_out : nullptr, K, 0, 1, act);
-  const bool canon = __builtin_amdgcn_readfirstlane(__syncthreads_or(bad)) == 0;  // wave-uniform
+  __syncthreads();
+  const bool canon = iq2_flags_clear(tflag, kWaves);
 
   // this lane's 64 activation values and its superblock's scale
   int4 xa[4];
@@ -145,7 +147,7 @@ __global__ void __launch_bounds__(kThreads) iq2_gemv_m1_kernel(Iq2Args a) {
 
   // kGen: any int8 tables, each weight byte the i8 product grid * sign;
   // otherwise the sign masks' negate
-  auto compute = [&](const RowBuf& buf, int k, auto gen) {
+  auto compute = [&](const RowBuf& buf, int k, auto gen) __attribute__((always_inline)) {
     constexpr bool kGen = decltype(gen)::value;
     const uint2* sgn = reinterpret_cast<const uint2*>(kGen ? traw : tsign);
     uint32_t q[4];
@@ -188,7 +190,7 @@ __global__ void __launch_bounds__(kThreads) iq2_gemv_m1_kernel(Iq2Args a) {
     if (lane == 0) a.Y[row_first + k * kWaves] = 0.125f * tot;
   };
 
-  auto rows = [&](auto gen) {
+  auto rows = [&](auto gen) __attribute__((always_inline)) {
     int k = 0;
     for (; k + 2 < nrows; k += 2) {
       issue(bufB, k + 1);

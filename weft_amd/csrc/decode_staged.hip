@@ -239,6 +239,7 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
 
   // IQ2: the grid, then the sign rows as byte masks, then as given; `bad`
   // marks a table word outside the masks' precondition (weft_common.h)
+  __shared__ uint32_t tflag[kWaves];
   bool bad = false;
   if constexpr (F == Fmt::IQ2_XXS || F == Fmt::IQ2_XS) {
     constexpr int kGridWords = F == Fmt::IQ2_XS ? 1024 : 512;
@@ -253,6 +254,7 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
       reinterpret_cast<uint32_t*>(tables + 4 * kGridWords + 1024)[i] = sg;
       bad |= !iq2_sign_word_ok(sg);
     }
+    iq2_flag_wave(tflag, bad);
   } else if constexpr (F == Fmt::MXFP4 || F == Fmt::NVFP4) {
     for (int i = threadIdx.x; i < 256; i += blockDim.x)
       reinterpret_cast<float*>(tables)[i] = reinterpret_cast<const float*>(a.tab1)[i];
@@ -300,8 +302,10 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
     else
       stage_q80_load(a.xq_in, K, a.m0, a.mb, act);
   }
+  __syncthreads();
   // IQ2 tables within the masks' precondition (the same in every workgroup)
-  const bool canon = __builtin_amdgcn_readfirstlane(__syncthreads_or(bad)) == 0;  // wave-uniform
+  bool canon = true;
+  if constexpr (F == Fmt::IQ2_XXS || F == Fmt::IQ2_XS) canon = iq2_flags_clear(tflag, nwaves);
 
   uint32_t c0 = 0, c1 = 0, c2 = 0, c3 = 0;
   if constexpr (F == Fmt::MXFP4 || F == Fmt::NVFP4) {

@@ -106,14 +106,20 @@ __device__ __forceinline__ void pin(int& v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ uint32_t apply_signs(uint32_t g, uint32_t m) {
   return (g ^ m) + (m & 0x01010101u);
 }
-// four weight bytes: the masks' negate, or (tables outside its
-// precondition) the i8 products of grid and sign bytes
-template <class Gen>
-__device__ __forceinline__ uint32_t sign8(uint32_t g, uint32_t z, Gen) {
-  if constexpr (Gen::value)
-    return mul8x4(g, z);
-  else
-    return apply_signs(g, z);
+// one operand's sixteen weight bytes (grid rows g0, g1 against sign rows
+// z0, z1): the masks' negate, or, for tables outside its precondition, the
+// i8 products of grid and sign bytes.  `canon` is wave-uniform; the branch
+// keeps the rare path off the common one.
+__device__ __forceinline__ v4i weight_bytes(uint2 g0, uint2 g1, uint2 z0, uint2 z1, bool canon) {
+  v4i bv;
+  if (__builtin_expect(canon, 1)) {
+    bv = (v4i){(int)apply_signs(g0.x, z0.x), (int)apply_signs(g0.y, z0.y), (int)apply_signs(g1.x, z1.x),
+               (int)apply_signs(g1.y, z1.y)};
+  } else {
+    bv = (v4i){(int)mul8x4(g0.x, z0.x), (int)mul8x4(g0.y, z0.y), (int)mul8x4(g1.x, z1.x),
+               (int)mul8x4(g1.y, z1.y)};
+  }
+  return bv;
 }
 
 // kXs (IQ2_XS, ggml-cpu/quants.c:897-946): u16 entries (grid row bits 0-8,
@@ -134,6 +140,7 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
   __shared__ __align__(16) uint8_t tgrid[TT::kGrid * 8];
   __shared__ __align__(16) uint8_t tsign[128 * 8];  // sign rows as byte masks
   __shared__ __align__(16) uint8_t traw[128 * 8];   // sign rows as given
+  __shared__ uint32_t tflag[kThreads / 64];          // per wave: a table byte outside the masks' precondition
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -217,13 +224,15 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
   const int sw = col & 15;
   const int sb0 = par * TT::kRec;  // this parity's record within the pair: 0 or 66 / 74
 
-  // kGen: any int8 tables, each weight byte the i8 product grid * sign;
-  // otherwise the sign masks' negate
-  auto step = [&](int pair, const uint8_t* cur, uint8_t* nxt, auto gen) {
-    constexpr bool kGen = decltype(gen)::value;
-    const uint8_t* tsg = kGen ? traw : tsign;
+  auto step = [&](int pair, const uint8_t* cur, uint8_t* nxt) {
     __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of this pair have landed
     __syncthreads();                // everyone's; the previous pair is consumed
+    // every wave has flagged its table words (before the first of these
+    // barriers): canon = the sign masks' negate; otherwise (tables outside
+    // its precondition) the i8 products of grid and sign bytes, on a scalar
+    // branch around the operand's four words only
+    const bool canon = iq2_flags_clear(tflag, kThreads / 64);
+    const uint8_t* tsg = canon ? tsign : traw;
     const bool refill = pair + 1 < npair;
     if (refill) {
       issue(pair + 1, nxt);
@@ -257,8 +266,7 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
         const uint2 g1 = *reinterpret_cast<const uint2*>(tgrid + 8 * (e1 & 511u));
         const uint2 z0 = *reinterpret_cast<const uint2*>(tsg + 8 * (e0 >> 9));
         const uint2 z1 = *reinterpret_cast<const uint2*>(tsg + 8 * (e1 >> 9));
-        const v4i bv = {(int)sign8(g0.x, z0.x, gen), (int)sign8(g0.y, z0.y, gen),
-                        (int)sign8(g1.x, z1.x, gen), (int)sign8(g1.y, z1.y, gen)};
+        const v4i bv = weight_bytes(g0, g1, z0, z1, canon);
         const v4i bz = {};
         const uint32_t sb = ((g < 4 ? scl0 : scl1) >> (8 * (g & 3))) & 0xffu;
         const int ls_lo = 2 * (int)(sb & 15u) + 1, ls_hi = 2 * (int)(sb >> 4) + 1;
@@ -289,8 +297,7 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
       const uint2 g1 = *reinterpret_cast<const uint2*>(tgrid + 8 * i1);
       const uint2 z0 = *reinterpret_cast<const uint2*>(tsg + 8 * s0);
       const uint2 z1 = *reinterpret_cast<const uint2*>(tsg + 8 * s1);
-      const v4i bv = {(int)sign8(g0.x, z0.x, gen), (int)sign8(g0.y, z0.y, gen),
-                      (int)sign8(g1.x, z1.x, gen), (int)sign8(g1.y, z1.y, gen)};
+      const v4i bv = weight_bytes(g0, g1, z0, z1, canon);
       const int ls = 2 * (int)(meta >> 28) + 1;
       const int chunk = (2 * g + kg) ^ sw;
 #pragma unroll
@@ -342,22 +349,15 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
     traw[i] = (uint8_t)sb;
     bad |= sb != 1 && sb != -1;
   }
-  // the same in every workgroup; wave-uniform, so the branch below is scalar
-  const bool canon = __builtin_amdgcn_readfirstlane(__syncthreads_or(bad)) == 0;
+  iq2_flag_wave(tflag, bad);  // read after the first pair's barrier (the same in every workgroup)
   if (wcol == 0) {
     load_dx(0);
     dxq[0][par][lane] = bf16_split3(dxr);
   }
-  auto run = [&](auto gen) {
-    for (int pair = 0; pair < npair; pair += 2) {
-      step(pair, ring0, ring1, gen);
-      if (pair + 1 < npair) step(pair + 1, ring1, ring0, gen);
-    }
-  };
-  if (canon)
-    run(std::false_type{});
-  else
-    run(std::true_type{});
+  for (int pair = 0; pair < npair; pair += 2) {
+    step(pair, ring0, ring1);
+    if (pair + 1 < npair) step(pair + 1, ring1, ring0);
+  }
 
   // both parities' partial sums -> two LDS planes (reusing the ring) -> Y
   __syncthreads();

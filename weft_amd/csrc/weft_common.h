@@ -416,6 +416,19 @@ __device__ __forceinline__ bool iq2_sign_word_ok(uint32_t s) {
   const uint32_t m = ((s >> 7) & 0x01010101u) * 0xffu;
   return s == (m | 0x01010101u);  // every byte 0x01 or 0xff
 }
+// Workgroup-wide "any bad table word" without a reducing barrier: before a
+// barrier every wave stores whether any of its lanes saw one (flags: one
+// word per wave of the workgroup, in LDS); after it, every lane ORs them.
+__device__ __forceinline__ void iq2_flag_wave(uint32_t* flags, bool bad) {
+  const bool any = __builtin_amdgcn_ballot_w64(bad) != 0;
+  if ((threadIdx.x & 63) == 0) flags[threadIdx.x >> 6] = any ? 1u : 0u;
+}
+__device__ __forceinline__ bool iq2_flags_clear(const uint32_t* flags, int nwaves) {
+  uint32_t any = 0;
+  for (int w = 0; w < nwaves; ++w) any |= flags[w];
+  return __builtin_amdgcn_readfirstlane(any) == 0;  // wave-uniform: scalar branches
+}
+
 // four i8 x i8 -> i8 products, byte by byte, modulo 256
 __device__ __forceinline__ uint32_t mul8x4(uint32_t g, uint32_t s) {
   typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
