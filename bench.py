@@ -376,7 +376,24 @@ class Bench:
             del bufs
             torch.cuda.empty_cache()
         out["stream_read"] = reads
+        out["mfma_valu_ns_per_mfma"] = self.mfma_probe()
         return out
+
+    def mfma_probe(self):
+        """ns per v_mfma_i32_32x32x32_i8 per SIMD with V independent VALU
+        instructions issued after each MFMA, at 1 and 2 waves per SIMD
+        (library probe weft_hip_probe_mfma): how much VALU work hides beside
+        the matrix pipe.  The prefill GEMMs issue 9-38 VALU per MFMA."""
+        torch = self.torch
+        sink = torch.empty(1 << 18, dtype=torch.int32, device=self.dev)
+        iters = 2000
+        res = {}
+        for waves in (1, 2):
+            for v in (0, 4, 8, 12, 16):
+                sec = self.time_calls(lambda i: self.lib.weft_hip_probe_mfma(v, waves, iters, sink.data_ptr()),
+                                      3, 2, windows=3)[0]
+                res[f"w{waves}_v{v}"] = round(sec * 1e9 / (2 * iters * waves), 2)
+        return res
 
     def vendor_int8_gemm(self, m, n, k):
         """hipBLASLt's plain int8 GEMM (torch._int_mm) of the same shape:
@@ -586,7 +603,7 @@ def cpu_baseline(n, k, budget_s):
 
 def brief(case: dict) -> dict:
     """The figures of an adjacent-format case kept in the output line."""
-    keep = ("us", "us_min", "us_max", "GBs", "TOPS", "frac_hbm_peak", "frac_int8_peak", "graph_us")
+    keep = ("us", "GBs", "TOPS", "frac_hbm_peak", "frac_int8_peak", "vs_read_floor")
     return {k: case[k] for k in keep if k in case}
 
 
@@ -660,7 +677,11 @@ def main():
                    "timing": f"median of {WINDOWS} windows of {steps} back-to-back calls (HIP events)"},
         "roofline": roofline,
         "cpu_baseline": cpu,
-        "floors": floors,
+        "floors": None if floors is None else {
+            "empty_launch_us": floors["empty_launch_us"],
+            "stream_read_headline": floors["stream_read"][str(head["algorithmic_bytes"])],
+            "stream_read_us": {k: v["us"] for k, v in floors["stream_read"].items()},
+            "mfma_valu_ns_per_mfma": floors["mfma_valu_ns_per_mfma"]},
         "adjacent": {name: brief(v) for name, v in results.items() if name not in labels},
         "configs": {labels[name]: results[name] for name in CASES if name in labels and name in results},
     }

@@ -93,6 +93,13 @@ void weft_hip_probe_read(const void *src, size_t bytes, uint32_t *sink, int grid
  * grid * threads / 64 words.  weft_hip_probe_read is (512, 4, 0). */
 void weft_hip_probe_read_shape(const void *src, size_t bytes, uint32_t *sink, int grid, int threads,
                                int unroll, int flags);
+/* Matrix-pipe probe: one workgroup per CU with `waves_per_simd` (1..4)
+ * waves per SIMD, each running `iters` iterations of two
+ * v_mfma_i32_32x32x32_i8 with `valu_per_mfma` (0, 4, 8, 12 or 16)
+ * independent integer VALU instructions after each; sink holds
+ * cu_count * 256 * waves_per_simd words.  Time per MFMA = elapsed /
+ * (2 * iters * waves_per_simd). */
+void weft_hip_probe_mfma(int valu_per_mfma, int waves_per_simd, int iters, uint32_t *sink);
 
 /* ------------------------------------------------------ row dequantize */
 /* examples/kernels/dequantize/q4_0.py:9-13; repro row_dequantize_runtime.cpp:177 */

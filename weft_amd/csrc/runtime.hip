@@ -225,6 +225,53 @@ __global__ void __launch_bounds__(1024) probe_read_kernel(const v4u* __restrict_
   if ((threadIdx.x & 63) == 0) sink[((size_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6] = acc;
 }
 
+// One i8 32x32x32 MFMA chain per wave (two accumulators, alternating) with
+// V independent integer VALU instructions (16-bit multiplies, masks,
+// shift-adds: the operand unpack's kinds) issued between consecutive MFMAs:
+// the per-MFMA time as V grows shows how much VALU work hides beside the
+// matrix pipe.  One workgroup per CU of `waves` waves per SIMD.
+typedef int probe_v4i __attribute__((ext_vector_type(4)));
+typedef int probe_v16i __attribute__((ext_vector_type(16)));
+typedef unsigned short probe_u16x2 __attribute__((ext_vector_type(2)));
+template <int V>
+__global__ void __launch_bounds__(1024) probe_mfma_kernel(int iters, uint32_t* __restrict__ sink) {
+  const int lane = threadIdx.x & 63;
+  const probe_v4i a = {lane, lane * 5, lane ^ 3, 7};
+  const probe_v4i b = {lane * 3, lane ^ 5, lane + 7, 1};
+  probe_v16i c0 = {}, c1 = {};
+  uint32_t u[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) u[i] = (uint32_t)(lane * 77 + i);
+  for (int it = 0; it < iters; ++it) {
+    c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c0, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const int j = i % 16;
+      if (i % 3 == 0)
+        u[j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(probe_u16x2, u[j]) * (probe_u16x2){3, 5});
+      else if (i % 3 == 1)
+        u[j] = (u[j] & 0x0f0f0f0fu) ^ (uint32_t)it;
+      else
+        u[j] = (u[j] << 3) + u[(j + 1) % 16];
+    }
+    c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(b, a, c1, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const int j = (i + 8) % 16;
+      if (i % 3 == 0)
+        u[j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(probe_u16x2, u[j]) * (probe_u16x2){3, 5});
+      else if (i % 3 == 1)
+        u[j] = (u[j] & 0x0f0f0f0fu) ^ (uint32_t)it;
+      else
+        u[j] = (u[j] << 3) + u[(j + 1) % 16];
+    }
+  }
+  uint32_t s = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s += (uint32_t)c0[i] + (uint32_t)c1[i] + u[i];
+  sink[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
 template <int U>
 bool launch_probe(bool nt, bool blocked, int grid, int threads, const v4u* src, size_t n16, uint32_t* sink) {
   hipStream_t s = current_stream();
@@ -268,6 +315,24 @@ void weft_hip_probe_read_shape(const void* src, size_t bytes, uint32_t* sink, in
     default: weft::set_error(hipErrorInvalidValue); return;
   }
   weft::check_launch("probe_read_kernel");
+}
+
+void weft_hip_probe_mfma(int valu_per_mfma, int waves_per_simd, int iters, uint32_t* sink) {
+  if (sink == nullptr || iters <= 0 || waves_per_simd < 1 || waves_per_simd > 4) {
+    weft::set_error(hipErrorInvalidValue);
+    return;
+  }
+  const int grid = weft::cu_count(), threads = 256 * waves_per_simd;
+  hipStream_t s = weft::current_stream();
+  switch (valu_per_mfma) {
+    case 0: weft::probe_mfma_kernel<0><<<grid, threads, 0, s>>>(iters, sink); break;
+    case 4: weft::probe_mfma_kernel<4><<<grid, threads, 0, s>>>(iters, sink); break;
+    case 8: weft::probe_mfma_kernel<8><<<grid, threads, 0, s>>>(iters, sink); break;
+    case 12: weft::probe_mfma_kernel<12><<<grid, threads, 0, s>>>(iters, sink); break;
+    case 16: weft::probe_mfma_kernel<16><<<grid, threads, 0, s>>>(iters, sink); break;
+    default: weft::set_error(hipErrorInvalidValue); return;
+  }
+  weft::check_launch("probe_mfma_kernel");
 }
 
 void weft_hip_probe_read(const void* src, size_t bytes, uint32_t* sink, int grid) {
