@@ -149,9 +149,18 @@ template <WFmt F>
 constexpr bool has_table() {
   return F == WFmt::MXFP4 || F == WFmt::NVFP4;
 }
+// LDS bytes per weight row and stage: the row's 8 records (2 kRec dwords).
+// Q4_1's 40-dword rows put the 32 rows a wave reads at one record offset
+// into 8 of the 64 banks (4-way conflicts): its rows get one pad dword (an
+// odd stride, 32 banks).  Padding the 36- and 34-dword rows (2-way, 1-way)
+// measured slower: two more wave-wide loads per stage.
+template <WFmt F>
+constexpr int w_lds_row() {
+  return 4 * (2 * WTraits<F>::kRec + ((2 * WTraits<F>::kRec) % 8 == 0 ? 1 : 0));
+}
 template <WFmt F>
 constexpr int q80_lds_bytes() {
-  return 4 * (kAQ + kNT * 8 * WTraits<F>::kRec) + 2 * 2 * 8 * kMT * 4 +
+  return 4 * (kAQ + kNT * w_lds_row<F>()) + 2 * 2 * 8 * kMT * 4 +
          (F == WFmt::Q4_1 ? 2 * 2 * 8 * kMT * 2 : 0) + (has_table<F>() ? 256 * 4 : 0);
 }
 
@@ -159,12 +168,14 @@ template <WFmt F, bool kGroup>
 __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
   using T = WTraits<F>;
   constexpr int kRB = 8 * T::kRec;           // raw weight bytes per row and stage
-  constexpr int kWT = kNT * kRB;             // 18432 (Q4_0) / 17408 (MXFP4)
+  constexpr int kRL = w_lds_row<F>();        // LDS bytes per weight row (Q4_1: kRB + 4)
+  constexpr int kWT = kNT * kRL;             // 18432 (Q4_0) / 17408 (MXFP4) / 20992 (Q4_1)
   constexpr int kStage = kAQ + kWT;
   constexpr int kWD = kRB / 4;               // dwords per weight row and stage
-  constexpr int kWSlots = kNT * kWD / 64;    // 72 / 68 wave-wide dword loads
-  constexpr int kWPerWave = kWSlots / 4;     // 18 / 17
-  static_assert(kNT * kWD % 256 == 0, "weight slots split evenly over four waves");
+  constexpr int kWDp = kRL / 4;              // the same, with the pad
+  constexpr int kWSlots = kNT * kWDp / 64;   // 72 / 68 / 82 wave-wide dword loads
+  constexpr int kWPerWave = (kWSlots + 3) / 4;
+  static_assert(kNT * kWDp % 64 == 0 && (kRL == kRB || kRL == kRB + 4), "whole wave-wide weight loads");
   static_assert(kTilePlaneBytes <= 2 * kStage, "an output plane fits one ring half");
 
   // two ring slots; a slot being filled by direct loads never aliases the
@@ -252,9 +263,12 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
 #pragma unroll
     for (int i = 0; i < kWPerWave; ++i) {
       const int k = wcol + 4 * i;
-      const int q = 64 * k + lane, row = q / kWD, part = q - kWD * row;
-      const uint8_t* g = W + (size_t)min(n0 + row, a.N - 1) * ws_row + (size_t)st * kRB + 4 * part;
-      lds_dma4(g, stage + kAQ + 256 * k);
+      if (kWSlots % 4 == 0 || k < kWSlots) {  // wave-uniform
+        // the pad dword repeats the row's last one
+        const int q = 64 * k + lane, row = q / kWDp, part = min(q - kWDp * row, kWD - 1);
+        const uint8_t* g = W + (size_t)min(n0 + row, a.N - 1) * ws_row + (size_t)st * kRB + 4 * part;
+        lds_dma4(g, stage + kAQ + 256 * k);
+      }
     }
   };
   uint4 dxraw = make_uint4(0, 0, 0, 0), sraw = make_uint4(0, 0, 0, 0);
@@ -294,7 +308,7 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
     if (2 * pair + par < nst) {
       const uint8_t* stage = cur + par * kStage;
       const uint8_t* AQ = stage;
-      const uint8_t* wrow = stage + kAQ + (32 * wcol + col) * kRB;
+      const uint8_t* wrow = stage + kAQ + (32 * wcol + col) * kRL;
       const float* dxs = &adt[pair & 1][par][0];
       const uint16_t* sxs = &ast[pair & 1][par][0];
 #pragma unroll
