@@ -583,26 +583,34 @@ __global__ void __launch_bounds__(256) q80_planar_kernel(const float* __restrict
 // GGML element k/2 + 16 (k%2), the order the pre-pass writes.
 //
 // Tiling: 64 tokens x 128 weight rows per workgroup, 8 waves = 2 column
-// halves x 4 K phases.  A stage is 8 blocks (256 K values); a wave takes
-// blocks 2p and 2p + 1 of each stage and computes all four 32x32 tiles of its
+// halves x 4 K phases.  The K loop walks pairs of stages (16 blocks, 512 K
+// values); phase p takes the pair's blocks 4p .. 4p + 3 (phases 0-1 the
+// first stage, 2-3 the second) and computes all four 32x32 tiles of its
 // 64 x 64 quarter, so each weight operand and each split activation operand
 // feeds two MFMAs.  The four phases' partial sums are added through LDS at
 // the end, in phase order.  Every global byte arrives by direct
-// global->LDS loads into a ring of four stages, a pair of stages ahead:
-// activation rows with their 16 chunks of 16 bytes XOR-swizzled by token
-// (conflict-free operand reads), the token scales block-major, and the raw
-// weight rows at an odd dword stride (140 bytes).  One barrier per two stages.
+// global->LDS loads into two pair slots, one pair ahead: activation rows
+// with their 16 chunks of 16 bytes XOR-swizzled by token (conflict-free
+// operand reads), the token scales block-major, and each weight row's 272
+// bytes of the pair (16 records) as 17 chunks of 16 bytes: 34 wave-wide
+// 16-byte loads a pair (a row's pair is 16-byte aligned when K is a
+// multiple of 512 and the rows are; otherwise, and for a last single
+// stage, 136 dword loads fill the same layout).  A phase's four records
+// start at a dword boundary of the row (68 p bytes), so its operand bytes
+// sit at fixed offsets from there.  One barrier per pair.
 namespace mx {
 
 constexpr int kMT = 64;
 constexpr int kNT = 128;
-constexpr int kRowW = 140;                 // LDS bytes per weight row and stage: 136 + pad
-constexpr int kSD = kMT * 256;             // 16384: token scales, fp16 [block pair][token][2]
-constexpr int kSW = kSD + kMT * 16;        // 17408: weight rows
-constexpr int kSlot = kSW + kNT * kRowW;   // 35328
-constexpr int kLds = 4 * kSlot;            // 141312
-constexpr int kWLoads = kNT * kRowW / 256; // 70 wave-wide dword loads of weights
-static_assert(kNT * kRowW % 256 == 0, "whole wave-wide weight loads");
+constexpr int kAct = kMT * 256;            // 16384: one stage's activation tile
+constexpr int kRowW = 272;                 // LDS bytes per weight row and pair
+constexpr int kSD = 2 * kAct;              // token scales, fp16 [stage][block pair][token][2]
+constexpr int kSW = kSD + 2 * kMT * 16;    // 34816: weight rows
+constexpr int kSlot = kSW + kNT * kRowW;   // 69632
+constexpr int kLds = 2 * kSlot;            // 139264
+constexpr int kW16Loads = kNT * kRowW / 1024;  // 34 wave-wide 16-byte loads of weights
+constexpr int kW4Loads = kNT * kRowW / 256;    // 136 wave-wide dword loads
+static_assert(kNT * kRowW % 1024 == 0 && kW4Loads % 8 == 0, "whole wave-wide weight loads");
 
 // Exponents whose block terms the scaled MFMA reproduces.  GGML forms
 // d = fp16(dx) * 2^(e-128), then sumf + d * I, each step rounded
@@ -696,42 +704,54 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
       return (uint32_t)r;
   };
 
-  // Load plan per stage: 16 activation loads (1 KB = 4 tokens each), 4 dword
-  // loads of the token scales (block pair kp of 64 tokens each), 70 weight
-  // dword loads.  Wave w issues loads g = w + 8i: g < 16 activation,
-  // 16 <= g < 20 scales, then weights g - 20.  Rows past M / N repeat the
-  // last row.
+  // Load plan per pair: 2 x 16 activation loads (1 KB = 4 tokens each), 8
+  // dword loads of the token scales (stage w / 4, block pair w % 4 of 64
+  // tokens: wave w), then the weight rows.  Rows past M / N repeat the last
+  // row.
   auto act_off = [&](int c) {
     const int q = 64 * c + lane, t = q >> 4, s = q & 15;
     return act_row(min(t, mlast)) * xs + 16 * (uint32_t)(s ^ (t & 15));
   };
-  auto w_off = [&](int k) {
-    const int q = 64 * k + lane, row = q / (kRowW / 4), part = q - (kRowW / 4) * row;
-    return (uint32_t)min(row, nlast) * ws_row + 4 * (uint32_t)min(part, 33);
-  };
   const uint32_t va0 = act_off(wave), va1 = act_off(wave + 8);
-  const uint32_t v2 = wave < 4 ? act_row(min(lane, mlast)) * xs + (uint32_t)a.K + 4 * wave : w_off(wave - 4);
-  uint32_t vw[9];
+  const uint32_t vsc = act_row(min(lane, mlast)) * xs + (uint32_t)a.K + 4 * (uint32_t)(wave & 3);
+  // 16-byte weight chunks: load k = wave + 8 i (< 34) covers chunks 64 k + lane
+  // (row q / 17, chunk q % 17)
+  const bool w16 = (((uintptr_t)wbase | ws_row) & 15) == 0;
+  uint32_t vw[5];
 #pragma unroll
-  for (int i = 0; i < 9; ++i) vw[i] = w_off(min(wave + 8 * i + 4, kWLoads - 1));
+  for (int i = 0; i < 5; ++i) {
+    const int q = 64 * min(wave + 8 * i, kW16Loads - 1) + lane, row = q / 17;
+    vw[i] = (uint32_t)min(row, nlast) * ws_row + 16 * (uint32_t)(q - 17 * row);
+  }
 
   // LDS byte addresses as integers from one wave-uniform base: no per-use
   // generic-to-LDS pointer casts (their null checks on VALU do not compile)
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
-  auto issue = [&](int st) {
-    const uint32_t slot = lds0 + (uint32_t)(st & 3) * kSlot;
-    const uint8_t* xb = xbase + 256 * (size_t)st;
-    const uint8_t* wb = wbase + 136 * (size_t)st;
-    dma16_s(xb, va0, slot + 1024 * wave);
-    dma16_s(xb, va1, slot + 1024 * (wave + 8));
-    if (wave < 4)
-      lds_dma4_s(xbase + 16 * (size_t)st, v2, slot + kSD + 256 * wave);
-    else
-      lds_dma4_s(wb, v2, slot + kSW + 256 * (wave - 4));
+  auto issue = [&](int p) {
+    const uint32_t slot = lds0 + (uint32_t)(p & 1) * kSlot;
+    const bool both = 2 * p + 1 < nst;  // the pair's second stage exists
 #pragma unroll
-    for (int i = 0; i < 9; ++i)
-      if (i < 8 || wave < 2)
-        lds_dma4_s(wb, vw[i], slot + kSW + 256 * (wave + 8 * i + 4));
+    for (int s = 0; s < 2; ++s)
+      if (s == 0 || both) {
+        const uint8_t* xb = xbase + 256 * (size_t)(2 * p + s);
+        dma16_s(xb, va0, slot + kAct * s + 1024 * wave);
+        dma16_s(xb, va1, slot + kAct * s + 1024 * (wave + 8));
+      }
+    if (wave < 4 || both) lds_dma4_s(xbase + 16 * (size_t)(2 * p + (wave >> 2)), vsc, slot + kSD + 256 * wave);
+    const uint8_t* wb = wbase + kRowW * (size_t)p;
+    if (w16 && both) {
+#pragma unroll
+      for (int i = 0; i < 5; ++i)
+        if (wave + 8 * i < kW16Loads) dma16_s(wb, vw[i], slot + kSW + 1024 * (wave + 8 * i));
+    } else {
+      // dword loads into the same layout; a single last stage has 34 dwords a row
+      const int dmax = both ? kRowW / 4 - 1 : kRowW / 8 - 1;
+      for (int i = 0; i < kW4Loads / 8; ++i) {
+        const int q = 64 * (wave + 8 * i) + lane, row = q / (kRowW / 4);
+        const int d = min(q - (kRowW / 4) * row, dmax);
+        lds_dma4_s(wb, (uint32_t)min(row, nlast) * ws_row + 4 * (uint32_t)d, slot + kSW + 256 * (wave + 8 * i));
+      }
+    }
   };
 
   v16f y[4];  // tile 2 * token half + column tile
@@ -739,56 +759,65 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
   for (int q = 0; q < 4; ++q) y[q] = v16f{};
   const v16f fzero = {};
   const int x_scale = h ? 127 + 9 : 127 + 13;  // B block 0: hi plane (x16), block 1: lo plane
+  const int sp = ph >> 1;                      // the phase's stage within a pair
 
-  // blocks 2 ph and 2 ph + 1 of stage st.  kExact false: every tile takes
-  // its exponent e as the hardware block scale, and `out` collects whether
-  // any e lies outside [kSafeLo, kSafeHi] (the results are then discarded).
+  // The phase's four blocks of pair p.  kExact false: every tile takes its
+  // exponent e as the hardware block scale, and `out` collects whether any
+  // e lies outside [kSafeLo, kSafeHi] (the results are then discarded).
   // kExact true: a column tile whose 32 rows all have exponents in range
   // does the same; otherwise (wave-uniform) its MFMA runs at unit scale and
   // the block is combined in GGML's order.
-  auto stage = [&](int st, auto exact_tag, bool& out) {
+  auto phase_blocks = [&](int p, auto exact_tag, bool& out) {
     constexpr bool kExact = decltype(exact_tag)::value;
-    const uint8_t* slot = lds + (st & 3) * kSlot;
-    const uint32_t slot_lds = lds0 + (uint32_t)(st & 3) * kSlot;
+    const uint8_t* slot = lds + (p & 1) * kSlot;
+    const uint32_t slot_lds = lds0 + (uint32_t)(p & 1) * kSlot;
+    // the 17 dwords holding records 4 ph .. 4 ph + 3 of rows 64 cp + 32 ct + col
+    uint32_t wd[2][17];
 #pragma unroll
-    for (int bi = 0; bi < 2; ++bi) {
-      const int b = 2 * ph + bi;
-      // weight records b of rows 64 cp + 32 ct + col: e at byte 17b, then
-      // 16 nibble bytes, read as aligned dwords and shifted into place
-      const int off = kMxfp4Bytes * b;
-      const int b4 = (off + 1) & ~3, sh = (off + 1) & 3;
+    for (int ct = 0; ct < 2; ++ct) {
+      const uint8_t* wr = slot + kSW + kRowW * (64 * cp + 32 * ct + col) + 68 * ph;
+#pragma unroll
+      for (int i = 0; i < 17; ++i) wd[ct][i] = ld32(wr + 4 * i);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int bs = 4 * (ph & 1) + j;  // block within stage sp
+      // record j: e at byte 17 j, then 16 nibble bytes
+      constexpr int kE[4] = {0, 17, 34, 51};
+      const int n0b = kE[j] + 1, dw0 = n0b >> 2, sh = n0b & 3;
       v8i wv[2];
       int wsc[2];
       bool exact[2] = {false, false};
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) {
-        const uint8_t* wr = slot + kSW + kRowW * (64 * cp + 32 * ct + col);
-        const uint32_t w0 = ld32(wr + b4), w1 = ld32(wr + b4 + 4), w2 = ld32(wr + b4 + 8),
-                       w3 = ld32(wr + b4 + 12), w4 = ld32(wr + b4 + 16);
-        const uint32_t e = __builtin_amdgcn_ubfe(ld32(wr + (off & ~3)), 8 * (off & 3), 8);
+        const uint32_t e = (wd[ct][kE[j] >> 2] >> (8 * (kE[j] & 3))) & 0xffu;
         const bool unsafe = e - kSafeLo > kSafeHi - kSafeLo;  // unsigned
         if constexpr (kExact)
           exact[ct] = __builtin_amdgcn_ballot_w64(unsafe) != 0;
         else
           out |= unsafe;
         wsc[ct] = exact[ct] ? 127 : (int)e;
-        wv[ct] = v8i{(int)__builtin_amdgcn_alignbyte(w1, w0, sh), (int)__builtin_amdgcn_alignbyte(w2, w1, sh),
-                     (int)__builtin_amdgcn_alignbyte(w3, w2, sh), (int)__builtin_amdgcn_alignbyte(w4, w3, sh),
-                     0, 0, 0, 0};
+        const uint32_t* w = &wd[ct][dw0];
+        wv[ct] = sh ? v8i{(int)__builtin_amdgcn_alignbyte(w[1], w[0], sh), (int)__builtin_amdgcn_alignbyte(w[2], w[1], sh),
+                          (int)__builtin_amdgcn_alignbyte(w[3], w[2], sh), (int)__builtin_amdgcn_alignbyte(w[4], w[3], sh),
+                          0, 0, 0, 0}
+                    : v8i{(int)w[0], (int)w[1], (int)w[2], (int)w[3], 0, 0, 0, 0};
       }
       v8i xv[2];
       float dx[2];
 #pragma unroll
       for (int th = 0; th < 2; ++th) {
         const int t = 32 * th + col;
-        const uint4 raw = *reinterpret_cast<const uint4*>(slot + 256 * t + 16 * ((2 * b + h) ^ (col & 15)));
+        const uint4 raw =
+            *reinterpret_cast<const uint4*>(slot + kAct * sp + 256 * t + 16 * ((2 * bs + h) ^ (col & 15)));
         const uint32_t rw[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           xv[th][k] = (int)(((rw[k] >> 4) & 0x07070707u) | (rw[k] & 0x80808080u));
           xv[th][4 + k] = (int)(rw[k] & 0x8f8f8f8fu);
         }
-        dx[th] = (float)*reinterpret_cast<const _Float16*>(slot + kSD + 4 * (64 * (b >> 1) + t) + 2 * (b & 1));
+        dx[th] = (float)*reinterpret_cast<const _Float16*>(slot + kSD + 1024 * sp + 4 * (64 * (bs >> 1) + t) +
+                                                            2 * (bs & 1));
       }
       // four independent MFMAs in flight, then y += dx * (ws * I)
       v16f d[4];
@@ -800,33 +829,25 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
       for (int q = 0; q < 4; ++q) {
         const int ct = q & 1;
         if (kExact && exact[ct])  // wave-uniform
-          y[q] = ggml_block_terms(y[q], d[q], dx[q >> 1], slot_lds + kSW + kRowW * (64 * cp + 32 * ct + 4 * h) + off);
+          y[q] = ggml_block_terms(y[q], d[q], dx[q >> 1],
+                                  slot_lds + kSW + kRowW * (64 * cp + 32 * ct + 4 * h) + 68 * ph + kE[j]);
         else
           y[q] = fma_block(y[q], d[q], dx[q >> 1]);
       }
     }
   };
 
-  // The K loop.  Two stages per barrier: the direct loads of the next pair
-  // go out right after the barrier, into the slots the previous pair used,
-  // so each wave waits for all of its own loads (vmcnt 0) at the top of a
-  // pair.
+  // The K loop.  The direct loads of the next pair go out right after the
+  // barrier, into the slot the previous pair used, so each wave waits for
+  // all of its own loads (vmcnt 0) at the top of a pair.
+  const int npair = (nst + 1) >> 1;
   auto kloop = [&](auto exact_tag, bool& out) {
     issue(0);
-    if (nst > 1) issue(1);
-    int st = 0;
-    for (; st + 1 < nst; st += 2) {
+    for (int p = 0; p < npair; ++p) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      lds_barrier();  // the pair is in for every wave; the previous pair's slots are free
-      if (st + 2 < nst) issue(st + 2);
-      if (st + 3 < nst) issue(st + 3);
-      stage(st, exact_tag, out);
-      stage(st + 1, exact_tag, out);
-    }
-    if (st < nst) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      lds_barrier();
-      stage(st, exact_tag, out);
+      lds_barrier();  // the pair is in for every wave; the previous pair's slot is free
+      if (p + 1 < npair) issue(p + 1);
+      if (2 * p + sp < nst) phase_blocks(p, exact_tag, out);
     }
   };
   // Weights quantized by GGML keep every exponent in range, and the loop
