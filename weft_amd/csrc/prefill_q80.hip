@@ -150,10 +150,14 @@ constexpr bool has_table() {
   return F == WFmt::MXFP4 || F == WFmt::NVFP4;
 }
 // LDS bytes per weight row and stage: the row's 8 records (2 kRec dwords).
-// Q4_1's 40-dword rows put the 32 rows a wave reads at one record offset
-// into 8 of the 64 banks (4-way conflicts): its rows get one pad dword (an
-// odd stride, 32 banks).  Padding the 36- and 34-dword rows (2-way, 1-way)
-// measured slower: two more wave-wide loads per stage.
+// Q4_0 / NVFP4 rows (144 bytes a stage, whole 16-byte chunks) arrive by
+// 16-byte direct loads when 16-byte aligned, else by dword loads, at that
+// stride (2-way bank conflicts on the operand reads).  Q4_1's 40-dword rows
+// would put the 32 rows a wave reads at one record offset into 8 of the 64
+// banks (4-way): its rows get one pad dword (an odd stride, 32 banks) and
+// dword loads (its 16-byte loads at the unpadded stride measured 2.3 us
+// slower; a padded 16-byte stride does not fit the LDS).  Padding the 36-
+// and 34-dword rows measured slower: two more wave-wide loads per stage.
 template <WFmt F>
 constexpr int w_lds_row() {
   return 4 * (2 * WTraits<F>::kRec + ((2 * WTraits<F>::kRec) % 8 == 0 ? 1 : 0));
@@ -175,7 +179,11 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
   constexpr int kWDp = kRL / 4;              // the same, with the pad
   constexpr int kWSlots = kNT * kWDp / 64;   // 72 / 68 / 82 wave-wide dword loads
   constexpr int kWPerWave = (kWSlots + 3) / 4;
+  constexpr int kCh = kRB / 16;              // 16-byte chunks per row and stage (9 / 10)
+  constexpr int kW16 = kNT * kCh / 64;       // 18 / 20 wave-wide 16-byte loads
+  constexpr int kW16PerWave = (kW16 + 3) / 4;
   static_assert(kNT * kWDp % 64 == 0 && (kRL == kRB || kRL == kRB + 4), "whole wave-wide weight loads");
+  static_assert(kRB % 16 != 0 || kNT * kCh % 64 == 0, "whole wave-wide 16-byte weight loads");
   static_assert(kTilePlaneBytes <= 2 * kStage, "an output plane fits one ring half");
 
   // two ring slots; a slot being filled by direct loads never aliases the
@@ -251,6 +259,20 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
   // per-block token scales of this parity's stage: wave wcol == 0, token = lane
   const uint8_t* dsrc = a.Xp + (size_t)act_row(min(lane, mrows - 1)) * xs + a.K;
 
+  // weight rows by 16-byte loads when a row's stage bytes are whole aligned
+  // chunks (wave-uniform), at LDS stride kRB; else dword loads at kRL
+  const bool w16 = kRL == kRB && kRB % 16 == 0 && ((reinterpret_cast<uintptr_t>(W) | ws_row) & 15) == 0;
+  const int rl = w16 ? kRB : kRL;
+  // chunk q = 64 k + lane of load k = wcol + 4 i: row q / kCh, chunk q % kCh
+  // (offsets from the tile's first row: the host keeps them in 32 bits)
+  const uint8_t* wtile = W + (size_t)n0 * ws_row;
+  uint32_t wv16[kW16PerWave];
+#pragma unroll
+  for (int i = 0; i < kW16PerWave; ++i) {
+    const int q = 64 * min(wcol + 4 * i, kW16 - 1) + lane, row = q / max(kCh, 1);
+    wv16[i] = (uint32_t)min(row, a.N - 1 - n0) * (uint32_t)ws_row + 16 * (uint32_t)(q - kCh * row);
+  }
+
   // LDS byte addresses as integers from one wave-uniform base: no per-use
   // generic-to-LDS pointer casts (their null checks on VALU do not compile)
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
@@ -260,6 +282,13 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       lds_dma16(asrc[i] + 256 * (size_t)st, stage + 1024 * (wcol + 4 * i));
+    if (kRL == kRB && kRB % 16 == 0 && w16) {
+#pragma unroll
+      for (int i = 0; i < kW16PerWave; ++i)
+        if (kW16 % 4 == 0 || wcol + 4 * i < kW16)  // wave-uniform
+          lds_dma16(wtile + (size_t)st * kRB + wv16[i], stage + kAQ + 1024 * (wcol + 4 * i));
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < kWPerWave; ++i) {
       const int k = wcol + 4 * i;
@@ -308,7 +337,7 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
     if (2 * pair + par < nst) {
       const uint8_t* stage = cur + par * kStage;
       const uint8_t* AQ = stage;
-      const uint8_t* wrow = stage + kAQ + (32 * wcol + col) * kRL;
+      const uint8_t* wrow = stage + kAQ + (32 * wcol + col) * rl;
       const float* dxs = &adt[pair & 1][par][0];
       const uint16_t* sxs = &ast[pair & 1][par][0];
 #pragma unroll
