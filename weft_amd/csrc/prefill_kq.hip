@@ -33,7 +33,8 @@
 // 128 h .. +127: Q6_K's ql/qh half, Q5_K's groups 4h .. 4h+3) for all 64
 // tokens as two 32x32 tiles that share the weight operand.  One superblock
 // per ring slot, two slots: the waves stage superblock b+1 by direct
-// global->LDS loads while computing b.  A Q6_K record (210 bytes) is 2-byte
+// global->LDS loads while computing b (Q5_K's 176-byte records as 16-byte
+// chunks when the rows are aligned).  A Q6_K record (210 bytes) is 2-byte
 // aligned for odd b, so its row is staged from the dword holding its first
 // byte (54 dwords, 216 bytes per LDS row) and the odd superblocks read with
 // a 2-byte alignment; the even/odd slots are the two instantiations of the
@@ -182,6 +183,7 @@ __global__ void __launch_bounds__(kThreads, 1) kq_mfma_gemm(GemmArgs a) {
                         16 * (lane & 1);
   const uint8_t* dsrc = a.Xq + (size_t)act_row(min(lane, mrows - 1)) * xrb;  // Q8_K d of token lane
 
+  const bool w16 = ((reinterpret_cast<uintptr_t>(W) | wrb) & 15) == 0;  // Q5_K: 16-byte weight loads
   const uint32_t ring_lds[2] = {(uint32_t)__builtin_amdgcn_readfirstlane(lds_addr(ring0)),
                                 (uint32_t)__builtin_amdgcn_readfirstlane(lds_addr(ring1))};
   auto issue = [&](int b, int slot) {
@@ -195,6 +197,22 @@ __global__ void __launch_bounds__(kThreads, 1) kq_mfma_gemm(GemmArgs a) {
     // weight rows: Q6_K from the dword holding the record's first byte (2
     // bytes before it for odd b); dword 53 is padding and re-reads dword 52
     const size_t wb = (size_t)b * TT::kRec - (k6 ? 2 * (b & 1) : 0);
+    if constexpr (!k6) {
+      // Q5_K records are 11 chunks of 16 bytes: 22 wave-wide 16-byte loads
+      // when the rows are 16-byte aligned (row q / 11, chunk q % 11)
+      if (w16) {
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+          const int k = wave + 8 * i;
+          if (k < kNT * 11 / 64) {
+            const int q = 64 * k + lane, row = q / 11;
+            const uint8_t* g = W + (size_t)min(n0 + row, a.N - 1) * wrb + wb + 16 * (q - 11 * row);
+            lds_dma16(g, base + kAQ + TT::kBS + 1024 * k);
+          }
+        }
+        return;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < (kWSlots + 7) / 8; ++i) {
       const int k = wave + 8 * i;
