@@ -16,8 +16,9 @@
 // Tiling as in the Q4_K prefill: 64 tokens x 128 weight rows per workgroup,
 // 8 waves (superblock parity x 4 column groups), each wave two 32x32 tiles.
 // A 66-byte record is only 2-byte aligned, so the weight rows of a superblock
-// PAIR (132 bytes, 4-byte aligned when K/256 is even) are staged together;
-// each parity reads its half with aligned dword reads and byte alignment.
+// PAIR (132 bytes, 4-byte aligned when K/256 is even) are staged together
+// (as whole 16-byte chunks when the rows allow, Tile below); each parity
+// reads its half with aligned dword reads and byte alignment.
 // Grid and sign tables live in LDS, the signs as byte masks (0xff per -1).
 #include <algorithm>
 #include <type_traits>
@@ -43,16 +44,24 @@ constexpr int kThreads = 512;  // 8 waves: 4 column groups x 2 superblock pariti
 constexpr int kAQ = kMT * 256;                    // activation int8 of one superblock
 
 // Per format (kXs: IQ2_XS, else IQ2_XXS): record bytes and the weight tile
-// of a superblock pair (4-byte aligned: 132 / 148 bytes per row).
+// of a superblock pair (4-byte aligned: 132 / 148 bytes per row).  Rows whose
+// bytes are whole 16-byte chunks (K a multiple of 2048, 16-byte aligned)
+// arrive as the 11 chunks holding the pair (at 4 (pair % 4) bytes into the
+// first), by 16-byte direct loads at an LDS stride of 176 bytes; other rows
+// by dword loads at the pair's own stride.
 template <bool kXs>
 struct Tile {
   static constexpr int kRec = kXs ? kIq2xsBytes : kIq2xxsBytes;  // 74 / 66
   static constexpr int kPairB = 2 * kRec;
-  static constexpr int kWT = kNT * kPairB;                      // 18944 / 16896
+  static constexpr int kRowL = 176;                             // LDS stride of 16-byte-loaded rows
+  static constexpr int kCh = kRowL / 16;                        // 11 chunks
+  static constexpr int kW16 = kNT * kCh / 64;                   // 22 wave-wide 16-byte loads
+  static constexpr int kWT = kNT * kRowL;                       // 22528
   static constexpr int kSlot = 2 * kAQ + kWT;                   // one ring slot: both parities + weights
   static constexpr int kSlotAlloc = kSlot + 16;                 // slack: a read may run past row 127
   static constexpr int kWD = kPairB / 4;                        // 37 / 33 dwords per row and pair
   static constexpr int kWSlots = kNT * kWD / 64;                // 74 / 66 wave-wide dword loads
+  static_assert(kPairB + 12 + 8 <= kRowL && kNT * kCh % 64 == 0, "a pair fits its 16-byte chunks");
   static constexpr int kGrid = kXs ? 512 : 256;                 // grid entries
   static_assert(kNT * kWD % 64 == 0, "weight pair tile is whole wave loads");
   static_assert(kTilePlaneBytes <= kSlot, "an output plane fits one ring slot");
@@ -192,12 +201,33 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
   // pointers (no per-load generic-to-LDS casts)
   const uint32_t ring_lds[2] = {(uint32_t)__builtin_amdgcn_readfirstlane(lds_addr(ring0)),
                                 (uint32_t)__builtin_amdgcn_readfirstlane(lds_addr(ring1))};
+  // weight rows by 16-byte loads (wave-uniform): rows, their stride and the
+  // row's bytes whole 16-byte chunks
+  const size_t rbytes = (size_t)nsb * TT::kRec;
+  const bool w16 = ((reinterpret_cast<uintptr_t>(W) | wrb | rbytes) & 15) == 0;
+  const int rl = w16 ? TT::kRowL : kPairB;
   auto issue = [&](int pair, uint8_t* ring) {
     const int b = 2 * pair + par;
     const uint32_t base = ring == ring0 ? ring_lds[0] : ring_lds[1];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       lds_dma16(asrc[i] + (size_t)b * kQ8_KBytes, base + par * kAQ + 1024 * (wcol + 4 * i));
+    if (w16) {
+      // the 11 chunks from the one holding the pair's first byte; chunks past
+      // the row's end re-read its last chunk (bytes no read uses)
+      const size_t cb = ((size_t)pair * kPairB) & ~(size_t)15;
+      const int cmax = (int)((rbytes - cb) / 16) - 1;
+#pragma unroll
+      for (int i = 0; i < (TT::kW16 + 7) / 8; ++i) {
+        const int k = wave + 8 * i;
+        if (k < TT::kW16) {
+          const int q = 64 * k + lane, row = q / TT::kCh, c = min(q - TT::kCh * row, cmax);
+          const uint8_t* g = W + (size_t)min(n0 + row, a.N - 1) * wrb + cb + 16 * c;
+          lds_dma16(g, base + 2 * kAQ + 1024 * k);
+        }
+      }
+      return;
+    }
     // weight pair: 66 dword loads over the 8 waves
 #pragma unroll
     for (int i = 0; i < (kWSlots + 7) / 8; ++i) {
@@ -239,7 +269,8 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
       if (wcol == 0) load_dx(pair + 1);
     }
     const uint8_t* AQ = cur + par * kAQ;
-    const uint8_t* rec = cur + 2 * kAQ + (32 * wcol + col) * kPairB + sb0;
+    const int o = w16 ? (pair * kPairB) & 15 : 0;  // the pair's first byte in its row's LDS copy
+    const uint8_t* rec = cur + 2 * kAQ + (32 * wcol + col) * rl + o + sb0;
     const uint4* dxb = &dxq[pair & 1][par][0];
     // fp16 d: bytes 0-1 of the record (rec is 4-byte aligned for parity 0,
     // 2 past an aligned dword for parity 1)
