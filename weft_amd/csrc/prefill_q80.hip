@@ -618,28 +618,30 @@ __global__ void __launch_bounds__(256) q80_planar_kernel(const float* __restrict
 // 64 x 64 quarter, so each weight operand and each split activation operand
 // feeds two MFMAs.  The four phases' partial sums are added through LDS at
 // the end, in phase order.  Every global byte arrives by direct
-// global->LDS loads into two pair slots, one pair ahead: activation rows
-// with their 16 chunks of 16 bytes XOR-swizzled by token (conflict-free
-// operand reads), the token scales block-major, and each weight row's 272
-// bytes of the pair (16 records) as 17 chunks of 16 bytes: 34 wave-wide
-// 16-byte loads a pair (a row's pair is 16-byte aligned when K is a
-// multiple of 512 and the rows are; otherwise, and for a last single
-// stage, 136 dword loads fill the same layout).  A phase's four records
-// start at a dword boundary of the row (68 p bytes), so its operand bytes
-// sit at fixed offsets from there.  One barrier per pair.
+// global->LDS 16-byte loads into two pair slots, one pair ahead:
+// activation rows with their 16 chunks of 16 bytes XOR-swizzled by token
+// (conflict-free operand reads), the token scales block-major, and each
+// weight row's 272 bytes of the pair (16 records) as four 68-byte phase
+// segments at 16-byte aligned LDS offsets 80 p of a 336-byte row (five
+// chunks each, the fifth ending at the segment's end; a 16-byte load needs
+// only a 4-byte aligned source).  A phase then reads its four records of a
+// row with four 16-byte LDS reads and one dword, at a row stride (84
+// dwords) that puts 16 lanes' 16-byte reads on all 64 banks.  One barrier
+// per pair.
 namespace mx {
 
 constexpr int kMT = 64;
 constexpr int kNT = 128;
 constexpr int kAct = kMT * 256;            // 16384: one stage's activation tile
-constexpr int kRowW = 272;                 // LDS bytes per weight row and pair
+constexpr int kRowW = 336;                 // LDS bytes per weight row and pair: 4 segments, 1 pad chunk
+constexpr int kSeg = 80;                   // LDS bytes per phase segment (68 used)
 constexpr int kSD = 2 * kAct;              // token scales, fp16 [stage][block pair][token][2]
 constexpr int kSW = kSD + 2 * kMT * 16;    // 34816: weight rows
-constexpr int kSlot = kSW + kNT * kRowW;   // 69632
-constexpr int kLds = 2 * kSlot;            // 139264
-constexpr int kW16Loads = kNT * kRowW / 1024;  // 34 wave-wide 16-byte loads of weights
-constexpr int kW4Loads = kNT * kRowW / 256;    // 136 wave-wide dword loads
-static_assert(kNT * kRowW % 1024 == 0 && kW4Loads % 8 == 0, "whole wave-wide weight loads");
+constexpr int kSlot = kSW + kNT * kRowW;   // 77824
+constexpr int kLds = 2 * kSlot;            // 155648
+constexpr int kWChunks = kRowW / 16;       // 21 chunks per LDS row
+constexpr int kWLoads = kNT * kWChunks / 64;  // 42 wave-wide 16-byte loads of weights
+static_assert(kNT * kWChunks % 64 == 0 && 4 * kSeg <= kRowW, "whole wave-wide weight loads");
 
 // Exponents whose block terms the scaled MFMA reproduces.  GGML forms
 // d = fp16(dx) * 2^(e-128), then sumf + d * I, each step rounded
@@ -743,15 +745,19 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
   };
   const uint32_t va0 = act_off(wave), va1 = act_off(wave + 8);
   const uint32_t vsc = act_row(min(lane, mlast)) * xs + (uint32_t)a.K + 4 * (uint32_t)(wave & 3);
-  // 16-byte weight chunks: load k = wave + 8 i (< 34) covers chunks 64 k + lane
-  // (row q / 17, chunk q % 17)
-  const bool w16 = (((uintptr_t)wbase | ws_row) & 15) == 0;
-  uint32_t vw[5];
+  // weight chunks: load k = wave + 8 i (< 42) covers LDS chunks q = 64 k + lane:
+  // row q / 21, chunk c = q % 21 = 5 s + j of segment s (c = 20: the pad,
+  // a copy of s = 3, j = 4); chunk j < 4 holds segment bytes 16 j .. +15,
+  // chunk 4 bytes 52 .. 67.  A single last stage has only segments 0-1:
+  // segments 2-3 then copy them (in the row; no phase reads them).
+  auto w_off = [&](int k, bool tail) {
+    const int q = 64 * min(k, kWLoads - 1) + lane, row = q / kWChunks, c = q - kWChunks * row;
+    const int sg = min(c / 5, 3), j = c - 5 * sg;
+    return (uint32_t)min(row, nlast) * ws_row + 68 * (uint32_t)(tail ? sg & 1 : sg) + (j < 4 ? 16 * j : 52);
+  };
+  uint32_t vw[6];
 #pragma unroll
-  for (int i = 0; i < 5; ++i) {
-    const int q = 64 * min(wave + 8 * i, kW16Loads - 1) + lane, row = q / 17;
-    vw[i] = (uint32_t)min(row, nlast) * ws_row + 16 * (uint32_t)(q - 17 * row);
-  }
+  for (int i = 0; i < 6; ++i) vw[i] = w_off(wave + 8 * i, false);
 
   // LDS byte addresses as integers from one wave-uniform base: no per-use
   // generic-to-LDS pointer casts (their null checks on VALU do not compile)
@@ -767,20 +773,11 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
         dma16_s(xb, va1, slot + kAct * s + 1024 * (wave + 8));
       }
     if (wave < 4 || both) lds_dma4_s(xbase + 16 * (size_t)(2 * p + (wave >> 2)), vsc, slot + kSD + 256 * wave);
-    const uint8_t* wb = wbase + kRowW * (size_t)p;
-    if (w16 && both) {
+    const uint8_t* wb = wbase + 272 * (size_t)p;
 #pragma unroll
-      for (int i = 0; i < 5; ++i)
-        if (wave + 8 * i < kW16Loads) dma16_s(wb, vw[i], slot + kSW + 1024 * (wave + 8 * i));
-    } else {
-      // dword loads into the same layout; a single last stage has 34 dwords a row
-      const int dmax = both ? kRowW / 4 - 1 : kRowW / 8 - 1;
-      for (int i = 0; i < kW4Loads / 8; ++i) {
-        const int q = 64 * (wave + 8 * i) + lane, row = q / (kRowW / 4);
-        const int d = min(q - (kRowW / 4) * row, dmax);
-        lds_dma4_s(wb, (uint32_t)min(row, nlast) * ws_row + 4 * (uint32_t)d, slot + kSW + 256 * (wave + 8 * i));
-      }
-    }
+    for (int i = 0; i < 6; ++i)
+      if (wave + 8 * i < kWLoads)
+        dma16_s(wb, both ? vw[i] : w_off(wave + 8 * i, true), slot + kSW + 1024 * (wave + 8 * i));
   };
 
   v16f y[4];  // tile 2 * token half + column tile
@@ -800,13 +797,18 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
     constexpr bool kExact = decltype(exact_tag)::value;
     const uint8_t* slot = lds + (p & 1) * kSlot;
     const uint32_t slot_lds = lds0 + (uint32_t)(p & 1) * kSlot;
-    // the 17 dwords holding records 4 ph .. 4 ph + 3 of rows 64 cp + 32 ct + col
+    // the 17 dwords holding records 4 ph .. 4 ph + 3 of rows 64 cp + 32 ct + col:
+    // four 16-byte reads and the segment's last dword (at byte 76 of its copy)
     uint32_t wd[2][17];
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
-      const uint8_t* wr = slot + kSW + kRowW * (64 * cp + 32 * ct + col) + 68 * ph;
+      const uint8_t* wr = slot + kSW + kRowW * (64 * cp + 32 * ct + col) + kSeg * ph;
 #pragma unroll
-      for (int i = 0; i < 17; ++i) wd[ct][i] = ld32(wr + 4 * i);
+      for (int i = 0; i < 4; ++i) {
+        const uint4 v = *reinterpret_cast<const uint4*>(wr + 16 * i);
+        wd[ct][4 * i] = v.x, wd[ct][4 * i + 1] = v.y, wd[ct][4 * i + 2] = v.z, wd[ct][4 * i + 3] = v.w;
+      }
+      wd[ct][16] = ld32(wr + 76);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -859,7 +861,7 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
         const int ct = q & 1;
         if (kExact && exact[ct])  // wave-uniform
           y[q] = ggml_block_terms(y[q], d[q], dx[q >> 1],
-                                  slot_lds + kSW + kRowW * (64 * cp + 32 * ct + 4 * h) + 68 * ph + kE[j]);
+                                  slot_lds + kSW + kRowW * (64 * cp + 32 * ct + 4 * h) + kSeg * ph + kE[j]);
         else
           y[q] = fma_block(y[q], d[q], dx[q >> 1]);
       }
