@@ -340,6 +340,23 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
       const uint8_t* wrow = stage + kAQ + (32 * wcol + col) * rl;
       const float* dxs = &adt[pair & 1][par][0];
       const uint16_t* sxs = &ast[pair & 1][par][0];
+      // Q4_0: the row's 144 stage bytes as nine 16-byte LDS reads (the 36-dword
+      // stride puts 16 lanes' 16-byte reads on all 64 banks); every record is
+      // then taken from registers at fixed offsets
+      uint32_t wq[F == WFmt::Q4_0 ? 36 : 1];
+      if constexpr (F == WFmt::Q4_0) {
+#pragma unroll
+        for (int i = 0; i < 9; ++i) {
+          const uint4 v = *reinterpret_cast<const uint4*>(wrow + 16 * i);
+          wq[4 * i] = v.x, wq[4 * i + 1] = v.y, wq[4 * i + 2] = v.z, wq[4 * i + 3] = v.w;
+        }
+      }
+      auto wld = [&](int byte) -> uint32_t {  // the row's aligned dword at `byte`
+        if constexpr (F == WFmt::Q4_0)
+          return wq[byte >> 2];
+        else
+          return ld32(wrow + byte);
+      };
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         if constexpr (F == WFmt::NVFP4) {
@@ -380,11 +397,10 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
         // raw record j of this lane's weight row: header, then 16 nibble bytes
         const int off = T::kRec * j + T::kHdr;  // first nibble byte
         const int sh = off & 3, b4 = off - sh;
-        uint32_t w0 = ld32(wrow + b4), w1 = ld32(wrow + b4 + 4), w2 = ld32(wrow + b4 + 8),
-                 w3 = ld32(wrow + b4 + 12);
+        uint32_t w0 = wld(b4), w1 = wld(b4 + 4), w2 = wld(b4 + 8), w3 = wld(b4 + 12);
         uint32_t q0 = w0, q1 = w1, q2 = w2, q3 = w3;
         if (sh) {
-          const uint32_t w4 = ld32(wrow + b4 + 16);
+          const uint32_t w4 = wld(b4 + 16);
           q0 = __builtin_amdgcn_alignbyte(w1, w0, sh);
           q1 = __builtin_amdgcn_alignbyte(w2, w1, sh);
           q2 = __builtin_amdgcn_alignbyte(w3, w2, sh);
@@ -397,7 +413,7 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
           const uint32_t hd = ld32(wrow + T::kRec * j);  // records are 4-byte aligned here
           wbits = hd & 0xffffu;
         } else if constexpr (F == WFmt::Q4_0) {
-          wbits = sh >= 2 ? (w0 & 0xffffu) : (ld32(wrow + b4 - 4) >> 16);
+          wbits = sh >= 2 ? (w0 & 0xffffu) : (wld(b4 - 4) >> 16);
         } else {
           const uint32_t e = sh >= 1 ? ((w0 >> (8 * (sh - 1))) & 0xffu) : (ld32(wrow + b4 - 4) >> 24);
           wsc = scl[e];
