@@ -16,9 +16,10 @@
 // Tiling as in the Q4_K prefill: 64 tokens x 128 weight rows per workgroup,
 // 8 waves (superblock parity x 4 column groups), each wave two 32x32 tiles.
 // A 66-byte record is only 2-byte aligned, so the weight rows of a superblock
-// PAIR (132 bytes, 4-byte aligned when K/256 is even) are staged together
-// (as whole 16-byte chunks when the rows allow, Tile below); each parity
-// reads its half with aligned dword reads and byte alignment.
+// PAIR (132 bytes, 4-byte aligned when K/256 is even) are staged together,
+// each parity's record in a 16-byte aligned segment of its own (Tile
+// below); a parity reads its group bytes with five 16-byte LDS reads and
+// byte alignment.
 // Grid and sign tables live in LDS, the signs as byte masks (0xff per -1).
 #include <algorithm>
 #include <type_traits>
@@ -44,26 +45,32 @@ constexpr int kThreads = 512;  // 8 waves: 4 column groups x 2 superblock pariti
 constexpr int kAQ = kMT * 256;                    // activation int8 of one superblock
 
 // Per format (kXs: IQ2_XS, else IQ2_XXS): record bytes and the weight tile
-// of a superblock pair (4-byte aligned: 132 / 148 bytes per row).  Rows whose
-// bytes are whole 16-byte chunks (K a multiple of 2048, 16-byte aligned)
-// arrive as the 11 chunks holding the pair (at 4 (pair % 4) bytes into the
-// first), by 16-byte direct loads at an LDS stride of 176 bytes; other rows
-// by dword loads at the pair's own stride.
+// of a superblock pair (4-byte aligned: 132 / 148 bytes per row).  A row's
+// pair is 11 chunks of 16 bytes in LDS (176-byte stride: 16 lanes' 16-byte
+// reads fall on all 64 banks), each copied by a 16-byte direct load from a
+// 4-byte aligned source (P: the pair's first byte in the row, R = kRec):
+//   chunks 0-4   bytes P + 16 c          record 0 from its first byte (d, then
+//                                         its group bytes at 2 + 8 g)
+//   chunks 5-8   bytes P + R + 2 + 16 j  record 1's group bytes from byte 0
+//   chunk 9      IQ2_XS: P + R + 58      record 1's scales at bytes 8-15
+//                IQ2_XXS: as chunk 10
+//   chunk 10     bytes P + R - 2         record 1's d at bytes 2-3
+// so both parities take group g's words from dwords 2g .. 2g + 2 of their
+// five chunks, shifted by 2 bytes (parity 0) or 0 (parity 1).
 template <bool kXs>
 struct Tile {
   static constexpr int kRec = kXs ? kIq2xsBytes : kIq2xxsBytes;  // 74 / 66
   static constexpr int kPairB = 2 * kRec;
-  static constexpr int kRowL = 176;                             // LDS stride of 16-byte-loaded rows
+  static constexpr int kRowL = 176;                             // LDS bytes per weight row and pair
   static constexpr int kCh = kRowL / 16;                        // 11 chunks
   static constexpr int kW16 = kNT * kCh / 64;                   // 22 wave-wide 16-byte loads
   static constexpr int kWT = kNT * kRowL;                       // 22528
   static constexpr int kSlot = 2 * kAQ + kWT;                   // one ring slot: both parities + weights
-  static constexpr int kSlotAlloc = kSlot + 16;                 // slack: a read may run past row 127
-  static constexpr int kWD = kPairB / 4;                        // 37 / 33 dwords per row and pair
-  static constexpr int kWSlots = kNT * kWD / 64;                // 74 / 66 wave-wide dword loads
-  static_assert(kPairB + 12 + 8 <= kRowL && kNT * kCh % 64 == 0, "a pair fits its 16-byte chunks");
+  static constexpr int kSlotAlloc = kSlot + 16;
+  static_assert((!kXs || kRec + 58 + 16 <= kPairB) && kRec + 66 <= kPairB && 80 <= kPairB &&
+                    kNT * kCh % 64 == 0,
+                "chunks within the pair");
   static constexpr int kGrid = kXs ? 512 : 256;                 // grid entries
-  static_assert(kNT * kWD % 64 == 0, "weight pair tile is whole wave loads");
   static_assert(kTilePlaneBytes <= kSlot, "an output plane fits one ring slot");
 };
 
@@ -86,12 +93,6 @@ struct GemmArgs {
 // in every instantiation.
 __device__ __forceinline__ void lds_dma16(const uint8_t* g, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-               :
-               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g)
-               : "memory", "m0");
-}
-__device__ __forceinline__ void lds_dma4(const uint8_t* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
                :
                : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g)
                : "memory", "m0");
@@ -140,7 +141,7 @@ __device__ __forceinline__ v4i weight_bytes(uint2 g0, uint2 g1, uint2 z0, uint2 
 template <bool kGroup, bool kXs = false>
 __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
   using TT = Tile<kXs>;
-  constexpr int kPairB = TT::kPairB, kWD = TT::kWD, kWSlots = TT::kWSlots;
+  constexpr int kPairB = TT::kPairB;
   __shared__ __align__(16) uint8_t ring0[TT::kSlotAlloc];
   __shared__ __align__(16) uint8_t ring1[TT::kSlotAlloc];
   // [slot][parity][token]: the token's Q8_K d as the bf16 parts of the
@@ -201,43 +202,26 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
   // pointers (no per-load generic-to-LDS casts)
   const uint32_t ring_lds[2] = {(uint32_t)__builtin_amdgcn_readfirstlane(lds_addr(ring0)),
                                 (uint32_t)__builtin_amdgcn_readfirstlane(lds_addr(ring1))};
-  // weight rows by 16-byte loads (wave-uniform): rows, their stride and the
-  // row's bytes whole 16-byte chunks
-  const size_t rbytes = (size_t)nsb * TT::kRec;
-  const bool w16 = ((reinterpret_cast<uintptr_t>(W) | wrb | rbytes) & 15) == 0;
-  const int rl = w16 ? TT::kRowL : kPairB;
+  // weight chunk q = 64 k + lane of load k = wave + 8 i (< 22): row q / 11,
+  // chunk q % 11 at the byte offsets of the layout above
+  uint32_t wv[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const int q = 64 * min(wave + 8 * i, TT::kW16 - 1) + lane, row = q / TT::kCh, c = q - TT::kCh * row;
+    const int off = c < 5 ? 16 * c : c < 9 ? TT::kRec + 2 + 16 * (c - 5) : (kXs && c == 9) ? TT::kRec + 58 : TT::kRec - 2;
+    wv[i] = (uint32_t)min(row, a.N - 1 - n0) * (uint32_t)wrb + (uint32_t)off;
+  }
+  const uint8_t* wtile = W + (size_t)n0 * wrb;
   auto issue = [&](int pair, uint8_t* ring) {
     const int b = 2 * pair + par;
     const uint32_t base = ring == ring0 ? ring_lds[0] : ring_lds[1];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       lds_dma16(asrc[i] + (size_t)b * kQ8_KBytes, base + par * kAQ + 1024 * (wcol + 4 * i));
-    if (w16) {
-      // the 11 chunks from the one holding the pair's first byte; chunks past
-      // the row's end re-read its last chunk (bytes no read uses)
-      const size_t cb = ((size_t)pair * kPairB) & ~(size_t)15;
-      const int cmax = (int)((rbytes - cb) / 16) - 1;
 #pragma unroll
-      for (int i = 0; i < (TT::kW16 + 7) / 8; ++i) {
-        const int k = wave + 8 * i;
-        if (k < TT::kW16) {
-          const int q = 64 * k + lane, row = q / TT::kCh, c = min(q - TT::kCh * row, cmax);
-          const uint8_t* g = W + (size_t)min(n0 + row, a.N - 1) * wrb + cb + 16 * c;
-          lds_dma16(g, base + 2 * kAQ + 1024 * k);
-        }
-      }
-      return;
-    }
-    // weight pair: 66 dword loads over the 8 waves
-#pragma unroll
-    for (int i = 0; i < (kWSlots + 7) / 8; ++i) {
-      const int k = wave + 8 * i;
-      if (k < kWSlots) {
-        const int q = 64 * k + lane, row = q / kWD, part = q - kWD * row;
-        const uint8_t* g = W + (size_t)min(n0 + row, a.N - 1) * wrb + (size_t)pair * kPairB + 4 * part;
-        lds_dma4(g, base + 2 * kAQ + 256 * k);
-      }
-    }
+    for (int i = 0; i < (TT::kW16 + 7) / 8; ++i)
+      if (wave + 8 * i < TT::kW16)
+        lds_dma16(wtile + (size_t)pair * kPairB + wv[i], base + 2 * kAQ + 1024 * (wave + 8 * i));
   };
   float dxr = 0.f;
   auto load_dx = [&](int pair) {
@@ -252,7 +236,6 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
     for (int r = 0; r < 16; ++r) y[t][r] = 0.f;
   const v16i zero = {};
   const int sw = col & 15;
-  const int sb0 = par * TT::kRec;  // this parity's record within the pair: 0 or 66 / 74
 
   auto step = [&](int pair, const uint8_t* cur, uint8_t* nxt) {
     __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of this pair have landed
@@ -269,19 +252,24 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
       if (wcol == 0) load_dx(pair + 1);
     }
     const uint8_t* AQ = cur + par * kAQ;
-    const int o = w16 ? (pair * kPairB) & 15 : 0;  // the pair's first byte in its row's LDS copy
-    const uint8_t* rec = cur + 2 * kAQ + (32 * wcol + col) * rl + o + sb0;
+    const uint8_t* wrow = cur + 2 * kAQ + (32 * wcol + col) * TT::kRowL;
+    const uint8_t* seg = wrow + 80 * par;  // this parity's five chunks
     const uint4* dxb = &dxq[pair & 1][par][0];
-    // fp16 d: bytes 0-1 of the record (rec is 4-byte aligned for parity 0,
-    // 2 past an aligned dword for parity 1)
-    const uint32_t dword0 = ld32(rec - 2 * par);
+    // fp16 d: bytes 0-1 of chunk 0 (parity 0) or 2-3 of chunk 10 (parity 1)
+    const uint32_t dword0 = ld32(par ? wrow + 160 : wrow);
     const float dw = fp16_to_fp32(par ? dword0 >> 16 : dword0 & 0xffffu);
-    const int sh = 2 - 2 * par;  // byte offset of group data (rec + 2 + 8g) in its dword
-    const uint8_t* gbase = rec + 2 - sh;  // 4-byte aligned
-    // IQ2_XS: the 8 scale bytes at rec + 66 (byte offset 2 - 2 par in its dword)
+    const int sh = 2 - 2 * par;  // byte offset of the group bytes in their dwords
+    uint32_t wq[20];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+      const uint4 v = *reinterpret_cast<const uint4*>(seg + 16 * i);
+      wq[4 * i] = v.x, wq[4 * i + 1] = v.y, wq[4 * i + 2] = v.z, wq[4 * i + 3] = v.w;
+    }
+    // IQ2_XS: the 8 scale bytes, at bytes 66-73 of parity 0's chunks and
+    // 8-15 of parity 1's chunk 9 (dwords 16-18 / 18-19, shift sh)
     uint32_t scl0 = 0, scl1 = 0;
     if constexpr (kXs) {
-      const uint8_t* sbase = rec + 66 - sh;  // 4-byte aligned
+      const uint8_t* sbase = seg + 64 + 8 * par;
       const uint32_t s0w = ld32(sbase), s1w = ld32(sbase + 4), s2w = ld32(sbase + 8);
       scl0 = __builtin_amdgcn_alignbyte(s1w, s0w, sh);
       scl1 = __builtin_amdgcn_alignbyte(s2w, s1w, sh);
@@ -289,7 +277,7 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
 #pragma unroll
     for (int g = 0; g < 8; ++g) {
       if constexpr (kXs) {
-        const uint32_t w0 = ld32(gbase + 8 * g), w1 = ld32(gbase + 8 * g + 4), w2 = ld32(gbase + 8 * g + 8);
+        const uint32_t w0 = wq[2 * g], w1 = wq[2 * g + 1], w2 = wq[2 * g + 2];
         // this lane's 16 elements: entries 2kg, 2kg + 1 = one u16 pair
         const uint32_t ew = kg ? __builtin_amdgcn_alignbyte(w2, w1, sh) : __builtin_amdgcn_alignbyte(w1, w0, sh);
         const uint32_t e0 = ew & 0xffffu, e1 = ew >> 16;
@@ -318,7 +306,7 @@ __global__ void __launch_bounds__(kThreads, 1) iq2_mfma_gemm(GemmArgs a) {
           }
         continue;
       }
-      const uint32_t w0 = ld32(gbase + 8 * g), w1 = ld32(gbase + 8 * g + 4), w2 = ld32(gbase + 8 * g + 8);
+      const uint32_t w0 = wq[2 * g], w1 = wq[2 * g + 1], w2 = wq[2 * g + 2];
       const uint32_t idx = __builtin_amdgcn_alignbyte(w1, w0, sh);   // 4 grid indices
       const uint32_t meta = __builtin_amdgcn_alignbyte(w2, w1, sh);  // 4 x 7-bit signs, 4-bit s
       // this lane's 16 elements: grid entries l = 2kg, 2kg+1 (8 elements each)
@@ -409,11 +397,13 @@ template <bool kXs = false>
 bool gemm_iq2_ok(const uint8_t* W, const void* Xq, const float* Y, const int8_t* grid,
                  const int8_t* signs, size_t N, size_t K, size_t M, const RowStrides& st) {
   // MFMA path: prefill shapes with an even number of superblocks per row and
-  // 4-byte aligned weight rows; the GEMV kernels take everything else
+  // 4-byte aligned weight rows whose tile of 128 rows stays within 32-bit
+  // offsets; the GEMV kernels take everything else
   constexpr size_t kRec = Tile<kXs>::kRec;
   const size_t ldw = N > 1 ? st.ldw : K / 256 * kRec;
   return M >= 16 && N > 0 && K > 0 && K % 512 == 0 && W != nullptr && Xq != nullptr &&
          Y != nullptr && grid != nullptr && signs != nullptr && aligned(W, 4) && ldw % 4 == 0 &&
+         (kNT - 1) * ldw + K / 256 * kRec < ((size_t)1 << 32) &&
          aligned(Xq, 4) && aligned(Y, 4) && N <= (size_t)INT32_MAX && K <= (size_t)INT32_MAX &&
          M <= (size_t)INT32_MAX && strides_ok(st, K / 256 * kRec, 2, K, N, N, M) &&
          ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT) <= (size_t)INT32_MAX;
@@ -437,7 +427,8 @@ bool mul_mat_id_iq2_grouped_ok(bool xs, const uint8_t* W, size_t xq_bytes, const
   const size_t rb = K / 256 * (xs ? kIq2xsBytes : kIq2xxsBytes);
   const size_t ldw = N > 1 ? st.ldw : rb;
   return N > 0 && n_pairs > 0 && K > 0 && K % 512 == 0 && W != nullptr && Y != nullptr &&
-         grid != nullptr && signs != nullptr && aligned(W, 4) && ldw % 4 == 0 && aligned(Y, 4) &&
+         grid != nullptr && signs != nullptr && aligned(W, 4) && ldw % 4 == 0 &&
+         (kNT - 1) * ldw + rb < ((size_t)1 << 32) && aligned(Y, 4) &&
          xq_bytes < ((size_t)1 << 32) && aligned(ws, 16) && ws_bytes >= moe_group_bytes(n_pairs, pr.n_as) &&
          pr.w_es % 4 == 0 && pr.n_as <= kMaxExperts && N <= (size_t)INT32_MAX && K <= (size_t)INT32_MAX &&
          strides_ok(st, rb, 2, K, N, N, 1) &&
