@@ -24,8 +24,10 @@ timed three ways on the library's stream:
     caches, then one call between two events; median of 20;
   * ``graph_us``: the same back-to-back calls replayed from a captured HIP
     graph (launch cost of a serving loop that captures its steps).
-Floors measured in the same run: an empty launch back to back, and one
-streaming-read launch of the same weight bytes (library probes); for the
+Floors measured in the same run: an empty launch back to back, one
+streaming-read launch of the same bytes, and for the write-bound row
+dequantize one streaming-write launch of its output bytes (library
+probes); for the
 prefill shapes, the vendor's plain int8 GEMM (hipBLASLt through
 torch._int_mm) of the same M x N x K.  ``kernels`` lists what one call
 launched (the library's launch log).
@@ -338,14 +340,16 @@ class Bench:
         self._lib.check("graph replay")
         return start.elapsed_time(end) / 1e3 / (calls * replays)
 
-    def floors(self, nbytes_list, sweep_bytes):
+    def floors(self, nbytes_list, sweep_bytes, write_list=()):
         """Per-launch floors on this stream: an empty kernel back to back, and
         the fastest single streaming-read launch of each byte count.  For
         sweep_bytes the read probe is swept over every shape it has (threads
         per workgroup, 16-byte loads in flight per lane, nontemporal or not,
         grid-stride or one contiguous chunk per workgroup) and grid size; the
         other byte counts try the five best shapes of that sweep.  The best
-        shape is then timed like a case (median of the windows)."""
+        shape is then timed like a case (median of the windows).  For each
+        of write_list (a write-bound case's output bytes) the write probe is
+        swept the same way (1, 2 or 4 stores in flight per lane)."""
         torch = self.torch
         lib = self.lib
         out = {"empty_launch_us": round(self.time_calls(lambda i: lib.weft_hip_probe_empty(), 100, 20)[0] * 1e6, 3)}
@@ -376,6 +380,29 @@ class Bench:
             del bufs
             torch.cuda.empty_cache()
         out["stream_read"] = reads
+        writes = {}
+        for nbytes in write_list:
+            n16 = (nbytes + 15) // 16 * 16
+            copies = max(2, int(np.ceil(2 * MALL_BYTES / n16)) + 1)
+            bufs = [torch.empty(n16, dtype=torch.uint8, device=self.dev) for _ in range(copies)]
+            tried = []
+            for t in (256, 512, 1024):
+                for u in (1, 2, 4):
+                    for f in (0, 1, 2, 3):
+                        for grid in grids:
+                            sec = self.time_calls(lambda i: lib.weft_hip_probe_write_shape(
+                                bufs[i % copies].data_ptr(), n16, grid, t, u, f), 10, 3, windows=3)[0]
+                            tried.append((sec, (t, u, f), grid))
+            tried.sort()
+            _, (t, u, f), grid = tried[0]
+            sec = self.time_calls(lambda i: lib.weft_hip_probe_write_shape(
+                bufs[i % copies].data_ptr(), n16, grid, t, u, f), 20, 5)[0]
+            writes[str(nbytes)] = {"us": round(sec * 1e6, 3), "GBs": round(nbytes / sec / 1e9, 1),
+                                   "grid": grid, "threads": t, "unroll": u, "nontemporal": bool(f & 1),
+                                   "blocked": bool(f & 2), "launch_shapes_tried": len(tried)}
+            del bufs
+            torch.cuda.empty_cache()
+        out["stream_write"] = writes
         out["mfma_valu_ns_per_mfma"] = self.mfma_probe()
         return out
 
@@ -533,6 +560,7 @@ def run_case(b: Bench, name: str, steps: int, warmup: int, extra: bool) -> dict:
            "algorithmic_bytes": int(nbytes), "GBs": round(nbytes / sec / 1e9, 2),
            "weight_copies_rotated": copies, "kernels": kernels}
     if m == 0:
+        out["write_bytes"] = 4 * n * k  # the fp32 rows written
         out["output_copies_rotated"] = ycopies
         # the same calls writing one output buffer (180 MB at config 2, part
         # of which the Infinity Cache keeps between calls)
@@ -631,12 +659,17 @@ def main():
     floors = None
     if extra:
         byte_counts = sorted({v["algorithmic_bytes"] for v in results.values() if v.get("frac_hbm_peak")})
-        floors = b.floors(byte_counts, head["algorithmic_bytes"])
+        write_counts = sorted({v["write_bytes"] for v in results.values() if v.get("write_bytes")})
+        floors = b.floors(byte_counts, head["algorithmic_bytes"], write_counts)
         for v in results.values():
             read = floors["stream_read"].get(str(v["algorithmic_bytes"])) if v.get("frac_hbm_peak") else None
             if read is not None:
                 v["read_floor_us"] = read["us"]
                 v["vs_read_floor"] = round(v["us"] / read["us"], 3)
+            write = floors["stream_write"].get(str(v.get("write_bytes")))
+            if write is not None:
+                v["write_floor_us"] = write["us"]
+                v["vs_write_floor"] = round(v["us"] / write["us"], 3)
     if args.calibrate_copy:
         nb = args.calibrate_copy << 20
         src = b.torch.empty(nb, dtype=b.torch.uint8, device=b.dev)
@@ -681,6 +714,7 @@ def main():
             "empty_launch_us": floors["empty_launch_us"],
             "stream_read_headline": floors["stream_read"][str(head["algorithmic_bytes"])],
             "stream_read_us": {k: v["us"] for k, v in floors["stream_read"].items()},
+            "stream_write": floors["stream_write"],
             "mfma_valu_ns_per_mfma": floors["mfma_valu_ns_per_mfma"]},
         "adjacent": {name: brief(v) for name, v in results.items() if name not in labels},
         "configs": {labels[name]: results[name] for name in CASES if name in labels and name in results},

@@ -93,6 +93,12 @@ void weft_hip_probe_read(const void *src, size_t bytes, uint32_t *sink, int grid
  * grid * threads / 64 words.  weft_hip_probe_read is (512, 4, 0). */
 void weft_hip_probe_read_shape(const void *src, size_t bytes, uint32_t *sink, int grid, int threads,
                                int unroll, int flags);
+/* The write-side twin: writes `bytes` (a multiple of 16, 16-byte aligned) of
+ * device memory with 16-byte stores, `threads` per workgroup as above,
+ * `unroll` stores in flight per lane (1, 2 or 4), flags as above (bit 0:
+ * nontemporal stores).  No counterpart in the reference: the floor a
+ * write-bound kernel (row dequantize) is measured against. */
+void weft_hip_probe_write_shape(void *dst, size_t bytes, int grid, int threads, int unroll, int flags);
 /* Matrix-pipe probe: one workgroup per CU with `waves_per_simd` (1..4)
  * waves per SIMD, each running `iters` iterations of two
  * v_mfma_i32_32x32x32_i8 with `valu_per_mfma` (0, 4, 8, 12 or 16)

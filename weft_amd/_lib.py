@@ -75,6 +75,9 @@ def load() -> ctypes.CDLL:
             lib.weft_hip_probe_read_shape.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
                                                       ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]
             lib.weft_hip_probe_read_shape.restype = None
+            lib.weft_hip_probe_write_shape.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int,
+                                                       ctypes.c_int, ctypes.c_int]
+            lib.weft_hip_probe_write_shape.restype = None
             lib.weft_hip_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
             lib.weft_hip_probe_mfma.restype = None
             _bind_ggml(lib)

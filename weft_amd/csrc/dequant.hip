@@ -8,11 +8,13 @@
 // GGML regardless of contraction.  Q6_K's (d * sc) * q rounds at the second
 // product, which has no addend to contract with, so it is bit-exact too.
 //
-// HBM write-bound (Q4_K: 0.56 B read, 4 B written per element).  The mapping
-// is output-major: lane l of a wave writes elements 4l..4l+3 of a 256-element
-// span with one 16-byte store, so each wave store instruction covers 1 KB of
-// contiguous output.  The record bytes a lane needs are re-read by its
-// neighbours from L2/L1 (the records are 7x smaller than the output).
+// HBM-bound, mostly writes (Q4_K: 0.56 B read, 4 B written per element).
+// The mapping is output-major: lane l of a wave writes elements 4l..4l+3 of
+// a 256-element span with one 16-byte store, so each wave store instruction
+// covers 1 KB of contiguous output.  The record bytes a lane needs are
+// re-read by its neighbours from L2/L1 (the records are 7x smaller than the
+// output); Q4_K (config 2) instead stages whole chunks of records in LDS by
+// 16-byte direct loads (dq_q4k_lds_kernel).
 #include <algorithm>
 
 #include "runtime.h"
@@ -91,6 +93,79 @@ __global__ void __launch_bounds__(kThreads) dq_q4k_kernel(const uint8_t* __restr
       store4<Y16>(Y + (s0 + u) * 256 + 4 * lane, d1 * (float)(n & 0xff) - m1,
                   d1 * (float)((n >> 8) & 0xff) - m1, d1 * (float)((n >> 16) & 0xff) - m1,
                   d1 * (float)(n >> 24) - m1);
+    }
+  }
+}
+
+// Q4_K from LDS-staged chunks: a workgroup (4 waves) walks chunks of 64
+// superblocks (9216 record bytes), copying each with nine wave-wide 16-byte
+// direct loads -- whole cache lines, one request per 16 bytes -- into one of
+// two LDS buffers a chunk ahead, then each wave dequantizes 16 superblocks
+// from LDS (the header broadcast, the lane's nibble word) and writes them as
+// 16 KB of contiguous 16-byte nontemporal stores.  The small per-lane record
+// reads of dq_q4k_kernel interleaved with the write stream are what held
+// that kernel at ~1.5 x the streaming-write time of the output.
+typedef __attribute__((address_space(3))) void* dq_lds_ptr;
+constexpr int kDqChunk = 64;                        // superblocks per chunk
+constexpr int kDqChunkBytes = kDqChunk * kQ4_KBytes;  // 9216
+static_assert(kDqChunkBytes % 1024 == 0, "whole wave-wide loads");
+
+// 16 bytes per lane from g into LDS [lds + 16 lane, +16); the kernel waits
+// (s_waitcnt) itself
+__device__ __forceinline__ void dq_dma16(const uint8_t* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g)
+               : "memory", "m0");
+}
+
+__global__ void __launch_bounds__(kThreads) dq_q4k_lds_kernel(const uint8_t* __restrict__ W,
+                                                              float* __restrict__ Y, long long nsb) {
+  __shared__ __align__(16) uint8_t buf[2][kDqChunkBytes];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+  const int g = lane >> 4;
+  const int e = (lane & 15) * 4;
+  const int sub = 2 * g + (e >= 32);
+  const int qoff = 16 + 32 * g + (e & 31);
+  const int shift = e >= 32 ? 4 : 0;
+  const long long nchunks = (nsb + kDqChunk - 1) / kDqChunk;
+  const long long total = nsb * kQ4_KBytes;  // record bytes (a multiple of 16)
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(dq_lds_ptr)&buf[0][0]);
+  // chunk c's loads: wave w issues wave-wide loads i = w + 4 j (< 9); bytes
+  // past the last record re-read the last 16 (never used)
+  auto issue = [&](long long c, int slot) {
+    const long long base = c * kDqChunkBytes;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int i = wave + 4 * j;
+      if (i < kDqChunkBytes / 1024) {
+        const long long off = min(base + 1024 * i + 16 * lane, total - 16);
+        dq_dma16(W + off, lds0 + (uint32_t)(slot * kDqChunkBytes + 1024 * i));
+      }
+    }
+  };
+  long long c = blockIdx.x;
+  if (c < nchunks) issue(c, 0);
+  for (int k = 0; c < nchunks; c += gridDim.x, ++k) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // chunk c is in LDS for every wave; the other buffer is free
+    if (c + gridDim.x < nchunks) issue(c + gridDim.x, (k + 1) & 1);
+    const uint8_t* cb = buf[k & 1];
+#pragma unroll 4
+    for (int u = 0; u < kDqChunk / 4; ++u) {
+      const int sl = 16 * wave + u;
+      const long long sb = c * kDqChunk + sl;
+      if (sb >= nsb) break;
+      const uint4 h = *reinterpret_cast<const uint4*>(cb + kQ4_KBytes * sl);
+      const uint32_t qs = *reinterpret_cast<const uint32_t*>(cb + kQ4_KBytes * sl + qoff);
+      int sc, m;
+      q4k_scale_min(sub, h.y, h.z, h.w, sc, m);
+      const float d = fp16_to_fp32(h.x & 0xffffu), dmin = fp16_to_fp32(h.x >> 16);
+      const float d1 = d * (float)sc, m1 = dmin * (float)m;
+      const uint32_t n = (qs >> shift) & 0x0f0f0f0fu;
+      store4<true>(Y + sb * 256 + 4 * lane, d1 * (float)(n & 0xff) - m1, d1 * (float)((n >> 8) & 0xff) - m1,
+                   d1 * (float)((n >> 16) & 0xff) - m1, d1 * (float)(n >> 24) - m1);
     }
   }
 }
@@ -342,6 +417,16 @@ void row_dequantize_q4_k(const uint8_t* W, float* Y, size_t K) {
   constexpr int U = 4;
   const int g = grid_for((nsb + U - 1) / U);
   const bool w16 = aligned(W, 16), y16 = aligned(Y, 16);
+  if (aligned(W, 4) && y16) {
+    // LDS-staged chunks, two workgroups per CU (measured on config 2: 35.3 us
+    // against 44.6 for dq_q4k_kernel; 1 per CU 36.3, 3-16 per CU 36.8-38.6,
+    // each wave on chunks of its own 38.0)
+    const long long nchunks = (nsb + kDqChunk - 1) / kDqChunk;
+    const int gl = (int)std::max<long long>(1, std::min<long long>(nchunks, 2LL * cu_count()));
+    dq_q4k_lds_kernel<<<gl, kThreads, 0, current_stream()>>>(W, Y, nsb);
+    check_launch("dq_q4k_lds_kernel");
+    return;
+  }
   if (w16 && y16)
     dq_q4k_kernel<U, true, true><<<g, kThreads, 0, current_stream()>>>(W, Y, nsb);
   else if (y16)

@@ -272,6 +272,50 @@ __global__ void __launch_bounds__(1024) probe_mfma_kernel(int iters, uint32_t* _
   sink[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
+// Streaming write of n16 16-byte chunks, the store-side twin of
+// probe_read_kernel (same shapes); kNT: nontemporal stores.
+template <int U, bool kNT, bool kBlocked>
+__global__ void __launch_bounds__(1024) probe_write_kernel(v4u* __restrict__ dst, size_t n16, uint32_t tag) {
+  size_t first, end, stride;
+  if constexpr (kBlocked) {
+    const size_t chunk = (n16 + gridDim.x - 1) / gridDim.x;
+    first = (size_t)blockIdx.x * chunk + threadIdx.x;
+    end = min(n16, (size_t)(blockIdx.x + 1) * chunk);
+    stride = blockDim.x;
+  } else {
+    first = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    end = n16;
+    stride = (size_t)gridDim.x * blockDim.x;
+  }
+  for (size_t i = first; i < end; i += stride * U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const size_t j = i + u * stride;
+      const v4u v = {(uint32_t)j, tag, (uint32_t)j ^ tag, 0u};
+      if (j < end) {
+        if constexpr (kNT)
+          __builtin_nontemporal_store(v, dst + j);
+        else
+          dst[j] = v;
+      }
+    }
+  }
+}
+
+template <int U>
+bool launch_write_probe(bool nt, bool blocked, int grid, int threads, v4u* dst, size_t n16) {
+  hipStream_t s = current_stream();
+  if (nt && blocked)
+    probe_write_kernel<U, true, true><<<grid, threads, 0, s>>>(dst, n16, 0x5a5a5a5au);
+  else if (nt)
+    probe_write_kernel<U, true, false><<<grid, threads, 0, s>>>(dst, n16, 0x5a5a5a5au);
+  else if (blocked)
+    probe_write_kernel<U, false, true><<<grid, threads, 0, s>>>(dst, n16, 0x5a5a5a5au);
+  else
+    probe_write_kernel<U, false, false><<<grid, threads, 0, s>>>(dst, n16, 0x5a5a5a5au);
+  return true;
+}
+
 template <int U>
 bool launch_probe(bool nt, bool blocked, int grid, int threads, const v4u* src, size_t n16, uint32_t* sink) {
   hipStream_t s = current_stream();
@@ -315,6 +359,24 @@ void weft_hip_probe_read_shape(const void* src, size_t bytes, uint32_t* sink, in
     default: weft::set_error(hipErrorInvalidValue); return;
   }
   weft::check_launch("probe_read_kernel");
+}
+
+void weft_hip_probe_write_shape(void* dst, size_t bytes, int grid, int threads, int unroll, int flags) {
+  if (dst == nullptr || grid <= 0 || bytes % 16 != 0 || !weft::aligned(dst, 16) || threads <= 0 ||
+      threads > 1024 || threads % 64 != 0 || (flags & ~3) != 0) {
+    weft::set_error(hipErrorInvalidValue);
+    return;
+  }
+  auto* p = static_cast<weft::v4u*>(dst);
+  const bool nt = flags & 1, blocked = flags & 2;
+  const size_t n16 = bytes / 16;
+  switch (unroll) {
+    case 1: weft::launch_write_probe<1>(nt, blocked, grid, threads, p, n16); break;
+    case 2: weft::launch_write_probe<2>(nt, blocked, grid, threads, p, n16); break;
+    case 4: weft::launch_write_probe<4>(nt, blocked, grid, threads, p, n16); break;
+    default: weft::set_error(hipErrorInvalidValue); return;
+  }
+  weft::check_launch("probe_write_kernel");
 }
 
 void weft_hip_probe_mfma(int valu_per_mfma, int waves_per_simd, int iters, uint32_t* sink) {
