@@ -170,6 +170,154 @@ __global__ void __launch_bounds__(kThreads) dq_q4k_lds_kernel(const uint8_t* __r
   }
 }
 
+// The other formats staged the same way: a 256-value unit (8 Q4_0 / Q4_1 /
+// MXFP4 records, 4 NVFP4 records, one Q5_K / Q6_K superblock) per wave
+// step, lane l producing elements 4l..4l+3 from the unit's bytes in LDS with
+// the per-lane arithmetic of the kernels below (bit-identical results).
+struct DqTab {
+  const int8_t* codebook;
+  const float* scale;
+};
+struct DqQ40 {
+  static constexpr int kVals = 32, kRec = kQ4_0Bytes;
+  __device__ static float4 lane4(const uint8_t* u, int lane, const DqTab&) {
+    const int p = lane & 7, shift = p >= 4 ? 4 : 0;
+    const uint8_t* rec = u + (lane >> 3) * kRec;
+    const float d = fp16_to_fp32(ld_u16(rec));
+    const uint32_t qs = ld_u32_a2(rec + 2 + 4 * (p & 3));
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = (float)((int)((qs >> (8 * i + shift)) & 0xf) - 8) * d;
+    return make_float4(v[0], v[1], v[2], v[3]);
+  }
+};
+struct DqMx {
+  static constexpr int kVals = 32, kRec = kMxfp4Bytes;
+  __device__ static float4 lane4(const uint8_t* u, int lane, const DqTab& t) {
+    const int p = lane & 7, shift = p >= 4 ? 4 : 0;
+    const uint8_t* rec = u + (lane >> 3) * kRec;
+    const float d = t.scale[rec[0]];
+    const uint32_t qs = ld_u32_a1(rec + 1 + 4 * (p & 3));
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = (float)t.codebook[(qs >> (8 * i + shift)) & 0xf] * d;
+    return make_float4(v[0], v[1], v[2], v[3]);
+  }
+};
+struct DqQ41 {
+  static constexpr int kVals = 32, kRec = kQ4_1Bytes;
+  __device__ static float4 lane4(const uint8_t* u, int lane, const DqTab&) {
+#pragma clang fp contract(off)
+    const int p = lane & 7, shift = p >= 4 ? 4 : 0;
+    const uint8_t* rec = u + (lane >> 3) * kRec;
+    const float d = fp16_to_fp32(ld_u16(rec)), m = fp16_to_fp32(ld_u16(rec + 2));
+    const uint32_t qs = ld_u32_a2(rec + 4 + 4 * (p & 3));
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = (float)((qs >> (8 * i + shift)) & 0xf) * d + m;
+    return make_float4(v[0], v[1], v[2], v[3]);
+  }
+};
+struct DqNv {
+  static constexpr int kVals = 64, kRec = kNvfp4Bytes;
+  __device__ static float4 lane4(const uint8_t* u, int lane, const DqTab& t) {
+    const int p = lane & 15, s = p >> 2, shift = (p & 2) ? 4 : 0;
+    const uint8_t* rec = u + (lane >> 4) * kRec;
+    const float d = t.scale[rec[s]];
+    const uint32_t qs = ld_u32_a1(rec + 4 + 8 * s + 4 * (p & 1));
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = (float)t.codebook[(qs >> (8 * i + shift)) & 0xf] * d;
+    return make_float4(v[0], v[1], v[2], v[3]);
+  }
+};
+struct DqQ6K {
+  static constexpr int kVals = 256, kRec = kQ6_KBytes;
+  __device__ static float4 lane4(const uint8_t* rec, int lane, const DqTab&) {
+    const int e = 4 * lane, h = e >> 7, i = e & 127;
+    const uint32_t ql = ld_u32_a1(rec + 64 * h + (i & 63));
+    const uint32_t qh = ld_u32_a1(rec + 128 + 32 * h + (i & 31));
+    const int sc = (int)(int8_t)rec[192 + (e >> 4)];
+    const uint32_t dh = (uint32_t)rec[208] | ((uint32_t)rec[209] << 8);
+    const float dsc = fp16_to_fp32(dh) * (float)sc;
+    const uint32_t q = ((ql >> (4 * (i >> 6))) & 0x0f0f0f0fu) | (((qh >> (2 * (i >> 5))) & 0x03030303u) << 4);
+    return make_float4(dsc * (float)((int)(q & 0xff) - 32), dsc * (float)((int)((q >> 8) & 0xff) - 32),
+                       dsc * (float)((int)((q >> 16) & 0xff) - 32), dsc * (float)((int)(q >> 24) - 32));
+  }
+};
+struct DqQ5K {
+  static constexpr int kVals = 256, kRec = kQ5_KBytes;
+  __device__ static float4 lane4(const uint8_t* rec, int lane, const DqTab&) {
+    const int g = lane >> 4, e = (lane & 15) * 4, sub = 2 * g + (e >= 32);
+    const int shift = e >= 32 ? 4 : 0;
+    uint32_t hw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hw[i] = ld_u32_a2(rec + 4 * i);
+    const uint32_t qs = ld_u32_a2(rec + 48 + 32 * g + (e & 31)), qh = ld_u32_a2(rec + 16 + (e & 31));
+    int sc, m;
+    q4k_scale_min(sub, hw[1], hw[2], hw[3], sc, m);
+    const float d = fp16_to_fp32(hw[0] & 0xffffu), dmin = fp16_to_fp32(hw[0] >> 16);
+    const float d1 = d * (float)sc, m1 = dmin * (float)m;
+    const uint32_t n = ((qs >> shift) & 0x0f0f0f0fu) | (((qh >> sub) & 0x01010101u) << 4);
+    return make_float4(d1 * (float)(n & 0xff) - m1, d1 * (float)((n >> 8) & 0xff) - m1,
+                       d1 * (float)((n >> 16) & 0xff) - m1, d1 * (float)(n >> 24) - m1);
+  }
+};
+
+template <class F>
+__global__ void __launch_bounds__(kThreads) dq_chunk_kernel(const uint8_t* __restrict__ W, DqTab t,
+                                                            float* __restrict__ Y, long long K) {
+  constexpr int kUnit = 256 / F::kVals * F::kRec;               // bytes per 256 values
+  constexpr int kLoads = (kDqChunk * kUnit + 1023) / 1024;      // wave-wide loads per chunk
+  __shared__ __align__(16) uint8_t buf[2][kLoads * 1024];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+  const long long nunits = (K + 255) / 256;
+  const long long nchunks = (nunits + kDqChunk - 1) / kDqChunk;
+  const long long total = K / F::kVals * F::kRec;  // record bytes (a multiple of 4)
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(dq_lds_ptr)&buf[0][0]);
+  auto issue = [&](long long c, int slot) {
+    const long long base = c * kDqChunk * kUnit;
+#pragma unroll
+    for (int j = 0; j < (kLoads + 3) / 4; ++j) {
+      const int i = wave + 4 * j;
+      if (i < kLoads) {
+        const long long off = min(base + 1024 * i + 16 * lane, total - 16);  // past the end: re-read
+        dq_dma16(W + off, lds0 + (uint32_t)(slot * kLoads * 1024 + 1024 * i));
+      }
+    }
+  };
+  long long c = blockIdx.x;
+  if (c < nchunks) issue(c, 0);
+  for (int k = 0; c < nchunks; c += gridDim.x, ++k) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // chunk c is in LDS for every wave; the other buffer is free
+    if (c + gridDim.x < nchunks) issue(c + gridDim.x, (k + 1) & 1);
+    const uint8_t* cb = buf[k & 1];
+#pragma unroll 4
+    for (int u = 0; u < kDqChunk / 4; ++u) {
+      const int ul = 16 * wave + u;
+      const long long e0 = (c * kDqChunk + ul) * 256 + 4 * lane;
+      if (e0 >= K) break;  // K is a multiple of 32: a lane's four values are all in or all out
+      const float4 v = F::lane4(cb + kUnit * ul, lane, t);
+      store4<true>(Y + e0, v.x, v.y, v.z, v.w);
+    }
+  }
+}
+
+// The chunk kernel when W is 4-byte aligned (16-byte direct loads), Y
+// 16-byte aligned and the record bytes whole 16-byte chunks (no lane's 16
+// bytes straddle the end); false: the caller runs its per-lane kernel.
+template <class F>
+bool launch_dq_chunk(const uint8_t* W, DqTab t, float* Y, long long K) {
+  if (!aligned(W, 4) || !aligned(Y, 16) || (K / F::kVals * F::kRec) % 16 != 0) return false;
+  const long long nchunks = ((K + 255) / 256 + kDqChunk - 1) / kDqChunk;
+  const int g = (int)std::max<long long>(1, std::min<long long>(nchunks, 2LL * cu_count()));
+  dq_chunk_kernel<F><<<g, kThreads, 0, current_stream()>>>(W, t, Y, K);
+  check_launch("dq_chunk_kernel");
+  return true;
+}
+
 // Q4_0 / MXFP4: 8 lanes per 32-block, 8 blocks per wave step
 template <bool MX, bool Y16>
 __global__ void __launch_bounds__(kThreads) dq_32_kernel(const uint8_t* __restrict__ W,
@@ -442,6 +590,7 @@ void row_dequantize_nvfp4(const uint8_t* W, const int8_t* codebook, const float*
   if (K == 0) return;
   if (K % 64 || bad(W, 1, Y) || codebook == nullptr || scale == nullptr || !aligned(scale, 4))
     return set_error(hipErrorInvalidValue);
+  if (launch_dq_chunk<DqNv>(W, DqTab{codebook, scale}, Y, (long long)K)) return;
   const long long nb = (long long)(K / 64);
   const int g = grid_for((nb + 3) / 4);
   if (aligned(Y, 16))
@@ -455,6 +604,7 @@ void row_dequantize_q5_k(const uint8_t* W, float* Y, size_t K) {
   using namespace weft;
   if (K == 0) return;
   if (K % 256 || bad(W, 2, Y)) return set_error(hipErrorInvalidValue);
+  if (launch_dq_chunk<DqQ5K>(W, DqTab{nullptr, nullptr}, Y, (long long)K)) return;
   const long long nsb = (long long)(K / 256);
   constexpr int U = 4;
   const int g = grid_for((nsb + U - 1) / U);
@@ -469,6 +619,7 @@ void row_dequantize_q6_k(const uint8_t* W, float* Y, size_t K) {
   using namespace weft;
   if (K == 0) return;
   if (K % 256 || bad(W, 1, Y)) return set_error(hipErrorInvalidValue);
+  if (launch_dq_chunk<DqQ6K>(W, DqTab{nullptr, nullptr}, Y, (long long)K)) return;
   const long long nsb = (long long)(K / 256);
   constexpr int U = 4;
   const int g = grid_for((nsb + U - 1) / U);
@@ -483,6 +634,7 @@ void row_dequantize_q4_0(const uint8_t* W, float* Y, size_t K) {
   using namespace weft;
   if (K == 0) return;
   if (K % 32 || bad(W, 2, Y)) return set_error(hipErrorInvalidValue);
+  if (launch_dq_chunk<DqQ40>(W, DqTab{nullptr, nullptr}, Y, (long long)K)) return;
   const long long nb = (long long)(K / 32);
   const int g = grid_for((nb + 7) / 8);
   if (aligned(Y, 16))
@@ -498,6 +650,7 @@ void row_dequantize_mxfp4(const uint8_t* W, const int8_t* codebook, const float*
   if (K == 0) return;
   if (K % 32 || bad(W, 1, Y) || codebook == nullptr || scale == nullptr || !aligned(scale, 4))
     return set_error(hipErrorInvalidValue);
+  if (launch_dq_chunk<DqMx>(W, DqTab{codebook, scale}, Y, (long long)K)) return;
   const long long nb = (long long)(K / 32);
   const int g = grid_for((nb + 7) / 8);
   if (aligned(Y, 16))
@@ -525,6 +678,7 @@ void row_dequantize_q4_1(const uint8_t* W, float* Y, size_t K) {
   using namespace weft;
   if (K == 0) return;
   if (K % 32 || bad(W, 2, Y)) return set_error(hipErrorInvalidValue);
+  if (launch_dq_chunk<DqQ41>(W, DqTab{nullptr, nullptr}, Y, (long long)K)) return;
   const long long nb = (long long)(K / 32);
   const int g = grid_for((nb + 7) / 8);
   if (aligned(Y, 16))
