@@ -100,6 +100,22 @@ def test_dequant_misaligned_pointers(hip, fmt):
     _dequant_case(hip, fmt, 19, 512, w_off=1, y_off=1)
 
 
+@pytest.mark.parametrize("fmt", ["q4_0", "q4_1", "q4_k", "q5_k", "q6_k", "mxfp4", "nvfp4"])
+@pytest.mark.parametrize("n,k", [(40, 1024), (2050, 4096)])
+def test_dequant_staged_chunks(hip, fmt, n, k):
+    """The LDS-staged path (16-byte direct loads of 64-superblock chunks):
+    a weight base 4 bytes past a 16-byte boundary, a partial last chunk
+    (2.5 chunks; 512.5 chunks, more than one grid's worth, so one block
+    takes a second chunk), every output written and bit-exact."""
+    w = weights(fmt, n, k)
+    total = n * k
+    assert (w.nbytes % 16) == 0 and (total // 256) % 64 != 0
+    y = hip.empty(4 * total, fill=SENTINEL)
+    hip.call("row_dequantize_" + fmt, hip.to_dev(w, offset=4), *tables(hip, fmt), y, total)
+    want = o.dequantize(fmt, w, k).reshape(-1)
+    np.testing.assert_array_equal(y.numpy(np.float32).view(np.uint32), want.view(np.uint32))
+
+
 # ---------------------------------------------------------------- quantize
 def edge_rows(k: int) -> np.ndarray:
     """Known-hard blocks: exact .5 ties, all-zero, +-equal max, denormals,
