@@ -99,6 +99,10 @@ def _declare(l: ctypes.CDLL) -> None:
         "wo_max_threads": ([], ctypes.c_int),
         "wo_mul_mat_ggml": ([ctypes.c_int, _P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int], None),
         "wo_evict": ([_P, ctypes.c_size_t], None),
+        "wo_quantize_row_iq2_xxs_ggml": ([_P, _P, _I64, _P], None),
+        "wo_quantize_row_iq2_xs_ggml": ([_P, _P, _I64, _P], None),
+        "wo_iq2_grid_index": ([ctypes.c_int, ctypes.c_int], ctypes.c_int),
+        "wo_iq2_neighbours": ([ctypes.c_int, ctypes.c_int, _P], ctypes.c_int),
     }
     for fmt in ("q4_0", "q4_K", "mxfp4", "iq2_xxs", "q6_K", "q5_K", "nvfp4", "q8_0", "q8_K", "q4_1", "q8_1"):
         sig[f"wo_quantize_row_{fmt}"] = ([_P, _P, _I64], None)
@@ -207,6 +211,34 @@ def quantize(fmt: str, x: np.ndarray, out: np.ndarray | None = None) -> np.ndarr
     # one call over all rows: records never straddle rows
     fn(_ptr(x), _ptr(out), rows * k)
     return out
+
+
+def quantize_ggml_iq2(fmt: str, x: np.ndarray, importance: np.ndarray | None = None) -> np.ndarray:
+    """GGML's own IQ2_XXS / IQ2_XS weight quantizer (quantize_iq2_xxs /
+    quantize_iq2_xs, ggml-quants.c:3580-3602) on rows of fp32 ``x`` (..., K),
+    with an importance matrix of x's shape (None: all ones, as the
+    reference's repro passes, examples/repro/weft/mul_mat_runtime.cpp:762-776)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    k = x.shape[-1]
+    out = np.zeros(x.shape[:-1] + (record_bytes(fmt, k),), np.uint8)
+    qw = None
+    if importance is not None:
+        qw = np.ascontiguousarray(np.broadcast_to(importance, x.shape), dtype=np.float32)
+    fn = {"iq2_xxs": lib().wo_quantize_row_iq2_xxs_ggml, "iq2_xs": lib().wo_quantize_row_iq2_xs_ggml}[fmt]
+    fn(_ptr(x), _ptr(out), x.size, None if qw is None else _ptr(qw))
+    return out
+
+
+def iq2_grid_index(fmt: str, u: int) -> int:
+    """The grid entry of 2-bit point u in GGML's quantizer map (-1: off the grid)."""
+    return lib().wo_iq2_grid_index(int(fmt == "iq2_xs"), u)
+
+
+def iq2_neighbours(fmt: str, u: int) -> list[int]:
+    """The neighbour list iq2xs_init_impl builds for off-grid point u."""
+    out = np.zeros(512, np.uint16)
+    n = lib().wo_iq2_neighbours(int(fmt == "iq2_xs"), u, _ptr(out))
+    return [int(v) for v in out[:n]]
 
 
 def dequantize(fmt: str, w: np.ndarray, k: int) -> np.ndarray:

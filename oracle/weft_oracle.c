@@ -21,7 +21,10 @@
  */
 #include "weft_oracle.h"
 
+#include <float.h>
 #include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
 #include <string.h>
 #ifdef _OPENMP
 #include <omp.h>
@@ -517,10 +520,11 @@ void wo_quantize_row_q5_K(const float *x, uint8_t *y, int64_t k) {
   }
 }
 
-/* IQ2_XXS input generator.  NOT GGML's quantize_iq2_xxs: that one needs the
- * iq2xs_init_impl neighbour tables and an importance matrix
- * (ggml-quants.c:2781-3186, :3198-3398).  This one makes valid records of
- * the same distribution by exhaustive nearest-grid search: per 32-group an
+/* Fast IQ2_XXS input generator, beside GGML's own quantizer
+ * (wo_quantize_row_iq2_xxs_ggml below, which searches the iq2xs_init_impl
+ * neighbour tables with an importance matrix and is far slower).  This one
+ * makes valid records of the same distribution by exhaustive nearest-grid
+ * search: per 32-group an
  * amax-derived 4-bit scale, per 8-chunk the sign pattern of x with an even
  * number of minus signs (the smallest |x| is flipped when needed) and the
  * grid row with the least squared error.  Parity unpinned as a quantizer;
@@ -583,6 +587,485 @@ void wo_quantize_row_iq2_xxs(const float *x, uint8_t *y, int64_t k) {
       for (int b = 0; b < 4; ++b) qs[b] = (uint8_t)(idx_word >> (8 * b));
       for (int b = 0; b < 4; ++b) qs[4 + b] = (uint8_t)(meta >> (8 * b));
     }
+  }
+}
+
+/* ------------------------------------------------------------------------
+ * GGML's IQ2_XXS and IQ2_XS weight quantizers: quantize_iq2_xxs /
+ * quantize_iq2_xs (ggml-quants.c:3580-3602), one row at a time through
+ * quantize_row_iq2_xxs_impl (:3222-3398) and quantize_row_iq2_xs_impl
+ * (:3400-3578), with the search tables of iq2xs_init_impl (:2781-3186) and
+ * the helpers make_qp_quants (:1018-1085) and iq2_find_best_neighbour
+ * (:3198-3220).  The C is restated with its types: make_qp_quants keeps its
+ * levels in uint8_t, so the one negated value of an odd-sign 8-chunk wraps
+ * there exactly as in GGML.  GGML asserts an importance matrix; qw == NULL
+ * here means every importance is 1, the matrix the reference's repro passes
+ * (examples/repro/weft/mul_mat_runtime.cpp:762-776).
+ * ---------------------------------------------------------------------- */
+
+/* Search tables of one grid (iq2xs_init_impl): every 8-lane point u of
+ * 2-bit levels (lane i in bits 2i, 2i+1; 0 <= u < 43692) is either a grid
+ * entry (map[u] = its index) or has a neighbour list: the grid entries whose
+ * squared distance to u, taken on the odd integers 2l + 1 of both points,
+ * is one of the two smallest distances present, in order of (distance,
+ * index).  lists holds, per off-grid point, the count then the indices. */
+#define IQ2_KMAP 43692
+typedef struct {
+  int ngrid;
+  const uint16_t *codes;
+  int32_t map[IQ2_KMAP];
+  int32_t off[IQ2_KMAP];
+  uint16_t *lists;
+  int8_t pos[512][8];
+} Iq2Search;
+
+static Iq2Search g_iq2_search[2];
+static pthread_once_t g_iq2_once[2] = {PTHREAD_ONCE_INIT, PTHREAD_ONCE_INIT};
+
+static int iq2_distance(const int8_t a[8], const int8_t b[8]) {
+  int d2 = 0;
+  for (int k = 0; k < 8; ++k) d2 += (a[k] - b[k]) * (a[k] - b[k]);
+  return d2;
+}
+
+static void iq2_search_build(Iq2Search *s) {
+  for (int j = 0; j < s->ngrid; ++j)
+    for (int k = 0; k < 8; ++k) s->pos[j][k] = (int8_t)(2 * ((s->codes[j] >> (2 * k)) & 3) + 1);
+  for (int u = 0; u < IQ2_KMAP; ++u) s->map[u] = -1;
+  for (int j = 0; j < s->ngrid; ++j) s->map[s->codes[j]] = j;
+  /* pass 1: list lengths (the two smallest distances and how many entries
+   * lie at them), pass 2: the lists */
+  int64_t total = 0;
+  for (int u = 0; u < IQ2_KMAP; ++u) {
+    s->off[u] = -1;
+    if (s->map[u] >= 0) continue;
+    int8_t p[8];
+    for (int k = 0; k < 8; ++k) p[k] = (int8_t)(2 * ((u >> (2 * k)) & 3) + 1);
+    int d1 = INT32_MAX, d2 = INT32_MAX, n = 0;
+    for (int j = 0; j < s->ngrid; ++j) {
+      const int d = iq2_distance(p, s->pos[j]);
+      if (d < d1) {
+        d2 = d1;
+        d1 = d;
+      } else if (d > d1 && d < d2) {
+        d2 = d;
+      }
+    }
+    for (int j = 0; j < s->ngrid; ++j) {
+      const int d = iq2_distance(p, s->pos[j]);
+      n += d == d1 || d == d2;
+    }
+    s->off[u] = (int32_t)total;
+    total += 1 + n;
+  }
+  s->lists = (uint16_t *)malloc((size_t)total * sizeof(uint16_t));
+  for (int u = 0; u < IQ2_KMAP; ++u) {
+    if (s->off[u] < 0) continue;
+    int8_t p[8];
+    for (int k = 0; k < 8; ++k) p[k] = (int8_t)(2 * ((u >> (2 * k)) & 3) + 1);
+    int d1 = INT32_MAX, d2 = INT32_MAX;
+    for (int j = 0; j < s->ngrid; ++j) {
+      const int d = iq2_distance(p, s->pos[j]);
+      if (d < d1) {
+        d2 = d1;
+        d1 = d;
+      } else if (d > d1 && d < d2) {
+        d2 = d;
+      }
+    }
+    uint16_t *out = s->lists + s->off[u];
+    int n = 0;
+    for (int pass = 0; pass < 2; ++pass) { /* distance d1 first, then d2; ascending index in each */
+      const int want = pass == 0 ? d1 : d2;
+      if (pass == 1 && d2 == INT32_MAX) break;
+      for (int j = 0; j < s->ngrid; ++j)
+        if (iq2_distance(p, s->pos[j]) == want) out[1 + n++] = (uint16_t)j;
+    }
+    out[0] = (uint16_t)n;
+  }
+}
+
+static void iq2_search_init_xxs(void) {
+  g_iq2_search[0].ngrid = 256;
+  g_iq2_search[0].codes = kIq2xxsCodes;
+  iq2_search_build(&g_iq2_search[0]);
+}
+static void iq2_search_init_xs(void) {
+  g_iq2_search[1].ngrid = 512;
+  g_iq2_search[1].codes = kIq2xsCodes;
+  iq2_search_build(&g_iq2_search[1]);
+}
+
+static const Iq2Search *iq2_search(int xs) {
+  pthread_once(&g_iq2_once[xs], xs ? iq2_search_init_xs : iq2_search_init_xxs);
+  return &g_iq2_search[xs];
+}
+
+int wo_iq2_grid_index(int xs, int u) {
+  if (u < 0 || u >= IQ2_KMAP) return -2;
+  return iq2_search(xs != 0)->map[u];
+}
+
+int wo_iq2_neighbours(int xs, int u, uint16_t *out) {
+  if (u < 0 || u >= IQ2_KMAP) return -1;
+  const Iq2Search *s = iq2_search(xs != 0);
+  if (s->off[u] < 0) return 0;
+  const uint16_t *l = s->lists + s->off[u];
+  for (int i = 0; i < l[0]; ++i) out[i] = l[1 + i];
+  return l[0];
+}
+
+/* make_qp_quants, ggml-quants.c:1018-1085 */
+static float make_qp_quants(int n, int nmax, const float *x, uint8_t *L, const float *quant_weights) {
+  float max = 0;
+  for (int i = 0; i < n; ++i) max = max > x[i] ? max : x[i];
+  if (max < 1e-15f) {
+    for (int i = 0; i < n; ++i) L[i] = 0;
+    return 0.f;
+  }
+  float iscale = nmax / max;
+  for (int i = 0; i < n; ++i) L[i] = (uint8_t)nearest_int(iscale * x[i]);
+  float scale = 1 / iscale;
+  float best_mse = 0;
+  for (int i = 0; i < n; ++i) {
+    const float diff = x[i] - scale * L[i];
+    const float w = quant_weights[i];
+    best_mse += w * diff * diff;
+  }
+  for (int is = -4; is <= 4; ++is) {
+    if (is == 0) continue;
+    const float iscale_is = (0.1f * is + nmax) / max;
+    const float scale_is = 1 / iscale_is;
+    float mse = 0;
+    for (int i = 0; i < n; ++i) {
+      int l = nearest_int(iscale_is * x[i]);
+      l = l < nmax ? l : nmax;
+      const float diff = x[i] - scale_is * l;
+      const float w = quant_weights[i];
+      mse += w * diff * diff;
+    }
+    if (mse < best_mse) {
+      best_mse = mse;
+      iscale = iscale_is;
+    }
+  }
+  float sumlx = 0, suml2 = 0;
+  for (int i = 0; i < n; ++i) {
+    int l = nearest_int(iscale * x[i]);
+    l = l < nmax ? l : nmax;
+    L[i] = (uint8_t)l;
+    const float w = quant_weights[i];
+    sumlx += w * x[i] * l;
+    suml2 += w * l * l;
+  }
+  for (int itry = 0; itry < 5; ++itry) {
+    int n_changed = 0;
+    for (int i = 0; i < n; ++i) {
+      const float w = quant_weights[i];
+      float slx = sumlx - w * x[i] * L[i];
+      float sl2 = suml2 - w * L[i] * L[i];
+      if (slx > 0 && sl2 > 0) {
+        int new_l = nearest_int(x[i] * sl2 / slx);
+        new_l = new_l < nmax ? new_l : nmax;
+        if (new_l != L[i]) {
+          slx += w * x[i] * new_l;
+          sl2 += w * new_l * new_l;
+          if (slx * slx * suml2 > sumlx * sumlx * sl2) {
+            L[i] = (uint8_t)new_l;
+            sumlx = slx;
+            suml2 = sl2;
+            ++n_changed;
+          }
+        }
+      }
+    }
+    if (!n_changed) break;
+  }
+  return suml2 > 0.0f ? sumlx / suml2 : 0.0f;
+}
+
+/* iq2_find_best_neighbour, ggml-quants.c:3198-3220: the neighbour with the
+ * least weighted squared error at this scale (first one on ties) */
+static int iq2_best_neighbour(const Iq2Search *s, int u, const float *xval, const float *weight, float scale,
+                              int8_t *L) {
+  const uint16_t *nb = s->lists + s->off[u];
+  float best_d2 = FLT_MAX;
+  int grid_index = -1;
+  for (int j = 1; j <= nb[0]; ++j) {
+    const int8_t *pg = s->pos[nb[j]];
+    float d2 = 0;
+    for (int i = 0; i < 8; ++i) {
+      const float q = pg[i];
+      const float diff = scale * q - xval[i];
+      d2 += weight[i] * diff * diff;
+    }
+    if (d2 < best_d2) {
+      best_d2 = d2;
+      grid_index = nb[j];
+    }
+  }
+  const int8_t *pg = s->pos[grid_index];
+  for (int i = 0; i < 8; ++i) L[i] = (int8_t)((pg[i] - 1) / 2);
+  return grid_index;
+}
+
+/* the sign pattern of an 8-chunk with an even number of minus signs
+ * (ggml-quants.c:3260-3279): the least weighted x^2 of an odd pattern is
+ * negated in xval and its sign bit flipped; returns the 7 stored bits */
+static uint8_t iq2_chunk_signs(const float *xb, const float *weight, float *xval) {
+  int nflip = 0;
+  uint8_t s = 0;
+  for (int i = 0; i < 8; ++i) {
+    if (xb[i] >= 0) {
+      xval[i] = xb[i];
+    } else {
+      xval[i] = -xb[i];
+      ++nflip;
+      s |= (uint8_t)(1 << i);
+    }
+  }
+  if (nflip % 2) {
+    int imin = 0;
+    float min = weight[imin] * xb[imin] * xb[imin];
+    for (int i = 1; i < 8; ++i) {
+      const float ax = weight[i] * xb[i] * xb[i];
+      if (ax < min) {
+        min = ax;
+        imin = i;
+      }
+    }
+    xval[imin] = -xval[imin];
+    s ^= (uint8_t)(1 << imin);
+  }
+  return s & 127;
+}
+
+/* the 2-bit levels of 8 values at inverse scale id, clamped to [0, 2] */
+static uint16_t iq2_levels(const float *xval, float id, int8_t *L) {
+  uint16_t u = 0;
+  for (int i = 0; i < 8; ++i) {
+    int l = nearest_int(0.5f * (id * xval[i] - 1));
+    l = l < 0 ? 0 : (l > 2 ? 2 : l);
+    L[i] = (int8_t)l;
+    u |= (uint16_t)(l << 2 * i);
+  }
+  return u;
+}
+
+/* quantize_row_iq2_xxs_impl, ggml-quants.c:3222-3398 */
+void wo_quantize_row_iq2_xxs_ggml(const float *x, uint8_t *y, int64_t k, const float *quant_weights) {
+  const Iq2Search *s = iq2_search(0);
+  const int kMaxQ = 3;
+  const int64_t nbl = k / QK_K;
+#pragma omp parallel for schedule(dynamic, 16)
+  for (int64_t ibl = 0; ibl < nbl; ++ibl) {
+    float scales[QK_K / 32], weight[32], xval[32], waux[32], ones[32];
+    int8_t L[32], Laux[32];
+    uint8_t block_signs[4];
+    uint32_t q2[2 * (QK_K / 32)];
+    uint8_t *rec = y + ibl * IQ2_XXS_BYTES;
+    for (int i = 0; i < 32; ++i) ones[i] = 1.f;
+    wr16(rec, wo_fp32_to_fp16(0.f));
+    memset(q2, 0, sizeof q2);
+    float max_scale = 0;
+    const float *xbl = x + QK_K * ibl;
+    float sumx2 = 0;
+    for (int i = 0; i < QK_K; ++i) sumx2 += xbl[i] * xbl[i];
+    const float sigma2 = sumx2 / QK_K;
+    for (int ib = 0; ib < QK_K / 32; ++ib) {
+      const float *xb = xbl + 32 * ib;
+      const float *qw = quant_weights ? quant_weights + QK_K * ibl + 32 * ib : ones;
+      for (int i = 0; i < 32; ++i) weight[i] = qw[i] * sqrtf(sigma2 + xb[i] * xb[i]);
+      for (int i = 0; i < 32; ++i) waux[i] = sqrtf(weight[i]);
+      for (int c = 0; c < 4; ++c) block_signs[c] = iq2_chunk_signs(xb + 8 * c, weight + 8 * c, xval + 8 * c);
+      float max = xval[0];
+      for (int i = 1; i < 32; ++i) max = max > xval[i] ? max : xval[i];
+      if (max < 1e-15f) {
+        scales[ib] = 0;
+        memset(L, 0, 32);
+        continue;
+      }
+      float scale = make_qp_quants(32, kMaxQ + 1, xval, (uint8_t *)L, weight);
+      const float eff_max = scale * kMaxQ;
+      if (eff_max <= 0) {
+        scales[ib] = 0;
+        memset(L, 0, 32);
+        continue;
+      }
+      float best = 0;
+      for (int is = -6; is <= 6; ++is) {
+        const float id = (2 * kMaxQ - 1 + is * 0.1f) / eff_max;
+        const float this_scale = 1 / id;
+        for (int c = 0; c < 4; ++c) {
+          const uint16_t u = iq2_levels(xval + 8 * c, id, Laux + 8 * c);
+          if (s->map[u] < 0) iq2_best_neighbour(s, u, xval + 8 * c, waux + 8 * c, this_scale, Laux + 8 * c);
+        }
+        float sumqx = 0, sumq2 = 0;
+        for (int i = 0; i < 32; ++i) {
+          const float w = weight[i];
+          const float q = 2 * Laux[i] + 1;
+          sumqx += w * xval[i] * q;
+          sumq2 += w * q * q;
+        }
+        if (sumq2 > 0 && sumqx * sumqx > best * sumq2) {
+          scale = sumqx / sumq2;
+          best = scale * sumqx;
+          memcpy(L, Laux, 32);
+        }
+      }
+      if (scale > 0) {
+        const float id = 1 / scale;
+        for (int c = 0; c < 4; ++c) {
+          const uint16_t u = iq2_levels(xval + 8 * c, id, L + 8 * c);
+          const int gi = s->map[u] >= 0 ? s->map[u] : iq2_best_neighbour(s, u, xval + 8 * c, waux + 8 * c, scale, L + 8 * c);
+          for (int i = 0; i < 8; ++i) L[8 * c + i] = (int8_t)((s->pos[gi][i] - 1) / 2);
+        }
+        float sumqx = 0, sumq2 = 0;
+        for (int i = 0; i < 32; ++i) {
+          const float w = weight[i];
+          const float q = 2 * L[i] + 1;
+          sumqx += w * xval[i] * q;
+          sumq2 += w * q * q;
+        }
+        if (sumq2 > 0) scale = sumqx / sumq2;
+      }
+      if (scale < 0) {
+        scale = -scale;
+        for (int c = 0; c < 4; ++c) block_signs[c] = (uint8_t)(~block_signs[c] & 127);
+      }
+      for (int c = 0; c < 4; ++c) {
+        uint16_t u = 0;
+        for (int i = 0; i < 8; ++i) u |= (uint16_t)(L[8 * c + i] << 2 * i);
+        const int gi = s->map[u]; /* on the grid by construction (GGML aborts otherwise) */
+        q2[2 * ib + 0] |= (uint32_t)gi << 8 * c;
+        q2[2 * ib + 1] |= (uint32_t)block_signs[c] << 7 * c;
+      }
+      scales[ib] = scale;
+      max_scale = max_scale > scale ? max_scale : scale;
+    }
+    if (!max_scale) {
+      memset(rec + 2, 0, QK_K / 4);
+      continue;
+    }
+    const float d = max_scale / 31;
+    wr16(rec, wo_fp32_to_fp16(d));
+    const float id = 1 / d;
+    for (int ib = 0; ib < QK_K / 32; ++ib) {
+      int l = nearest_int(0.5f * (id * scales[ib] - 1));
+      l = l < 0 ? 0 : (l > 15 ? 15 : l);
+      q2[2 * ib + 1] |= (uint32_t)l << 28;
+    }
+    for (int w = 0; w < 16; ++w)
+      for (int b = 0; b < 4; ++b) rec[2 + 4 * w + b] = (uint8_t)(q2[w] >> (8 * b));
+  }
+}
+
+/* quantize_row_iq2_xs_impl, ggml-quants.c:3400-3578 */
+void wo_quantize_row_iq2_xs_ggml(const float *x, uint8_t *y, int64_t k, const float *quant_weights) {
+  const Iq2Search *s = iq2_search(1);
+  const int kMaxQ = 3;
+  const int64_t nbl = k / QK_K;
+#pragma omp parallel for schedule(dynamic, 16)
+  for (int64_t ibl = 0; ibl < nbl; ++ibl) {
+    float scales[QK_K / 16], weight[16], xval[16], waux[16], ones[16];
+    int8_t L[16], Laux[16];
+    int on_grid[2], on_grid_aux[2];
+    uint8_t block_signs[2];
+    uint16_t q2[2 * (QK_K / 16)];
+    uint8_t *rec = y + ibl * IQ2_XS_BYTES;
+    for (int i = 0; i < 16; ++i) ones[i] = 1.f;
+    wr16(rec, wo_fp32_to_fp16(0.f));
+    memset(q2, 0, sizeof q2);
+    memset(rec + 2 + QK_K / 4, 0, QK_K / 32);
+    float max_scale = 0;
+    const float *xbl = x + QK_K * ibl;
+    float sumx2 = 0;
+    for (int i = 0; i < QK_K; ++i) sumx2 += xbl[i] * xbl[i];
+    const float sigma2 = sumx2 / QK_K;
+    for (int ib = 0; ib < QK_K / 16; ++ib) {
+      const float *xb = xbl + 16 * ib;
+      const float *qw = quant_weights ? quant_weights + QK_K * ibl + 16 * ib : ones;
+      for (int i = 0; i < 16; ++i) weight[i] = qw[i] * sqrtf(sigma2 + xb[i] * xb[i]);
+      for (int i = 0; i < 16; ++i) waux[i] = sqrtf(weight[i]);
+      for (int c = 0; c < 2; ++c) block_signs[c] = iq2_chunk_signs(xb + 8 * c, weight + 8 * c, xval + 8 * c);
+      float max = xval[0];
+      for (int i = 1; i < 16; ++i) max = max > xval[i] ? max : xval[i];
+      memset(L, 0, 16);
+      if (max < 1e-15f) {
+        scales[ib] = 0;
+        continue;
+      }
+      float best = 0;
+      float scale = max / (2 * kMaxQ - 1);
+      on_grid[0] = on_grid[1] = 1;
+      for (int is = -9; is <= 9; ++is) {
+        const float id = (2 * kMaxQ - 1 + is * 0.1f) / max;
+        const float this_scale = 1 / id;
+        for (int c = 0; c < 2; ++c) {
+          const uint16_t u = iq2_levels(xval + 8 * c, id, Laux + 8 * c);
+          on_grid_aux[c] = s->map[u] >= 0;
+          if (!on_grid_aux[c]) iq2_best_neighbour(s, u, xval + 8 * c, waux + 8 * c, this_scale, Laux + 8 * c);
+        }
+        float sumqx = 0, sumq2 = 0;
+        for (int i = 0; i < 16; ++i) {
+          const float w = weight[i];
+          const float q = 2 * Laux[i] + 1;
+          sumqx += w * xval[i] * q;
+          sumq2 += w * q * q;
+        }
+        if (sumq2 > 0 && sumqx * sumqx > best * sumq2) {
+          scale = sumqx / sumq2;
+          best = scale * sumqx;
+          memcpy(L, Laux, 16);
+          on_grid[0] = on_grid_aux[0];
+          on_grid[1] = on_grid_aux[1];
+        }
+      }
+      if ((!on_grid[0] || !on_grid[1]) && scale > 0) {
+        const float id = 1 / scale;
+        for (int c = 0; c < 2; ++c) {
+          if (on_grid[c]) continue;
+          const uint16_t u = iq2_levels(xval + 8 * c, id, L + 8 * c);
+          if (s->map[u] < 0) iq2_best_neighbour(s, u, xval + 8 * c, waux + 8 * c, scale, L + 8 * c);
+        }
+        float sumqx = 0, sumq2 = 0;
+        for (int i = 0; i < 16; ++i) {
+          const float w = weight[i];
+          const float q = 2 * L[i] + 1;
+          sumqx += w * xval[i] * q;
+          sumq2 += w * q * q;
+        }
+        if (sumq2 > 0) scale = sumqx / sumq2;
+      }
+      if (scale < 0) {
+        scale = -scale;
+        for (int c = 0; c < 2; ++c) block_signs[c] = (uint8_t)(~block_signs[c] & 127);
+      }
+      for (int c = 0; c < 2; ++c) {
+        uint16_t u = 0;
+        for (int i = 0; i < 8; ++i) u |= (uint16_t)(L[8 * c + i] << 2 * i);
+        q2[2 * ib + c] = (uint16_t)(s->map[u] | (block_signs[c] << 9));
+      }
+      scales[ib] = scale;
+      max_scale = max_scale > scale ? max_scale : scale;
+    }
+    if (!max_scale) {
+      memset(rec + 2, 0, QK_K / 4);
+      continue;
+    }
+    const float d = max_scale / 31;
+    wr16(rec, wo_fp32_to_fp16(d));
+    const float id = 1 / d;
+    uint8_t *sc = rec + 2 + QK_K / 4;
+    for (int ib = 0; ib < QK_K / 16; ++ib) {
+      int l = nearest_int(0.5f * (id * scales[ib] - 1));
+      l = l < 0 ? 0 : (l > 15 ? 15 : l);
+      if (ib % 2 == 0)
+        sc[ib / 2] = (uint8_t)l;
+      else
+        sc[ib / 2] |= (uint8_t)(l << 4);
+    }
+    for (int w = 0; w < 32; ++w) wr16(rec + 2 + 2 * w, q2[w]);
   }
 }
 

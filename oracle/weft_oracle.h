@@ -62,6 +62,15 @@ void wo_quantize_row_q4_0(const float *x, uint8_t *y, int64_t k);
 void wo_quantize_row_q4_K(const float *x, uint8_t *y, int64_t k);
 void wo_quantize_row_mxfp4(const float *x, uint8_t *y, int64_t k);
 void wo_quantize_row_iq2_xxs(const float *x, uint8_t *y, int64_t k);
+/* GGML's quantize_iq2_xxs / quantize_iq2_xs (ggml-quants.c:3580-3602):
+ * quant_weights = the importance matrix (k values), NULL = all ones */
+void wo_quantize_row_iq2_xxs_ggml(const float *x, uint8_t *y, int64_t k, const float *quant_weights);
+void wo_quantize_row_iq2_xs_ggml(const float *x, uint8_t *y, int64_t k, const float *quant_weights);
+/* the search tables of iq2xs_init_impl (xs: 0 = IQ2_XXS, 1 = IQ2_XS): the
+ * grid index of 2-bit point u (-1: not on the grid), and its neighbour list
+ * (returns the count written to out, 0 for a grid point) */
+int wo_iq2_grid_index(int xs, int u);
+int wo_iq2_neighbours(int xs, int u, uint16_t *out);
 void wo_quantize_row_q6_K(const float *x, uint8_t *y, int64_t k);
 void wo_quantize_row_q5_K(const float *x, uint8_t *y, int64_t k);
 void wo_quantize_row_nvfp4(const float *x, uint8_t *y, int64_t k);

@@ -28,11 +28,12 @@ NAN = 0x7FC00001  # a quiet NaN the kernels never produce
 
 
 def make_weights(fmt, n, k, seed):
-    """GGML-quantized N(0, 0.02) rows; IQ2_XS (no quantizer restated) as
-    random records."""
-    if fmt == "iq2_xs":
-        return o.random_records(fmt, n, k, seed=seed)
-    return o.quantize(fmt, o.seeded_normal(seed, (n, k), 0.02))
+    """GGML-quantized N(0, 0.02) rows (the IQ2 formats by GGML's own
+    quantize_iq2_xxs / quantize_iq2_xs, unit importance)."""
+    x = o.seeded_normal(seed, (n, k), 0.02)
+    if fmt in ("iq2_xs", "iq2_xxs"):
+        return o.quantize_ggml_iq2(fmt, x)
+    return o.quantize(fmt, x)
 
 
 def run(hip, fmt, k, n, m, planes0=(1, 1), planes1=(1, 1), pad_w=0, pad_x=0, pad_y=0,

@@ -2,12 +2,14 @@
 through the C ABI on the GPU, against the pinned oracle: row dequantize
 bit-exact, vec_dot and mul_mat within the fp64 re-accumulation bar, the Xq
 workspace bit-exact Q8_K.  Weights are random records with a moderate fp16
-d (GGML's IQ2_XS quantizer, an importance-weighted grid search, is not
-restated; every byte pattern is a valid record), plus records with both
-scale nibbles at 0 and 15 and d = 0, and corner records (grid and sign
-indices at 0 and at their maxima, subnormal and large d) for the MFMA GEMM
-and the batch-1 kernel."""
+d (every byte pattern is a valid record, so every grid and sign index
+occurs), records with both scale nibbles at 0 and 15 and d = 0, corner
+records (grid and sign indices at 0 and at their maxima, subnormal and
+large d) for the MFMA GEMM and the batch-1 kernel, and records from GGML's
+own quantize_iq2_xs as restated in oracle/."""
 from __future__ import annotations
+
+import functools
 
 import numpy as np
 import pytest
@@ -63,6 +65,21 @@ def test_mul_mat_iq2_xs(hip, symbol, n, k, m):
     w = weights(n, k)
     w, x, xq, y = run_mul_mat(hip, symbol, "iq2_xs", n, k, m, w=w)
     check_mul_mat("iq2_xs", w, x, xq, y, n, k, m)
+
+
+@pytest.mark.parametrize("symbol", ["production_mul_mat_iq2_xs", "production_mul_mat_iq2_xs_staged"])
+@pytest.mark.parametrize("n,k,m", [(4096, 4096, 1), (4096, 4096, 512), (300, 1536, 70)])
+def test_mul_mat_iq2_xs_ggml_quantized(hip, symbol, n, k, m):
+    """Records from GGML's own quantize_iq2_xs (unit importance) of N(0, 0.02)
+    rows, through the batch-1 kernel, the MFMA GEMM and the staged GEMV."""
+    w = ggml_weights(n, k)
+    w, x, xq, y = run_mul_mat(hip, symbol, "iq2_xs", n, k, m, w=w)
+    check_mul_mat("iq2_xs", w, x, xq, y, n, k, m)
+
+
+@functools.lru_cache(maxsize=None)
+def ggml_weights(n, k, seed=5):
+    return o.quantize_ggml_iq2("iq2_xs", o.seeded_normal(seed, (n, k), 0.02))
 
 
 def test_ggml_mul_mat_iq2_xs(hip):

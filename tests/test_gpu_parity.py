@@ -26,8 +26,11 @@ SENTINEL = 0xA5
 
 @functools.lru_cache(maxsize=None)
 def weights(fmt: str, n: int, k: int, seed: int = 1) -> np.ndarray:
+    """GGML-quantized N(0, 0.02) rows; IQ2_XXS by GGML's own quantize_iq2_xxs
+    with unit importance, as the reference's repro builds its records
+    (examples/repro/weft/mul_mat_runtime.cpp:762-776)."""
     w = o.seeded_normal(seed, (n, k), 0.02)
-    return o.quantize(fmt, w)
+    return o.quantize_ggml_iq2(fmt, w) if fmt == "iq2_xxs" else o.quantize(fmt, w)
 
 
 @functools.lru_cache(maxsize=None)
