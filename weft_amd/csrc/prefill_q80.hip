@@ -326,170 +326,180 @@ __device__ __forceinline__ void q80_gemm_body(const GemmArgs& a, uint8_t* lds) {
   const int npair = (nst + 1) >> 1;
   const int sw = col & 15;
 
+  // Blocks J0 .. J0 + 3 of this wave's stage of the pair in `cur`.
+  auto half = [&](int pair, const uint8_t* cur, auto j0_tag) {
+    constexpr int J0 = decltype(j0_tag)::value;
+    const uint8_t* stage = cur + par * kStage;
+    const uint8_t* AQ = stage;
+    const uint8_t* wrow = stage + kAQ + (32 * wcol + col) * rl;
+    const float* dxs = &adt[pair & 1][par][0];
+    const uint16_t* sxs = &ast[pair & 1][par][0];
+    // Q4_0: the row's 144 stage bytes as nine 16-byte LDS reads (the 36-dword
+    // stride puts 16 lanes' 16-byte reads on all 64 banks); every record is
+    // then taken from registers at fixed offsets
+    uint32_t wq[F == WFmt::Q4_0 ? 36 : 1];
+    if constexpr (F == WFmt::Q4_0) {
+#pragma unroll
+      for (int i = 0; i < 9; ++i) {
+        // this half's records (and the dword before a record's nibbles
+        // holding its scale) lie in bytes [18 J0, 18 J0 + 72)
+        if (16 * i >= 18 * J0 + 72 || 16 * i + 16 <= 18 * J0) continue;
+        const uint4 v = *reinterpret_cast<const uint4*>(wrow + 16 * i);
+        wq[4 * i] = v.x, wq[4 * i + 1] = v.y, wq[4 * i + 2] = v.z, wq[4 * i + 3] = v.w;
+      }
+    }
+    auto wld = [&](int byte) -> uint32_t {  // the row's aligned dword at `byte`
+      if constexpr (F == WFmt::Q4_0)
+        return wq[byte >> 2];
+      else
+        return ld32(wrow + byte);
+    };
+#pragma unroll
+    for (int j = J0; j < J0 + 4; ++j) {
+      if constexpr (F == WFmt::NVFP4) {
+        // block j is half j % 2 of record j / 2: sub-blocks 2 (j % 2) + kg;
+        // this lane's 16 elements are the low nibbles of its sub-block's 8
+        // code bytes, then their high nibbles
+        const uint8_t* rec = wrow + 36 * (j >> 1);
+        const uint32_t sc4 = ld32(rec);
+        const uint32_t u0 = ld32(rec + 4 + 16 * (j & 1) + 8 * kg), u1 = ld32(rec + 8 + 16 * (j & 1) + 8 * kg);
+        const float wlo = scl[(sc4 >> (16 * (j & 1))) & 0xffu], whi = scl[(sc4 >> (16 * (j & 1) + 8)) & 0xffu];
+        const v4i bv = {(int)lookup16(u0 & 0x0f0f0f0fu, c0, c1, c2, c3),
+                        (int)lookup16(u1 & 0x0f0f0f0fu, c0, c1, c2, c3),
+                        (int)lookup16((u0 >> 4) & 0x0f0f0f0fu, c0, c1, c2, c3),
+                        (int)lookup16((u1 >> 4) & 0x0f0f0f0fu, c0, c1, c2, c3)};
+        const v4i bz = {};
+        const int chunk = (2 * j + kg) ^ sw;
+        v16i I2[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const v4i av = *reinterpret_cast<const v4i*>(AQ + (32 * t + col) * 256 + 16 * chunk);
+          I[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, kg ? bz : bv, zero, 0, 0, 0);
+          I2[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, kg ? bv : bz, zero, 0, 0, 0);
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const float4 d4 = *reinterpret_cast<const float4*>(dxs + j * kMT + 32 * t + 8 * r4 + 4 * kg);
+            const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int r = 4 * r4 + q;
+              y[t][r] += dv[q] * (wlo * (float)I[t][r] + whi * (float)I2[t][r]);
+            }
+          }
+        continue;
+      }
+      // raw record j of this lane's weight row: header, then 16 nibble bytes
+      const int off = T::kRec * j + T::kHdr;  // first nibble byte
+      const int sh = off & 3, b4 = off - sh;
+      uint32_t w0 = wld(b4), w1 = wld(b4 + 4), w2 = wld(b4 + 8), w3 = wld(b4 + 12);
+      uint32_t q0 = w0, q1 = w1, q2 = w2, q3 = w3;
+      if (sh) {
+        const uint32_t w4 = wld(b4 + 16);
+        q0 = __builtin_amdgcn_alignbyte(w1, w0, sh);
+        q1 = __builtin_amdgcn_alignbyte(w2, w1, sh);
+        q2 = __builtin_amdgcn_alignbyte(w3, w2, sh);
+        q3 = __builtin_amdgcn_alignbyte(w4, w3, sh);
+      }
+      // header byte(s) just before the nibbles
+      float wsc = 0.f;
+      uint32_t wbits = 0;  // Q4_0 / Q4_1: the fp16 scale's bits
+      if constexpr (F == WFmt::Q4_1) {
+        const uint32_t hd = ld32(wrow + T::kRec * j);  // records are 4-byte aligned here
+        wbits = hd & 0xffffu;
+      } else if constexpr (F == WFmt::Q4_0) {
+        wbits = sh >= 2 ? (w0 & 0xffffu) : (wld(b4 - 4) >> 16);
+      } else {
+        const uint32_t e = sh >= 1 ? ((w0 >> (8 * (sh - 1))) & 0xffu) : (ld32(wrow + b4 - 4) >> 24);
+        wsc = scl[e];
+      }
+      const uint32_t shn = 4 * kg;  // kg 0: elements 0..15 (low nibbles), 1: 16..31 (high)
+      uint32_t n[4] = {(q0 >> shn) & 0x0f0f0f0fu, (q1 >> shn) & 0x0f0f0f0fu,
+                       (q2 >> shn) & 0x0f0f0f0fu, (q3 >> shn) & 0x0f0f0f0fu};
+      v4i bv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (F == WFmt::Q4_0)
+          bv[i] = (int)(((n[i] | 0x80808080u) - 0x08080808u) ^ 0x80808080u);  // q - 8 per byte
+        else if constexpr (F == WFmt::Q4_1)
+          bv[i] = (int)n[i];  // q in 0..15
+        else
+          bv[i] = (int)lookup16(n[i], c0, c1, c2, c3);
+      }
+      const int chunk = (2 * j + kg) ^ sw;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const v4i av = *reinterpret_cast<const v4i*>(AQ + (32 * t + col) * 256 + 16 * chunk);
+        I[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, zero, 0, 0, 0);
+      }
+      if constexpr (F == WFmt::Q4_0 || F == WFmt::Q4_1) {
+        // y += (dx dw) I with the factor dx dw of every output from one f16
+        // MFMA per tile as an outer product: K slot 0 holds the token's dx
+        // and the row's dw (both fp16, so each product is exact in fp32,
+        // as the VALU product it replaces), every other slot 0
+        // (operands as raw bits: the kg half's slots are zero without a branch)
+        const uint32_t kmask = kg ? 0u : 0xffffu;
+        const v2u bq = {wbits & kmask, 0u};
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const _Float16 dxh = (_Float16)dxs[j * kMT + 32 * t + col];
+          const v2u aq = {(uint32_t)__builtin_bit_cast(uint16_t, dxh) & kmask, 0u};
+          const v16f qd = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, aq), __builtin_bit_cast(v4h, bq),
+                                                              fzero, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) y[t][r] = fmaf(qd[r], (float)I[t][r], y[t][r]);
+        }
+        // keep the blocks' factor MFMAs in block order (hoisted, their
+        // results would hold registers across the whole stage)
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+        // y += (dx * ws) * I; register r of a tile holds token 8*(r/4) + 4*kg + r%4
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const float4 d4 = *reinterpret_cast<const float4*>(dxs + j * kMT + 32 * t + 8 * r4 + 4 * kg);
+            const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int r = 4 * r4 + q;
+              y[t][r] += (dv[q] * wsc) * (float)I[t][r];
+            }
+          }
+      }
+    }
+    if constexpr (F == WFmt::Q4_1 && J0 == 4) {
+      // Q4_1's min term, m s per block (ggml-cpu/quants.c:241), for the
+      // stage's eight blocks at once: one f16 MFMA per tile (K = 8 blocks)
+      // of the tokens' fp16 block sums against the rows' fp16 mins, added
+      // into y.  Both are fp16, so every product is exact in fp32.
+      const uint8_t* mrec = wrow + T::kRec * 4 * kg;  // blocks 4 kg .. 4 kg + 3 of this lane's row
+      const uint32_t h0 = ld32(mrec), h1 = ld32(mrec + T::kRec), h2 = ld32(mrec + 2 * T::kRec),
+                     h3 = ld32(mrec + 3 * T::kRec);
+      const uint2 bm = make_uint2(__builtin_amdgcn_perm(h1, h0, 0x07060302u), __builtin_amdgcn_perm(h3, h2, 0x07060302u));
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint2 am = *reinterpret_cast<const uint2*>(sxs + 8 * (32 * t + col) + 4 * kg);
+        y[t] = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, am), __builtin_bit_cast(v4h, bm), y[t],
+                                                   0, 0, 0);
+      }
+    }
+  };
+  // A pair: the stage's first four blocks, then this wave's share of the
+  // next pair's direct loads, then the last four.  Issued right after the
+  // barrier, every wave's first block waited behind the workgroup's queued
+  // loads (the MXFP4 GEMM measured 39.5 -> 37.8 us per call for the move).
   auto step = [&](int pair, const uint8_t* cur, uint8_t* nxt) {
     __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of this pair have landed
     __syncthreads();                // everyone's; the previous pair is consumed
     const bool refill = pair + 1 < npair;
-    if (refill) {
-      issue(pair + 1, nxt);
-      if (wcol == 0) load_dx(pair + 1);
-    }
-    if (2 * pair + par < nst) {
-      const uint8_t* stage = cur + par * kStage;
-      const uint8_t* AQ = stage;
-      const uint8_t* wrow = stage + kAQ + (32 * wcol + col) * rl;
-      const float* dxs = &adt[pair & 1][par][0];
-      const uint16_t* sxs = &ast[pair & 1][par][0];
-      // Q4_0: the row's 144 stage bytes as nine 16-byte LDS reads (the 36-dword
-      // stride puts 16 lanes' 16-byte reads on all 64 banks); every record is
-      // then taken from registers at fixed offsets
-      uint32_t wq[F == WFmt::Q4_0 ? 36 : 1];
-      if constexpr (F == WFmt::Q4_0) {
-#pragma unroll
-        for (int i = 0; i < 9; ++i) {
-          const uint4 v = *reinterpret_cast<const uint4*>(wrow + 16 * i);
-          wq[4 * i] = v.x, wq[4 * i + 1] = v.y, wq[4 * i + 2] = v.z, wq[4 * i + 3] = v.w;
-        }
-      }
-      auto wld = [&](int byte) -> uint32_t {  // the row's aligned dword at `byte`
-        if constexpr (F == WFmt::Q4_0)
-          return wq[byte >> 2];
-        else
-          return ld32(wrow + byte);
-      };
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if constexpr (F == WFmt::NVFP4) {
-          // block j is half j % 2 of record j / 2: sub-blocks 2 (j % 2) + kg;
-          // this lane's 16 elements are the low nibbles of its sub-block's 8
-          // code bytes, then their high nibbles
-          const uint8_t* rec = wrow + 36 * (j >> 1);
-          const uint32_t sc4 = ld32(rec);
-          const uint32_t u0 = ld32(rec + 4 + 16 * (j & 1) + 8 * kg), u1 = ld32(rec + 8 + 16 * (j & 1) + 8 * kg);
-          const float wlo = scl[(sc4 >> (16 * (j & 1))) & 0xffu], whi = scl[(sc4 >> (16 * (j & 1) + 8)) & 0xffu];
-          const v4i bv = {(int)lookup16(u0 & 0x0f0f0f0fu, c0, c1, c2, c3),
-                          (int)lookup16(u1 & 0x0f0f0f0fu, c0, c1, c2, c3),
-                          (int)lookup16((u0 >> 4) & 0x0f0f0f0fu, c0, c1, c2, c3),
-                          (int)lookup16((u1 >> 4) & 0x0f0f0f0fu, c0, c1, c2, c3)};
-          const v4i bz = {};
-          const int chunk = (2 * j + kg) ^ sw;
-          v16i I2[2];
-#pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            const v4i av = *reinterpret_cast<const v4i*>(AQ + (32 * t + col) * 256 + 16 * chunk);
-            I[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, kg ? bz : bv, zero, 0, 0, 0);
-            I2[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, kg ? bv : bz, zero, 0, 0, 0);
-          }
-#pragma unroll
-          for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4) {
-              const float4 d4 = *reinterpret_cast<const float4*>(dxs + j * kMT + 32 * t + 8 * r4 + 4 * kg);
-              const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-              for (int q = 0; q < 4; ++q) {
-                const int r = 4 * r4 + q;
-                y[t][r] += dv[q] * (wlo * (float)I[t][r] + whi * (float)I2[t][r]);
-              }
-            }
-          continue;
-        }
-        // raw record j of this lane's weight row: header, then 16 nibble bytes
-        const int off = T::kRec * j + T::kHdr;  // first nibble byte
-        const int sh = off & 3, b4 = off - sh;
-        uint32_t w0 = wld(b4), w1 = wld(b4 + 4), w2 = wld(b4 + 8), w3 = wld(b4 + 12);
-        uint32_t q0 = w0, q1 = w1, q2 = w2, q3 = w3;
-        if (sh) {
-          const uint32_t w4 = wld(b4 + 16);
-          q0 = __builtin_amdgcn_alignbyte(w1, w0, sh);
-          q1 = __builtin_amdgcn_alignbyte(w2, w1, sh);
-          q2 = __builtin_amdgcn_alignbyte(w3, w2, sh);
-          q3 = __builtin_amdgcn_alignbyte(w4, w3, sh);
-        }
-        // header byte(s) just before the nibbles
-        float wsc = 0.f;
-        uint32_t wbits = 0;  // Q4_0 / Q4_1: the fp16 scale's bits
-        if constexpr (F == WFmt::Q4_1) {
-          const uint32_t hd = ld32(wrow + T::kRec * j);  // records are 4-byte aligned here
-          wbits = hd & 0xffffu;
-        } else if constexpr (F == WFmt::Q4_0) {
-          wbits = sh >= 2 ? (w0 & 0xffffu) : (wld(b4 - 4) >> 16);
-        } else {
-          const uint32_t e = sh >= 1 ? ((w0 >> (8 * (sh - 1))) & 0xffu) : (ld32(wrow + b4 - 4) >> 24);
-          wsc = scl[e];
-        }
-        const uint32_t shn = 4 * kg;  // kg 0: elements 0..15 (low nibbles), 1: 16..31 (high)
-        uint32_t n[4] = {(q0 >> shn) & 0x0f0f0f0fu, (q1 >> shn) & 0x0f0f0f0fu,
-                         (q2 >> shn) & 0x0f0f0f0fu, (q3 >> shn) & 0x0f0f0f0fu};
-        v4i bv;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if constexpr (F == WFmt::Q4_0)
-            bv[i] = (int)(((n[i] | 0x80808080u) - 0x08080808u) ^ 0x80808080u);  // q - 8 per byte
-          else if constexpr (F == WFmt::Q4_1)
-            bv[i] = (int)n[i];  // q in 0..15
-          else
-            bv[i] = (int)lookup16(n[i], c0, c1, c2, c3);
-        }
-        const int chunk = (2 * j + kg) ^ sw;
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const v4i av = *reinterpret_cast<const v4i*>(AQ + (32 * t + col) * 256 + 16 * chunk);
-          I[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, zero, 0, 0, 0);
-        }
-        if constexpr (F == WFmt::Q4_0 || F == WFmt::Q4_1) {
-          // y += (dx dw) I with the factor dx dw of every output from one f16
-          // MFMA per tile as an outer product: K slot 0 holds the token's dx
-          // and the row's dw (both fp16, so each product is exact in fp32,
-          // as the VALU product it replaces), every other slot 0
-          // (operands as raw bits: the kg half's slots are zero without a branch)
-          const uint32_t kmask = kg ? 0u : 0xffffu;
-          const v2u bq = {wbits & kmask, 0u};
-#pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            const _Float16 dxh = (_Float16)dxs[j * kMT + 32 * t + col];
-            const v2u aq = {(uint32_t)__builtin_bit_cast(uint16_t, dxh) & kmask, 0u};
-            const v16f qd = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, aq), __builtin_bit_cast(v4h, bq),
-                                                                fzero, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) y[t][r] = fmaf(qd[r], (float)I[t][r], y[t][r]);
-          }
-          // keep the blocks' factor MFMAs in block order (hoisted, their
-          // results would hold registers across the whole stage)
-          __builtin_amdgcn_sched_barrier(0);
-        } else {
-          // y += (dx * ws) * I; register r of a tile holds token 8*(r/4) + 4*kg + r%4
-#pragma unroll
-          for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4) {
-              const float4 d4 = *reinterpret_cast<const float4*>(dxs + j * kMT + 32 * t + 8 * r4 + 4 * kg);
-              const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-              for (int q = 0; q < 4; ++q) {
-                const int r = 4 * r4 + q;
-                y[t][r] += (dv[q] * wsc) * (float)I[t][r];
-              }
-            }
-        }
-      }
-      if constexpr (F == WFmt::Q4_1) {
-        // Q4_1's min term, m s per block (ggml-cpu/quants.c:241), for the
-        // stage's eight blocks at once: one f16 MFMA per tile (K = 8 blocks)
-        // of the tokens' fp16 block sums against the rows' fp16 mins, added
-        // into y.  Both are fp16, so every product is exact in fp32.
-        const uint8_t* mrec = wrow + T::kRec * 4 * kg;  // blocks 4 kg .. 4 kg + 3 of this lane's row
-        const uint32_t h0 = ld32(mrec), h1 = ld32(mrec + T::kRec), h2 = ld32(mrec + 2 * T::kRec),
-                       h3 = ld32(mrec + 3 * T::kRec);
-        const uint2 bm = make_uint2(__builtin_amdgcn_perm(h1, h0, 0x07060302u), __builtin_amdgcn_perm(h3, h2, 0x07060302u));
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const uint2 am = *reinterpret_cast<const uint2*>(sxs + 8 * (32 * t + col) + 4 * kg);
-          y[t] = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, am), __builtin_bit_cast(v4h, bm), y[t],
-                                                     0, 0, 0);
-        }
-      }
-    }
+    if (refill && wcol == 0) load_dx(pair + 1);
+    const bool active = 2 * pair + par < nst;
+    if (active) half(pair, cur, std::integral_constant<int, 0>{});
+    if (refill) issue(pair + 1, nxt);
+    if (active) half(pair, cur, std::integral_constant<int, 4>{});
     if (refill && wcol == 0) store_dx((pair + 1) & 1);  // slot last read a pair ago
   };
 
@@ -778,6 +788,22 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
   // LDS byte addresses as integers from one wave-uniform base: no per-use
   // generic-to-LDS pointer casts (their null checks on VALU do not compile)
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+  // a pair with both stages (every pair but an odd K's last): the loads
+  // without the tail offsets
+  auto issue_pair = [&](int p) {
+    const uint32_t slot = lds0 + (uint32_t)(p & 1) * kSlot;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const uint8_t* xb = xbase + 256 * (size_t)(2 * p + s);
+      dma16_s(xb, va0, slot + kAct * s + 1024 * wave);
+      dma16_s(xb, va1, slot + kAct * s + 1024 * (wave + 8));
+    }
+    lds_dma4_s(xbase + 16 * (size_t)(2 * p + (wave >> 2)), vsc, slot + kSD + 256 * wave);
+    const uint8_t* wb = wbase + 272 * (size_t)p;
+#pragma unroll
+    for (int i = 0; i < 6; ++i)
+      if (wave + 8 * i < kWLoads) dma16_s(wb, vw[i], slot + kSW + 1024 * (wave + 8 * i));
+  };
   auto issue = [&](int p) {
     const uint32_t slot = lds0 + (uint32_t)(p & 1) * kSlot;
     const bool both = 2 * p + 1 < nst;  // the pair's second stage exists
@@ -803,31 +829,35 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
   const int x_scale = h ? 127 + 9 : 127 + 13;  // B block 0: hi plane (x16), block 1: lo plane
   const int sp = ph >> 1;                      // the phase's stage within a pair
 
-  // The phase's four blocks of pair p.  kExact false: every tile takes its
-  // exponent e as the hardware block scale, and `out` collects whether any
-  // e lies outside [kSafeLo, kSafeHi] (the results are then discarded).
-  // kExact true: a column tile whose 32 rows all have exponents in range
-  // does the same; otherwise (wave-uniform) its MFMA runs at unit scale and
-  // the block is combined in GGML's order.
-  auto phase_blocks = [&](int p, auto exact_tag, bool& out) {
+  // Blocks J0, J0 + 1 of the phase's four blocks of pair p.  kExact false:
+  // every tile takes its exponent e as the hardware block scale, and `out`
+  // collects whether any e lies outside [kSafeLo, kSafeHi] (the results are
+  // then discarded).  kExact true: a column tile whose 32 rows all have
+  // exponents in range does the same; otherwise (wave-uniform) its MFMA runs
+  // at unit scale and the block is combined in GGML's order.
+  auto phase_blocks = [&](int p, auto exact_tag, bool& out, auto j0_tag) {
     constexpr bool kExact = decltype(exact_tag)::value;
+    constexpr int J0 = decltype(j0_tag)::value;
     const uint8_t* slot = lds + (p & 1) * kSlot;
     const uint32_t slot_lds = lds0 + (uint32_t)(p & 1) * kSlot;
-    // the 17 dwords holding records 4 ph .. 4 ph + 3 of rows 64 cp + 32 ct + col:
-    // four 16-byte reads and the segment's last dword (at byte 76 of its copy)
+    // of the 17 dwords holding records 4 ph .. 4 ph + 3 of rows
+    // 64 cp + 32 ct + col (four 16-byte reads and the segment's last dword,
+    // at byte 76 of its copy), those of records J0 and J0 + 1: bytes
+    // [17 J0, 17 J0 + 34)
     uint32_t wd[2][17];
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
       const uint8_t* wr = slot + kSW + kRowW * (64 * cp + 32 * ct + col) + kSeg * ph;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
+        if (16 * i + 16 <= 17 * J0 || 16 * i >= 17 * J0 + 34) continue;
         const uint4 v = *reinterpret_cast<const uint4*>(wr + 16 * i);
         wd[ct][4 * i] = v.x, wd[ct][4 * i + 1] = v.y, wd[ct][4 * i + 2] = v.z, wd[ct][4 * i + 3] = v.w;
       }
-      wd[ct][16] = ld32(wr + 76);
+      if (J0 == 2) wd[ct][16] = ld32(wr + 76);
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = J0; j < J0 + 2; ++j) {
       const int bs = 4 * (ph & 1) + j;  // block within stage sp
       // record j: e at byte 17 j, then 16 nibble bytes
       constexpr int kE[4] = {0, 17, 34, 51};
@@ -884,17 +914,26 @@ __device__ void scaled_body(const GemmArgs& a, uint8_t* lds) {
     }
   };
 
-  // The K loop.  The direct loads of the next pair go out right after the
-  // barrier, into the slot the previous pair used, so each wave waits for
-  // all of its own loads (vmcnt 0) at the top of a pair.
+  // The K loop.  The direct loads of the next pair go into the slot the
+  // previous pair used (free after the barrier), and each wave waits for all
+  // of its own loads (vmcnt 0) at the top of a pair.  A wave issues its share
+  // between its phase's second and third blocks: issued right after the
+  // barrier, every wave's first block waited behind the workgroup's ~80
+  // queued loads (39.5 -> 37.8 us per call at 512 x 4096 x 4096); issued
+  // after the third block or spread over the blocks they land too late for
+  // the next barrier.  An odd K's last pair (one stage) is issued at the top.
   const int npair = (nst + 1) >> 1;
   auto kloop = [&](auto exact_tag, bool& out) {
     issue(0);
     for (int p = 0; p < npair; ++p) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       lds_barrier();  // the pair is in for every wave; the previous pair's slot is free
-      if (p + 1 < npair) issue(p + 1);
-      if (2 * p + sp < nst) phase_blocks(p, exact_tag, out);
+      const bool next = p + 1 < npair, full = 2 * (p + 1) + 1 < nst;
+      if (next && !full) issue(p + 1);
+      const bool active = 2 * p + sp < nst;
+      if (active) phase_blocks(p, exact_tag, out, std::integral_constant<int, 0>{});
+      if (next && full) issue_pair(p + 1);
+      if (active) phase_blocks(p, exact_tag, out, std::integral_constant<int, 2>{});
     }
   };
   // Weights quantized by GGML keep every exponent in range, and the loop
