@@ -361,7 +361,7 @@ def iq2_tables_mul_mat_f64(fmt: str, W: np.ndarray, Xq: np.ndarray, n: int, k: i
     IQ2_XS: a 16-element half with 2 s + 1 from its scale nibble), then
     fp16 d * Q8_K d * 0.125 per superblock.  GGML's generic vec_dots
     (ggml-cpu/quants.c:855-946) are the same function on GGML's tables.
-    Numpy, small shapes (tests only).  E = sum of the superblock terms, A =
+    Numpy, small shapes (tests only).  E = sum of the scale-group terms, A =
     sum of their magnitudes (oracle.within_tolerance), as wo_mul_mat_f64."""
     xs = fmt == "iq2_xs"
     rec = 74 if xs else 66
@@ -394,10 +394,13 @@ def iq2_tables_mul_mat_f64(fmt: str, W: np.ndarray, Xq: np.ndarray, n: int, k: i
     term = part * (2 * ls[None] + 1)
     if not xs:  # one scale per 32-group: the two halves' integer sum times 2 s + 1
         term = (part[..., 0::2] + part[..., 1::2]) * (2 * ls[None, ..., 0::2] + 1)
-    block = term.sum(axis=3)                                    # each superblock's exact integer sum
-    scale = 0.125 * dw[None, :, :] * dx[:, None, :]                                     # (m, n, nsb)
-    e = (scale * block).sum(axis=2)
-    a = np.abs(scale * block).sum(axis=2)
+    t = 0.125 * dw[None, :, :, None] * dx[:, None, :, None] * term                      # (m, n, nsb, groups)
+    e = np.zeros((m, n))
+    a = np.zeros((m, n))
+    for b in range(nsb):  # wo_mul_mat_f64's order: superblocks, then their scale groups
+        for g in range(t.shape[3]):
+            e += t[:, :, b, g]
+            a += np.abs(t[:, :, b, g])
     return e, a
 
 
@@ -406,9 +409,14 @@ def max_threads() -> int:
 
 
 # Tolerance for fp32 outputs against the fp64 re-accumulation E with
-# magnitude A = sum_b |scale_b * P_b|: relative 1e-4 of |E| plus 4e-6 of A
-# (about 64 fp32 ulps of the magnitude: room for the fp32 rounding of up to
-# ~90 block terms in any summation order).
+# magnitude A = sum_b |scale_b * P_b| over the format's scale groups (a
+# 32- or 16-element block or sub-block, the K-quants' min terms apart):
+# relative 1e-4 of |E| plus 4e-6 of A (about 64 fp32 ulps of the magnitude:
+# room for the fp32 rounding of up to ~90 group terms in any summation
+# order).  Every partial sum a kernel rounds to fp32 is a sum of whole scale
+# groups, so |partial| <= A: a K-quant superblock's two halves can each be
+# hundreds of times its total (the min terms of x's halves cancel), which a
+# per-superblock A would not bound.
 REL_TOL = 1e-4
 MAG_TOL = 4e-6
 

@@ -2038,7 +2038,7 @@ int64_t wo_int_partials(int fmt, const uint8_t *w, const uint8_t *x, int64_t k, 
     for (int64_t i = 0; i < nb; ++i) {
       const uint8_t *wr = w + i * IQ2_XXS_BYTES;
       const int8_t *q8 = (const int8_t *)(x + i * Q8_K_BYTES + 4);
-      int32_t b = 0;
+      /* one int32 per 32-element group: its partial times 2 ls + 1 */
       for (int g = 0; g < 8; ++g) {
         const uint8_t *qs = wr + 2 + 8 * g;
         const uint32_t meta = rd32(qs + 4);
@@ -2048,9 +2048,8 @@ int64_t wo_int_partials(int fmt, const uint8_t *w, const uint8_t *x, int64_t k, 
           for (int j = 0; j < 8; ++j)
             s += grid[8 * qs[l] + j] * q8[32 * g + 8 * l + j] * ((sg >> j) & 1 ? -1 : 1);
         }
-        b += s * (int32_t)(2 * (meta >> 28) + 1);
+        out[n++] = s * (int32_t)(2 * (meta >> 28) + 1);
       }
-      out[n++] = b;
     }
   } else if (fmt == WO_Q6_K) {
     const int64_t nb = k / QK_K;
@@ -2096,11 +2095,12 @@ void wo_mul_mat_f64(int fmt, const uint8_t *W, const uint8_t *Xq, double *E, dou
           const uint8_t *wr = w + i * IQ2_XS_BYTES;
           const uint8_t *xr = x + i * Q8_K_BYTES;
           wo_int_partials(fmt, wr, xr, QK_K, parts);
-          int64_t S = 0;
-          for (int h = 0; h < 16; ++h) S += (int64_t)(2 * ((wr[66 + h / 2] >> (4 * (h & 1))) & 0xf) + 1) * parts[h];
-          const double t = 0.125 * wo_fp16_to_fp32(rd16(wr)) * (double)rdf32(xr) * (double)S;
-          e += t;
-          a += fabs(t);
+          const double f = 0.125 * wo_fp16_to_fp32(rd16(wr)) * (double)rdf32(xr);
+          for (int h = 0; h < 16; ++h) {
+            const double t = f * (double)((int64_t)(2 * ((wr[66 + h / 2] >> (4 * (h & 1))) & 0xf) + 1) * parts[h]);
+            e += t;
+            a += fabs(t);
+          }
         }
       } else if (fmt == WO_Q4_0 || fmt == WO_MXFP4) {
         for (int64_t base = 0; base < K; base += 8192) {
@@ -2135,11 +2135,12 @@ void wo_mul_mat_f64(int fmt, const uint8_t *W, const uint8_t *Xq, double *E, dou
           const uint8_t *wr = w + i * Q6_K_BYTES;
           const uint8_t *xr = x + i * Q8_K_BYTES;
           wo_int_partials(fmt, wr, xr, QK_K, parts);
-          int64_t S = 0;
-          for (int g = 0; g < 16; ++g) S += (int64_t)((const int8_t *)(wr + 192))[g] * parts[g];
-          const double t = (double)wo_fp16_to_fp32(rd16(wr + 208)) * (double)rdf32(xr) * (double)S;
-          e += t;
-          a += fabs(t);
+          const double f = (double)wo_fp16_to_fp32(rd16(wr + 208)) * (double)rdf32(xr);
+          for (int g = 0; g < 16; ++g) {
+            const double t = f * (double)((int64_t)((const int8_t *)(wr + 192))[g] * parts[g]);
+            e += t;
+            a += fabs(t);
+          }
         }
       } else {
         const int64_t nb = K / QK_K;
@@ -2150,20 +2151,21 @@ void wo_mul_mat_f64(int fmt, const uint8_t *W, const uint8_t *Xq, double *E, dou
           const double dx = rdf32(xr);
           const double dw = wo_fp16_to_fp32(rd16(wr));
           if (fmt == WO_Q4_K || fmt == WO_Q5_K) {
-            uint8_t sc, mm;
-            int64_t S = 0;
-            for (int s = 0; s < 8; ++s) {
-              scale_min_k4(s, wr + 4, &sc, &mm);
-              S += (int64_t)sc * parts[s];
-            }
             const double dmin = wo_fp16_to_fp32(rd16(wr + 2));
-            const double t1 = dw * dx * (double)S, t2 = dmin * dx * (double)parts[8];
-            e += t1 - t2;
-            a += fabs(t1) + fabs(t2);
+            for (int s = 0; s < 8; ++s) {
+              uint8_t sc, mm;
+              scale_min_k4(s, wr + 4, &sc, &mm);
+              const int32_t bs = (int16_t)rd16(xr + 260 + 4 * s) + (int16_t)rd16(xr + 262 + 4 * s);
+              const double t1 = dw * dx * (double)((int64_t)sc * parts[s]), t2 = dmin * dx * (double)(mm * bs);
+              e += t1 - t2;
+              a += fabs(t1) + fabs(t2);
+            }
           } else {
-            const double t = 0.125 * dw * dx * (double)parts[0];
-            e += t;
-            a += fabs(t);
+            for (int g = 0; g < 8; ++g) {
+              const double t = 0.125 * dw * dx * (double)parts[g];
+              e += t;
+              a += fabs(t);
+            }
           }
         }
       }

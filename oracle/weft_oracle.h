@@ -119,14 +119,19 @@ void wo_mul_mat_q(int fmt, const uint8_t *W, const uint8_t *Xq, float *Y,
 
 /* fp64 re-accumulation of the exact integer partials of every output:
  * E[m, n] = sum_b scale_b * P_b evaluated in double, and
- * A[m, n] = sum_b |scale_b * P_b| (the magnitude a tolerance is taken on). */
+ * A[m, n] = sum_b |scale_b * P_b| (the magnitude a tolerance is taken on),
+ * b over the format's scale groups: 32-blocks, NVFP4's 16-sub-blocks, the
+ * K-quants' sub-blocks (Q4_K / Q5_K: the scale and the min term of each),
+ * IQ2_XXS's 32-groups and IQ2_XS's 16-halves. */
 void wo_mul_mat_f64(int fmt, const uint8_t *W, const uint8_t *Xq, double *E,
                     double *A, int64_t N, int64_t K, int64_t M, int nthreads);
 
 /* Integer partials of one row pair, for exactness checks on tiny inputs:
  * Q4_0 / MXFP4 : one int32 per 32-block (P)
  * Q4_K / Q5_K  : per superblock, 8 sub-block sums P_s then the min sum Mn
- * IQ2_XXS      : one int32 per superblock (B = sum_g I_g * (2 s_g + 1))
+ * IQ2_XXS      : one int32 per 32-group (I_g * (2 s_g + 1))
+ * IQ2_XS       : one int32 per 16-element half (its 4-bit scale's partial)
+ * NVFP4        : one int32 per 16-element sub-block
  * Q6_K         : per superblock, the 16 group sums P_g (16 elements each)
  * returns the number of int32 written. */
 int64_t wo_int_partials(int fmt, const uint8_t *w, const uint8_t *x, int64_t k,

@@ -739,6 +739,62 @@ def _codes_k(fmt: str, rec: np.ndarray) -> np.ndarray:
     return q
 
 
+def _k_halves(fmt: str, w: np.ndarray, xq: np.ndarray) -> np.ndarray:
+    """(m, n, 2): each K = 256 output's two half-superblock terms in fp64,
+    from the record bytes (Q4_K / Q5_K: dx (d sum sc P - dmin sum m B),
+    B = the group's two Q8_K bsums; Q6_K: dx d sum sc P)."""
+    rb = o.RECORD[fmt][1]
+    rec = w.reshape(-1, rb)
+    codes = _codes_k(fmt, rec).astype(np.int64)                         # (n, 256)
+    xv = xq[:, 4:260].view(np.int8).astype(np.int64)                    # (m, 256)
+    dx = xq[:, 0:4].copy().view(np.float32)[:, 0].astype(np.float64)
+    bs = xq[:, 260:292].copy().view(np.int16).astype(np.int64)          # (m, 16)
+    f16 = lambda b: b.copy().view(np.float16).astype(np.float64)[..., 0]  # noqa: E731
+    out = np.zeros((xq.shape[0], rec.shape[0], 2))
+    if fmt == "q6_k":
+        d = f16(rec[:, 208:210])
+        sc = rec[:, 192:208].view(np.int8).astype(np.int64)
+        for j in range(16):
+            p = xv[:, 16 * j:16 * j + 16] @ (codes[:, 16 * j:16 * j + 16] - 32).T
+            out[:, :, j // 8] += dx[:, None] * d[None, :] * (sc[None, :, j] * p)
+        return out
+    d, dmin = f16(rec[:, 0:2]), f16(rec[:, 2:4])
+    for j in range(8):
+        sc, m = _k_scale_min(rec[:, 4:16].astype(np.int64), j)
+        p = xv[:, 32 * j:32 * j + 32] @ codes[:, 32 * j:32 * j + 32].T
+        b = bs[:, 2 * j] + bs[:, 2 * j + 1]
+        out[:, :, j // 4] += dx[:, None] * (d[None, :] * (sc[None, :] * p) - dmin[None, :] * (m[None, :] * b[:, None]))
+    return out
+
+
+def test_mul_mat_f64_magnitude_bounds_half_superblocks():
+    """A (the tolerance's magnitude) is summed over scale groups, so it
+    bounds every partial sum of whole groups a kernel may round to fp32.
+    The case is a Q5_K output of a randomized GPU shape sweep (K = 256):
+    its half-superblock terms are +-0.225 and its total 1.2e-5, so a
+    per-superblock A (|dx d S| + |dx dmin Mn| ~ 1e-3) was 450x too small
+    to cover the fp32 rounding of the halves (1.3e-8)."""
+    x = o.seeded_normal(447344297, (285, 256))[40:41]
+    w = o.quantize("q5_k", o.seeded_normal(1029995214, (1814, 256), 0.02)[1755:1756])
+    xq = o.quantize("q8_k", x)
+    e, a = o.mul_mat_f64("q5_k", w, xq, 1, 256, 1)
+    halves = _k_halves("q5_k", w, xq)[0, 0]
+    assert abs(halves.sum() - e[0, 0]) <= 1e-15 * np.abs(halves).sum()
+    assert abs(e[0, 0]) < 2e-5 and np.abs(halves).min() > 0.2
+    assert a[0, 0] >= np.abs(halves).sum()
+    # fp32 halves summed in fp32 (one rounding each, then the sum) pass the bar
+    y = np.float32(np.float32(halves[0]) + np.float32(halves[1]))
+    assert o.within_tolerance(np.array([[y]]), e, a).all()
+    # and the property on random rows of each K-quant
+    for fmt in ("q4_k", "q5_k", "q6_k"):
+        w = o.quantize(fmt, o.seeded_normal(61, (64, 256), 0.02))
+        xq = o.quantize("q8_k", o.seeded_normal(62, (48, 256)))
+        e, a = o.mul_mat_f64(fmt, w, xq, 64, 256, 48)
+        halves = _k_halves(fmt, w, xq)
+        np.testing.assert_allclose(halves.sum(axis=2), e, rtol=0, atol=1e-12 * a.max())
+        assert (a >= np.abs(halves).sum(axis=2) * (1 - 1e-12)).all(), fmt
+
+
 def _nearest_int(v: np.ndarray) -> np.ndarray:
     return np.rint(v.astype(np.float32)).astype(np.int64)  # RNE, as GGML's 1.5 * 2^23 trick
 
