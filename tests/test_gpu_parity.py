@@ -433,6 +433,28 @@ def test_mxfp4_caller_tables_are_used(hip, symbol, m):
     assert_close(y.numpy(np.float32).reshape(m, n), 2.0 * e, 2.0 * a, "mxfp4 with doubled scale table")
 
 
+@pytest.mark.parametrize("fmt,symbol,m", [
+    ("mxfp4", "production_mul_mat_mxfp4_decode", 1), ("mxfp4", "production_mul_mat_mxfp4", 64),
+    ("nvfp4", "production_mul_mat_nvfp4_decode", 1), ("nvfp4", "production_mul_mat_nvfp4", 64)])
+def test_fp4_caller_codebook_is_used(hip, fmt, symbol, m):
+    """A codebook that is not GGML's (kvalues_mxfp4 negated) is honoured:
+    the batch-1 kernels look it up with v_perm instead of converting the
+    nibbles as E2M1 codes, the prefill takes its table-driven body, and the
+    result is exactly minus GGML's."""
+    n, k = 256, 1024
+    w, x = weights(fmt, n, k), acts(m, k)
+    neg = hip.to_dev((-o.kvalues_mxfp4().astype(np.int16)).astype(np.int8))
+    tab = hip.scale if fmt == "mxfp4" else hip.ue4m3
+    xq = hip.empty(o.record_bytes("q8_0", k) * m, fill=SENTINEL)
+    y = hip.empty(4 * m * n, fill=SENTINEL)
+    hip.call(symbol, hip.to_dev(w), hip.to_dev(x), xq, neg, tab, y, n, k, m)
+    want_xq = np.full((m, o.record_bytes("q8_0", k)), SENTINEL, np.uint8)
+    o.quantize("q8_0", x, out=want_xq)
+    np.testing.assert_array_equal(xq.numpy(np.uint8).reshape(m, -1), want_xq)
+    e, a = o.mul_mat_f64(fmt, w, want_xq, n, k, m)
+    assert_close(y.numpy(np.float32).reshape(m, n), -e, a, f"{fmt} with a negated codebook")
+
+
 # ------------------------------------------------------------ error paths
 def test_invalid_shape_reports_error_and_launches_nothing(hip):
     y = hip.empty(16, fill=SENTINEL)
