@@ -10,7 +10,8 @@ compared with it.  Each check is independent of the oracle's own formula:
     kernels compute it (examples/kernels/dequantize/*.py) -- a different
     description from the GGML C the oracle restates;
   * Q8 quantizers by hand-computed known answers (rounding ties, first-index
-    maximum, all-zero block) and invariants;
+    maximum, all-zero block) and invariants; the Q4_0 / Q4_1 / MXFP4 / NVFP4
+    weight quantizers likewise (inputs on the grid, rounding and tie rules);
   * vec_dot / mul_mat and the fp64 re-accumulation against an independent
     numpy path: dequantize both operands to float64 and take the dot.
 GGML itself is not built here: ggml-impl.h includes gguf.h, which the
@@ -850,6 +851,79 @@ def test_q4_0_quantizer_error_is_half_a_step():
     err = np.abs(o.dequantize("q4_0", q, 32).astype(np.float64) - w.reshape(-1, 32))
     # the block maximum maps to -8 exactly; the +7 clamp side may lose up to a full step
     assert (err <= d[:, None] * 1.001 + 1e-7).all()
+
+
+def _q4_0_codes(rec: np.ndarray) -> np.ndarray:
+    qs = rec[:, 2:18].astype(np.int64)
+    return np.concatenate([qs & 15, qs >> 4], axis=1)  # element j: low nibble, j + 16: high
+
+
+def test_q4_0_quantizer_known_answers():
+    """quantize_row_q4_0_ref (ggml-quants.c:28-53): d = max / -8 with max
+    the signed value of largest |x| (first index on ties), id = 1 / d,
+    q = MIN(15, (int8_t)(x id + 8.5)), i.e. round half up and truncation
+    toward zero of the biased value, element j in the low nibble of byte j
+    and j + 16 in the high one."""
+    rng = np.random.default_rng(5)
+    # blocks on the grid: x = d (q - 8) with one element at -8 d, d random fp16
+    nblk = 64
+    q = rng.integers(0, 16, size=(nblk, 32))
+    q[np.arange(nblk), rng.integers(0, 32, size=nblk)] = 0
+    d = o.fp16_to_fp32(o.fp32_to_fp16(rng.uniform(1e-3, 1.0, size=nblk).astype(np.float32)))
+    d[::2] = -d[::2]  # a negative d: the largest magnitude is positive
+    x = (d[:, None].astype(np.float64) * (q - 8)).astype(np.float32)
+    rec = o.quantize("q4_0", x.reshape(1, -1)).reshape(nblk, 18)
+    assert np.array_equal(rec[:, 0:2].copy().view(np.uint16)[:, 0], o.fp32_to_fp16(d))
+    assert np.array_equal(_q4_0_codes(rec), q)
+    # rounding: with d = 2^-3 (id exact) x id = v gives floor(v + 8.5), clamped to 15
+    v = np.array([-8, -1.5, -0.5, 0.5, 1.5, 2.5, -2.5, 6.49, 6.5, 7.0, 7.49, 7.5, 8.0, 0.0,
+                  3.25, -3.25, -7.5, 5.5, 4.5, -4.5, 1, 2, 3, 4, 5, 6, 7, -7, -6, -5, -4, -3])
+    x = (np.float32(-0.125) * v).astype(np.float32)  # max = x[0] = +1, d = 1 / -8
+    rec = o.quantize("q4_0", x.reshape(1, 32))
+    want = np.minimum(15, np.floor(v + 8.5)).astype(np.int64)
+    assert np.array_equal(_q4_0_codes(rec.reshape(1, 18))[0], want)
+    # a tie on |x|: the first index sets the sign of d
+    x = np.zeros((1, 32), np.float32)
+    x[0, 3], x[0, 9] = -2.0, 2.0
+    rec = o.quantize("q4_0", x).reshape(1, 18)
+    assert o.fp16_to_fp32(rec[:, 0:2].copy().view(np.uint16))[0] == 0.25  # -2 / -8
+    assert _q4_0_codes(rec)[0, 3] == 0 and _q4_0_codes(rec)[0, 9] == 15  # 8 + 8.5 -> 16 -> 15
+    # an all-zero block: d = 0 / -8 = -0 (fp16 0x8000), id = 0, every code 8
+    rec = o.quantize("q4_0", np.zeros((1, 32), np.float32)).reshape(1, 18)
+    assert rec[0, 0:2].copy().view(np.uint16)[0] == 0x8000 and (rec[0, 2:] == 0x88).all()
+
+
+def test_mxfp4_quantizer_known_answers():
+    """quantize_row_mxfp4_ref / best_index_mxfp4 (ggml-quants.c:299-344):
+    e = floor(log2(amax)) - 2 + 127, d = 2^(e - 128), and each value takes
+    the first kvalues_mxfp4 index at the smallest |kv d - x|: on ties the
+    lower index (0 before -0, 4 before 6, -4 before -6)."""
+    kv = o.kvalues_mxfp4().astype(np.int64)
+    rng = np.random.default_rng(6)
+    nblk = 64
+    p = rng.integers(-20, 20, size=nblk)                   # amax in [2^p, 2^(p+1))
+    d = np.ldexp(1.0, p - 3)                               # 2^(e - 128) with e = p + 125
+    c = rng.integers(0, 16, size=(nblk, 32))
+    c[c == 8] = 0                                          # kv[8] = -0 encodes as index 0
+    top = rng.integers(0, 32, size=nblk)
+    c[np.arange(nblk), top] = np.where(rng.integers(0, 2, size=nblk) == 1, 7, 15)  # +-12: amax = 1.5 2^p
+    x = (kv[c] * d[:, None]).astype(np.float32)
+    rec = o.quantize("mxfp4", x.reshape(1, -1)).reshape(nblk, 17)
+    assert np.array_equal(rec[:, 0].astype(np.int64), p + 125)
+    codes = np.concatenate([rec[:, 1:17] & 15, rec[:, 1:17] >> 4], axis=1).astype(np.int64)
+    assert np.array_equal(codes, c)
+    # ties and values between the grid points, in units of d = 2^-3 (amax = 1.5)
+    u = np.array([12, 5, -5, 7, -7, 10, -10, 0.5, -0.5, 1.5, 2.5, 3.5, 15, -15, 0, 0.49,
+                  5.01, 4.99, 9.99, 10.01, -1.5, -2.5, -3.5, -0.51, 11.9, 6, -12, 8, -8, 3, 2, 1])
+    want = [7, 4, 12, 5, 13, 6, 14, 0, 0, 1, 2, 3, 7, 15, 0, 0,
+            5, 4, 6, 7, 9, 10, 11, 9, 7, 5, 15, 6, 14, 3, 2, 1]
+    x = (u * 0.125).astype(np.float32).reshape(1, 32)
+    rec = o.quantize("mxfp4", x).reshape(1, 17)
+    assert rec[0, 0] == 125  # amax = 15/8: floor(log2) = 0, e = 0 - 2 + 127
+    got = np.concatenate([rec[0, 1:17] & 15, rec[0, 1:17] >> 4])
+    assert list(got) == want
+    # an all-zero block: e = 0 and every code 0
+    assert not o.quantize("mxfp4", np.zeros((1, 32), np.float32)).any()
 
 
 # ------------------------------------------------ Q4K_I[16] interleave layout
