@@ -6,7 +6,8 @@ Bars (declared before any run):
     same sentinel fill on both sides);
   * fp32 outputs of vec_dot / mul_mat: |y - E| <= 1e-4 |E| + 4e-6 A, where E
     is the fp64 re-accumulation of the exact integer partials of the same
-    quantized operands and A = sum |scale * partial| (oracle.within_tolerance).
+    quantized operands and A = sum |scale * partial| over the format's scale
+    groups (oracle.within_tolerance).
 Shapes are BASELINE.json's configs where the oracle finishes in seconds;
 the prefill N=11008 case checks a seeded sample of output columns.
 """
