@@ -246,6 +246,34 @@ def test_decode_small_shapes(hip, fmt, n, k, m):
 
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "iq2_xxs", "mxfp4"])
+@pytest.mark.parametrize("m", [1, 3, 64])
+def test_long_rows(hip, fmt, m):
+    """K = 65536: the batch-1 and small-batch GEMVs stage the whole quantized
+    activation row in LDS (about 72 KB), the prefill GEMMs stream it by
+    superblock pairs."""
+    n, k = 96, 65536
+    w, x, xq, y = run_mul_mat(hip, MM_PREFILL[fmt] if m >= 16 else MM_DECODE[fmt], fmt, n, k, m)
+    check_mul_mat(fmt, w, x, xq, y, n, k, m)
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "mxfp4"])
+def test_row_past_the_lds_is_refused(hip, fmt):
+    """A batch-1 row whose quantized activation exceeds the LDS of a
+    workgroup (K = 2^18: ~270 KB) is refused with an error and writes
+    nothing, instead of a partial or wrong result."""
+    n, k = 2, 1 << 18
+    w = hip.empty(o.record_bytes(fmt, k) * n)
+    x = hip.to_dev(np.ones((1, k), np.float32))
+    xq = hip.empty(o.record_bytes(o.ACT_OF[fmt], k), fill=SENTINEL)
+    y = hip.empty(4 * n, fill=SENTINEL)
+    args = [w, x, xq, *tables(hip, fmt), y]
+    getattr(hip.lib, MM_DECODE[fmt])(*[a.ptr for a in args], n, k, 1)
+    hip.torch.cuda.synchronize()
+    assert hip.last_error() != 0
+    assert (y.numpy(np.uint8) == SENTINEL).all() and (xq.numpy(np.uint8) == SENTINEL).all()
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "iq2_xxs", "mxfp4"])
 def test_prefill_entry_points(hip, fmt):
     n, k, m = 512, 4096, 64
     w, x, xq, y = run_mul_mat(hip, MM_PREFILL[fmt], fmt, n, k, m)
