@@ -256,11 +256,47 @@ def test_long_rows(hip, fmt, m):
     check_mul_mat(fmt, w, x, xq, y, n, k, m)
 
 
+MM_ANY = {"q4_0": "production_mul_mat_q4_0", "q4_1": "production_mul_mat_q4_1",
+          "mxfp4": "production_mul_mat_mxfp4", "nvfp4": "production_mul_mat_nvfp4",
+          "q4_k": "production_mul_mat_q4_k_staged", "q5_k": "production_mul_mat_q5_k",
+          "q6_k": "production_mul_mat_q6_k", "iq2_xxs": "production_mul_mat_iq2_xxs_staged",
+          "iq2_xs": "production_mul_mat_iq2_xs_staged"}
+
+
+def launch_log(hip):
+    import ctypes
+    buf = ctypes.create_string_buffer(4096)
+    hip.lib.weft_hip_launch_log(buf, len(buf))
+    return buf.value.decode()
+
+
+@pytest.mark.parametrize("fmt", list(MM_ANY))
+@pytest.mark.parametrize("m", [1, 3])
+def test_long_row_small_batch_takes_the_gemm(hip, fmt, m):
+    """K = 2^18 (a quantized activation row of ~300 KB, past a workgroup's
+    LDS) below 16 activation rows: the mul_mat entry points run the
+    format's prefill GEMM, which streams K, instead of the GEMVs that keep
+    the row in LDS; every output against the oracle."""
+    n, k = 8, 1 << 18
+    x = o.seeded_normal(31, (m, k))
+    w = (o.random_records(fmt, n, k, seed=32) if fmt.startswith("iq2")
+         else o.quantize(fmt, o.seeded_normal(32, (n, k), 0.02)))
+    was = hip.lib.weft_hip_set_launch_log(1)
+    try:
+        launch_log(hip)  # drop earlier names
+        w_, x_, xq, y = run_mul_mat(hip, MM_ANY[fmt], fmt, n, k, m, w=w, x=x)
+        names = launch_log(hip)
+    finally:
+        hip.lib.weft_hip_set_launch_log(was)
+    assert "gemm" in names and "gemv" not in names, names
+    check_mul_mat(fmt, w_, x_, xq, y, n, k, m)
+
+
 @pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "mxfp4"])
-def test_row_past_the_lds_is_refused(hip, fmt):
-    """A batch-1 row whose quantized activation exceeds the LDS of a
-    workgroup (K = 2^18: ~270 KB) is refused with an error and writes
-    nothing, instead of a partial or wrong result."""
+def test_decode_row_past_the_lds_is_refused(hip, fmt):
+    """The batch-1 decode entry points keep the activation row in LDS: a
+    row past it (K = 2^18: ~300 KB) is refused with an error and nothing
+    written, instead of a partial or wrong result."""
     n, k = 2, 1 << 18
     w = hip.empty(o.record_bytes(fmt, k) * n)
     x = hip.to_dev(np.ones((1, k), np.float32))

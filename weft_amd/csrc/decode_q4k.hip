@@ -497,6 +497,14 @@ void launch_one(bool a16, dim3 grid, size_t lds, const Q4KArgs& a) {
     q4k_gemv_kernel<false, MB, NT><<<grid, NT, lds, current_stream()>>>(a);
 }
 
+}  // namespace
+
+bool q4k_gemv_fits(size_t K) {
+  return K == 0 || K > (size_t)INT32_MAX || q8k_lds_row_bytes((int)K) <= max_lds_per_block();
+}
+
+namespace {
+
 // X != null -> quantize (and write Xq), else read xq_in.  pr: MUL_MAT_ID
 // pairs (one activation row each, blockIdx.y = pair).
 void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_out, float* Y,

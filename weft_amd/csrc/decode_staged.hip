@@ -792,6 +792,33 @@ void decode_nvfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* c
   launch<Fmt::NVFP4>(W, X, nullptr, Xq, codebook, scale, Y, N, K, M, st);
 }
 
+namespace {
+template <Fmt F>
+bool staged_fits(size_t K) {
+  using T = Traits<F>;
+  if (K == 0 || K > (size_t)INT32_MAX) return true;  // refused elsewhere, not for its LDS
+  const size_t row_lds = T::kQ8K ? q8k_lds_row_bytes((int)K)
+                         : act_q81<F>() ? q81_lds_row_bytes((int)K)
+                                        : q80_lds_row_bytes((int)K);
+  return (size_t)kWaves * kWindow + table_bytes<F>() + row_lds <= max_lds_per_block();
+}
+}  // namespace
+
+// Whether the staged GEMV's LDS holds one activation row of K values (the
+// same test as launch<F>'s): a longer row goes to the prefill GEMM.
+bool staged_gemv_fits(int fmt, size_t K) {
+  switch (fmt) {
+    case 0: return staged_fits<Fmt::Q4_0>(K);
+    case 1: return staged_fits<Fmt::MXFP4>(K);
+    case 3: return staged_fits<Fmt::Q6_K>(K);
+    case 4: return staged_fits<Fmt::Q5_K>(K);
+    case 5: return staged_fits<Fmt::NVFP4>(K);
+    case 6: return staged_fits<Fmt::Q4_1>(K);
+    case 7: return staged_fits<Fmt::IQ2_XS>(K);
+    default: return staged_fits<Fmt::IQ2_XXS>(K);
+  }
+}
+
 void decode_quantized(int fmt, const uint8_t* W, const uint8_t* Xq, const int8_t* tab0,
                       const void* tab1, float* Y, size_t N, size_t K, size_t M,
                       const RowStrides& st) {

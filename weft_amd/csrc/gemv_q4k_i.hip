@@ -247,11 +247,30 @@ __global__ void __launch_bounds__(256) q4k_i16_pack_kernel(const uint8_t* __rest
 }  // namespace
 
 namespace {
+// waves per cohort: the power of two (up to 16, and at most one per
+// superblock) nearest to 4096 waves in all, which measured best from 14 to
+// 22 waves per CU at the reference's shapes
+int i16_waves(size_t cohorts, size_t nsb) {
+  int waves = 1;
+  while (waves < 16 && (size_t)waves * 2 <= nsb && (double)cohorts * waves * 1.41421356 < 4096.0) waves *= 2;
+  return waves;
+}
+// LDS of one workgroup: the waves' rings, the Q8_K row (qs, pair sums, d)
+// and the partial sums
+size_t i16_lds(int waves, size_t nsb) {
+  return (size_t)waves * kRing * kBlock + nsb * (256 + 32 + 4) + (size_t)waves * kCohort * 4;
+}
+
 bool gemv_shape_ok(size_t M, size_t K) {
   return K % 256 == 0 && M % kCohort == 0 && M <= (size_t)INT32_MAX && K <= (size_t)INT32_MAX;
 }
 
 }  // namespace
+
+bool q4k_i16_gemv_fits(size_t M, size_t K) {
+  const size_t nsb = K / 256;
+  return i16_lds(i16_waves(M / kCohort, nsb), nsb) <= max_lds_per_block();
+}
 
 size_t q4k_i16_packed_size(size_t M, size_t K) {
   if (!gemv_shape_ok(M, K)) {
@@ -285,13 +304,9 @@ void q4k_i16_gemv(const uint8_t* W, const uint8_t* X, float* Y, size_t M, size_t
     set_error(hipErrorInvalidValue);
     return;
   }
-  // waves per cohort: the power of two (up to 16, and at most one per
-  // superblock) nearest to 4096 waves in all, which measured best from
-  // 14 to 22 waves per CU at the reference's shapes
   const size_t nsb = K / 256, cohorts = M / kCohort;
-  int waves = 1;
-  while (waves < 16 && (size_t)waves * 2 <= nsb && (double)cohorts * waves * 1.41421356 < 4096.0) waves *= 2;
-  const size_t lds = (size_t)waves * kRing * kBlock + nsb * (256 + 32 + 4) + (size_t)waves * kCohort * 4;
+  const int waves = i16_waves(cohorts, nsb);
+  const size_t lds = i16_lds(waves, nsb);
   if (lds > max_lds_per_block()) {
     set_error(hipErrorInvalidValue);  // the activation does not fit in LDS
     return;

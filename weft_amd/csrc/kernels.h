@@ -125,6 +125,14 @@ void mul_mat_id_iq2_grouped(bool xs, const uint8_t* W, const uint8_t* Xq, const 
 // Q4_0 (fmt 0), MXFP4 (1), IQ2_XXS (2), Q6_K (3), Q5_K (4), NVFP4 (5), Q4_1 (6) or
 // IQ2_XS (7) GEMV over an already quantized activation (Q8_0, Q8_1 or Q8_K
 // records, read only)
+// Whether a GEMV keeps one activation row of K values in LDS (the
+// staged GEMV by format code as decode_quantized takes it; the Q4_K GEMV;
+// the Q4K_I[16] GEMV).  Below 16 activation rows the prefill GEMMs take the
+// rows these refuse.
+bool staged_gemv_fits(int fmt, size_t K);
+bool q4k_gemv_fits(size_t K);
+bool q4k_i16_gemv_fits(size_t M, size_t K);  // M weight rows
+
 void decode_quantized(int fmt, const uint8_t* W, const uint8_t* Xq, const int8_t* tab0,
                       const void* tab1, float* Y, size_t N, size_t K, size_t M,
                       const RowStrides& st);

@@ -410,7 +410,9 @@ bool gemm_iq2_ok(const uint8_t* W, const void* Xq, const float* Y, const int8_t*
   // offsets; the GEMV kernels take everything else
   constexpr size_t kRec = Tile<kXs>::kRec;
   const size_t ldw = N > 1 ? st.ldw : K / 256 * kRec;
-  return M >= 16 && N > 0 && K > 0 && K % 512 == 0 && W != nullptr && Xq != nullptr &&
+  // (below 16 activation rows only when the GEMV's LDS cannot hold a row)
+  return (M >= 16 || !staged_gemv_fits(kXs ? 7 : 2, K)) && N > 0 && K > 0 && K % 512 == 0 &&
+         W != nullptr && Xq != nullptr &&
          Y != nullptr && grid != nullptr && signs != nullptr && aligned(W, 4) && ldw % 4 == 0 &&
          (kNT - 1) * ldw + K / 256 * kRec < ((size_t)1 << 32) &&
          aligned(Xq, 4) && aligned(Y, 4) && N <= (size_t)INT32_MAX && K <= (size_t)INT32_MAX &&

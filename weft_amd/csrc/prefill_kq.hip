@@ -412,7 +412,9 @@ bool gemm_kq_ok(const uint8_t* W, const void* Xq, const float* Y, size_t N, size
   constexpr size_t kRec = KTile<F>::kRec;
   const size_t ldw = N > 1 ? st.ldw : K / 256 * kRec;
   const size_t kq = F == KQ::Q6_K ? 512 : 256;
-  return M >= 16 && N > 0 && K > 0 && K % kq == 0 && W != nullptr && Xq != nullptr && Y != nullptr &&
+  // below 16 activation rows only when the GEMV's LDS cannot hold a row
+  return (M >= 16 || !staged_gemv_fits(F == KQ::Q6_K ? 3 : 4, K)) && N > 0 && K > 0 && K % kq == 0 &&
+         W != nullptr && Xq != nullptr && Y != nullptr &&
          aligned(W, 4) && ldw % 4 == 0 && aligned(Xq, 4) && aligned(Y, 4) && N <= (size_t)INT32_MAX &&
          K <= (size_t)INT32_MAX && M <= (size_t)INT32_MAX && strides_ok(st, K / 256 * kRec, 2, K, N, N, M) &&
          ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT) <= (size_t)INT32_MAX;

@@ -611,7 +611,9 @@ bool args_ok(const uint8_t* W, const void* Xq, const float* Y, size_t N, size_t 
 void mul_mat_q4k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
                  size_t M, const RowStrides& st) {
   if (N == 0 || M == 0 || K == 0) return;
-  if (M >= 16 && X != nullptr && args_ok(W, Xq, Y, N, K, M, st) && gemm_q4k_ok(W, N, K, M, st)) {
+  // the GEMV below 16 activation rows, unless its LDS cannot hold a row
+  if ((M >= 16 || !q4k_gemv_fits(K)) && X != nullptr && args_ok(W, Xq, Y, N, K, M, st) &&
+      gemm_q4k_ok(W, N, K, M, st)) {
     quantize_q8_k_rows(X, st.ldx, Xq, M, K);
     gemm_q4k(W, Xq, Y, N, K, M, st);
   } else {
@@ -665,7 +667,7 @@ void mul_mat_q4k_persistent(const uint8_t* W, const float* X, uint8_t* Xq, float
     return;
   }
   quantize_q8_k_rows(X, K, Xq, M, K);
-  if (M >= 16 && gemm_q4k_ok(W, N, K, M, st)) {
+  if ((M >= 16 || !q4k_i16_gemv_fits(N, K)) && gemm_q4k_ok(W, N, K, M, st)) {
     gemm_q4k<true>(W, Xq, Y, N, K, M, st);
   } else {
     for (size_t m = 0; m < M; ++m) q4k_i16_gemv(W, Xq + m * xrb, Y + m * N, N, K);
@@ -675,7 +677,7 @@ void mul_mat_q4k_persistent(const uint8_t* W, const float* X, uint8_t* Xq, float
 void mul_mat_q4k_quantized(const uint8_t* W, const uint8_t* Xq, float* Y, size_t N, size_t K,
                            size_t M, const RowStrides& st) {
   if (N == 0 || M == 0 || K == 0) return;
-  if (M >= 16 && args_ok(W, Xq, Y, N, K, M, st) && gemm_q4k_ok(W, N, K, M, st))
+  if ((M >= 16 || !q4k_gemv_fits(K)) && args_ok(W, Xq, Y, N, K, M, st) && gemm_q4k_ok(W, N, K, M, st))
     gemm_q4k(W, Xq, Y, N, K, M, st);
   else
     decode_q4k_quantized(W, Xq, Y, N, K, M, st);
