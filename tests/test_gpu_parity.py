@@ -292,13 +292,32 @@ def test_long_row_small_batch_takes_the_gemm(hip, fmt, m):
     check_mul_mat(fmt, w_, x_, xq, y, n, k, m)
 
 
+@pytest.mark.parametrize("fmt", [f for f in MM_ANY if f != "iq2_xs"])  # IQ2_XS has no _decode entry
+def test_long_row_decode_entry_takes_the_gemm(hip, fmt):
+    """The batch-1 decode entry points with a row past the GEMV's LDS
+    (K = 2^18) run the format's GEMM too."""
+    n, k, m = 8, 1 << 18, 1
+    x = o.seeded_normal(33, (m, k))
+    w = (o.random_records(fmt, n, k, seed=34) if fmt.startswith("iq2")
+         else o.quantize(fmt, o.seeded_normal(34, (n, k), 0.02)))
+    was = hip.lib.weft_hip_set_launch_log(1)
+    try:
+        launch_log(hip)
+        w_, x_, xq, y = run_mul_mat(hip, f"production_mul_mat_{fmt}_decode", fmt, n, k, m, w=w, x=x)
+        names = launch_log(hip)
+    finally:
+        hip.lib.weft_hip_set_launch_log(was)
+    assert "gemm" in names and "gemv" not in names, names
+    check_mul_mat(fmt, w_, x_, xq, y, n, k, m)
+
+
 @pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "mxfp4"])
-def test_decode_row_past_the_lds_is_refused(hip, fmt):
-    """The batch-1 decode entry points keep the activation row in LDS: a
-    row past it (K = 2^18: ~300 KB) is refused with an error and nothing
-    written, instead of a partial or wrong result."""
+def test_long_row_no_path_is_refused(hip, fmt):
+    """A row past the GEMV's LDS whose weights the GEMM cannot take either
+    (a base 2 bytes past 4-byte alignment: the GEMMs' direct loads need 4)
+    is refused with an error and nothing written."""
     n, k = 2, 1 << 18
-    w = hip.empty(o.record_bytes(fmt, k) * n)
+    w = hip.empty(o.record_bytes(fmt, k) * n, offset=2)
     x = hip.to_dev(np.ones((1, k), np.float32))
     xq = hip.empty(o.record_bytes(o.ACT_OF[fmt], k), fill=SENTINEL)
     y = hip.empty(4 * n, fill=SENTINEL)

@@ -624,6 +624,8 @@ void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t*
 
 void decode_q4k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
                 size_t M, const RowStrides& st) {
+  // a row the GEMV's LDS cannot hold goes to the GEMM when it takes the call
+  if (!q4k_gemv_fits(K) && gemm_q4k_try(W, X, Xq, Y, N, K, M, st)) return;
   launch_q4k(W, X, nullptr, Xq, Y, N, K, M, st);
 }
 

@@ -737,18 +737,22 @@ void launch(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_
 
 }  // namespace
 
-// Decode entry points shared with the prefill file for small M.
+// Decode entry points shared with the prefill file for small M.  A row the
+// GEMV's LDS cannot hold goes to the format's GEMM when it takes the call.
 void decode_q4_0(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
                  size_t M, const RowStrides& st) {
+  if (!staged_gemv_fits(0, K) && gemm_q80_try(0, W, X, Xq, nullptr, nullptr, Y, N, K, M, st)) return;
   launch<Fmt::Q4_0>(W, X, nullptr, Xq, nullptr, nullptr, Y, N, K, M, st);
 }
 void decode_mxfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
                   const float* scale, float* Y, size_t N, size_t K, size_t M, const RowStrides& st) {
+  if (!staged_gemv_fits(1, K) && gemm_q80_try(1, W, X, Xq, codebook, scale, Y, N, K, M, st)) return;
   launch<Fmt::MXFP4>(W, X, nullptr, Xq, codebook, scale, Y, N, K, M, st);
 }
 void decode_iq2_xxs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,
                     const int8_t* signs, float* Y, size_t N, size_t K, size_t M,
                     const RowStrides& st) {
+  if (!staged_gemv_fits(2, K) && gemm_iq2_try(false, W, X, Xq, grid, signs, Y, N, K, M, st)) return;
   launch<Fmt::IQ2_XXS>(W, X, nullptr, Xq, grid, signs, Y, N, K, M, st);
 }
 
@@ -769,26 +773,31 @@ void decode_pairs(int fmt, const uint8_t* W, const float* X, const uint8_t* xq_i
 
 void decode_q4_1(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
                  size_t M, const RowStrides& st) {
+  if (!staged_gemv_fits(6, K) && gemm_q80_try(6, W, X, Xq, nullptr, nullptr, Y, N, K, M, st)) return;
   launch<Fmt::Q4_1>(W, X, nullptr, Xq, nullptr, nullptr, Y, N, K, M, st);
 }
 
 void decode_iq2_xs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,
                    const int8_t* signs, float* Y, size_t N, size_t K, size_t M, const RowStrides& st) {
+  if (!staged_gemv_fits(7, K) && gemm_iq2_try(true, W, X, Xq, grid, signs, Y, N, K, M, st)) return;
   launch<Fmt::IQ2_XS>(W, X, nullptr, Xq, grid, signs, Y, N, K, M, st);
 }
 
 void decode_q6_k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
                  size_t M, const RowStrides& st) {
+  if (!staged_gemv_fits(3, K) && gemm_kq_try(true, W, X, Xq, Y, N, K, M, st)) return;
   launch<Fmt::Q6_K>(W, X, nullptr, Xq, nullptr, nullptr, Y, N, K, M, st);
 }
 
 void decode_q5_k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
                  size_t M, const RowStrides& st) {
+  if (!staged_gemv_fits(4, K) && gemm_kq_try(false, W, X, Xq, Y, N, K, M, st)) return;
   launch<Fmt::Q5_K>(W, X, nullptr, Xq, nullptr, nullptr, Y, N, K, M, st);
 }
 
 void decode_nvfp4(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
                   const float* scale, float* Y, size_t N, size_t K, size_t M, const RowStrides& st) {
+  if (!staged_gemv_fits(5, K) && gemm_q80_try(5, W, X, Xq, codebook, scale, Y, N, K, M, st)) return;
   launch<Fmt::NVFP4>(W, X, nullptr, Xq, codebook, scale, Y, N, K, M, st);
 }
 

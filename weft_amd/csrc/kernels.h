@@ -130,6 +130,17 @@ void mul_mat_id_iq2_grouped(bool xs, const uint8_t* W, const uint8_t* Xq, const 
 // the Q4K_I[16] GEMV).  Below 16 activation rows the prefill GEMMs take the
 // rows these refuse.
 bool staged_gemv_fits(int fmt, size_t K);
+// The format's prefill GEMM on X (quantized into Xq) if it takes the call;
+// false, with nothing launched, otherwise.  They never fall back to a GEMV,
+// so a GEMV entry point can try them first for a row it cannot hold.
+bool gemm_q80_try(int fmt, const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
+                  const float* scale, float* Y, size_t N, size_t K, size_t M, const RowStrides& st);
+bool gemm_kq_try(bool q6, const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
+                 size_t M, const RowStrides& st);
+bool gemm_iq2_try(bool xs, const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,
+                  const int8_t* signs, float* Y, size_t N, size_t K, size_t M, const RowStrides& st);
+bool gemm_q4k_try(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K, size_t M,
+                  const RowStrides& st);
 bool q4k_gemv_fits(size_t K);
 bool q4k_i16_gemv_fits(size_t M, size_t K);  // M weight rows
 

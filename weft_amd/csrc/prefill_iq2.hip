@@ -462,6 +462,21 @@ void mul_mat_id_iq2_grouped(bool xs, const uint8_t* W, const uint8_t* Xq, const 
   }
 }
 
+bool gemm_iq2_try(bool xs, const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,
+                  const int8_t* signs, float* Y, size_t N, size_t K, size_t M, const RowStrides& st) {
+  if (X == nullptr || !aligned(X, 4)) return false;
+  if (xs) {
+    if (!gemm_iq2_ok<true>(W, Xq, Y, grid, signs, N, K, M, st)) return false;
+    quantize_q8_k_rows(X, st.ldx, Xq, M, K);
+    gemm_iq2<true>(W, Xq, grid, signs, Y, N, K, M, st);
+  } else {
+    if (!gemm_iq2_ok(W, Xq, Y, grid, signs, N, K, M, st)) return false;
+    quantize_q8_k_rows(X, st.ldx, Xq, M, K);
+    gemm_iq2(W, Xq, grid, signs, Y, N, K, M, st);
+  }
+  return true;
+}
+
 void mul_mat_iq2_xxs(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* grid,
                      const int8_t* signs, float* Y, size_t N, size_t K, size_t M,
                      const RowStrides& st) {

@@ -439,6 +439,21 @@ void mul_mat_q6k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t
   gemm_kq<KQ::Q6_K>(W, Xq, Y, N, K, M, st);
 }
 
+bool gemm_kq_try(bool q6, const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
+                 size_t M, const RowStrides& st) {
+  if (X == nullptr || !aligned(X, 4)) return false;
+  if (q6) {
+    if (!gemm_kq_ok<KQ::Q6_K>(W, Xq, Y, N, K, M, st)) return false;
+    quantize_q8_k_rows(X, st.ldx, Xq, M, K);
+    gemm_kq<KQ::Q6_K>(W, Xq, Y, N, K, M, st);
+  } else {
+    if (!gemm_kq_ok<KQ::Q5_K>(W, Xq, Y, N, K, M, st)) return false;
+    quantize_q8_k_rows(X, st.ldx, Xq, M, K);
+    gemm_kq<KQ::Q5_K>(W, Xq, Y, N, K, M, st);
+  }
+  return true;
+}
+
 void mul_mat_q5k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K, size_t M,
                  const RowStrides& st) {
   if (X == nullptr || !aligned(X, 4) || !gemm_kq_ok<KQ::Q5_K>(W, Xq, Y, N, K, M, st))

@@ -607,6 +607,16 @@ bool args_ok(const uint8_t* W, const void* Xq, const float* Y, size_t N, size_t 
 
 }  // namespace
 
+bool gemm_q4k_try(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K, size_t M,
+                  const RowStrides& st) {
+  if (N == 0 || M == 0 || K == 0 || X == nullptr || !args_ok(W, Xq, Y, N, K, M, st) ||
+      !gemm_q4k_ok(W, N, K, M, st))
+    return false;
+  quantize_q8_k_rows(X, st.ldx, Xq, M, K);
+  gemm_q4k(W, Xq, Y, N, K, M, st);
+  return true;
+}
+
 // Prefill entry: MFMA GEMM when the shape suits it, the decode GEMV otherwise.
 void mul_mat_q4k(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
                  size_t M, const RowStrides& st) {

@@ -1119,6 +1119,18 @@ void mul_mat_id_q80_grouped(int fmt, const uint8_t* W, const float* X, uint8_t* 
                (K / 32) * kQ8_0Bytes);
 }
 
+bool gemm_q80_try(int fmt, const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* codebook,
+                  const float* scale, float* Y, size_t N, size_t K, size_t M, const RowStrides& st) {
+  if (N == 0 || M == 0 || K == 0 || W == nullptr || X == nullptr || Xq == nullptr || Y == nullptr) return false;
+  switch (fmt) {
+    case 0: return prefill_q80<WFmt::Q4_0>(W, X, Xq, nullptr, nullptr, Y, N, K, M, st);
+    case 1: return prefill_q80<WFmt::MXFP4>(W, X, Xq, codebook, scale, Y, N, K, M, st);
+    case 5: return prefill_q80<WFmt::NVFP4>(W, X, Xq, codebook, scale, Y, N, K, M, st);
+    case 6: return prefill_q80<WFmt::Q4_1>(W, X, Xq, nullptr, nullptr, Y, N, K, M, st);
+    default: return false;
+  }
+}
+
 void mul_mat_q4_0(const uint8_t* W, const float* X, uint8_t* Xq, float* Y, size_t N, size_t K,
                   size_t M, const RowStrides& st) {
   if (N == 0 || M == 0 || K == 0) return decode_q4_0(W, X, Xq, Y, N, K, M, st);
