@@ -311,17 +311,58 @@ def test_long_row_decode_entry_takes_the_gemm(hip, fmt):
     check_mul_mat(fmt, w_, x_, xq, y, n, k, m)
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "mxfp4"])
-def test_long_row_no_path_is_refused(hip, fmt):
-    """A row past the GEMV's LDS whose weights the GEMM cannot take either
-    (a base 2 bytes past 4-byte alignment: the GEMMs' direct loads need 4)
-    is refused with an error and nothing written."""
-    n, k = 2, 1 << 18
+VD_ANY = {"q4_0": "q8_0", "q4_1": "q8_1", "mxfp4": "q8_0", "nvfp4": "q8_0", "q4_k": "q8_k",
+          "q5_k": "q8_k", "q6_k": "q8_k", "iq2_xxs": "q8_k", "iq2_xs": "q8_k"}
+
+
+@pytest.mark.parametrize("fmt", list(VD_ANY))
+def test_long_row_vec_dot(hip, fmt):
+    """quantized_vec_dot_* with K = 2^18, the activation already quantized:
+    the staged GEMV walks K in chunks its LDS holds (the first stores Y, the
+    rest add), Q4_K takes its GEMM; against the oracle."""
+    k = 1 << 18
+    w = (o.random_records(fmt, 1, k, seed=35) if fmt.startswith("iq2")
+         else o.quantize(fmt, o.seeded_normal(35, (1, k), 0.02)))
+    xq = o.quantize(VD_ANY[fmt], o.seeded_normal(36, (1, k)))
+    y = hip.empty(4, fill=SENTINEL)
+    hip.call(f"quantized_vec_dot_{fmt}_{VD_ANY[fmt]}", hip.to_dev(w), hip.to_dev(xq), *tables(hip, fmt), y, k)
+    e, a = o.mul_mat_f64(fmt, w, xq, 1, k, 1)
+    assert_close(y.numpy(np.float32).reshape(1, 1), e, a, f"vec_dot {fmt} K=2^18")
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "mxfp4"])
+@pytest.mark.parametrize("m", [1, 3])
+def test_long_row_chunked_gemv(hip, fmt, m):
+    """A row past the GEMV's LDS whose weights the GEMM cannot take (a base
+    2 bytes past 4-byte alignment; the GEMMs' direct loads need 4): the
+    staged GEMV walks K in chunks, one activation row at a time; Xq and
+    every output against the oracle."""
+    n, k = 8, 1 << 18
+    w = o.quantize(fmt, o.seeded_normal(37, (n, k), 0.02))
+    x = o.seeded_normal(38, (m, k))
+    xq = hip.empty(o.record_bytes(o.ACT_OF[fmt], k) * m, fill=SENTINEL)
+    y = hip.empty(4 * m * n, fill=SENTINEL)
+    was = hip.lib.weft_hip_set_launch_log(1)
+    try:
+        launch_log(hip)
+        hip.call(MM_DECODE[fmt], hip.to_dev(w, offset=2), hip.to_dev(x), xq, *tables(hip, fmt), y, n, k, m)
+        names = launch_log(hip)
+    finally:
+        hip.lib.weft_hip_set_launch_log(was)
+    assert "gemm" not in names and names.count("staged_gemv_kernel") >= 4 * m, names
+    check_mul_mat(fmt, w, x, xq.numpy(np.uint8).reshape(m, -1), y.numpy(np.float32).reshape(m, n), n, k, m)
+
+
+def test_long_row_no_path_is_refused(hip):
+    """Q4_K's GEMV keeps the row in LDS and has no chunked mode: a row past
+    it whose weights the GEMM cannot take (a base 2 bytes past 4-byte
+    alignment) is refused with an error and nothing written."""
+    fmt, n, k = "q4_k", 2, 1 << 18
     w = hip.empty(o.record_bytes(fmt, k) * n, offset=2)
     x = hip.to_dev(np.ones((1, k), np.float32))
     xq = hip.empty(o.record_bytes(o.ACT_OF[fmt], k), fill=SENTINEL)
     y = hip.empty(4 * n, fill=SENTINEL)
-    args = [w, x, xq, *tables(hip, fmt), y]
+    args = [w, x, xq, y]
     getattr(hip.lib, MM_DECODE[fmt])(*[a.ptr for a in args], n, k, 1)
     hip.torch.cuda.synchronize()
     assert hip.last_error() != 0

@@ -658,7 +658,10 @@ void quantized_vec_dot_q4_k_q8_k(const uint8_t* W, const uint8_t* X, float* Y, s
     weft::set_error(hipErrorInvalidValue);
     return;
   }
-  weft::launch_q4k(W, nullptr, X, nullptr, Y, 1, K, 1, weft::packed(K / 256 * weft::kQ4_KBytes, K, 1));
+  const weft::RowStrides st = weft::packed(K / 256 * weft::kQ4_KBytes, K, 1);
+  // a row the GEMV's LDS cannot hold: the GEMM on the quantized row
+  if (!weft::q4k_gemv_fits(K)) return weft::mul_mat_q4k_quantized(W, X, Y, 1, K, 1, st);
+  weft::launch_q4k(W, nullptr, X, nullptr, Y, 1, K, 1, st);
 }
 
 }  // extern "C"

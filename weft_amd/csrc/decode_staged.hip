@@ -123,6 +123,7 @@ struct Args {
   size_t ldw;  // bytes between weight rows
   size_t ldx;  // elements between activation rows
   PairArgs pair;  // MUL_MAT_ID pairs (pair.ids null: none)
+  int accumulate;  // K chunk after the first: add to Y instead of storing
 };
 
 // 4 bytes starting at any LDS byte offset o (o+7 must be inside the buffer)
@@ -638,8 +639,68 @@ __global__ void __launch_bounds__(kThreads) staged_gemv_kernel(Args a) {
         if (m >= a.mb) break;
         float tot = wave_sum_f(acc[m]);
         if constexpr (F == Fmt::IQ2_XXS || F == Fmt::IQ2_XS) tot *= 0.125f;
-        if (lane == 0) a.Y[(size_t)(a.m0 + m) * a.y_stride + row] = tot;
+        if (lane == 0) {
+          float* yp = a.Y + (size_t)(a.m0 + m) * a.y_stride + row;
+          *yp = a.accumulate ? *yp + tot : tot;
+        }
       }
+    }
+  }
+}
+
+// A row whose quantized activation does not fit the LDS beside the windows:
+// one launch per activation row and K chunk (a multiple of 1024 values that
+// fits), each staging and quantizing its chunk of the row (block 0 writes
+// that chunk's Xq records, which fall on whole Q8 blocks) and adding its
+// partial dot products to Y, which the first chunk stores.  Launches are
+// ordered on the stream.
+template <Fmt F>
+void launch_chunked(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_out,
+                    const int8_t* tab0, const void* tab1, float* Y, size_t N, size_t K, size_t M,
+                    const RowStrides& st) {
+  using T = Traits<F>;
+  auto row_lds = [](size_t k) {
+    return T::kQ8K ? q8k_lds_row_bytes((int)k) : act_q81<F>() ? q81_lds_row_bytes((int)k) : q80_lds_row_bytes((int)k);
+  };
+  const size_t fixed = (size_t)kWaves * kWindow + table_bytes<F>();
+  const size_t cap = max_lds_per_block();
+  size_t kc = 0;
+  while (fixed + row_lds(kc + 1024) <= cap) kc += 1024;
+  if (kc == 0) {
+    set_error(hipErrorInvalidValue);
+    return;
+  }
+  const size_t act_elems = T::kQ8K ? 256 : 32;
+  const size_t act_rec = T::kQ8K ? kQ8_KBytes : act_q81<F>() ? kQ8_1Bytes : kQ8_0Bytes;
+  const size_t xrow = K / act_elems * act_rec;  // bytes of one quantized activation row
+  const int cus = cu_count();
+  const TileBindings& tb = tile_bindings();
+  const int rows_per_wg = tb.nc > 0 ? (int)std::min<size_t>(N, (size_t)tb.nc) : (int)((N + cus - 1) / cus);
+  const int grid = (int)((N + rows_per_wg - 1) / rows_per_wg);
+  for (size_t m = 0; m < M; ++m) {
+    for (size_t k0 = 0; k0 < K; k0 += kc) {
+      const size_t k = std::min(kc, K - k0);
+      const size_t xo = m * xrow + k0 / act_elems * act_rec;
+      Args a;
+      a.W = W + k0 / T::kElems * T::kBytes;
+      a.X = X != nullptr ? X + m * st.ldx + k0 : nullptr;
+      a.xq_in = xq_in != nullptr ? xq_in + xo : nullptr;
+      a.xq_out = xq_out != nullptr ? xq_out + xo : nullptr;
+      a.tab0 = tab0;
+      a.tab1 = tab1;
+      a.Y = Y + m * st.ldy;
+      a.N = (int)N;
+      a.K = (int)k;
+      a.m0 = 0;
+      a.mb = 1;
+      a.rows_per_wg = rows_per_wg;
+      a.y_stride = (long long)st.ldy;
+      a.ldw = st.ldw;
+      a.ldx = st.ldx;
+      a.pair = PairArgs{};
+      a.accumulate = k0 > 0;
+      staged_gemv_kernel<F><<<grid, kThreads, fixed + row_lds(k), current_stream()>>>(a);
+      check_launch("staged_gemv_kernel");
     }
   }
 }
@@ -693,6 +754,7 @@ void launch(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_
   const size_t fixed = (size_t)kWaves * kWindow + table_bytes<F>();
   const size_t cap = max_lds_per_block();
   if (fixed + row_lds > cap) {
+    if (pr == nullptr) return launch_chunked<F>(W, X, xq_in, xq_out, tab0, tab1, Y, N, K, M, st);
     set_error(hipErrorInvalidValue);
     return;
   }
@@ -720,6 +782,7 @@ void launch(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t* xq_
     a.ldw = st.ldw;
     a.ldx = st.ldx;
     a.pair = PairArgs{};
+    a.accumulate = 0;
     if (pr == nullptr) {
       staged_gemv_kernel<F><<<grid, kThreads, fixed + row_lds * a.mb, current_stream()>>>(a);
       check_launch("staged_gemv_kernel");
