@@ -227,6 +227,18 @@ def test_mul_mat_id_grouped_gemm(hip, fmt, ne11, prequant):
     assert any("gemm" in name for name in launched) != gemv, launched
 
 
+@pytest.mark.parametrize("fmt,prequant", [(f, False) for f in FMTS] +
+                         [(f, True) for f in ("q4_k", "q6_k", "iq2_xxs")])
+def test_mul_mat_id_rows_past_the_pair_gemv(hip, fmt, prequant):
+    """Four pairs with K = 2^18 (a quantized row of ~300 KB, past the pair
+    GEMV's LDS): the grouped MFMA GEMM takes them whatever the pair count."""
+    from weft_amd import _lib
+    _lib.launch_log()
+    run_id(hip, fmt, 1 << 18, 8, 3, 2, 1, 2, np.array([[2, 0], [0, 1]]), prequant=prequant)
+    launched = _lib.launch_log()
+    assert any("gemm" in name for name in launched) and not any("gemv" in name for name in launched), launched
+
+
 @pytest.mark.parametrize("k", [8192, 11008])
 def test_mul_mat_id_decode_long_rows(hip, k):
     # batch-1 pairs with rows of two / three 4096-column steps: the

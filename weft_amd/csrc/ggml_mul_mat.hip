@@ -403,11 +403,21 @@ hipError_t mul_mat_id(const weft_ggml_tensor* s0, const weft_ggml_tensor* s1,
   const uint8_t* xq_in = quantize ? nullptr : static_cast<const uint8_t*>(s1->data);
   uint8_t* xq_out = quantize ? static_cast<uint8_t*>(wdata) : nullptr;
   float* Y = static_cast<float*>(d->data);
-  // several pairs per expert on average: group the pairs by expert on the
-  // device and run the grouped MFMA GEMM (GGML's own order: quantize src1,
-  // group, multiply); the grouping lives in the part of wdata GGML's plan
-  // reserves for its row mapping
-  if (n_pairs >= 64 && n_pairs >= 4 * n_as && wdata != nullptr) {
+  // several pairs per expert on average, or rows the pair GEMV cannot hold
+  // in LDS: group the pairs by expert on the device and run the grouped MFMA
+  // GEMM (GGML's own order: quantize src1, group, multiply); the grouping
+  // lives in the part of wdata GGML's plan reserves for its row mapping
+  const int gemv_fmt = s0->type == WEFT_GGML_TYPE_Q4_0     ? 0
+                       : s0->type == WEFT_GGML_TYPE_MXFP4   ? 1
+                       : s0->type == WEFT_GGML_TYPE_IQ2_XXS ? 2
+                       : s0->type == WEFT_GGML_TYPE_Q6_K    ? 3
+                       : s0->type == WEFT_GGML_TYPE_Q5_K    ? 4
+                       : s0->type == WEFT_GGML_TYPE_NVFP4   ? 5
+                       : s0->type == WEFT_GGML_TYPE_Q4_1    ? 6
+                                                            : 7;
+  const bool pair_gemv_fits = s0->type == WEFT_GGML_TYPE_Q4_K ? q4k_gemv_fits((size_t)K)
+                                                              : staged_gemv_fits(gemv_fmt, (size_t)K);
+  if (((n_pairs >= 64 && n_pairs >= 4 * n_as) || !pair_gemv_fits) && wdata != nullptr) {
     const size_t xq_bytes = nbw1 * (size_t)(ne11 * n_tok);
     const size_t used = quantize ? (xq_bytes + 15) & ~(size_t)15 : 0;
     uint8_t* ws = static_cast<uint8_t*>(wdata) + used;
