@@ -1030,8 +1030,8 @@ bool prefill_q80(const uint8_t* W, const float* X, uint8_t* Xq, const int8_t* co
   // hold a row of K values.
   constexpr int kGemvFmt = F == WFmt::Q4_0 ? 0 : F == WFmt::MXFP4 ? 1 : F == WFmt::Q4_1 ? 6 : 5;
   if ((M < 16 && staged_gemv_fits(kGemvFmt, K)) || K % 256 || !aligned(W, 4) || ldw % 4 != 0 ||
-      (kNT - 1) * ldw + rb >= ((size_t)1 << 32) || !aligned(Xq, 16) || !aligned(Y, 4) || !aligned(X, 4) || N > (size_t)INT32_MAX ||
-      K > (size_t)INT32_MAX || M > (size_t)INT32_MAX ||
+      (kNT - 1) * ldw + rb >= ((size_t)1 << 32) || !aligned(Xq, 16) || !aligned(Y, 4) || !aligned(X, 4) ||
+      N > (size_t)INT32_MAX || K > (size_t)INT32_MAX || M > (size_t)INT32_MAX ||
       !strides_ok(st, rb, 1, K, N, N, M) ||
       ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT) > (size_t)INT32_MAX)
     return false;
