@@ -353,6 +353,29 @@ def test_long_row_chunked_gemv(hip, fmt, m):
     check_mul_mat(fmt, w, x, xq.numpy(np.uint8).reshape(m, -1), y.numpy(np.float32).reshape(m, n), n, k, m)
 
 
+@pytest.mark.parametrize("k,launches", [(76864, 1), (76928, 2)])
+def test_staged_row_lds_boundary(hip, k, launches):
+    """The staged GEMV's LDS edge for Q4_0 (16 wave windows of 4640 bytes,
+    3 KB of tables and a Q8_0 row of 1.125 K bytes in 160 KB): K = 76864 is
+    the longest row one pass holds, K = 76928 takes two chunks (76800 +
+    128); weights 2 bytes past 4-byte alignment keep the GEMM out.  Both
+    against the oracle."""
+    fmt, n, m = "q4_0", 8, 1
+    w = o.quantize(fmt, o.seeded_normal(39, (n, k), 0.02))
+    x = o.seeded_normal(40, (m, k))
+    xq = hip.empty(o.record_bytes(o.ACT_OF[fmt], k) * m, fill=SENTINEL)
+    y = hip.empty(4 * m * n, fill=SENTINEL)
+    was = hip.lib.weft_hip_set_launch_log(1)
+    try:
+        launch_log(hip)
+        hip.call(MM_DECODE[fmt], hip.to_dev(w, offset=2), hip.to_dev(x), xq, y, n, k, m)
+        names = launch_log(hip)
+    finally:
+        hip.lib.weft_hip_set_launch_log(was)
+    assert names.count("staged_gemv_kernel") == launches, names
+    check_mul_mat(fmt, w, x, xq.numpy(np.uint8).reshape(m, -1), y.numpy(np.float32).reshape(m, n), n, k, m)
+
+
 def test_long_row_no_path_is_refused(hip):
     """Q4_K's GEMV keeps the row in LDS and has no chunked mode: a row past
     it whose weights the GEMM cannot take (a base 2 bytes past 4-byte
