@@ -677,7 +677,13 @@ def main():
         b.torch.cuda.synchronize()
         dst.copy_(src)
         b.torch.cuda.synchronize()
-    cpu = None if args.no_cpu else cpu_baseline(11008, 4096, args.cpu_seconds)
+    cpu = None
+    if not args.no_cpu:
+        # a reported baseline only: a failure here must not lose the GPU line
+        try:
+            cpu = cpu_baseline(11008, 4096, args.cpu_seconds)
+        except Exception as e:  # noqa: BLE001
+            cpu = {"value": None, "unit": "GB/s", "error": f"{type(e).__name__}: {e}"[:300]}
 
     roofline = {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": profiled_traffic("q4k_decode_w_up"),
