@@ -50,6 +50,7 @@ struct Q4KArgs {
   size_t ldw;            // bytes between weight rows
   size_t ldx;            // elements between activation rows
   PairArgs pair;         // MUL_MAT_ID pairs (pair.ids null: none)
+  int accumulate = 0;    // K chunk after the first (q4k_gemv_kernel): add to Y
 };
 
 template <bool A16>
@@ -174,7 +175,10 @@ __global__ void __launch_bounds__(NT) q4k_gemv_kernel(Q4KArgs a) {
           for (int m = 0; m < MB; ++m) {
             if (m >= a.mb) break;
             const float tot = wave_sum_f(acc[m]);
-            if (lane == 0) a.Y[(size_t)(a.m0 + m) * a.y_stride + row] = tot;
+            if (lane == 0) {
+              float* yp = a.Y + (size_t)(a.m0 + m) * a.y_stride + row;
+              *yp = a.accumulate ? *yp + tot : tot;
+            }
             acc[m] = 0.f;
           }
         }
@@ -523,7 +527,46 @@ void launch_q4k(const uint8_t* W, const float* X, const uint8_t* xq_in, uint8_t*
   const size_t row_lds = q8k_lds_row_bytes((int)K);
   const size_t lds_cap = max_lds_per_block();
   if (row_lds > lds_cap) {
-    set_error(hipErrorInvalidValue);  // activation row does not fit in LDS
+    if (pr != nullptr) {
+      set_error(hipErrorInvalidValue);  // activation row does not fit in LDS
+      return;
+    }
+    // one launch per activation row and K chunk (a multiple of 1024 values
+    // whose Q8_K row fits), staging and quantizing that chunk (workgroup 0
+    // writes its Xq records, whole superblocks) and adding its partial dot
+    // products to Y, which the first chunk stores; ordered on the stream
+    constexpr int NT = 1024;
+    size_t kc = 0;
+    while (q8k_lds_row_bytes((int)(kc + 1024)) <= lds_cap) kc += 1024;
+    const int cus = cu_count();
+    const TileBindings& tb = tile_bindings();
+    const int rows_per_wg = tb.nc > 0 ? (int)std::min<size_t>(N, (size_t)tb.nc) : (int)((N + cus - 1) / cus);
+    const dim3 grid((unsigned)((N + rows_per_wg - 1) / rows_per_wg));
+    const size_t xrow = K / 256 * kQ8_KBytes;
+    for (size_t m = 0; m < M; ++m) {
+      for (size_t k0 = 0; k0 < K; k0 += kc) {
+        const size_t k = std::min(kc, K - k0);
+        Q4KArgs a;
+        a.W = W + k0 / 256 * kQ4_KBytes;
+        a.X = X != nullptr ? X + m * st.ldx + k0 : nullptr;
+        a.xq_in = xq_in != nullptr ? xq_in + m * xrow + k0 / 256 * kQ8_KBytes : nullptr;
+        a.xq_out = xq_out != nullptr ? xq_out + m * xrow + k0 / 256 * kQ8_KBytes : nullptr;
+        a.Y = Y + m * st.ldy;
+        a.N = (int)N;
+        a.K = (int)k;
+        a.m0 = 0;
+        a.mb = 1;
+        a.rows_per_wg = rows_per_wg;
+        a.y_stride = (long long)st.ldy;
+        a.ldw = st.ldw;
+        a.ldx = st.ldx;
+        a.pair = PairArgs{};
+        a.accumulate = k0 > 0;
+        const bool a16 = aligned(a.W, 16) && (N == 1 || st.ldw % 16 == 0);
+        launch_one<1, NT>(a16, grid, q8k_lds_row_bytes((int)k), a);
+        check_launch("q4k_gemv_kernel");
+      }
+    }
     return;
   }
   constexpr int NT = 1024;
