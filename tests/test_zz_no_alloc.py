@@ -63,6 +63,15 @@ def test_noalloc_matches_work_buffer_twice(hip, fmt):
         np.testing.assert_array_equal(got, ref)
 
 
+@pytest.mark.parametrize("fmt", ["q4_k", "mxfp4", "q4_0"])
+def test_noalloc_long_rows(hip, fmt):
+    # four pairs of K = 2^18 rows, past the pair GEMV's LDS: the grouped GEMM
+    # takes them whatever the pair count, its grouping in the scratch
+    ref, got = run_both(hip, fmt, 1 << 18, 8, 3, 2, 2, 13)
+    assert (ref != NAN).all()
+    np.testing.assert_array_equal(got, ref)
+
+
 def test_noalloc_refuses_work_beyond_the_scratch(hip):
     # Q8_K src1 of 32768 tokens x 4096: 37 MB of work buffer > 32 MiB
     k, n, n_tok = 4096, 16, 32768
